@@ -1,0 +1,338 @@
+"""ctypes binding of the CPU oracle (liboracle.so) and of the reference kernels built from source (_ref/).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
+checker. The shipped library never loads this. Functions mirror oracle/esq_oracle.h; arrays are numpy.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import shutil
+import tempfile
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+Q4_0, Q5_0, Q2_K, Q4_K, Q6_K = 2, 6, 10, 12, 14
+TYPES = {"Q4_0": Q4_0, "Q5_0": Q5_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K}
+NAMES = {v: k for k, v in TYPES.items()}
+STRICT, CONTRACT = 0, 1
+PATH_X86, PATH_SCALAR = 0, 1
+
+# activation blocks: es_blk_q80 (src/es_quant.h:31), es_block_q8_K (src/es_q2k.h:31-38)
+Q80 = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])
+Q8K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+assert Q80.itemsize == 36 and Q8K.itemsize == 292
+
+BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q2_K: 256, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q2_K: 84, Q4_K: 144, Q6_K: 210}
+
+
+def uses_q8k(t: int) -> bool:
+    return BLOCK_ELEMS[t] == 256
+
+
+def row_bytes(t: int, cols: int) -> int:
+    return cols // BLOCK_ELEMS[t] * BLOCK_BYTES[t]
+
+
+def act_dtype(t: int):
+    return Q8K if uses_q8k(t) else Q80
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Oracle:
+    """The CPU restatement (esq_oracle.c)."""
+
+    def __init__(self, path: str | None = None):
+        path = path or os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = self.lib = C.CDLL(path)
+        vp, i, u32, sz, f = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t, C.c_float
+        sig = {
+            "esq_half_to_float": (f, [C.c_uint16]),
+            "esq_float_to_half": (C.c_uint16, [f]),
+            "esq_quantize_q8_0": (None, [vp, vp, i]),
+            "esq_quantize_q8_K": (None, [vp, vp, i]),
+            "esq_matvec": (None, [u32, vp, i, i, i, vp, vp, i, i]),
+            "esq_matvec_multi": (None, [u32, vp, i, i, i, vp, sz, i, vp, sz, i, i]),
+            "esq_block_ints": (None, [u32, vp, i, i, vp, vp, vp]),
+            "esq_dequant_row": (None, [u32, vp, vp, i]),
+            "esq_quantize_q2_K_ref": (None, [vp, vp, i]),
+            "esq_quantize_row": (None, [u32, vp, vp, i]),
+            "esq_fill_gauss": (None, [C.c_uint64, f, vp, sz]),
+            "esq_mtest_blocks": (None, [u32, vp, vp, i, i]),
+            "esq_mtest_acts": (None, [vp, vp, sz]),
+            "esq_route_softmax": (i, [vp, i, i, i, vp, vp]),
+            "esq_moe_group": (i, [vp, i, i, vp, vp, vp, vp, vp]),
+            "esq_swiglu": (None, [vp, vp, vp, i]),
+            "esq_moe_combine": (None, [vp, vp, vp, i, i, i, vp]),
+            "esq_cpu_bench": (C.c_double, [vp, u32, vp, sz, i, i, i, vp, sz, i, vp, i, C.c_double, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+
+    # ---- fp16 / activations ----
+    def half_to_float(self, h: int) -> float:
+        return self.lib.esq_half_to_float(h)
+
+    def float_to_half(self, x: float) -> int:
+        return self.lib.esq_float_to_half(x)
+
+    def quantize_q8_0(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        y = np.zeros(x.size // 32, Q80)
+        self.lib.esq_quantize_q8_0(_p(x), _p(y), x.size)
+        return y
+
+    def quantize_q8_K(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        y = np.zeros(x.size // 256, Q8K)
+        self.lib.esq_quantize_q8_K(_p(x), _p(y), x.size)
+        return y
+
+    def quantize_act(self, t: int, x: np.ndarray) -> np.ndarray:
+        """x [na, cols] fp32 -> [na, nblocks] activation blocks of the type's kind"""
+        x = np.ascontiguousarray(x, np.float32)
+        na, cols = x.reshape(-1, x.shape[-1]).shape
+        q = self.quantize_q8_K(x) if uses_q8k(t) else self.quantize_q8_0(x)
+        return q.reshape(na, -1)
+
+    # ---- products ----
+    def matvec(self, t, W, cols, r0, r1, act, order=CONTRACT, path=PATH_X86, rows=None):
+        rows = rows if rows is not None else r1
+        y = np.zeros(rows, np.float32)
+        act = np.ascontiguousarray(act)
+        self.lib.esq_matvec(t, _p(W), cols, r0, r1, _p(act), _p(y), order, path)
+        return y
+
+    def matvec_multi(self, t, W, cols, rows, acts, order=CONTRACT, path=PATH_X86):
+        """acts [na, nblocks] -> y [na, rows]"""
+        acts = np.ascontiguousarray(acts)
+        na = acts.shape[0]
+        y = np.zeros((na, rows), np.float32)
+        self.lib.esq_matvec_multi(t, _p(W), cols, 0, rows, _p(acts), acts.strides[0], na, _p(y), rows, order, path)
+        return y
+
+    def block_ints(self, t, W, cols, rows, act):
+        nb = cols // BLOCK_ELEMS[t]
+        dots = np.zeros((rows, nb), np.int32)
+        aux = np.zeros((rows, nb), np.int32)
+        self.lib.esq_block_ints(t, _p(W), cols, rows, _p(np.ascontiguousarray(act)), _p(dots), _p(aux))
+        return dots, aux
+
+    def dequant(self, t, W, n):
+        y = np.zeros(n, np.float32)
+        self.lib.esq_dequant_row(t, _p(W), _p(y), n)
+        return y
+
+    # ---- weights / inputs ----
+    def quantize_rows(self, t, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        rows, cols = x.shape
+        W = np.zeros(rows * row_bytes(t, cols), np.uint8)
+        rb = row_bytes(t, cols)
+        for r in range(rows):
+            self.lib.esq_quantize_row(t, _p(x[r]), C.c_void_p(W.ctypes.data + r * rb), cols)
+        return W
+
+    def quantize_q2_K_ref(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        W = np.zeros(x.size // 256 * 84, np.uint8)
+        self.lib.esq_quantize_q2_K_ref(_p(x), _p(W), x.size)
+        return W
+
+    def gauss(self, seed: int, sigma: float, n: int) -> np.ndarray:
+        x = np.zeros(n, np.float32)
+        self.lib.esq_fill_gauss(seed, sigma, _p(x), n)
+        return x
+
+    def mtest_blocks(self, t, state: np.ndarray, rows, cols) -> np.ndarray:
+        W = np.zeros(rows * row_bytes(t, cols), np.uint8)
+        self.lib.esq_mtest_blocks(t, _p(state), _p(W), rows, cols)
+        return W
+
+    def mtest_acts(self, state: np.ndarray, n) -> np.ndarray:
+        x = np.zeros(n, np.float32)
+        self.lib.esq_mtest_acts(_p(state), _p(x), n)
+        return x
+
+    # ---- MoE glue ----
+    def route_softmax(self, logits: np.ndarray, k: int, norm_topk: bool):
+        """logits [n_tok, ne] -> sel [n_tok, k] int32, w [n_tok, k] fp32 (softmax probs left in a copy)"""
+        lg = np.ascontiguousarray(logits, np.float32).copy()
+        n_tok, ne = lg.shape
+        sel = np.zeros((n_tok, k), np.int32)
+        w = np.zeros((n_tok, k), np.float32)
+        for t in range(n_tok):
+            self.lib.esq_route_softmax(C.c_void_p(lg.ctypes.data + t * ne * 4), ne, k, int(norm_topk),
+                                       C.c_void_p(sel.ctypes.data + t * k * 4), C.c_void_p(w.ctypes.data + t * k * 4))
+        return sel, w, lg
+
+    def moe_group(self, sel: np.ndarray):
+        sel = np.ascontiguousarray(sel, np.int32)
+        n_tok, k = sel.shape
+        n = n_tok * k
+        uex, cnt, start = (np.zeros(n, np.int32) for _ in range(3))
+        rowof = np.zeros((n_tok, k), np.int32)
+        tok_of = np.zeros(n, np.int32)
+        nu = self.lib.esq_moe_group(_p(sel), n_tok, k, _p(uex), _p(cnt), _p(start), _p(rowof), _p(tok_of))
+        return uex[:nu].copy(), cnt[:nu].copy(), start[:nu].copy(), rowof, tok_of
+
+    def swiglu(self, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        h = np.zeros_like(g)
+        self.lib.esq_swiglu(_p(g), _p(u), _p(h), g.size)
+        return h
+
+    def moe_combine(self, ye: np.ndarray, rowof: np.ndarray, w: np.ndarray) -> np.ndarray:
+        n_tok, k = rowof.shape
+        n = ye.shape[1]
+        out = np.zeros((n_tok, n), np.float32)
+        self.lib.esq_moe_combine(_p(np.ascontiguousarray(ye, np.float32)), _p(np.ascontiguousarray(rowof, np.int32)),
+                                 _p(np.ascontiguousarray(w, np.float32)), n_tok, k, n, _p(out))
+        return out
+
+    # ---- CPU baseline ----
+    def cpu_bench(self, fn_ptr, t, W, mat_bytes, nmat, rows, cols, acts, nthreads, min_seconds=0.4):
+        acts = np.ascontiguousarray(acts)
+        na = acts.shape[0]
+        y = np.zeros((na, rows), np.float32)
+        passes = C.c_int(0)
+        sec = self.lib.esq_cpu_bench(fn_ptr, t, _p(W), mat_bytes, nmat, rows, cols, _p(acts), acts.strides[0], na,
+                                     _p(y), nthreads, min_seconds, C.byref(passes))
+        return sec, passes.value, y
+
+    def multi_fn_ptr(self):
+        return C.cast(self.lib.esq_multi_x86_contract, C.c_void_p)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the reference's kernels built from its own sources (oracle/_ref, see oracle/Makefile)
+
+class _EsAct(C.Structure):   # es_act, src/es_quant.h:32-37
+    _fields_ = [("x", C.c_void_p), ("q8", C.c_void_p), ("q80", C.c_void_p), ("cols", C.c_int)]
+
+
+def ref_path(cc: str) -> str:
+    return os.path.join(HERE, "_ref", f"libesref_{cc}.so")
+
+
+def ref_available(cc: str = "gcc") -> bool:
+    return os.path.exists(ref_path(cc))
+
+
+class RefLib:
+    """The reference's es_quant.c/es_q2k.c, compiled from /root/reference by oracle/Makefile.
+
+    scalar=True loads a private copy of the library with ES_NO_AVX2 set before its first call, which selects the
+    scalar mv_* kernels (src/es_quant.c:1833, 1857); the variable is read once per library instance.
+    """
+
+    def __init__(self, cc: str = "gcc", scalar: bool = False):
+        path = ref_path(cc)
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle ref` where /root/reference exists")
+        self._tmp = None
+        if scalar:
+            self._tmp = tempfile.mkdtemp(prefix="esref_")
+            dst = os.path.join(self._tmp, f"libesref_{cc}_scalar.so")
+            shutil.copy(path, dst)
+            path = dst
+        old = os.environ.get("ES_NO_AVX2")
+        if scalar:
+            os.environ["ES_NO_AVX2"] = "1"
+        elif "ES_NO_AVX2" in os.environ:
+            del os.environ["ES_NO_AVX2"]
+        L = self.lib = C.CDLL(path)
+        vp, i, u32, sz = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t
+        for name, res, args in [
+            ("es_act_arena_init", None, [sz]),
+            ("es_act_arena_reset", None, []),
+            ("es_act_prepare", None, [vp, vp, i, vp]),
+            ("es_matvec", None, [u32, vp, i, i, i, vp, vp, vp]),
+            ("es_matvec_multi", None, [u32, vp, i, i, i, vp, i, vp, sz, vp]),
+            ("es_row_bytes", sz, [u32, i]),
+            ("es_dequant_row", None, [u32, vp, vp, i]),
+            ("es_quantize_q8_K", None, [vp, vp, i]),
+            ("es_quantize_q2_K_ref", None, [vp, vp, i]),
+            ("es_fp32_to_fp16", C.c_uint16, [C.c_float]),
+            ("es_dot_q2_K_q8_K_ref", C.c_float, [i, vp, vp]),
+            ("es_dot_q2_K_q8_K", C.c_float, [i, vp, vp]),
+        ]:
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+        L.es_act_arena_init(1 << 26)
+        # force the one-time dispatch decision now, while the environment is as requested
+        self._warm()
+        if old is None:
+            os.environ.pop("ES_NO_AVX2", None)
+        else:
+            os.environ["ES_NO_AVX2"] = old
+
+    def _warm(self):
+        x = np.ones(256, np.float32)
+        W = np.zeros(144, np.uint8)
+        self.matvec_f32(Q4_K, W, 256, 1, x[None, :])
+
+    def prepare(self, x: np.ndarray):
+        """fp32 rows -> (es_act array, keep-alive list, q80 view, q8K view) exactly as es_act_prepare makes them"""
+        x = np.ascontiguousarray(x, np.float32)
+        na, cols = x.shape
+        self.lib.es_act_arena_reset()
+        nk = cols // 256
+        q8 = np.zeros((na, max(nk, 1)), Q8K)
+        acts = (_EsAct * na)()
+        for q in range(na):
+            self.lib.es_act_prepare(C.byref(acts[q]), C.c_void_p(x.ctypes.data + q * cols * 4), cols,
+                                    C.c_void_p(q8.ctypes.data + q * q8.strides[0]) if nk else None)
+        q80 = np.zeros((na, cols // 32), Q80)
+        for q in range(na):
+            if acts[q].q80:
+                C.memmove(q80.ctypes.data + q * q80.strides[0], acts[q].q80, (cols // 32) * 36)
+        return acts, [x, q8], q80, q8[:, :nk]
+
+    def matvec_f32(self, t, W, cols, rows, x: np.ndarray, r0=0, multi=False):
+        """x [na, cols] fp32 through es_act_prepare + es_matvec (one per activation) or es_matvec_multi"""
+        acts, keep, _, _ = self.prepare(x)
+        na = x.shape[0]
+        y = np.zeros((na, rows), np.float32)
+        scratch = np.zeros(cols, np.float32)
+        if multi:
+            self.lib.es_matvec_multi(t, _p(W), cols, r0, rows, acts, na, _p(y), rows, _p(scratch))
+        else:
+            for q in range(na):
+                self.lib.es_matvec(t, _p(W), cols, r0, rows, C.byref(acts[q]), C.c_void_p(y.ctypes.data + q * rows * 4),
+                                   _p(scratch))
+        del keep
+        return y
+
+    def quantize_q8_K(self, x):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        y = np.zeros(x.size // 256, Q8K)
+        self.lib.es_quantize_q8_K(_p(x), _p(y), x.size)
+        return y
+
+    def quantize_q2_K_ref(self, x):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        W = np.zeros(x.size // 256 * 84, np.uint8)
+        self.lib.es_quantize_q2_K_ref(_p(x), _p(W), x.size)
+        return W
+
+    def dequant(self, t, W, n):
+        y = np.zeros(n, np.float32)
+        self.lib.es_dequant_row(t, _p(W), _p(y), n)
+        return y
+
+    def fp32_to_fp16(self, f):
+        return self.lib.es_fp32_to_fp16(f)
+
+    def multi_fn_ptr(self):
+        return None   # the reference's es_matvec_multi takes es_act*, not strided blocks; timed via bench_ref below
