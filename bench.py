@@ -1,0 +1,220 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized matrix-product path on one MI355X.
+
+Headline (decode form): Q4_K matvec at T=1 over the Llama-3.2-1B FFN shapes (gate and up
+8192x2048, down 2048x8192), 38 layer copies = 1.08 GB of packed weights in HBM, rotated so every step streams from HBM rather
+than the 256 MB Infinity Cache. One step = one launch of a prepared job batch (the engine's run_jobs) over all 114
+matrices. value = weight bytes / step time, the reference's "weight GB/s" (tools/es_fmtbench.c:40, tools/es_kbench.c:294).
+
+Also reported: config 2's prefill form (T=512, int8 TOPS = 2*T*rows*cols / time), configs 1 and 3, the kernel's roofline
+(achieved vs 8 TB/s, kernel time from HIP events on the launch stream) and the reference's CPU kernels timed on this host
+(cpu_baseline: the reference's es_matvec_multi built from its sources, oracle/_ref, driven es_kbench-style).
+
+Inputs are synthetic: es_mtest-style random weight blocks with sane fp16 scales (tools/es_mtest.c:9-35) and N(0,1)
+activations quantized to the reference's Q8 blocks in numpy. Kernel speed does not depend on the values.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "stream-_amd"))
+import es_hip_quant as E  # noqa: E402
+
+METRIC = "decode matvec weight GB/s (% HBM peak); prefill int8 TOPS (% MFMA peak)"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+Q80 = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])
+Q8K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+SCALE_POS = {E.Q4_0: (0, None), E.Q5_0: (0, None), E.Q4_K: (0, 2), E.Q6_K: (208, None), E.Q2_K: (80, 82)}
+
+
+def random_blocks(t, rows, cols, rng):
+    """random block bytes with sane fp16 scales, the es_mtest recipe (tools/es_mtest.c:30-35)"""
+    nb, bb = cols // E.BLOCK_ELEMS[t], E.BLOCK_BYTES[t]
+    W = rng.integers(0, 256, (rows, nb, bb), dtype=np.uint8)
+    dp, mp = SCALE_POS[t]
+    W[:, :, dp:dp + 2] = (0.001 + rng.integers(0, 1000, (rows, nb)) / 1e5).astype(np.float16)[..., None].view(np.uint8)
+    if mp is not None:
+        W[:, :, mp:mp + 2] = (0.0005 + rng.integers(0, 1000, (rows, nb)) / 1e5).astype(np.float16)[..., None].view(np.uint8)
+    return W.reshape(-1)
+
+
+def quantize_acts(t, x):
+    """fp32 [n, cols] -> the reference's activation blocks [n, nblocks] (Q8_K for K-quants, Q8_0 otherwise)"""
+    n, cols = x.shape
+    if E.BLOCK_ELEMS[t] == 256:
+        xb = x.reshape(n, cols // 256, 256)
+        amax = np.abs(xb).max(axis=2)
+        q = np.clip(np.rint(xb * (127.0 / np.maximum(amax, 1e-30))[..., None]), -127, 127).astype(np.int8)
+        out = np.zeros((n, cols // 256), Q8K)
+        out["d"] = amax / 127.0
+        out["qs"] = q
+        out["bsums"] = q.reshape(n, cols // 256, 16, 16).astype(np.int32).sum(axis=3)
+        return out
+    xb = x.reshape(n, cols // 32, 32)
+    d = np.abs(xb).max(axis=2) / 127.0
+    v = xb * np.where(d > 0, 1.0 / np.maximum(d, 1e-30), 0.0)[..., None]
+    out = np.zeros((n, cols // 32), Q80)
+    out["d"] = d
+    out["qs"] = np.trunc(np.where(v < 0, v - 0.5, v + 0.5)).astype(np.int8)
+    return out
+
+
+class Workload:
+    """A rotating set of `copies` copies of some matrices, all against the same activations, as one prepared batch."""
+
+    def __init__(self, lib, rng, mats, na, copies):
+        self.lib, self.keep, specs = lib, [], []
+        self.weight_bytes = 0
+        self.ops = 0
+        for (t, rows, cols) in mats:
+            W = random_blocks(t, rows, cols, rng)
+            acts = quantize_acts(t, rng.standard_normal((na, cols)).astype(np.float32))
+            dA = lib.upload(acts)
+            dW = lib.alloc(W.nbytes * copies)
+            src = lib.upload(W)
+            for c in range(copies):
+                lib.copy_d2d(dW.offset(c * W.nbytes), src, W.nbytes)
+            src.close()
+            dY = lib.alloc(4 * na * rows * copies)
+            self.keep += [dA, dW, dY]
+            for c in range(copies):
+                specs.append(dict(type=t, rows=rows, cols=cols, W=dW.offset(c * W.nbytes), act=dA,
+                                  astride=acts.strides[0], nb=na, y=dY.offset(4 * na * rows * c), ystride=rows))
+                self.weight_bytes += W.nbytes
+                self.ops += 2 * na * rows * cols
+        self.plan = lib.plan(specs)
+        self.launches_per_step = len(self.plan_groups(mats))
+
+    @staticmethod
+    def plan_groups(mats):
+        return {m[0] for m in mats}   # one launch per format
+
+    def time(self, warmup, steps):
+        """(wall ms per step, event ms per step): events on the launch stream around `steps` back-to-back runs"""
+        for _ in range(warmup):
+            self.plan.run()
+        self.lib.synchronize()
+        t0 = time.perf_counter()
+        ev = self.plan.time_ms(0, steps)
+        self.lib.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        return wall, ev
+
+    def close(self):
+        self.plan.close()
+        for b in self.keep:
+            b.close()
+
+
+def cpu_baseline(t, rows, cols, rng, seconds):
+    """The reference's es_matvec_multi (oracle/_ref/libesref_clang.so, built from its sources) or, where that build is
+    absent, the oracle's restatement, timed es_kbench-style on this host: a rotating set larger than the host LLC,
+    pinned threads taking 16-row chunks, >= `seconds` per point."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    orc = O.Oracle()
+    if O.ref_available("clang"):
+        ref = O.RefLib("clang")
+        fn, kind = orc.reference_fn_ptr(ref), "reference"
+    else:
+        fn, kind = orc.multi_fn_ptr(), "port"
+    W1 = random_blocks(t, rows, cols, rng)
+    nmat = max(1, (288 << 20) // W1.nbytes + 1)
+    W = np.tile(W1, nmat)
+    acts = quantize_acts(t, rng.standard_normal((1, cols)).astype(np.float32))
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    allc = max(1, min(16, avail))
+    points = {}
+    for nt in sorted({1, min(8, allc), allc}):
+        sec, passes, _ = orc.cpu_bench(fn, t, W, W1.nbytes, nmat, rows, cols, acts, nt, seconds)
+        points[nt] = W1.nbytes * nmat / sec / 1e9
+    return {"value": round(points[allc], 2), "unit": "GB/s", "cores": allc, "kind": kind,
+            "sample": f"Q4_K {rows}x{cols} matvec (T=1), {nmat} matrices = {W1.nbytes * nmat / 2**20:.0f} MiB rotating, "
+                      f">= {seconds:.1f} s per point, 16-row chunks (src/es_engine.c:152-171)",
+            "by_threads_gbs": {str(k): round(v, 2) for k, v in points.items()}, "host_cpus_visible": avail}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=2.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the path shards by output rows or by "
+              "experts across GPUs, which is not part of this build", file=sys.stderr)
+        sys.exit(2)
+
+    lib = E.Lib()
+    if not lib.available():
+        raise SystemExit("no usable gfx950 device: " + lib.last_error())
+    rng = np.random.default_rng(20260101)
+    K, Wm = args.steps, args.warmup
+
+    # ---- headline: config 2 decode, Q4_K, T=1, 1.08 GB rotating set
+    copies = 38
+    dec = Workload(lib, rng, [(E.Q4_K, 8192, 2048), (E.Q4_K, 8192, 2048), (E.Q4_K, 2048, 8192)], 1, copies)
+    wall, ev = dec.time(Wm, K)
+    gbs = dec.weight_bytes / (ev * 1e-3) / 1e9
+    head_bytes = dec.weight_bytes
+    dec.close()
+
+    # ---- config 2 prefill, T=512
+    pre = Workload(lib, rng, [(E.Q4_K, 8192, 2048), (E.Q4_K, 8192, 2048), (E.Q4_K, 2048, 8192)], 512, 1)
+    pwall, pev = pre.time(Wm, max(3, K // 4))
+    tops = pre.ops / (pev * 1e-3) / 1e12
+    pre.close()
+
+    extra = {}
+    # ---- config 1: Q4_0 4864x896, b=1, 410 copies (1.0 GB)
+    c1 = Workload(lib, rng, [(E.Q4_0, 4864, 896)], 1, 410)
+    _, e1 = c1.time(Wm, K)
+    extra["config1_q4_0_decode"] = {"gbs": round(c1.weight_bytes / (e1 * 1e-3) / 1e9, 1), "ms": round(e1, 4),
+                                    "weight_bytes": c1.weight_bytes}
+    c1.close()
+    # ---- config 3: Q6_K head 151936x1024 (K padded from 896), b=1 and b=64, 8 copies (1.0 GB)
+    for b in (1, 64):
+        c3 = Workload(lib, rng, [(E.Q6_K, 151936, 1024)], b, 8)
+        _, e3 = c3.time(Wm, max(3, K // 2))
+        extra[f"config3_q6_k_head_b{b}"] = {"gbs": round(c3.weight_bytes / (e3 * 1e-3) / 1e9, 1), "ms": round(e3, 4),
+                                           "weight_bytes": c3.weight_bytes}
+        c3.close()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(E.Q4_K, 8192, 2048, rng, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": Wm,
+        "ms_per_step": round(wall, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "Q4_K decode matvec, Llama-3.2-1B FFN shapes (gate/up 8192x2048, down 2048x8192), T=1, "
+                               f"{copies} layer copies = {head_bytes / 1e9:.2f} GB rotating, one batched launch per step",
+                   "global_batch": 1, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "prefill": {"workload": "Q4_K prefill T=512: gate/up 8192x2048 and down 2048x8192, one batched launch",
+                    "value": round(tops, 2), "unit": "TOPS", "ms": round(pev, 4),
+                    "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                                 "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None}},
+        "configs": extra,
+        "device": lib.device_name(),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

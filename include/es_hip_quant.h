@@ -1,0 +1,143 @@
+/*
+ * es_hip_quant.h — C ABI of the MI355X (gfx950) quantized matrix-product library (libes_hip_quant.so).
+ *
+ * What it replaces. The reference engine (Tharunmaks/Stream-, "ExpertStream") computes every weight x activation product on
+ * the CPU through three headers:
+ *   src/es_quant.h:25-49    es_act_prepare / es_matvec / es_matvec_multi / es_row_bytes / es_quant_supported
+ *   src/es_q2k.h:24-86      the Q2_K / Q8_K block structs, es_quantize_q8_K, es_matvec_q2_K
+ *   src/es_compute.h:10-25  the thread pool that fans a queue of row jobs out to cores (driven by src/es_engine.c:144-186)
+ * This library computes the same products on one MI355X for the GGUF formats Q4_0, Q5_0, Q4_K, Q6_K and Q2_K against the
+ * reference's Q8 activations, with the packed weight blocks kept byte-for-byte in device memory.
+ *
+ * Results. The integer block dots are exact. The fp32 epilogue is evaluated in the reference's own order, so outputs are
+ * bit-identical to the reference's CPU kernels in the selected build flavour (es_hip_set_order):
+ *   ES_HIP_ORDER_X86_CONTRACT  the reference's default x86 build (clang, -ffp-contract=on; Makefile:1-4) — the default here
+ *   ES_HIP_ORDER_X86_STRICT    the same AVX2 kernels built by gcc -std=c11 (no contraction)
+ *   ES_HIP_ORDER_SCALAR        the scalar mv_* kernels (ES_NO_AVX2=1, src/es_quant.c:1013-1117)
+ *
+ * Conventions (same as the reference): every buffer belongs to the caller; W points at row 0 of a row-major matrix whose row
+ * stride is es_hip_row_bytes(type, cols); outputs are written only for rows [r0, r1), at absolute row indices, activation q's
+ * result at y + q * ystride. Activation blocks are the reference's: Q8_0 (36 bytes: float d, int8 qs[32]) for Q4_0/Q5_0 and
+ * Q8_K (292 bytes: float d, int8 qs[256], int16 bsums[16]) for Q2_K/Q4_K/Q6_K.
+ *
+ * Errors. The reference's entry points return void and cannot fail. Here the device-pointer entry points return 0 on success
+ * and a negative ES_HIP_E* code otherwise; es_hip_last_error() describes the most recent failure. There is no CPU fallback:
+ * without a usable gfx950 device every compute call fails with ES_HIP_ENODEV.
+ *
+ * Streams are passed as void* (a hipStream_t; NULL means the null stream) so this header needs no HIP include.
+ */
+#ifndef ES_HIP_QUANT_H
+#define ES_HIP_QUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids of the formats computed here (reference src/es_quant.h:15-22) */
+enum { ES_HIP_Q4_0 = 2, ES_HIP_Q5_0 = 6, ES_HIP_Q2_K = 10, ES_HIP_Q4_K = 12, ES_HIP_Q6_K = 14 };
+
+/* fp32 epilogue order, see the header comment */
+enum { ES_HIP_ORDER_X86_CONTRACT = 0, ES_HIP_ORDER_X86_STRICT = 1, ES_HIP_ORDER_SCALAR = 2 };
+
+/* status codes */
+enum {
+    ES_HIP_OK = 0,
+    ES_HIP_ENODEV = -1,   /* no usable gfx950 device */
+    ES_HIP_EINVAL = -2,   /* bad type, shape, stride, alignment or pointer */
+    ES_HIP_ERUNTIME = -3, /* a HIP runtime call failed */
+    ES_HIP_ENOMEM = -4
+};
+
+/* Activation blocks and the prepared-activation record: the same byte layouts as the reference's es_blk_q80
+ * (src/es_quant.h:31), es_block_q8_K (src/es_q2k.h:31-38) and es_act (src/es_quant.h:32-37). */
+typedef struct { float d; int8_t qs[32]; } es_hip_blk_q80;
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } es_hip_block_q8_K;
+typedef struct {
+    const float *x;
+    es_hip_block_q8_K *q8;   /* NULL unless cols % 256 == 0 */
+    es_hip_blk_q80 *q80;     /* NULL unless cols % 32 == 0 */
+    int cols;
+} es_hip_act;
+
+/* ---- library state ------------------------------------------------------------------------------------------------ */
+int         es_hip_available(void);          /* 1 if a gfx950 device is usable (initialises the library once) */
+const char *es_hip_last_error(void);         /* text of the most recent failure ("" if none); per thread */
+const char *es_hip_device_name(void);        /* gcnArchName of the device in use, or "" */
+int         es_hip_set_order(int order);     /* select the epilogue order; returns the previous one, or ES_HIP_EINVAL */
+int         es_hip_get_order(void);
+
+/* ---- format facts (reference src/es_quant.h:24-26, 48-49; src/es_quant.c:39-73) ------------------------------------- */
+int    es_hip_quant_supported(uint32_t type);   /* 1 for the five formats above */
+size_t es_hip_row_bytes(uint32_t type, int cols);
+
+/* ---- device memory helpers (plumbing for callers without their own HIP allocator) ---------------------------------- */
+void *es_hip_malloc(size_t bytes);                            /* NULL on failure */
+int   es_hip_free(void *dev);
+int   es_hip_memcpy_h2d(void *dev, const void *host, size_t bytes);
+int   es_hip_memcpy_d2h(void *host, const void *dev, size_t bytes);
+int   es_hip_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int   es_hip_memset(void *dev, int value, size_t bytes);
+int   es_hip_synchronize(void);
+
+/* ---- products on device memory --------------------------------------------------------------------------------------- */
+/* es_matvec (src/es_quant.h:44-45) on device memory: y[r] for r in [r0, r1). act: the activation blocks of one input. */
+int es_hip_matvec_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, float *y, void *stream);
+/* es_matvec_multi (src/es_quant.h:46-47) on device memory: na activations, activation q's blocks at act + q * astride bytes,
+ * outputs at y + q * ystride. Bit-identical to na calls of es_hip_matvec_dev (the reference's es_mtest invariant). */
+int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride, int na,
+                            float *y, size_t ystride, void *stream);
+
+/* One queued product: the reference engine's mv_job (src/es_engine.c:144) with device pointers. rows are [0, rows). */
+typedef struct {
+    uint32_t type;
+    int rows, cols;
+    const void *W;      /* device, row 0 */
+    const void *act;    /* device activation blocks, activation q at act + q * astride bytes */
+    size_t astride;     /* bytes; 0 means packed (cols / block elements * block bytes) */
+    int nb;             /* number of activations (the reference's nb) */
+    float *y;           /* device, activation q's outputs at y + q * ystride */
+    size_t ystride;     /* floats */
+} es_hip_job;
+
+/* run_jobs (src/es_engine.c:177-186): every queued product in as few launches as possible (one per format). */
+int es_hip_run_jobs(const es_hip_job *jobs, int njobs, void *stream);
+
+/* A prepared job batch: the job table is uploaded once, so a launch costs only the kernel dispatches. The jobs' pointers
+ * are captured when the plan is made; the memory they point to may change between runs. */
+typedef struct es_hip_plan es_hip_plan;
+es_hip_plan *es_hip_plan_create(const es_hip_job *jobs, int njobs);   /* NULL on failure */
+int          es_hip_plan_run(es_hip_plan *plan, void *stream);
+void         es_hip_plan_destroy(es_hip_plan *plan);
+
+/* ---- drop-ins on host memory (same prototypes and meaning as the reference) ------------------------------------------ */
+/* Weights registered here stay resident on the device, byte-for-byte; es_hip_matvec / es_hip_matvec_multi find a W inside a
+ * registered range and use the device copy. Unregistered weights are uploaded for the one call. Re-register (or
+ * es_hip_update) after the host bytes change (e.g. an expert cache slot that received another expert). */
+int es_hip_register(const void *host, size_t bytes);
+int es_hip_update(const void *host);
+int es_hip_unregister(const void *host);
+/* es_matvec / es_matvec_multi (src/es_quant.h:44-47): host W, host activations (a->q80 for Q4_0/Q5_0, a->q8 for the K-quants),
+ * host y. Synchronous. The scratch argument is unused (kept for the prototype). They clear es_hip_last_error() on entry;
+ * on failure y is left untouched and es_hip_last_error() says why (the reference's void prototype has no other error
+ * channel). */
+void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch);
+void es_hip_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
+                         size_t ystride, float *scratch);
+
+/* ---- diagnostics ----------------------------------------------------------------------------------------------------- */
+/* The integer part of every (row, block) of rows [0, rows) against one activation, as the reference's kernels form it:
+ * dots[r * nb + b] = the block's integer dot (Q4_0/Q5_0: the sum of the eight AVX2 lane sums; Q4_K: dot; Q6_K: tot;
+ * Q2_K: isum) and aux[r * nb + b] = Q4_K mins or Q2_K summs (0 for the others). nb = cols / block elements. Device memory. */
+int es_hip_block_ints_dev(uint32_t type, const void *W, int cols, int rows, const void *act, int32_t *dots, int32_t *aux,
+                          void *stream);
+/* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`
+ * (after `warmup` untimed runs). */
+double es_hip_plan_time_ms(es_hip_plan *plan, int warmup, int iters, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -660,6 +660,35 @@ void esq_multi_x86_contract(uint32_t t, const void *W, int cols, int r0, int r1,
     esq_matvec_multi(t, W, cols, r0, r1, act, astride, na, y, ystride, ESQ_CONTRACT, ESQ_PATH_X86);
 }
 
+typedef struct { const float *x; const void *q8; const void *q80; int cols; } ref_act;   /* es_act layout */
+typedef void (*ref_multi_t)(uint32_t, const void *, int, int, int, const ref_act *, int, float *, size_t, float *);
+static ref_multi_t REF_MULTI;
+
+void esq_bind_reference(void *fn) { REF_MULTI = (ref_multi_t)fn; }
+
+void esq_multi_reference(uint32_t t, const void *W, int cols, int r0, int r1, const void *act, size_t astride, int na,
+                         float *y, size_t ystride) {
+    static _Thread_local float *scratch;
+    static _Thread_local int scratch_n;
+    if (scratch_n < cols) {
+        free(scratch);
+        scratch = (float *)calloc((size_t)cols, sizeof(float));
+        scratch_n = scratch ? cols : 0;
+    }
+    ref_act a[64];
+    for (int q0 = 0; q0 < na; q0 += 64) {
+        const int n = na - q0 < 64 ? na - q0 : 64;
+        for (int q = 0; q < n; q++) {
+            const void *blk = (const uint8_t *)act + (size_t)(q0 + q) * astride;
+            a[q].x = NULL;
+            a[q].q8 = esq_uses_q8K(t) ? blk : NULL;
+            a[q].q80 = esq_uses_q8K(t) ? NULL : blk;
+            a[q].cols = cols;
+        }
+        REF_MULTI(t, W, cols, r0, r1, a, n, y + (size_t)q0 * ystride, ystride, scratch);
+    }
+}
+
 typedef struct {
     esq_multi_fn fn;
     uint32_t type;

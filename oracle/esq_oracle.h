@@ -115,6 +115,12 @@ double esq_cpu_bench(esq_multi_fn fn, uint32_t type, const void *W, size_t mat_b
 /* the oracle itself as an esq_multi_fn (x86 path, contract order) */
 void esq_multi_x86_contract(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride,
                             int na, float *y, size_t ystride);
+/* The reference's own es_matvec_multi (oracle/_ref, loaded by the caller) as an esq_multi_fn: esq_bind_reference takes its
+ * address; esq_multi_reference builds the reference's es_act records (src/es_quant.h:32-37) over the strided activation
+ * blocks (q8 for the K-quants, q80 for Q4_0/Q5_0) and calls it with a per-thread scratch of cols floats. */
+void esq_bind_reference(void *es_matvec_multi_fn);
+void esq_multi_reference(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride, int na,
+                         float *y, size_t ystride);
 
 #ifdef __cplusplus
 }

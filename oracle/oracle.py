@@ -73,6 +73,8 @@ class Oracle:
             "esq_swiglu": (None, [vp, vp, vp, i]),
             "esq_moe_combine": (None, [vp, vp, vp, i, i, i, vp]),
             "esq_cpu_bench": (C.c_double, [vp, u32, vp, sz, i, i, i, vp, sz, i, vp, i, C.c_double, vp]),
+            "esq_bind_reference": (None, [vp]),
+            "esq_multi_reference": (None, [u32, vp, i, i, i, vp, sz, i, vp, sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -212,6 +214,20 @@ class Oracle:
 
     def multi_fn_ptr(self):
         return C.cast(self.lib.esq_multi_x86_contract, C.c_void_p)
+
+    def reference_fn_ptr(self, ref: "RefLib"):
+        """the reference's es_matvec_multi (from a RefLib) behind the esq_multi_fn signature"""
+        self.lib.esq_bind_reference(C.cast(ref.lib.es_matvec_multi, C.c_void_p))
+        return C.cast(self.lib.esq_multi_reference, C.c_void_p)
+
+    def matvec_multi_reference(self, ref: "RefLib", t, W, cols, rows, acts):
+        """acts [na, nblocks] through the reference's es_matvec_multi (es_act records over these blocks)"""
+        self.reference_fn_ptr(ref)
+        acts = np.ascontiguousarray(acts)
+        na = acts.shape[0]
+        y = np.zeros((na, rows), np.float32)
+        self.lib.esq_multi_reference(t, _p(W), cols, 0, rows, _p(acts), acts.strides[0], na, _p(y), rows)
+        return y
 
 
 # ---------------------------------------------------------------------------------------------------------------------

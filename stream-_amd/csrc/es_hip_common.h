@@ -1,0 +1,70 @@
+// Shared device helpers and the job record of the quantized products. Included by the .hip translation units only.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "es_hip_quant.h"
+
+namespace esq {
+
+constexpr int WAVE = 64;
+
+// Block geometry of the five formats (reference src/es_quant.c:11-19, src/es_q2k.h:24-38):
+//   BE elements per block, BB bytes per block, AB bytes of the matching activation block (Q8_0 36, Q8_K 292),
+//   LPB lanes that share one block in the decode kernels.
+template <int F> struct Fmt;
+template <> struct Fmt<ES_HIP_Q4_0> { static constexpr int BE = 32, BB = 18, AB = 36, LPB = 1; };
+template <> struct Fmt<ES_HIP_Q5_0> { static constexpr int BE = 32, BB = 22, AB = 36, LPB = 1; };
+template <> struct Fmt<ES_HIP_Q2_K> { static constexpr int BE = 256, BB = 84, AB = 292, LPB = 8; };
+template <> struct Fmt<ES_HIP_Q4_K> { static constexpr int BE = 256, BB = 144, AB = 292, LPB = 8; };
+template <> struct Fmt<ES_HIP_Q6_K> { static constexpr int BE = 256, BB = 210, AB = 292, LPB = 8; };
+
+// One product handed to a kernel: rows [r0, r1) of W against na activations. Tiles of `rows_per_wg` rows, one per
+// workgroup, numbered from tile0 across the jobs of a launch.
+struct MvJob {
+    const uint8_t *W;     // row 0
+    const uint8_t *act;   // activation 0's first block
+    float *y;             // activation q's row r at y[q * ystride + r]
+    int32_t *ints;        // optional: per (row, block) integer dots of activation 0 (diagnostics), else null
+    int32_t *ints_aux;
+    uint64_t astride;     // bytes between activations
+    uint64_t ystride;     // floats between activations' outputs
+    uint64_t row_bytes;
+    int r0, r1, cols, na;
+    int tile0, rows_per_wg, chain_rows;
+    int pad_;
+};
+
+// One launch of the decode kernel: format, activations per pass, block chunks per lane, workgroups, LDS bytes.
+struct MvLaunch {
+    int type, nt, cpr;
+    int grid;
+    size_t lds;
+};
+hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s);
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    // exact for every finite half, subnormals included (v_cvt_f32_f16)
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xffffu)));
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// ({hi, lo} >> 8 * sel)[31:0]
+__device__ __forceinline__ uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sel);
+}
+
+template <typename T> __device__ __forceinline__ T ldg(const void *p) { return *reinterpret_cast<const T *>(p); }
+
+// Sum over groups of G consecutive lanes (G = 1, 2, 4, 8); every lane of a group ends with the group's sum.
+template <int G> __device__ __forceinline__ int group_sum(int v) {
+    if constexpr (G >= 2) v += __shfl_xor(v, 1);
+    if constexpr (G >= 4) v += __shfl_xor(v, 2);
+    if constexpr (G >= 8) v += __shfl_xor(v, 4);
+    return v;
+}
+
+}  // namespace esq

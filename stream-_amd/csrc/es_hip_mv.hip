@@ -1,0 +1,481 @@
+// Decode / small-batch products on the vector ALU (v_dot4_i32_i8), all five formats.
+//
+// One wave per workgroup owns `rows_per_wg` consecutive rows of one job. Two phases per batch of `chain_rows` rows:
+//
+//  1. Integer phase, block-parallel and coalesced. The wave's 64 lanes are cut into slots of LPB lanes; each slot takes one
+//     weight block (consecutive slots take consecutive blocks, so a wave-wide load covers a contiguous byte range) and each
+//     lane of the slot takes a fixed share of the block's elements. The lane unpacks its share into int8 lanes, dots it with
+//     the activation bytes it holds in registers (v_dot4) and the slot sums the partials (shuffles). Integer arithmetic is
+//     exact, so the order of these sums does not matter. The slot leader turns the block's integers into the float terms of
+//     the reference epilogue and stores them in LDS.
+//  2. Float phase, one lane per (row, activation[, AVX2 lane]). The lane runs the reference's accumulation over the row's
+//     blocks in the reference's order (a strict sequential fp32 chain), so outputs are bit-identical to the CPU kernels.
+//
+// The activation slice a lane needs depends only on its block position inside the row, which stays fixed while the wave
+// walks down the rows, so activations are loaded into registers once per batch of NT activations.
+//
+// Reference kernels restated (integer parts and float order): src/es_quant.c:1013-1117 (scalar mv_*), 1252-1343 and
+// 1443-1469 (AVX2 Q4_0/Q5_0/Q4_K/Q6_K), 1344-1368 and src/es_q2k.c:127-190 (Q2_K).
+#include "es_hip_common.h"
+
+namespace esq {
+
+// float terms of one block for one activation, consumed by the chain:
+//   K-quants and the scalar 32-wide path: s = s (+) A (x) B in the selected order
+//   AVX2 32-wide path: acc_i = fma((float)lane_i, dyd, acc_i) for the eight AVX2 lanes
+struct Term2 { float a, b; };
+
+enum { CH_FMA = 0, CH_MULADD = 1, CH_LANES = 2 };
+
+__device__ __forceinline__ float chain_step(int mode, float s, float a, float b) {
+    return mode == CH_FMA ? __builtin_fmaf(a, b, s) : s + a * b;   // built with -ffp-contract=off: s + a*b rounds twice
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// Per-format lane work
+
+template <int F> struct Lane;
+
+// Q4_K: lane k of 8 takes qs bytes [16k, 16k+16): chunk c = k/2, half h = k%2; its low nibbles are elements
+// 64c + 16h + [0,16) (sub-block 2c), its high nibbles 64c + 32 + 16h + [0,16) (sub-block 2c+1). src/es_quant.c:1056-1080.
+template <> struct Lane<ES_HIP_Q4_K> {
+    struct Act { uint32_t lo[4], hi[4]; int bs0, bs1; float d; };
+    struct Wt { uint32_t lo[4], hi[4]; int sc0, sc1, mn0, mn1; float d, dmin; };
+    struct Ints { int dot, aux; };
+
+    static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
+        const int c = k >> 1, h = k & 1;
+        x.d = ldg<float>(a);
+        const uint4 v0 = ldg<uint4>(a + 4 + 64 * c + 16 * h), v1 = ldg<uint4>(a + 4 + 64 * c + 32 + 16 * h);
+        x.lo[0] = v0.x; x.lo[1] = v0.y; x.lo[2] = v0.z; x.lo[3] = v0.w;
+        x.hi[0] = v1.x; x.hi[1] = v1.y; x.hi[2] = v1.z; x.hi[3] = v1.w;
+        const int16_t *bs = reinterpret_cast<const int16_t *>(a + 260);
+        x.bs0 = bs[4 * c + h];
+        x.bs1 = bs[4 * c + 2 + h];
+    }
+    static __device__ __forceinline__ void zero_act(Act &x) {
+        for (int i = 0; i < 4; i++) x.lo[i] = x.hi[i] = 0;
+        x.bs0 = x.bs1 = 0;
+        x.d = 0.0f;
+    }
+    // 6-bit scale and min of sub-block j from the 12 packed bytes (scale_min_k4, src/es_quant.c:75-83)
+    static __device__ __forceinline__ void scale_min(uint32_t s03, uint32_t s47, uint32_t s811, int j, int &sc, int &mn) {
+        const int jj = (j & 3) * 8;
+        const uint32_t a = (s03 >> jj) & 0xff, b = (s47 >> jj) & 0xff, c = (s811 >> jj) & 0xff;
+        if (j < 4) { sc = a & 63; mn = b & 63; }
+        else { sc = (c & 15) | ((a >> 6) << 4); mn = (c >> 4) | ((b >> 6) << 4); }
+    }
+    static __device__ __forceinline__ void load_w(const uint8_t *blk, int k, Wt &w) {
+        const uint4 hdr = ldg<uint4>(blk);
+        const uint4 q = ldg<uint4>(blk + 16 + 16 * k);
+        const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+        for (int i = 0; i < 4; i++) { w.lo[i] = qq[i] & 0x0f0f0f0fu; w.hi[i] = (qq[i] >> 4) & 0x0f0f0f0fu; }
+        const int c = k >> 1;
+        scale_min(hdr.y, hdr.z, hdr.w, 2 * c, w.sc0, w.mn0);
+        scale_min(hdr.y, hdr.z, hdr.w, 2 * c + 1, w.sc1, w.mn1);
+        w.d = half_bits_to_float(hdr.x);
+        w.dmin = half_bits_to_float(hdr.x >> 16);
+    }
+    static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
+        int lo = 0, hi = 0;
+        for (int i = 0; i < 4; i++) { lo = sdot4(w.lo[i], x.lo[i], lo); hi = sdot4(w.hi[i], x.hi[i], hi); }
+        return {w.sc0 * lo + w.sc1 * hi, w.mn0 * x.bs0 + w.mn1 * x.bs1};
+    }
+    // s += y.d * (d * dot - dmin * mins)   (src/es_quant.c:1077, 1339)
+    static __device__ __forceinline__ Term2 term(const Wt &w, const Act &x, Ints v, bool contract) {
+        const float q = w.dmin * static_cast<float>(v.aux);
+        const float in = contract ? __builtin_fmaf(w.d, static_cast<float>(v.dot), -q) : w.d * static_cast<float>(v.dot) - q;
+        return {x.d, in};
+    }
+};
+
+// Q6_K: lane k of 8: half h = k/4, j = (k/2)%2, p = k%2. It takes ql[64h + 32p + 16j, +16) and qh[32h + 16j, +16);
+// low nibbles (with qh bits 2p, 2p+1) are group g1 = 8h + 2p + j, high nibbles (qh bits 2p+4, 2p+5) group g1 + 4, where a
+// group is 16 consecutive elements with one int8 scale. The 6-bit codes are dotted unsigned and corrected by
+// 32 * bsums (the same integer as the signed form). src/es_quant.c:1081-1117, 1443-1469.
+template <> struct Lane<ES_HIP_Q6_K> {
+    struct Act { uint32_t y1[4], y2[4]; int bs1, bs2; float d; };
+    struct Wt { uint32_t q1[4], q2[4]; int sc1, sc2; float d; };
+    struct Ints { int dot, aux; };
+
+    static __device__ __forceinline__ int g1_of(int k) { return 8 * (k >> 2) + 2 * (k & 1) + ((k >> 1) & 1); }
+    static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
+        const int g1 = g1_of(k), g2 = g1 + 4;
+        x.d = ldg<float>(a);
+        const uint4 v0 = ldg<uint4>(a + 4 + 16 * g1), v1 = ldg<uint4>(a + 4 + 16 * g2);
+        x.y1[0] = v0.x; x.y1[1] = v0.y; x.y1[2] = v0.z; x.y1[3] = v0.w;
+        x.y2[0] = v1.x; x.y2[1] = v1.y; x.y2[2] = v1.z; x.y2[3] = v1.w;
+        const int16_t *bs = reinterpret_cast<const int16_t *>(a + 260);
+        x.bs1 = bs[g1];
+        x.bs2 = bs[g2];
+    }
+    static __device__ __forceinline__ void zero_act(Act &x) {
+        for (int i = 0; i < 4; i++) x.y1[i] = x.y2[i] = 0;
+        x.bs1 = x.bs2 = 0;
+        x.d = 0.0f;
+    }
+    // 16 bytes at a 2-byte aligned address inside the block, from five aligned dwords (all inside the block: the block
+    // starts at a 4-byte aligned address or 2 bytes past one, and the last 16-byte field read here ends 18 bytes before
+    // the block's end)
+    static __device__ __forceinline__ void ld16(const uint8_t *p, uint32_t out[4]) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+        const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~static_cast<uintptr_t>(3));
+        const uint32_t sel = static_cast<uint32_t>(a & 3);
+        const uint4 v = ldg<uint4>(base);
+        const uint32_t w4 = base[4];
+        out[0] = alignbyte(v.y, v.x, sel);
+        out[1] = alignbyte(v.z, v.y, sel);
+        out[2] = alignbyte(v.w, v.z, sel);
+        out[3] = alignbyte(w4, v.w, sel);
+    }
+    static __device__ __forceinline__ void load_w(const uint8_t *blk, int k, Wt &w) {
+        const int h = k >> 2, j = (k >> 1) & 1, p = k & 1;
+        uint32_t ql[4], qh[4];
+        ld16(blk + 64 * h + 32 * p + 16 * j, ql);
+        ld16(blk + 128 + 32 * h + 16 * j, qh);
+        const int sl = 2 * p, sh = 2 * p + 4;
+        for (int i = 0; i < 4; i++) {
+            w.q1[i] = (ql[i] & 0x0f0f0f0fu) | (((qh[i] >> sl) & 0x03030303u) << 4);
+            w.q2[i] = ((ql[i] >> 4) & 0x0f0f0f0fu) | (((qh[i] >> sh) & 0x03030303u) << 4);
+        }
+        const int g1 = g1_of(k);
+        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192);
+        w.sc1 = sc[g1];
+        w.sc2 = sc[g1 + 4];
+        w.d = half_bits_to_float(*reinterpret_cast<const uint16_t *>(blk + 208));
+    }
+    static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
+        int s1 = 0, s2 = 0;
+        for (int i = 0; i < 4; i++) { s1 = sdot4(w.q1[i], x.y1[i], s1); s2 = sdot4(w.q2[i], x.y2[i], s2); }
+        return {w.sc1 * (s1 - 32 * x.bs1) + w.sc2 * (s2 - 32 * x.bs2), 0};
+    }
+    // s += y.d * d * tot   (src/es_quant.c:1114, 1466)
+    static __device__ __forceinline__ Term2 term(const Wt &w, const Act &x, Ints v, bool) {
+        return {x.d * w.d, static_cast<float>(v.dot)};
+    }
+};
+
+// Q2_K: lane k of 8: half h = k/4, part = (k/2)%2, sub = k%2. It takes qs[32h + 16part + 8sub, +8); shift 2s of those
+// bytes holds elements 16g + 8sub + [0,8) of group g = 8h + 2s + part (weight order of src/es_q2k.h:1-15).
+// isum = sum_g (sc[g] & 15) * sum q*y; summs = sum_g bsums[g] * (sc[g] >> 4), added once per group (sub 0 lanes).
+// src/es_q2k.c:127-148, src/es_quant.c:1344-1368.
+template <> struct Lane<ES_HIP_Q2_K> {
+    struct Act { uint32_t y[4][2]; int bs[4]; float d; };
+    struct Wt { uint32_t q[2]; int scl[4], mn[4]; float d, dmin; };
+    struct Ints { int dot, aux; };
+
+    static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
+        const int h = k >> 2, part = (k >> 1) & 1, sub = k & 1;
+        x.d = ldg<float>(a);
+        const int16_t *bs = reinterpret_cast<const int16_t *>(a + 260);
+        for (int s = 0; s < 4; s++) {
+            const int g = 8 * h + 2 * s + part;
+            const uint2 v = ldg<uint2>(a + 4 + 16 * g + 8 * sub);
+            x.y[s][0] = v.x;
+            x.y[s][1] = v.y;
+            x.bs[s] = sub == 0 ? bs[g] : 0;
+        }
+    }
+    static __device__ __forceinline__ void zero_act(Act &x) {
+        for (int s = 0; s < 4; s++) { x.y[s][0] = x.y[s][1] = 0; x.bs[s] = 0; }
+        x.d = 0.0f;
+    }
+    static __device__ __forceinline__ void load_w(const uint8_t *blk, int k, Wt &w) {
+        const int h = k >> 2, part = (k >> 1) & 1, sub = k & 1;
+        const uint2 q = ldg<uint2>(blk + 16 + 32 * h + 16 * part + 8 * sub);
+        w.q[0] = q.x;
+        w.q[1] = q.y;
+        const uint2 sc = ldg<uint2>(blk + 8 * h);   // scales[8h .. 8h+8): byte 2s + part is group 8h + 2s + part
+        for (int s = 0; s < 4; s++) {
+            const int byte = 2 * s + part;
+            const uint32_t v = ((byte < 4 ? sc.x : sc.y) >> (8 * (byte & 3))) & 0xff;
+            w.scl[s] = v & 15;
+            w.mn[s] = v >> 4;
+        }
+        const uint32_t dd = ldg<uint32_t>(blk + 80);
+        w.d = half_bits_to_float(dd);
+        w.dmin = half_bits_to_float(dd >> 16);
+    }
+    static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
+        int isum = 0, summs = 0;
+        for (int s = 0; s < 4; s++) {
+            const uint32_t m = 0x03030303u;
+            int p = sdot4((w.q[0] >> (2 * s)) & m, x.y[s][0], 0);
+            p = sdot4((w.q[1] >> (2 * s)) & m, x.y[s][1], p);
+            isum += w.scl[s] * p;
+            summs += x.bs[s] * w.mn[s];
+        }
+        return {isum, summs};
+    }
+    // s += dall*isum - dmin*summs with dall = y.d*d, dmin = y.d*dmin   (src/es_q2k.c:142-146, src/es_quant.c:1364-1365)
+    static __device__ __forceinline__ Term2 term(const Wt &w, const Act &x, Ints v, bool contract) {
+        const float dall = x.d * w.d, dmn = x.d * w.dmin;
+        const float q = dmn * static_cast<float>(v.aux);
+        const float in = contract ? __builtin_fmaf(dall, static_cast<float>(v.dot), -q) : dall * static_cast<float>(v.dot) - q;
+        return {1.0f, in};   // chain: s + 1*in == s + in in both orders
+    }
+};
+
+// Q4_0 / Q5_0: one lane per 32-element block. AVX2 lane i of the reference sums elements 4i..4i+3 (one v_dot4 here):
+// lane_i = sum (code - offset) * y over those four elements, formed as dot(code, y) - offset * sum(y).
+// src/es_quant.c:1013-1055 (scalar), 1252-1323 (AVX2).
+template <int F> struct Lane32 {
+    static constexpr int OFF = F == ES_HIP_Q4_0 ? 8 : 16;
+    struct Act { uint32_t y[8]; int ns[8]; float d; };   // ns[i] = -OFF * (sum of the four bytes of y[i])
+    struct Wt { uint32_t q[8]; float d; };
+    struct Ints { int lane[8]; };
+
+    static __device__ __forceinline__ void load_act(const uint8_t *a, int, Act &x) {
+        x.d = ldg<float>(a);
+        const uint4 v0 = ldg<uint4>(a + 4), v1 = ldg<uint4>(a + 20);
+        x.y[0] = v0.x; x.y[1] = v0.y; x.y[2] = v0.z; x.y[3] = v0.w;
+        x.y[4] = v1.x; x.y[5] = v1.y; x.y[6] = v1.z; x.y[7] = v1.w;
+        for (int i = 0; i < 8; i++) x.ns[i] = -OFF * sdot4(0x01010101u, x.y[i], 0);
+    }
+    static __device__ __forceinline__ void zero_act(Act &x) {
+        for (int i = 0; i < 8; i++) { x.y[i] = 0; x.ns[i] = 0; }
+        x.d = 0.0f;
+    }
+    // The block starts 2-aligned. A 16-byte load at the 4-aligned one of blk / blk+2 plus 2- and 4-byte loads for the
+    // rest reads exactly the block's bytes.
+    static __device__ __forceinline__ void load_w(const uint8_t *blk, int, Wt &w) {
+        const uint32_t par = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk) & 2);
+        uint32_t qs[4], d16, qh = 0;
+        if constexpr (F == ES_HIP_Q4_0) {   // d f16 @0, qs[16] @2
+            const uint4 v = ldg<uint4>(blk + par);
+            const uint32_t u = *reinterpret_cast<const uint16_t *>(par ? blk : blk + 16);
+            if (par == 0) {
+                d16 = v.x;
+                qs[0] = alignbyte(v.y, v.x, 2); qs[1] = alignbyte(v.z, v.y, 2);
+                qs[2] = alignbyte(v.w, v.z, 2); qs[3] = alignbyte(u, v.w, 2);
+            } else {
+                d16 = u;
+                qs[0] = v.x; qs[1] = v.y; qs[2] = v.z; qs[3] = v.w;
+            }
+        } else {                            // d f16 @0, qh u32 @2, qs[16] @6
+            const uint4 v = ldg<uint4>(blk + par);
+            const uint32_t w4 = ldg<uint32_t>(blk + par + 16);
+            const uint32_t u = *reinterpret_cast<const uint16_t *>(par ? blk : blk + 20);
+            if (par == 0) {
+                d16 = v.x;
+                qh = alignbyte(v.y, v.x, 2);
+                qs[0] = alignbyte(v.z, v.y, 2); qs[1] = alignbyte(v.w, v.z, 2);
+                qs[2] = alignbyte(w4, v.w, 2); qs[3] = alignbyte(u, w4, 2);
+            } else {
+                d16 = u;
+                qh = v.x;
+                qs[0] = v.y; qs[1] = v.z; qs[2] = v.w; qs[3] = w4;
+            }
+        }
+        for (int i = 0; i < 4; i++) { w.q[i] = qs[i] & 0x0f0f0f0fu; w.q[i + 4] = (qs[i] >> 4) & 0x0f0f0f0fu; }
+        if constexpr (F == ES_HIP_Q5_0) {   // fifth bit of element e is bit e of qh
+            for (int i = 0; i < 8; i++) {
+                const uint32_t nib = (qh >> (4 * i)) & 15u;
+                w.q[i] |= ((nib * 0x00204081u) & 0x01010101u) << 4;
+            }
+        }
+        w.d = half_bits_to_float(d16);
+    }
+    static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
+        Ints v;
+        for (int i = 0; i < 8; i++) v.lane[i] = sdot4(w.q[i], x.y[i], x.ns[i]);
+        return v;
+    }
+};
+template <> struct Lane<ES_HIP_Q4_0> : Lane32<ES_HIP_Q4_0> {};
+template <> struct Lane<ES_HIP_Q5_0> : Lane32<ES_HIP_Q5_0> {};
+
+template <int F> constexpr bool is32() { return F == ES_HIP_Q4_0 || F == ES_HIP_Q5_0; }
+
+// ---------------------------------------------------------------------------------------------------------------------
+// The kernel
+
+__device__ __forceinline__ int find_job(const MvJob *jobs, int njobs, int bid) {
+    int lo = 0, hi = njobs - 1;   // last job with tile0 <= bid
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (jobs[mid].tile0 <= bid) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// order: ES_HIP_ORDER_*; NT activations per pass; CPR = most blocks per lane slot in one row (nb <= CPR * slots).
+template <int F, int NT, int CPR>
+__global__ __launch_bounds__(WAVE) void mv_kernel(const MvJob *__restrict__ jobs, int njobs, MvJob single, int order) {
+    using L = Lane<F>;
+    constexpr int LPB = Fmt<F>::LPB, BE = Fmt<F>::BE, BB = Fmt<F>::BB, AB = Fmt<F>::AB;
+    constexpr int SLOTS = WAVE / LPB;
+    constexpr bool W32 = is32<F>();
+
+    MvJob J;
+    if (jobs) J = jobs[find_job(jobs, njobs, blockIdx.x)];
+    else J = single;
+    const int nbk = J.cols / BE;
+    const int tile = blockIdx.x - J.tile0;
+    const int ra0 = J.r0 + tile * J.rows_per_wg;
+    const int rend = min(ra0 + J.rows_per_wg, J.r1);
+
+    const int lane = threadIdx.x;
+    const int slot = lane / LPB, k = lane % LPB;
+    int rpi, rowoff, bpos;
+    if (nbk <= SLOTS) { rpi = SLOTS / nbk; rowoff = slot / nbk; bpos = slot % nbk; }
+    else { rpi = 1; rowoff = 0; bpos = slot; }
+    const bool slot_live = rowoff < rpi;
+
+    // chain mode
+    const bool x86 = order != ES_HIP_ORDER_SCALAR;
+    const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
+    const int cmode = W32 ? (x86 ? CH_LANES : CH_MULADD) : (contract ? CH_FMA : CH_MULADD);
+    constexpr int CW = W32 ? 9 : 2;   // floats per (row, block, activation) in LDS
+    extern __shared__ float lds[];
+
+    for (int t0 = 0; t0 < J.na; t0 += NT) {
+        const int nt = min(NT, J.na - t0);
+        typename L::Act act[CPR][NT];
+#pragma unroll
+        for (int c = 0; c < CPR; c++) {
+            const int b = bpos + c * SLOTS;
+            const bool ok = slot_live && b < nbk;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                if (ok && t < nt) L::load_act(J.act + (size_t)(t0 + t) * J.astride + (size_t)b * AB, k, act[c][t]);
+                else L::zero_act(act[c][t]);
+            }
+        }
+
+        for (int ra = ra0; ra < rend; ra += J.chain_rows) {
+            const int rb = min(ra + J.chain_rows, rend);
+            // ---- phase 1: integers per block, float terms to LDS
+            for (int r = ra; r < rb; r += rpi) {
+                const int row = r + rowoff;
+                const bool row_ok = slot_live && row < rb;
+                const uint8_t *wrow = J.W + (size_t)row * J.row_bytes;
+#pragma unroll
+                for (int c = 0; c < CPR; c++) {
+                    const int b = bpos + c * SLOTS;
+                    const bool ok = row_ok && b < nbk;
+                    typename L::Wt w;
+                    typename L::Ints v[NT];
+                    if (ok) {
+                        L::load_w(wrow + (size_t)b * BB, k, w);
+#pragma unroll
+                        for (int t = 0; t < NT; t++) v[t] = L::ints(w, act[c][t]);
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < NT; t++) v[t] = typename L::Ints{};
+                    }
+                    if constexpr (!W32) {
+#pragma unroll
+                        for (int t = 0; t < NT; t++) { v[t].dot = group_sum<LPB>(v[t].dot); v[t].aux = group_sum<LPB>(v[t].aux); }
+                    }
+                    if (ok && k == 0) {
+                        float *e = lds + ((size_t)(row - ra) * nbk + b) * NT * CW;
+                        if constexpr (W32) {
+#pragma unroll
+                            for (int t = 0; t < NT; t++) {
+                                const float dyd = w.d * act[c][t].d;
+                                if (cmode == CH_LANES) {
+                                    e[t * CW] = dyd;
+                                    for (int i = 0; i < 8; i++) e[t * CW + 1 + i] = static_cast<float>(v[t].lane[i]);
+                                } else {
+                                    int a = 0;
+                                    for (int i = 0; i < 8; i++) a += v[t].lane[i];
+                                    e[t * CW] = dyd;
+                                    e[t * CW + 1] = static_cast<float>(a);
+                                }
+                            }
+                            if (J.ints && t0 == 0) {
+                                int a = 0;
+                                for (int i = 0; i < 8; i++) a += v[0].lane[i];
+                                J.ints[(size_t)row * nbk + b] = a;
+                                J.ints_aux[(size_t)row * nbk + b] = 0;
+                            }
+                        } else {
+#pragma unroll
+                            for (int t = 0; t < NT; t++) {
+                                const Term2 tm = L::term(w, act[c][t], v[t], contract);
+                                e[t * CW] = tm.a;
+                                e[t * CW + 1] = tm.b;
+                            }
+                            if (J.ints && t0 == 0) {
+                                J.ints[(size_t)row * nbk + b] = v[0].dot;
+                                J.ints_aux[(size_t)row * nbk + b] = v[0].aux;
+                            }
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            // ---- phase 2: the reference's sequential accumulation over the row's blocks
+            const int nrow = rb - ra;
+            const int per = cmode == CH_LANES ? 8 : 1;
+            for (int idx = lane; idx < nrow * NT * per; idx += WAVE) {
+                const int i = idx % per, t = (idx / per) % NT, rl = idx / (per * NT);
+                const float *e = lds + (size_t)rl * nbk * NT * CW + t * CW;
+                float s = 0.0f;
+                if (cmode == CH_LANES) {
+                    for (int b = 0; b < nbk; b++, e += NT * CW) s = __builtin_fmaf(e[1 + i], e[0], s);
+                } else if (cmode == CH_FMA) {
+                    for (int b = 0; b < nbk; b++, e += NT * CW) s = __builtin_fmaf(e[0], e[1], s);
+                } else {
+                    for (int b = 0; b < nbk; b++, e += NT * CW) s = s + e[0] * e[1];
+                }
+                if (cmode == CH_LANES) {   // hsum_ps of the eight lanes: ((0+4)+(2+6))+((1+5)+(3+7))  (src/es_quant.c:1185-1187)
+                    s = s + __shfl_xor(s, 4);
+                    s = s + __shfl_xor(s, 2);
+                    s = s + __shfl_xor(s, 1);
+                }
+                if (i == 0 && t < nt) J.y[(size_t)(t0 + t) * J.ystride + ra + rl] = s;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+}  // namespace esq
+
+// ---------------------------------------------------------------------------------------------------------------------
+// Launch glue (called from es_hip_quant.cpp)
+
+namespace esq {
+
+using MvFn = void (*)(const MvJob *, int, MvJob, int);
+
+template <int F, int NT> static MvFn pick_cpr(int cpr) {
+    switch (cpr) {
+    case 1: return mv_kernel<F, NT, 1>;
+    case 2: return mv_kernel<F, NT, 2>;
+    case 4: return mv_kernel<F, NT, 4>;
+    case 8: return mv_kernel<F, NT, 8>;
+    }
+    return nullptr;
+}
+template <int F> static MvFn pick_nt(int nt, int cpr) {
+    switch (nt) {
+    case 1: return pick_cpr<F, 1>(cpr);
+    case 2: return pick_cpr<F, 2>(cpr);
+    case 4: return pick_cpr<F, 4>(cpr);
+    }
+    return nullptr;
+}
+
+hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s) {
+    MvFn fn = nullptr;
+    switch (L.type) {
+    case ES_HIP_Q4_0: fn = pick_nt<ES_HIP_Q4_0>(L.nt, L.cpr); break;
+    case ES_HIP_Q5_0: fn = pick_nt<ES_HIP_Q5_0>(L.nt, L.cpr); break;
+    case ES_HIP_Q2_K: fn = pick_nt<ES_HIP_Q2_K>(L.nt, L.cpr); break;
+    case ES_HIP_Q4_K: fn = pick_nt<ES_HIP_Q4_K>(L.nt, L.cpr); break;
+    case ES_HIP_Q6_K: fn = pick_nt<ES_HIP_Q6_K>(L.nt, L.cpr); break;
+    }
+    if (!fn) return hipErrorInvalidValue;
+    if (L.lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(L.lds));
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fn, dim3(L.grid), dim3(WAVE), L.lds, s, jobs, njobs, single, order);
+    return hipGetLastError();
+}
+
+}  // namespace esq

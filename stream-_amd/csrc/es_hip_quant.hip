@@ -1,0 +1,552 @@
+// Host side of libes_hip_quant.so: the C ABI declared in include/es_hip_quant.h.
+//
+// It validates shapes and pointers, turns a queue of products (the reference engine's jobn/run_jobs,
+// src/es_engine.c:144-186) into one launch per weight format with a device-side job table, keeps registered host weights
+// resident on the device byte-for-byte, and offers the reference's host-memory prototypes (es_matvec /
+// es_matvec_multi, src/es_quant.h:44-47) on top. There is no CPU compute path: without a gfx950 device every compute entry
+// point fails with ES_HIP_ENODEV.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "es_hip_common.h"
+
+using esq::MvJob;
+using esq::MvLaunch;
+
+namespace {
+
+thread_local std::string g_err;
+std::atomic<int> g_order{ES_HIP_ORDER_X86_CONTRACT};
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(e == hipErrorOutOfMemory ? ES_HIP_ENOMEM : ES_HIP_ERUNTIME, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ---- device discovery ---------------------------------------------------------------------------------------------
+struct Device {
+    int ok = 0;
+    int id = -1;
+    std::string arch, why;
+};
+
+Device &device() {
+    static Device d;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int n = 0;
+        hipError_t e = hipGetDeviceCount(&n);
+        if (e != hipSuccess || n == 0) {
+            d.why = std::string("no HIP device: ") + (e != hipSuccess ? hipGetErrorString(e) : "device count is 0");
+            return;
+        }
+        int cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess) cur = 0;
+        hipDeviceProp_t p;
+        if ((e = hipGetDeviceProperties(&p, cur)) != hipSuccess) {
+            d.why = std::string("hipGetDeviceProperties: ") + hipGetErrorString(e);
+            return;
+        }
+        d.arch = p.gcnArchName;
+        if (d.arch.compare(0, 6, "gfx950") != 0) {
+            d.why = "device " + std::to_string(cur) + " is " + d.arch + ", this library is built for gfx950 only";
+            return;
+        }
+        d.id = cur;
+        d.ok = 1;
+    });
+    return d;
+}
+
+int need_device() {
+    Device &d = device();
+    if (!d.ok) return fail(ES_HIP_ENODEV, "%s", d.why.c_str());
+    return ES_HIP_OK;
+}
+
+// ---- formats --------------------------------------------------------------------------------------------------------
+struct FmtInfo {
+    int be, bb, ab, lpb;
+};
+
+bool fmt_info(uint32_t t, FmtInfo &f) {
+    switch (t) {
+    case ES_HIP_Q4_0: f = {32, 18, 36, 1}; return true;
+    case ES_HIP_Q5_0: f = {32, 22, 36, 1}; return true;
+    case ES_HIP_Q2_K: f = {256, 84, 292, 8}; return true;
+    case ES_HIP_Q4_K: f = {256, 144, 292, 8}; return true;
+    case ES_HIP_Q6_K: f = {256, 210, 292, 8}; return true;
+    }
+    return false;
+}
+
+// ---- job batches ----------------------------------------------------------------------------------------------------
+constexpr size_t LDS_TARGET = 16 * 1024;   // bytes of chain terms per workgroup when the row length allows
+constexpr size_t LDS_MAX = 160 * 1024;      // gfx950 LDS per workgroup
+constexpr int MIN_WG_PER_JOB = 1024;        // at least this many workgroups per job when it has the rows
+
+struct Group {
+    MvLaunch L{};
+    std::vector<MvJob> jobs;
+};
+
+struct Req {   // one product as the launch planner sees it
+    uint32_t type;
+    const void *W, *act;
+    float *y;
+    int32_t *ints, *aux;
+    int r0, r1, cols, na;
+    size_t astride, ystride;
+};
+
+int check_req(const Req &q, const FmtInfo &f) {
+    if (q.cols <= 0 || q.cols % f.be) return fail(ES_HIP_EINVAL, "type %u: cols %d is not a positive multiple of %d", q.type, q.cols, f.be);
+    if (q.r0 < 0 || q.r1 < q.r0) return fail(ES_HIP_EINVAL, "bad row range [%d, %d)", q.r0, q.r1);
+    if (q.na < 0) return fail(ES_HIP_EINVAL, "negative activation count %d", q.na);
+    if (q.r1 == q.r0 || q.na == 0) return ES_HIP_OK;
+    if (!q.W || !q.act || !q.y) return fail(ES_HIP_EINVAL, "null W, activation or output pointer");
+    if (reinterpret_cast<uintptr_t>(q.W) & 3) return fail(ES_HIP_EINVAL, "W must be 4-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(q.act) & 3) || (q.astride & 3))
+        return fail(ES_HIP_EINVAL, "activation blocks must be 4-byte aligned (pointer and stride)");
+    if (reinterpret_cast<uintptr_t>(q.y) & 3) return fail(ES_HIP_EINVAL, "y must be 4-byte aligned");
+    const size_t packed = (size_t)(q.cols / f.be) * f.ab;
+    if (q.na > 1 && q.astride < packed) return fail(ES_HIP_EINVAL, "activation stride %zu < %zu bytes of one activation", q.astride, packed);
+    if (q.na > 1 && q.ystride < (size_t)q.r1) return fail(ES_HIP_EINVAL, "ystride %zu < r1 %d: outputs of activations overlap", q.ystride, q.r1);
+    const int slots = 64 / f.lpb, nbk = q.cols / f.be;
+    if (nbk > 8 * slots) return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this kernel handles", q.type, q.cols, 8 * slots * f.be);
+    return ES_HIP_OK;
+}
+
+int pow2_at_least(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+// Plan one launch per format. The job order inside a format is kept.
+int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
+    out.clear();
+    std::map<uint32_t, std::vector<const Req *>> by_type;
+    for (const Req &q : reqs) {
+        FmtInfo f;
+        if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
+        int rc = check_req(q, f);
+        if (rc) return rc;
+        if (q.r1 > q.r0 && q.na > 0) by_type[q.type].push_back(&q);
+    }
+    for (auto &kv : by_type) {
+        FmtInfo f;
+        fmt_info(kv.first, f);
+        const bool w32 = f.be == 32;
+        const int slots = 64 / f.lpb;
+        int cpr = 1, max_na = 1;
+        for (const Req *q : kv.second) {
+            const int nbk = q->cols / f.be;
+            cpr = std::max(cpr, pow2_at_least((nbk + slots - 1) / slots));
+            max_na = std::max(max_na, q->na);
+        }
+        int nt = max_na >= 4 ? 4 : max_na >= 2 ? 2 : 1;
+        const int cap = w32 ? 4 : 8;   // register budget: activation slices per lane
+        while (nt > 1 && nt * cpr > cap) nt >>= 1;
+        Group g;
+        g.L.type = static_cast<int>(kv.first);
+        g.L.nt = nt;
+        g.L.cpr = cpr;
+        int tile = 0;
+        size_t lds = 0;
+        const int cw = w32 ? 9 : 2;
+        for (const Req *q : kv.second) {
+            const int nbk = q->cols / f.be, rows = q->r1 - q->r0;
+            const int rpi = nbk <= slots ? slots / nbk : 1;
+            const size_t per_row = (size_t)nbk * nt * cw * sizeof(float);
+            if (per_row > LDS_MAX) return fail(ES_HIP_EINVAL, "type %u cols %d: a row needs %zu bytes of LDS", q->type, q->cols, per_row);
+            int chain_cap = (int)std::min<size_t>(64, std::max<size_t>(1, LDS_TARGET / per_row));
+            if (chain_cap >= rpi) chain_cap -= chain_cap % rpi;
+            int rpw = std::max(rpi, (rows + MIN_WG_PER_JOB - 1) / MIN_WG_PER_JOB);
+            rpw = (rpw + rpi - 1) / rpi * rpi;
+            const int chain = std::min(chain_cap, rpw);
+            rpw = (rpw + chain - 1) / chain * chain;   // whole chain batches per workgroup
+            MvJob j{};
+            j.W = static_cast<const uint8_t *>(q->W);
+            j.act = static_cast<const uint8_t *>(q->act);
+            j.y = q->y;
+            j.ints = q->ints;
+            j.ints_aux = q->aux;
+            j.astride = q->astride ? q->astride : (size_t)nbk * f.ab;
+            j.ystride = q->ystride;
+            j.row_bytes = (size_t)nbk * f.bb;
+            j.r0 = q->r0;
+            j.r1 = q->r1;
+            j.cols = q->cols;
+            j.na = q->na;
+            j.tile0 = tile;
+            j.rows_per_wg = rpw;
+            j.chain_rows = chain;
+            tile += (rows + rpw - 1) / rpw;
+            lds = std::max(lds, (size_t)chain * per_row);
+            g.jobs.push_back(j);
+        }
+        g.L.grid = tile;
+        g.L.lds = lds;
+        out.push_back(std::move(g));
+    }
+    return ES_HIP_OK;
+}
+
+int launch_single(const Group &g, hipStream_t s) {
+    hipError_t e = esq::mv_launch(g.L, nullptr, 1, g.jobs[0], g_order.load(), s);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "kernel launch");
+}
+
+// ---- reusable device scratch (host drop-ins, run_jobs tables) ----------------------------------------------------
+struct Scratch {
+    std::mutex mu;
+    void *p = nullptr;
+    size_t n = 0;
+    int get(size_t bytes, void **out) {
+        if (bytes > n) {
+            if (p) (void)hipFree(p);
+            p = nullptr;
+            n = 0;
+            size_t want = std::max(bytes, (size_t)1 << 20);
+            hipError_t e = hipMalloc(&p, want);
+            if (e != hipSuccess) return hip_fail(e, "hipMalloc scratch");
+            n = want;
+        }
+        *out = p;
+        return ES_HIP_OK;
+    }
+};
+Scratch g_table, g_wtmp, g_atmp, g_ytmp;
+std::mutex g_call_mu;   // serialises the synchronous convenience entry points that share scratch
+
+// ---- weight registry ------------------------------------------------------------------------------------------------
+struct Reg {
+    size_t bytes;
+    void *dev;
+};
+std::mutex g_reg_mu;
+std::map<uintptr_t, Reg> g_reg;
+
+// device address of host range [h, h + n) if it lies inside one registered range
+void *reg_lookup(const void *h, size_t n) {
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(h);
+    auto it = g_reg.upper_bound(a);
+    if (it == g_reg.begin()) return nullptr;
+    --it;
+    if (a + n > it->first + it->second.bytes) return nullptr;
+    return static_cast<uint8_t *>(it->second.dev) + (a - it->first);
+}
+
+}  // namespace
+
+// =====================================================================================================================
+extern "C" {
+
+int es_hip_available(void) { return need_device() == ES_HIP_OK ? 1 : 0; }
+const char *es_hip_last_error(void) { return g_err.c_str(); }
+const char *es_hip_device_name(void) { return device().arch.c_str(); }
+
+int es_hip_set_order(int order) {
+    if (order < ES_HIP_ORDER_X86_CONTRACT || order > ES_HIP_ORDER_SCALAR) return fail(ES_HIP_EINVAL, "bad order %d", order);
+    return g_order.exchange(order);
+}
+int es_hip_get_order(void) { return g_order.load(); }
+
+int es_hip_quant_supported(uint32_t type) {
+    FmtInfo f;
+    return fmt_info(type, f) ? 1 : 0;
+}
+
+size_t es_hip_row_bytes(uint32_t type, int cols) {
+    FmtInfo f;
+    if (!fmt_info(type, f) || cols < 0) return 0;
+    return (size_t)(cols / f.be) * f.bb;   // src/es_quant.c:39-73: whole blocks
+}
+
+// ---- memory helpers ---------------------------------------------------------------------------------------------------
+void *es_hip_malloc(size_t bytes) {
+    if (need_device()) return nullptr;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) { hip_fail(e, "hipMalloc"); return nullptr; }
+    return p;
+}
+int es_hip_free(void *dev) {
+    if (!dev) return ES_HIP_OK;
+    hipError_t e = hipFree(dev);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipFree");
+}
+int es_hip_memcpy_h2d(void *dev, const void *host, size_t bytes) {
+    if (int rc = need_device()) return rc;
+    hipError_t e = hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipMemcpy H2D");
+}
+int es_hip_memcpy_d2h(void *host, const void *dev, size_t bytes) {
+    if (int rc = need_device()) return rc;
+    hipError_t e = hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipMemcpy D2H");
+}
+int es_hip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    if (int rc = need_device()) return rc;
+    hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipMemcpy D2D");
+}
+int es_hip_memset(void *dev, int value, size_t bytes) {
+    if (int rc = need_device()) return rc;
+    hipError_t e = hipMemset(dev, value, bytes);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipMemset");
+}
+int es_hip_synchronize(void) {
+    if (int rc = need_device()) return rc;
+    hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipDeviceSynchronize");
+}
+
+// ---- products on device memory ----------------------------------------------------------------------------------------
+int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride, int na,
+                            float *y, size_t ystride, void *stream) {
+    if (int rc = need_device()) return rc;
+    std::vector<Req> reqs{{type, W, act, y, nullptr, nullptr, r0, r1, cols, na, astride, ystride}};
+    std::vector<Group> groups;
+    if (int rc = plan_groups(reqs, groups)) return rc;
+    if (groups.empty()) return ES_HIP_OK;
+    return launch_single(groups[0], static_cast<hipStream_t>(stream));
+}
+
+int es_hip_matvec_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, float *y, void *stream) {
+    return es_hip_matvec_multi_dev(type, W, cols, r0, r1, act, 0, 1, y, 0, stream);
+}
+
+int es_hip_block_ints_dev(uint32_t type, const void *W, int cols, int rows, const void *act, int32_t *dots, int32_t *aux,
+                          void *stream) {
+    if (int rc = need_device()) return rc;
+    if (!dots || !aux) return fail(ES_HIP_EINVAL, "null dots/aux");
+    void *ytmp = nullptr;
+    std::lock_guard<std::mutex> lk(g_call_mu);
+    if (int rc = g_ytmp.get((size_t)std::max(rows, 1) * sizeof(float), &ytmp)) return rc;
+    std::vector<Req> reqs{{type, W, act, static_cast<float *>(ytmp), dots, aux, 0, rows, cols, 1, 0, 0}};
+    std::vector<Group> groups;
+    if (int rc = plan_groups(reqs, groups)) return rc;
+    if (groups.empty()) return ES_HIP_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int rc = launch_single(groups[0], s)) return rc;
+    hipError_t e = hipStreamSynchronize(s);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+static void to_reqs(const es_hip_job *jobs, int njobs, std::vector<Req> &reqs) {
+    reqs.clear();
+    for (int i = 0; i < njobs; i++) {
+        const es_hip_job &j = jobs[i];
+        reqs.push_back({j.type, j.W, j.act, j.y, nullptr, nullptr, 0, j.rows, j.cols, j.nb, j.astride, j.ystride});
+    }
+}
+
+int es_hip_run_jobs(const es_hip_job *jobs, int njobs, void *stream) {
+    if (int rc = need_device()) return rc;
+    if (njobs < 0 || (njobs > 0 && !jobs)) return fail(ES_HIP_EINVAL, "bad job list");
+    std::vector<Req> reqs;
+    to_reqs(jobs, njobs, reqs);
+    std::vector<Group> groups;
+    if (int rc = plan_groups(reqs, groups)) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    std::lock_guard<std::mutex> lk(g_call_mu);
+    size_t total = 0;
+    for (auto &g : groups) total += g.jobs.size() * sizeof(MvJob);
+    void *table = nullptr;
+    if (total) {
+        hipError_t e = hipStreamSynchronize(s);   // the table buffer may still be read by an earlier call's kernels
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        if (int rc = g_table.get(total, &table)) return rc;
+    }
+    size_t off = 0;
+    for (auto &g : groups) {
+        MvJob *dj = reinterpret_cast<MvJob *>(static_cast<uint8_t *>(table) + off);
+        hipError_t e = hipMemcpyAsync(dj, g.jobs.data(), g.jobs.size() * sizeof(MvJob), hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return hip_fail(e, "job table upload");
+        e = esq::mv_launch(g.L, dj, (int)g.jobs.size(), g.jobs[0], g_order.load(), s);
+        if (e != hipSuccess) return hip_fail(e, "kernel launch");
+        off += g.jobs.size() * sizeof(MvJob);
+    }
+    hipError_t e = hipStreamSynchronize(s);   // run_jobs returns when every product is done, like the reference's
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+}  // extern "C"
+
+struct es_hip_plan {
+    std::vector<Group> groups;
+    std::vector<MvJob *> tables;
+    int order;
+};
+
+extern "C" {
+
+es_hip_plan *es_hip_plan_create(const es_hip_job *jobs, int njobs) {
+    if (need_device()) return nullptr;
+    if (njobs < 0 || (njobs > 0 && !jobs)) { fail(ES_HIP_EINVAL, "bad job list"); return nullptr; }
+    std::vector<Req> reqs;
+    to_reqs(jobs, njobs, reqs);
+    auto *p = new es_hip_plan();
+    p->order = g_order.load();
+    if (plan_groups(reqs, p->groups)) { delete p; return nullptr; }
+    for (auto &g : p->groups) {
+        MvJob *dj = nullptr;
+        hipError_t e = hipMalloc(&dj, g.jobs.size() * sizeof(MvJob));
+        if (e == hipSuccess) e = hipMemcpy(dj, g.jobs.data(), g.jobs.size() * sizeof(MvJob), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            hip_fail(e, "plan table");
+            if (dj) (void)hipFree(dj);
+            es_hip_plan_destroy(p);
+            return nullptr;
+        }
+        p->tables.push_back(dj);
+    }
+    return p;
+}
+
+int es_hip_plan_run(es_hip_plan *p, void *stream) {
+    if (!p) return fail(ES_HIP_EINVAL, "null plan");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (size_t i = 0; i < p->groups.size(); i++) {
+        const Group &g = p->groups[i];
+        hipError_t e = esq::mv_launch(g.L, p->tables[i], (int)g.jobs.size(), g.jobs[0], p->order, s);
+        if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    }
+    return ES_HIP_OK;
+}
+
+void es_hip_plan_destroy(es_hip_plan *p) {
+    if (!p) return;
+    for (MvJob *t : p->tables) (void)hipFree(t);
+    delete p;
+}
+
+double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
+    if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < warmup; i++)
+        if (es_hip_plan_run(p, stream)) return -1.0;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { fail(ES_HIP_ERUNTIME, "hipEventCreate"); return -1.0; }
+    (void)hipEventRecord(a, s);
+    for (int i = 0; i < iters; i++)
+        if (es_hip_plan_run(p, stream)) return -1.0;
+    (void)hipEventRecord(b, s);
+    (void)hipEventSynchronize(b);
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return (double)ms / iters;
+}
+
+// ---- weight registry and host-memory drop-ins ---------------------------------------------------------------------
+int es_hip_register(const void *host, size_t bytes) {
+    if (int rc = need_device()) return rc;
+    if (!host || !bytes) return fail(ES_HIP_EINVAL, "empty registration");
+    es_hip_unregister(host);
+    void *d = nullptr;
+    hipError_t e = hipMalloc(&d, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc (register)");
+    e = hipMemcpy(d, host, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { (void)hipFree(d); return hip_fail(e, "hipMemcpy (register)"); }
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    g_reg[reinterpret_cast<uintptr_t>(host)] = {bytes, d};
+    return ES_HIP_OK;
+}
+
+int es_hip_update(const void *host) {
+    if (int rc = need_device()) return rc;
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    auto it = g_reg.find(reinterpret_cast<uintptr_t>(host));
+    if (it == g_reg.end()) return fail(ES_HIP_EINVAL, "not registered");
+    hipError_t e = hipMemcpy(it->second.dev, host, it->second.bytes, hipMemcpyHostToDevice);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipMemcpy (update)");
+}
+
+int es_hip_unregister(const void *host) {
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    auto it = g_reg.find(reinterpret_cast<uintptr_t>(host));
+    if (it == g_reg.end()) return ES_HIP_EINVAL;
+    (void)hipFree(it->second.dev);
+    g_reg.erase(it);
+    return ES_HIP_OK;
+}
+
+static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
+                      size_t ystride) {
+    g_err.clear();   // the void drop-ins report failure only through es_hip_last_error()
+    if (int rc = need_device()) return rc;
+    FmtInfo f;
+    if (!fmt_info(type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", type);
+    if (cols <= 0 || cols % f.be || r0 < 0 || r1 < r0 || na < 0) return fail(ES_HIP_EINVAL, "bad shape");
+    if (r1 == r0 || na == 0) return ES_HIP_OK;
+    if (!W || !a || !y) return fail(ES_HIP_EINVAL, "null pointer");
+    const int nbk = cols / f.be;
+    const size_t rb = (size_t)nbk * f.bb, ab = (size_t)nbk * f.ab;
+    const int n = r1 - r0;
+    for (int q = 0; q < na; q++) {
+        const void *blk = f.be == 32 ? static_cast<const void *>(a[q].q80) : static_cast<const void *>(a[q].q8);
+        if (!blk) return fail(ES_HIP_EINVAL, "activation %d has no %s blocks (the reference's float fallback is not provided)", q, f.be == 32 ? "Q8_0" : "Q8_K");
+    }
+    std::lock_guard<std::mutex> lk(g_call_mu);
+    const uint8_t *wsub = static_cast<const uint8_t *>(W) + rb * r0;
+    const void *dW = reg_lookup(wsub, rb * n);
+    void *wt = nullptr, *at = nullptr, *yt = nullptr;
+    hipError_t e;
+    if (!dW) {   // not resident: upload the rows for this call
+        if (int rc = g_wtmp.get(rb * n, &wt)) return rc;
+        if ((e = hipMemcpy(wt, wsub, rb * n, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "weight upload");
+        dW = wt;
+    }
+    if (int rc = g_atmp.get(ab * na, &at)) return rc;
+    std::vector<uint8_t> pack(ab * na);
+    for (int q = 0; q < na; q++) {
+        const void *blk = f.be == 32 ? static_cast<const void *>(a[q].q80) : static_cast<const void *>(a[q].q8);
+        memcpy(pack.data() + ab * q, blk, ab);
+    }
+    if ((e = hipMemcpy(at, pack.data(), pack.size(), hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
+    if (int rc = g_ytmp.get(sizeof(float) * n * na, &yt)) return rc;
+    std::vector<Req> reqs{{type, dW, at, static_cast<float *>(yt), nullptr, nullptr, 0, n, cols, na, ab, (size_t)n}};
+    std::vector<Group> groups;
+    if (int rc = plan_groups(reqs, groups)) return rc;
+    if (int rc = launch_single(groups[0], nullptr)) return rc;
+    std::vector<float> out((size_t)n * na);
+    if ((e = hipMemcpy(out.data(), yt, out.size() * sizeof(float), hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
+    for (int q = 0; q < na; q++) memcpy(y + ystride * q + r0, out.data() + (size_t)n * q, sizeof(float) * n);
+    return ES_HIP_OK;
+}
+
+void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch) {
+    (void)scratch;
+    host_multi(type, W, cols, r0, r1, a, 1, y, 0);
+}
+
+void es_hip_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
+                         size_t ystride, float *scratch) {
+    (void)scratch;
+    host_multi(type, W, cols, r0, r1, a, na, y, ystride);
+}
+
+}  // extern "C"

@@ -1,0 +1,252 @@
+"""ctypes binding of libes_hip_quant.so (the C ABI of include/es_hip_quant.h).
+
+Plumbing for the tests and bench.py: device buffers, job tables and the drop-in entry points, with numpy arrays on the host
+side. Every compute call goes through the HIP library; a failing call raises EsHipError with the library's message, and a
+missing library or device raises too: there is no CPU path here.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libes_hip_quant.so")
+
+Q4_0, Q5_0, Q2_K, Q4_K, Q6_K = 2, 6, 10, 12, 14
+TYPES = {"Q4_0": Q4_0, "Q5_0": Q5_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K}
+ORDER_X86_CONTRACT, ORDER_X86_STRICT, ORDER_SCALAR = 0, 1, 2
+BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q2_K: 256, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q2_K: 84, Q4_K: 144, Q6_K: 210}
+ACT_BYTES = {Q4_0: 36, Q5_0: 36, Q2_K: 292, Q4_K: 292, Q6_K: 292}
+
+
+class EsHipError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"es_hip error {code}: {msg}")
+        self.code = code
+
+
+class Job(C.Structure):   # es_hip_job
+    _fields_ = [("type", C.c_uint32), ("rows", C.c_int), ("cols", C.c_int), ("W", C.c_void_p), ("act", C.c_void_p),
+                ("astride", C.c_size_t), ("nb", C.c_int), ("y", C.c_void_p), ("ystride", C.c_size_t)]
+
+
+class Act(C.Structure):   # es_hip_act (= the reference's es_act)
+    _fields_ = [("x", C.c_void_p), ("q8", C.c_void_p), ("q80", C.c_void_p), ("cols", C.c_int)]
+
+
+def row_bytes(t: int, cols: int) -> int:
+    return cols // BLOCK_ELEMS[t] * BLOCK_BYTES[t]
+
+
+def act_bytes(t: int, cols: int) -> int:
+    return cols // BLOCK_ELEMS[t] * ACT_BYTES[t]
+
+
+class DevBuf:
+    """A device allocation owned by Python; freed on close() or garbage collection."""
+
+    def __init__(self, lib: "Lib", nbytes: int):
+        self.lib, self.nbytes = lib, int(nbytes)
+        self.ptr = lib._L.es_hip_malloc(max(self.nbytes, 1))
+        if not self.ptr:
+            raise EsHipError(-4, lib.last_error())
+
+    def close(self):
+        if self.ptr:
+            self.lib._L.es_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __int__(self):
+        return int(self.ptr)
+
+    def offset(self, nbytes: int) -> int:
+        return int(self.ptr) + int(nbytes)
+
+
+class Lib:
+    def __init__(self, path: str | None = None):
+        path = path or LIB_PATH
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is missing: build it with `make -C stream-_amd` (or __graft_entry__.build())")
+        L = self._L = C.CDLL(path)
+        vp, i, u32, sz = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t
+        for name, res, args in [
+            ("es_hip_available", i, []), ("es_hip_last_error", C.c_char_p, []), ("es_hip_device_name", C.c_char_p, []),
+            ("es_hip_set_order", i, [i]), ("es_hip_get_order", i, []),
+            ("es_hip_quant_supported", i, [u32]), ("es_hip_row_bytes", sz, [u32, i]),
+            ("es_hip_malloc", vp, [sz]), ("es_hip_free", i, [vp]),
+            ("es_hip_memcpy_h2d", i, [vp, vp, sz]), ("es_hip_memcpy_d2h", i, [vp, vp, sz]),
+            ("es_hip_memcpy_d2d", i, [vp, vp, sz]), ("es_hip_memset", i, [vp, i, sz]), ("es_hip_synchronize", i, []),
+            ("es_hip_matvec_dev", i, [u32, vp, i, i, i, vp, vp, vp]),
+            ("es_hip_matvec_multi_dev", i, [u32, vp, i, i, i, vp, sz, i, vp, sz, vp]),
+            ("es_hip_run_jobs", i, [vp, i, vp]),
+            ("es_hip_plan_create", vp, [vp, i]), ("es_hip_plan_run", i, [vp, vp]), ("es_hip_plan_destroy", None, [vp]),
+            ("es_hip_plan_time_ms", C.c_double, [vp, i, i, vp]),
+            ("es_hip_register", i, [vp, sz]), ("es_hip_update", i, [vp]), ("es_hip_unregister", i, [vp]),
+            ("es_hip_matvec", None, [u32, vp, i, i, i, vp, vp, vp]),
+            ("es_hip_matvec_multi", None, [u32, vp, i, i, i, vp, i, vp, sz, vp]),
+            ("es_hip_block_ints_dev", i, [u32, vp, i, i, vp, vp, vp, vp]),
+        ]:
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+
+    # ---- state ----
+    def available(self) -> bool:
+        return bool(self._L.es_hip_available())
+
+    def last_error(self) -> str:
+        return (self._L.es_hip_last_error() or b"").decode()
+
+    def device_name(self) -> str:
+        return (self._L.es_hip_device_name() or b"").decode()
+
+    def set_order(self, order: int) -> int:
+        return self._check(self._L.es_hip_set_order(order))
+
+    def get_order(self) -> int:
+        return self._L.es_hip_get_order()
+
+    def _check(self, rc):
+        if rc is not None and rc < 0:
+            raise EsHipError(rc, self.last_error())
+        return rc
+
+    # ---- memory ----
+    def alloc(self, nbytes: int) -> DevBuf:
+        return DevBuf(self, nbytes)
+
+    def upload(self, arr: np.ndarray) -> DevBuf:
+        arr = np.ascontiguousarray(arr)
+        buf = DevBuf(self, arr.nbytes)
+        if arr.nbytes:
+            self._check(self._L.es_hip_memcpy_h2d(buf.ptr, arr.ctypes.data, arr.nbytes))
+        return buf
+
+    def download(self, dev, out: np.ndarray, offset: int = 0) -> np.ndarray:
+        assert out.flags.c_contiguous
+        if out.nbytes:
+            self._check(self._L.es_hip_memcpy_d2h(out.ctypes.data, int(dev) + offset, out.nbytes))
+        return out
+
+    def memset(self, dev, value: int, nbytes: int):
+        self._check(self._L.es_hip_memset(int(dev), value, nbytes))
+
+    def copy_d2d(self, dst, src, nbytes: int):
+        self._check(self._L.es_hip_memcpy_d2d(int(dst), int(src), nbytes))
+
+    def synchronize(self):
+        self._check(self._L.es_hip_synchronize())
+
+    # ---- device-pointer products ----
+    def matvec_multi_dev(self, t, W, cols, r0, r1, act, astride, na, y, ystride, stream=None):
+        self._check(self._L.es_hip_matvec_multi_dev(t, int(W), cols, r0, r1, int(act), astride, na, int(y), ystride, stream))
+
+    def matvec_dev(self, t, W, cols, r0, r1, act, y, stream=None):
+        self._check(self._L.es_hip_matvec_dev(t, int(W), cols, r0, r1, int(act), int(y), stream))
+
+    @staticmethod
+    def make_jobs(specs) -> C.Array:
+        """specs: iterable of dicts with type, rows, cols, W, act, astride, nb, y, ystride (device pointers as ints)"""
+        specs = list(specs)
+        arr = (Job * max(len(specs), 1))()
+        for k, s in enumerate(specs):
+            arr[k] = Job(s["type"], s["rows"], s["cols"], int(s["W"]), int(s["act"]), s.get("astride", 0), s.get("nb", 1),
+                         int(s["y"]), s.get("ystride", 0))
+        return arr, len(specs)
+
+    def run_jobs(self, specs, stream=None):
+        arr, n = self.make_jobs(specs)
+        self._check(self._L.es_hip_run_jobs(arr, n, stream))
+
+    def plan(self, specs) -> "Plan":
+        arr, n = self.make_jobs(specs)
+        p = self._L.es_hip_plan_create(arr, n)
+        if not p:
+            raise EsHipError(-2, self.last_error())
+        return Plan(self, p)
+
+    def block_ints_dev(self, t, W, cols, rows, act):
+        nb = cols // BLOCK_ELEMS[t]
+        d = self.alloc(rows * nb * 4)
+        a = self.alloc(rows * nb * 4)
+        self._check(self._L.es_hip_block_ints_dev(t, int(W), cols, rows, int(act), d.ptr, a.ptr, None))
+        dots = self.download(d, np.zeros((rows, nb), np.int32))
+        aux = self.download(a, np.zeros((rows, nb), np.int32))
+        return dots, aux
+
+    # ---- host-memory convenience (uploads, computes, downloads) ----
+    def matvec_multi(self, t, W: np.ndarray, cols: int, rows: int, acts: np.ndarray, r0: int = 0, r1: int | None = None):
+        """acts: [na, nblocks] activation blocks (any structured dtype of the right size) -> y [na, rows] fp32;
+        rows outside [r0, r1) stay zero"""
+        r1 = rows if r1 is None else r1
+        acts = np.ascontiguousarray(acts)
+        na = acts.shape[0]
+        dW, dA = self.upload(W), self.upload(acts)
+        dY = self.alloc(na * rows * 4)
+        self.memset(dY, 0, na * rows * 4)
+        self.matvec_multi_dev(t, dW, cols, r0, r1, dA, acts.strides[0] if na > 1 else 0, na, dY, rows)
+        y = self.download(dY, np.zeros((na, rows), np.float32))
+        for b in (dW, dA, dY):
+            b.close()
+        return y
+
+    # ---- the reference prototypes on host memory ----
+    def register(self, W: np.ndarray):
+        self._check(self._L.es_hip_register(W.ctypes.data, W.nbytes))
+
+    def update(self, W: np.ndarray):
+        self._check(self._L.es_hip_update(W.ctypes.data))
+
+    def unregister(self, W: np.ndarray):
+        return self._L.es_hip_unregister(W.ctypes.data)
+
+    def host_matvec_multi(self, t, W: np.ndarray, cols: int, r0: int, r1: int, acts: np.ndarray, y: np.ndarray):
+        """es_hip_matvec_multi with es_act records pointing at `acts` [na, nblocks]; y [na, ystride] updated in place"""
+        acts = np.ascontiguousarray(acts)
+        na = acts.shape[0]
+        recs = (Act * na)()
+        for q in range(na):
+            p = acts.ctypes.data + q * acts.strides[0]
+            recs[q] = Act(None, p if BLOCK_ELEMS[t] == 256 else None, p if BLOCK_ELEMS[t] == 32 else None, cols)
+        if na == 1:
+            self._L.es_hip_matvec(t, W.ctypes.data, cols, r0, r1, recs, y.ctypes.data, None)
+        else:
+            self._L.es_hip_matvec_multi(t, W.ctypes.data, cols, r0, r1, recs, na, y.ctypes.data, y.strides[0] // 4, None)
+        err = self.last_error()   # the void drop-ins clear it on entry
+        if err:
+            raise EsHipError(-1, err)
+        return y
+
+
+class Plan:
+    def __init__(self, lib: Lib, handle):
+        self.lib, self.h = lib, handle
+
+    def run(self, stream=None):
+        self.lib._check(self.lib._L.es_hip_plan_run(self.h, stream))
+
+    def time_ms(self, warmup: int, iters: int, stream=None) -> float:
+        ms = self.lib._L.es_hip_plan_time_ms(self.h, warmup, iters, stream)
+        if ms < 0:
+            raise EsHipError(-3, self.lib.last_error())
+        return ms
+
+    def close(self):
+        if self.h:
+            self.lib._L.es_hip_plan_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

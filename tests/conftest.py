@@ -39,8 +39,24 @@ def golden():
 @pytest.fixture(scope="session")
 def hip():
     """The HIP library through its C-ABI. Fails (not skips) when it is missing: GPU tests must run native code."""
+    _ensure_hip_lib()
     import es_hip_quant as E
     lib = E.Lib()
     if not lib.available():
         pytest.fail("es_hip_available() == 0: no usable gfx950 device: " + lib.last_error())
     return lib
+
+
+def _ensure_hip_lib():
+    so = os.path.join(ROOT, "stream-_amd", "libes_hip_quant.so")
+    if not os.path.exists(so):   # built by __graft_entry__.build(); build here only if nothing is there
+        subprocess.run(["make", "-C", os.path.join(ROOT, "stream-_amd"), "-j4"], check=True, capture_output=True)
+    return so
+
+
+@pytest.fixture(scope="session")
+def hiplib():
+    """The library loaded without requiring a device (CPU tests of the boundary)."""
+    _ensure_hip_lib()
+    import es_hip_quant as E
+    return E.Lib()

@@ -1,0 +1,243 @@
+"""GPU parity: the HIP kernels against the reference's own outputs (golden vectors made from the reference built from its
+sources) and against the oracle (the CPU restatement pinned to those vectors), bit for bit.
+
+Every call goes through the C ABI of libes_hip_quant.so. Order modes map to the reference builds:
+X86_CONTRACT = clang (the reference's default CC), X86_STRICT = gcc -std=c11, SCALAR = gcc with ES_NO_AVX2=1.
+"""
+import numpy as np
+import pytest
+
+import es_hip_quant as E
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K"]
+MODES = [(E.ORDER_X86_CONTRACT, "clang", O.CONTRACT, O.PATH_X86), (E.ORDER_X86_STRICT, "gcc", O.STRICT, O.PATH_X86),
+         (E.ORDER_SCALAR, "scalar", O.STRICT, O.PATH_SCALAR)]
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def golden_acts(golden, F, case):
+    t = O.TYPES[F]
+    raw = golden[f"{F}/{case}_q8"]
+    return np.ascontiguousarray(raw).view(O.act_dtype(t)).reshape(raw.shape[0], -1)
+
+
+@pytest.fixture
+def order(hip):
+    """restore the default order after a test that changes it"""
+    yield hip
+    hip.set_order(E.ORDER_X86_CONTRACT)
+
+
+def mismatch_report(y, ref):
+    bad = np.argwhere(bits(y) != bits(ref))
+    if not len(bad):
+        return ""
+    q, r = bad[0]
+    return f"{len(bad)} of {y.size} differ; first at act {q} row {r}: {y[q, r]!r} vs {ref[q, r]!r}"
+
+
+@pytest.mark.parametrize("F", FMTS)
+@pytest.mark.parametrize("case", ["mtest", "gauss"])
+@pytest.mark.parametrize("mode", MODES, ids=[m[1] for m in MODES])
+def test_golden_vectors_bit_exact(order, golden, F, case, mode):
+    """es_matvec over rows [3, rows) of the reference's own test shapes (tools/es_mtest.c:17, 40)"""
+    hip = order
+    hip.set_order(mode[0])
+    t = O.TYPES[F]
+    cols, rows = (int(v) for v in golden[f"{F}/{case}_shape"])
+    y = hip.matvec_multi(t, golden[f"{F}/{case}_W"], cols, rows, golden_acts(golden, F, case), r0=3)
+    ref = golden[f"{F}/{case}_y_{mode[1]}"]
+    assert np.array_equal(bits(y), bits(ref)), mismatch_report(y, ref)
+
+
+@pytest.mark.parametrize("F", FMTS)
+@pytest.mark.parametrize("case", ["mtest", "gauss"])
+def test_block_integer_dots_exact(hip, orc, golden, F, case):
+    t = O.TYPES[F]
+    cols, rows = (int(v) for v in golden[f"{F}/{case}_shape"])
+    W = golden[f"{F}/{case}_W"]
+    acts = golden_acts(golden, F, case)
+    dW = hip.upload(W)
+    for q in range(acts.shape[0]):
+        dA = hip.upload(acts[q])
+        dots, aux = hip.block_ints_dev(t, dW, cols, rows, dA)
+        rd, ra = orc.block_ints(t, W, cols, rows, acts[q])
+        assert np.array_equal(dots, rd), (F, case, q)
+        assert np.array_equal(aux, ra), (F, case, q)
+
+
+def mtest_inputs(orc, t, rows, cols, na, seed):
+    st = np.array([seed], np.uint64)
+    W = orc.mtest_blocks(t, st, rows, cols)
+    x = orc.mtest_acts(st, na * cols).reshape(na, cols)
+    return W, orc.quantize_act(t, x)
+
+
+# BASELINE.json shapes (rows x cols), at token counts the oracle finishes in seconds
+SHAPES = [
+    ("Q4_0", 4864, 896, 1),     # config 1
+    ("Q4_K", 8192, 2048, 3),    # config 2 gate/up
+    ("Q4_K", 2048, 8192, 2),    # config 2 down
+    ("Q6_K", 151936, 1024, 1),  # config 3 head (K padded to 1024)
+    ("Q2_K", 1024, 2048, 5),    # config 4 expert gate/up
+    ("Q2_K", 2048, 1024, 4),    # config 4 expert down
+    ("Q4_K", 768, 2048, 3),     # config 5 expert gate/up
+    ("Q6_K", 2048, 768, 3),     # config 5 expert down
+    ("Q5_0", 4096, 2048, 4),    # config 5 attention q
+    ("Q5_0", 512, 2048, 5),     # config 5 attention k/v
+]
+
+
+@pytest.mark.parametrize("F,rows,cols,na", SHAPES, ids=[f"{s[0]}-{s[1]}x{s[2]}-n{s[3]}" for s in SHAPES])
+@pytest.mark.parametrize("mode", MODES[:2], ids=["clang", "gcc"])
+def test_baseline_shapes_vs_oracle(order, orc, F, rows, cols, na, mode):
+    hip = order
+    hip.set_order(mode[0])
+    t = O.TYPES[F]
+    W, acts = mtest_inputs(orc, t, rows, cols, na, 1000 + rows + cols)
+    y = hip.matvec_multi(t, W, cols, rows, acts)
+    ref = orc.matvec_multi(t, W, cols, rows, acts, mode[2], mode[3])
+    assert np.array_equal(bits(y), bits(ref)), mismatch_report(y, ref)
+
+
+@pytest.mark.parametrize("F,rows,cols", [("Q4_K", 512, 2048), ("Q6_K", 300, 1024), ("Q2_K", 256, 2048),
+                                          ("Q4_0", 200, 896), ("Q5_0", 128, 2048), ("Q4_K", 64, 14336)])
+def test_multi_equals_single(hip, orc, F, rows, cols):
+    """es_mtest's invariant on the device: one launch over na activations == na single-activation launches"""
+    t = O.TYPES[F]
+    na = 11
+    W, acts = mtest_inputs(orc, t, rows, cols, na, 7 + rows)
+    ym = hip.matvec_multi(t, W, cols, rows, acts)
+    for q in range(na):
+        y1 = hip.matvec_multi(t, W, cols, rows, acts[q:q + 1])
+        assert np.array_equal(bits(ym[q]), bits(y1[0])), (F, q)
+    # and the oracle on a few of them
+    ref = orc.matvec_multi(t, W, cols, rows, acts[:3])
+    assert np.array_equal(bits(ym[:3]), bits(ref))
+
+
+@pytest.mark.parametrize("F", FMTS)
+def test_row_ranges_and_strides(hip, orc, F):
+    """rows [r0, r1) only, absolute indices, padded activation and output strides; nothing else is written"""
+    t = O.TYPES[F]
+    cols = 512 if O.BLOCK_ELEMS[t] == 256 else 256
+    rows, na, r0, r1 = 97, 3, 13, 90
+    W, acts = mtest_inputs(orc, t, rows, cols, na, 31)
+    ab = O.row_bytes(t, cols) // O.BLOCK_BYTES[t] * O.act_dtype(t).itemsize
+    astride = ab + 40                      # padded activation records
+    araw = np.zeros(na * astride, np.uint8)
+    for q in range(na):
+        araw[q * astride:q * astride + ab] = acts[q].view(np.uint8)
+    ystride = rows + 29
+    sentinel = np.float32(-12345.0)
+    dW, dA = hip.upload(W), hip.upload(araw)
+    dY = hip.upload(np.full(na * ystride, sentinel, np.float32))
+    hip.matvec_multi_dev(t, dW, cols, r0, r1, dA, astride, na, dY, ystride)
+    y = hip.download(dY, np.zeros((na, ystride), np.float32))
+    ref = orc.matvec_multi(t, W, cols, rows, acts)
+    assert np.array_equal(bits(y[:, r0:r1]), bits(ref[:, r0:r1]))
+    assert np.all(y[:, :r0] == sentinel) and np.all(y[:, r1:] == sentinel)
+
+
+@pytest.mark.parametrize("F", FMTS)
+def test_edge_blocks(hip, orc, F):
+    """all-0xff and all-zero weight bytes, zero activations (d = 0 blocks), subnormal fp16 scales, +-127 activations"""
+    t = O.TYPES[F]
+    be, bb = O.BLOCK_ELEMS[t], O.BLOCK_BYTES[t]
+    cols = 4 * be
+    rows = 6
+    W = np.zeros((rows, cols // be, bb), np.uint8)
+    W[0] = 0xFF
+    W[2] = 0xFF
+    rng = np.random.default_rng(9)
+    W[3] = rng.integers(0, 256, W[3].shape, dtype=np.uint8)
+    W[4] = rng.integers(0, 256, W[4].shape, dtype=np.uint8)
+    dpos = {O.Q4_0: [0], O.Q5_0: [0], O.Q4_K: [0, 2], O.Q6_K: [208], O.Q2_K: [80, 82]}[t]
+    for p in dpos:
+        W[2, :, p:p + 2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)   # 1.0: extreme integers, sane scale
+        W[3, :, p:p + 2] = np.frombuffer(np.uint16(0x0007).tobytes(), np.uint8)   # subnormal half
+        W[4, :, p:p + 2] = np.frombuffer(np.uint16(0x8201).tobytes(), np.uint8)   # negative subnormal
+    W = W.reshape(-1)
+    x = np.zeros((4, cols), np.float32)
+    x[1] = np.where(np.arange(cols) % 2, 3.0, -3.0)
+    x[2] = 3.0
+    x[3] = rng.standard_normal(cols).astype(np.float32)
+    acts = orc.quantize_act(t, x)
+    for mode in MODES:
+        hip.set_order(mode[0])
+        y = hip.matvec_multi(t, W, cols, rows, acts)
+        ref = orc.matvec_multi(t, W, cols, rows, acts, mode[2], mode[3])
+        assert np.array_equal(bits(y), bits(ref)), (mode[1], mismatch_report(y, ref))
+    hip.set_order(E.ORDER_X86_CONTRACT)
+
+
+def test_host_drop_in_matches_device_path(hip, orc):
+    """es_hip_matvec / es_hip_matvec_multi on host memory, with and without a registered weight copy"""
+    t = O.Q4_K
+    rows, cols, na = 300, 2048, 4
+    W, acts = mtest_inputs(orc, t, rows, cols, na, 77)
+    ref = orc.matvec_multi(t, W, cols, rows, acts)
+    for registered in (False, True):
+        if registered:
+            hip.register(W)
+        y = np.full((na, rows), -1.0, np.float32)
+        hip.host_matvec_multi(t, W, cols, 10, 290, acts, y)
+        assert np.array_equal(bits(y[:, 10:290]), bits(ref[:, 10:290]))
+        assert np.all(y[:, :10] == -1.0) and np.all(y[:, 290:] == -1.0)
+        y1 = np.zeros((1, rows), np.float32)
+        hip.host_matvec_multi(t, W, cols, 0, rows, acts[2:3], y1)
+        assert np.array_equal(bits(y1[0]), bits(ref[2]))
+    # a changed host weight is seen after es_hip_update
+    W2 = W.copy()
+    W[:] = orc.mtest_blocks(t, np.array([5], np.uint64), rows, cols)
+    hip.update(W)
+    y = np.zeros((1, rows), np.float32)
+    hip.host_matvec_multi(t, W, cols, 0, rows, acts[:1], y)
+    assert np.array_equal(bits(y[0]), bits(orc.matvec_multi(t, W, cols, rows, acts[:1])[0]))
+    assert hip.unregister(W) == 0
+    del W2
+
+
+def test_run_jobs_and_plan_mixed_formats(hip, orc):
+    """one queued batch over all five formats (the engine's run_jobs) == the products one by one"""
+    specs, keep, refs = [], [], []
+    for k, (F, rows, cols, na) in enumerate([("Q4_K", 256, 2048, 1), ("Q6_K", 130, 768, 3), ("Q2_K", 96, 1024, 2),
+                                             ("Q4_0", 77, 896, 1), ("Q5_0", 64, 2048, 5), ("Q4_K", 33, 512, 4)]):
+        t = O.TYPES[F]
+        W, acts = mtest_inputs(orc, t, rows, cols, na, 300 + k)
+        dW, dA, dY = hip.upload(W), hip.upload(acts), hip.alloc(na * rows * 4)
+        keep += [dW, dA, dY]
+        specs.append(dict(type=t, rows=rows, cols=cols, W=dW, act=dA, astride=acts.strides[0], nb=na, y=dY,
+                          ystride=rows))
+        refs.append((dY, na, rows, orc.matvec_multi(t, W, cols, rows, acts)))
+    hip.run_jobs(specs)
+    for dY, na, rows, ref in refs:
+        assert np.array_equal(bits(hip.download(dY, np.zeros((na, rows), np.float32))), bits(ref))
+        hip.memset(dY, 0, na * rows * 4)
+    plan = hip.plan(specs)
+    plan.run()
+    hip.synchronize()
+    for dY, na, rows, ref in refs:
+        assert np.array_equal(bits(hip.download(dY, np.zeros((na, rows), np.float32))), bits(ref))
+    assert plan.time_ms(1, 3) > 0
+    plan.close()
+
+
+def test_invalid_arguments_are_rejected(hip):
+    buf = hip.alloc(1 << 16)
+    with pytest.raises(E.EsHipError):   # cols not a multiple of the block
+        hip.matvec_multi_dev(E.Q4_K, buf, 300, 0, 4, buf, 0, 1, buf, 0)
+    with pytest.raises(E.EsHipError):   # misaligned weights
+        hip.matvec_multi_dev(E.Q4_K, buf.offset(2), 256, 0, 4, buf, 0, 1, buf, 0)
+    with pytest.raises(E.EsHipError):   # unsupported type
+        hip.matvec_multi_dev(11, buf, 256, 0, 4, buf, 0, 1, buf, 0)
+    with pytest.raises(E.EsHipError):   # overlapping outputs
+        hip.matvec_multi_dev(E.Q4_K, buf, 256, 0, 4, buf, 292, 2, buf, 2)
+    hip.matvec_multi_dev(E.Q4_K, buf, 256, 4, 4, buf, 0, 1, buf, 0)   # empty range: nothing to do
+    buf.close()

@@ -244,3 +244,20 @@ def test_live_reference_wide_shapes(orc):
             R = O.RefLib(cc)
             ref = R.matvec_f32(t, W, cols, rows, x, multi=True)
             assert np.array_equal(_bits(orc.matvec_multi(t, W, cols, rows, acts, order)), _bits(ref)), (F, cols, cc)
+
+
+@pytest.mark.skipif(not O.ref_available("clang"), reason="reference not built here (no /root/reference)")
+def test_reference_adapter_for_cpu_baseline(orc):
+    """the cpu_baseline leg times the reference's es_matvec_multi through esq_multi_reference: it must compute the same
+    numbers as es_act_prepare + es_matvec_multi, and the threaded harness must not change them"""
+    R = O.RefLib("clang")
+    for F, cols in (("Q4_K", 2048), ("Q4_0", 896), ("Q6_K", 1024), ("Q2_K", 1024), ("Q5_0", 512)):
+        t = O.TYPES[F]
+        rows = 40
+        W = orc.quantize_rows(t, orc.gauss(21, 0.02, rows * cols).reshape(rows, cols))
+        x = orc.gauss(22, 1.0, 3 * cols).reshape(3, cols)
+        acts = orc.quantize_act(t, x)
+        ref = R.matvec_f32(t, W, cols, rows, x, multi=True)
+        assert np.array_equal(_bits(orc.matvec_multi_reference(R, t, W, cols, rows, acts)), _bits(ref)), F
+        sec, passes, y = orc.cpu_bench(orc.reference_fn_ptr(R), t, W, W.size, 1, rows, cols, acts, 3, 0.01)
+        assert passes >= 1 and np.array_equal(_bits(y), _bits(ref)), F
