@@ -35,9 +35,9 @@ struct MvJob {
     int pad_;
 };
 
-// One launch of the decode kernel: format, activations per pass, block chunks per lane, workgroups, LDS bytes.
+// One launch of the decode kernel: format, activations per pass, waves per workgroup, workgroups, LDS bytes.
 struct MvLaunch {
-    int type, nt, cpr;
+    int type, nt, waves;
     int grid;
     size_t lds;
 };
@@ -59,11 +59,38 @@ __device__ __forceinline__ uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t
 
 template <typename T> __device__ __forceinline__ T ldg(const void *p) { return *reinterpret_cast<const T *>(p); }
 
+// Weight loads. Every weight byte is read once per pass, so ESQ_NT_WEIGHTS=1 marks them non-temporal (streamed past the
+// caches); 0 uses ordinary loads. Build-time choice, same results either way.
+#ifndef ESQ_NT_WEIGHTS
+#define ESQ_NT_WEIGHTS 0
+#endif
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ldw4(const void *p) {
+#if ESQ_NT_WEIGHTS
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *reinterpret_cast<const uint4 *>(p);
+#endif
+}
+__device__ __forceinline__ uint2 ldw2(const void *p) {
+#if ESQ_NT_WEIGHTS
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+    return make_uint2(v.x, v.y);
+#else
+    return *reinterpret_cast<const uint2 *>(p);
+#endif
+}
+
 // Sum over groups of G consecutive lanes (G = 1, 2, 4, 8); every lane of a group ends with the group's sum.
+// DPP lane moves, no LDS round trip: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror (lane i of each 8 reads
+// lane 7 - i). After the two quad steps every lane holds its quad's sum; the half mirror pairs each quad with the other
+// quad of its 8 lanes. Integer sums, so the pairing order does not matter.
 template <int G> __device__ __forceinline__ int group_sum(int v) {
-    if constexpr (G >= 2) v += __shfl_xor(v, 1);
-    if constexpr (G >= 4) v += __shfl_xor(v, 2);
-    if constexpr (G >= 8) v += __shfl_xor(v, 4);
+    if constexpr (G >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    if constexpr (G >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    if constexpr (G >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
     return v;
 }
 

@@ -1,22 +1,34 @@
 // Decode / small-batch products on the vector ALU (v_dot4_i32_i8), all five formats.
 //
-// One wave per workgroup owns `rows_per_wg` consecutive rows of one job. Two phases per batch of `chain_rows` rows:
+// One workgroup of W waves owns `rows_per_wg` consecutive rows of one job. Two phases per batch of `chain_rows` rows:
 //
 //  1. Integer phase, block-parallel and coalesced. The wave's 64 lanes are cut into slots of LPB lanes; each slot takes one
 //     weight block (consecutive slots take consecutive blocks, so a wave-wide load covers a contiguous byte range) and each
 //     lane of the slot takes a fixed share of the block's elements. The lane unpacks its share into int8 lanes, dots it with
-//     the activation bytes it holds in registers (v_dot4) and the slot sums the partials (shuffles). Integer arithmetic is
-//     exact, so the order of these sums does not matter. The slot leader turns the block's integers into the float terms of
-//     the reference epilogue and stores them in LDS.
+//     the activation bytes it holds in registers (v_dot4) and the slot sums the partials (DPP lane moves). Integer
+//     arithmetic is exact, so the order of these sums does not matter. The slot leader turns the block's integers into
+//     the float terms of the reference epilogue and stores them in LDS. The raw loads of U units (a unit is one block
+//     position of one row) are issued together before any of them is used, so every wave keeps U loads in flight.
 //  2. Float phase, one lane per (row, activation[, AVX2 lane]). The lane runs the reference's accumulation over the row's
 //     blocks in the reference's order (a strict sequential fp32 chain), so outputs are bit-identical to the CPU kernels.
 //
 // The activation slice a lane needs depends only on its block position inside the row, which stays fixed while the wave
-// walks down the rows, so activations are loaded into registers once per batch of NT activations.
+// walks down the rows (long rows are split across the workgroup's waves), so activations are loaded into registers once
+// per batch of NT activations.
 //
 // Reference kernels restated (integer parts and float order): src/es_quant.c:1013-1117 (scalar mv_*), 1252-1343 and
 // 1443-1469 (AVX2 Q4_0/Q5_0/Q4_K/Q6_K), 1344-1368 and src/es_q2k.c:127-190 (Q2_K).
 #include "es_hip_common.h"
+
+
+// units (one block position of one row each) whose raw loads a wave issues before using any of them; a power of two
+#ifndef ESQ_UNITS
+#define ESQ_UNITS 4
+#endif
+// resident waves per SIMD the register allocation must allow
+#ifndef ESQ_MIN_WAVES
+#define ESQ_MIN_WAVES 1
+#endif
 
 namespace esq {
 
@@ -27,18 +39,15 @@ struct Term2 { float a, b; };
 
 enum { CH_FMA = 0, CH_MULADD = 1, CH_LANES = 2 };
 
-__device__ __forceinline__ float chain_step(int mode, float s, float a, float b) {
-    return mode == CH_FMA ? __builtin_fmaf(a, b, s) : s + a * b;   // built with -ffp-contract=off: s + a*b rounds twice
-}
-
 // ---------------------------------------------------------------------------------------------------------------------
-// Per-format lane work
+// Per-format lane work: Raw (the bytes one lane loads), Wt (unpacked), Act (activation slice), Ints (integer partials)
 
 template <int F> struct Lane;
 
 // Q4_K: lane k of 8 takes qs bytes [16k, 16k+16): chunk c = k/2, half h = k%2; its low nibbles are elements
 // 64c + 16h + [0,16) (sub-block 2c), its high nibbles 64c + 32 + 16h + [0,16) (sub-block 2c+1). src/es_quant.c:1056-1080.
 template <> struct Lane<ES_HIP_Q4_K> {
+    struct Raw { uint4 hdr, q; };
     struct Act { uint32_t lo[4], hi[4]; int bs0, bs1; float d; };
     struct Wt { uint32_t lo[4], hi[4]; int sc0, sc1, mn0, mn1; float d, dmin; };
     struct Ints { int dot, aux; };
@@ -58,6 +67,10 @@ template <> struct Lane<ES_HIP_Q4_K> {
         x.bs0 = x.bs1 = 0;
         x.d = 0.0f;
     }
+    static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
+        r.hdr = ldw4(blk);
+        r.q = ldw4(blk + 16 + 16 * k);
+    }
     // 6-bit scale and min of sub-block j from the 12 packed bytes (scale_min_k4, src/es_quant.c:75-83)
     static __device__ __forceinline__ void scale_min(uint32_t s03, uint32_t s47, uint32_t s811, int j, int &sc, int &mn) {
         const int jj = (j & 3) * 8;
@@ -65,16 +78,14 @@ template <> struct Lane<ES_HIP_Q4_K> {
         if (j < 4) { sc = a & 63; mn = b & 63; }
         else { sc = (c & 15) | ((a >> 6) << 4); mn = (c >> 4) | ((b >> 6) << 4); }
     }
-    static __device__ __forceinline__ void load_w(const uint8_t *blk, int k, Wt &w) {
-        const uint4 hdr = ldg<uint4>(blk);
-        const uint4 q = ldg<uint4>(blk + 16 + 16 * k);
-        const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+    static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
+        const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
         for (int i = 0; i < 4; i++) { w.lo[i] = qq[i] & 0x0f0f0f0fu; w.hi[i] = (qq[i] >> 4) & 0x0f0f0f0fu; }
         const int c = k >> 1;
-        scale_min(hdr.y, hdr.z, hdr.w, 2 * c, w.sc0, w.mn0);
-        scale_min(hdr.y, hdr.z, hdr.w, 2 * c + 1, w.sc1, w.mn1);
-        w.d = half_bits_to_float(hdr.x);
-        w.dmin = half_bits_to_float(hdr.x >> 16);
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * c, w.sc0, w.mn0);
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * c + 1, w.sc1, w.mn1);
+        w.d = half_bits_to_float(r.hdr.x);
+        w.dmin = half_bits_to_float(r.hdr.x >> 16);
     }
     static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
         int lo = 0, hi = 0;
@@ -94,6 +105,10 @@ template <> struct Lane<ES_HIP_Q4_K> {
 // group is 16 consecutive elements with one int8 scale. The 6-bit codes are dotted unsigned and corrected by
 // 32 * bsums (the same integer as the signed form). src/es_quant.c:1081-1117, 1443-1469.
 template <> struct Lane<ES_HIP_Q6_K> {
+    // 16-byte fields at 2-byte aligned addresses are read as five aligned dwords and realigned with v_alignbyte. All of it
+    // lies inside the block: the block starts 4-byte aligned or 2 bytes past (then the dword before is the previous
+    // block's), and the last field read here (qh, offset 176) ends 18 bytes before the block does.
+    struct Raw { uint4 lv, hv; uint32_t l4, h4, sel; int s1, s2; uint32_t d16; };
     struct Act { uint32_t y1[4], y2[4]; int bs1, bs2; float d; };
     struct Wt { uint32_t q1[4], q2[4]; int sc1, sc2; float d; };
     struct Ints { int dot, aux; };
@@ -114,35 +129,36 @@ template <> struct Lane<ES_HIP_Q6_K> {
         x.bs1 = x.bs2 = 0;
         x.d = 0.0f;
     }
-    // 16 bytes at a 2-byte aligned address inside the block, from five aligned dwords (all inside the block: the block
-    // starts at a 4-byte aligned address or 2 bytes past one, and the last 16-byte field read here ends 18 bytes before
-    // the block's end)
-    static __device__ __forceinline__ void ld16(const uint8_t *p, uint32_t out[4]) {
-        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-        const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~static_cast<uintptr_t>(3));
-        const uint32_t sel = static_cast<uint32_t>(a & 3);
-        const uint4 v = ldg<uint4>(base);
-        const uint32_t w4 = base[4];
-        out[0] = alignbyte(v.y, v.x, sel);
-        out[1] = alignbyte(v.z, v.y, sel);
-        out[2] = alignbyte(v.w, v.z, sel);
-        out[3] = alignbyte(w4, v.w, sel);
-    }
-    static __device__ __forceinline__ void load_w(const uint8_t *blk, int k, Wt &w) {
+    static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
         const int h = k >> 2, j = (k >> 1) & 1, p = k & 1;
-        uint32_t ql[4], qh[4];
-        ld16(blk + 64 * h + 32 * p + 16 * j, ql);
-        ld16(blk + 128 + 32 * h + 16 * j, qh);
-        const int sl = 2 * p, sh = 2 * p + 4;
+        const uintptr_t al = reinterpret_cast<uintptr_t>(blk + 64 * h + 32 * p + 16 * j);
+        const uintptr_t ah = reinterpret_cast<uintptr_t>(blk + 128 + 32 * h + 16 * j);
+        const uint32_t *bl = reinterpret_cast<const uint32_t *>(al & ~static_cast<uintptr_t>(3));
+        const uint32_t *bh = reinterpret_cast<const uint32_t *>(ah & ~static_cast<uintptr_t>(3));
+        r.sel = static_cast<uint32_t>(al & 3);   // same for both fields (offsets differ by multiples of 16)
+        r.lv = ldw4(bl);
+        r.l4 = bl[4];
+        r.hv = ldw4(bh);
+        r.h4 = bh[4];
+        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192);
+        const int g1 = g1_of(k);
+        r.s1 = sc[g1];
+        r.s2 = sc[g1 + 4];
+        r.d16 = *reinterpret_cast<const uint16_t *>(blk + 208);
+    }
+    static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
+        const uint32_t ql[4] = {alignbyte(r.lv.y, r.lv.x, r.sel), alignbyte(r.lv.z, r.lv.y, r.sel),
+                                alignbyte(r.lv.w, r.lv.z, r.sel), alignbyte(r.l4, r.lv.w, r.sel)};
+        const uint32_t qh[4] = {alignbyte(r.hv.y, r.hv.x, r.sel), alignbyte(r.hv.z, r.hv.y, r.sel),
+                                alignbyte(r.hv.w, r.hv.z, r.sel), alignbyte(r.h4, r.hv.w, r.sel)};
+        const int p = k & 1, sl = 2 * p, sh = 2 * p + 4;
         for (int i = 0; i < 4; i++) {
             w.q1[i] = (ql[i] & 0x0f0f0f0fu) | (((qh[i] >> sl) & 0x03030303u) << 4);
             w.q2[i] = ((ql[i] >> 4) & 0x0f0f0f0fu) | (((qh[i] >> sh) & 0x03030303u) << 4);
         }
-        const int g1 = g1_of(k);
-        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192);
-        w.sc1 = sc[g1];
-        w.sc2 = sc[g1 + 4];
-        w.d = half_bits_to_float(*reinterpret_cast<const uint16_t *>(blk + 208));
+        w.sc1 = r.s1;
+        w.sc2 = r.s2;
+        w.d = half_bits_to_float(r.d16);
     }
     static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
         int s1 = 0, s2 = 0;
@@ -160,6 +176,7 @@ template <> struct Lane<ES_HIP_Q6_K> {
 // isum = sum_g (sc[g] & 15) * sum q*y; summs = sum_g bsums[g] * (sc[g] >> 4), added once per group (sub 0 lanes).
 // src/es_q2k.c:127-148, src/es_quant.c:1344-1368.
 template <> struct Lane<ES_HIP_Q2_K> {
+    struct Raw { uint2 q, sc; uint32_t dd; };
     struct Act { uint32_t y[4][2]; int bs[4]; float d; };
     struct Wt { uint32_t q[2]; int scl[4], mn[4]; float d, dmin; };
     struct Ints { int dot, aux; };
@@ -180,21 +197,24 @@ template <> struct Lane<ES_HIP_Q2_K> {
         for (int s = 0; s < 4; s++) { x.y[s][0] = x.y[s][1] = 0; x.bs[s] = 0; }
         x.d = 0.0f;
     }
-    static __device__ __forceinline__ void load_w(const uint8_t *blk, int k, Wt &w) {
+    static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
         const int h = k >> 2, part = (k >> 1) & 1, sub = k & 1;
-        const uint2 q = ldg<uint2>(blk + 16 + 32 * h + 16 * part + 8 * sub);
-        w.q[0] = q.x;
-        w.q[1] = q.y;
-        const uint2 sc = ldg<uint2>(blk + 8 * h);   // scales[8h .. 8h+8): byte 2s + part is group 8h + 2s + part
+        r.q = ldw2(blk + 16 + 32 * h + 16 * part + 8 * sub);
+        r.sc = ldg<uint2>(blk + 8 * h);   // scales[8h .. 8h+8): byte 2s + part is group 8h + 2s + part
+        r.dd = ldg<uint32_t>(blk + 80);
+    }
+    static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
+        const int part = (k >> 1) & 1;
+        w.q[0] = r.q.x;
+        w.q[1] = r.q.y;
         for (int s = 0; s < 4; s++) {
             const int byte = 2 * s + part;
-            const uint32_t v = ((byte < 4 ? sc.x : sc.y) >> (8 * (byte & 3))) & 0xff;
+            const uint32_t v = ((byte < 4 ? r.sc.x : r.sc.y) >> (8 * (byte & 3))) & 0xff;
             w.scl[s] = v & 15;
             w.mn[s] = v >> 4;
         }
-        const uint32_t dd = ldg<uint32_t>(blk + 80);
-        w.d = half_bits_to_float(dd);
-        w.dmin = half_bits_to_float(dd >> 16);
+        w.d = half_bits_to_float(r.dd);
+        w.dmin = half_bits_to_float(r.dd >> 16);
     }
     static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
         int isum = 0, summs = 0;
@@ -221,6 +241,9 @@ template <> struct Lane<ES_HIP_Q2_K> {
 // src/es_quant.c:1013-1055 (scalar), 1252-1323 (AVX2).
 template <int F> struct Lane32 {
     static constexpr int OFF = F == ES_HIP_Q4_0 ? 8 : 16;
+    // The block starts 2-aligned. A 16-byte load at the 4-aligned one of blk / blk+2 plus 2- and 4-byte loads for the
+    // rest reads exactly the block's bytes.
+    struct Raw { uint4 v; uint32_t w4, u, par; };
     struct Act { uint32_t y[8]; int ns[8]; float d; };   // ns[i] = -OFF * (sum of the four bytes of y[i])
     struct Wt { uint32_t q[8]; float d; };
     struct Ints { int lane[8]; };
@@ -236,35 +259,39 @@ template <int F> struct Lane32 {
         for (int i = 0; i < 8; i++) { x.y[i] = 0; x.ns[i] = 0; }
         x.d = 0.0f;
     }
-    // The block starts 2-aligned. A 16-byte load at the 4-aligned one of blk / blk+2 plus 2- and 4-byte loads for the
-    // rest reads exactly the block's bytes.
-    static __device__ __forceinline__ void load_w(const uint8_t *blk, int, Wt &w) {
-        const uint32_t par = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk) & 2);
-        uint32_t qs[4], d16, qh = 0;
+    static __device__ __forceinline__ void load_raw(const uint8_t *blk, int, Raw &r) {
+        r.par = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk) & 2);
+        r.v = ldw4(blk + r.par);
         if constexpr (F == ES_HIP_Q4_0) {   // d f16 @0, qs[16] @2
-            const uint4 v = ldg<uint4>(blk + par);
-            const uint32_t u = *reinterpret_cast<const uint16_t *>(par ? blk : blk + 16);
-            if (par == 0) {
+            r.w4 = 0;
+            r.u = *reinterpret_cast<const uint16_t *>(r.par ? blk : blk + 16);
+        } else {                            // d f16 @0, qh u32 @2, qs[16] @6
+            r.w4 = ldg<uint32_t>(blk + r.par + 16);
+            r.u = *reinterpret_cast<const uint16_t *>(r.par ? blk : blk + 20);
+        }
+    }
+    static __device__ __forceinline__ void unpack(const Raw &r, int, Wt &w) {
+        uint32_t qs[4], d16, qh = 0;
+        const uint4 v = r.v;
+        if constexpr (F == ES_HIP_Q4_0) {
+            if (r.par == 0) {
                 d16 = v.x;
                 qs[0] = alignbyte(v.y, v.x, 2); qs[1] = alignbyte(v.z, v.y, 2);
-                qs[2] = alignbyte(v.w, v.z, 2); qs[3] = alignbyte(u, v.w, 2);
+                qs[2] = alignbyte(v.w, v.z, 2); qs[3] = alignbyte(r.u, v.w, 2);
             } else {
-                d16 = u;
+                d16 = r.u;
                 qs[0] = v.x; qs[1] = v.y; qs[2] = v.z; qs[3] = v.w;
             }
-        } else {                            // d f16 @0, qh u32 @2, qs[16] @6
-            const uint4 v = ldg<uint4>(blk + par);
-            const uint32_t w4 = ldg<uint32_t>(blk + par + 16);
-            const uint32_t u = *reinterpret_cast<const uint16_t *>(par ? blk : blk + 20);
-            if (par == 0) {
+        } else {
+            if (r.par == 0) {
                 d16 = v.x;
                 qh = alignbyte(v.y, v.x, 2);
                 qs[0] = alignbyte(v.z, v.y, 2); qs[1] = alignbyte(v.w, v.z, 2);
-                qs[2] = alignbyte(w4, v.w, 2); qs[3] = alignbyte(u, w4, 2);
+                qs[2] = alignbyte(r.w4, v.w, 2); qs[3] = alignbyte(r.u, r.w4, 2);
             } else {
-                d16 = u;
+                d16 = r.u;
                 qh = v.x;
-                qs[0] = v.y; qs[1] = v.z; qs[2] = v.w; qs[3] = w4;
+                qs[0] = v.y; qs[1] = v.z; qs[2] = v.w; qs[3] = r.w4;
             }
         }
         for (int i = 0; i < 4; i++) { w.q[i] = qs[i] & 0x0f0f0f0fu; w.q[i + 4] = (qs[i] >> 4) & 0x0f0f0f0fu; }
@@ -299,13 +326,19 @@ __device__ __forceinline__ int find_job(const MvJob *jobs, int njobs, int bid) {
     return lo;
 }
 
-// order: ES_HIP_ORDER_*; NT activations per pass; CPR = most blocks per lane slot in one row (nb <= CPR * slots).
-template <int F, int NT, int CPR>
-__global__ __launch_bounds__(WAVE) void mv_kernel(const MvJob *__restrict__ jobs, int njobs, MvJob single, int order) {
+// W waves per workgroup. A row of nbk blocks is cut into seg = ceil(nbk / slots) segments of `slots` blocks, one wave
+// each, so every lane keeps one fixed block position and its activation slice stays in registers; when seg < W the
+// W / seg wave groups take different rows. All waves write their blocks' float terms to the workgroup's LDS, then the
+// whole workgroup runs the per-row chains. order: ES_HIP_ORDER_*; NT activations per pass. One workgroup per tile
+// (rows_per_wg rows of one job).
+template <int F, int NT, int W>
+__global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob *__restrict__ jobs, int njobs, MvJob single,
+                                                                     int order) {
     using L = Lane<F>;
     constexpr int LPB = Fmt<F>::LPB, BE = Fmt<F>::BE, BB = Fmt<F>::BB, AB = Fmt<F>::AB;
     constexpr int SLOTS = WAVE / LPB;
     constexpr bool W32 = is32<F>();
+    constexpr int U = ESQ_UNITS;   // row passes whose raw loads a wave issues before using any of them
 
     MvJob J;
     if (jobs) J = jobs[find_job(jobs, njobs, blockIdx.x)];
@@ -314,15 +347,20 @@ __global__ __launch_bounds__(WAVE) void mv_kernel(const MvJob *__restrict__ jobs
     const int tile = blockIdx.x - J.tile0;
     const int ra0 = J.r0 + tile * J.rows_per_wg;
     const int rend = min(ra0 + J.rows_per_wg, J.r1);
+    const uint8_t *const dummy = J.W + (size_t)J.r0 * J.row_bytes;   // a valid block for lanes with nothing to load
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int slot = lane / LPB, k = lane % LPB;
-    int rpi, rowoff, bpos;
-    if (nbk <= SLOTS) { rpi = SLOTS / nbk; rowoff = slot / nbk; bpos = slot % nbk; }
-    else { rpi = 1; rowoff = 0; bpos = slot; }
-    const bool slot_live = rowoff < rpi;
+    int seg = 1;                                      // waves per row, a power of two (the planner keeps seg <= W)
+    while (seg * SLOTS < nbk) seg <<= 1;
+    const int my_seg = wave % seg, rowgrp = wave / seg, nrowgrp = W / seg;
+    int rpi, rowoff, b;
+    if (nbk <= SLOTS) { rpi = SLOTS / nbk; rowoff = slot / nbk; b = slot % nbk; }
+    else { rpi = 1; rowoff = 0; b = my_seg * SLOTS + slot; }
+    const bool live = rowoff < rpi && b < nbk;
+    const int rstep = nrowgrp * rpi;                  // rows advanced by one pass of the whole workgroup
+    const int rfirst = rowgrp * rpi + rowoff;
 
-    // chain mode
     const bool x86 = order != ES_HIP_ORDER_SCALAR;
     const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
     const int cmode = W32 ? (x86 ? CH_LANES : CH_MULADD) : (contract ? CH_FMA : CH_MULADD);
@@ -331,56 +369,48 @@ __global__ __launch_bounds__(WAVE) void mv_kernel(const MvJob *__restrict__ jobs
 
     for (int t0 = 0; t0 < J.na; t0 += NT) {
         const int nt = min(NT, J.na - t0);
-        typename L::Act act[CPR][NT];
+        typename L::Act act[NT];
 #pragma unroll
-        for (int c = 0; c < CPR; c++) {
-            const int b = bpos + c * SLOTS;
-            const bool ok = slot_live && b < nbk;
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                if (ok && t < nt) L::load_act(J.act + (size_t)(t0 + t) * J.astride + (size_t)b * AB, k, act[c][t]);
-                else L::zero_act(act[c][t]);
-            }
+        for (int t = 0; t < NT; t++) {
+            if (live && t < nt) L::load_act(J.act + (size_t)(t0 + t) * J.astride + (size_t)b * AB, k, act[t]);
+            else L::zero_act(act[t]);
         }
 
         for (int ra = ra0; ra < rend; ra += J.chain_rows) {
             const int rb = min(ra + J.chain_rows, rend);
             // ---- phase 1: integers per block, float terms to LDS
-            for (int r = ra; r < rb; r += rpi) {
-                const int row = r + rowoff;
-                const bool row_ok = slot_live && row < rb;
-                const uint8_t *wrow = J.W + (size_t)row * J.row_bytes;
+            for (int r0 = ra + rfirst; r0 - rowoff < rb; r0 += U * rstep) {
+                typename L::Raw raw[U];
+                bool ok[U];
 #pragma unroll
-                for (int c = 0; c < CPR; c++) {
-                    const int b = bpos + c * SLOTS;
-                    const bool ok = row_ok && b < nbk;
+                for (int u = 0; u < U; u++) {
+                    const int row = r0 + u * rstep;
+                    ok[u] = live && row < rb;
+                    L::load_raw(ok[u] ? J.W + (size_t)row * J.row_bytes + (size_t)b * BB : dummy, k, raw[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int row = r0 + u * rstep;
                     typename L::Wt w;
+                    L::unpack(raw[u], k, w);
                     typename L::Ints v[NT];
-                    if (ok) {
-                        L::load_w(wrow + (size_t)b * BB, k, w);
 #pragma unroll
-                        for (int t = 0; t < NT; t++) v[t] = L::ints(w, act[c][t]);
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < NT; t++) v[t] = typename L::Ints{};
-                    }
+                    for (int t = 0; t < NT; t++) v[t] = ok[u] ? L::ints(w, act[t]) : typename L::Ints{};
                     if constexpr (!W32) {
 #pragma unroll
                         for (int t = 0; t < NT; t++) { v[t].dot = group_sum<LPB>(v[t].dot); v[t].aux = group_sum<LPB>(v[t].aux); }
                     }
-                    if (ok && k == 0) {
+                    if (ok[u] && k == 0) {
                         float *e = lds + ((size_t)(row - ra) * nbk + b) * NT * CW;
                         if constexpr (W32) {
 #pragma unroll
                             for (int t = 0; t < NT; t++) {
-                                const float dyd = w.d * act[c][t].d;
+                                e[t * CW] = w.d * act[t].d;
                                 if (cmode == CH_LANES) {
-                                    e[t * CW] = dyd;
                                     for (int i = 0; i < 8; i++) e[t * CW + 1 + i] = static_cast<float>(v[t].lane[i]);
                                 } else {
                                     int a = 0;
                                     for (int i = 0; i < 8; i++) a += v[t].lane[i];
-                                    e[t * CW] = dyd;
                                     e[t * CW + 1] = static_cast<float>(a);
                                 }
                             }
@@ -393,7 +423,7 @@ __global__ __launch_bounds__(WAVE) void mv_kernel(const MvJob *__restrict__ jobs
                         } else {
 #pragma unroll
                             for (int t = 0; t < NT; t++) {
-                                const Term2 tm = L::term(w, act[c][t], v[t], contract);
+                                const Term2 tm = L::term(w, act[t], v[t], contract);
                                 e[t * CW] = tm.a;
                                 e[t * CW + 1] = tm.b;
                             }
@@ -406,19 +436,30 @@ __global__ __launch_bounds__(WAVE) void mv_kernel(const MvJob *__restrict__ jobs
                 }
             }
             __syncthreads();
-            // ---- phase 2: the reference's sequential accumulation over the row's blocks
+            // ---- phase 2: the reference's sequential accumulation over the row's blocks, terms read 8 blocks ahead
             const int nrow = rb - ra;
             const int per = cmode == CH_LANES ? 8 : 1;
-            for (int idx = lane; idx < nrow * NT * per; idx += WAVE) {
+            for (int idx = tid; idx < nrow * NT * per; idx += WAVE * W) {
                 const int i = idx % per, t = (idx / per) % NT, rl = idx / (per * NT);
                 const float *e = lds + (size_t)rl * nbk * NT * CW + t * CW;
+                const int oa = cmode == CH_LANES ? 1 + i : 0, ob = cmode == CH_LANES ? 0 : 1;
                 float s = 0.0f;
-                if (cmode == CH_LANES) {
-                    for (int b = 0; b < nbk; b++, e += NT * CW) s = __builtin_fmaf(e[1 + i], e[0], s);
-                } else if (cmode == CH_FMA) {
-                    for (int b = 0; b < nbk; b++, e += NT * CW) s = __builtin_fmaf(e[0], e[1], s);
-                } else {
-                    for (int b = 0; b < nbk; b++, e += NT * CW) s = s + e[0] * e[1];
+                int bb = 0;
+                for (; bb + 8 <= nbk; bb += 8) {
+                    float ta[8], tb[8];
+#pragma unroll
+                    for (int q = 0; q < 8; q++) { ta[q] = e[(bb + q) * NT * CW + oa]; tb[q] = e[(bb + q) * NT * CW + ob]; }
+                    if (cmode == CH_MULADD) {
+#pragma unroll
+                        for (int q = 0; q < 8; q++) s = s + ta[q] * tb[q];   // -ffp-contract=off: two roundings
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 8; q++) s = __builtin_fmaf(ta[q], tb[q], s);
+                    }
+                }
+                for (; bb < nbk; bb++) {
+                    const float ta = e[bb * NT * CW + oa], tb = e[bb * NT * CW + ob];
+                    s = cmode == CH_MULADD ? s + ta * tb : __builtin_fmaf(ta, tb, s);
                 }
                 if (cmode == CH_LANES) {   // hsum_ps of the eight lanes: ((0+4)+(2+6))+((1+5)+(3+7))  (src/es_quant.c:1185-1187)
                     s = s + __shfl_xor(s, 4);
@@ -435,26 +476,25 @@ __global__ __launch_bounds__(WAVE) void mv_kernel(const MvJob *__restrict__ jobs
 }  // namespace esq
 
 // ---------------------------------------------------------------------------------------------------------------------
-// Launch glue (called from es_hip_quant.cpp)
+// Launch glue (called from es_hip_quant.hip)
 
 namespace esq {
 
 using MvFn = void (*)(const MvJob *, int, MvJob, int);
 
-template <int F, int NT> static MvFn pick_cpr(int cpr) {
-    switch (cpr) {
-    case 1: return mv_kernel<F, NT, 1>;
-    case 2: return mv_kernel<F, NT, 2>;
+// Only the (NT, W) pairs the planner uses are instantiated.
+template <int F, int NT> static MvFn pick_w(int w) {
+    switch (w) {
     case 4: return mv_kernel<F, NT, 4>;
     case 8: return mv_kernel<F, NT, 8>;
     }
     return nullptr;
 }
-template <int F> static MvFn pick_nt(int nt, int cpr) {
+template <int F> static MvFn pick_nt(int nt, int w) {
     switch (nt) {
-    case 1: return pick_cpr<F, 1>(cpr);
-    case 2: return pick_cpr<F, 2>(cpr);
-    case 4: return pick_cpr<F, 4>(cpr);
+    case 1: return pick_w<F, 1>(w);
+    case 2: return pick_w<F, 2>(w);
+    case 4: return pick_w<F, 4>(w);
     }
     return nullptr;
 }
@@ -462,11 +502,11 @@ template <int F> static MvFn pick_nt(int nt, int cpr) {
 hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s) {
     MvFn fn = nullptr;
     switch (L.type) {
-    case ES_HIP_Q4_0: fn = pick_nt<ES_HIP_Q4_0>(L.nt, L.cpr); break;
-    case ES_HIP_Q5_0: fn = pick_nt<ES_HIP_Q5_0>(L.nt, L.cpr); break;
-    case ES_HIP_Q2_K: fn = pick_nt<ES_HIP_Q2_K>(L.nt, L.cpr); break;
-    case ES_HIP_Q4_K: fn = pick_nt<ES_HIP_Q4_K>(L.nt, L.cpr); break;
-    case ES_HIP_Q6_K: fn = pick_nt<ES_HIP_Q6_K>(L.nt, L.cpr); break;
+    case ES_HIP_Q4_0: fn = pick_nt<ES_HIP_Q4_0>(L.nt, L.waves); break;
+    case ES_HIP_Q5_0: fn = pick_nt<ES_HIP_Q5_0>(L.nt, L.waves); break;
+    case ES_HIP_Q2_K: fn = pick_nt<ES_HIP_Q2_K>(L.nt, L.waves); break;
+    case ES_HIP_Q4_K: fn = pick_nt<ES_HIP_Q4_K>(L.nt, L.waves); break;
+    case ES_HIP_Q6_K: fn = pick_nt<ES_HIP_Q6_K>(L.nt, L.waves); break;
     }
     if (!fn) return hipErrorInvalidValue;
     if (L.lds > 64 * 1024) {
@@ -474,7 +514,7 @@ hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJo
                                            static_cast<int>(L.lds));
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(fn, dim3(L.grid), dim3(WAVE), L.lds, s, jobs, njobs, single, order);
+    hipLaunchKernelGGL(fn, dim3(L.grid), dim3(WAVE * L.waves), L.lds, s, jobs, njobs, single, order);
     return hipGetLastError();
 }
 

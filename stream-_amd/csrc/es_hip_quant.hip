@@ -99,9 +99,10 @@ bool fmt_info(uint32_t t, FmtInfo &f) {
 }
 
 // ---- job batches ----------------------------------------------------------------------------------------------------
-constexpr size_t LDS_TARGET = 16 * 1024;   // bytes of chain terms per workgroup when the row length allows
+constexpr size_t LDS_TARGET = 32 * 1024;   // bytes of chain terms per workgroup when the row length allows
 constexpr size_t LDS_MAX = 160 * 1024;      // gfx950 LDS per workgroup
-constexpr int MIN_WG_PER_JOB = 1024;        // at least this many workgroups per job when it has the rows
+constexpr size_t TARGET_WG = 8192;          // workgroups a launch aims for (256 CUs x 8 resident 4-wave groups x 4)
+constexpr int MIN_ITERS = 4;                // row passes per workgroup at least (one pipelined load group)
 
 struct Group {
     MvLaunch L{};
@@ -131,7 +132,7 @@ int check_req(const Req &q, const FmtInfo &f) {
     if (q.na > 1 && q.astride < packed) return fail(ES_HIP_EINVAL, "activation stride %zu < %zu bytes of one activation", q.astride, packed);
     if (q.na > 1 && q.ystride < (size_t)q.r1) return fail(ES_HIP_EINVAL, "ystride %zu < r1 %d: outputs of activations overlap", q.ystride, q.r1);
     const int slots = 64 / f.lpb, nbk = q.cols / f.be;
-    if (nbk > 8 * slots) return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this kernel handles", q.type, q.cols, 8 * slots * f.be);
+    if (nbk > 8 * slots) return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this kernel handles", q.type, q.cols, 8 * slots * f.be);   // 8 waves x one segment each
     return ES_HIP_OK;
 }
 
@@ -141,47 +142,59 @@ int pow2_at_least(int v) {
     return p;
 }
 
-// Plan one launch per format. The job order inside a format is kept.
+// waves one row is split over in the decode kernel: a power of two covering ceil(nbk / slots)
+int segments(int nbk, int slots) {
+    int seg = 1;
+    while (seg * slots < nbk) seg <<= 1;
+    return seg;
+}
+
+// Plan the launches: one per (format, workgroup size). The job order inside a launch is kept.
 int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
     out.clear();
-    std::map<uint32_t, std::vector<const Req *>> by_type;
+    std::map<std::pair<uint32_t, int>, std::vector<const Req *>> by_kind;
+    size_t total_blocks = 0;
     for (const Req &q : reqs) {
         FmtInfo f;
         if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
         int rc = check_req(q, f);
         if (rc) return rc;
-        if (q.r1 > q.r0 && q.na > 0) by_type[q.type].push_back(&q);
+        if (q.r1 == q.r0 || q.na == 0) continue;
+        const int seg = segments(q.cols / f.be, 64 / f.lpb);
+        by_kind[{q.type, seg <= 4 ? 4 : 8}].push_back(&q);
+        total_blocks += (size_t)(q.r1 - q.r0) * (q.cols / f.be);
     }
-    for (auto &kv : by_type) {
+    // workgroups of about total/TARGET_WG blocks each, each wave making at least MIN_ITERS row passes, so one launch keeps
+    // every CU busy whether it holds one matrix or a hundred
+    const size_t wg_blocks = std::max<size_t>(1, total_blocks / TARGET_WG);
+    for (auto &kv : by_kind) {
         FmtInfo f;
-        fmt_info(kv.first, f);
+        fmt_info(kv.first.first, f);
         const bool w32 = f.be == 32;
         const int slots = 64 / f.lpb;
-        int cpr = 1, max_na = 1;
-        for (const Req *q : kv.second) {
-            const int nbk = q->cols / f.be;
-            cpr = std::max(cpr, pow2_at_least((nbk + slots - 1) / slots));
-            max_na = std::max(max_na, q->na);
-        }
-        int nt = max_na >= 4 ? 4 : max_na >= 2 ? 2 : 1;
-        const int cap = w32 ? 4 : 8;   // register budget: activation slices per lane
-        while (nt > 1 && nt * cpr > cap) nt >>= 1;
+        const int waves = kv.first.second;
+        int max_na = 1;
+        for (const Req *q : kv.second) max_na = std::max(max_na, q->na);
+        const int nt = max_na >= 4 ? 4 : max_na >= 2 ? 2 : 1;
         Group g;
-        g.L.type = static_cast<int>(kv.first);
+        g.L.type = static_cast<int>(kv.first.first);
         g.L.nt = nt;
-        g.L.cpr = cpr;
+        g.L.waves = waves;
         int tile = 0;
         size_t lds = 0;
         const int cw = w32 ? 9 : 2;
         for (const Req *q : kv.second) {
             const int nbk = q->cols / f.be, rows = q->r1 - q->r0;
             const int rpi = nbk <= slots ? slots / nbk : 1;
+            const int seg = segments(nbk, slots);
+            const int rstep = (waves / seg) * rpi;   // rows one pass of the workgroup covers
             const size_t per_row = (size_t)nbk * nt * cw * sizeof(float);
             if (per_row > LDS_MAX) return fail(ES_HIP_EINVAL, "type %u cols %d: a row needs %zu bytes of LDS", q->type, q->cols, per_row);
-            int chain_cap = (int)std::min<size_t>(64, std::max<size_t>(1, LDS_TARGET / per_row));
-            if (chain_cap >= rpi) chain_cap -= chain_cap % rpi;
-            int rpw = std::max(rpi, (rows + MIN_WG_PER_JOB - 1) / MIN_WG_PER_JOB);
-            rpw = (rpw + rpi - 1) / rpi * rpi;
+            int chain_cap = (int)std::min<size_t>(256, std::max<size_t>(1, LDS_TARGET / per_row));
+            if (chain_cap >= rstep) chain_cap -= chain_cap % rstep;
+            int rpw = (int)std::max<size_t>((size_t)MIN_ITERS * rstep, (wg_blocks + nbk - 1) / nbk);
+            rpw = std::min(rpw, (rows + rstep - 1) / rstep * rstep);
+            rpw = (rpw + rstep - 1) / rstep * rstep;
             const int chain = std::min(chain_cap, rpw);
             rpw = (rpw + chain - 1) / chain * chain;   // whole chain batches per workgroup
             MvJob j{};
