@@ -126,6 +126,19 @@ int es_hip_unregister(const void *host);
 void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch);
 void es_hip_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
                          size_t ystride, float *scratch);
+/* The engine's queued job on host memory: mv_job (src/es_engine.c:144) field for field. */
+typedef struct {
+    uint32_t type;
+    const void *w;          /* host weights, row 0 (registered ranges are used in place) */
+    int rows, cols;
+    const es_hip_act *a;    /* nb prepared activations */
+    float *y;               /* host outputs, activation q's row r at y[q * ys + r] */
+    int nb;
+    size_t ys;
+} es_hip_host_job;
+/* run_jobs (src/es_engine.c:177-186) for a queue on host memory: activations go up in one copy, every job runs in one
+ * launch per format, outputs come back in one copy. Synchronous, like the reference's. Returns 0 or ES_HIP_E*. */
+int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs);
 
 /* ---- diagnostics ----------------------------------------------------------------------------------------------------- */
 /* The integer part of every (row, block) of rows [0, rows) against one activation, as the reference's kernels form it:

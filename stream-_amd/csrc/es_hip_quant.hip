@@ -551,6 +551,92 @@ static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, co
     return ES_HIP_OK;
 }
 
+int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
+    if (int rc = need_device()) return rc;
+    if (njobs < 0 || (njobs > 0 && !jobs)) return fail(ES_HIP_EINVAL, "bad job list");
+    // sizes of the staged activations, outputs and unregistered weights
+    struct Stage { size_t aoff, yoff, woff; const void *dW; size_t ab, rb; };
+    std::vector<Stage> st(njobs);
+    size_t abytes = 0, ybytes = 0, wbytes = 0;
+    for (int i = 0; i < njobs; i++) {
+        const es_hip_host_job &j = jobs[i];
+        FmtInfo f;
+        if (!fmt_info(j.type, f)) return fail(ES_HIP_EINVAL, "job %d: type %u is not computed by this library", i, j.type);
+        if (j.cols <= 0 || j.cols % f.be || j.rows < 0 || j.nb < 0) return fail(ES_HIP_EINVAL, "job %d: bad shape", i);
+        if (j.rows == 0 || j.nb == 0) continue;
+        if (!j.w || !j.a || !j.y) return fail(ES_HIP_EINVAL, "job %d: null pointer", i);
+        const int nbk = j.cols / f.be;
+        st[i].ab = (size_t)nbk * f.ab;
+        st[i].rb = (size_t)nbk * f.bb;
+        for (int q = 0; q < j.nb; q++) {
+            const void *blk = f.be == 32 ? static_cast<const void *>(j.a[q].q80) : static_cast<const void *>(j.a[q].q8);
+            if (!blk) return fail(ES_HIP_EINVAL, "job %d activation %d has no %s blocks", i, q, f.be == 32 ? "Q8_0" : "Q8_K");
+        }
+        st[i].aoff = abytes;
+        abytes += (st[i].ab * j.nb + 255) / 256 * 256;
+        st[i].yoff = ybytes;
+        ybytes += ((size_t)j.rows * j.nb * sizeof(float) + 255) / 256 * 256;
+        st[i].dW = reg_lookup(j.w, st[i].rb * j.rows);
+        if (!st[i].dW) { st[i].woff = wbytes; wbytes += (st[i].rb * j.rows + 255) / 256 * 256; }
+    }
+    std::lock_guard<std::mutex> lk(g_call_mu);
+    void *at = nullptr, *yt = nullptr, *wt = nullptr;
+    if (abytes)
+        if (int rc = g_atmp.get(abytes, &at)) return rc;
+    if (ybytes)
+        if (int rc = g_ytmp.get(ybytes, &yt)) return rc;
+    if (wbytes)
+        if (int rc = g_wtmp.get(wbytes, &wt)) return rc;
+    std::vector<uint8_t> pack(abytes);
+    std::vector<Req> reqs;
+    hipError_t e;
+    for (int i = 0; i < njobs; i++) {
+        const es_hip_host_job &j = jobs[i];
+        if (j.rows == 0 || j.nb == 0) continue;
+        FmtInfo f;
+        fmt_info(j.type, f);
+        for (int q = 0; q < j.nb; q++) {
+            const void *blk = f.be == 32 ? static_cast<const void *>(j.a[q].q80) : static_cast<const void *>(j.a[q].q8);
+            memcpy(pack.data() + st[i].aoff + st[i].ab * q, blk, st[i].ab);
+        }
+        const void *dW = st[i].dW;
+        if (!dW) {
+            dW = static_cast<uint8_t *>(wt) + st[i].woff;
+            if ((e = hipMemcpy(const_cast<void *>(dW), j.w, st[i].rb * j.rows, hipMemcpyHostToDevice)) != hipSuccess)
+                return hip_fail(e, "weight upload");
+        }
+        reqs.push_back({j.type, dW, static_cast<uint8_t *>(at) + st[i].aoff,
+                        reinterpret_cast<float *>(static_cast<uint8_t *>(yt) + st[i].yoff), nullptr, nullptr, 0, j.rows, j.cols,
+                        j.nb, st[i].ab, (size_t)j.rows});
+    }
+    if (abytes && (e = hipMemcpy(at, pack.data(), abytes, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
+    std::vector<Group> groups;
+    if (int rc = plan_groups(reqs, groups)) return rc;
+    size_t total = 0;
+    for (auto &g : groups) total += g.jobs.size() * sizeof(MvJob);
+    void *table = nullptr;
+    if (total)
+        if (int rc = g_table.get(total, &table)) return rc;
+    size_t off = 0;
+    for (auto &g : groups) {
+        MvJob *dj = reinterpret_cast<MvJob *>(static_cast<uint8_t *>(table) + off);
+        if ((e = hipMemcpy(dj, g.jobs.data(), g.jobs.size() * sizeof(MvJob), hipMemcpyHostToDevice)) != hipSuccess)
+            return hip_fail(e, "job table upload");
+        if ((e = esq::mv_launch(g.L, dj, (int)g.jobs.size(), g.jobs[0], g_order.load(), nullptr)) != hipSuccess)
+            return hip_fail(e, "kernel launch");
+        off += g.jobs.size() * sizeof(MvJob);
+    }
+    std::vector<uint8_t> out(ybytes);
+    if (ybytes && (e = hipMemcpy(out.data(), yt, ybytes, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
+    for (int i = 0; i < njobs; i++) {
+        const es_hip_host_job &j = jobs[i];
+        if (j.rows == 0 || j.nb == 0) continue;
+        const float *src = reinterpret_cast<const float *>(out.data() + st[i].yoff);
+        for (int q = 0; q < j.nb; q++) memcpy(j.y + j.ys * q, src + (size_t)j.rows * q, sizeof(float) * j.rows);
+    }
+    return ES_HIP_OK;
+}
+
 void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch) {
     (void)scratch;
     host_multi(type, W, cols, r0, r1, a, 1, y, 0);

@@ -37,6 +37,21 @@ class Act(C.Structure):   # es_hip_act (= the reference's es_act)
     _fields_ = [("x", C.c_void_p), ("q8", C.c_void_p), ("q80", C.c_void_p), ("cols", C.c_int)]
 
 
+class HostJob(C.Structure):   # es_hip_host_job (= the reference engine's mv_job)
+    _fields_ = [("type", C.c_uint32), ("w", C.c_void_p), ("rows", C.c_int), ("cols", C.c_int), ("a", C.c_void_p),
+                ("y", C.c_void_p), ("nb", C.c_int), ("ys", C.c_size_t)]
+
+
+def act_records(t: int, acts: np.ndarray, cols: int):
+    """es_act records pointing at the rows of `acts` [na, nblocks] (q8 for K-quants, q80 for Q4_0/Q5_0)"""
+    na = acts.shape[0]
+    recs = (Act * max(na, 1))()
+    for q in range(na):
+        p = acts.ctypes.data + q * acts.strides[0]
+        recs[q] = Act(None, p if BLOCK_ELEMS[t] == 256 else None, p if BLOCK_ELEMS[t] == 32 else None, cols)
+    return recs
+
+
 def row_bytes(t: int, cols: int) -> int:
     return cols // BLOCK_ELEMS[t] * BLOCK_BYTES[t]
 
@@ -95,6 +110,7 @@ class Lib:
             ("es_hip_matvec", None, [u32, vp, i, i, i, vp, vp, vp]),
             ("es_hip_matvec_multi", None, [u32, vp, i, i, i, vp, i, vp, sz, vp]),
             ("es_hip_block_ints_dev", i, [u32, vp, i, i, vp, vp, vp, vp]),
+            ("es_hip_run_jobs_host", i, [vp, i]),
         ]:
             fn = getattr(L, name)
             fn.restype, fn.argtypes = res, args
@@ -213,10 +229,7 @@ class Lib:
         """es_hip_matvec_multi with es_act records pointing at `acts` [na, nblocks]; y [na, ystride] updated in place"""
         acts = np.ascontiguousarray(acts)
         na = acts.shape[0]
-        recs = (Act * na)()
-        for q in range(na):
-            p = acts.ctypes.data + q * acts.strides[0]
-            recs[q] = Act(None, p if BLOCK_ELEMS[t] == 256 else None, p if BLOCK_ELEMS[t] == 32 else None, cols)
+        recs = act_records(t, acts, cols)
         if na == 1:
             self._L.es_hip_matvec(t, W.ctypes.data, cols, r0, r1, recs, y.ctypes.data, None)
         else:
@@ -225,6 +238,20 @@ class Lib:
         if err:
             raise EsHipError(-1, err)
         return y
+
+
+    def run_jobs_host(self, jobs):
+        """jobs: list of (type, W host uint8, rows, cols, acts [nb, nblocks], y [nb, ys] float32 written in place)"""
+        arr = (HostJob * max(len(jobs), 1))()
+        keep = []
+        for k, (t, W, rows, cols, acts, y) in enumerate(jobs):
+            acts = np.ascontiguousarray(acts)
+            recs = act_records(t, acts, cols)
+            keep += [acts, recs]
+            arr[k] = HostJob(t, W.ctypes.data, rows, cols, C.cast(recs, C.c_void_p), y.ctypes.data, acts.shape[0],
+                             y.strides[0] // 4)
+        self._check(self._L.es_hip_run_jobs_host(arr, len(jobs)))
+        del keep
 
 
 class Plan:

@@ -241,3 +241,21 @@ def test_invalid_arguments_are_rejected(hip):
         hip.matvec_multi_dev(E.Q4_K, buf, 256, 0, 4, buf, 292, 2, buf, 2)
     hip.matvec_multi_dev(E.Q4_K, buf, 256, 4, 4, buf, 0, 1, buf, 0)   # empty range: nothing to do
     buf.close()
+
+
+def test_run_jobs_host_is_the_engine_queue(hip, orc):
+    """es_hip_run_jobs_host: the engine's run_jobs queue on host memory (registered and unregistered weights, mixed formats,
+    gate/up written into one buffer with ystride 2ff as moe_n/dense_n do, src/es_engine.c:899-902, 957-960)"""
+    ff, n, na = 768, 2048, 3
+    Wg, acts = mtest_inputs(orc, O.Q4_K, ff, n, na, 501)
+    Wu, _ = mtest_inputs(orc, O.Q4_K, ff, n, na, 502)
+    Wh, hacts = mtest_inputs(orc, O.Q6_K, n, ff, na, 503)
+    hip.register(Wu)
+    gu = np.zeros((na, 2 * ff), np.float32)
+    yd = np.zeros((na, n), np.float32)
+    hip.run_jobs_host([(O.Q4_K, Wg, ff, n, acts, gu[:, :ff]), (O.Q4_K, Wu, ff, n, acts, gu[:, ff:]),
+                       (O.Q6_K, Wh, n, ff, hacts, yd)])
+    assert np.array_equal(bits(gu[:, :ff]), bits(orc.matvec_multi(O.Q4_K, Wg, n, ff, acts)))
+    assert np.array_equal(bits(gu[:, ff:]), bits(orc.matvec_multi(O.Q4_K, Wu, n, ff, acts)))
+    assert np.array_equal(bits(yd), bits(orc.matvec_multi(O.Q6_K, Wh, ff, n, hacts)))
+    hip.unregister(Wu)
