@@ -146,6 +146,9 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs);
  * Q2_K: isum) and aux[r * nb + b] = Q4_K mins or Q2_K summs (0 for the others). nb = cols / block elements. Device memory. */
 int es_hip_block_ints_dev(uint32_t type, const void *W, int cols, int rows, const void *act, int32_t *dots, int32_t *aux,
                           void *stream);
+/* Products with at least n activations (Q4_K) run on the int8 matrix cores; fewer go to the vector kernels. n <= 0 keeps
+ * everything on the vector kernels. Default 32. Returns the previous value. Results are identical either way. */
+int es_hip_set_mfma_min_batch(int n);
 /* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`
  * (after `warmup` untimed runs). */
 double es_hip_plan_time_ms(es_hip_plan *plan, int warmup, int iters, void *stream);

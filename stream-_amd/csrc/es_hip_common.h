@@ -43,6 +43,24 @@ struct MvLaunch {
 };
 hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s);
 
+// The batched (matrix-core) form: rows [r0, r1) against na activations that a pre-pass has re-laid out as
+// xq[nbk][na_pad][256] int8 values and xm[nbk][na_pad][MM_XM_BYTES] meta.
+constexpr int MM_NA_PAD = 128;           // activation count padding of the pre-pass planes (workgroup tiles: 64 or 128 each way)
+constexpr int MM_XM_BYTES = 32;   // lo[2], hi[2] (pair sums split in bytes), d, pad
+struct MmJob {
+    const uint8_t *W;     // row 0
+    const uint8_t *xq;
+    const uint8_t *xm;
+    float *y;
+    uint64_t ystride, row_bytes;
+    int r0, r1, cols, na, na_pad;
+    int tile0, ntok_tiles;
+};
+hipError_t mm_prep_launch(const uint8_t *act, uint64_t astride, int na, int na_pad, int nbk, uint8_t *xq, uint8_t *xm,
+                          hipStream_t s);
+hipError_t mm_launch(int type, int bm, int bn, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
+                     hipStream_t s);
+
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     // exact for every finite half, subnormals included (v_cvt_f32_f16)
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xffffu)));

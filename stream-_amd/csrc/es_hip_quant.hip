@@ -19,6 +19,12 @@
 
 #include "es_hip_common.h"
 
+// activations per workgroup tile of the matrix-core kernel (its rows are 64): 0 chooses per product, 64 or 128 fixes it
+// (a build-time tuning knob)
+#ifndef ESQ_MM_BN
+#define ESQ_MM_BN 0
+#endif
+
 using esq::MvJob;
 using esq::MvLaunch;
 
@@ -229,6 +235,158 @@ int launch_single(const Group &g, hipStream_t s) {
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "kernel launch");
 }
 
+// ---- batches: decode-kernel launches plus, for large Q4_K batches, pre-passes and one matrix-core launch -------------
+std::atomic<int> g_mm_min{32};   // activations per product from which the matrix-core kernel is used (<= 0: never)
+
+struct Prep {   // one activation pre-pass (shared by products that read the same activations)
+    const uint8_t *act;
+    uint64_t astride;
+    int na, na_pad, nbk;
+    size_t xq_off, xm_off;
+};
+
+struct MmGroup {   // one matrix-core launch: products sharing a workgroup tile shape
+    int bm, bn, grid = 0;
+    std::vector<esq::MmJob> jobs;
+    size_t off = 0;   // byte offset of the job table in the device image
+};
+
+struct Batch {
+    std::vector<Group> mv;
+    std::vector<Prep> preps;
+    std::vector<esq::MmJob> mm;   // xq / xm hold workspace offsets until bind(); copied into mmg by plan_batch
+    std::vector<MmGroup> mmg;
+    size_t ws_bytes = 0;
+    std::vector<size_t> mv_off;   // byte offsets of the job tables in the device image
+    size_t table_bytes = 0;
+};
+
+// Workgroup tile of a product: the largest (best operand reuse) that still gives every CU a workgroup.
+void mm_tile(const esq::MmJob &j, int &bm, int &bn) {
+    static const int cand[2] = {128, 64};
+    const int rows = j.r1 - j.r0;
+    bm = 64;
+    for (int c : cand) {
+        bn = ESQ_MM_BN ? ESQ_MM_BN : c;
+        if ((long)((rows + bm - 1) / bm) * (j.na_pad / bn) >= 256) return;
+    }
+}
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+bool mm_eligible(const Req &q) {
+    const int mn = g_mm_min.load();
+    return q.type == ES_HIP_Q4_K && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
+}
+
+int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
+    bt = Batch();
+    std::vector<Req> mv;
+    for (const Req &q : reqs) {
+        FmtInfo f;
+        if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
+        if (int rc = check_req(q, f)) return rc;
+        if (!mm_eligible(q)) { mv.push_back(q); continue; }
+        const int nbk = q.cols / 256, na_pad = (q.na + esq::MM_NA_PAD - 1) / esq::MM_NA_PAD * esq::MM_NA_PAD;
+        const uint64_t astride = q.astride ? q.astride : (uint64_t)nbk * f.ab;
+        const Prep *pp = nullptr;
+        for (const Prep &p : bt.preps)
+            if (p.act == q.act && p.astride == astride && p.na == q.na && p.nbk == nbk) pp = &p;
+        if (!pp) {
+            Prep p{static_cast<const uint8_t *>(q.act), astride, q.na, na_pad, nbk, 0, 0};
+            p.xq_off = bt.ws_bytes;
+            bt.ws_bytes += align256((size_t)nbk * na_pad * 256);
+            p.xm_off = bt.ws_bytes;
+            bt.ws_bytes += align256((size_t)nbk * na_pad * esq::MM_XM_BYTES);
+            bt.preps.push_back(p);
+            pp = &bt.preps.back();
+        }
+        esq::MmJob j{};
+        j.W = static_cast<const uint8_t *>(q.W);
+        j.xq = reinterpret_cast<const uint8_t *>(pp->xq_off);
+        j.xm = reinterpret_cast<const uint8_t *>(pp->xm_off);
+        j.y = q.y;
+        j.ystride = q.ystride;
+        j.row_bytes = (uint64_t)nbk * f.bb;
+        j.r0 = q.r0;
+        j.r1 = q.r1;
+        j.cols = q.cols;
+        j.na = q.na;
+        j.na_pad = na_pad;
+        bt.mm.push_back(j);
+    }
+    // one launch per tile shape; inside a launch the longest rows (most superblocks) come first, so the longest-running
+    // workgroups start first
+    std::stable_sort(bt.mm.begin(), bt.mm.end(), [](const esq::MmJob &x, const esq::MmJob &y) { return x.cols > y.cols; });
+    for (esq::MmJob j : bt.mm) {
+        int bm, bn;
+        mm_tile(j, bm, bn);
+        MmGroup *g = nullptr;
+        for (MmGroup &x : bt.mmg)
+            if (x.bm == bm && x.bn == bn) g = &x;
+        if (!g) { bt.mmg.push_back(MmGroup{bm, bn}); g = &bt.mmg.back(); }
+        j.tile0 = g->grid;   // a multiple of 8: the kernel maps tiles to XCDs by id % 8
+        j.ntok_tiles = j.na_pad / bn;
+        const int row_tiles = (j.r1 - j.r0 + bm - 1) / bm;
+        g->grid += 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
+        g->jobs.push_back(j);
+    }
+    if (int rc = plan_groups(mv, bt.mv)) return rc;
+    size_t off = 0;
+    for (const Group &g : bt.mv) {
+        bt.mv_off.push_back(off);
+        off += align256(g.jobs.size() * sizeof(MvJob));
+    }
+    for (MmGroup &g : bt.mmg) {
+        g.off = off;
+        off += align256(g.jobs.size() * sizeof(esq::MmJob));
+    }
+    bt.table_bytes = off;
+    return ES_HIP_OK;
+}
+
+// point the matrix-core jobs at a workspace of ws_bytes
+void bind(Batch &bt, uint8_t *ws) {
+    for (MmGroup &g : bt.mmg)
+        for (esq::MmJob &j : g.jobs) {
+            j.xq = ws + reinterpret_cast<uintptr_t>(j.xq);
+            j.xm = ws + reinterpret_cast<uintptr_t>(j.xm);
+        }
+    for (Prep &p : bt.preps) {   // offsets become addresses too (kept as integers)
+        p.xq_off = reinterpret_cast<uintptr_t>(ws) + p.xq_off;
+        p.xm_off = reinterpret_cast<uintptr_t>(ws) + p.xm_off;
+    }
+}
+
+std::vector<uint8_t> table_image(const Batch &bt) {
+    std::vector<uint8_t> img(bt.table_bytes);
+    for (size_t i = 0; i < bt.mv.size(); i++)
+        memcpy(img.data() + bt.mv_off[i], bt.mv[i].jobs.data(), bt.mv[i].jobs.size() * sizeof(MvJob));
+    for (const MmGroup &g : bt.mmg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MmJob));
+    return img;
+}
+
+// launches in stream order: pre-passes, decode kernels, matrix-core kernel. tables: the uploaded image, or null to pass
+// single jobs by value.
+int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t s) {
+    hipError_t e;
+    for (const Prep &p : bt.preps)
+        if ((e = esq::mm_prep_launch(p.act, p.astride, p.na, p.na_pad, p.nbk, reinterpret_cast<uint8_t *>(p.xq_off),
+                                     reinterpret_cast<uint8_t *>(p.xm_off), s)) != hipSuccess)
+            return hip_fail(e, "pre-pass launch");
+    for (size_t i = 0; i < bt.mv.size(); i++) {
+        const Group &g = bt.mv[i];
+        const MvJob *dj = tables ? reinterpret_cast<const MvJob *>(tables + bt.mv_off[i]) : nullptr;
+        if ((e = esq::mv_launch(g.L, dj, (int)g.jobs.size(), g.jobs[0], order, s)) != hipSuccess) return hip_fail(e, "kernel launch");
+    }
+    for (const MmGroup &g : bt.mmg) {
+        const esq::MmJob *dj = tables ? reinterpret_cast<const esq::MmJob *>(tables + g.off) : nullptr;
+        if ((e = esq::mm_launch(ES_HIP_Q4_K, g.bm, g.bn, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+            return hip_fail(e, "matrix-core launch");
+    }
+    return ES_HIP_OK;
+}
+
 // ---- reusable device scratch (host drop-ins, run_jobs tables) ----------------------------------------------------
 struct Scratch {
     std::mutex mu;
@@ -268,6 +426,26 @@ void *reg_lookup(const void *h, size_t n) {
     --it;
     if (a + n > it->first + it->second.bytes) return nullptr;
     return static_cast<uint8_t *>(it->second.dev) + (a - it->first);
+}
+
+// Plan, upload the job tables (and bind the pre-pass workspace) in scratch, launch, wait: the synchronous path shared by
+// run_jobs, run_jobs_host and the host drop-ins. The caller holds g_call_mu.
+int run_sync(const std::vector<Req> &reqs, hipStream_t s) {
+    Batch bt;
+    if (int rc = plan_batch(reqs, bt)) return rc;
+    if (bt.mv.empty() && bt.mm.empty()) return ES_HIP_OK;
+    hipError_t e = hipStreamSynchronize(s);   // the scratch may still be read by an earlier call's kernels
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    void *dev = nullptr;
+    const size_t ws_at = align256(bt.table_bytes);
+    if (int rc = g_table.get(ws_at + bt.ws_bytes, &dev)) return rc;
+    bind(bt, static_cast<uint8_t *>(dev) + ws_at);
+    const std::vector<uint8_t> img = table_image(bt);
+    if (!img.empty() && (e = hipMemcpyAsync(dev, img.data(), img.size(), hipMemcpyHostToDevice, s)) != hipSuccess)
+        return hip_fail(e, "job table upload");
+    if (int rc = launch_batch(bt, static_cast<const uint8_t *>(dev), g_order.load(), s)) return rc;
+    e = hipStreamSynchronize(s);   // like the reference's run_jobs: every product is done on return
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
 }  // namespace
@@ -340,10 +518,19 @@ int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int 
                             float *y, size_t ystride, void *stream) {
     if (int rc = need_device()) return rc;
     std::vector<Req> reqs{{type, W, act, y, nullptr, nullptr, r0, r1, cols, na, astride, ystride}};
-    std::vector<Group> groups;
-    if (int rc = plan_groups(reqs, groups)) return rc;
-    if (groups.empty()) return ES_HIP_OK;
-    return launch_single(groups[0], static_cast<hipStream_t>(stream));
+    Batch bt;
+    if (int rc = plan_batch(reqs, bt)) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (bt.mm.empty()) return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
+    // matrix-core path: a stream-ordered workspace for the pre-pass, jobs passed by value
+    void *ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, bt.ws_bytes, s);
+    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (pre-pass workspace)");
+    bind(bt, static_cast<uint8_t *>(ws));
+    const int rc = launch_batch(bt, nullptr, g_order.load(), s);
+    e = hipFreeAsync(ws, s);
+    if (rc) return rc;
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipFreeAsync");
 }
 
 int es_hip_matvec_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, float *y, void *stream) {
@@ -380,36 +567,15 @@ int es_hip_run_jobs(const es_hip_job *jobs, int njobs, void *stream) {
     if (njobs < 0 || (njobs > 0 && !jobs)) return fail(ES_HIP_EINVAL, "bad job list");
     std::vector<Req> reqs;
     to_reqs(jobs, njobs, reqs);
-    std::vector<Group> groups;
-    if (int rc = plan_groups(reqs, groups)) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     std::lock_guard<std::mutex> lk(g_call_mu);
-    size_t total = 0;
-    for (auto &g : groups) total += g.jobs.size() * sizeof(MvJob);
-    void *table = nullptr;
-    if (total) {
-        hipError_t e = hipStreamSynchronize(s);   // the table buffer may still be read by an earlier call's kernels
-        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-        if (int rc = g_table.get(total, &table)) return rc;
-    }
-    size_t off = 0;
-    for (auto &g : groups) {
-        MvJob *dj = reinterpret_cast<MvJob *>(static_cast<uint8_t *>(table) + off);
-        hipError_t e = hipMemcpyAsync(dj, g.jobs.data(), g.jobs.size() * sizeof(MvJob), hipMemcpyHostToDevice, s);
-        if (e != hipSuccess) return hip_fail(e, "job table upload");
-        e = esq::mv_launch(g.L, dj, (int)g.jobs.size(), g.jobs[0], g_order.load(), s);
-        if (e != hipSuccess) return hip_fail(e, "kernel launch");
-        off += g.jobs.size() * sizeof(MvJob);
-    }
-    hipError_t e = hipStreamSynchronize(s);   // run_jobs returns when every product is done, like the reference's
-    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipStreamSynchronize");
+    return run_sync(reqs, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"
 
 struct es_hip_plan {
-    std::vector<Group> groups;
-    std::vector<MvJob *> tables;
+    Batch bt;
+    uint8_t *dev = nullptr;   // job tables, then the pre-pass workspace
     int order;
 };
 
@@ -422,38 +588,34 @@ es_hip_plan *es_hip_plan_create(const es_hip_job *jobs, int njobs) {
     to_reqs(jobs, njobs, reqs);
     auto *p = new es_hip_plan();
     p->order = g_order.load();
-    if (plan_groups(reqs, p->groups)) { delete p; return nullptr; }
-    for (auto &g : p->groups) {
-        MvJob *dj = nullptr;
-        hipError_t e = hipMalloc(&dj, g.jobs.size() * sizeof(MvJob));
-        if (e == hipSuccess) e = hipMemcpy(dj, g.jobs.data(), g.jobs.size() * sizeof(MvJob), hipMemcpyHostToDevice);
-        if (e != hipSuccess) {
-            hip_fail(e, "plan table");
-            if (dj) (void)hipFree(dj);
-            es_hip_plan_destroy(p);
-            return nullptr;
-        }
-        p->tables.push_back(dj);
+    if (plan_batch(reqs, p->bt)) { delete p; return nullptr; }
+    const size_t ws_at = align256(p->bt.table_bytes);
+    hipError_t e = hipMalloc(&p->dev, std::max<size_t>(ws_at + p->bt.ws_bytes, 256));
+    if (e == hipSuccess) {
+        bind(p->bt, p->dev + ws_at);
+        const std::vector<uint8_t> img = table_image(p->bt);
+        if (!img.empty()) e = hipMemcpy(p->dev, img.data(), img.size(), hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+        hip_fail(e, "plan tables");
+        es_hip_plan_destroy(p);
+        return nullptr;
     }
     return p;
 }
 
 int es_hip_plan_run(es_hip_plan *p, void *stream) {
     if (!p) return fail(ES_HIP_EINVAL, "null plan");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    for (size_t i = 0; i < p->groups.size(); i++) {
-        const Group &g = p->groups[i];
-        hipError_t e = esq::mv_launch(g.L, p->tables[i], (int)g.jobs.size(), g.jobs[0], p->order, s);
-        if (e != hipSuccess) return hip_fail(e, "kernel launch");
-    }
-    return ES_HIP_OK;
+    return launch_batch(p->bt, p->dev, p->order, static_cast<hipStream_t>(stream));
 }
 
 void es_hip_plan_destroy(es_hip_plan *p) {
     if (!p) return;
-    for (MvJob *t : p->tables) (void)hipFree(t);
+    if (p->dev) (void)hipFree(p->dev);
     delete p;
 }
+
+int es_hip_set_mfma_min_batch(int n) { return g_mm_min.exchange(n); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
@@ -542,9 +704,7 @@ static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, co
     if ((e = hipMemcpy(at, pack.data(), pack.size(), hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
     if (int rc = g_ytmp.get(sizeof(float) * n * na, &yt)) return rc;
     std::vector<Req> reqs{{type, dW, at, static_cast<float *>(yt), nullptr, nullptr, 0, n, cols, na, ab, (size_t)n}};
-    std::vector<Group> groups;
-    if (int rc = plan_groups(reqs, groups)) return rc;
-    if (int rc = launch_single(groups[0], nullptr)) return rc;
+    if (int rc = run_sync(reqs, nullptr)) return rc;
     std::vector<float> out((size_t)n * na);
     if ((e = hipMemcpy(out.data(), yt, out.size() * sizeof(float), hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
     for (int q = 0; q < na; q++) memcpy(y + ystride * q + r0, out.data() + (size_t)n * q, sizeof(float) * n);
@@ -610,22 +770,7 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
                         j.nb, st[i].ab, (size_t)j.rows});
     }
     if (abytes && (e = hipMemcpy(at, pack.data(), abytes, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
-    std::vector<Group> groups;
-    if (int rc = plan_groups(reqs, groups)) return rc;
-    size_t total = 0;
-    for (auto &g : groups) total += g.jobs.size() * sizeof(MvJob);
-    void *table = nullptr;
-    if (total)
-        if (int rc = g_table.get(total, &table)) return rc;
-    size_t off = 0;
-    for (auto &g : groups) {
-        MvJob *dj = reinterpret_cast<MvJob *>(static_cast<uint8_t *>(table) + off);
-        if ((e = hipMemcpy(dj, g.jobs.data(), g.jobs.size() * sizeof(MvJob), hipMemcpyHostToDevice)) != hipSuccess)
-            return hip_fail(e, "job table upload");
-        if ((e = esq::mv_launch(g.L, dj, (int)g.jobs.size(), g.jobs[0], g_order.load(), nullptr)) != hipSuccess)
-            return hip_fail(e, "kernel launch");
-        off += g.jobs.size() * sizeof(MvJob);
-    }
+    if (int rc = run_sync(reqs, nullptr)) return rc;
     std::vector<uint8_t> out(ybytes);
     if (ybytes && (e = hipMemcpy(out.data(), yt, ybytes, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
     for (int i = 0; i < njobs; i++) {

@@ -111,6 +111,7 @@ class Lib:
             ("es_hip_matvec_multi", None, [u32, vp, i, i, i, vp, i, vp, sz, vp]),
             ("es_hip_block_ints_dev", i, [u32, vp, i, i, vp, vp, vp, vp]),
             ("es_hip_run_jobs_host", i, [vp, i]),
+            ("es_hip_set_mfma_min_batch", i, [i]),
         ]:
             fn = getattr(L, name)
             fn.restype, fn.argtypes = res, args
@@ -130,6 +131,9 @@ class Lib:
 
     def get_order(self) -> int:
         return self._L.es_hip_get_order()
+
+    def set_mfma_min_batch(self, n: int) -> int:
+        return self._L.es_hip_set_mfma_min_batch(n)
 
     def _check(self, rc):
         if rc is not None and rc < 0:

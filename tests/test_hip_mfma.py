@@ -1,0 +1,110 @@
+"""GPU parity of the batched (matrix-core) Q4_K path: bit-identical to the oracle, and to the vector kernels, in every
+reference order, at the BASELINE prefill shapes and at ragged edges (rows not a multiple of the 64-row tile, activation
+counts not a multiple of the 128-activation tile, row sub-ranges, padded strides)."""
+import numpy as np
+import pytest
+
+import es_hip_quant as E
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MODES = [(E.ORDER_X86_CONTRACT, O.CONTRACT, O.PATH_X86), (E.ORDER_X86_STRICT, O.STRICT, O.PATH_X86),
+         (E.ORDER_SCALAR, O.STRICT, O.PATH_SCALAR)]
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def inputs(orc, rows, cols, na, seed, gauss=False):
+    st = np.array([seed], np.uint64)
+    if gauss:
+        W = orc.quantize_rows(O.Q4_K, orc.gauss(seed, 0.02, rows * cols).reshape(rows, cols))
+        x = orc.gauss(seed + 1, 1.0, na * cols).reshape(na, cols)
+    else:
+        W = orc.mtest_blocks(O.Q4_K, st, rows, cols)
+        x = orc.mtest_acts(st, na * cols).reshape(na, cols)
+    return W, orc.quantize_act(O.Q4_K, x)
+
+
+@pytest.fixture
+def hipm(hip):
+    prev = hip.set_mfma_min_batch(32)
+    yield hip
+    hip.set_mfma_min_batch(prev)
+    hip.set_order(E.ORDER_X86_CONTRACT)
+
+
+@pytest.mark.parametrize("rows,cols,na,gauss", [(8192, 2048, 40, True), (2048, 8192, 33, False), (768, 2048, 130, False),
+                                                (100, 512, 37, False), (64, 256, 128, True)])
+@pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
+def test_mfma_vs_oracle(hipm, orc, rows, cols, na, gauss, mode):
+    hipm.set_order(mode[0])
+    W, acts = inputs(orc, rows, cols, na, rows + na, gauss)
+    y = hipm.matvec_multi(O.Q4_K, W, cols, rows, acts)
+    pick = np.unique(np.array([0, 1, na // 2, na - 1]))
+    ref = orc.matvec_multi(O.Q4_K, W, cols, rows, acts[pick], mode[1], mode[2])
+    assert np.array_equal(bits(y[pick]), bits(ref))
+
+
+@pytest.mark.parametrize("rows,cols,na", [(8192, 2048, 512), (2048, 8192, 512), (1000, 1024, 200)])
+def test_mfma_equals_vector_path(hipm, orc, rows, cols, na):
+    """the full BASELINE prefill shape (T=512): matrix-core result == vector-kernel result, bit for bit"""
+    W, acts = inputs(orc, rows, cols, na, 7 * rows + na)
+    y_mm = hipm.matvec_multi(O.Q4_K, W, cols, rows, acts)
+    hipm.set_mfma_min_batch(0)
+    y_mv = hipm.matvec_multi(O.Q4_K, W, cols, rows, acts)
+    hipm.set_mfma_min_batch(32)
+    assert np.array_equal(bits(y_mm), bits(y_mv))
+    ref = orc.matvec_multi(O.Q4_K, W, cols, rows, acts[:2])
+    assert np.array_equal(bits(y_mm[:2]), bits(ref))
+
+
+def test_mfma_row_range_and_strides(hipm, orc):
+    rows, cols, na, r0, r1 = 300, 1024, 70, 37, 251
+    W, acts = inputs(orc, rows, cols, na, 99)
+    ab = cols // 256 * 292
+    astride = ab + 52
+    araw = np.zeros(na * astride, np.uint8)
+    for q in range(na):
+        araw[q * astride:q * astride + ab] = acts[q].view(np.uint8)
+    ystride = rows + 13
+    sentinel = np.float32(-777.0)
+    dW, dA = hipm.upload(W), hipm.upload(araw)
+    dY = hipm.upload(np.full(na * ystride, sentinel, np.float32))
+    hipm.matvec_multi_dev(O.Q4_K, dW, cols, r0, r1, dA, astride, na, dY, ystride)
+    y = hipm.download(dY, np.zeros((na, ystride), np.float32))
+    ref = orc.matvec_multi(O.Q4_K, W, cols, rows, acts[[0, 69]])
+    assert np.array_equal(bits(y[[0, 69], r0:r1]), bits(ref[:, r0:r1]))
+    assert np.all(y[:, :r0] == sentinel) and np.all(y[:, r1:rows] == sentinel) and np.all(y[:, rows:] == sentinel)
+
+
+def test_mfma_in_job_batches_and_plans(hipm, orc):
+    """gate and up sharing one activation set (one pre-pass) plus down, in one run_jobs call and in a plan"""
+    n, ff, T = 1024, 768, 64
+    Wg, xa = inputs(orc, ff, n, T, 11)
+    Wu, _ = inputs(orc, ff, n, T, 12)
+    Wd, ha = inputs(orc, n, ff, T, 13)
+    dWg, dWu, dWd, dxa, dha = (hipm.upload(a) for a in (Wg, Wu, Wd, xa, ha))
+    dgu, dy = hipm.alloc(T * 2 * ff * 4), hipm.alloc(T * n * 4)
+    specs = [dict(type=O.Q4_K, rows=ff, cols=n, W=dWg, act=dxa, astride=xa.strides[0], nb=T, y=dgu, ystride=2 * ff),
+             dict(type=O.Q4_K, rows=ff, cols=n, W=dWu, act=dxa, astride=xa.strides[0], nb=T, y=dgu.offset(ff * 4), ystride=2 * ff),
+             dict(type=O.Q4_K, rows=n, cols=ff, W=dWd, act=dha, astride=ha.strides[0], nb=T, y=dy, ystride=n)]
+    refs = [orc.matvec_multi(O.Q4_K, Wg, n, ff, xa[:3]), orc.matvec_multi(O.Q4_K, Wu, n, ff, xa[:3]),
+            orc.matvec_multi(O.Q4_K, Wd, ff, n, ha[:3])]
+    for runner in ("run_jobs", "plan"):
+        hipm.memset(dgu, 0, T * 2 * ff * 4)
+        hipm.memset(dy, 0, T * n * 4)
+        if runner == "run_jobs":
+            hipm.run_jobs(specs)
+        else:
+            p = hipm.plan(specs)
+            p.run()
+            hipm.synchronize()
+            p.close()
+        gu = hipm.download(dgu, np.zeros((T, 2 * ff), np.float32))
+        y = hipm.download(dy, np.zeros((T, n), np.float32))
+        assert np.array_equal(bits(gu[:3, :ff]), bits(refs[0])), runner
+        assert np.array_equal(bits(gu[:3, ff:]), bits(refs[1])), runner
+        assert np.array_equal(bits(y[:3]), bits(refs[2])), runner
