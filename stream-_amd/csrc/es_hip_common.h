@@ -44,9 +44,10 @@ struct MvLaunch {
 hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s);
 
 // The batched (matrix-core) form: rows [r0, r1) against na activations that a pre-pass has re-laid out as
-// xq[nbk][na_pad][256] int8 values and xm[nbk][na_pad][MM_XM_BYTES] meta.
-constexpr int MM_NA_PAD = 128;           // activation count padding of the pre-pass planes (workgroup tiles: 64 or 128 each way)
-constexpr int MM_XM_BYTES = 32;   // lo[2], hi[2] (pair sums split in bytes), d, pad
+// xq[nbk][na_pad][256] int8 values, then (at xm, in the same allocation) xm[nbk][na_pad][16] pair sums and
+// xd[nbk][na_pad] float scales, xd = xm + nbk * na_pad * 16.
+constexpr int MM_NA_PAD = 128;    // activation count padding of the pre-pass planes (workgroup tiles: 64 or 128 each way)
+constexpr int MM_XM_BYTES = 20;   // per activation and superblock: 8 low bytes, 8 high bytes of the pair sums, d
 struct MmJob {
     const uint8_t *W;     // row 0
     const uint8_t *xq;

@@ -19,8 +19,8 @@
 
 #include "es_hip_common.h"
 
-// activations per workgroup tile of the matrix-core kernel (its rows are 64): 0 chooses per product, 64 or 128 fixes it
-// (a build-time tuning knob)
+// workgroup tile of the matrix-core kernel (rows = activations): 0 chooses per product, 64 or 128 fixes it (a build-time
+// tuning knob)
 #ifndef ESQ_MM_BN
 #define ESQ_MM_BN 0
 #endif
@@ -263,11 +263,10 @@ struct Batch {
 
 // Workgroup tile of a product: the largest (best operand reuse) that still gives every CU a workgroup.
 void mm_tile(const esq::MmJob &j, int &bm, int &bn) {
-    static const int cand[2] = {128, 64};
+    static const int cand[2] = {128, 64};   // square tiles: 128 x 128, 64 x 64
     const int rows = j.r1 - j.r0;
-    bm = 64;
     for (int c : cand) {
-        bn = ESQ_MM_BN ? ESQ_MM_BN : c;
+        bm = bn = ESQ_MM_BN ? ESQ_MM_BN : c;
         if ((long)((rows + bm - 1) / bm) * (j.na_pad / bn) >= 256) return;
     }
 }
