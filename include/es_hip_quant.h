@@ -140,6 +140,39 @@ typedef struct {
  * launch per format, outputs come back in one copy. Synchronous, like the reference's. Returns 0 or ES_HIP_E*. */
 int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs);
 
+/* ---- MoE expert FFN: the expert part of moe_n (src/es_engine.c:848-942) --------------------------------------------- */
+/* The routed experts of one layer, resident on the device. Experts whose pointers are NULL must not be routed. */
+typedef struct {
+    uint32_t gate_type, up_type, down_type;   /* GGML types; gate and up take the same kind of activation blocks */
+    int n;                                    /* model width: gate/up cols, down rows */
+    int ff;                                   /* expert width: gate/up rows, down cols */
+    int n_exp;
+    const void *const *gate;                  /* host arrays of n_exp device pointers, row 0 of expert e's matrix */
+    const void *const *up;
+    const void *const *down;
+} es_hip_moe;
+/* The expert FFN of N tokens routed by route() (src/es_engine.c:744-835): token t's k[t] <= kmax experts are
+ * sel[t * kmax + j] with weights w[t * kmax + j] (host arrays). x: device activation blocks of the N tokens (Q8_K for a
+ * K-quant gate/up, Q8_0 for Q4_0/Q5_0), token t at x + t * xstride bytes (0: packed). out: device, token t's n outputs at
+ * out + t * ostride floats. In stream order on the device:
+ *   the pairs (t, j) are grouped by expert in order of first use (:871-888);
+ *   gate and up products of every pair into [pair][2 ff] (:899-903), one launch per format;
+ *   h = g / (1 + expf(-g)) * u, requantized as es_act_prepare does for the down type (:913-914);
+ *   down products into [pair][n] (:916-918);
+ *   out[t] = sum over j of w[t][j] * y[pair (t, j)], in j order from 0 (:925-932).
+ * Results are bit-identical to moe_n's expert part for a model without expert biases, latent projection or the gpt-oss /
+ * situ activations. es_hip_moe_ffn is synchronous. */
+int es_hip_moe_ffn(const es_hip_moe *m, int N, const int *k, const int *sel, const float *w, int kmax, const void *x,
+                   size_t xstride, float *out, size_t ostride, void *stream);
+/* The same as a prepared plan: grouping, job tables and workspace are made once; runs are asynchronous on `stream`. The
+ * routing (k, sel, w) is captured at creation; x, out and the expert bytes may change between runs. */
+typedef struct es_hip_moe_plan es_hip_moe_plan;
+es_hip_moe_plan *es_hip_moe_plan_create(const es_hip_moe *m, int N, const int *k, const int *sel, const float *w, int kmax,
+                                        const void *x, size_t xstride, float *out, size_t ostride);   /* NULL on failure */
+int    es_hip_moe_plan_run(es_hip_moe_plan *plan, void *stream);
+void   es_hip_moe_plan_destroy(es_hip_moe_plan *plan);
+double es_hip_moe_plan_time_ms(es_hip_moe_plan *plan, int warmup, int iters, void *stream);
+
 /* ---- diagnostics ----------------------------------------------------------------------------------------------------- */
 /* The integer part of every (row, block) of rows [0, rows) against one activation, as the reference's kernels form it:
  * dots[r * nb + b] = the block's integer dot (Q4_0/Q5_0: the sum of the eight AVX2 lane sums; Q4_K: dot; Q6_K: tot;
@@ -149,6 +182,8 @@ int es_hip_block_ints_dev(uint32_t type, const void *W, int cols, int rows, cons
 /* Products with at least n activations (Q4_K) run on the int8 matrix cores; fewer go to the vector kernels. n <= 0 keeps
  * everything on the vector kernels. Default 32. Returns the previous value. Results are identical either way. */
 int es_hip_set_mfma_min_batch(int n);
+/* The MoE SwiGLU alone on n device floats: h[i] = g[i] / (1 + expf(-g[i])) * u[i] as src/es_engine.c:913 computes it. */
+int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream);
 /* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`
  * (after `warmup` untimed runs). */
 double es_hip_plan_time_ms(es_hip_plan *plan, int warmup, int iters, void *stream);

@@ -202,6 +202,52 @@ class Oracle:
                                  _p(np.ascontiguousarray(w, np.float32)), n_tok, k, n, _p(out))
         return out
 
+    def moe_ffn(self, types, experts, n, ff, x_acts, sel, w, k=None, order=CONTRACT, path=PATH_X86):
+        """The expert part of moe_n (src/es_engine.c:871-932) for N tokens, composed from the restated pieces:
+        types = (gate, up, down); experts[e] = (Wg, Wu, Wd) block bytes; x_acts [N, blocks] Q8 rows of the gate/up type;
+        sel, w [N, kmax]; k [N] experts per token (default kmax). Returns out [N, n]."""
+        sel = np.asarray(sel, np.int32)
+        N, kmax = sel.shape
+        k = np.full(N, kmax, np.int32) if k is None else np.asarray(k, np.int32)
+        uex, cnt = [], []            # distinct experts in order of first use (:871-879)
+        for t in range(N):
+            for j in range(k[t]):
+                e = int(sel[t, j])
+                if e not in uex:
+                    uex.append(e)
+                    cnt.append(0)
+                cnt[uex.index(e)] += 1
+        start = np.concatenate([[0], np.cumsum(cnt)[:-1]]).astype(int) if uex else np.zeros(0, int)
+        fill = [0] * len(uex)
+        rowof = np.zeros((N, kmax), np.int32)
+        tok_of = np.zeros(int(sum(cnt)), np.int32)
+        for t in range(N):           # (:880-888)
+            for j in range(k[t]):
+                u = uex.index(int(sel[t, j]))
+                r = start[u] + fill[u]
+                fill[u] += 1
+                rowof[t, j] = r
+                tok_of[r] = t
+        R = len(tok_of)
+        gt, ut, dt = types
+        gu = np.zeros((R, 2 * ff), np.float32)
+        for u, e in enumerate(uex):  # gate/up multi-jobs (:899-903)
+            rows = slice(start[u], start[u] + cnt[u])
+            xa = x_acts[tok_of[rows]]
+            gu[rows, :ff] = self.matvec_multi(gt, experts[e][0], n, ff, xa, order, path)
+            gu[rows, ff:] = self.matvec_multi(ut, experts[e][1], n, ff, xa, order, path)
+        h = self.swiglu(gu[:, :ff], gu[:, ff:]) if R else np.zeros((0, ff), np.float32)   # (:913)
+        ha = self.quantize_act(dt, h) if R else None                                      # (:914)
+        ye = np.zeros((R, n), np.float32)
+        for u, e in enumerate(uex):  # down multi-jobs (:916-918)
+            rows = slice(start[u], start[u] + cnt[u])
+            ye[rows] = self.matvec_multi(dt, experts[e][2], ff, n, ha[rows], order, path)
+        out = np.zeros((N, n), np.float32)
+        for t in range(N):           # combine (:925-932), one token at a time so k may vary
+            if k[t]:
+                out[t] = self.moe_combine(ye, rowof[t:t + 1, :k[t]], np.asarray(w, np.float32)[t:t + 1, :k[t]])[0]
+        return out
+
     # ---- CPU baseline ----
     def cpu_bench(self, fn_ptr, t, W, mat_bytes, nmat, rows, cols, acts, nthreads, min_seconds=0.4):
         acts = np.ascontiguousarray(acts)

@@ -27,6 +27,7 @@ struct MvJob {
     float *y;             // activation q's row r at y[q * ystride + r]
     int32_t *ints;        // optional: per (row, block) integer dots of activation 0 (diagnostics), else null
     int32_t *ints_aux;
+    const int *arow;      // optional: activation q is row arow[q] of act (a gather), else row q
     uint64_t astride;     // bytes between activations
     uint64_t ystride;     // floats between activations' outputs
     uint64_t row_bytes;
@@ -57,10 +58,17 @@ struct MmJob {
     int r0, r1, cols, na, na_pad;
     int tile0, ntok_tiles;
 };
-hipError_t mm_prep_launch(const uint8_t *act, uint64_t astride, int na, int na_pad, int nbk, uint8_t *xq, uint8_t *xm,
-                          hipStream_t s);
+hipError_t mm_prep_launch(const uint8_t *act, const int *arow, uint64_t astride, int na, int na_pad, int nbk, uint8_t *xq,
+                          uint8_t *xm, hipStream_t s);
 hipError_t mm_launch(int type, int bm, int bn, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                      hipStream_t s);
+
+// MoE glue (es_hip_moe.hip): SwiGLU + requantization of rows x ff gate|up pairs ([row][2 ff] floats) into Q8_K (q8k) or
+// Q8_0 blocks at ha + row * hstride; the weighted combine of the expert outputs ye[pair][n] into out[t][n].
+hipError_t moe_swiglu_launch(const float *gu, int rows, int ff, bool q8k, uint8_t *ha, uint64_t hstride, hipStream_t s);
+hipError_t moe_combine_launch(const float *ye, const int *rowof, const float *w, const int *k, int kmax, int ntok, int n,
+                              float *out, uint64_t ostride, hipStream_t s);
+hipError_t swiglu_plain_launch(const float *g, const float *u, float *h, long n, hipStream_t s);
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     // exact for every finite half, subnormals included (v_cvt_f32_f16)

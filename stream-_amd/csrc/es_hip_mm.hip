@@ -41,14 +41,14 @@ __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
 
 // ---- pre-pass --------------------------------------------------------------------------------------------------------
 // One thread per dword of an activation's Q8_K row (nbk blocks of 73 dwords: d, 64 of qs, 8 of bsums pairs), so the
-// reads are coalesced; padding activations t >= na get zeros.
-__global__ void act_prep_q8k(const uint8_t *__restrict__ act, uint64_t astride, int na, int na_pad, int nbk,
-                             uint8_t *__restrict__ xq, uint8_t *__restrict__ xm) {
+// reads are coalesced; padding activations t >= na get zeros. Activation t is row arow[t] of act when arow is given.
+__global__ void act_prep_q8k(const uint8_t *__restrict__ act, const int *__restrict__ arow, uint64_t astride, int na,
+                             int na_pad, int nbk, uint8_t *__restrict__ xq, uint8_t *__restrict__ xm) {
     const long per = (long)nbk * 73;
     const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= (long)na_pad * per) return;
     const int t = (int)(id / per), k = (int)(id % per), b = k / 73, w = k % 73;
-    const uint32_t v = t < na ? ldg<uint32_t>(act + (size_t)t * astride + 4 * (size_t)k) : 0u;
+    const uint32_t v = t < na ? ldg<uint32_t>(act + (size_t)(arow ? arow[t] : t) * astride + 4 * (size_t)k) : 0u;
     const size_t bt = (size_t)b * na_pad + t;
     if (w == 0) {
         reinterpret_cast<uint32_t *>(xm + (size_t)nbk * na_pad * 16)[bt] = v;   // d
@@ -306,12 +306,12 @@ __global__ __launch_bounds__(512) void mm_q4k_kernel(const MmJob *__restrict__ j
 }
 
 // ---- launch glue -------------------------------------------------------------------------------------------------
-hipError_t mm_prep_launch(const uint8_t *act, uint64_t astride, int na, int na_pad, int nbk, uint8_t *xq, uint8_t *xm,
-                          hipStream_t s) {
+hipError_t mm_prep_launch(const uint8_t *act, const int *arow, uint64_t astride, int na, int na_pad, int nbk, uint8_t *xq,
+                          uint8_t *xm, hipStream_t s) {
     const long total = (long)na_pad * nbk * 73;
     const int threads = 256;
-    hipLaunchKernelGGL(act_prep_q8k, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0, s, act, astride, na,
-                       na_pad, nbk, xq, xm);
+    hipLaunchKernelGGL(act_prep_q8k, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0, s, act, arow, astride,
+                       na, na_pad, nbk, xq, xm);
     return hipGetLastError();
 }
 

@@ -372,7 +372,10 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
         typename L::Act act[NT];
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            if (live && t < nt) L::load_act(J.act + (size_t)(t0 + t) * J.astride + (size_t)b * AB, k, act[t]);
+            if (live && t < nt) {
+                const int q = J.arow ? J.arow[t0 + t] : t0 + t;
+                L::load_act(J.act + (size_t)q * J.astride + (size_t)b * AB, k, act[t]);
+            }
             else L::zero_act(act[t]);
         }
 

@@ -122,6 +122,7 @@ struct Req {   // one product as the launch planner sees it
     int32_t *ints, *aux;
     int r0, r1, cols, na;
     size_t astride, ystride;
+    const int *arow;   // optional device gather table: activation q is row arow[q] of act
 };
 
 int check_req(const Req &q, const FmtInfo &f) {
@@ -135,7 +136,7 @@ int check_req(const Req &q, const FmtInfo &f) {
         return fail(ES_HIP_EINVAL, "activation blocks must be 4-byte aligned (pointer and stride)");
     if (reinterpret_cast<uintptr_t>(q.y) & 3) return fail(ES_HIP_EINVAL, "y must be 4-byte aligned");
     const size_t packed = (size_t)(q.cols / f.be) * f.ab;
-    if (q.na > 1 && q.astride < packed) return fail(ES_HIP_EINVAL, "activation stride %zu < %zu bytes of one activation", q.astride, packed);
+    if ((q.na > 1 || q.arow) && q.astride < packed) return fail(ES_HIP_EINVAL, "activation stride %zu < %zu bytes of one activation", q.astride, packed);
     if (q.na > 1 && q.ystride < (size_t)q.r1) return fail(ES_HIP_EINVAL, "ystride %zu < r1 %d: outputs of activations overlap", q.ystride, q.r1);
     const int slots = 64 / f.lpb, nbk = q.cols / f.be;
     if (nbk > 8 * slots) return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this kernel handles", q.type, q.cols, 8 * slots * f.be);   // 8 waves x one segment each
@@ -209,6 +210,7 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
             j.y = q->y;
             j.ints = q->ints;
             j.ints_aux = q->aux;
+            j.arow = q->arow;
             j.astride = q->astride ? q->astride : (size_t)nbk * f.ab;
             j.ystride = q->ystride;
             j.row_bytes = (size_t)nbk * f.bb;
@@ -240,6 +242,7 @@ std::atomic<int> g_mm_min{32};   // activations per product from which the matri
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
+    const int *arow;
     uint64_t astride;
     int na, na_pad, nbk;
     size_t xq_off, xm_off;
@@ -290,9 +293,9 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         const uint64_t astride = q.astride ? q.astride : (uint64_t)nbk * f.ab;
         const Prep *pp = nullptr;
         for (const Prep &p : bt.preps)
-            if (p.act == q.act && p.astride == astride && p.na == q.na && p.nbk == nbk) pp = &p;
+            if (p.act == q.act && p.arow == q.arow && p.astride == astride && p.na == q.na && p.nbk == nbk) pp = &p;
         if (!pp) {
-            Prep p{static_cast<const uint8_t *>(q.act), astride, q.na, na_pad, nbk, 0, 0};
+            Prep p{static_cast<const uint8_t *>(q.act), q.arow, astride, q.na, na_pad, nbk, 0, 0};
             p.xq_off = bt.ws_bytes;
             bt.ws_bytes += align256((size_t)nbk * na_pad * 256);
             p.xm_off = bt.ws_bytes;
@@ -370,7 +373,7 @@ std::vector<uint8_t> table_image(const Batch &bt) {
 int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t s) {
     hipError_t e;
     for (const Prep &p : bt.preps)
-        if ((e = esq::mm_prep_launch(p.act, p.astride, p.na, p.na_pad, p.nbk, reinterpret_cast<uint8_t *>(p.xq_off),
+        if ((e = esq::mm_prep_launch(p.act, p.arow, p.astride, p.na, p.na_pad, p.nbk, reinterpret_cast<uint8_t *>(p.xq_off),
                                      reinterpret_cast<uint8_t *>(p.xm_off), s)) != hipSuccess)
             return hip_fail(e, "pre-pass launch");
     for (size_t i = 0; i < bt.mv.size(); i++) {
@@ -790,6 +793,219 @@ void es_hip_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1,
                          size_t ystride, float *scratch) {
     (void)scratch;
     host_multi(type, W, cols, r0, r1, a, na, y, ystride);
+}
+
+}  // extern "C"
+
+// ---- MoE expert FFN ---------------------------------------------------------------------------------------------------
+struct es_hip_moe_plan {
+    Batch gu, dn;                // gate/up products, down products
+    uint8_t *bufs = nullptr;     // gather table, combine tables, gate|up outputs, requantized h, expert outputs
+    uint8_t *tabs = nullptr;     // job tables and pre-pass workspaces of both batches
+    size_t gu_tab = 0, dn_tab = 0;
+    int order = 0;
+    int rows = 0, ff = 0, n = 0, ntok = 0, kmax = 0;
+    bool h_q8k = true;
+    uint64_t hstride = 0, ostride = 0;
+    float *bgu = nullptr, *bye = nullptr, *out = nullptr, *w = nullptr;
+    uint8_t *ha = nullptr;
+    int *rowof = nullptr, *kk = nullptr;
+};
+
+namespace {
+
+// moe_n's grouping (src/es_engine.c:871-888): distinct experts in order of first use, each pair's row grouped by expert
+void moe_group(int ntok, const int *k, const int *sel, int kmax, std::vector<int> &uex, std::vector<int> &cnt,
+               std::vector<int> &start, std::vector<int> &rowof, std::vector<int> &tok_of) {
+    uex.clear();
+    cnt.clear();
+    std::vector<int> slot(ntok * (size_t)kmax, -1);
+    for (int t = 0; t < ntok; t++)
+        for (int j = 0; j < k[t]; j++) {
+            const int e = sel[t * kmax + j];
+            size_t u = 0;
+            while (u < uex.size() && uex[u] != e) u++;
+            if (u == uex.size()) { uex.push_back(e); cnt.push_back(0); }
+            cnt[u]++;
+            slot[t * (size_t)kmax + j] = (int)u;
+        }
+    start.assign(uex.size(), 0);
+    for (size_t u = 0, r = 0; u < uex.size(); u++) { start[u] = (int)r; r += cnt[u]; }
+    std::vector<int> fill(uex.size(), 0);
+    rowof.assign(ntok * (size_t)kmax, 0);
+    tok_of.clear();
+    int total = 0;
+    for (int c : cnt) total += c;
+    tok_of.assign(total, 0);
+    for (int t = 0; t < ntok; t++)
+        for (int j = 0; j < k[t]; j++) {
+            const int u = slot[t * (size_t)kmax + j], r = start[u] + fill[u]++;
+            rowof[t * (size_t)kmax + j] = r;
+            tok_of[r] = t;
+        }
+}
+
+int moe_build(es_hip_moe_plan *p, const es_hip_moe *m, int N, const int *k, const int *sel, const float *w, int kmax,
+              const void *x, size_t xstride, float *out, size_t ostride) {
+    if (!m) return fail(ES_HIP_EINVAL, "null expert set");
+    FmtInfo fg, fu, fd;
+    if (!fmt_info(m->gate_type, fg) || !fmt_info(m->up_type, fu) || !fmt_info(m->down_type, fd))
+        return fail(ES_HIP_EINVAL, "an expert type is not computed by this library");
+    if (fg.be != fu.be) return fail(ES_HIP_EINVAL, "gate and up take different activation blocks");
+    if (m->n <= 0 || m->ff <= 0 || m->n % fg.be || m->ff % fd.be) return fail(ES_HIP_EINVAL, "bad widths n %d, ff %d", m->n, m->ff);
+    if (m->n_exp <= 0 || !m->gate || !m->up || !m->down) return fail(ES_HIP_EINVAL, "bad expert table");
+    if (N < 0 || kmax <= 0 || (N > 0 && (!k || !sel || !w || !x || !out))) return fail(ES_HIP_EINVAL, "bad routing or buffers");
+    if (ostride == 0) ostride = (size_t)m->n;
+    if (N > 1 && ostride < (size_t)m->n) return fail(ES_HIP_EINVAL, "ostride %zu < n %d", ostride, m->n);
+    for (int t = 0; t < N; t++) {
+        if (k[t] < 0 || k[t] > kmax) return fail(ES_HIP_EINVAL, "token %d: k %d outside [0, %d]", t, k[t], kmax);
+        for (int j = 0; j < k[t]; j++) {
+            const int e = sel[t * kmax + j];
+            if (e < 0 || e >= m->n_exp) return fail(ES_HIP_EINVAL, "token %d: expert %d outside [0, %d)", t, e, m->n_exp);
+            if (!m->gate[e] || !m->up[e] || !m->down[e]) return fail(ES_HIP_EINVAL, "expert %d is routed but has no weights", e);
+        }
+    }
+    std::vector<int> uex, cnt, start, rowof, tok_of;
+    moe_group(N, k, sel, kmax, uex, cnt, start, rowof, tok_of);
+    const int R = (int)tok_of.size(), n = m->n, ff = m->ff;
+    p->order = g_order.load();
+    p->rows = R;
+    p->ff = ff;
+    p->n = n;
+    p->ntok = N;
+    p->kmax = kmax;
+    p->h_q8k = fd.be == 256;
+    p->hstride = (uint64_t)(ff / fd.be) * fd.ab;
+    p->ostride = ostride;
+    p->out = out;
+    // fixed buffers
+    size_t off = 0;
+    const size_t o_arow = off;  off += align256(sizeof(int) * std::max(R, 1));
+    const size_t o_rowof = off; off += align256(sizeof(int) * std::max<size_t>(rowof.size(), 1));
+    const size_t o_w = off;     off += align256(sizeof(float) * std::max<size_t>(rowof.size(), 1));
+    const size_t o_k = off;     off += align256(sizeof(int) * std::max(N, 1));
+    const size_t o_gu = off;    off += align256(sizeof(float) * 2 * ff * (size_t)std::max(R, 1));
+    const size_t o_ha = off;    off += align256(p->hstride * std::max(R, 1));
+    const size_t o_ye = off;    off += align256(sizeof(float) * n * (size_t)std::max(R, 1));
+    hipError_t e = hipMalloc(&p->bufs, off);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc (MoE buffers)");
+    int *arow = reinterpret_cast<int *>(p->bufs + o_arow);
+    p->rowof = reinterpret_cast<int *>(p->bufs + o_rowof);
+    p->w = reinterpret_cast<float *>(p->bufs + o_w);
+    p->kk = reinterpret_cast<int *>(p->bufs + o_k);
+    p->bgu = reinterpret_cast<float *>(p->bufs + o_gu);
+    p->ha = p->bufs + o_ha;
+    p->bye = reinterpret_cast<float *>(p->bufs + o_ye);
+    std::vector<float> wv(rowof.size(), 0.0f);
+    for (int t = 0; t < N; t++)
+        for (int j = 0; j < k[t]; j++) wv[t * (size_t)kmax + j] = w[t * kmax + j];
+    std::vector<int> kv(k, k + N);
+    if ((R && (e = hipMemcpy(arow, tok_of.data(), sizeof(int) * R, hipMemcpyHostToDevice)) != hipSuccess) ||
+        (N && (e = hipMemcpy(p->rowof, rowof.data(), sizeof(int) * rowof.size(), hipMemcpyHostToDevice)) != hipSuccess) ||
+        (N && (e = hipMemcpy(p->w, wv.data(), sizeof(float) * wv.size(), hipMemcpyHostToDevice)) != hipSuccess) ||
+        (N && (e = hipMemcpy(p->kk, kv.data(), sizeof(int) * N, hipMemcpyHostToDevice)) != hipSuccess))
+        return hip_fail(e, "MoE table upload");
+    // the two grouped products
+    const uint64_t xs = xstride ? xstride : (uint64_t)(n / fg.be) * fg.ab;
+    std::vector<Req> gu, dn;
+    for (size_t u = 0; u < uex.size(); u++) {
+        const int ex = uex[u], s0 = start[u], c = cnt[u];
+        float *y = p->bgu + (size_t)s0 * 2 * ff;
+        gu.push_back({m->gate_type, m->gate[ex], x, y, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0});
+        gu.push_back({m->up_type, m->up[ex], x, y + ff, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0});
+        dn.push_back({m->down_type, m->down[ex], p->ha + (size_t)s0 * p->hstride, p->bye + (size_t)s0 * n, nullptr, nullptr, 0, n,
+                      ff, c, p->hstride, (size_t)n, nullptr});
+    }
+    if (int rc = plan_batch(gu, p->gu)) return rc;
+    if (int rc = plan_batch(dn, p->dn)) return rc;
+    const size_t gu_ws = align256(p->gu.table_bytes), dn_tab = align256(gu_ws + p->gu.ws_bytes),
+                 dn_ws = align256(dn_tab + p->dn.table_bytes), total = dn_ws + p->dn.ws_bytes;
+    if ((e = hipMalloc(&p->tabs, std::max<size_t>(total, 256))) != hipSuccess) return hip_fail(e, "hipMalloc (MoE tables)");
+    p->gu_tab = 0;
+    p->dn_tab = dn_tab;
+    bind(p->gu, p->tabs + gu_ws);
+    bind(p->dn, p->tabs + dn_ws);
+    const std::vector<uint8_t> gi = table_image(p->gu), di = table_image(p->dn);
+    if ((!gi.empty() && (e = hipMemcpy(p->tabs, gi.data(), gi.size(), hipMemcpyHostToDevice)) != hipSuccess) ||
+        (!di.empty() && (e = hipMemcpy(p->tabs + dn_tab, di.data(), di.size(), hipMemcpyHostToDevice)) != hipSuccess))
+        return hip_fail(e, "MoE job tables");
+    return ES_HIP_OK;
+}
+
+int moe_run(const es_hip_moe_plan *p, hipStream_t s) {
+    if (int rc = launch_batch(p->gu, p->tabs + p->gu_tab, p->order, s)) return rc;
+    hipError_t e = esq::moe_swiglu_launch(p->bgu, p->rows, p->ff, p->h_q8k, p->ha, p->hstride, s);
+    if (e != hipSuccess) return hip_fail(e, "SwiGLU launch");
+    if (int rc = launch_batch(p->dn, p->tabs + p->dn_tab, p->order, s)) return rc;
+    e = esq::moe_combine_launch(p->bye, p->rowof, p->w, p->kk, p->kmax, p->ntok, p->n, p->out, p->ostride, s);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "combine launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+es_hip_moe_plan *es_hip_moe_plan_create(const es_hip_moe *m, int N, const int *k, const int *sel, const float *w, int kmax,
+                                        const void *x, size_t xstride, float *out, size_t ostride) {
+    if (need_device()) return nullptr;
+    auto *p = new es_hip_moe_plan();
+    if (moe_build(p, m, N, k, sel, w, kmax, x, xstride, out, ostride)) {
+        es_hip_moe_plan_destroy(p);
+        return nullptr;
+    }
+    return p;
+}
+
+int es_hip_moe_plan_run(es_hip_moe_plan *p, void *stream) {
+    if (!p) return fail(ES_HIP_EINVAL, "null plan");
+    return moe_run(p, static_cast<hipStream_t>(stream));
+}
+
+void es_hip_moe_plan_destroy(es_hip_moe_plan *p) {
+    if (!p) return;
+    if (p->bufs) (void)hipFree(p->bufs);
+    if (p->tabs) (void)hipFree(p->tabs);
+    delete p;
+}
+
+double es_hip_moe_plan_time_ms(es_hip_moe_plan *p, int warmup, int iters, void *stream) {
+    if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < warmup; i++)
+        if (moe_run(p, s)) return -1.0;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { fail(ES_HIP_ERUNTIME, "hipEventCreate"); return -1.0; }
+    (void)hipEventRecord(a, s);
+    for (int i = 0; i < iters; i++)
+        if (moe_run(p, s)) return -1.0;
+    (void)hipEventRecord(b, s);
+    (void)hipEventSynchronize(b);
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return (double)ms / iters;
+}
+
+int es_hip_moe_ffn(const es_hip_moe *m, int N, const int *k, const int *sel, const float *w, int kmax, const void *x,
+                   size_t xstride, float *out, size_t ostride, void *stream) {
+    if (int rc = need_device()) return rc;
+    es_hip_moe_plan p;
+    int rc = moe_build(&p, m, N, k, sel, w, kmax, x, xstride, out, ostride);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!rc) rc = moe_run(&p, s);
+    hipError_t e = hipStreamSynchronize(s);   // the plan's buffers are freed below
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    if (p.bufs) (void)hipFree(p.bufs);
+    if (p.tabs) (void)hipFree(p.tabs);
+    return rc;
+}
+
+int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream) {
+    if (int rc = need_device()) return rc;
+    if (n < 0 || (n > 0 && (!g || !u || !h))) return fail(ES_HIP_EINVAL, "bad SwiGLU arguments");
+    hipError_t e = esq::swiglu_plain_launch(g, u, h, n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "SwiGLU launch");
 }
 
 }  // extern "C"

@@ -33,6 +33,11 @@ class Job(C.Structure):   # es_hip_job
                 ("astride", C.c_size_t), ("nb", C.c_int), ("y", C.c_void_p), ("ystride", C.c_size_t)]
 
 
+class Moe(C.Structure):   # es_hip_moe
+    _fields_ = [("gate_type", C.c_uint32), ("up_type", C.c_uint32), ("down_type", C.c_uint32), ("n", C.c_int),
+                ("ff", C.c_int), ("n_exp", C.c_int), ("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p)]
+
+
 class Act(C.Structure):   # es_hip_act (= the reference's es_act)
     _fields_ = [("x", C.c_void_p), ("q8", C.c_void_p), ("q80", C.c_void_p), ("cols", C.c_int)]
 
@@ -112,6 +117,11 @@ class Lib:
             ("es_hip_block_ints_dev", i, [u32, vp, i, i, vp, vp, vp, vp]),
             ("es_hip_run_jobs_host", i, [vp, i]),
             ("es_hip_set_mfma_min_batch", i, [i]),
+            ("es_hip_moe_ffn", i, [vp, i, vp, vp, vp, i, vp, sz, vp, sz, vp]),
+            ("es_hip_moe_plan_create", vp, [vp, i, vp, vp, vp, i, vp, sz, vp, sz]),
+            ("es_hip_moe_plan_run", i, [vp, vp]), ("es_hip_moe_plan_destroy", None, [vp]),
+            ("es_hip_moe_plan_time_ms", C.c_double, [vp, i, i, vp]),
+            ("es_hip_swiglu_dev", i, [vp, vp, vp, C.c_long, vp]),
         ]:
             fn = getattr(L, name)
             fn.restype, fn.argtypes = res, args
@@ -194,6 +204,19 @@ class Lib:
             raise EsHipError(-2, self.last_error())
         return Plan(self, p)
 
+    # ---- MoE expert FFN ----
+    def moe_ffn(self, args: "MoeArgs", x, xstride, out, ostride, stream=None):
+        self._check(self._L.es_hip_moe_ffn(*args.c_args(), int(x), xstride, int(out), ostride, stream))
+
+    def moe_plan(self, args: "MoeArgs", x, xstride, out, ostride) -> "Plan":
+        h = self._L.es_hip_moe_plan_create(*args.c_args(), int(x), xstride, int(out), ostride)
+        if not h:
+            raise EsHipError(-2, self.last_error())
+        return Plan(self, h, moe=True)
+
+    def swiglu_dev(self, g, u, h, n, stream=None):
+        self._check(self._L.es_hip_swiglu_dev(int(g), int(u), int(h), n, stream))
+
     def block_ints_dev(self, t, W, cols, rows, act):
         nb = cols // BLOCK_ELEMS[t]
         d = self.alloc(rows * nb * 4)
@@ -258,22 +281,46 @@ class Lib:
         del keep
 
 
+class MoeArgs:
+    """es_hip_moe plus the routing arrays, kept alive for the C call. experts: dicts of gate/up/down device pointers
+    (None for experts never routed); k: [N] ints; sel, w: [N, kmax]."""
+
+    def __init__(self, gate_type, up_type, down_type, n, ff, experts, k, sel, w):
+        ne = len(experts)
+        P = C.c_void_p * max(ne, 1)
+        self.g = P(*[int(e["gate"]) if e else None for e in experts])
+        self.u = P(*[int(e["up"]) if e else None for e in experts])
+        self.d = P(*[int(e["down"]) if e else None for e in experts])
+        self.m = Moe(gate_type, up_type, down_type, n, ff, ne, C.cast(self.g, C.c_void_p), C.cast(self.u, C.c_void_p),
+                     C.cast(self.d, C.c_void_p))
+        self.k = np.ascontiguousarray(k, np.int32)
+        self.sel = np.ascontiguousarray(sel, np.int32)
+        self.w = np.ascontiguousarray(w, np.float32)
+        self.N, self.kmax = int(self.k.shape[0]), int(self.sel.shape[1]) if self.sel.ndim == 2 else 1
+
+    def c_args(self):
+        return (C.byref(self.m), self.N, self.k.ctypes.data, self.sel.ctypes.data, self.w.ctypes.data, self.kmax)
+
+
+
 class Plan:
-    def __init__(self, lib: Lib, handle):
+    def __init__(self, lib: Lib, handle, moe: bool = False):
         self.lib, self.h = lib, handle
+        p = "es_hip_moe_plan_" if moe else "es_hip_plan_"
+        self._run, self._time, self._destroy = (getattr(lib._L, p + x) for x in ("run", "time_ms", "destroy"))
 
     def run(self, stream=None):
-        self.lib._check(self.lib._L.es_hip_plan_run(self.h, stream))
+        self.lib._check(self._run(self.h, stream))
 
     def time_ms(self, warmup: int, iters: int, stream=None) -> float:
-        ms = self.lib._L.es_hip_plan_time_ms(self.h, warmup, iters, stream)
+        ms = self._time(self.h, warmup, iters, stream)
         if ms < 0:
             raise EsHipError(-3, self.lib.last_error())
         return ms
 
     def close(self):
         if self.h:
-            self.lib._L.es_hip_plan_destroy(self.h)
+            self._destroy(self.h)
             self.h = None
 
     def __del__(self):
