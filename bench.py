@@ -6,7 +6,8 @@ Headline (decode form): Q4_K matvec at T=1 over the Llam
 than the 256 MB Infinity Cache. One step = one launch of a prepared job batch (the engine's run_jobs) over all 114
 matrices. value = weight bytes / step time, the reference's "weight GB/s" (tools/es_fmtbench.c:40, tools/es_kbench.c:294).
 
-Also reported: config 2's prefill form (T=512, int8 TOPS = 2*T*rows*cols / time), configs 1 and 3, the kernel's roofline
+Also reported: config 2's prefill form (T=512, int8 TOPS = 2*T*rows*cols / time), configs 1 and 3, the MoE layers of
+configs 4 and 5 (weight GB/s over the experts actually routed, plus config 5's attention products), the kernel's roofline
 (achieved vs 8 TB/s, kernel time from HIP events on the launch stream) and the reference's CPU kernels timed on this host
 (cpu_baseline: the reference's es_matvec_multi built from its sources, oracle/_ref, driven es_kbench-style).
 
@@ -115,6 +116,79 @@ class Workload:
             b.close()
 
 
+def route_topk(rng, n_tok, n_exp, k, norm_topk):
+    """synthetic routing: softmax over N(0,1) logits, the k largest probabilities (route(), src/es_engine.c:744-835)"""
+    logits = rng.standard_normal((n_tok, n_exp)).astype(np.float32)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    sel = np.argsort(-p, axis=1, kind="stable")[:, :k].astype(np.int32)
+    w = np.take_along_axis(p, sel, axis=1).astype(np.float32)
+    if norm_topk:
+        w /= w.sum(axis=1, keepdims=True)
+    return sel, w
+
+
+class MoeWorkload:
+    """`copies` copies of one MoE layer (experts in device memory) with one routing of N tokens, one MoE plan per copy, and
+    optionally the attention products of the same tokens (one job-batch plan per copy). A step runs every copy once."""
+
+    def __init__(self, lib, rng, types, n, ff, n_exp, k, n_tok, norm_topk, copies, attn=()):
+        self.lib, self.keep, self.plans, self.moe = lib, [], [], []
+        gt, ut, dt = types
+        sel, w = route_topk(rng, n_tok, n_exp, k, norm_topk)
+        used = sorted(set(sel.reshape(-1).tolist()))
+        eb = [E.row_bytes(gt, n) * ff, E.row_bytes(ut, n) * ff, E.row_bytes(dt, ff) * n]
+        self.weight_bytes = copies * len(used) * sum(eb)
+        one = [random_blocks(gt, ff, n, rng), random_blocks(ut, ff, n, rng), random_blocks(dt, n, ff, rng)]
+        x = quantize_acts(gt, rng.standard_normal((n_tok, n)).astype(np.float32))
+        dx = lib.upload(x)
+        self.keep.append(dx)
+        xa = quantize_acts(E.Q5_0, rng.standard_normal((n_tok, n)).astype(np.float32)) if attn else None
+        dxa = lib.upload(xa) if attn else None
+        for c in range(copies):
+            dev = lib.alloc(n_exp * sum(eb))
+            self.keep.append(dev)
+            srcs = [lib.upload(m) for m in one]
+            experts = []
+            for e in range(n_exp):
+                base = e * sum(eb)
+                ptrs = {}
+                for m, (name, nb) in enumerate(zip(("gate", "up", "down"), eb)):
+                    lib.copy_d2d(dev.offset(base), srcs[m], nb)   # every expert its own copy of the bytes
+                    ptrs[name] = dev.offset(base)
+                    base += nb
+                experts.append(ptrs)
+            for b in srcs:
+                b.close()
+            out = lib.alloc(n_tok * n * 4)
+            self.keep.append(out)
+            args = E.MoeArgs(gt, ut, dt, n, ff, experts, np.full(n_tok, k), sel, w)
+            self.moe.append(lib.moe_plan(args, dx, x.strides[0], out, n))
+            if attn:
+                specs = []
+                for (rows, cols) in attn:
+                    Wa = lib.upload(random_blocks(E.Q5_0, rows, cols, rng))
+                    ya = lib.alloc(n_tok * rows * 4)
+                    self.keep += [Wa, ya]
+                    specs.append(dict(type=E.Q5_0, rows=rows, cols=cols, W=Wa, act=dxa, astride=xa.strides[0], nb=n_tok,
+                                      y=ya, ystride=rows))
+                    self.weight_bytes += E.row_bytes(E.Q5_0, cols) * rows
+                self.plans.append(lib.plan(specs))
+        if attn:
+            self.keep.append(dxa)
+        self.copies, self.distinct = copies, len(used)
+
+    def time(self, warmup, steps):
+        """ms per copy (one layer)"""
+        return self.lib.step_time_ms(self.plans, self.moe, warmup, steps) / self.copies
+
+    def close(self):
+        for p in self.plans + self.moe:
+            p.close()
+        for b in self.keep:
+            b.close()
+
+
 def cpu_baseline(t, rows, cols, rng, seconds):
     """The reference's es_matvec_multi (oracle/_ref/libesref_clang.so, built from its sources) or, where that build is
     absent, the oracle's restatement, timed es_kbench-style on this host: a rotating set larger than the host LLC,
@@ -191,6 +265,24 @@ def main():
         extra[f"config3_q6_k_head_b{b}"] = {"gbs": round(c3.weight_bytes / (e3 * 1e-3) / 1e9, 1), "ms": round(e3, 4),
                                            "weight_bytes": c3.weight_bytes}
         c3.close()
+
+    # ---- config 4: OLMoE Q2_K experts (64 x gate/up 1024x2048, down 2048x1024), 128 tokens top-8; 8 layer copies
+    c4 = MoeWorkload(lib, rng, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8)
+    e4 = c4.time(Wm, max(3, K // 2))
+    extra["config4_q2_k_moe"] = {"gbs": round(c4.weight_bytes / c4.copies / (e4 * 1e-3) / 1e9, 1), "ms": round(e4, 4),
+                                 "weight_bytes": c4.weight_bytes // c4.copies, "experts_used": c4.distinct,
+                                 "hbm_frac": round(c4.weight_bytes / c4.copies / (e4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    c4.close()
+    # ---- config 5: Qwen3-30B-A3B-like decode batch of 32: Q5_0 attention q/k/v + 128 experts (Q4_K gate/up 768x2048,
+    # Q6_K down 2048x768) top-8 renormalised; 3 layer copies
+    c5 = MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
+                     attn=((4096, 2048), (512, 2048), (512, 2048)))
+    e5 = c5.time(Wm, max(3, K // 2))
+    extra["config5_mixed_moe_decode"] = {"gbs": round(c5.weight_bytes / c5.copies / (e5 * 1e-3) / 1e9, 1),
+                                         "ms": round(e5, 4), "weight_bytes": c5.weight_bytes // c5.copies,
+                                         "experts_used": c5.distinct,
+                                         "hbm_frac": round(c5.weight_bytes / c5.copies / (e5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    c5.close()
 
     cpu = None
     if not args.no_cpu:

@@ -171,7 +171,6 @@ es_hip_moe_plan *es_hip_moe_plan_create(const es_hip_moe *m, int N, const int *k
                                         const void *x, size_t xstride, float *out, size_t ostride);   /* NULL on failure */
 int    es_hip_moe_plan_run(es_hip_moe_plan *plan, void *stream);
 void   es_hip_moe_plan_destroy(es_hip_moe_plan *plan);
-double es_hip_moe_plan_time_ms(es_hip_moe_plan *plan, int warmup, int iters, void *stream);
 
 /* ---- diagnostics ----------------------------------------------------------------------------------------------------- */
 /* The integer part of every (row, block) of rows [0, rows) against one activation, as the reference's kernels form it:
@@ -187,6 +186,10 @@ int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *st
 /* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`
  * (after `warmup` untimed runs). */
 double es_hip_plan_time_ms(es_hip_plan *plan, int warmup, int iters, void *stream);
+/* The same for a step made of several prepared batches: each iteration runs the np plans, then the nm MoE plans, in order.
+ * Returns milliseconds per iteration, or a negative value on failure. */
+double es_hip_step_time_ms(es_hip_plan *const *plans, int np, es_hip_moe_plan *const *moe, int nm, int warmup, int iters,
+                           void *stream);
 
 #ifdef __cplusplus
 }

@@ -398,16 +398,21 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
                     L::unpack(raw[u], k, w);
                     typename L::Ints v[NT];
 #pragma unroll
-                    for (int t = 0; t < NT; t++) v[t] = ok[u] ? L::ints(w, act[t]) : typename L::Ints{};
+                    for (int t = 0; t < NT; t++) {   // activations past nt (a uniform bound) are skipped
+                        if (t < nt) v[t] = ok[u] ? L::ints(w, act[t]) : typename L::Ints{};
+                        else v[t] = typename L::Ints{};
+                    }
                     if constexpr (!W32) {
 #pragma unroll
-                        for (int t = 0; t < NT; t++) { v[t].dot = group_sum<LPB>(v[t].dot); v[t].aux = group_sum<LPB>(v[t].aux); }
+                        for (int t = 0; t < NT; t++)
+                            if (t < nt) { v[t].dot = group_sum<LPB>(v[t].dot); v[t].aux = group_sum<LPB>(v[t].aux); }
                     }
                     if (ok[u] && k == 0) {
                         float *e = lds + ((size_t)(row - ra) * nbk + b) * NT * CW;
                         if constexpr (W32) {
 #pragma unroll
                             for (int t = 0; t < NT; t++) {
+                                if (t >= nt) continue;
                                 e[t * CW] = w.d * act[t].d;
                                 if (cmode == CH_LANES) {
                                     for (int i = 0; i < 8; i++) e[t * CW + 1 + i] = static_cast<float>(v[t].lane[i]);
@@ -426,6 +431,7 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
                         } else {
 #pragma unroll
                             for (int t = 0; t < NT; t++) {
+                                if (t >= nt) continue;
                                 const Term2 tm = L::term(w, act[t], v[t], contract);
                                 e[t * CW] = tm.a;
                                 e[t * CW + 1] = tm.b;
@@ -442,8 +448,8 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
             // ---- phase 2: the reference's sequential accumulation over the row's blocks, terms read 8 blocks ahead
             const int nrow = rb - ra;
             const int per = cmode == CH_LANES ? 8 : 1;
-            for (int idx = tid; idx < nrow * NT * per; idx += WAVE * W) {
-                const int i = idx % per, t = (idx / per) % NT, rl = idx / (per * NT);
+            for (int idx = tid; idx < nrow * nt * per; idx += WAVE * W) {
+                const int i = idx % per, t = (idx / per) % nt, rl = idx / (per * nt);
                 const float *e = lds + (size_t)rl * nbk * NT * CW + t * CW;
                 const int oa = cmode == CH_LANES ? 1 + i : 0, ob = cmode == CH_LANES ? 0 : 1;
                 float s = 0.0f;

@@ -968,16 +968,24 @@ void es_hip_moe_plan_destroy(es_hip_moe_plan *p) {
     delete p;
 }
 
-double es_hip_moe_plan_time_ms(es_hip_moe_plan *p, int warmup, int iters, void *stream) {
-    if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
+double es_hip_step_time_ms(es_hip_plan *const *plans, int np, es_hip_moe_plan *const *moe, int nm, int warmup, int iters,
+                           void *stream) {
+    if (np < 0 || nm < 0 || iters <= 0 || (np && !plans) || (nm && !moe)) { fail(ES_HIP_EINVAL, "bad step"); return -1.0; }
     hipStream_t s = static_cast<hipStream_t>(stream);
+    auto one = [&]() {
+        for (int i = 0; i < np; i++)
+            if (es_hip_plan_run(plans[i], stream)) return false;
+        for (int i = 0; i < nm; i++)
+            if (es_hip_moe_plan_run(moe[i], stream)) return false;
+        return true;
+    };
     for (int i = 0; i < warmup; i++)
-        if (moe_run(p, s)) return -1.0;
+        if (!one()) return -1.0;
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { fail(ES_HIP_ERUNTIME, "hipEventCreate"); return -1.0; }
     (void)hipEventRecord(a, s);
     for (int i = 0; i < iters; i++)
-        if (moe_run(p, s)) return -1.0;
+        if (!one()) return -1.0;
     (void)hipEventRecord(b, s);
     (void)hipEventSynchronize(b);
     float ms = 0.0f;

@@ -120,7 +120,7 @@ class Lib:
             ("es_hip_moe_ffn", i, [vp, i, vp, vp, vp, i, vp, sz, vp, sz, vp]),
             ("es_hip_moe_plan_create", vp, [vp, i, vp, vp, vp, i, vp, sz, vp, sz]),
             ("es_hip_moe_plan_run", i, [vp, vp]), ("es_hip_moe_plan_destroy", None, [vp]),
-            ("es_hip_moe_plan_time_ms", C.c_double, [vp, i, i, vp]),
+            ("es_hip_step_time_ms", C.c_double, [vp, i, vp, i, i, i, vp]),
             ("es_hip_swiglu_dev", i, [vp, vp, vp, C.c_long, vp]),
         ]:
             fn = getattr(L, name)
@@ -213,6 +213,15 @@ class Lib:
         if not h:
             raise EsHipError(-2, self.last_error())
         return Plan(self, h, moe=True)
+
+    def step_time_ms(self, plans, moe_plans, warmup: int, iters: int, stream=None) -> float:
+        """ms per iteration of: every plan in `plans`, then every MoE plan in `moe_plans`, timed with HIP events"""
+        P = (C.c_void_p * max(len(plans), 1))(*[p.h for p in plans])
+        M = (C.c_void_p * max(len(moe_plans), 1))(*[p.h for p in moe_plans])
+        ms = self._L.es_hip_step_time_ms(P, len(plans), M, len(moe_plans), warmup, iters, stream)
+        if ms < 0:
+            raise EsHipError(-3, self.last_error())
+        return ms
 
     def swiglu_dev(self, g, u, h, n, stream=None):
         self._check(self._L.es_hip_swiglu_dev(int(g), int(u), int(h), n, stream))
@@ -307,16 +316,14 @@ class Plan:
     def __init__(self, lib: Lib, handle, moe: bool = False):
         self.lib, self.h = lib, handle
         p = "es_hip_moe_plan_" if moe else "es_hip_plan_"
-        self._run, self._time, self._destroy = (getattr(lib._L, p + x) for x in ("run", "time_ms", "destroy"))
+        self.moe = moe
+        self._run, self._destroy = getattr(lib._L, p + "run"), getattr(lib._L, p + "destroy")
 
     def run(self, stream=None):
         self.lib._check(self._run(self.h, stream))
 
     def time_ms(self, warmup: int, iters: int, stream=None) -> float:
-        ms = self._time(self.h, warmup, iters, stream)
-        if ms < 0:
-            raise EsHipError(-3, self.lib.last_error())
-        return ms
+        return self.lib.step_time_ms([] if self.moe else [self], [self] if self.moe else [], warmup, iters, stream)
 
     def close(self):
         if self.h:
