@@ -178,9 +178,13 @@ void   es_hip_moe_plan_destroy(es_hip_moe_plan *plan);
  * Q2_K: isum) and aux[r * nb + b] = Q4_K mins or Q2_K summs (0 for the others). nb = cols / block elements. Device memory. */
 int es_hip_block_ints_dev(uint32_t type, const void *W, int cols, int rows, const void *act, int32_t *dots, int32_t *aux,
                           void *stream);
-/* Products with at least n activations (Q4_K) run on the int8 matrix cores; fewer go to the vector kernels. n <= 0 keeps
- * everything on the vector kernels. Default 32. Returns the previous value. Results are identical either way. */
+/* Kernel choice by batch size (results are identical either way; each returns the previous value):
+ *   es_hip_set_mfma_min_batch: Q4_K products with at least n activations run on the prefill matrix-core kernel (default 32);
+ *   es_hip_set_small_batch_min: other Q2_K / Q4_K products with at least n activations run on the small-batch matrix-core
+ *     kernel (default 8);
+ * the rest go to the vector kernels. n <= 0 switches the kernel off. */
 int es_hip_set_mfma_min_batch(int n);
+int es_hip_set_small_batch_min(int n);
 /* The MoE SwiGLU alone on n device floats: h[i] = g[i] / (1 + expf(-g[i])) * u[i] as src/es_engine.c:913 computes it. */
 int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream);
 /* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`

@@ -45,10 +45,9 @@ struct MvLaunch {
 hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s);
 
 // The batched (matrix-core) form: rows [r0, r1) against na activations that a pre-pass has re-laid out as
-// xq[nbk][na_pad][256] int8 values, then (at xm, in the same allocation) xm[nbk][na_pad][16] pair sums and
-// xd[nbk][na_pad] float scales, xd = xm + nbk * na_pad * 16.
-constexpr int MM_NA_PAD = 128;    // activation count padding of the pre-pass planes (workgroup tiles: 64 or 128 each way)
-constexpr int MM_XM_BYTES = 20;   // per activation and superblock: 8 low bytes, 8 high bytes of the pair sums, d
+// xq[nbk][na_pad][256] int8 values, then (at xm, in the same allocation) xm[nbk][na_pad][16 or 32] meta and
+// xd[nbk][na_pad] float scales right after the xm plane.
+constexpr int MM_NA_PAD = 128;    // activation count padding of the pre-pass planes for the prefill kernel
 struct MmJob {
     const uint8_t *W;     // row 0
     const uint8_t *xq;
@@ -58,10 +57,35 @@ struct MmJob {
     int r0, r1, cols, na, na_pad;
     int tile0, ntok_tiles;
 };
-hipError_t mm_prep_launch(const uint8_t *act, const int *arow, uint64_t astride, int na, int na_pad, int nbk, uint8_t *xq,
-                          uint8_t *xm, hipStream_t s);
+// One activation pre-pass: kind 0 writes 16 bytes of meta per activation and superblock (pair sums of the Q4_K
+// sub-blocks, low | high bytes), kind 1 32 bytes (the 16 bsums, low | high bytes); xd follows the xm plane. All the
+// pre-passes of a batch run in one launch of `total` threads, pre-pass i taking threads [start, start + na_pad*nbk*73);
+// every start is a multiple of PREP_BLOCK, the launch's block size.
+constexpr int PREP_BLOCK = 256;
+struct PrepJob {
+    const uint8_t *act;
+    const int *arow;
+    uint8_t *xq, *xm;
+    uint64_t astride;
+    long start;
+    int na, na_pad, nbk, kind;
+};
+hipError_t prep_launch(const PrepJob *jobs, int njobs, const PrepJob &single, long total, hipStream_t s);
 hipError_t mm_launch(int type, int bm, int bn, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                      hipStream_t s);
+
+// The small-batch matrix-core form (es_hip_mq.hip): rows [r0, r1) against activations [t0, t0 + 16*wn) of na (at most
+// 64 per job), from pre-pass planes padded to na_pad activations. One workgroup per 64 rows.
+struct MqJob {
+    const uint8_t *W;     // row 0
+    const uint8_t *xq;    // pre-pass planes (xq, then xm and xd)
+    const uint8_t *xm;
+    float *y;
+    uint64_t ystride, row_bytes;
+    int r0, r1, cols, na, na_pad, t0;
+    int tile0, pad_;
+};
+hipError_t mq_launch(int type, int wn, const MqJob *jobs, int njobs, const MqJob &single, int grid, int order, hipStream_t s);
 
 // MoE glue (es_hip_moe.hip): SwiGLU + requantization of rows x ff gate|up pairs ([row][2 ff] floats) into Q8_K (q8k) or
 // Q8_0 blocks at ha + row * hstride; the weighted combine of the expert outputs ye[pair][n] into out[t][n].

@@ -42,22 +42,40 @@ __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
 // ---- pre-pass --------------------------------------------------------------------------------------------------------
 // One thread per dword of an activation's Q8_K row (nbk blocks of 73 dwords: d, 64 of qs, 8 of bsums pairs), so the
 // reads are coalesced; padding activations t >= na get zeros. Activation t is row arow[t] of act when arow is given.
-__global__ void act_prep_q8k(const uint8_t *__restrict__ act, const int *__restrict__ arow, uint64_t astride, int na,
-                             int na_pad, int nbk, uint8_t *__restrict__ xq, uint8_t *__restrict__ xm) {
-    const long per = (long)nbk * 73;
-    const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (id >= (long)na_pad * per) return;
-    const int t = (int)(id / per), k = (int)(id % per), b = k / 73, w = k % 73;
-    const uint32_t v = t < na ? ldg<uint32_t>(act + (size_t)(arow ? arow[t] : t) * astride + 4 * (size_t)k) : 0u;
-    const size_t bt = (size_t)b * na_pad + t;
+// kind 0 writes the pair sums (Q4_K sub-blocks), kind 1 the 16 bsums, both split as 128*hi + lo, one byte each.
+__global__ void act_prep_q8k(const PrepJob *__restrict__ jobs, int njobs, PrepJob single, long total) {
+    const long id0 = (long)blockIdx.x * blockDim.x, id = id0 + threadIdx.x;
+    if (id >= total) return;
+    int j = 0;
+    if (jobs) {   // last pre-pass with start <= id0 (starts are multiples of the block size: one search per block)
+        int lo = 0, hi = njobs - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (jobs[mid].start <= id0) lo = mid; else hi = mid - 1;
+        }
+        j = lo;
+    }
+    const PrepJob P = jobs ? jobs[j] : single;
+    const long per = (long)P.nbk * 73, lid = id - P.start;
+    if (lid < 0 || lid >= (long)P.na_pad * per) return;
+    const int t = (int)(lid / per), k = (int)(lid % per), b = k / 73, w = k % 73;
+    const uint32_t v = t < P.na ? ldg<uint32_t>(P.act + (size_t)(P.arow ? P.arow[t] : t) * P.astride + 4 * (size_t)k) : 0u;
+    const size_t bt = (size_t)b * P.na_pad + t;
+    uint8_t *xm = P.xm;
     if (w == 0) {
-        reinterpret_cast<uint32_t *>(xm + (size_t)nbk * na_pad * 16)[bt] = v;   // d
+        reinterpret_cast<uint32_t *>(xm + (size_t)P.nbk * P.na_pad * (P.kind ? 32 : 16))[bt] = v;   // d
     } else if (w <= 64) {
-        reinterpret_cast<uint32_t *>(xq + bt * 256)[w - 1] = v;                  // qs
+        reinterpret_cast<uint32_t *>(P.xq + bt * 256)[w - 1] = v;                                  // qs
+    } else if (P.kind == 0) {
+        const int jj = w - 65, p = (int16_t)(v & 0xffff) + (int16_t)(v >> 16);   // bsums[2jj] + bsums[2jj+1]
+        xm[bt * 16 + jj] = (uint8_t)(p & 127);
+        xm[bt * 16 + 8 + jj] = (uint8_t)((p >> 7) & 0xff);
     } else {
-        const int j = w - 65, p = (int16_t)(v & 0xffff) + (int16_t)(v >> 16);  // bsums[2j] + bsums[2j+1]
-        xm[bt * 16 + j] = (uint8_t)(p & 127);
-        xm[bt * 16 + 8 + j] = (uint8_t)((p >> 7) & 0xff);
+        const int g = 2 * (w - 65), p0 = (int16_t)(v & 0xffff), p1 = (int16_t)(v >> 16);   // bsums[g], bsums[g+1]
+        xm[bt * 32 + g] = (uint8_t)(p0 & 127);
+        xm[bt * 32 + g + 1] = (uint8_t)(p1 & 127);
+        xm[bt * 32 + 16 + g] = (uint8_t)((p0 >> 7) & 0xff);
+        xm[bt * 32 + 16 + g + 1] = (uint8_t)((p1 >> 7) & 0xff);
     }
 }
 
@@ -306,12 +324,11 @@ __global__ __launch_bounds__(512) void mm_q4k_kernel(const MmJob *__restrict__ j
 }
 
 // ---- launch glue -------------------------------------------------------------------------------------------------
-hipError_t mm_prep_launch(const uint8_t *act, const int *arow, uint64_t astride, int na, int na_pad, int nbk, uint8_t *xq,
-                          uint8_t *xm, hipStream_t s) {
-    const long total = (long)na_pad * nbk * 73;
-    const int threads = 256;
-    hipLaunchKernelGGL(act_prep_q8k, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0, s, act, arow, astride,
-                       na, na_pad, nbk, xq, xm);
+hipError_t prep_launch(const PrepJob *jobs, int njobs, const PrepJob &single, long total, hipStream_t s) {
+    if (total <= 0) return hipSuccess;
+    const int threads = PREP_BLOCK;
+    hipLaunchKernelGGL(act_prep_q8k, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0, s, jobs, njobs, single,
+                       total);
     return hipGetLastError();
 }
 

@@ -238,14 +238,21 @@ int launch_single(const Group &g, hipStream_t s) {
 }
 
 // ---- batches: decode-kernel launches plus, for large Q4_K batches, pre-passes and one matrix-core launch -------------
-std::atomic<int> g_mm_min{32};   // activations per product from which the matrix-core kernel is used (<= 0: never)
+std::atomic<int> g_mm_min{32};   // activations per Q4_K product from which the prefill kernel is used (<= 0: never)
+std::atomic<int> g_mq_min{8};    // activations per K-quant product from which the small-batch kernel is used (<= 0: never)
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
     const int *arow;
     uint64_t astride;
-    int na, na_pad, nbk;
+    int na, na_pad, nbk, kind;
     size_t xq_off, xm_off;
+};
+
+struct MqGroup {   // one small-batch matrix-core launch: products of one format and activation-tile count
+    int type, wn, grid = 0;
+    std::vector<esq::MqJob> jobs;
+    size_t off = 0;
 };
 
 struct MmGroup {   // one matrix-core launch: products sharing a workgroup tile shape
@@ -259,6 +266,10 @@ struct Batch {
     std::vector<Prep> preps;
     std::vector<esq::MmJob> mm;   // xq / xm hold workspace offsets until bind(); copied into mmg by plan_batch
     std::vector<MmGroup> mmg;
+    std::vector<MqGroup> mqg;
+    std::vector<esq::PrepJob> pj;   // the pre-passes as launched (filled by bind)
+    long prep_total = 0;
+    size_t prep_off = 0;
     size_t ws_bytes = 0;
     std::vector<size_t> mv_off;   // byte offsets of the job tables in the device image
     size_t table_bytes = 0;
@@ -281,6 +292,28 @@ bool mm_eligible(const Req &q) {
     return q.type == ES_HIP_Q4_K && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
 }
 
+bool mq_eligible(const Req &q) {
+    const int mn = g_mq_min.load();
+    return (q.type == ES_HIP_Q4_K || q.type == ES_HIP_Q2_K) && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
+}
+
+// the pre-pass of q's activations in layout (kind, na_pad), shared with earlier products that read the same ones
+const Prep &get_prep(Batch &bt, const Req &q, const FmtInfo &f, int kind, int na_pad) {
+    const int nbk = q.cols / 256;
+    const uint64_t astride = q.astride ? q.astride : (uint64_t)nbk * f.ab;
+    for (const Prep &p : bt.preps)
+        if (p.act == q.act && p.arow == q.arow && p.astride == astride && p.na == q.na && p.nbk == nbk && p.kind == kind &&
+            p.na_pad == na_pad)
+            return p;
+    Prep p{static_cast<const uint8_t *>(q.act), q.arow, astride, q.na, na_pad, nbk, kind, 0, 0};
+    p.xq_off = bt.ws_bytes;
+    bt.ws_bytes += align256((size_t)nbk * na_pad * 256);
+    p.xm_off = bt.ws_bytes;
+    bt.ws_bytes += align256((size_t)nbk * na_pad * (kind ? 36 : 20));   // meta, then the float scales
+    bt.preps.push_back(p);
+    return bt.preps.back();
+}
+
 int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
     bt = Batch();
     std::vector<Req> mv;
@@ -288,21 +321,39 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         FmtInfo f;
         if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
         if (int rc = check_req(q, f)) return rc;
-        if (!mm_eligible(q)) { mv.push_back(q); continue; }
-        const int nbk = q.cols / 256, na_pad = (q.na + esq::MM_NA_PAD - 1) / esq::MM_NA_PAD * esq::MM_NA_PAD;
-        const uint64_t astride = q.astride ? q.astride : (uint64_t)nbk * f.ab;
-        const Prep *pp = nullptr;
-        for (const Prep &p : bt.preps)
-            if (p.act == q.act && p.arow == q.arow && p.astride == astride && p.na == q.na && p.nbk == nbk) pp = &p;
-        if (!pp) {
-            Prep p{static_cast<const uint8_t *>(q.act), q.arow, astride, q.na, na_pad, nbk, 0, 0};
-            p.xq_off = bt.ws_bytes;
-            bt.ws_bytes += align256((size_t)nbk * na_pad * 256);
-            p.xm_off = bt.ws_bytes;
-            bt.ws_bytes += align256((size_t)nbk * na_pad * esq::MM_XM_BYTES);
-            bt.preps.push_back(p);
-            pp = &bt.preps.back();
+        const int nbk = q.cols / 256;
+        if (!mm_eligible(q)) {
+            if (!mq_eligible(q)) { mv.push_back(q); continue; }
+            // small batch: activation groups of at most 64, one launch per (format, 16-wide tiles per group)
+            const int na_pad = (q.na + 15) / 16 * 16;
+            const Prep &pp = get_prep(bt, q, f, q.type == ES_HIP_Q4_K ? 0 : 1, na_pad);
+            for (int t0 = 0; t0 < q.na; t0 += 64) {
+                const int wn = (std::min(64, q.na - t0) + 15) / 16;
+                MqGroup *g = nullptr;
+                for (MqGroup &x : bt.mqg)
+                    if (x.type == (int)q.type && x.wn == wn) g = &x;
+                if (!g) { bt.mqg.push_back(MqGroup{(int)q.type, wn}); g = &bt.mqg.back(); }
+                esq::MqJob j{};
+                j.W = static_cast<const uint8_t *>(q.W);
+                j.xq = reinterpret_cast<const uint8_t *>(pp.xq_off);
+                j.xm = reinterpret_cast<const uint8_t *>(pp.xm_off);
+                j.y = q.y;
+                j.ystride = q.ystride;
+                j.row_bytes = (uint64_t)nbk * f.bb;
+                j.r0 = q.r0;
+                j.r1 = q.r1;
+                j.cols = q.cols;
+                j.na = q.na;
+                j.na_pad = na_pad;
+                j.t0 = t0;
+                j.tile0 = g->grid;
+                g->grid += (q.r1 - q.r0 + 63) / 64;
+                g->jobs.push_back(j);
+            }
+            continue;
         }
+        const int na_pad = (q.na + esq::MM_NA_PAD - 1) / esq::MM_NA_PAD * esq::MM_NA_PAD;
+        const Prep *pp = &get_prep(bt, q, f, 0, na_pad);
         esq::MmJob j{};
         j.W = static_cast<const uint8_t *>(q.W);
         j.xq = reinterpret_cast<const uint8_t *>(pp->xq_off);
@@ -343,6 +394,12 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         g.off = off;
         off += align256(g.jobs.size() * sizeof(esq::MmJob));
     }
+    for (MqGroup &g : bt.mqg) {
+        g.off = off;
+        off += align256(g.jobs.size() * sizeof(esq::MqJob));
+    }
+    bt.prep_off = off;
+    off += align256(bt.preps.size() * sizeof(esq::PrepJob));
     bt.table_bytes = off;
     return ES_HIP_OK;
 }
@@ -354,9 +411,21 @@ void bind(Batch &bt, uint8_t *ws) {
             j.xq = ws + reinterpret_cast<uintptr_t>(j.xq);
             j.xm = ws + reinterpret_cast<uintptr_t>(j.xm);
         }
+    for (MqGroup &g : bt.mqg)
+        for (esq::MqJob &j : g.jobs) {
+            j.xq = ws + reinterpret_cast<uintptr_t>(j.xq);
+            j.xm = ws + reinterpret_cast<uintptr_t>(j.xm);
+        }
+    bt.pj.clear();
+    bt.prep_total = 0;
     for (Prep &p : bt.preps) {   // offsets become addresses too (kept as integers)
         p.xq_off = reinterpret_cast<uintptr_t>(ws) + p.xq_off;
         p.xm_off = reinterpret_cast<uintptr_t>(ws) + p.xm_off;
+        esq::PrepJob j{p.act, p.arow, reinterpret_cast<uint8_t *>(p.xq_off), reinterpret_cast<uint8_t *>(p.xm_off), p.astride,
+                       bt.prep_total, p.na, p.na_pad, p.nbk, p.kind};
+        bt.pj.push_back(j);
+        const long n = (long)p.na_pad * p.nbk * 73;
+        bt.prep_total += (n + esq::PREP_BLOCK - 1) / esq::PREP_BLOCK * esq::PREP_BLOCK;
     }
 }
 
@@ -365,6 +434,8 @@ std::vector<uint8_t> table_image(const Batch &bt) {
     for (size_t i = 0; i < bt.mv.size(); i++)
         memcpy(img.data() + bt.mv_off[i], bt.mv[i].jobs.data(), bt.mv[i].jobs.size() * sizeof(MvJob));
     for (const MmGroup &g : bt.mmg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MmJob));
+    for (const MqGroup &g : bt.mqg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MqJob));
+    if (!bt.pj.empty()) memcpy(img.data() + bt.prep_off, bt.pj.data(), bt.pj.size() * sizeof(esq::PrepJob));
     return img;
 }
 
@@ -372,10 +443,17 @@ std::vector<uint8_t> table_image(const Batch &bt) {
 // single jobs by value.
 int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t s) {
     hipError_t e;
-    for (const Prep &p : bt.preps)
-        if ((e = esq::mm_prep_launch(p.act, p.arow, p.astride, p.na, p.na_pad, p.nbk, reinterpret_cast<uint8_t *>(p.xq_off),
-                                     reinterpret_cast<uint8_t *>(p.xm_off), s)) != hipSuccess)
-            return hip_fail(e, "pre-pass launch");
+    if (tables && !bt.pj.empty()) {   // every pre-pass in one launch
+        e = esq::prep_launch(reinterpret_cast<const esq::PrepJob *>(tables + bt.prep_off), (int)bt.pj.size(), bt.pj[0],
+                             bt.prep_total, s);
+        if (e != hipSuccess) return hip_fail(e, "pre-pass launch");
+    } else {
+        for (esq::PrepJob j : bt.pj) {
+            const long n = (long)j.na_pad * j.nbk * 73;
+            j.start = 0;
+            if ((e = esq::prep_launch(nullptr, 1, j, n, s)) != hipSuccess) return hip_fail(e, "pre-pass launch");
+        }
+    }
     for (size_t i = 0; i < bt.mv.size(); i++) {
         const Group &g = bt.mv[i];
         const MvJob *dj = tables ? reinterpret_cast<const MvJob *>(tables + bt.mv_off[i]) : nullptr;
@@ -385,6 +463,11 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
         const esq::MmJob *dj = tables ? reinterpret_cast<const esq::MmJob *>(tables + g.off) : nullptr;
         if ((e = esq::mm_launch(ES_HIP_Q4_K, g.bm, g.bn, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
             return hip_fail(e, "matrix-core launch");
+    }
+    for (const MqGroup &g : bt.mqg) {
+        const esq::MqJob *dj = tables ? reinterpret_cast<const esq::MqJob *>(tables + g.off) : nullptr;
+        if ((e = esq::mq_launch(g.type, g.wn, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+            return hip_fail(e, "small-batch launch");
     }
     return ES_HIP_OK;
 }
@@ -435,7 +518,7 @@ void *reg_lookup(const void *h, size_t n) {
 int run_sync(const std::vector<Req> &reqs, hipStream_t s) {
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
-    if (bt.mv.empty() && bt.mm.empty()) return ES_HIP_OK;
+    if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty()) return ES_HIP_OK;
     hipError_t e = hipStreamSynchronize(s);   // the scratch may still be read by an earlier call's kernels
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     void *dev = nullptr;
@@ -523,7 +606,7 @@ int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int 
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (bt.mm.empty()) return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
+    if (bt.mm.empty() && bt.mqg.empty()) return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
     // matrix-core path: a stream-ordered workspace for the pre-pass, jobs passed by value
     void *ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, bt.ws_bytes, s);
@@ -618,6 +701,7 @@ void es_hip_plan_destroy(es_hip_plan *p) {
 }
 
 int es_hip_set_mfma_min_batch(int n) { return g_mm_min.exchange(n); }
+int es_hip_set_small_batch_min(int n) { return g_mq_min.exchange(n); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }

@@ -31,9 +31,21 @@ def inputs(orc, rows, cols, na, seed, gauss=False):
 @pytest.fixture
 def hipm(hip):
     prev = hip.set_mfma_min_batch(32)
+    prev_s = hip.set_small_batch_min(8)
     yield hip
     hip.set_mfma_min_batch(prev)
+    hip.set_small_batch_min(prev_s)
     hip.set_order(E.ORDER_X86_CONTRACT)
+
+
+def vector_path(hip, fn):
+    """fn() with both matrix-core kernels switched off"""
+    a, b = hip.set_mfma_min_batch(0), hip.set_small_batch_min(0)
+    try:
+        return fn()
+    finally:
+        hip.set_mfma_min_batch(a)
+        hip.set_small_batch_min(b)
 
 
 @pytest.mark.parametrize("rows,cols,na,gauss", [(8192, 2048, 40, True), (2048, 8192, 33, False), (768, 2048, 130, False),
@@ -53,9 +65,7 @@ def test_mfma_equals_vector_path(hipm, orc, rows, cols, na):
     """the full BASELINE prefill shape (T=512): matrix-core result == vector-kernel result, bit for bit"""
     W, acts = inputs(orc, rows, cols, na, 7 * rows + na)
     y_mm = hipm.matvec_multi(O.Q4_K, W, cols, rows, acts)
-    hipm.set_mfma_min_batch(0)
-    y_mv = hipm.matvec_multi(O.Q4_K, W, cols, rows, acts)
-    hipm.set_mfma_min_batch(32)
+    y_mv = vector_path(hipm, lambda: hipm.matvec_multi(O.Q4_K, W, cols, rows, acts))
     assert np.array_equal(bits(y_mm), bits(y_mv))
     ref = orc.matvec_multi(O.Q4_K, W, cols, rows, acts[:2])
     assert np.array_equal(bits(y_mm[:2]), bits(ref))
@@ -108,3 +118,41 @@ def test_mfma_in_job_batches_and_plans(hipm, orc):
         assert np.array_equal(bits(gu[:3, :ff]), bits(refs[0])), runner
         assert np.array_equal(bits(gu[:3, ff:]), bits(refs[1])), runner
         assert np.array_equal(bits(y[:3]), bits(refs[2])), runner
+
+
+# ---- the small-batch kernel (Q2_K and Q4_K with 8 .. 31 activations, and Q2_K with more) ---------------------------------
+def sb_inputs(orc, t, rows, cols, na, seed):
+    st = np.array([seed], np.uint64)
+    W = orc.mtest_blocks(t, st, rows, cols)
+    x = orc.mtest_acts(st, na * cols).reshape(na, cols)
+    return W, orc.quantize_act(t, x)
+
+
+@pytest.mark.parametrize("t,rows,cols,na", [(O.Q2_K, 1024, 2048, 16), (O.Q2_K, 2048, 1024, 17), (O.Q2_K, 300, 512, 64),
+                                            (O.Q2_K, 100, 256, 100), (O.Q4_K, 768, 2048, 8), (O.Q4_K, 2048, 768, 31),
+                                            (O.Q4_K, 77, 512, 20)])
+@pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
+def test_small_batch_vs_oracle(hipm, orc, t, rows, cols, na, mode):
+    hipm.set_order(mode[0])
+    W, acts = sb_inputs(orc, t, rows, cols, na, rows * 3 + na)
+    y = hipm.matvec_multi(t, W, cols, rows, acts)
+    ref = orc.matvec_multi(t, W, cols, rows, acts, mode[1], mode[2])
+    assert np.array_equal(bits(y), bits(ref))
+
+
+@pytest.mark.parametrize("t", [O.Q2_K, O.Q4_K])
+def test_small_batch_equals_vector_path_with_ranges(hipm, orc, t):
+    rows, cols, na, r0, r1 = 260, 1024, 24, 13, 251
+    W, acts = sb_inputs(orc, t, rows, cols, na, 5)
+    ab = acts.strides[0]
+    araw = np.zeros((na, ab + 36), np.uint8)
+    araw[:, :ab] = acts.view(np.uint8).reshape(na, ab)
+    ystride = rows + 7
+    out = []
+    for fn in (lambda f: f(), lambda f: vector_path(hipm, f)):
+        dW, dA = hipm.upload(W), hipm.upload(araw)
+        dY = hipm.upload(np.full(na * ystride, -555.0, np.float32))
+        fn(lambda: hipm.matvec_multi_dev(t, dW, cols, r0, r1, dA, araw.strides[0], na, dY, ystride))
+        out.append(hipm.download(dY, np.zeros((na, ystride), np.float32)))
+    assert np.array_equal(bits(out[0]), bits(out[1]))
+    assert np.all(out[0][:, :r0] == -555.0) and np.all(out[0][:, r1:] == -555.0)
