@@ -179,12 +179,16 @@ void   es_hip_moe_plan_destroy(es_hip_moe_plan *plan);
 int es_hip_block_ints_dev(uint32_t type, const void *W, int cols, int rows, const void *act, int32_t *dots, int32_t *aux,
                           void *stream);
 /* Kernel choice by batch size (results are identical either way; each returns the previous value):
- *   es_hip_set_mfma_min_batch: Q4_K products with at least n activations run on the prefill matrix-core kernel (default 32);
+ *   es_hip_set_mfma_min_batch: Q4_K products with at least n activations run on the matrix-core kernel that stages weights
+ *     and activations through LDS (default 8; batches up to 64 use 16-, 32- or 64-wide activation tiles);
  *   es_hip_set_small_batch_min: other Q2_K / Q4_K products with at least n activations run on the small-batch matrix-core
- *     kernel (default 8);
- * the rest go to the vector kernels. n <= 0 switches the kernel off. */
+ *     kernel that streams weights through registers (default 8);
+ * the rest go to the vector kernels. n <= 0 switches the kernel off (here and below). */
 int es_hip_set_mfma_min_batch(int n);
 int es_hip_set_small_batch_min(int n);
+/* Q4_0 / Q5_0 products with at least n activations run on the batched kernel (one lane per row and activation) instead of
+ * the vector kernel (default 2). */
+int es_hip_set_batched32_min(int n);
 /* The MoE SwiGLU alone on n device floats: h[i] = g[i] / (1 + expf(-g[i])) * u[i] as src/es_engine.c:913 computes it. */
 int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream);
 /* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`

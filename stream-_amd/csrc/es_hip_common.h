@@ -44,6 +44,19 @@ struct MvLaunch {
 };
 hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s);
 
+// Batched 32-wide form (Q4_0 / Q5_0, es_hip_mv.hip): rows [r0, r1) against activations [t0, t0 + ta) of na, one lane per
+// (row, activation); ta is a power of two <= 64 and a workgroup of 4 waves covers 4 * 64 / ta rows.
+struct MbJob {
+    const uint8_t *W;     // row 0
+    const uint8_t *act;   // activation 0's first block
+    const int *arow;      // optional gather: activation q is row arow[q] of act
+    float *y;
+    uint64_t astride, ystride, row_bytes;
+    int r0, r1, cols, na, t0, ta;
+    int tile0, pad_;
+};
+hipError_t mb32_launch(int type, const MbJob *jobs, int njobs, const MbJob &single, int grid, int order, hipStream_t s);
+
 // The batched (matrix-core) form: rows [r0, r1) against na activations that a pre-pass has re-laid out as
 // xq[nbk][na_pad][256] int8 values, then (at xm, in the same allocation) xm[nbk][na_pad][16 or 32] meta and
 // xd[nbk][na_pad] float scales right after the xm plane.
@@ -108,29 +121,42 @@ __device__ __forceinline__ uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t
     return __builtin_amdgcn_alignbyte(hi, lo, sel);
 }
 
-template <typename T> __device__ __forceinline__ T ldg(const void *p) { return *reinterpret_cast<const T *>(p); }
+// Device memory accesses through pointers that were loaded from job tables: the pointers are generic (flat) to the
+// compiler, which would emit flat loads (slower, and counted against the LDS counter too, so every wait drains both).
+// These helpers name the global address space explicitly.
+#define ESQ_GLOBAL __attribute__((address_space(1)))
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ T ldg(const void *p) {   // 8- and 16-byte types go through native vectors
+    if constexpr (sizeof(T) == 16) return __builtin_bit_cast(T, *(const ESQ_GLOBAL u32x4 *)p);
+    else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, *(const ESQ_GLOBAL u32x2 *)p);
+    else return *(const ESQ_GLOBAL T *)p;
+}
+template <typename T> __device__ __forceinline__ void stg(void *p, const T &v) {
+    if constexpr (sizeof(T) == 16) *(ESQ_GLOBAL u32x4 *)p = __builtin_bit_cast(u32x4, v);
+    else if constexpr (sizeof(T) == 8) *(ESQ_GLOBAL u32x2 *)p = __builtin_bit_cast(u32x2, v);
+    else *(ESQ_GLOBAL T *)p = v;
+}
 
 // Weight loads. Every weight byte is read once per pass, so ESQ_NT_WEIGHTS=1 marks them non-temporal (streamed past the
 // caches); 0 uses ordinary loads. Build-time choice, same results either way.
 #ifndef ESQ_NT_WEIGHTS
 #define ESQ_NT_WEIGHTS 0
 #endif
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 ldw4(const void *p) {
 #if ESQ_NT_WEIGHTS
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    const u32x4 v = __builtin_nontemporal_load((const ESQ_GLOBAL u32x4 *)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 #else
-    return *reinterpret_cast<const uint4 *>(p);
+    return ldg<uint4>(p);
 #endif
 }
 __device__ __forceinline__ uint2 ldw2(const void *p) {
 #if ESQ_NT_WEIGHTS
-    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+    const u32x2 v = __builtin_nontemporal_load((const ESQ_GLOBAL u32x2 *)p);
     return make_uint2(v.x, v.y);
 #else
-    return *reinterpret_cast<const uint2 *>(p);
+    return ldg<uint2>(p);
 #endif
 }
 

@@ -59,23 +59,23 @@ __global__ void act_prep_q8k(const PrepJob *__restrict__ jobs, int njobs, PrepJo
     const long per = (long)P.nbk * 73, lid = id - P.start;
     if (lid < 0 || lid >= (long)P.na_pad * per) return;
     const int t = (int)(lid / per), k = (int)(lid % per), b = k / 73, w = k % 73;
-    const uint32_t v = t < P.na ? ldg<uint32_t>(P.act + (size_t)(P.arow ? P.arow[t] : t) * P.astride + 4 * (size_t)k) : 0u;
+    const uint32_t v = t < P.na ? ldg<uint32_t>(P.act + (size_t)(P.arow ? ldg<int>(P.arow + t) : t) * P.astride + 4 * (size_t)k) : 0u;
     const size_t bt = (size_t)b * P.na_pad + t;
     uint8_t *xm = P.xm;
     if (w == 0) {
-        reinterpret_cast<uint32_t *>(xm + (size_t)P.nbk * P.na_pad * (P.kind ? 32 : 16))[bt] = v;   // d
+        stg<uint32_t>(xm + (size_t)P.nbk * P.na_pad * (P.kind ? 32 : 16) + bt * 4, v);   // d
     } else if (w <= 64) {
-        reinterpret_cast<uint32_t *>(P.xq + bt * 256)[w - 1] = v;                                  // qs
+        stg<uint32_t>(P.xq + bt * 256 + 4 * (w - 1), v);                                  // qs
     } else if (P.kind == 0) {
         const int jj = w - 65, p = (int16_t)(v & 0xffff) + (int16_t)(v >> 16);   // bsums[2jj] + bsums[2jj+1]
-        xm[bt * 16 + jj] = (uint8_t)(p & 127);
-        xm[bt * 16 + 8 + jj] = (uint8_t)((p >> 7) & 0xff);
+        stg<uint8_t>(xm + bt * 16 + jj, (uint8_t)(p & 127));
+        stg<uint8_t>(xm + bt * 16 + 8 + jj, (uint8_t)((p >> 7) & 0xff));
     } else {
         const int g = 2 * (w - 65), p0 = (int16_t)(v & 0xffff), p1 = (int16_t)(v >> 16);   // bsums[g], bsums[g+1]
-        xm[bt * 32 + g] = (uint8_t)(p0 & 127);
-        xm[bt * 32 + g + 1] = (uint8_t)(p1 & 127);
-        xm[bt * 32 + 16 + g] = (uint8_t)((p0 >> 7) & 0xff);
-        xm[bt * 32 + 16 + g + 1] = (uint8_t)((p1 >> 7) & 0xff);
+        stg<uint8_t>(xm + bt * 32 + g, (uint8_t)(p0 & 127));
+        stg<uint8_t>(xm + bt * 32 + g + 1, (uint8_t)(p1 & 127));
+        stg<uint8_t>(xm + bt * 32 + 16 + g, (uint8_t)((p0 >> 7) & 0xff));
+        stg<uint8_t>(xm + bt * 32 + 16 + g + 1, (uint8_t)((p1 >> 7) & 0xff));
     }
 }
 
@@ -314,11 +314,11 @@ __global__ __launch_bounds__(512) void mm_q4k_kernel(const MmJob *__restrict__ j
             const int r = row0 + wr + 16 * a + 4 * lg;   // this lane holds rows r .. r+3 of activation t
             float *yp = J.y + (size_t)t * J.ystride + r;
             if (r + 3 < J.r1 && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
-                *reinterpret_cast<float4 *>(yp) = make_float4(s[a][c][0], s[a][c][1], s[a][c][2], s[a][c][3]);
+                stg<float4>(yp, make_float4(s[a][c][0], s[a][c][1], s[a][c][2], s[a][c][3]));
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    if (r + i < J.r1) yp[i] = s[a][c][i];
+                    if (r + i < J.r1) stg<float>(yp + i, s[a][c][i]);
             }
         }
 }
@@ -341,11 +341,15 @@ static hipError_t mm_launch_cfg(const MmJob *jobs, int njobs, const MmJob &singl
     return hipGetLastError();
 }
 
-// workgroup tiles: 128 x 128 (8 waves of 16 rows x 128 activations) and 64 x 64 (4 x 2 waves of 16 rows x 32)
+// workgroup tiles: 128 x 128 (8 waves of 16 rows x 128 activations), 64 x 64 (4 x 2 waves of 16 rows x 32), and for small
+// batches 128 rows x 16, 32 or 64 activations
 hipError_t mm_launch(int type, int bm, int bn, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                      hipStream_t s) {
     if (type != ES_HIP_Q4_K) return hipErrorInvalidValue;
     if (bm == 128 && bn == 128) return mm_launch_cfg<8, 1, 8>(jobs, njobs, single, grid, order, s);
+    if (bm == 128 && bn == 64) return mm_launch_cfg<8, 1, 4>(jobs, njobs, single, grid, order, s);
+    if (bm == 128 && bn == 32) return mm_launch_cfg<8, 1, 2>(jobs, njobs, single, grid, order, s);
+    if (bm == 128 && bn == 16) return mm_launch_cfg<8, 1, 1>(jobs, njobs, single, grid, order, s);
     if (bm == 64 && bn == 64) return mm_launch_cfg<4, 1, 2>(jobs, njobs, single, grid, order, s);
     return hipErrorInvalidValue;
 }

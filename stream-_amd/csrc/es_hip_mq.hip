@@ -185,26 +185,25 @@ __global__ __launch_bounds__(256, 2) void mq_kernel(const MqJob *__restrict__ jo
             B.td[c] = ldg<float>(xd_plane + t * 4);
         }
     };
-    // Weights run DEPTH superblocks ahead (a register ring, indexed by compile-time slots: the loop is unrolled by the ring
-    // size); for up to two activation tiles the activation side of superblock b + 1 is loaded while b is computed.
-    // Q4_K's ring is the larger per superblock; more activation tiles leave fewer registers for it
-    constexpr int DEPTH = (F == ES_HIP_Q4_K ? 2 : 3) - (WN > 2 ? 1 : 0), RING = DEPTH + 1;
+    // Weights run DEPTH superblocks ahead in a register ring that shifts by one each step; for up to two activation tiles
+    // the activation side of superblock b + 1 is loaded while b is computed. Every load is unconditional (past the last
+    // superblock the last one is read again), so the compiler's memory-counter waits count exactly and the loads in
+    // flight are never drained early.
+    constexpr int DEPTH = (F == ES_HIP_Q4_K ? 2 : 3) - (WN > 2 ? 1 : 0);
     constexpr bool PF = WN <= (F == ES_HIP_Q4_K ? 1 : 2);
-    typename M::Raw raw[RING];
+    typename M::Raw ring[DEPTH];
 #pragma unroll
-    for (int d = 0; d < DEPTH; d++)
-        if (d < nbk) M::load(wrow + (size_t)d * M::BB, lg, raw[d]);
+    for (int d = 0; d < DEPTH; d++) M::load(wrow + (size_t)min(d, nbk - 1) * M::BB, lg, ring[d]);
     Bset cur, nxt;
     load_b(0, cur);
-    auto step = [&](int b, auto slot) {
-        constexpr int SL = decltype(slot)::value;
+    for (int b = 0; b < nbk; b++) {
         typename M::A a;
-        M::build(raw[SL], lg, a);
-        const uint32_t hdd = M::dd(raw[SL]);
-        if (b + DEPTH < nbk) M::load(wrow + (size_t)(b + DEPTH) * M::BB, lg, raw[(SL + DEPTH) % RING]);
-        if constexpr (PF) {
-            if (b + 1 < nbk) load_b(b + 1, nxt);
-        }
+        M::build(ring[0], lg, a);
+        const uint32_t hdd = M::dd(ring[0]);
+        if constexpr (PF) load_b(min(b + 1, nbk - 1), nxt);   // issued in the order they are needed
+#pragma unroll
+        for (int d = 0; d + 1 < DEPTH; d++) ring[d] = ring[d + 1];
+        M::load(wrow + (size_t)min(b + DEPTH, nbk - 1) * M::BB, lg, ring[DEPTH - 1]);
         uint32_t dd[4];   // d | dmin of output rows 4lg + i, held by lanes 4lg + i (the A layout puts row r in lane r)
 #pragma unroll
         for (int i = 0; i < 4; i++) dd[i] = __shfl(hdd, 4 * lg + i);
@@ -216,20 +215,8 @@ __global__ __launch_bounds__(256, 2) void mq_kernel(const MqJob *__restrict__ jo
 #pragma unroll
             for (int i = 0; i < 4; i++) s[c][i] = M::template chain<CONTRACT>(s[c][i], acc, i, dd[i], cur.td[c]);
         }
-        if (b + 1 < nbk) {
-            if constexpr (PF) cur = nxt;
-            else load_b(b + 1, cur);
-        }
-    };
-    for (int b = 0; b < nbk; b += RING) {
-        step(b, IC<0>{});
-        if (b + 1 < nbk) step(b + 1, IC<1>{});
-        if constexpr (RING > 2) {
-            if (b + 2 < nbk) step(b + 2, IC<2 % RING>{});
-        }
-        if constexpr (RING > 3) {
-            if (b + 3 < nbk) step(b + 3, IC<3 % RING>{});
-        }
+        if constexpr (PF) cur = nxt;
+        else load_b(min(b + 1, nbk - 1), cur);
     }
 
     // outputs: lane holds rows row0 + 4lg + i of activation t0 + 16c + lr
@@ -240,11 +227,11 @@ __global__ __launch_bounds__(256, 2) void mq_kernel(const MqJob *__restrict__ jo
         const int r = row0 + 4 * lg;
         float *yp = J.y + (size_t)t * J.ystride + r;
         if (r + 3 < J.r1 && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
-            *reinterpret_cast<float4 *>(yp) = make_float4(s[c][0], s[c][1], s[c][2], s[c][3]);
+            stg<float4>(yp, make_float4(s[c][0], s[c][1], s[c][2], s[c][3]));
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if (r + i < J.r1) yp[i] = s[c][i];
+                if (r + i < J.r1) stg<float>(yp + i, s[c][i]);
         }
     }
 }

@@ -58,9 +58,8 @@ template <> struct Lane<ES_HIP_Q4_K> {
         const uint4 v0 = ldg<uint4>(a + 4 + 64 * c + 16 * h), v1 = ldg<uint4>(a + 4 + 64 * c + 32 + 16 * h);
         x.lo[0] = v0.x; x.lo[1] = v0.y; x.lo[2] = v0.z; x.lo[3] = v0.w;
         x.hi[0] = v1.x; x.hi[1] = v1.y; x.hi[2] = v1.z; x.hi[3] = v1.w;
-        const int16_t *bs = reinterpret_cast<const int16_t *>(a + 260);
-        x.bs0 = bs[4 * c + h];
-        x.bs1 = bs[4 * c + 2 + h];
+        x.bs0 = ldg<int16_t>(a + 260 + 2 * (4 * c + h));
+        x.bs1 = ldg<int16_t>(a + 260 + 2 * (4 * c + 2 + h));
     }
     static __device__ __forceinline__ void zero_act(Act &x) {
         for (int i = 0; i < 4; i++) x.lo[i] = x.hi[i] = 0;
@@ -120,9 +119,8 @@ template <> struct Lane<ES_HIP_Q6_K> {
         const uint4 v0 = ldg<uint4>(a + 4 + 16 * g1), v1 = ldg<uint4>(a + 4 + 16 * g2);
         x.y1[0] = v0.x; x.y1[1] = v0.y; x.y1[2] = v0.z; x.y1[3] = v0.w;
         x.y2[0] = v1.x; x.y2[1] = v1.y; x.y2[2] = v1.z; x.y2[3] = v1.w;
-        const int16_t *bs = reinterpret_cast<const int16_t *>(a + 260);
-        x.bs1 = bs[g1];
-        x.bs2 = bs[g2];
+        x.bs1 = ldg<int16_t>(a + 260 + 2 * g1);
+        x.bs2 = ldg<int16_t>(a + 260 + 2 * g2);
     }
     static __device__ __forceinline__ void zero_act(Act &x) {
         for (int i = 0; i < 4; i++) x.y1[i] = x.y2[i] = 0;
@@ -133,18 +131,17 @@ template <> struct Lane<ES_HIP_Q6_K> {
         const int h = k >> 2, j = (k >> 1) & 1, p = k & 1;
         const uintptr_t al = reinterpret_cast<uintptr_t>(blk + 64 * h + 32 * p + 16 * j);
         const uintptr_t ah = reinterpret_cast<uintptr_t>(blk + 128 + 32 * h + 16 * j);
-        const uint32_t *bl = reinterpret_cast<const uint32_t *>(al & ~static_cast<uintptr_t>(3));
-        const uint32_t *bh = reinterpret_cast<const uint32_t *>(ah & ~static_cast<uintptr_t>(3));
+        const uint8_t *bl = reinterpret_cast<const uint8_t *>(al & ~static_cast<uintptr_t>(3));
+        const uint8_t *bh = reinterpret_cast<const uint8_t *>(ah & ~static_cast<uintptr_t>(3));
         r.sel = static_cast<uint32_t>(al & 3);   // same for both fields (offsets differ by multiples of 16)
         r.lv = ldw4(bl);
-        r.l4 = bl[4];
+        r.l4 = ldg<uint32_t>(bl + 16);
         r.hv = ldw4(bh);
-        r.h4 = bh[4];
-        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192);
+        r.h4 = ldg<uint32_t>(bh + 16);
         const int g1 = g1_of(k);
-        r.s1 = sc[g1];
-        r.s2 = sc[g1 + 4];
-        r.d16 = *reinterpret_cast<const uint16_t *>(blk + 208);
+        r.s1 = ldg<int8_t>(blk + 192 + g1);
+        r.s2 = ldg<int8_t>(blk + 192 + g1 + 4);
+        r.d16 = ldg<uint16_t>(blk + 208);
     }
     static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
         const uint32_t ql[4] = {alignbyte(r.lv.y, r.lv.x, r.sel), alignbyte(r.lv.z, r.lv.y, r.sel),
@@ -184,13 +181,12 @@ template <> struct Lane<ES_HIP_Q2_K> {
     static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
         const int h = k >> 2, part = (k >> 1) & 1, sub = k & 1;
         x.d = ldg<float>(a);
-        const int16_t *bs = reinterpret_cast<const int16_t *>(a + 260);
         for (int s = 0; s < 4; s++) {
             const int g = 8 * h + 2 * s + part;
             const uint2 v = ldg<uint2>(a + 4 + 16 * g + 8 * sub);
             x.y[s][0] = v.x;
             x.y[s][1] = v.y;
-            x.bs[s] = sub == 0 ? bs[g] : 0;
+            x.bs[s] = sub == 0 ? ldg<int16_t>(a + 260 + 2 * g) : 0;
         }
     }
     static __device__ __forceinline__ void zero_act(Act &x) {
@@ -264,10 +260,10 @@ template <int F> struct Lane32 {
         r.v = ldw4(blk + r.par);
         if constexpr (F == ES_HIP_Q4_0) {   // d f16 @0, qs[16] @2
             r.w4 = 0;
-            r.u = *reinterpret_cast<const uint16_t *>(r.par ? blk : blk + 16);
+            r.u = ldg<uint16_t>(r.par ? blk : blk + 16);
         } else {                            // d f16 @0, qh u32 @2, qs[16] @6
             r.w4 = ldg<uint32_t>(blk + r.par + 16);
-            r.u = *reinterpret_cast<const uint16_t *>(r.par ? blk : blk + 20);
+            r.u = ldg<uint16_t>(r.par ? blk : blk + 20);
         }
     }
     static __device__ __forceinline__ void unpack(const Raw &r, int, Wt &w) {
@@ -317,7 +313,7 @@ template <int F> constexpr bool is32() { return F == ES_HIP_Q4_0 || F == ES_HIP_
 // ---------------------------------------------------------------------------------------------------------------------
 // The kernel
 
-__device__ __forceinline__ int find_job(const MvJob *jobs, int njobs, int bid) {
+template <typename JobT> __device__ __forceinline__ int find_job(const JobT *jobs, int njobs, int bid) {
     int lo = 0, hi = njobs - 1;   // last job with tile0 <= bid
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -373,7 +369,7 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if (live && t < nt) {
-                const int q = J.arow ? J.arow[t0 + t] : t0 + t;
+                const int q = J.arow ? ldg<int>(J.arow + t0 + t) : t0 + t;
                 L::load_act(J.act + (size_t)q * J.astride + (size_t)b * AB, k, act[t]);
             }
             else L::zero_act(act[t]);
@@ -425,8 +421,8 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
                             if (J.ints && t0 == 0) {
                                 int a = 0;
                                 for (int i = 0; i < 8; i++) a += v[0].lane[i];
-                                J.ints[(size_t)row * nbk + b] = a;
-                                J.ints_aux[(size_t)row * nbk + b] = 0;
+                                stg<int32_t>(J.ints + (size_t)row * nbk + b, a);
+                                stg<int32_t>(J.ints_aux + (size_t)row * nbk + b, 0);
                             }
                         } else {
 #pragma unroll
@@ -437,8 +433,8 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
                                 e[t * CW + 1] = tm.b;
                             }
                             if (J.ints && t0 == 0) {
-                                J.ints[(size_t)row * nbk + b] = v[0].dot;
-                                J.ints_aux[(size_t)row * nbk + b] = v[0].aux;
+                                stg<int32_t>(J.ints + (size_t)row * nbk + b, v[0].dot);
+                                stg<int32_t>(J.ints_aux + (size_t)row * nbk + b, v[0].aux);
                             }
                         }
                     }
@@ -475,7 +471,7 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
                     s = s + __shfl_xor(s, 2);
                     s = s + __shfl_xor(s, 1);
                 }
-                if (i == 0 && t < nt) J.y[(size_t)(t0 + t) * J.ystride + ra + rl] = s;
+                if (i == 0 && t < nt) stg<float>(J.y + (size_t)(t0 + t) * J.ystride + ra + rl, s);
             }
             __syncthreads();
         }
@@ -524,6 +520,71 @@ hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJo
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(fn, dim3(L.grid), dim3(WAVE * L.waves), L.lds, s, jobs, njobs, single, order);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// Batched 32-wide formats (Q4_0 / Q5_0 against 2..64 activations): one lane per (row, activation) runs that output's whole
+// chain over the row's blocks in registers, so there are no LDS terms and no second phase. The lanes of a wave take
+// ta consecutive activations (a power of two) of 64 / ta consecutive rows; lanes of one row read the same weight block
+// (one memory transaction), the activation blocks come from L2. The next block is loaded while one is computed.
+// x86 order: the eight AVX2 lane sums of a block go into eight fused chains acc_i = fma(lane_i, d*yd, acc_i), summed at
+// the end as ((0+4)+(2+6))+((1+5)+(3+7)) (src/es_quant.c:1185-1187, 1252-1323); scalar order: s = s + (d*yd)*sum
+// (src/es_quant.c:1013-1055).
+template <int F>
+__global__ __launch_bounds__(256) void mb32_kernel(const MbJob *__restrict__ jobs, int njobs, MbJob single, int order) {
+    using L = Lane32<F>;
+    constexpr int BB = Fmt<F>::BB, AB = Fmt<F>::AB;
+    MbJob J;
+    if (jobs) J = jobs[find_job(jobs, njobs, blockIdx.x)];
+    else J = single;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rows_per_wave = 64 / J.ta;
+    const int row = J.r0 + ((blockIdx.x - J.tile0) * 4 + wave) * rows_per_wave + lane / J.ta;
+    const int t = J.t0 + lane % J.ta;
+    const bool live = row < J.r1 && t < J.na;
+    const int nbk = J.cols / 32;
+    const uint8_t *wrow = J.W + (size_t)min(row, J.r1 - 1) * J.row_bytes;
+    const int tq = min(t, J.na - 1);
+    const uint8_t *arow = J.act + (size_t)(J.arow ? ldg<int>(J.arow + tq) : tq) * J.astride;
+    const bool x86 = order != ES_HIP_ORDER_SCALAR;
+
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, s = 0.0f;
+    typename L::Raw raw;
+    typename L::Act x;
+    L::load_raw(wrow, 0, raw);
+    L::load_act(arow, 0, x);
+    for (int b = 0; b < nbk; b++) {
+        typename L::Wt w;
+        L::unpack(raw, 0, w);
+        const typename L::Act xc = x;
+        if (b + 1 < nbk) {   // the next block's bytes in flight
+            L::load_raw(wrow + (size_t)(b + 1) * BB, 0, raw);
+            L::load_act(arow + (size_t)(b + 1) * AB, 0, x);
+        }
+        const typename L::Ints v = L::ints(w, xc);
+        const float dy = w.d * xc.d;
+        if (x86) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i] = __builtin_fmaf(static_cast<float>(v.lane[i]), dy, acc[i]);
+        } else {
+            int a = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) a += v.lane[i];
+            s = s + dy * static_cast<float>(a);
+        }
+    }
+    if (x86) s = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+    if (live) stg<float>(J.y + (size_t)t * J.ystride + row, s);
+}
+
+hipError_t mb32_launch(int type, const MbJob *jobs, int njobs, const MbJob &single, int grid, int order, hipStream_t s) {
+    if (type == ES_HIP_Q4_0)
+        hipLaunchKernelGGL(mb32_kernel<ES_HIP_Q4_0>, dim3(grid), dim3(256), 0, s, jobs, njobs, single, order);
+    else if (type == ES_HIP_Q5_0)
+        hipLaunchKernelGGL(mb32_kernel<ES_HIP_Q5_0>, dim3(grid), dim3(256), 0, s, jobs, njobs, single, order);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

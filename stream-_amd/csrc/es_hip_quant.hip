@@ -238,8 +238,9 @@ int launch_single(const Group &g, hipStream_t s) {
 }
 
 // ---- batches: decode-kernel launches plus, for large Q4_K batches, pre-passes and one matrix-core launch -------------
-std::atomic<int> g_mm_min{32};   // activations per Q4_K product from which the prefill kernel is used (<= 0: never)
+std::atomic<int> g_mm_min{8};    // activations per Q4_K product from which the prefill kernel is used (<= 0: never)
 std::atomic<int> g_mq_min{8};    // activations per K-quant product from which the small-batch kernel is used (<= 0: never)
+std::atomic<int> g_mb_min{2};    // activations per Q4_0/Q5_0 product from which the batched kernel is used (<= 0: never)
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
@@ -247,6 +248,12 @@ struct Prep {   // one activation pre-pass (shared by products that read the sam
     uint64_t astride;
     int na, na_pad, nbk, kind;
     size_t xq_off, xm_off;
+};
+
+struct MbGroup {   // one batched 32-wide launch: products of one format
+    int type, grid = 0;
+    std::vector<esq::MbJob> jobs;
+    size_t off = 0;
 };
 
 struct MqGroup {   // one small-batch matrix-core launch: products of one format and activation-tile count
@@ -267,6 +274,7 @@ struct Batch {
     std::vector<esq::MmJob> mm;   // xq / xm hold workspace offsets until bind(); copied into mmg by plan_batch
     std::vector<MmGroup> mmg;
     std::vector<MqGroup> mqg;
+    std::vector<MbGroup> mbg;
     std::vector<esq::PrepJob> pj;   // the pre-passes as launched (filled by bind)
     long prep_total = 0;
     size_t prep_off = 0;
@@ -277,6 +285,11 @@ struct Batch {
 
 // Workgroup tile of a product: the largest (best operand reuse) that still gives every CU a workgroup.
 void mm_tile(const esq::MmJob &j, int &bm, int &bn) {
+    if (j.na_pad < 128) {   // small batches: 128 rows x all the activations (16, 32 or 64)
+        bm = 128;
+        bn = j.na_pad;
+        return;
+    }
     static const int cand[2] = {128, 64};   // square tiles: 128 x 128, 64 x 64
     const int rows = j.r1 - j.r0;
     for (int c : cand) {
@@ -290,6 +303,11 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 bool mm_eligible(const Req &q) {
     const int mn = g_mm_min.load();
     return q.type == ES_HIP_Q4_K && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
+}
+
+bool mb_eligible(const Req &q) {
+    const int mn = g_mb_min.load();
+    return (q.type == ES_HIP_Q4_0 || q.type == ES_HIP_Q5_0) && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
 }
 
 bool mq_eligible(const Req &q) {
@@ -321,6 +339,36 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         FmtInfo f;
         if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
         if (int rc = check_req(q, f)) return rc;
+        if (mb_eligible(q)) {   // batched 32-wide: activation groups of at most 64
+            MbGroup *g = nullptr;
+            for (MbGroup &x : bt.mbg)
+                if (x.type == (int)q.type) g = &x;
+            if (!g) { bt.mbg.push_back(MbGroup{(int)q.type}); g = &bt.mbg.back(); }
+            const int nbk32 = q.cols / 32;
+            for (int t0 = 0; t0 < q.na; t0 += 64) {
+                int ta = 1;
+                while (ta < std::min(64, q.na - t0)) ta <<= 1;
+                esq::MbJob j{};
+                j.W = static_cast<const uint8_t *>(q.W);
+                j.act = static_cast<const uint8_t *>(q.act);
+                j.arow = q.arow;
+                j.y = q.y;
+                j.astride = q.astride ? q.astride : (uint64_t)nbk32 * f.ab;
+                j.ystride = q.ystride;
+                j.row_bytes = (uint64_t)nbk32 * f.bb;
+                j.r0 = q.r0;
+                j.r1 = q.r1;
+                j.cols = q.cols;
+                j.na = q.na;
+                j.t0 = t0;
+                j.ta = ta;
+                j.tile0 = g->grid;
+                const int rows_per_wg = 4 * (64 / ta);
+                g->grid += (q.r1 - q.r0 + rows_per_wg - 1) / rows_per_wg;
+                g->jobs.push_back(j);
+            }
+            continue;
+        }
         const int nbk = q.cols / 256;
         if (!mm_eligible(q)) {
             if (!mq_eligible(q)) { mv.push_back(q); continue; }
@@ -352,7 +400,8 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             }
             continue;
         }
-        const int na_pad = (q.na + esq::MM_NA_PAD - 1) / esq::MM_NA_PAD * esq::MM_NA_PAD;
+        const int na_pad = q.na <= 16 ? 16 : q.na <= 32 ? 32 : q.na <= 64 ? 64
+                                        : (q.na + esq::MM_NA_PAD - 1) / esq::MM_NA_PAD * esq::MM_NA_PAD;
         const Prep *pp = &get_prep(bt, q, f, 0, na_pad);
         esq::MmJob j{};
         j.W = static_cast<const uint8_t *>(q.W);
@@ -398,6 +447,10 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         g.off = off;
         off += align256(g.jobs.size() * sizeof(esq::MqJob));
     }
+    for (MbGroup &g : bt.mbg) {
+        g.off = off;
+        off += align256(g.jobs.size() * sizeof(esq::MbJob));
+    }
     bt.prep_off = off;
     off += align256(bt.preps.size() * sizeof(esq::PrepJob));
     bt.table_bytes = off;
@@ -435,6 +488,7 @@ std::vector<uint8_t> table_image(const Batch &bt) {
         memcpy(img.data() + bt.mv_off[i], bt.mv[i].jobs.data(), bt.mv[i].jobs.size() * sizeof(MvJob));
     for (const MmGroup &g : bt.mmg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MmJob));
     for (const MqGroup &g : bt.mqg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MqJob));
+    for (const MbGroup &g : bt.mbg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MbJob));
     if (!bt.pj.empty()) memcpy(img.data() + bt.prep_off, bt.pj.data(), bt.pj.size() * sizeof(esq::PrepJob));
     return img;
 }
@@ -463,6 +517,11 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
         const esq::MmJob *dj = tables ? reinterpret_cast<const esq::MmJob *>(tables + g.off) : nullptr;
         if ((e = esq::mm_launch(ES_HIP_Q4_K, g.bm, g.bn, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
             return hip_fail(e, "matrix-core launch");
+    }
+    for (const MbGroup &g : bt.mbg) {
+        const esq::MbJob *dj = tables ? reinterpret_cast<const esq::MbJob *>(tables + g.off) : nullptr;
+        if ((e = esq::mb32_launch(g.type, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+            return hip_fail(e, "batched launch");
     }
     for (const MqGroup &g : bt.mqg) {
         const esq::MqJob *dj = tables ? reinterpret_cast<const esq::MqJob *>(tables + g.off) : nullptr;
@@ -518,7 +577,7 @@ void *reg_lookup(const void *h, size_t n) {
 int run_sync(const std::vector<Req> &reqs, hipStream_t s) {
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
-    if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty()) return ES_HIP_OK;
+    if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty()) return ES_HIP_OK;
     hipError_t e = hipStreamSynchronize(s);   // the scratch may still be read by an earlier call's kernels
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     void *dev = nullptr;
@@ -606,14 +665,20 @@ int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int 
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (bt.mm.empty() && bt.mqg.empty()) return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
-    // matrix-core path: a stream-ordered workspace for the pre-pass, jobs passed by value
-    void *ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, bt.ws_bytes, s);
-    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (pre-pass workspace)");
-    bind(bt, static_cast<uint8_t *>(ws));
-    const int rc = launch_batch(bt, nullptr, g_order.load(), s);
-    e = hipFreeAsync(ws, s);
+    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty()) return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
+    // other kernels (possibly several jobs per launch, pre-passes): a stream-ordered allocation for the job tables and the
+    // pre-pass workspace. The tables are copied from pageable memory, which the copy has consumed when it returns.
+    void *dev = nullptr;
+    const size_t ws_at = align256(bt.table_bytes);
+    hipError_t e = hipMallocAsync(&dev, std::max<size_t>(ws_at + bt.ws_bytes, 256), s);
+    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (tables and workspace)");
+    bind(bt, static_cast<uint8_t *>(dev) + ws_at);
+    const std::vector<uint8_t> img = table_image(bt);
+    int rc = ES_HIP_OK;
+    if (!img.empty() && (e = hipMemcpyAsync(dev, img.data(), img.size(), hipMemcpyHostToDevice, s)) != hipSuccess)
+        rc = hip_fail(e, "job table upload");
+    if (!rc) rc = launch_batch(bt, static_cast<const uint8_t *>(dev), g_order.load(), s);
+    e = hipFreeAsync(dev, s);
     if (rc) return rc;
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipFreeAsync");
 }
@@ -702,6 +767,7 @@ void es_hip_plan_destroy(es_hip_plan *p) {
 
 int es_hip_set_mfma_min_batch(int n) { return g_mm_min.exchange(n); }
 int es_hip_set_small_batch_min(int n) { return g_mq_min.exchange(n); }
+int es_hip_set_batched32_min(int n) { return g_mb_min.exchange(n); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }

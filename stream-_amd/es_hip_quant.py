@@ -117,6 +117,7 @@ class Lib:
             ("es_hip_block_ints_dev", i, [u32, vp, i, i, vp, vp, vp, vp]),
             ("es_hip_run_jobs_host", i, [vp, i]),
             ("es_hip_set_mfma_min_batch", i, [i]), ("es_hip_set_small_batch_min", i, [i]),
+            ("es_hip_set_batched32_min", i, [i]),
             ("es_hip_moe_ffn", i, [vp, i, vp, vp, vp, i, vp, sz, vp, sz, vp]),
             ("es_hip_moe_plan_create", vp, [vp, i, vp, vp, vp, i, vp, sz, vp, sz]),
             ("es_hip_moe_plan_run", i, [vp, vp]), ("es_hip_moe_plan_destroy", None, [vp]),
@@ -147,6 +148,9 @@ class Lib:
 
     def set_small_batch_min(self, n: int) -> int:
         return self._L.es_hip_set_small_batch_min(n)
+
+    def set_batched32_min(self, n: int) -> int:
+        return self._L.es_hip_set_batched32_min(n)
 
     def _check(self, rc):
         if rc is not None and rc < 0:

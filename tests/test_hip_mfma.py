@@ -28,9 +28,10 @@ def inputs(orc, rows, cols, na, seed, gauss=False):
     return W, orc.quantize_act(O.Q4_K, x)
 
 
-@pytest.fixture
-def hipm(hip):
-    prev = hip.set_mfma_min_batch(32)
+@pytest.fixture(params=[8, 32], ids=["lds", "regs"])
+def hipm(hip, request):
+    """Q4_K batches of 8..31 on the LDS-staged kernel (threshold 8) or on the register-streaming one (threshold 32)"""
+    prev = hip.set_mfma_min_batch(request.param)
     prev_s = hip.set_small_batch_min(8)
     yield hip
     hip.set_mfma_min_batch(prev)
