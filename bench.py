@@ -14,7 +14,7 @@ configs 4 and 5 (weight GB/s over the experts actually routed, plus config 5's a
 Inputs are synthetic: es_mtest-style random weight blocks with sane fp16 scales (tools/es_mtest.c:9-35) and N(0,1)
 activations quantized to the reference's Q8 blocks in numpy. Kernel speed does not depend on the values.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only WORKLOAD]
 """
 import argparse
 import json
@@ -218,6 +218,39 @@ def cpu_baseline(t, rows, cols, rng, seconds):
             "by_threads_gbs": {str(k): round(v, 2) for k, v in points.items()}, "host_cpus_visible": avail}
 
 
+Q4K_FFN = [(E.Q4_K, 8192, 2048), (E.Q4_K, 8192, 2048), (E.Q4_K, 2048, 8192)]
+
+
+def only(lib, rng, name, K, Wm):
+    """one workload of the bench, alone: the command profiler summaries are taken from"""
+    if name == "copy":   # a plain device copy of known size, the reference for HBM byte counters
+        n = 1 << 30
+        a, b = lib.alloc(n), lib.alloc(n)
+        lib.memset(a, 1, n)
+        for _ in range(Wm + K):
+            lib.copy_d2d(b, a, n)
+        lib.synchronize()
+        a.close()
+        b.close()
+        return {"workload": "copy", "bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": Wm + K}
+    if name in ("config4", "config5"):
+        w = (MoeWorkload(lib, rng, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8) if name == "config4" else
+             MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
+                         attn=((4096, 2048), (512, 2048), (512, 2048))))
+        ms = w.time(Wm, K)
+        out = {"workload": name, "ms_per_layer": round(ms, 4), "weight_bytes_per_layer": w.weight_bytes // w.copies}
+        w.close()
+        return out
+    mats, na, copies = {"decode": (Q4K_FFN, 1, 38), "prefill": (Q4K_FFN, 512, 1), "config1": ([(E.Q4_0, 4864, 896)], 1, 410),
+                        "config3b1": ([(E.Q6_K, 151936, 1024)], 1, 8), "config3b64": ([(E.Q6_K, 151936, 1024)], 64, 8)}[name]
+    w = Workload(lib, rng, mats, na, copies)
+    _, ev = w.time(Wm, K)
+    out = {"workload": name, "ms_per_launch": round(ev, 4), "weight_bytes_per_launch": w.weight_bytes,
+           "gbs": round(w.weight_bytes / (ev * 1e-3) / 1e9, 1), "tops": round(w.ops / (ev * 1e-3) / 1e12, 2)}
+    w.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,6 +258,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=2.0)
+    ap.add_argument("--only", choices=["decode", "prefill", "config1", "config3b1", "config3b64", "config4", "config5", "copy"],
+                    help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the path shards by output rows or by "
@@ -236,17 +271,20 @@ def main():
         raise SystemExit("no usable gfx950 device: " + lib.last_error())
     rng = np.random.default_rng(20260101)
     K, Wm = args.steps, args.warmup
+    if args.only:
+        print(json.dumps(only(lib, rng, args.only, K, Wm)), flush=True)
+        return
 
     # ---- headline: config 2 decode, Q4_K, T=1, 1.08 GB rotating set
     copies = 38
-    dec = Workload(lib, rng, [(E.Q4_K, 8192, 2048), (E.Q4_K, 8192, 2048), (E.Q4_K, 2048, 8192)], 1, copies)
+    dec = Workload(lib, rng, Q4K_FFN, 1, copies)
     wall, ev = dec.time(Wm, K)
     gbs = dec.weight_bytes / (ev * 1e-3) / 1e9
     head_bytes = dec.weight_bytes
     dec.close()
 
     # ---- config 2 prefill, T=512
-    pre = Workload(lib, rng, [(E.Q4_K, 8192, 2048), (E.Q4_K, 8192, 2048), (E.Q4_K, 2048, 8192)], 512, 1)
+    pre = Workload(lib, rng, Q4K_FFN, 512, 1)
     pwall, pev = pre.time(Wm, max(3, K // 4))
     tops = pre.ops / (pev * 1e-3) / 1e12
     pre.close()
@@ -288,6 +326,12 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(E.Q4_K, 8192, 2048, rng, args.cpu_seconds)
 
+    # HBM bytes per launch of the same workloads, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summaries
+    traffic = {}
+    tj = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if os.path.exists(tj):
+        for k, v in json.load(open(tj))["workloads"].items():
+            traffic[k] = v["hbm_read_bytes"] + v["hbm_write_bytes"]
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": Wm,
         "ms_per_step": round(wall, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -296,12 +340,13 @@ def main():
                                f"{copies} layer copies = {head_bytes / 1e9:.2f} GB rotating, one batched launch per step",
                    "global_batch": 1, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic.get("decode"),
+                     "algorithmic_bytes": head_bytes},
         "cpu_baseline": cpu,
         "prefill": {"workload": "Q4_K prefill T=512: gate/up 8192x2048 and down 2048x8192, one batched launch",
                     "value": round(tops, 2), "unit": "TOPS", "ms": round(pev, 4),
                     "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
-                                 "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None}},
+                                 "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": traffic.get("prefill")}},
         "configs": extra,
         "device": lib.device_name(),
     }
