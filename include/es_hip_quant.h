@@ -186,6 +186,10 @@ int es_hip_block_ints_dev(uint32_t type, const void *W, int cols, int rows, cons
  * the rest go to the vector kernels. n <= 0 switches the kernel off (here and below). */
 int es_hip_set_mfma_min_batch(int n);
 int es_hip_set_small_batch_min(int n);
+/* Workgroup tile of the matrix-core kernel for products of at least 128 activations: bm rows x bn activations on `waves`
+ * waves, one of 128 x 128 x 8, 128 x 64 x 8, 64 x 64 x 8, 64 x 64 x 4, 32 x 128 x 4; (0, 0, 0) restores the automatic
+ * choice (128 x 128 when that gives every CU a workgroup, else 64 x 64 x 8). Returns ES_HIP_OK or ES_HIP_EINVAL. */
+int es_hip_set_mfma_tile(int bm, int bn, int waves);
 /* Q4_0 / Q5_0 products with at least n activations run on the batched kernel (one lane per row and activation) instead of
  * the vector kernel (default 2). */
 int es_hip_set_batched32_min(int n);

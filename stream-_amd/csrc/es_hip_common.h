@@ -71,10 +71,11 @@ struct MmJob {
     int tile0, ntok_tiles;
 };
 // One activation pre-pass: kind 0 writes 16 bytes of meta per activation and superblock (pair sums of the Q4_K
-// sub-blocks, low | high bytes), kind 1 32 bytes (the 16 bsums, low | high bytes); xd follows the xm plane. All the
-// pre-passes of a batch run in one launch of `total` threads, pre-pass i taking threads [start, start + na_pad*nbk*73);
-// every start is a multiple of PREP_BLOCK, the launch's block size.
-constexpr int PREP_BLOCK = 256;
+// sub-blocks, low | high bytes), kind 1 32 bytes (the 16 bsums, low | high bytes), kind 2 32 bytes (the 16 bsums as
+// halves); xd follows the xm plane. All the
+// pre-passes of a batch run in one launch over `total` items (one dword of an activation row each), pre-pass i taking
+// items [start, start + na_pad*nbk*73); every start is a multiple of PREP_SPAN, the items of one workgroup.
+constexpr int PREP_BLOCK = 256, PREP_UNROLL = 8, PREP_SPAN = PREP_BLOCK * PREP_UNROLL;
 struct PrepJob {
     const uint8_t *act;
     const int *arow;
@@ -84,8 +85,9 @@ struct PrepJob {
     int na, na_pad, nbk, kind;
 };
 hipError_t prep_launch(const PrepJob *jobs, int njobs, const PrepJob &single, long total, hipStream_t s);
-hipError_t mm_launch(int type, int bm, int bn, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
+hipError_t mm_launch(int type, int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                      hipStream_t s);
+bool mm_tile_ok(int bm, int bn, int nw);   // a workgroup tile (rows x activations, waves) mm_launch has
 
 // The small-batch matrix-core form (es_hip_mq.hip): rows [r0, r1) against activations [t0, t0 + 16*wn) of na (at most
 // 64 per job), from pre-pass planes padded to na_pad activations. One workgroup per 64 rows.

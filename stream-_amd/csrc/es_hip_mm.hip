@@ -31,6 +31,7 @@
 
 namespace esq {
 
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
@@ -40,14 +41,32 @@ __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
 }
 
 // ---- pre-pass --------------------------------------------------------------------------------------------------------
-// One thread per dword of an activation's Q8_K row (nbk blocks of 73 dwords: d, 64 of qs, 8 of bsums pairs), so the
-// reads are coalesced; padding activations t >= na get zeros. Activation t is row arow[t] of act when arow is given.
-// kind 0 writes the pair sums (Q4_K sub-blocks), kind 1 the 16 bsums, both split as 128*hi + lo, one byte each.
-__global__ void act_prep_q8k(const PrepJob *__restrict__ jobs, int njobs, PrepJob single, long total) {
-    const long id0 = (long)blockIdx.x * blockDim.x, id = id0 + threadIdx.x;
-    if (id >= total) return;
+// One item per dword of an activation's Q8_K row (nbk blocks of 73 dwords: d, 64 of qs, 8 of bsums pairs), consecutive
+// items on consecutive threads so the reads are coalesced, PREP_UNROLL items per thread with every load issued before
+// the first store; padding activations t >= na get zeros. Activation t is row arow[t] of act when arow is given.
+// kind 0 writes the pair sums (Q4_K sub-blocks) and kind 1 the 16 bsums, both split as 128*hi + lo, one byte each; kind 2
+// writes the 16 bsums as halves (exact: a Q8_K block's bsums are sums of 16 int8 values, |bsums| <= 2048).
+// Index arithmetic is 32-bit within a pre-pass (the host keeps every pre-pass below 2^31 threads).
+// the loads of one thread's items: row indices (for a gather), then the activation words
+template <bool GATHER>
+__device__ __forceinline__ void prep_loads(const PrepJob &P, uint32_t base, uint32_t per, const bool (&ok)[PREP_UNROLL],
+                                           uint32_t (&row)[PREP_UNROLL], uint32_t (&v)[PREP_UNROLL]) {
+    if constexpr (GATHER) {
+#pragma unroll
+        for (int u = 0; u < PREP_UNROLL; u++) row[u] = (uint32_t)ldg<int>(P.arow + row[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < PREP_UNROLL; u++) {
+        const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x, t = lid / per, k = ok[u] ? lid - t * per : 0u;
+        v[u] = ldg<uint32_t>(P.act + (size_t)row[u] * P.astride + 4 * (size_t)k);
+    }
+}
+
+__global__ __launch_bounds__(PREP_BLOCK) void act_prep_q8k(const PrepJob *__restrict__ jobs, int njobs, PrepJob single,
+                                                            long total) {
+    const long id0 = (long)blockIdx.x * PREP_SPAN;
     int j = 0;
-    if (jobs) {   // last pre-pass with start <= id0 (starts are multiples of the block size: one search per block)
+    if (jobs) {   // last pre-pass with start <= id0 (starts are multiples of the span: one search per block)
         int lo = 0, hi = njobs - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
@@ -55,27 +74,51 @@ __global__ void act_prep_q8k(const PrepJob *__restrict__ jobs, int njobs, PrepJo
         }
         j = lo;
     }
-    const PrepJob P = jobs ? jobs[j] : single;
-    const long per = (long)P.nbk * 73, lid = id - P.start;
-    if (lid < 0 || lid >= (long)P.na_pad * per) return;
-    const int t = (int)(lid / per), k = (int)(lid % per), b = k / 73, w = k % 73;
-    const uint32_t v = t < P.na ? ldg<uint32_t>(P.act + (size_t)(P.arow ? ldg<int>(P.arow + t) : t) * P.astride + 4 * (size_t)k) : 0u;
-    const size_t bt = (size_t)b * P.na_pad + t;
-    uint8_t *xm = P.xm;
-    if (w == 0) {
-        stg<uint32_t>(xm + (size_t)P.nbk * P.na_pad * (P.kind ? 32 : 16) + bt * 4, v);   // d
-    } else if (w <= 64) {
-        stg<uint32_t>(P.xq + bt * 256 + 4 * (w - 1), v);                                  // qs
-    } else if (P.kind == 0) {
-        const int jj = w - 65, p = (int16_t)(v & 0xffff) + (int16_t)(v >> 16);   // bsums[2jj] + bsums[2jj+1]
-        stg<uint8_t>(xm + bt * 16 + jj, (uint8_t)(p & 127));
-        stg<uint8_t>(xm + bt * 16 + 8 + jj, (uint8_t)((p >> 7) & 0xff));
-    } else {
-        const int g = 2 * (w - 65), p0 = (int16_t)(v & 0xffff), p1 = (int16_t)(v >> 16);   // bsums[g], bsums[g+1]
-        stg<uint8_t>(xm + bt * 32 + g, (uint8_t)(p0 & 127));
-        stg<uint8_t>(xm + bt * 32 + g + 1, (uint8_t)(p1 & 127));
-        stg<uint8_t>(xm + bt * 32 + 16 + g, (uint8_t)((p0 >> 7) & 0xff));
-        stg<uint8_t>(xm + bt * 32 + 16 + g + 1, (uint8_t)((p1 >> 7) & 0xff));
+    PrepJob P;
+    if (jobs) P = jobs[j];
+    else P = single;
+    const uint32_t per = (uint32_t)P.nbk * 73u, n = (uint32_t)P.na_pad * per, base = (uint32_t)(id0 - P.start);
+    const int mb = P.kind == 0 ? 16 : 32;   // meta bytes per (activation, superblock)
+    // every load of the span first, unconditionally (items past the end read the first word and keep 0), so they are all
+    // in flight together; then the stores
+    uint32_t v[PREP_UNROLL], row[PREP_UNROLL];
+    bool ok[PREP_UNROLL];
+#pragma unroll
+    for (int u = 0; u < PREP_UNROLL; u++) {
+        const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x, t = lid / per;
+        ok[u] = lid < n && (int)t < P.na;
+        row[u] = ok[u] ? t : 0u;
+    }
+    if (P.arow) prep_loads<true>(P, base, per, ok, row, v);   // two copies of the loads, so no branch splits them
+    else prep_loads<false>(P, base, per, ok, row, v);
+#pragma unroll
+    for (int u = 0; u < PREP_UNROLL; u++) v[u] = ok[u] ? v[u] : 0u;
+#pragma unroll
+    for (int u = 0; u < PREP_UNROLL; u++) {
+        const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x;
+        if (lid >= n) break;
+        const uint32_t t = lid / per, k = lid - t * per, b = k / 73u, w = k - 73u * b;
+        const size_t bt = (size_t)b * P.na_pad + t;
+        uint8_t *xm = P.xm;
+        if (w == 0) {
+            stg<uint32_t>(xm + (size_t)P.nbk * P.na_pad * mb + bt * 4, v[u]);   // d
+        } else if (w <= 64) {
+            stg<uint32_t>(P.xq + bt * 256 + 4 * (w - 1), v[u]);                 // qs
+        } else if (P.kind == 2) {
+            const _Float16 h0 = (_Float16)(int16_t)(v[u] & 0xffff), h1 = (_Float16)(int16_t)(v[u] >> 16);
+            stg<uint32_t>(xm + bt * 32 + 4 * (w - 65),
+                          (uint32_t)__builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        } else if (P.kind == 0) {
+            const int jj = w - 65, p = (int16_t)(v[u] & 0xffff) + (int16_t)(v[u] >> 16);   // bsums[2jj] + bsums[2jj+1]
+            stg<uint8_t>(xm + bt * 16 + jj, (uint8_t)(p & 127));
+            stg<uint8_t>(xm + bt * 16 + 8 + jj, (uint8_t)((p >> 7) & 0xff));
+        } else {
+            const int g = 2 * (w - 65), p0 = (int16_t)(v[u] & 0xffff), p1 = (int16_t)(v[u] >> 16);   // bsums[g], bsums[g+1]
+            stg<uint8_t>(xm + bt * 32 + g, (uint8_t)(p0 & 127));
+            stg<uint8_t>(xm + bt * 32 + g + 1, (uint8_t)(p1 & 127));
+            stg<uint8_t>(xm + bt * 32 + 16 + g, (uint8_t)((p0 >> 7) & 0xff));
+            stg<uint8_t>(xm + bt * 32 + 16 + g + 1, (uint8_t)((p1 >> 7) & 0xff));
+        }
     }
 }
 
@@ -102,25 +145,42 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 }
 
 template <int N> __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+// s_waitcnt vmcnt(n * L) for a wave-uniform n in 0 .. NMAX
+template <int L, int NMAX> __device__ __forceinline__ void wait_stages(int n) {
+    if constexpr (NMAX > 0) {
+        if (n >= NMAX) { wait_vmcnt<L * NMAX>(); return; }
+        wait_stages<L, NMAX - 1>(n);
+    } else {
+        wait_vmcnt<0>();
+    }
+}
 
-template <int RW, int WM, int WN> struct MmGeom {
-    static constexpr int TW = 8 / RW;
-    static constexpr int BM = 16 * WM * RW, BN = 16 * WN * TW;
-    // stage regions in bytes: weights BM x 144 | activations BN x 256 | pair sums BN x 16 | scales BN x 4
-    static constexpr int X_OFF = BM * 144, M_OFF = X_OFF + BN * 256, D_OFF = M_OFF + BN * 16, STAGE = D_OFF + BN * 4;
-    static constexpr int CW = BM * 9, CX = BN * 16, CM = BN, CD = BN / 4, NCH = CW + CX + CM + CD;   // 16-byte chunks
+template <int RW, int TW, int WN, int NST> struct MmGeom {
+    static constexpr int NW = RW * TW;   // waves
+    static constexpr int BM = 16 * RW, BN = 16 * WN * TW;
+    // 16-byte chunks of a stage: weights BM x 9 (the region padded to whole wave-loads) | activations BN x 16 | bsums
+    // BN x 2 | scales BN / 4
+    static constexpr int CW = BM * 9, CWP = (CW + 63) / 64 * 64, CX = BN * 16, CM = BN * 2, CD = BN / 4;
+    static constexpr int NCH = CWP + CX + CM + CD;
+    static constexpr int X_OFF = CWP * 16, M_OFF = X_OFF + BN * 256, D_OFF = M_OFF + BN * 32, STAGE = D_OFF + BN * 4;
     static constexpr int NWL = (NCH + 63) / 64;   // wave-loads per stage
-    static constexpr int LOADS = (NWL + 7) / 8;   // per wave per stage
-    static_assert(CW % 64 == 0, "weight chunks end on a wave-load boundary");
-    static_assert(RW * TW == 8, "8 waves");
+    static constexpr int LOADS = (NWL + NW - 1) / NW;   // per wave per stage
+    static constexpr int LDS = NST * STAGE + 1024;   // the stages and a sink for the spare loads
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    static_assert(NST >= 2 && LDS <= 160 * 1024, "stages fit the LDS");
+    static_assert(LOADS * (NST - 2) <= 63, "vmcnt range");
 };
 
-// RW: waves along the rows (the others split the activations); WM, WN: 16 x 16 MFMA tiles per wave along rows and
-// activations. CONTRACT: the clang order (fused multiply-adds), else the gcc / scalar order.
-template <int RW, int WM, int WN, bool CONTRACT>
-__global__ __launch_bounds__(512) void mm_q4k_kernel(const MmJob *__restrict__ jobs, int njobs, MmJob single) {
-    using G = MmGeom<RW, WM, WN>;
-    __shared__ __align__(16) uint8_t smem[3 * G::STAGE + 1024];   // three stages and a sink for the spare loads
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// RW x TW waves: RW along the rows, TW along the activations; WN: 16 x 16 MFMA tiles per wave along the activations;
+// NST: LDS stages. CONTRACT: the clang order (fused multiply-adds), else the gcc / scalar order.
+template <int RW, int TW, int WN, int NST, bool CONTRACT>
+__global__ __launch_bounds__(64 * RW * TW) void mm_q4k_kernel(const MmJob *__restrict__ jobs, int njobs, MmJob single) {
+    using G = MmGeom<RW, TW, WN, NST>;
+    __shared__ __align__(16) uint8_t smem[G::LDS];
 
     MmJob J;
     if (jobs) J = jobs[find_mm_job(jobs, njobs, blockIdx.x)];
@@ -135,47 +195,47 @@ __global__ __launch_bounds__(512) void mm_q4k_kernel(const MmJob *__restrict__ j
     const int row0 = J.r0 + rt * G::BM, tok0 = tt * G::BN;
     const int nbk = J.cols / 256;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int wr = (wave % RW) * 16 * WM, wt = (wave / RW) * 16 * WN;   // this wave's rows / activations in the tile
+    const int wr = (wave % RW) * 16, wt = (wave / RW) * 16 * WN;   // this wave's rows / activations in the tile
     const int lr = lane & 15, lg = lane >> 4;
 
     // ---- per-lane sources of this wave's stage loads: wave-load L = wave + 8*kk covers chunks 64L .. 64L+63.
     // Weight chunks: base J.W + row0*row_bytes, offset + 144 per superblock. Activation-side chunks (the three planes of
     // one workspace allocation): base J.xq, offset + (plane stride per superblock).
     const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
-    const uint32_t xm_rel = (uint32_t)(J.xm - J.xq), xd_rel = xm_rel + (uint32_t)nbk * J.na_pad * 16;
+    const uint32_t xm_rel = (uint32_t)(J.xm - J.xq), xd_rel = xm_rel + (uint32_t)nbk * J.na_pad * 32;
     const int last_row = J.r1 - 1 - row0;
     uint32_t off[G::LOADS], step_off[G::LOADS];
     bool live[G::LOADS];
 #pragma unroll
     for (int kk = 0; kk < G::LOADS; kk++) {
-        const int L = wave + 8 * kk, c = 64 * L + lane;
-        live[kk] = c < G::NCH;
-        if (c < G::CW) {
+        const int L = wave + G::NW * kk, c = 64 * L + lane;
+        live[kk] = c < G::NCH && (c < G::CW || c >= G::CWP);
+        if (c < G::CWP) {
             const int r = min(c / 9, last_row);   // rows past the end repeat the last one; their results are not stored
             off[kk] = (uint32_t)r * (uint32_t)J.row_bytes + 16 * (c % 9);
             step_off[kk] = 144;
-        } else if (c < G::CW + G::CX) {
-            const int cx = c - G::CW, t = cx >> 4, q = (cx & 15) ^ (t & 15);
+        } else if (c < G::CWP + G::CX) {
+            const int cx = c - G::CWP, t = cx >> 4, q = (cx & 15) ^ (t & 15);
             off[kk] = (uint32_t)(tok0 + t) * 256 + 16 * q;
             step_off[kk] = (uint32_t)J.na_pad * 256;
-        } else if (c < G::CW + G::CX + G::CM) {
-            const int t = c - G::CW - G::CX;
-            off[kk] = xm_rel + (uint32_t)(tok0 + t) * 16;
-            step_off[kk] = (uint32_t)J.na_pad * 16;
+        } else if (c < G::CWP + G::CX + G::CM) {
+            const int cm = c - G::CWP - G::CX;
+            off[kk] = xm_rel + (uint32_t)(tok0 + (cm >> 1)) * 32 + 16 * (cm & 1);
+            step_off[kk] = (uint32_t)J.na_pad * 32;
         } else {
-            const int t4 = min(c - G::CW - G::CX - G::CM, G::CD - 1);
+            const int t4 = min(c - G::CWP - G::CX - G::CM, G::CD - 1);
             off[kk] = xd_rel + (uint32_t)(tok0 + 4 * t4) * 4;
             step_off[kk] = (uint32_t)J.na_pad * 4;
         }
     }
 
-    // the loads of superblock b into stage st (the offsets already point at superblock b)
+    // the loads of the next superblock into stage st (the offsets already point at it)
     auto issue = [&](int st) {
-        const uint32_t base = lds_addr(smem) + st * G::STAGE, snk = lds_addr(smem) + 3 * G::STAGE, off0 = off[0];
+        const uint32_t base = lds_addr(smem) + st * G::STAGE, snk = lds_addr(smem) + NST * G::STAGE, off0 = off[0];
 #pragma unroll
         for (int kk = 0; kk < G::LOADS; kk++) {
-            const int L = wave + 8 * kk;
-            const bool wl = 64 * L < G::CW;   // wave-uniform: weight or activation-side wave-load
+            const int L = wave + G::NW * kk;
+            const bool wl = 64 * L < G::CWP;   // wave-uniform: weight or activation-side wave-load
             if (L < G::NWL) {
                 if (live[kk]) load_lds16(wl ? wbase : J.xq, off[kk], base + 1024 * L);
             } else {
@@ -185,120 +245,152 @@ __global__ __launch_bounds__(512) void mm_q4k_kernel(const MmJob *__restrict__ j
         }
     };
 
-    float s[WM][WN][4];
+    // Permuted k order. MFMA slice s (0..3), lane group lg: the 16 nibbles of qs chunk lg + 4*(s >> 1) (low nibbles for
+    // even s, high for odd s), i.e. sub-block j = 2*((lg >> 1) + 2*(s >> 1)) + (s & 1), elements 32j + 16*(lg & 1) + [0, 16).
+    // The activation side reads the same elements: natural 16-element chunk nat(s) of the activation row.
+    uint32_t xo[4];   // activation chunk offsets of this lane in a stage (tile c adds 4096*c)
 #pragma unroll
-    for (int a = 0; a < WM; a++)
-#pragma unroll
-        for (int c = 0; c < WN; c++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[a][c][i] = 0.0f;
+    for (int s = 0; s < 4; s++) {
+        const int nat = 4 * (lg >> 1) + 8 * (s >> 1) + 2 * (s & 1) + (lg & 1);
+        xo[s] = G::X_OFF + (wt + lr) * 256 + 16 * (nat ^ lr);
+    }
+    const uint32_t mo = G::M_OFF + (wt + lr) * 32 + 16 * (lg & 1), dof = G::D_OFF + (wt + lr) * 4;
+    // byte selectors (v_perm_b32) that put byte (lg >> 1)*2 + e of a word into both 16-bit halves, the other bytes zero
+    const uint32_t sel0 = 0x0c000c00u + (uint32_t)(2 * (lg >> 1)) * 0x00010001u, sel1 = sel0 + 0x00010001u;
+    const int myrow = wr + lr;
 
-    const uint32_t nsh = lg >= 2 ? 4 : 0;   // high nibbles for lanes 32..63
+    float s[WN][4];
+#pragma unroll
+    for (int c = 0; c < WN; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[c][i] = 0.0f;
 
-    issue(0);
-    if (nbk > 1) issue(1);
+#pragma unroll
+    for (int k = 0; k < NST - 1; k++)
+        if (k < nbk) issue(k);
     int st = 0;   // stage of superblock b
     for (int b = 0; b < nbk; b++) {
-        if (b + 1 < nbk) wait_vmcnt<G::LOADS>();   // this wave's loads of stage b are in LDS (stage b+1 may still fly)
-        else wait_vmcnt<0>();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's reads of stage b-1 are done
-        __builtin_amdgcn_s_barrier();                         // ... and every wave's loads and reads
+        wait_stages<G::LOADS, NST - 2>(min(NST - 2, nbk - 1 - b));   // this wave's loads of stage b are in LDS
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");           // this wave's reads of stage b-1 are done
+        __builtin_amdgcn_s_barrier();                                 // ... and every wave's loads and reads
         asm volatile("" ::: "memory");
-        if (b + 2 < nbk) issue(st == 0 ? 2 : st - 1);         // stage (st + 2) % 3
-        const uint8_t *wb = smem + st * G::STAGE, *xb = wb + G::X_OFF, *mb = wb + G::M_OFF, *db = wb + G::D_OFF;
-        st = st == 2 ? 0 : st + 1;
+        if (b + NST - 1 < nbk) issue(st == 0 ? NST - 1 : st - 1);      // stage (st + NST - 1) % NST
+        const uint8_t *wb = smem + st * G::STAGE;
+        st = st == NST - 1 ? 0 : st + 1;
 
-        // rows' 6-bit scales and mins, byte-parallel (scale_min_k4, src/es_quant.c:75-83), and the A operands of all four
-        // k slices
-        v4i amin[WM], alo[WM][4], ahi[WM][4];
+        // LDS reads in the order they are needed (they complete in order): the weight rows for the A operands and the row
+        // scales, the activation scales of every tile, then the activation tiles 0 and 1; afterwards tile c+2 is read
+        // while tile c goes through the matrix cores and tile c-1 through the vector epilogue.
+        const uint8_t *row = wb + myrow * 144;
+        const uint4 h = *reinterpret_cast<const uint4 *>(row);
+        const uint4 q0 = *reinterpret_cast<const uint4 *>(row + 16 + 16 * lg);
+        const uint4 q1 = *reinterpret_cast<const uint4 *>(row + 80 + 16 * lg);
+        uint32_t ddw[4];
 #pragma unroll
-        for (int a = 0; a < WM; a++) {
-            const uint8_t *row = wb + (wr + 16 * a + lr) * 144;
-            const uint4 h = *reinterpret_cast<const uint4 *>(row);
-            const uint32_t sc0 = h.y & 0x3f3f3f3fu, sc1 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
-            const uint32_t mn0 = h.z & 0x3f3f3f3fu, mn1 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-            amin[a] = lg == 0 ? v4i{(int)mn0, (int)mn1, 0, 0} : v4i{0, 0, 0, 0};
+        for (int i = 0; i < 4; i++) ddw[i] = *reinterpret_cast<const uint32_t *>(wb + (wr + 4 * lg + i) * 144);
+        float tdv[WN];
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {   // this lane's sub-block in slice ks: j = 2ks + (lg >> 1)
-                const uint32_t scw = ks < 2 ? sc0 : sc1;
-                const uint32_t sc = (scw >> (16 * (ks & 1) + 8 * (lg >> 1))) & 0xff;
-                const uint32_t sl16 = (sc & 7) * 0x00010001u, sh16 = (sc >> 3) * 0x00010001u;
-                const uint4 w4 = *reinterpret_cast<const uint4 *>(row + 16 + 32 * ks + 16 * (lg & 1));
-                const uint32_t qq[4] = {w4.x, w4.y, w4.z, w4.w};
+        for (int c = 0; c < WN; c++) tdv[c] = *reinterpret_cast<const float *>(wb + dof + 64 * c);
+        struct Bt { v4i x[4]; v8h m; };
+        auto load_b = [&](int c, Bt &B) {
+#pragma unroll
+            for (int sl = 0; sl < 4; sl++) B.x[sl] = *reinterpret_cast<const v4i *>(wb + xo[sl] + 4096 * c);
+            B.m = *reinterpret_cast<const v8h *>(wb + mo + 512 * c);
+        };
+        constexpr int PD = WN < 2 ? WN : 2;   // tiles read ahead
+        Bt B[PD + 1];
+#pragma unroll
+        for (int c = 0; c < PD; c++) load_b(c, B[c]);
+
+        // ---- A operands of this wave's 16 rows: scales byte-parallel (scale_min_k4, src/es_quant.c:75-83)
+        const uint32_t sc0 = h.y & 0x3f3f3f3fu, sc1 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+        const uint32_t mn0 = h.z & 0x3f3f3f3fu, mn1 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+        // sc = 8*sh + sl; (sl, sh) of sub-blocks 2*(lg>>1) + {0, 1} (from sc0) and + {4, 5} (from sc1), each byte
+        // broadcast into both 16-bit halves
+        const uint32_t l0 = sc0 & 0x07070707u, h0 = (sc0 >> 3) & 0x07070707u;
+        const uint32_t l1 = sc1 & 0x07070707u, h1 = (sc1 >> 3) & 0x07070707u;
+        const uint32_t slw[4] = {__builtin_amdgcn_perm(0, l0, sel0), __builtin_amdgcn_perm(0, l0, sel1),
+                                 __builtin_amdgcn_perm(0, l1, sel0), __builtin_amdgcn_perm(0, l1, sel1)};
+        const uint32_t shw[4] = {__builtin_amdgcn_perm(0, h0, sel0), __builtin_amdgcn_perm(0, h0, sel1),
+                                 __builtin_amdgcn_perm(0, h1, sel0), __builtin_amdgcn_perm(0, h1, sel1)};
+        v4i alo[4], ahi[4];
+        {
+            const uint32_t qa[2][4] = {{q0.x, q0.y, q0.z, q0.w}, {q1.x, q1.y, q1.z, q1.w}};
+#pragma unroll
+            for (int sl = 0; sl < 4; sl++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const uint32_t nib = (qq[i] >> nsh) & 0x0f0f0f0fu;
-                    alo[a][ks][i] = (int)pk_mul_u16(nib, sl16);   // byte * scale <= 105: no carry between bytes
-                    ahi[a][ks][i] = (int)pk_mul_u16(nib, sh16);
+                    const uint32_t w = qa[sl >> 1][i];
+                    const uint32_t nib = (sl & 1) ? (w >> 4) & 0x0f0f0f0fu : w & 0x0f0f0f0fu;
+                    alo[sl][i] = (int)pk_mul_u16(nib, slw[sl]);   // byte * scale <= 105: no carry between bytes
+                    ahi[sl][i] = (int)pk_mul_u16(nib, shw[sl]);
                 }
-            }
         }
-        // d, dmin of the output rows of this lane: rows wr + 16a + 4lg + i
-        float dv[WM][4], dm[WM][4];
+        // mins operand (halves): lanes 0..15 carry mn_0..3, lanes 16..31 mn_4..7, each twice (k positions 2j, 2j+1 meet
+        // bsums[2j], bsums[2j+1]); lanes 32..63 zero. Each half is built as 1024 + m (byte m under the exponent of 1024)
+        // and 1024 subtracted exactly.
+        v8h amin;
+        {
+            const uint32_t mw = lg == 0 ? mn0 : lg == 1 ? mn1 : 0u;
+            const uint32_t m1024 = 0xe400e400u;   // -1024, -1024
 #pragma unroll
-        for (int a = 0; a < WM; a++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t dd = *reinterpret_cast<const uint32_t *>(wb + (wr + 16 * a + 4 * lg + i) * 144);
-                dv[a][i] = half_bits_to_float(dd);
-                dm[a][i] = half_bits_to_float(dd >> 16);
+            for (int e = 0; e < 4; e++) {
+                const uint32_t pr = __builtin_amdgcn_perm(0x64646464u, mw, 0x04000400u + (uint32_t)e * 0x00010001u);
+                const h2 v = __builtin_bit_cast(h2, pr) + __builtin_bit_cast(h2, m1024);
+                amin[2 * e] = v[0];
+                amin[2 * e + 1] = v[1];
             }
-
-        // Activation tiles one after another, software-pipelined: the LDS reads of tile c+1 are issued before the matrix
-        // work of tile c, and that before the vector epilogue of tile c-1.
-        struct Bt { v4i x[4]; uint4 m; float td; };
-        auto load_b = [&](int c, Bt &B) {
-            const int t = wt + 16 * c + lr;
+            if (lg >= 2) amin = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        // d, dmin of the output rows of this lane: rows wr + 4lg + i
+        float dv[4], dm[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) B.x[ks] = *reinterpret_cast<const v4i *>(xb + t * 256 + 16 * ((4 * ks + lg) ^ lr));
-            B.m = *reinterpret_cast<const uint4 *>(mb + t * 16);
-            B.td = *reinterpret_cast<const float *>(db + t * 4);
-        };
-        v4i acc_lo[2][WM], acc_hi[2][WM], mn_lo[2][WM], mn_hi[2][WM];
-        float tdv[2];
+        for (int i = 0; i < 4; i++) {
+            dv[i] = half_bits_to_float(ddw[i]);
+            dm[i] = half_bits_to_float(ddw[i] >> 16);
+        }
+
+        v4i acc_lo[2], acc_hi[2];
+        v4f acc_mn[2];
         auto mma = [&](int c, const Bt &B) {
             const int u = c & 1;
-            tdv[u] = B.td;
-            // mins on the matrix cores: k positions 0..7 (the first 8 bytes of lanes 0..15) carry the pairs; the other
-            // positions of amin are zero, so whatever B holds there does not count
-            const v4i blo = v4i{(int)B.m.x, (int)B.m.y, (int)B.m.z, (int)B.m.w};
-            const v4i bhi = v4i{(int)B.m.z, (int)B.m.w, (int)B.m.x, (int)B.m.y};
+            acc_mn[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, B.m, v4f{0, 0, 0, 0}, 0, 0, 0);
+            acc_lo[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[0], B.x[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            acc_hi[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[0], B.x[0], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-            for (int a = 0; a < WM; a++) {
-                mn_lo[u][a] = __builtin_amdgcn_mfma_i32_16x16x64_i8(amin[a], blo, v4i{0, 0, 0, 0}, 0, 0, 0);
-                mn_hi[u][a] = __builtin_amdgcn_mfma_i32_16x16x64_i8(amin[a], bhi, v4i{0, 0, 0, 0}, 0, 0, 0);
+            for (int sl = 1; sl < 4; sl++) {
+                acc_lo[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[sl], B.x[sl], acc_lo[u], 0, 0, 0);
+                acc_hi[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[sl], B.x[sl], acc_hi[u], 0, 0, 0);
             }
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int a = 0; a < WM; a++) {
-                    const v4i zlo = ks ? acc_lo[u][a] : v4i{0, 0, 0, 0}, zhi = ks ? acc_hi[u][a] : v4i{0, 0, 0, 0};
-                    acc_lo[u][a] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[a][ks], B.x[ks], zlo, 0, 0, 0);
-                    acc_hi[u][a] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[a][ks], B.x[ks], zhi, 0, 0, 0);
-                }
         };
         // fp32 epilogue of superblock b for tile c, per (row, activation), in the reference's order
         auto epi = [&](int c) {
             const int u = c & 1;
 #pragma unroll
-            for (int a = 0; a < WM; a++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int dot = acc_lo[u][a][i] + 8 * acc_hi[u][a][i];
-                    const float q = dm[a][i] * static_cast<float>(mn_lo[u][a][i] + 128 * mn_hi[u][a][i]);
-                    if constexpr (CONTRACT)
-                        s[a][c][i] = __builtin_fmaf(tdv[u], __builtin_fmaf(dv[a][i], static_cast<float>(dot), -q), s[a][c][i]);
-                    else
-                        s[a][c][i] = s[a][c][i] + tdv[u] * (dv[a][i] * static_cast<float>(dot) - q);
-                }
+            for (int i = 0; i < 4; i++) {
+                const int dot = acc_lo[u][i] + 8 * acc_hi[u][i];
+                const float q = dm[i] * acc_mn[u][i];   // the mins are exact integers in the f32 accumulator
+                if constexpr (CONTRACT)
+                    s[c][i] = __builtin_fmaf(tdv[c], __builtin_fmaf(dv[i], static_cast<float>(dot), -q), s[c][i]);
+                else
+                    s[c][i] = s[c][i] + tdv[c] * (dv[i] * static_cast<float>(dot) - q);
+            }
         };
-        Bt B[2];
-        load_b(0, B[0]);
+        // One scheduling group per tile, its instructions interleaved as 1 MFMA : 2 VALU (: 1 LDS read): a SIMD issues
+        // about two vector instructions in the shadow of each 16-cycle MFMA, the rest would cost their full time.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < WN; c++) {
-            if (c + 1 < WN) load_b(c + 1, B[(c + 1) & 1]);
-            mma(c, B[c & 1]);
+            if (c + PD < WN) load_b(c + PD, B[(c + PD) % (PD + 1)]);
+            mma(c, B[c % (PD + 1)]);
             if (c) epi(c - 1);
+#pragma unroll
+            for (int k = 0; k < 9; k++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+                if (k < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         epi(WN - 1);
         asm volatile("" ::: "memory");   // stage b's LDS reads stay before the next superblock's barrier
@@ -306,51 +398,59 @@ __global__ __launch_bounds__(512) void mm_q4k_kernel(const MmJob *__restrict__ j
 
     // ---- outputs
 #pragma unroll
-    for (int a = 0; a < WM; a++)
+    for (int c = 0; c < WN; c++) {
+        const int t = tok0 + wt + 16 * c + lr;
+        if (t >= J.na) continue;
+        const int r = row0 + wr + 4 * lg;   // this lane holds rows r .. r+3 of activation t
+        float *yp = J.y + (size_t)t * J.ystride + r;
+        if (r + 3 < J.r1 && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
+            stg<float4>(yp, make_float4(s[c][0], s[c][1], s[c][2], s[c][3]));
+        } else {
 #pragma unroll
-        for (int c = 0; c < WN; c++) {
-            const int t = tok0 + wt + 16 * c + lr;
-            if (t >= J.na) continue;
-            const int r = row0 + wr + 16 * a + 4 * lg;   // this lane holds rows r .. r+3 of activation t
-            float *yp = J.y + (size_t)t * J.ystride + r;
-            if (r + 3 < J.r1 && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
-                stg<float4>(yp, make_float4(s[a][c][0], s[a][c][1], s[a][c][2], s[a][c][3]));
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (r + i < J.r1) stg<float>(yp + i, s[a][c][i]);
-            }
+            for (int i = 0; i < 4; i++)
+                if (r + i < J.r1) stg<float>(yp + i, s[c][i]);
         }
+    }
 }
 
 // ---- launch glue -------------------------------------------------------------------------------------------------
 hipError_t prep_launch(const PrepJob *jobs, int njobs, const PrepJob &single, long total, hipStream_t s) {
     if (total <= 0) return hipSuccess;
-    const int threads = PREP_BLOCK;
-    hipLaunchKernelGGL(act_prep_q8k, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0, s, jobs, njobs, single,
-                       total);
+    hipLaunchKernelGGL(act_prep_q8k, dim3((unsigned)((total + PREP_SPAN - 1) / PREP_SPAN)), dim3(PREP_BLOCK), 0, s, jobs, njobs,
+                       single, total);
     return hipGetLastError();
 }
 
-template <int RW, int WM, int WN>
+template <int RW, int TW, int WN, int NST>
 static hipError_t mm_launch_cfg(const MmJob *jobs, int njobs, const MmJob &single, int grid, int order, hipStream_t s) {
     if (order == ES_HIP_ORDER_X86_CONTRACT)
-        hipLaunchKernelGGL((mm_q4k_kernel<RW, WM, WN, true>), dim3(grid), dim3(512), 0, s, jobs, njobs, single);
+        hipLaunchKernelGGL((mm_q4k_kernel<RW, TW, WN, NST, true>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
     else
-        hipLaunchKernelGGL((mm_q4k_kernel<RW, WM, WN, false>), dim3(grid), dim3(512), 0, s, jobs, njobs, single);
+        hipLaunchKernelGGL((mm_q4k_kernel<RW, TW, WN, NST, false>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
     return hipGetLastError();
 }
 
-// workgroup tiles: 128 x 128 (8 waves of 16 rows x 128 activations), 64 x 64 (4 x 2 waves of 16 rows x 32), and for small
-// batches 128 rows x 16, 32 or 64 activations
-hipError_t mm_launch(int type, int bm, int bn, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
+// Workgroup tiles (rows x activations, waves): 128 x 128 (8 waves of 16 rows x 128 activations), 64 x 64 (4 x 2 waves of
+// 16 x 32, or 4 waves of 16 x 64), 32 x 128 (2 x 2 waves of 16 x 64), and for small batches 128 rows x 16, 32 or 64
+// activations; as many LDS stages as fit (at least two).
+bool mm_tile_ok(int bm, int bn, int nw) {
+    return (nw == 8 && bm == 128 && (bn == 128 || bn == 64 || bn == 32 || bn == 16)) || (nw == 8 && bm == 64 && bn == 64) ||
+           (nw == 4 && bm == 64 && bn == 64) || (nw == 4 && bm == 32 && bn == 128);
+}
+
+hipError_t mm_launch(int type, int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                      hipStream_t s) {
     if (type != ES_HIP_Q4_K) return hipErrorInvalidValue;
-    if (bm == 128 && bn == 128) return mm_launch_cfg<8, 1, 8>(jobs, njobs, single, grid, order, s);
-    if (bm == 128 && bn == 64) return mm_launch_cfg<8, 1, 4>(jobs, njobs, single, grid, order, s);
-    if (bm == 128 && bn == 32) return mm_launch_cfg<8, 1, 2>(jobs, njobs, single, grid, order, s);
-    if (bm == 128 && bn == 16) return mm_launch_cfg<8, 1, 1>(jobs, njobs, single, grid, order, s);
-    if (bm == 64 && bn == 64) return mm_launch_cfg<4, 1, 2>(jobs, njobs, single, grid, order, s);
+    if (nw == 8) {
+        if (bm == 128 && bn == 128) return mm_launch_cfg<8, 1, 8, 2>(jobs, njobs, single, grid, order, s);
+        if (bm == 128 && bn == 64) return mm_launch_cfg<8, 1, 4, 4>(jobs, njobs, single, grid, order, s);
+        if (bm == 128 && bn == 32) return mm_launch_cfg<8, 1, 2, 5>(jobs, njobs, single, grid, order, s);
+        if (bm == 128 && bn == 16) return mm_launch_cfg<8, 1, 1, 6>(jobs, njobs, single, grid, order, s);
+        if (bm == 64 && bn == 64) return mm_launch_cfg<4, 2, 2, 5>(jobs, njobs, single, grid, order, s);
+    } else if (nw == 4) {
+        if (bm == 64 && bn == 64) return mm_launch_cfg<4, 1, 4, 5>(jobs, njobs, single, grid, order, s);
+        if (bm == 32 && bn == 128) return mm_launch_cfg<2, 2, 4, 3>(jobs, njobs, single, grid, order, s);
+    }
     return hipErrorInvalidValue;
 }
 

@@ -19,12 +19,6 @@
 
 #include "es_hip_common.h"
 
-// workgroup tile of the matrix-core kernel (rows = activations): 0 chooses per product, 64 or 128 fixes it (a build-time
-// tuning knob)
-#ifndef ESQ_MM_BN
-#define ESQ_MM_BN 0
-#endif
-
 using esq::MvJob;
 using esq::MvLaunch;
 
@@ -140,6 +134,7 @@ int check_req(const Req &q, const FmtInfo &f) {
     if (q.na > 1 && q.ystride < (size_t)q.r1) return fail(ES_HIP_EINVAL, "ystride %zu < r1 %d: outputs of activations overlap", q.ystride, q.r1);
     const int slots = 64 / f.lpb, nbk = q.cols / f.be;
     if (nbk > 8 * slots) return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this kernel handles", q.type, q.cols, 8 * slots * f.be);   // 8 waves x one segment each
+    if ((long)q.na * nbk * 73 > (1L << 30)) return fail(ES_HIP_EINVAL, "%d activations of %d columns: above 2^30 words per product", q.na, q.cols);
     return ES_HIP_OK;
 }
 
@@ -263,7 +258,7 @@ struct MqGroup {   // one small-batch matrix-core launch: products of one format
 };
 
 struct MmGroup {   // one matrix-core launch: products sharing a workgroup tile shape
-    int bm, bn, grid = 0;
+    int bm, bn, nw, grid = 0;
     std::vector<esq::MmJob> jobs;
     size_t off = 0;   // byte offset of the job table in the device image
 };
@@ -283,19 +278,26 @@ struct Batch {
     size_t table_bytes = 0;
 };
 
+std::atomic<int> g_mm_tile{0};   // forced tile for batches of >= 128 activations: bm | bn << 10 | waves << 20 (0: automatic)
+
 // Workgroup tile of a product: the largest (best operand reuse) that still gives every CU a workgroup.
-void mm_tile(const esq::MmJob &j, int &bm, int &bn) {
+void mm_tile(const esq::MmJob &j, int &bm, int &bn, int &nw) {
+    nw = 8;
     if (j.na_pad < 128) {   // small batches: 128 rows x all the activations (16, 32 or 64)
         bm = 128;
         bn = j.na_pad;
         return;
     }
-    static const int cand[2] = {128, 64};   // square tiles: 128 x 128, 64 x 64
-    const int rows = j.r1 - j.r0;
-    for (int c : cand) {
-        bm = bn = ESQ_MM_BN ? ESQ_MM_BN : c;
-        if ((long)((rows + bm - 1) / bm) * (j.na_pad / bn) >= 256) return;
+    if (const int f = g_mm_tile.load()) {
+        bm = f & 1023;
+        bn = (f >> 10) & 1023;
+        nw = f >> 20;
+        return;
     }
+    const int rows = j.r1 - j.r0;
+    bm = bn = 128;
+    if ((long)((rows + 127) / 128) * (j.na_pad / 128) >= 256) return;
+    bm = bn = 64;   // 64 x 64: four times the workgroups
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
@@ -402,7 +404,7 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         }
         const int na_pad = q.na <= 16 ? 16 : q.na <= 32 ? 32 : q.na <= 64 ? 64
                                         : (q.na + esq::MM_NA_PAD - 1) / esq::MM_NA_PAD * esq::MM_NA_PAD;
-        const Prep *pp = &get_prep(bt, q, f, 0, na_pad);
+        const Prep *pp = &get_prep(bt, q, f, 2, na_pad);
         esq::MmJob j{};
         j.W = static_cast<const uint8_t *>(q.W);
         j.xq = reinterpret_cast<const uint8_t *>(pp->xq_off);
@@ -421,12 +423,12 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
     // workgroups start first
     std::stable_sort(bt.mm.begin(), bt.mm.end(), [](const esq::MmJob &x, const esq::MmJob &y) { return x.cols > y.cols; });
     for (esq::MmJob j : bt.mm) {
-        int bm, bn;
-        mm_tile(j, bm, bn);
+        int bm, bn, nw;
+        mm_tile(j, bm, bn, nw);
         MmGroup *g = nullptr;
         for (MmGroup &x : bt.mmg)
-            if (x.bm == bm && x.bn == bn) g = &x;
-        if (!g) { bt.mmg.push_back(MmGroup{bm, bn}); g = &bt.mmg.back(); }
+            if (x.bm == bm && x.bn == bn && x.nw == nw) g = &x;
+        if (!g) { bt.mmg.push_back(MmGroup{bm, bn, nw}); g = &bt.mmg.back(); }
         j.tile0 = g->grid;   // a multiple of 8: the kernel maps tiles to XCDs by id % 8
         j.ntok_tiles = j.na_pad / bn;
         const int row_tiles = (j.r1 - j.r0 + bm - 1) / bm;
@@ -478,7 +480,7 @@ void bind(Batch &bt, uint8_t *ws) {
                        bt.prep_total, p.na, p.na_pad, p.nbk, p.kind};
         bt.pj.push_back(j);
         const long n = (long)p.na_pad * p.nbk * 73;
-        bt.prep_total += (n + esq::PREP_BLOCK - 1) / esq::PREP_BLOCK * esq::PREP_BLOCK;
+        bt.prep_total += (n + esq::PREP_SPAN - 1) / esq::PREP_SPAN * esq::PREP_SPAN;
     }
 }
 
@@ -515,7 +517,7 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
     }
     for (const MmGroup &g : bt.mmg) {
         const esq::MmJob *dj = tables ? reinterpret_cast<const esq::MmJob *>(tables + g.off) : nullptr;
-        if ((e = esq::mm_launch(ES_HIP_Q4_K, g.bm, g.bn, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+        if ((e = esq::mm_launch(ES_HIP_Q4_K, g.bm, g.bn, g.nw, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
             return hip_fail(e, "matrix-core launch");
     }
     for (const MbGroup &g : bt.mbg) {
@@ -766,6 +768,15 @@ void es_hip_plan_destroy(es_hip_plan *p) {
 }
 
 int es_hip_set_mfma_min_batch(int n) { return g_mm_min.exchange(n); }
+int es_hip_set_mfma_tile(int bm, int bn, int waves) {
+    if (bm == 0 && bn == 0 && waves == 0) {
+        g_mm_tile.store(0);
+        return ES_HIP_OK;
+    }
+    if (!esq::mm_tile_ok(bm, bn, waves) || bn < 64) return fail(ES_HIP_EINVAL, "no %d x %d tile with %d waves", bm, bn, waves);
+    g_mm_tile.store(bm | bn << 10 | waves << 20);
+    return ES_HIP_OK;
+}
 int es_hip_set_small_batch_min(int n) { return g_mq_min.exchange(n); }
 int es_hip_set_batched32_min(int n) { return g_mb_min.exchange(n); }
 

@@ -117,6 +117,7 @@ class Lib:
             ("es_hip_block_ints_dev", i, [u32, vp, i, i, vp, vp, vp, vp]),
             ("es_hip_run_jobs_host", i, [vp, i]),
             ("es_hip_set_mfma_min_batch", i, [i]), ("es_hip_set_small_batch_min", i, [i]),
+            ("es_hip_set_mfma_tile", i, [i, i, i]),
             ("es_hip_set_batched32_min", i, [i]),
             ("es_hip_moe_ffn", i, [vp, i, vp, vp, vp, i, vp, sz, vp, sz, vp]),
             ("es_hip_moe_plan_create", vp, [vp, i, vp, vp, vp, i, vp, sz, vp, sz]),
@@ -148,6 +149,9 @@ class Lib:
 
     def set_small_batch_min(self, n: int) -> int:
         return self._L.es_hip_set_small_batch_min(n)
+
+    def set_mfma_tile(self, bm: int = 0, bn: int = 0, waves: int = 0) -> int:
+        return self._check(self._L.es_hip_set_mfma_tile(bm, bn, waves))
 
     def set_batched32_min(self, n: int) -> int:
         return self._L.es_hip_set_batched32_min(n)

@@ -72,6 +72,33 @@ def test_mfma_equals_vector_path(hipm, orc, rows, cols, na):
     assert np.array_equal(bits(y_mm[:2]), bits(ref))
 
 
+TILES = [(128, 128, 8), (128, 64, 8), (64, 64, 8), (64, 64, 4), (32, 128, 4)]
+
+
+@pytest.mark.parametrize("tile", TILES, ids=["x".join(map(str, t)) for t in TILES])
+@pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
+def test_mfma_every_tile(hip, orc, tile, mode):
+    """each workgroup tile of the prefill kernel (forced), on ragged rows and activations: bit-identical to the oracle"""
+    rows, cols, na = 200, 1024, 150
+    W, acts = inputs(orc, rows, cols, na, 4242)
+    hip.set_order(mode[0])
+    hip.set_mfma_tile(*tile)
+    try:
+        y = hip.matvec_multi(O.Q4_K, W, cols, rows, acts)
+    finally:
+        hip.set_mfma_tile(0, 0, 0)
+        hip.set_order(E.ORDER_X86_CONTRACT)
+    pick = np.array([0, 1, 63, 64, 127, 128, 149])
+    ref = orc.matvec_multi(O.Q4_K, W, cols, rows, acts[pick], mode[1], mode[2])
+    assert np.array_equal(bits(y[pick]), bits(ref))
+
+
+def test_mfma_tile_knob_rejects_unknown_shapes(hip):
+    for bad in [(128, 128, 4), (64, 128, 8), (96, 64, 8), (128, 16, 8)]:
+        with pytest.raises(E.EsHipError):
+            hip.set_mfma_tile(*bad)
+
+
 def test_mfma_row_range_and_strides(hipm, orc):
     rows, cols, na, r0, r1 = 300, 1024, 70, 37, 251
     W, acts = inputs(orc, rows, cols, na, 99)
