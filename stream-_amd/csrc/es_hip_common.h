@@ -88,6 +88,9 @@ hipError_t prep_launch(const PrepJob *jobs, int njobs, const PrepJob &single, lo
 hipError_t mm_launch(int type, int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                      hipStream_t s);
 bool mm_tile_ok(int bm, int bn, int nw);   // a workgroup tile (rows x activations, waves) mm_launch has
+// The Q6_K form (es_hip_mm6.hip): tiles of 128 rows x 16, 32 or 64 activations on 8 waves
+hipError_t mm6_launch(int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
+                      hipStream_t s);
 
 // The small-batch matrix-core form (es_hip_mq.hip): rows [r0, r1) against activations [t0, t0 + 16*wn) of na (at most
 // 64 per job), from pre-pass planes padded to na_pad activations. One workgroup per 64 rows.
@@ -171,6 +174,55 @@ template <int G> __device__ __forceinline__ int group_sum(int v) {
     if constexpr (G >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
     if constexpr (G >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
     return v;
+}
+
+
+// ---- matrix-core kernel helpers (es_hip_mm.hip, es_hip_mm6.hip) --------------------------------------------------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// two 16-bit lanes multiplied (v_pk_mul_lo_u16): four bytes times a small scale at once when no byte product exceeds 255
+__device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
+}
+
+__device__ __forceinline__ int find_mm_job(const MmJob *jobs, int njobs, int bid) {
+    int lo = 0, hi = njobs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (jobs[mid].tile0 <= bid) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// One wave's 64 x 16 bytes from global memory straight into LDS: lane l's 16 bytes at base + off land at lds + 16*l
+// (lds is wave-uniform). Written as inline assembly so that the compiler does not track these LDS writes: it would
+// otherwise wait for every one of them to finish before any LDS read. The kernel orders them itself (s_waitcnt vmcnt +
+// s_barrier before a stage is read). M0 is set inside the statement; nothing else in these kernels uses M0.
+__device__ __forceinline__ void load_lds16(const uint8_t *base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory");
+}
+// The same for 4 bytes per lane (global_load_lds_dword): lane l's dword at base + off lands at lds + 4*l.
+__device__ __forceinline__ void load_lds4(const uint8_t *base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+
+template <int N> __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+// s_waitcnt vmcnt(n * L) for a wave-uniform n in 0 .. NMAX
+template <int L, int NMAX> __device__ __forceinline__ void wait_stages(int n) {
+    if constexpr (NMAX > 0) {
+        if (n >= NMAX) { wait_vmcnt<L * NMAX>(); return; }
+        wait_stages<L, NMAX - 1>(n);
+    } else {
+        wait_vmcnt<0>();
+    }
 }
 
 }  // namespace esq

@@ -32,13 +32,7 @@
 namespace esq {
 
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
-// two 16-bit lanes multiplied (v_pk_mul_lo_u16): four bytes times a small scale at once when no byte product exceeds 255
-__device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
-}
 
 // ---- pre-pass --------------------------------------------------------------------------------------------------------
 // One item per dword of an activation's Q8_K row (nbk blocks of 73 dwords: d, 64 of qs, 8 of bsums pairs), consecutive
@@ -123,37 +117,8 @@ __global__ __launch_bounds__(PREP_BLOCK) void act_prep_q8k(const PrepJob *__rest
 }
 
 // ---- main kernel ---------------------------------------------------------------------------------------------------
-__device__ __forceinline__ int find_mm_job(const MmJob *jobs, int njobs, int bid) {
-    int lo = 0, hi = njobs - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (jobs[mid].tile0 <= bid) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-}
 
-// One wave's 64 x 16 bytes from global memory straight into LDS: lane l's 16 bytes at base + off land at lds + 16*l
-// (lds is wave-uniform). Written as inline assembly so that the compiler does not track these LDS writes: it would
-// otherwise wait for every one of them to finish before any LDS read. The kernel orders them itself (s_waitcnt vmcnt +
-// s_barrier before a stage is read). M0 is set inside the statement; nothing else in these kernels uses M0.
-__device__ __forceinline__ void load_lds16(const uint8_t *base, uint32_t off, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-                 : "memory");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t *)p;
-}
 
-template <int N> __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
-// s_waitcnt vmcnt(n * L) for a wave-uniform n in 0 .. NMAX
-template <int L, int NMAX> __device__ __forceinline__ void wait_stages(int n) {
-    if constexpr (NMAX > 0) {
-        if (n >= NMAX) { wait_vmcnt<L * NMAX>(); return; }
-        wait_stages<L, NMAX - 1>(n);
-    } else {
-        wait_vmcnt<0>();
-    }
-}
 
 template <int RW, int TW, int WN, int NST> struct MmGeom {
     static constexpr int NW = RW * TW;   // waves
@@ -171,9 +136,6 @@ template <int RW, int TW, int WN, int NST> struct MmGeom {
     static_assert(LOADS * (NST - 2) <= 63, "vmcnt range");
 };
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float v4f __attribute__((ext_vector_type(4)));
 
 // RW x TW waves: RW along the rows, TW along the activations; WN: 16 x 16 MFMA tiles per wave along the activations;
 // NST: LDS stages. CONTRACT: the clang order (fused multiply-adds), else the gcc / scalar order.
@@ -440,6 +402,7 @@ bool mm_tile_ok(int bm, int bn, int nw) {
 
 hipError_t mm_launch(int type, int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                      hipStream_t s) {
+    if (type == ES_HIP_Q6_K) return mm6_launch(bm, bn, nw, jobs, njobs, single, grid, order, s);
     if (type != ES_HIP_Q4_K) return hipErrorInvalidValue;
     if (nw == 8) {
         if (bm == 128 && bn == 128) return mm_launch_cfg<8, 1, 8, 2>(jobs, njobs, single, grid, order, s);

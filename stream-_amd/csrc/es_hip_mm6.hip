@@ -1,0 +1,308 @@
+// Batched Q6_K products on the int8 matrix cores: the prompt-reading form of es_matvec_multi (src/es_quant.c:1818-1850)
+// for Q6_K rows against 16 or more activations (e.g. an output head over a prompt tail). The reference forms, per row,
+// activation and superblock, tot = sum sc * q_u * x - 32 * sum_g sc_g * bsums_g with q_u the unsigned 6-bit code, then
+// s += (y.d * d) * tot (src/es_quant.c:1602-1640).
+//
+// The products q_u * sc (up to 63 * 128 in size) do not fit int8. With sc_u = sc + 128 = 16h + l and q_u = 8a + b (h, l
+// in 0..15, a, b in 0..7):  q_u * sc = q_u * sc_u - 128 q_u = 128 (a h - q_u) + 16 b h + 8 a l + b l,
+// four int8 planes (a h - q_u in -63..105, the others in 0..105) through the matrix cores, recombined exactly in int32:
+//   sum q_u * sc * x = 128 D(ah - q_u) + 16 D(bh) + 8 D(al) + D(bl).
+// corr = sum_g sc_g * bsums_g goes through one f16 MFMA (scales and bsums are exact halves and every partial sum stays
+// below 2^24: exact).
+//
+// Weights: a 210-byte superblock starts 2-byte aligned, so each row's superblock b is staged by dword loads of the
+// 212-byte dword-aligned stretch that covers it (from byte 210b - 2(b & 1) of the row). Rows must be 4-byte aligned (an
+// even number of superblocks); the stretch then never leaves the row. The A fields are read at 2-byte aligned LDS
+// addresses (the hardware's unaligned LDS access).
+//
+// K order: MFMA slice ks (0..3) and lane group lg (0..3) take scale group g = 4 ks + lg: with n = ks >> 1, qn = ks & 1,
+// qo = lg >> 1, lh = lg & 1, the 16 elements 128 n + 32 (2 qn + qo) + 16 lh + [0, 16), whose low 4 bits are nibble qn of
+// ql[64 n + 32 qo + 16 lh + i] and high 2 bits field 2 qn + qo of qh[32 n + 16 lh + i] (src/es_quant.c:158-176). The
+// activation operand is the natural 16-element chunk g of the activation row, as in the pre-pass planes.
+#include "es_hip_common.h"
+
+namespace esq {
+
+template <int RW, int TW, int WN, int NST> struct Mm6Geom {
+    static constexpr int NW = RW * TW, BM = 16 * RW, BN = 16 * WN * TW;
+    static constexpr int RB = 212;                                       // staged bytes per row
+    static constexpr int NWLW = (BM * 53 + 63) / 64;                     // dword wave-loads of weights (256 bytes each)
+    static constexpr int CX = BN * 18 + BN / 4, NWLX = (CX + 63) / 64;   // 16-byte activation chunks, their wave-loads
+    static constexpr int X_OFF = NWLW * 256, M_OFF = X_OFF + BN * 256, D_OFF = M_OFF + BN * 32;
+    static constexpr int STAGE = X_OFF + NWLX * 1024;
+    static constexpr int LW = (NWLW + NW - 1) / NW, LX = (NWLX + NW - 1) / NW, LOADS = LW + LX;   // per wave per stage
+    static constexpr int SINK = NST * STAGE, LDS = SINK + 1024;          // the stages and a sink for the spare loads
+    static constexpr int PER_TILE = (LOADS + WN - 1) / WN;               // loads issued with each activation tile
+    static_assert(NW == 8, "8 waves");
+    static_assert(NST >= 2 && LDS <= 160 * 1024, "stages fit the LDS");
+    static_assert(LOADS * (NST - 2) <= 63, "vmcnt range");
+};
+
+__device__ __forceinline__ uint4 lds_u128(const uint8_t *p) {   // 16 bytes at a 2-byte aligned LDS address
+    uint4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 16);
+    return v;
+}
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t *p) {
+    return *reinterpret_cast<const uint16_t *>(__builtin_assume_aligned(p, 2));
+}
+
+// RW x TW waves: RW along the rows, TW along the activations; WN: 16 x 16 MFMA tiles per wave along the activations;
+// NST: LDS stages. CONTRACT: the clang order (fused multiply-adds), else the gcc / scalar order.
+template <int RW, int TW, int WN, int NST, bool CONTRACT>
+__global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__restrict__ jobs, int njobs, MmJob single) {
+    using G = Mm6Geom<RW, TW, WN, NST>;
+    __shared__ __align__(16) uint8_t smem[G::LDS];
+
+    MmJob J;
+    if (jobs) J = jobs[find_mm_job(jobs, njobs, blockIdx.x)];
+    else J = single;
+    // XCD-aware tile order, as in the Q4_K kernel: all activation tiles of row tile rt on one XCD
+    const int tile = blockIdx.x - J.tile0;
+    const int x = tile & 7, kq = tile >> 3;
+    const int rt = x + 8 * (kq / J.ntok_tiles), tt = kq % J.ntok_tiles;
+    if (rt * G::BM >= J.r1 - J.r0) return;
+    const int row0 = J.r0 + rt * G::BM, tok0 = tt * G::BN;
+    const int nbk = J.cols / 256;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int wr = (wave % RW) * 16, wt = (wave / RW) * 16 * WN;   // this wave's rows / activations in the tile
+    const int lr = lane & 15, lg = lane >> 4;
+    const uint32_t lds0 = lds_addr(smem);
+
+    // ---- per-lane sources of this wave's stage loads. Weight wave-load L (dwords 64L .. 64L+63 of a stage): dword c is
+    // dword c % 53 of row c / 53's stretch, at row * row_bytes + 210b - 2(b & 1) + 4(c % 53) (rows past the end repeat
+    // the last one; their results are not stored). Activation wave-load L (16-byte chunks 64L ..): the three planes of
+    // one workspace allocation, base J.xq, + the plane stride per superblock.
+    const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
+    const uint32_t xm_rel = (uint32_t)(J.xm - J.xq), xd_rel = xm_rel + (uint32_t)nbk * J.na_pad * 32;
+    const int last_row = J.r1 - 1 - row0;
+    uint32_t offw[G::LW], offx[G::LX], stepx[G::LX];
+    bool livew[G::LW], livex[G::LX];
+#pragma unroll
+    for (int kk = 0; kk < G::LW; kk++) {
+        const int L = wave + G::NW * kk, c = 64 * L + lane;
+        livew[kk] = c < G::BM * 53;
+        offw[kk] = (uint32_t)min(c / 53, last_row) * (uint32_t)J.row_bytes + 4 * (c % 53);
+    }
+#pragma unroll
+    for (int kk = 0; kk < G::LX; kk++) {
+        const int L = wave + G::NW * kk, c = 64 * L + lane;
+        livex[kk] = c < G::CX;
+        if (c < G::BN * 16) {
+            const int t = c >> 4, q = (c & 15) ^ (t & 15);   // chunk q of activation t at slot q ^ (t & 15)
+            offx[kk] = (uint32_t)(tok0 + t) * 256 + 16 * q;
+            stepx[kk] = (uint32_t)J.na_pad * 256;
+        } else if (c < G::BN * 18) {
+            const int cm = c - G::BN * 16;
+            offx[kk] = xm_rel + (uint32_t)(tok0 + (cm >> 1)) * 32 + 16 * (cm & 1);
+            stepx[kk] = (uint32_t)J.na_pad * 32;
+        } else {
+            const int t4 = min(c - G::BN * 18, G::BN / 4 - 1);
+            offx[kk] = xd_rel + (uint32_t)(tok0 + 4 * t4) * 4;
+            stepx[kk] = (uint32_t)J.na_pad * 4;
+        }
+    }
+    const uint32_t offw0 = offw[0];   // a weight dword of row 0's stretch of superblock 0: the source of the spare loads
+    // load u (of LOADS) of superblock bi into stage st; every wave issues LOADS per stage (the spares go to the sink)
+    auto issue_unit = [&](int u, int st, int bi) {
+        const uint32_t base = lds0 + st * G::STAGE;
+        if (u < G::LW) {
+            const int L = wave + G::NW * u;
+            if (L < G::NWLW) {
+                if (livew[u]) load_lds4(wbase, offw[u] + 210u * bi - 2u * (bi & 1), base + 256 * L);
+            } else {
+                load_lds4(wbase, offw0, lds0 + G::SINK);
+            }
+        } else {
+            const int k = u - G::LW, L = wave + G::NW * k;
+            if (L < G::NWLX) {
+                if (livex[k]) load_lds16(J.xq, offx[k] + (uint32_t)bi * stepx[k], base + G::X_OFF + 1024 * L);
+            } else {
+                load_lds16(J.xq, 0, lds0 + G::SINK);
+            }
+        }
+    };
+
+    uint32_t xo[4];   // activation chunk offsets of this lane in a stage (tile c adds 4096*c): chunk 4ks + lg
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) xo[ks] = G::X_OFF + (wt + lr) * 256 + 16 * ((4 * ks + lg) ^ lr);
+    const uint32_t mo = G::M_OFF + (wt + lr) * 32 + 16 * (lg & 1), dof = G::D_OFF + (wt + lr) * 4;
+    const int qo = lg >> 1, lh = lg & 1;
+    const uint32_t rowoff = (wr + lr) * G::RB, ddoff = (wr + 4 * lg) * G::RB + 208;
+    const uint32_t sel = 0x0c000c00u + (uint32_t)lg * 0x00010001u;   // byte lg of a word into both 16-bit halves
+
+    float s[WN][4];
+#pragma unroll
+    for (int c = 0; c < WN; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[c][i] = 0.0f;
+
+#pragma unroll
+    for (int k = 0; k < NST - 1; k++)
+        if (k < nbk)
+#pragma unroll
+            for (int u = 0; u < G::LOADS; u++) issue_unit(u, k, k);
+    int st = 0;   // stage of superblock b
+    for (int b = 0; b < nbk; b++) {
+        wait_stages<G::LOADS, NST - 2>(min(NST - 2, nbk - 1 - b));   // this wave's loads of stage b are in LDS
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");           // this wave's reads of stage b-1 are done
+        __builtin_amdgcn_s_barrier();                                 // ... and every wave's loads and reads
+        asm volatile("" ::: "memory");
+        const uint8_t *wb = smem + st * G::STAGE;
+        const int sti = st == 0 ? NST - 1 : st - 1;   // stage of superblock b + NST - 1 (its loads go out with the tiles)
+        const bool more = b + NST - 1 < nbk;
+        st = st == NST - 1 ? 0 : st + 1;
+
+        // LDS reads in the order they are needed: the weight fields, the row scales, then activation tile 0
+        const uint8_t *rowp = wb + rowoff + 2 * (b & 1);
+        const uint4 ql0 = lds_u128(rowp + 32 * qo + 16 * lh), ql1 = lds_u128(rowp + 64 + 32 * qo + 16 * lh);
+        const uint4 qh0 = lds_u128(rowp + 128 + 16 * lh), qh1 = lds_u128(rowp + 160 + 16 * lh);
+        const uint4 scw = lds_u128(rowp + 192);
+        float dv[4];   // d of this lane's four output rows
+#pragma unroll
+        for (int i = 0; i < 4; i++) dv[i] = half_bits_to_float(lds_u16(wb + ddoff + 2 * (b & 1) + G::RB * i));
+        struct Bt { v4i x[4]; v8h m; float td; };
+        auto load_b = [&](int c, Bt &B) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) B.x[ks] = *reinterpret_cast<const v4i *>(wb + xo[ks] + 4096 * c);
+            B.m = *reinterpret_cast<const v8h *>(wb + mo + 512 * c);
+            B.td = *reinterpret_cast<const float *>(wb + dof + 64 * c);
+        };
+        Bt B[2];
+        load_b(0, B[0]);
+
+        // ---- A operands: per slice ks the four planes, and the scales as halves for corr
+        const uint32_t u[4] = {scw.x ^ 0x80808080u, scw.y ^ 0x80808080u, scw.z ^ 0x80808080u, scw.w ^ 0x80808080u};   // sc + 128
+        v4i p1[4], p2[4], p3[4], p4[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int n = ks >> 1, qn = ks & 1;
+            const uint32_t lsc = __builtin_amdgcn_perm(0, u[ks] & 0x0f0f0f0fu, sel);          // l, in both halves
+            const uint32_t hsc = __builtin_amdgcn_perm(0, (u[ks] >> 4) & 0x0f0f0f0fu, sel);   // h
+            const uint4 qlv = n ? ql1 : ql0, qhv = n ? qh1 : qh0;
+            const uint32_t qlw[4] = {qlv.x, qlv.y, qlv.z, qlv.w}, qhw[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+            const uint32_t shq = 4 * qn + 2 * qo;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t nib = qn ? (qlw[i] >> 4) & 0x0f0f0f0fu : qlw[i] & 0x0f0f0f0fu;
+                const uint32_t qu = nib | (((qhw[i] >> shq) & 0x03030303u) << 4);   // 6-bit codes, one per byte
+                const uint32_t a = (qu >> 3) & 0x07070707u, bb = qu & 0x07070707u;
+                // a h - q_u per byte: (a h + 128 - q_u) stays in 65..233, so no borrow crosses a byte
+                p1[ks][i] = (int)(((pk_mul_u16(a, hsc) | 0x80808080u) - qu) ^ 0x80808080u);
+                p2[ks][i] = (int)pk_mul_u16(a, lsc);
+                p3[ks][i] = (int)pk_mul_u16(bb, hsc);
+                p4[ks][i] = (int)pk_mul_u16(bb, lsc);
+            }
+        }
+        // corr operand (halves): lanes 0..15 carry sc_0..7, lanes 16..31 sc_8..15 (k positions meet bsums 0..7 / 8..15);
+        // lanes 32..63 zero. Each half is built as 1024 + sc_u (byte under the exponent of 1024), then 1152 subtracted.
+        v8h acorr;
+        {
+            const uint32_t w0 = lg == 0 ? u[0] : u[2], w1 = lg == 0 ? u[1] : u[3];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t k0 = (2 * e) & 3;
+                const uint32_t pr = __builtin_amdgcn_perm(0x64646464u, e < 2 ? w0 : w1,
+                                                          k0 | 0x0400u | (k0 + 1) << 16 | 0x04000000u);
+                const h2 v = __builtin_bit_cast(h2, pr) + __builtin_bit_cast(h2, 0xe480e480u);   // - 1152
+                acorr[2 * e] = v[0];
+                acorr[2 * e + 1] = v[1];
+            }
+            if (lg >= 2) acorr = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+
+        v4i d1[2], d2[2], d3[2], d4[2];
+        v4f dc[2];
+        float tdv[2];
+        auto mma = [&](int c, const Bt &Bc) {
+            const int w = c & 1;
+            tdv[w] = Bc.td;
+            dc[w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(acorr, Bc.m, v4f{0, 0, 0, 0}, 0, 0, 0);
+            d1[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p1[0], Bc.x[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            d2[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p2[0], Bc.x[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            d3[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p3[0], Bc.x[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            d4[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p4[0], Bc.x[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int ks = 1; ks < 4; ks++) {
+                d1[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p1[ks], Bc.x[ks], d1[w], 0, 0, 0);
+                d2[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p2[ks], Bc.x[ks], d2[w], 0, 0, 0);
+                d3[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p3[ks], Bc.x[ks], d3[w], 0, 0, 0);
+                d4[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p4[ks], Bc.x[ks], d4[w], 0, 0, 0);
+            }
+        };
+        // fp32 epilogue of superblock b for tile c, per (row, activation), in the reference's order
+        auto epi = [&](int c) {
+            const int w = c & 1;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tot = d4[w][i] + 8 * d2[w][i] + 16 * d3[w][i] + 128 * d1[w][i] - 32 * (int)dc[w][i];
+                const float f = tdv[w] * dv[i];
+                if constexpr (CONTRACT) s[c][i] = __builtin_fmaf(f, static_cast<float>(tot), s[c][i]);
+                else s[c][i] = s[c][i] + f * static_cast<float>(tot);
+            }
+        };
+        // one scheduling group per tile: the next superblock's loads, tile c+1's LDS reads, tile c's matrix work and tile
+        // c-1's epilogue, interleaved as 1 MFMA : 2 VALU (: 1 LDS read)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < WN; c++) {
+            if (more) {
+#pragma unroll
+                for (int uu = c * G::PER_TILE; uu < (c + 1) * G::PER_TILE; uu++)
+                    if (uu < G::LOADS) issue_unit(uu, sti, b + NST - 1);
+            }
+            if (c + 1 < WN) load_b(c + 1, B[(c + 1) & 1]);
+            mma(c, B[c & 1]);
+            if (c) epi(c - 1);
+#pragma unroll
+            for (int k = 0; k < 17; k++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+                if (k < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        epi(WN - 1);
+        asm volatile("" ::: "memory");   // stage b's LDS reads stay before the next superblock's barrier
+    }
+
+    // ---- outputs
+#pragma unroll
+    for (int c = 0; c < WN; c++) {
+        const int t = tok0 + wt + 16 * c + lr;
+        if (t >= J.na) continue;
+        const int r = row0 + wr + 4 * lg;   // this lane holds rows r .. r+3 of activation t
+        float *yp = J.y + (size_t)t * J.ystride + r;
+        if (r + 3 < J.r1 && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
+            stg<float4>(yp, make_float4(s[c][0], s[c][1], s[c][2], s[c][3]));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (r + i < J.r1) stg<float>(yp + i, s[c][i]);
+        }
+    }
+}
+
+template <int RW, int TW, int WN, int NST>
+static hipError_t mm6_launch_cfg(const MmJob *jobs, int njobs, const MmJob &single, int grid, int order, hipStream_t s) {
+    if (order == ES_HIP_ORDER_X86_CONTRACT)
+        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, NST, true>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
+    else
+        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, NST, false>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
+    return hipGetLastError();
+}
+
+// Q6_K workgroup tiles: 128 rows x 16, 32 or 64 activations on 8 waves (16 rows x all the activations each)
+bool mm6_tile_ok(int bm, int bn, int nw) { return nw == 8 && bm == 128 && (bn == 16 || bn == 32 || bn == 64); }
+
+hipError_t mm6_launch(int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
+                      hipStream_t s) {
+    if (nw == 8 && bm == 128) {
+        if (bn == 64) return mm6_launch_cfg<8, 1, 4, 3>(jobs, njobs, single, grid, order, s);
+        if (bn == 32) return mm6_launch_cfg<8, 1, 2, 4>(jobs, njobs, single, grid, order, s);
+        if (bn == 16) return mm6_launch_cfg<8, 1, 1, 5>(jobs, njobs, single, grid, order, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace esq

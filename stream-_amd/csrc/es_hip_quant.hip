@@ -236,6 +236,7 @@ int launch_single(const Group &g, hipStream_t s) {
 std::atomic<int> g_mm_min{8};    // activations per Q4_K product from which the prefill kernel is used (<= 0: never)
 std::atomic<int> g_mq_min{8};    // activations per K-quant product from which the small-batch kernel is used (<= 0: never)
 std::atomic<int> g_mb_min{2};    // activations per Q4_0/Q5_0 product from which the batched kernel is used (<= 0: never)
+std::atomic<int> g_mm6_min{16};  // activations per Q6_K product from which its matrix-core kernel is used (<= 0: never)
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
@@ -257,8 +258,8 @@ struct MqGroup {   // one small-batch matrix-core launch: products of one format
     size_t off = 0;
 };
 
-struct MmGroup {   // one matrix-core launch: products sharing a workgroup tile shape
-    int bm, bn, nw, grid = 0;
+struct MmGroup {   // one matrix-core launch: products of one format sharing a workgroup tile shape
+    int type, bm, bn, nw, grid = 0;
     std::vector<esq::MmJob> jobs;
     size_t off = 0;   // byte offset of the job table in the device image
 };
@@ -266,7 +267,7 @@ struct MmGroup {   // one matrix-core launch: products sharing a workgroup tile 
 struct Batch {
     std::vector<Group> mv;
     std::vector<Prep> preps;
-    std::vector<esq::MmJob> mm;   // xq / xm hold workspace offsets until bind(); copied into mmg by plan_batch
+    std::vector<std::pair<int, esq::MmJob>> mm;   // (type, job); xq / xm hold workspace offsets until bind(); copied into mmg
     std::vector<MmGroup> mmg;
     std::vector<MqGroup> mqg;
     std::vector<MbGroup> mbg;
@@ -281,8 +282,13 @@ struct Batch {
 std::atomic<int> g_mm_tile{0};   // forced tile for batches of >= 128 activations: bm | bn << 10 | waves << 20 (0: automatic)
 
 // Workgroup tile of a product: the largest (best operand reuse) that still gives every CU a workgroup.
-void mm_tile(const esq::MmJob &j, int &bm, int &bn, int &nw) {
+void mm_tile(int type, const esq::MmJob &j, int &bm, int &bn, int &nw) {
     nw = 8;
+    if (type == ES_HIP_Q6_K) {   // 128 rows x up to 64 activations
+        bm = 128;
+        bn = std::min(j.na_pad, 64);
+        return;
+    }
     if (j.na_pad < 128) {   // small batches: 128 rows x all the activations (16, 32 or 64)
         bm = 128;
         bn = j.na_pad;
@@ -303,8 +309,9 @@ void mm_tile(const esq::MmJob &j, int &bm, int &bn, int &nw) {
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 bool mm_eligible(const Req &q) {
-    const int mn = g_mm_min.load();
-    return q.type == ES_HIP_Q4_K && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
+    const int mn = q.type == ES_HIP_Q6_K ? g_mm6_min.load() : g_mm_min.load();
+    if (q.type == ES_HIP_Q6_K && (q.cols / 256) % 2) return false;   // rows must be 4-byte aligned
+    return (q.type == ES_HIP_Q4_K || q.type == ES_HIP_Q6_K) && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
 }
 
 bool mb_eligible(const Req &q) {
@@ -402,8 +409,8 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             }
             continue;
         }
-        const int na_pad = q.na <= 16 ? 16 : q.na <= 32 ? 32 : q.na <= 64 ? 64
-                                        : (q.na + esq::MM_NA_PAD - 1) / esq::MM_NA_PAD * esq::MM_NA_PAD;
+        const int pad = q.type == ES_HIP_Q6_K ? 64 : esq::MM_NA_PAD;
+        const int na_pad = q.na <= 16 ? 16 : q.na <= 32 ? 32 : q.na <= 64 ? 64 : (q.na + pad - 1) / pad * pad;
         const Prep *pp = &get_prep(bt, q, f, 2, na_pad);
         esq::MmJob j{};
         j.W = static_cast<const uint8_t *>(q.W);
@@ -417,18 +424,19 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         j.cols = q.cols;
         j.na = q.na;
         j.na_pad = na_pad;
-        bt.mm.push_back(j);
+        bt.mm.push_back({(int)q.type, j});
     }
     // one launch per tile shape; inside a launch the longest rows (most superblocks) come first, so the longest-running
     // workgroups start first
-    std::stable_sort(bt.mm.begin(), bt.mm.end(), [](const esq::MmJob &x, const esq::MmJob &y) { return x.cols > y.cols; });
-    for (esq::MmJob j : bt.mm) {
+    std::stable_sort(bt.mm.begin(), bt.mm.end(),
+                     [](const std::pair<int, esq::MmJob> &x, const std::pair<int, esq::MmJob> &y) { return x.second.cols > y.second.cols; });
+    for (auto [type, j] : bt.mm) {
         int bm, bn, nw;
-        mm_tile(j, bm, bn, nw);
+        mm_tile(type, j, bm, bn, nw);
         MmGroup *g = nullptr;
         for (MmGroup &x : bt.mmg)
-            if (x.bm == bm && x.bn == bn && x.nw == nw) g = &x;
-        if (!g) { bt.mmg.push_back(MmGroup{bm, bn, nw}); g = &bt.mmg.back(); }
+            if (x.type == type && x.bm == bm && x.bn == bn && x.nw == nw) g = &x;
+        if (!g) { bt.mmg.push_back(MmGroup{type, bm, bn, nw}); g = &bt.mmg.back(); }
         j.tile0 = g->grid;   // a multiple of 8: the kernel maps tiles to XCDs by id % 8
         j.ntok_tiles = j.na_pad / bn;
         const int row_tiles = (j.r1 - j.r0 + bm - 1) / bm;
@@ -517,7 +525,7 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
     }
     for (const MmGroup &g : bt.mmg) {
         const esq::MmJob *dj = tables ? reinterpret_cast<const esq::MmJob *>(tables + g.off) : nullptr;
-        if ((e = esq::mm_launch(ES_HIP_Q4_K, g.bm, g.bn, g.nw, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+        if ((e = esq::mm_launch(g.type, g.bm, g.bn, g.nw, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
             return hip_fail(e, "matrix-core launch");
     }
     for (const MbGroup &g : bt.mbg) {
@@ -779,6 +787,7 @@ int es_hip_set_mfma_tile(int bm, int bn, int waves) {
 }
 int es_hip_set_small_batch_min(int n) { return g_mq_min.exchange(n); }
 int es_hip_set_batched32_min(int n) { return g_mb_min.exchange(n); }
+int es_hip_set_q6k_mfma_min_batch(int n) { return g_mm6_min.exchange(n); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
