@@ -10,11 +10,10 @@
 // corr = sum_g sc_g * bsums_g goes through one f16 MFMA (scales and bsums are exact halves and every partial sum stays
 // below 2^24: exact).
 //
-// Weights: a 210-byte superblock starts 2-byte aligned, so each row's superblock b is staged by dword loads of the
-// 212-byte dword-aligned stretch that covers it (from byte 210b - 2(b & 1) of the row). Rows must be 4-byte aligned (an
-// even number of superblocks); the stretch then never leaves the row. The A fields are read at 2-byte aligned LDS
-// addresses (the hardware's unaligned LDS access).
-//
+// Weights: a 210-byte superblock starts 2-byte aligned. Each row's superblock is read with 16-byte loads at 2-byte aligned
+// addresses (the hardware's unaligned global access) and a 2-byte load of d, and written to LDS as an aligned 208-byte
+// row (ql | qh | scales) plus d in a separate array. Activations come through the same registers-to-LDS path, from the
+// pre-pass planes. Rows must be 4-byte aligned (an even number of superblocks).
 // K order: MFMA slice ks (0..3) and lane group lg (0..3) take scale group g = 4 ks + lg: with n = ks >> 1, qn = ks & 1,
 // qo = lg >> 1, lh = lg & 1, the 16 elements 128 n + 32 (2 qn + qo) + 16 lh + [0, 16), whose low 4 bits are nibble qn of
 // ql[64 n + 32 qo + 16 lh + i] and high 2 bits field 2 qn + qo of qh[32 n + 16 lh + i] (src/es_quant.c:158-176). The
@@ -23,35 +22,32 @@
 
 namespace esq {
 
-template <int RW, int TW, int WN, int NST> struct Mm6Geom {
-    static constexpr int NW = RW * TW, BM = 16 * RW, BN = 16 * WN * TW;
-    static constexpr int RB = 212;                                       // staged bytes per row
-    static constexpr int NWLW = (BM * 53 + 63) / 64;                     // dword wave-loads of weights (256 bytes each)
-    static constexpr int CX = BN * 18 + BN / 4, NWLX = (CX + 63) / 64;   // 16-byte activation chunks, their wave-loads
-    static constexpr int X_OFF = NWLW * 256, M_OFF = X_OFF + BN * 256, D_OFF = M_OFF + BN * 32;
-    static constexpr int STAGE = X_OFF + NWLX * 1024;
-    static constexpr int LW = (NWLW + NW - 1) / NW, LX = (NWLX + NW - 1) / NW, LOADS = LW + LX;   // per wave per stage
-    static constexpr int SINK = NST * STAGE, LDS = SINK + 1024;          // the stages and a sink for the spare loads
-    static constexpr int PER_TILE = (LOADS + WN - 1) / WN;               // loads issued with each activation tile
+template <int RW, int TW, int WN> struct Mm6Geom {
+    static constexpr int NW = RW * TW, NT = 64 * NW, BM = 16 * RW, BN = 16 * WN * TW;
+    // stage: weight rows BM x 208 (ql | qh | scales) | d BM x 2 | activations BN x 256 | bsums BN x 32 | scales BN x 4
+    static constexpr int CW = BM * 13, CX = BN * 18 + BN / 4;          // 16-byte chunks
+    static constexpr int D_W = BM * 208, X_OFF = D_W + (BM * 2 + 15) / 16 * 16;
+    static constexpr int M_OFF = X_OFF + BN * 256, D_OFF = M_OFF + BN * 32, STAGE = D_OFF + (BN * 4 + 15) / 16 * 16;
+    static constexpr int SW = (CW + NT - 1) / NT, SX = (CX + NT - 1) / NT;   // chunks per thread
+    static constexpr int LDS = 2 * STAGE;
     static_assert(NW == 8, "8 waves");
-    static_assert(NST >= 2 && LDS <= 160 * 1024, "stages fit the LDS");
-    static_assert(LOADS * (NST - 2) <= 63, "vmcnt range");
+    static_assert(LDS <= 160 * 1024, "two stages fit the LDS");
+    static_assert(BM <= NT, "one d per thread");
 };
 
-__device__ __forceinline__ uint4 lds_u128(const uint8_t *p) {   // 16 bytes at a 2-byte aligned LDS address
-    uint4 v;
-    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 16);
-    return v;
-}
-__device__ __forceinline__ uint32_t lds_u16(const uint8_t *p) {
-    return *reinterpret_cast<const uint16_t *>(__builtin_assume_aligned(p, 2));
+// 16 bytes of global memory at a 2-byte aligned address
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+__device__ __forceinline__ uint4 ldg_u128_a2(const uint8_t *p) {
+    const u32x4_a2 v = *(const ESQ_GLOBAL u32x4_a2 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// RW x TW waves: RW along the rows, TW along the activations; WN: 16 x 16 MFMA tiles per wave along the activations;
-// NST: LDS stages. CONTRACT: the clang order (fused multiply-adds), else the gcc / scalar order.
-template <int RW, int TW, int WN, int NST, bool CONTRACT>
+
+// RW x TW waves: RW along the rows, TW along the activations; WN: 16 x 16 MFMA tiles per wave along the activations.
+// CONTRACT: the clang order (fused multiply-adds), else the gcc / scalar order.
+template <int RW, int TW, int WN, bool CONTRACT>
 __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__restrict__ jobs, int njobs, MmJob single) {
-    using G = Mm6Geom<RW, TW, WN, NST>;
+    using G = Mm6Geom<RW, TW, WN>;
     __shared__ __align__(16) uint8_t smem[G::LDS];
 
     MmJob J;
@@ -64,63 +60,69 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
     if (rt * G::BM >= J.r1 - J.r0) return;
     const int row0 = J.r0 + rt * G::BM, tok0 = tt * G::BN;
     const int nbk = J.cols / 256;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wr = (wave % RW) * 16, wt = (wave / RW) * 16 * WN;   // this wave's rows / activations in the tile
     const int lr = lane & 15, lg = lane >> 4;
-    const uint32_t lds0 = lds_addr(smem);
 
-    // ---- per-lane sources of this wave's stage loads. Weight wave-load L (dwords 64L .. 64L+63 of a stage): dword c is
-    // dword c % 53 of row c / 53's stretch, at row * row_bytes + 210b - 2(b & 1) + 4(c % 53) (rows past the end repeat
-    // the last one; their results are not stored). Activation wave-load L (16-byte chunks 64L ..): the three planes of
-    // one workspace allocation, base J.xq, + the plane stride per superblock.
+    // ---- this thread's share of a stage: weight chunk c = tid + NT*k (row c / 13, 16-byte piece c % 13 of its first 208
+    // bytes; rows past the end repeat the last one, their results are not stored), d of row tid, activation chunk
+    // tid + NT*k (values, swizzled: chunk q of activation t at slot q ^ (t & 15); bsums; scales, four activations a chunk)
     const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
-    const uint32_t xm_rel = (uint32_t)(J.xm - J.xq), xd_rel = xm_rel + (uint32_t)nbk * J.na_pad * 32;
     const int last_row = J.r1 - 1 - row0;
-    uint32_t offw[G::LW], offx[G::LX], stepx[G::LX];
-    bool livew[G::LW], livex[G::LX];
+    uint32_t wsrc[G::SW], wdst[G::SW], xsrc[G::SX], xstep[G::SX], xdst[G::SX];
+    bool wok[G::SW], xok[G::SX];
 #pragma unroll
-    for (int kk = 0; kk < G::LW; kk++) {
-        const int L = wave + G::NW * kk, c = 64 * L + lane;
-        livew[kk] = c < G::BM * 53;
-        offw[kk] = (uint32_t)min(c / 53, last_row) * (uint32_t)J.row_bytes + 4 * (c % 53);
+    for (int k = 0; k < G::SW; k++) {
+        const int c = tid + G::NT * k;
+        wok[k] = c < G::CW;
+        wsrc[k] = (uint32_t)min(c / 13, last_row) * (uint32_t)J.row_bytes + 16 * (c % 13);
+        wdst[k] = 16 * c;
     }
+    const bool dok = tid < G::BM;
+    const uint32_t dsrc = (uint32_t)min(tid, last_row) * (uint32_t)J.row_bytes + 208;
+    const uint32_t xm_rel = (uint32_t)(J.xm - J.xq), xd_rel = xm_rel + (uint32_t)nbk * J.na_pad * 32;
 #pragma unroll
-    for (int kk = 0; kk < G::LX; kk++) {
-        const int L = wave + G::NW * kk, c = 64 * L + lane;
-        livex[kk] = c < G::CX;
+    for (int k = 0; k < G::SX; k++) {
+        const int c = tid + G::NT * k;
+        xok[k] = c < G::CX;
         if (c < G::BN * 16) {
-            const int t = c >> 4, q = (c & 15) ^ (t & 15);   // chunk q of activation t at slot q ^ (t & 15)
-            offx[kk] = (uint32_t)(tok0 + t) * 256 + 16 * q;
-            stepx[kk] = (uint32_t)J.na_pad * 256;
+            const int t = c >> 4, q = c & 15;
+            xsrc[k] = (uint32_t)(tok0 + t) * 256 + 16 * q;
+            xstep[k] = (uint32_t)J.na_pad * 256;
+            xdst[k] = G::X_OFF + t * 256 + 16 * (q ^ (t & 15));
         } else if (c < G::BN * 18) {
             const int cm = c - G::BN * 16;
-            offx[kk] = xm_rel + (uint32_t)(tok0 + (cm >> 1)) * 32 + 16 * (cm & 1);
-            stepx[kk] = (uint32_t)J.na_pad * 32;
+            xsrc[k] = xm_rel + (uint32_t)(tok0 + (cm >> 1)) * 32 + 16 * (cm & 1);
+            xstep[k] = (uint32_t)J.na_pad * 32;
+            xdst[k] = G::M_OFF + 16 * cm;
         } else {
             const int t4 = min(c - G::BN * 18, G::BN / 4 - 1);
-            offx[kk] = xd_rel + (uint32_t)(tok0 + 4 * t4) * 4;
-            stepx[kk] = (uint32_t)J.na_pad * 4;
+            xsrc[k] = xd_rel + (uint32_t)(tok0 + 4 * t4) * 4;
+            xstep[k] = (uint32_t)J.na_pad * 4;
+            xdst[k] = G::D_OFF + 16 * t4;
         }
     }
-    const uint32_t offw0 = offw[0];   // a weight dword of row 0's stretch of superblock 0: the source of the spare loads
-    // load u (of LOADS) of superblock bi into stage st; every wave issues LOADS per stage (the spares go to the sink)
-    auto issue_unit = [&](int u, int st, int bi) {
-        const uint32_t base = lds0 + st * G::STAGE;
-        if (u < G::LW) {
-            const int L = wave + G::NW * u;
-            if (L < G::NWLW) {
-                if (livew[u]) load_lds4(wbase, offw[u] + 210u * bi - 2u * (bi & 1), base + 256 * L);
-            } else {
-                load_lds4(wbase, offw0, lds0 + G::SINK);
-            }
-        } else {
-            const int k = u - G::LW, L = wave + G::NW * k;
-            if (L < G::NWLX) {
-                if (livex[k]) load_lds16(J.xq, offx[k] + (uint32_t)bi * stepx[k], base + G::X_OFF + 1024 * L);
-            } else {
-                load_lds16(J.xq, 0, lds0 + G::SINK);
-            }
-        }
+    // the global loads of superblock bi into registers, and their LDS writes into stage st
+    uint4 rw[G::SW], rx[G::SX];
+    uint32_t rd = 0;
+    auto gload = [&](int bi) {
+#pragma unroll
+        for (int k = 0; k < G::SW; k++)
+            if (wok[k]) rw[k] = ldg_u128_a2(wbase + 210u * bi + wsrc[k]);
+        if (dok) rd = ldg<uint16_t>(wbase + 210u * bi + dsrc);
+#pragma unroll
+        for (int k = 0; k < G::SX; k++)
+            if (xok[k]) rx[k] = ldg<uint4>(J.xq + xsrc[k] + (uint32_t)bi * xstep[k]);
+    };
+    auto lstore = [&](int st) {
+        uint8_t *sb = smem + st * G::STAGE;
+#pragma unroll
+        for (int k = 0; k < G::SW; k++)
+            if (wok[k]) *reinterpret_cast<uint4 *>(sb + wdst[k]) = rw[k];
+        if (dok) *reinterpret_cast<uint16_t *>(sb + G::D_W + 2 * tid) = (uint16_t)rd;
+#pragma unroll
+        for (int k = 0; k < G::SX; k++)
+            if (xok[k]) *reinterpret_cast<uint4 *>(sb + xdst[k]) = rx[k];
     };
 
     uint32_t xo[4];   // activation chunk offsets of this lane in a stage (tile c adds 4096*c): chunk 4ks + lg
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
     for (int ks = 0; ks < 4; ks++) xo[ks] = G::X_OFF + (wt + lr) * 256 + 16 * ((4 * ks + lg) ^ lr);
     const uint32_t mo = G::M_OFF + (wt + lr) * 32 + 16 * (lg & 1), dof = G::D_OFF + (wt + lr) * 4;
     const int qo = lg >> 1, lh = lg & 1;
-    const uint32_t rowoff = (wr + lr) * G::RB, ddoff = (wr + 4 * lg) * G::RB + 208;
+    const uint32_t rowoff = (wr + lr) * 208, ddoff = G::D_W + (wr + 4 * lg) * 2;
     const uint32_t sel = 0x0c000c00u + (uint32_t)lg * 0x00010001u;   // byte lg of a word into both 16-bit halves
 
     float s[WN][4];
@@ -137,30 +139,30 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
 #pragma unroll
         for (int i = 0; i < 4; i++) s[c][i] = 0.0f;
 
-#pragma unroll
-    for (int k = 0; k < NST - 1; k++)
-        if (k < nbk)
-#pragma unroll
-            for (int u = 0; u < G::LOADS; u++) issue_unit(u, k, k);
-    int st = 0;   // stage of superblock b
+    // Two stages. Superblock b+1's loads went out during superblock b-1 (into registers); at the top of b they are written
+    // to stage (b+1) & 1, whose last readers finished b-1 (barrier), and superblock b+2's loads go out.
+    gload(0);
+    lstore(0);
+    if (nbk > 1) gload(1);
     for (int b = 0; b < nbk; b++) {
-        wait_stages<G::LOADS, NST - 2>(min(NST - 2, nbk - 1 - b));   // this wave's loads of stage b are in LDS
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");           // this wave's reads of stage b-1 are done
-        __builtin_amdgcn_s_barrier();                                 // ... and every wave's loads and reads
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's LDS writes of stage b and reads of b-1 are done
+        __builtin_amdgcn_s_barrier();                         // ... and every wave's
         asm volatile("" ::: "memory");
-        const uint8_t *wb = smem + st * G::STAGE;
-        const int sti = st == 0 ? NST - 1 : st - 1;   // stage of superblock b + NST - 1 (its loads go out with the tiles)
-        const bool more = b + NST - 1 < nbk;
-        st = st == NST - 1 ? 0 : st + 1;
+        const uint8_t *wb = smem + (b & 1) * G::STAGE;
+        if (b + 1 < nbk) {
+            lstore((b + 1) & 1);
+            if (b + 2 < nbk) gload(b + 2);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // the loads stay here, a whole superblock ahead of their LDS writes
 
         // LDS reads in the order they are needed: the weight fields, the row scales, then activation tile 0
-        const uint8_t *rowp = wb + rowoff + 2 * (b & 1);
-        const uint4 ql0 = lds_u128(rowp + 32 * qo + 16 * lh), ql1 = lds_u128(rowp + 64 + 32 * qo + 16 * lh);
-        const uint4 qh0 = lds_u128(rowp + 128 + 16 * lh), qh1 = lds_u128(rowp + 160 + 16 * lh);
-        const uint4 scw = lds_u128(rowp + 192);
+        const uint8_t *rowp = wb + rowoff;
+        auto ld16 = [&](int off) { return *reinterpret_cast<const uint4 *>(rowp + off); };
+        const uint4 ql0 = ld16(32 * qo + 16 * lh), ql1 = ld16(64 + 32 * qo + 16 * lh);
+        const uint4 qh0 = ld16(128 + 16 * lh), qh1 = ld16(160 + 16 * lh), scw = ld16(192);
         float dv[4];   // d of this lane's four output rows
 #pragma unroll
-        for (int i = 0; i < 4; i++) dv[i] = half_bits_to_float(lds_u16(wb + ddoff + 2 * (b & 1) + G::RB * i));
+        for (int i = 0; i < 4; i++) dv[i] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(wb + ddoff + 2 * i));
         struct Bt { v4i x[4]; v8h m; float td; };
         auto load_b = [&](int c, Bt &B) {
 #pragma unroll
@@ -241,16 +243,11 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
                 else s[c][i] = s[c][i] + f * static_cast<float>(tot);
             }
         };
-        // one scheduling group per tile: the next superblock's loads, tile c+1's LDS reads, tile c's matrix work and tile
-        // c-1's epilogue, interleaved as 1 MFMA : 2 VALU (: 1 LDS read)
+        // one scheduling group per tile: tile c+1's LDS reads, tile c's matrix work and tile c-1's epilogue, interleaved as
+        // 1 MFMA : 2 VALU (: 1 LDS read)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < WN; c++) {
-            if (more) {
-#pragma unroll
-                for (int uu = c * G::PER_TILE; uu < (c + 1) * G::PER_TILE; uu++)
-                    if (uu < G::LOADS) issue_unit(uu, sti, b + NST - 1);
-            }
             if (c + 1 < WN) load_b(c + 1, B[(c + 1) & 1]);
             mma(c, B[c & 1]);
             if (c) epi(c - 1);
@@ -283,12 +280,12 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
     }
 }
 
-template <int RW, int TW, int WN, int NST>
+template <int RW, int TW, int WN>
 static hipError_t mm6_launch_cfg(const MmJob *jobs, int njobs, const MmJob &single, int grid, int order, hipStream_t s) {
     if (order == ES_HIP_ORDER_X86_CONTRACT)
-        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, NST, true>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
+        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, true>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
     else
-        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, NST, false>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
+        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, false>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
     return hipGetLastError();
 }
 
@@ -298,9 +295,9 @@ bool mm6_tile_ok(int bm, int bn, int nw) { return nw == 8 && bm == 128 && (bn ==
 hipError_t mm6_launch(int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                       hipStream_t s) {
     if (nw == 8 && bm == 128) {
-        if (bn == 64) return mm6_launch_cfg<8, 1, 4, 3>(jobs, njobs, single, grid, order, s);
-        if (bn == 32) return mm6_launch_cfg<8, 1, 2, 4>(jobs, njobs, single, grid, order, s);
-        if (bn == 16) return mm6_launch_cfg<8, 1, 1, 5>(jobs, njobs, single, grid, order, s);
+        if (bn == 64) return mm6_launch_cfg<8, 1, 4>(jobs, njobs, single, grid, order, s);
+        if (bn == 32) return mm6_launch_cfg<8, 1, 2>(jobs, njobs, single, grid, order, s);
+        if (bn == 16) return mm6_launch_cfg<8, 1, 1>(jobs, njobs, single, grid, order, s);
     }
     return hipErrorInvalidValue;
 }
