@@ -34,6 +34,7 @@ INT8_PEAK_TOPS = 5000.0
 
 Q80 = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])
 Q8K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+SETTLE_S = 0.3   # untimed runs before each workload's warmup steps: the GPU leaves its idle clocks
 SCALE_POS = {E.Q4_0: (0, None), E.Q5_0: (0, None), E.Q4_K: (0, 2), E.Q6_K: (208, None), E.Q2_K: (80, 82)}
 
 
@@ -100,7 +101,13 @@ class Workload:
         return {m[0] for m in mats}   # one launch per format
 
     def time(self, warmup, steps):
-        """(wall ms per step, event ms per step): events on the launch stream around `steps` back-to-back runs"""
+        """(wall ms per step, event ms per step): events on the launch stream around `steps` back-to-back runs, after
+        SETTLE_S seconds of untimed runs (so the clocks have left idle) and `warmup` more"""
+        t_end = time.perf_counter() + SETTLE_S
+        while time.perf_counter() < t_end:
+            for _ in range(10):
+                self.plan.run()
+            self.lib.synchronize()
         for _ in range(warmup):
             self.plan.run()
         self.lib.synchronize()
@@ -179,7 +186,10 @@ class MoeWorkload:
         self.copies, self.distinct = copies, len(used)
 
     def time(self, warmup, steps):
-        """ms per copy (one layer)"""
+        """ms per copy (one layer), after SETTLE_S seconds of untimed steps"""
+        t_end = time.perf_counter() + SETTLE_S
+        while time.perf_counter() < t_end:
+            self.lib.step_time_ms(self.plans, self.moe, 0, 2)
         return self.lib.step_time_ms(self.plans, self.moe, warmup, steps) / self.copies
 
     def close(self):

@@ -196,6 +196,9 @@ int es_hip_set_batched32_min(int n);
 /* Q6_K products with at least n activations (and an even number of superblocks per row) run on the Q6_K matrix-core
  * kernel (default 16). */
 int es_hip_set_q6k_mfma_min_batch(int n);
+/* Q2_K products with at least n activations run on the Q2_K LDS-staged matrix-core kernel (default 2); below that, or
+ * with it off, the small-batch kernel (es_hip_set_small_batch_min) or the vector kernel. */
+int es_hip_set_q2k_mfma_min_batch(int n);
 /* The MoE SwiGLU alone on n device floats: h[i] = g[i] / (1 + expf(-g[i])) * u[i] as src/es_engine.c:913 computes it. */
 int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream);
 /* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`

@@ -91,6 +91,9 @@ bool mm_tile_ok(int bm, int bn, int nw);   // a workgroup tile (rows x activatio
 // The Q6_K form (es_hip_mm6.hip): tiles of 128 rows x 16, 32 or 64 activations on 8 waves
 hipError_t mm6_launch(int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                       hipStream_t s);
+// The Q2_K form (es_hip_mm2.hip): tiles of 128 rows x 16, 32 or 64 activations on 8 waves
+hipError_t mm2_launch(int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
+                      hipStream_t s);
 
 // The small-batch matrix-core form (es_hip_mq.hip): rows [r0, r1) against activations [t0, t0 + 16*wn) of na (at most
 // 64 per job), from pre-pass planes padded to na_pad activations. One workgroup per 64 rows.

@@ -237,6 +237,7 @@ std::atomic<int> g_mm_min{8};    // activations per Q4_K product from which the 
 std::atomic<int> g_mq_min{8};    // activations per K-quant product from which the small-batch kernel is used (<= 0: never)
 std::atomic<int> g_mb_min{2};    // activations per Q4_0/Q5_0 product from which the batched kernel is used (<= 0: never)
 std::atomic<int> g_mm6_min{16};  // activations per Q6_K product from which its matrix-core kernel is used (<= 0: never)
+std::atomic<int> g_mm2_min{2};   // activations per Q2_K product from which its LDS-staged matrix-core kernel is used
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
@@ -284,7 +285,7 @@ std::atomic<int> g_mm_tile{0};   // forced tile for batches of >= 128 activation
 // Workgroup tile of a product: the largest (best operand reuse) that still gives every CU a workgroup.
 void mm_tile(int type, const esq::MmJob &j, int &bm, int &bn, int &nw) {
     nw = 8;
-    if (type == ES_HIP_Q6_K) {   // 128 rows x up to 64 activations
+    if (type == ES_HIP_Q6_K || type == ES_HIP_Q2_K) {   // 128 rows x up to 64 activations (Q2_K: at least 32)
         bm = 128;
         bn = std::min(j.na_pad, 64);
         return;
@@ -309,9 +310,10 @@ void mm_tile(int type, const esq::MmJob &j, int &bm, int &bn, int &nw) {
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 bool mm_eligible(const Req &q) {
-    const int mn = q.type == ES_HIP_Q6_K ? g_mm6_min.load() : g_mm_min.load();
+    const int mn = q.type == ES_HIP_Q6_K ? g_mm6_min.load() : q.type == ES_HIP_Q2_K ? g_mm2_min.load() : g_mm_min.load();
     if (q.type == ES_HIP_Q6_K && (q.cols / 256) % 2) return false;   // rows must be 4-byte aligned
-    return (q.type == ES_HIP_Q4_K || q.type == ES_HIP_Q6_K) && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
+    return (q.type == ES_HIP_Q4_K || q.type == ES_HIP_Q6_K || q.type == ES_HIP_Q2_K) && mn > 0 && q.na >= mn && !q.ints &&
+           q.r1 > q.r0;
 }
 
 bool mb_eligible(const Req &q) {
@@ -409,8 +411,9 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             }
             continue;
         }
-        const int pad = q.type == ES_HIP_Q6_K ? 64 : esq::MM_NA_PAD;
-        const int na_pad = q.na <= 16 ? 16 : q.na <= 32 ? 32 : q.na <= 64 ? 64 : (q.na + pad - 1) / pad * pad;
+        const int pad = q.type == ES_HIP_Q4_K ? esq::MM_NA_PAD : 64;
+        // Q2_K batches of up to 32 share one 32-wide tile: few launches for MoE experts of any size
+        const int na_pad = q.na <= 16 && q.type != ES_HIP_Q2_K ? 16 : q.na <= 32 ? 32 : q.na <= 64 ? 64 : (q.na + pad - 1) / pad * pad;
         const Prep *pp = &get_prep(bt, q, f, 2, na_pad);
         esq::MmJob j{};
         j.W = static_cast<const uint8_t *>(q.W);
@@ -788,6 +791,7 @@ int es_hip_set_mfma_tile(int bm, int bn, int waves) {
 int es_hip_set_small_batch_min(int n) { return g_mq_min.exchange(n); }
 int es_hip_set_batched32_min(int n) { return g_mb_min.exchange(n); }
 int es_hip_set_q6k_mfma_min_batch(int n) { return g_mm6_min.exchange(n); }
+int es_hip_set_q2k_mfma_min_batch(int n) { return g_mm2_min.exchange(n); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
