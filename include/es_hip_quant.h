@@ -193,6 +193,9 @@ int es_hip_set_mfma_tile(int bm, int bn, int waves);
 /* Q4_0 / Q5_0 products with at least n activations run on the batched kernel (one lane per row and activation) instead of
  * the vector kernel (default 2). */
 int es_hip_set_batched32_min(int n);
+/* Of those, products with at least n activations run on the batched matrix-core kernel (one int8 MFMA per block forms the
+ * eight AVX2 lane sums of 4 rows x 32 activations; default 2); the others on the one-lane-per-output kernel. */
+int es_hip_set_batched32_mfma_min(int n);
 /* Q6_K products with at least n activations (and an even number of superblocks per row) run on the Q6_K matrix-core
  * kernel (default 16). */
 int es_hip_set_q6k_mfma_min_batch(int n);

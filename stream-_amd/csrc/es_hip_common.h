@@ -56,6 +56,9 @@ struct MbJob {
     int tile0, pad_;
 };
 hipError_t mb32_launch(int type, const MbJob *jobs, int njobs, const MbJob &single, int grid, int order, hipStream_t s);
+// The same products on the matrix cores (es_hip_mb.hip): workgroups of 16 rows x activations [t0, t0 + 32).
+constexpr int MB32M_ROWS = 16, MB32M_TOKENS = 32;
+hipError_t mb32m_launch(int type, const MbJob *jobs, int njobs, const MbJob &single, int grid, int order, hipStream_t s);
 
 // The batched (matrix-core) form: rows [r0, r1) against na activations that a pre-pass has re-laid out as
 // xq[nbk][na_pad][256] int8 values, then (at xm, in the same allocation) xm[nbk][na_pad][16 or 32] meta and
@@ -192,7 +195,15 @@ __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
 }
 
-__device__ __forceinline__ int find_mm_job(const MmJob *jobs, int njobs, int bid) {
+// The job of workgroup bid in a launch whose jobs hold consecutive tile ranges from tile0 (the last job with
+// tile0 <= bid). When the jobs are of equal size (an MoE layer's experts, copies of one matrix) the proportional guess
+// is that job, found in one round trip (its two bounds are independent loads); otherwise a binary search follows.
+template <typename JobT> __device__ __forceinline__ int find_tile_job(const JobT *jobs, int njobs, int bid) {
+    {
+        const int g = min(njobs - 1, static_cast<int>((static_cast<long>(bid) * njobs) / static_cast<long>(gridDim.x)));
+        const int a = jobs[g].tile0, b = g + 1 < njobs ? jobs[g + 1].tile0 : 0x7fffffff;
+        if (a <= bid && bid < b) return g;
+    }
     int lo = 0, hi = njobs - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;

@@ -32,15 +32,6 @@ __device__ __forceinline__ uint4 ld16a4(const uint8_t *p) {
 template <int N> struct IC { static constexpr int value = N; };
 __device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 
-__device__ __forceinline__ int find_mq_job(const MqJob *jobs, int njobs, int bid) {
-    int lo = 0, hi = njobs - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (jobs[mid].tile0 <= bid) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-}
-
 // ---- per-format superblock work ---------------------------------------------------------------------------------------
 // Raw: the bytes a lane loads for its row; A: the lane's A operands; then per activation tile the integers and the chain.
 template <int F> struct Mq;
@@ -151,7 +142,7 @@ template <int F, int WN, bool CONTRACT>
 __global__ __launch_bounds__(256, 2) void mq_kernel(const MqJob *__restrict__ jobs, int njobs, MqJob single) {
     using M = Mq<F>;
     MqJob J;
-    if (jobs) J = jobs[find_mq_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
     else J = single;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int lr = lane & 15, lg = lane >> 4;

@@ -313,15 +313,6 @@ template <int F> constexpr bool is32() { return F == ES_HIP_Q4_0 || F == ES_HIP_
 // ---------------------------------------------------------------------------------------------------------------------
 // The kernel
 
-template <typename JobT> __device__ __forceinline__ int find_job(const JobT *jobs, int njobs, int bid) {
-    int lo = 0, hi = njobs - 1;   // last job with tile0 <= bid
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (jobs[mid].tile0 <= bid) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-}
-
 // W waves per workgroup. A row of nbk blocks is cut into seg = ceil(nbk / slots) segments of `slots` blocks, one wave
 // each, so every lane keeps one fixed block position and its activation slice stays in registers; when seg < W the
 // W / seg wave groups take different rows. All waves write their blocks' float terms to the workgroup's LDS, then the
@@ -337,7 +328,7 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
     constexpr int U = ESQ_UNITS;   // row passes whose raw loads a wave issues before using any of them
 
     MvJob J;
-    if (jobs) J = jobs[find_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
     else J = single;
     const int nbk = J.cols / BE;
     const int tile = blockIdx.x - J.tile0;
@@ -536,7 +527,7 @@ __global__ __launch_bounds__(256) void mb32_kernel(const MbJob *__restrict__ job
     using L = Lane32<F>;
     constexpr int BB = Fmt<F>::BB, AB = Fmt<F>::AB;
     MbJob J;
-    if (jobs) J = jobs[find_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
     else J = single;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rows_per_wave = 64 / J.ta;

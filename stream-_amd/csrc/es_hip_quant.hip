@@ -103,6 +103,9 @@ constexpr size_t LDS_TARGET = 32 * 1024;   // bytes of chain terms per workgroup
 constexpr size_t LDS_MAX = 160 * 1024;      // gfx950 LDS per workgroup
 constexpr size_t TARGET_WG = 8192;          // workgroups a launch aims for (256 CUs x 8 resident 4-wave groups x 4)
 constexpr int MIN_ITERS = 4;                // row passes per workgroup at least (one pipelined load group)
+constexpr size_t MIN_WG_BLOCKS = 512;       // blocks per workgroup at least: a workgroup's set-up (job lookup, gathered
+                                            // activation loads) is a chain of dependent loads that small launches (an
+                                            // MoE layer's experts at a few tokens each) would otherwise repeat per 24 rows
 
 struct Group {
     MvLaunch L{};
@@ -168,7 +171,7 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
     }
     // workgroups of about total/TARGET_WG blocks each, each wave making at least MIN_ITERS row passes, so one launch keeps
     // every CU busy whether it holds one matrix or a hundred
-    const size_t wg_blocks = std::max<size_t>(1, total_blocks / TARGET_WG);
+    const size_t wg_blocks = std::max<size_t>(MIN_WG_BLOCKS, total_blocks / TARGET_WG);
     for (auto &kv : by_kind) {
         FmtInfo f;
         fmt_info(kv.first.first, f);
@@ -236,6 +239,7 @@ int launch_single(const Group &g, hipStream_t s) {
 std::atomic<int> g_mm_min{8};    // activations per Q4_K product from which the prefill kernel is used (<= 0: never)
 std::atomic<int> g_mq_min{8};    // activations per K-quant product from which the small-batch kernel is used (<= 0: never)
 std::atomic<int> g_mb_min{2};    // activations per Q4_0/Q5_0 product from which the batched kernel is used (<= 0: never)
+std::atomic<int> g_mbm_min{2};   // ... and from which that batched kernel is the matrix-core one (<= 0: never)
 std::atomic<int> g_mm6_min{16};  // activations per Q6_K product from which its matrix-core kernel is used (<= 0: never)
 std::atomic<int> g_mm2_min{2};   // activations per Q2_K product from which its LDS-staged matrix-core kernel is used
 
@@ -247,8 +251,10 @@ struct Prep {   // one activation pre-pass (shared by products that read the sam
     size_t xq_off, xm_off;
 };
 
-struct MbGroup {   // one batched 32-wide launch: products of one format
-    int type, grid = 0;
+struct MbGroup {   // one batched 32-wide launch: products of one format on one of the two kernels
+    int type;
+    bool mfma;
+    int grid = 0;
     std::vector<esq::MbJob> jobs;
     size_t off = 0;
 };
@@ -351,14 +357,18 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
         if (int rc = check_req(q, f)) return rc;
         if (mb_eligible(q)) {   // batched 32-wide: activation groups of at most 64
+            const int mm = g_mbm_min.load();
+            const bool mfma = mm > 0 && q.na >= mm;
             MbGroup *g = nullptr;
             for (MbGroup &x : bt.mbg)
-                if (x.type == (int)q.type) g = &x;
-            if (!g) { bt.mbg.push_back(MbGroup{(int)q.type}); g = &bt.mbg.back(); }
+                if (x.type == (int)q.type && x.mfma == mfma) g = &x;
+            if (!g) { bt.mbg.push_back(MbGroup{(int)q.type, mfma}); g = &bt.mbg.back(); }
             const int nbk32 = q.cols / 32;
-            for (int t0 = 0; t0 < q.na; t0 += 64) {
+            const int tstep = mfma ? esq::MB32M_TOKENS : 64;
+            for (int t0 = 0; t0 < q.na; t0 += tstep) {
                 int ta = 1;
                 while (ta < std::min(64, q.na - t0)) ta <<= 1;
+                if (mfma) ta = esq::MB32M_TOKENS;
                 esq::MbJob j{};
                 j.W = static_cast<const uint8_t *>(q.W);
                 j.act = static_cast<const uint8_t *>(q.act);
@@ -374,7 +384,7 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
                 j.t0 = t0;
                 j.ta = ta;
                 j.tile0 = g->grid;
-                const int rows_per_wg = 4 * (64 / ta);
+                const int rows_per_wg = mfma ? esq::MB32M_ROWS : 4 * (64 / ta);
                 g->grid += (q.r1 - q.r0 + rows_per_wg - 1) / rows_per_wg;
                 g->jobs.push_back(j);
             }
@@ -533,7 +543,8 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
     }
     for (const MbGroup &g : bt.mbg) {
         const esq::MbJob *dj = tables ? reinterpret_cast<const esq::MbJob *>(tables + g.off) : nullptr;
-        if ((e = esq::mb32_launch(g.type, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+        if ((e = (g.mfma ? esq::mb32m_launch : esq::mb32_launch)(g.type, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) !=
+            hipSuccess)
             return hip_fail(e, "batched launch");
     }
     for (const MqGroup &g : bt.mqg) {
@@ -790,6 +801,7 @@ int es_hip_set_mfma_tile(int bm, int bn, int waves) {
 }
 int es_hip_set_small_batch_min(int n) { return g_mq_min.exchange(n); }
 int es_hip_set_batched32_min(int n) { return g_mb_min.exchange(n); }
+int es_hip_set_batched32_mfma_min(int n) { return g_mbm_min.exchange(n); }
 int es_hip_set_q6k_mfma_min_batch(int n) { return g_mm6_min.exchange(n); }
 int es_hip_set_q2k_mfma_min_batch(int n) { return g_mm2_min.exchange(n); }
 

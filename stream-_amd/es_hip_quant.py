@@ -118,7 +118,7 @@ class Lib:
             ("es_hip_run_jobs_host", i, [vp, i]),
             ("es_hip_set_mfma_min_batch", i, [i]), ("es_hip_set_small_batch_min", i, [i]),
             ("es_hip_set_mfma_tile", i, [i, i, i]),
-            ("es_hip_set_batched32_min", i, [i]), ("es_hip_set_q6k_mfma_min_batch", i, [i]), ("es_hip_set_q2k_mfma_min_batch", i, [i]),
+            ("es_hip_set_batched32_min", i, [i]), ("es_hip_set_batched32_mfma_min", i, [i]), ("es_hip_set_q6k_mfma_min_batch", i, [i]), ("es_hip_set_q2k_mfma_min_batch", i, [i]),
             ("es_hip_moe_ffn", i, [vp, i, vp, vp, vp, i, vp, sz, vp, sz, vp]),
             ("es_hip_moe_plan_create", vp, [vp, i, vp, vp, vp, i, vp, sz, vp, sz]),
             ("es_hip_moe_plan_run", i, [vp, vp]), ("es_hip_moe_plan_destroy", None, [vp]),
@@ -155,6 +155,9 @@ class Lib:
 
     def set_batched32_min(self, n: int) -> int:
         return self._L.es_hip_set_batched32_min(n)
+
+    def set_batched32_mfma_min(self, n: int) -> int:
+        return self._L.es_hip_set_batched32_mfma_min(n)
 
     def set_q6k_mfma_min_batch(self, n: int) -> int:
         return self._L.es_hip_set_q6k_mfma_min_batch(n)

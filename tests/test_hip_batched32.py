@@ -1,6 +1,8 @@
-"""GPU parity of the batched Q4_0 / Q5_0 kernel (one lane per row and activation, chains in registers): bit-identical to the
-oracle in every reference order and to the vector kernel, over activation counts that exercise every lane split (2 .. 64
-per group, several groups), ragged row counts and padded strides."""
+"""GPU parity of the batched Q4_0 / Q5_0 kernels, the matrix-core one (es_hip_mb.hip: one int8 MFMA per block for 4 rows x
+32 activations, chains in registers, 8 blocks in flight) and the one-lane-per-output one (es_hip_mv.hip): bit-identical to
+the oracle in every reference order and to the vector kernel, over activation counts that exercise every lane split and
+token tile (2 .. 64 per group, several groups), ragged row counts, rows of every block count around the load pipeline's
+depth, 2-byte aligned rows, extreme codes and padded strides."""
 import numpy as np
 import pytest
 
@@ -17,11 +19,16 @@ def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.fixture
-def hipb(hip):
+KERNELS = {"mfma": 2, "lanes": 0}   # es_hip_set_batched32_mfma_min for each kernel
+
+
+@pytest.fixture(params=list(KERNELS))
+def hipb(hip, request):
     prev = hip.set_batched32_min(2)
+    prevm = hip.set_batched32_mfma_min(KERNELS[request.param])
     yield hip
     hip.set_batched32_min(prev)
+    hip.set_batched32_mfma_min(prevm)
     hip.set_order(E.ORDER_X86_CONTRACT)
 
 
@@ -65,3 +72,46 @@ def test_batched32_equals_vector_kernel_with_ranges(hipb, orc, t):
                 hipb.set_batched32_min(prev)
     assert np.array_equal(bits(out[0]), bits(out[1]))
     assert np.all(out[0][:, :r0] == -555.0) and np.all(out[0][:, r1:] == -555.0)
+
+
+@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0], ids=["q4_0", "q5_0"])
+@pytest.mark.parametrize("cols", [32, 96, 224, 256, 288, 544, 2080])
+@pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
+def test_batched32_block_counts(hipb, orc, t, cols, mode):
+    """1 .. 65 blocks per row: fewer than, exactly and just past the 8 blocks the matrix-core kernel keeps in flight; odd
+    block counts give rows that start only 2-byte aligned"""
+    hipb.set_order(mode[0])
+    rows, na = 45, 33
+    W, acts = inputs(orc, t, rows, cols, na, cols + t)
+    y = hipb.matvec_multi(t, W, cols, rows, acts)
+    ref = orc.matvec_multi(t, W, cols, rows, acts, mode[1], mode[2])
+    assert np.array_equal(bits(y), bits(ref))
+
+
+@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0], ids=["q4_0", "q5_0"])
+def test_batched32_extreme_codes(hipb, orc, t):
+    """codes at both ends (0 and 15 / 31, every high bit set or clear) against activations of +-127"""
+    rows, cols, na = 40, 512, 32
+    rng = np.random.default_rng(11)
+    W, acts = inputs(orc, t, rows, cols, na, 4)
+    bb = 18 if t == O.Q4_0 else 22
+    Wb = W.view(np.uint8).reshape(rows, -1).copy()
+    for r in range(rows):
+        for b in range(cols // 32):
+            blk = Wb[r, bb * b:bb * (b + 1)]
+            pat = rng.integers(0, 3)
+            if pat < 2:
+                blk[bb - 16:] = 0xff if pat == 0 else 0x00
+                if t == O.Q5_0:
+                    blk[2:6] = 0xff if pat == 0 else 0x00
+    W = Wb.reshape(W.shape)
+    A = acts.view(np.uint8).reshape(na, -1).copy()
+    for q in range(na):
+        for b in range(cols // 32):
+            A[q, 36 * b + 4:36 * (b + 1)] = np.where(rng.random(32) < 0.5, 127, 0x81).astype(np.uint8)   # +127 / -127
+    acts = A.view(acts.dtype).reshape(acts.shape)
+    for mode in MODES:
+        hipb.set_order(mode[0])
+        y = hipb.matvec_multi(t, W, cols, rows, acts)
+        ref = orc.matvec_multi(t, W, cols, rows, acts, mode[1], mode[2])
+        assert np.array_equal(bits(y), bits(ref)), mode
