@@ -50,14 +50,18 @@ struct MbJob {
     const uint8_t *W;     // row 0
     const uint8_t *act;   // activation 0's first block
     const int *arow;      // optional gather: activation q is row arow[q] of act
+    const uint8_t *xq;    // matrix-core form: the activations as a kind 3 pre-pass laid them out (act / arow unused)
+    const uint8_t *xm;
     float *y;
     uint64_t astride, ystride, row_bytes;
     int r0, r1, cols, na, t0, ta;
     int tile0, pad_;
 };
 hipError_t mb32_launch(int type, const MbJob *jobs, int njobs, const MbJob &single, int grid, int order, hipStream_t s);
-// The same products on the matrix cores (es_hip_mb.hip): workgroups of 16 rows x activations [t0, t0 + 32).
-constexpr int MB32M_ROWS = 16, MB32M_TOKENS = 32;
+// The same products on the matrix cores (es_hip_mb.hip): workgroups of 16 rows x activations [t0, t0 + 32), the
+// activations read from a kind 3 pre-pass.
+constexpr int MB32M_ROWS = 16, MB32M_TOKENS = 32, PREP_KIND_Q80 = 3;
+__host__ __device__ constexpr uint32_t prep_words(int kind) { return kind == PREP_KIND_Q80 ? 9u : 73u; }   // per block
 hipError_t mb32m_launch(int type, const MbJob *jobs, int njobs, const MbJob &single, int grid, int order, hipStream_t s);
 
 // The batched (matrix-core) form: rows [r0, r1) against na activations that a pre-pass has re-laid out as
@@ -75,9 +79,12 @@ struct MmJob {
 };
 // One activation pre-pass: kind 0 writes 16 bytes of meta per activation and superblock (pair sums of the Q4_K
 // sub-blocks, low | high bytes), kind 1 32 bytes (the 16 bsums, low | high bytes), kind 2 32 bytes (the 16 bsums as
-// halves); xd follows the xm plane. All the
+// halves); xd follows the xm plane. Kind 3 takes Q8_0 rows (nbk blocks of 9 dwords: d, 32 int8) and writes, per tile of
+// 32 activations and block, the 32 x 32 values as xq[tile][block][half h][activation n][16 bytes] (values 16 h..16 h+15
+// of activation n: lane 32 h + n of the batched matrix-core kernel reads 16 bytes at 16 * lane) and the scales as
+// xm[tile][block][n] floats. All the
 // pre-passes of a batch run in one launch over `total` items (one dword of an activation row each), pre-pass i taking
-// items [start, start + na_pad*nbk*73); every start is a multiple of PREP_SPAN, the items of one workgroup.
+// items [start, start + na_pad*nbk*W) (W = 73 dwords per Q8_K block, 9 per Q8_0 block); every start is a multiple of PREP_SPAN, the items of one workgroup.
 constexpr int PREP_BLOCK = 256, PREP_UNROLL = 8, PREP_SPAN = PREP_BLOCK * PREP_UNROLL;
 struct PrepJob {
     const uint8_t *act;

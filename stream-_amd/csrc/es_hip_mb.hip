@@ -17,15 +17,16 @@
 // supplies group i's codes in register i % 4 of half i / 4 is matched by the activation bytes 16 (i / 4) + 4 (i % 4)..+3
 // in the same register of the same half.
 //
-// Loads: per block a lane reads its group's code dword (+ the Q5_0 high-bit dword) and its row's d, and 16 bytes of its
-// activation's block plus that block's d; P blocks are in flight while one is computed. No LDS, no barriers.
+// Loads: per block a lane reads the aligned dwords around its row's d (and Q5_0 high bits) and its group's code dword
+// (blocks are 18 or 22 bytes, so fields sit at 2-byte alignment; unaligned dword loads cost more than two aligned ones),
+// and from the kind 3 pre-pass layout 16 bytes of activation values (one contiguous 1 KB wave load per block) and the
+// activation's block scale. P blocks are in flight while one is computed. No LDS, no barriers.
 #include "es_hip_common.h"
 
 namespace esq {
 namespace {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
-typedef uint32_t u32_a2 __attribute__((aligned(2)));   // a dword at a 2-byte aligned address (blocks are 18 / 22 bytes)
 
 template <int F> struct Mb32Fmt;
 // Q4_0: d f16 @0, qs[16] @2; codes 0..15, offset 8. Q5_0: d f16 @0, qh u32 @2, qs[16] @6; codes 0..31, offset 16.
@@ -34,26 +35,35 @@ template <> struct Mb32Fmt<ES_HIP_Q4_0> { static constexpr int QS = 2, QH = -1; 
 template <> struct Mb32Fmt<ES_HIP_Q5_0> { static constexpr int QS = 6, QH = 2; static constexpr uint32_t BIAS = 0x70707070u; };
 
 struct Stage {
-    uint32_t qs, qh, d16;   // this lane's group codes (packed nibbles), high bits, its row's d
-    u32x4 y;                // 16 activation bytes (this lane's half of the block)
-    float yd;               // the activation block's d
+    uint32_t w0, w1;   // the aligned dwords at and after the block's start: d (and Q5_0 qh)
+    uint32_t qa, qb;   // the aligned dwords at and after this lane's code dword
+    u32x4 y;           // 16 activation values (this lane's half of the block)
+    float yd;          // the activation block's scale
 };
 
+// wblk: the block (2-byte aligned); every dword read lies inside it: the block's first two aligned dwords (it is at least
+// 18 bytes long), the aligned dword holding the code field's first byte, and the next one unless that would pass the
+// block's last aligned dword (then the field is 4-byte aligned and the second dword is not used).
 template <int F>
-__device__ __forceinline__ void load_stage(Stage &s, const uint8_t *wblk, const uint8_t *xblk, int gq, int h) {
-    s.d16 = ldg<uint16_t>(wblk);
-    s.qs = ldg<u32_a2>(wblk + Mb32Fmt<F>::QS + 4 * gq);
-    if constexpr (Mb32Fmt<F>::QH >= 0) s.qh = ldg<u32_a2>(wblk + Mb32Fmt<F>::QH);
-    else s.qh = 0;
-    s.y = ldg<u32x4>(xblk + 4 + 16 * h);
-    s.yd = ldg<float>(xblk);
+__device__ __forceinline__ void load_stage(Stage &s, const uint8_t *wblk, const uint8_t *xq, const uint8_t *xm, int lane, int gq) {
+    constexpr int BB = Fmt<F>::BB;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(wblk);
+    const uint8_t *const al = wblk - (a & 2);
+    s.w0 = ldg<uint32_t>(al);
+    s.w1 = Mb32Fmt<F>::QH >= 0 ? ldg<uint32_t>(al + 4) : 0u;
+    const uintptr_t f = a + Mb32Fmt<F>::QS + 4 * gq, fa = f & ~uintptr_t(3), last = (a + BB - 1) & ~uintptr_t(3);
+    s.qa = ldg<uint32_t>(reinterpret_cast<const void *>(fa));
+    s.qb = ldg<uint32_t>(reinterpret_cast<const void *>(fa + 4 <= last ? fa + 4 : fa));
+    s.y = ldg<u32x4>(xq + 16 * lane);
+    s.yd = ldg<float>(xm + 4 * (lane & 31));
 }
 
-// Tiles of 4 waves x 4 rows against 32 activations [t0, t0 + 32) of the job (those past na are computed on a copy of
-// activation na - 1 and not stored). P: blocks in flight per wave. X86: the AVX2 order (else the scalar one).
+// Tiles of 4 waves x 4 rows against 32 activations [t0, t0 + 32) of the job (the pre-pass wrote zeros for those past na;
+// they are not stored). P: blocks in flight per wave (even). X86: the AVX2 order (else the scalar one).
 template <int F, int P, bool X86>
 __global__ __launch_bounds__(256) void mb32m_kernel(const MbJob *__restrict__ jobs, int njobs, MbJob single) {
-    constexpr int BB = Fmt<F>::BB, AB = Fmt<F>::AB;
+    constexpr int BB = Fmt<F>::BB;
+    static_assert(P % 2 == 0, "block parity is the stage's");
     MbJob J;
     if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
     else J = single;
@@ -68,28 +78,34 @@ __global__ __launch_bounds__(256) void mb32m_kernel(const MbJob *__restrict__ jo
     uint32_t sel[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) sel[j] = j == gq ? keep : 0u;
-    const int nshift = 4 * (gi >> 2), hshift = 4 * gi;
+    const int nshift = 4 * (gi >> 2);
     const uint8_t *const wrow = J.W + (size_t)min(row0 + (n >> 3), J.r1 - 1) * J.row_bytes;
-    // B side: activation t
-    const int t = J.t0 + n;
-    const int tq = min(t, J.na - 1);
-    const uint8_t *const xrow = J.act + (size_t)(J.arow ? ldg<int>(J.arow + tq) : tq) * J.astride;
+    // Blocks are 2 mod 4 bytes long, so their 2-byte misalignment alternates: block b of this row starts misaligned by
+    // wmis ^ (2 * (b & 1)) bytes. The Q5_0 high bits of group gi sit at bit 16 + 4 gi of {w1, w0} (32 + 4 gi when
+    // misaligned); the code dword is misaligned exactly when the block is not (QS is 2 mod 4).
+    const uint32_t wmis = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wrow)) & 2u;
+    const int t = J.t0 + n;   // B side: activation t (the job's planes start at this tile)
     const int nbk = J.cols / 32;
 
     float acc[16];   // x86: acc[4 r + jj] = chain of group 4 h + jj of row r; scalar: acc[r] = the row's chain
 #pragma unroll
     for (int j = 0; j < 16; j++) acc[j] = 0.0f;
 
-    auto step = [&](const Stage &c) {
-        uint32_t q = (c.qs >> nshift) & 0x0f0f0f0fu;
-        if constexpr (F == ES_HIP_Q5_0) q |= ((((c.qh >> hshift) & 15u) * 0x00204081u) & 0x01010101u) << 4;   // bit e of qh -> bit 4 of byte e
+    auto step = [&](const Stage &c, int parity) {
+        const uint32_t mis = wmis ^ (2u * parity);
+        const uint32_t qs = alignbyte(c.qb, c.qa, mis ^ 2u);
+        uint32_t q = (qs >> nshift) & 0x0f0f0f0fu;
+        if constexpr (F == ES_HIP_Q5_0) {   // bit e of qh -> bit 4 of byte e
+            const uint64_t hw = (static_cast<uint64_t>(c.w1) << 32 | c.w0) >> (16 + 8 * mis + 4 * gi);
+            q |= (((static_cast<uint32_t>(hw) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+        }
         q = (q + Mb32Fmt<F>::BIAS) ^ 0x80808080u;
         v4i a;
 #pragma unroll
         for (int j = 0; j < 4; j++) a[j] = static_cast<int>(q & sel[j]);
         const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, __builtin_bit_cast(v4i, c.y), v16i{}, 0, 0, 0);
         // d of rows 0..3 (float), read from lanes 0, 8, 16, 24, which loaded them
-        const float wd = half_bits_to_float(c.d16);
+        const float wd = half_bits_to_float(alignbyte(c.w0, c.w0, mis));
         float dy[4];
 #pragma unroll
         for (int r = 0; r < 4; r++)
@@ -107,24 +123,23 @@ __global__ __launch_bounds__(256) void mb32m_kernel(const MbJob *__restrict__ jo
         }
     };
 
+    auto load = [&](Stage &s, int b) {
+        load_stage<F>(s, wrow + (size_t)b * BB, J.xq + (size_t)b * 1024, J.xm + (size_t)b * 128, lane, gq);
+    };
     Stage st[P];
 #pragma unroll
-    for (int p = 0; p < P; p++) {
-        const int b = min(p, nbk - 1);
-        load_stage<F>(st[p], wrow + (size_t)b * BB, xrow + (size_t)b * AB, gq, h);
-    }
+    for (int p = 0; p < P; p++) load(st[p], min(p, nbk - 1));
     int b0 = 0;
-    for (; b0 + P <= nbk; b0 += P) {
+    for (; b0 + P <= nbk; b0 += P) {   // block b0 + p is in st[p]; b0 is a multiple of P, so its parity is p's
 #pragma unroll
         for (int p = 0; p < P; p++) {
-            step(st[p]);
-            const int b = min(b0 + p + P, nbk - 1);   // past the end: a harmless reload of the last block
-            load_stage<F>(st[p], wrow + (size_t)b * BB, xrow + (size_t)b * AB, gq, h);
+            step(st[p], p & 1);
+            load(st[p], min(b0 + p + P, nbk - 1));   // past the end: a harmless reload of the last block
         }
     }
 #pragma unroll
     for (int p = 0; p < P; p++)
-        if (b0 + p < nbk) step(st[p]);
+        if (b0 + p < nbk) step(st[p], p & 1);
 
     const bool tok_ok = t < J.na;
 #pragma unroll

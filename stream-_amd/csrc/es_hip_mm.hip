@@ -39,7 +39,8 @@ namespace esq {
 // items on consecutive threads so the reads are coalesced, PREP_UNROLL items per thread with every load issued before
 // the first store; padding activations t >= na get zeros. Activation t is row arow[t] of act when arow is given.
 // kind 0 writes the pair sums (Q4_K sub-blocks) and kind 1 the 16 bsums, both split as 128*hi + lo, one byte each; kind 2
-// writes the 16 bsums as halves (exact: a Q8_K block's bsums are sums of 16 int8 values, |bsums| <= 2048).
+// writes the 16 bsums as halves (exact: a Q8_K block's bsums are sums of 16 int8 values, |bsums| <= 2048). Kind 3 reads
+// Q8_0 rows (9 dwords per block) and writes the batched 32-wide matrix-core layout (tiles of 32 activations).
 // Index arithmetic is 32-bit within a pre-pass (the host keeps every pre-pass below 2^31 threads).
 // the loads of one thread's items: row indices (for a gather), then the activation words
 template <bool GATHER>
@@ -71,7 +72,8 @@ __global__ __launch_bounds__(PREP_BLOCK) void act_prep_q8k(const PrepJob *__rest
     PrepJob P;
     if (jobs) P = jobs[j];
     else P = single;
-    const uint32_t per = (uint32_t)P.nbk * 73u, n = (uint32_t)P.na_pad * per, base = (uint32_t)(id0 - P.start);
+    const uint32_t words = prep_words(P.kind);
+    const uint32_t per = (uint32_t)P.nbk * words, n = (uint32_t)P.na_pad * per, base = (uint32_t)(id0 - P.start);
     const int mb = P.kind == 0 ? 16 : 32;   // meta bytes per (activation, superblock)
     // every load of the span first, unconditionally (items past the end read the first word and keep 0), so they are all
     // in flight together; then the stores
@@ -91,10 +93,14 @@ __global__ __launch_bounds__(PREP_BLOCK) void act_prep_q8k(const PrepJob *__rest
     for (int u = 0; u < PREP_UNROLL; u++) {
         const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x;
         if (lid >= n) break;
-        const uint32_t t = lid / per, k = lid - t * per, b = k / 73u, w = k - 73u * b;
+        const uint32_t t = lid / per, k = lid - t * per, b = k / words, w = k - words * b;
         const size_t bt = (size_t)b * P.na_pad + t;
         uint8_t *xm = P.xm;
-        if (w == 0) {
+        if (P.kind == PREP_KIND_Q80) {
+            const uint32_t tb = (t >> 5) * (uint32_t)P.nbk + b, nn = t & 31u;   // (tile, block), activation in the tile
+            if (w == 0) stg<uint32_t>(xm + ((size_t)tb * 32 + nn) * 4, v[u]);
+            else stg<uint32_t>(P.xq + ((size_t)tb * 64 + 32 * ((w - 1) >> 2) + nn) * 16 + 4 * ((w - 1) & 3), v[u]);
+        } else if (w == 0) {
             stg<uint32_t>(xm + (size_t)P.nbk * P.na_pad * mb + bt * 4, v[u]);   // d
         } else if (w <= 64) {
             stg<uint32_t>(P.xq + bt * 256 + 4 * (w - 1), v[u]);                 // qs

@@ -334,7 +334,8 @@ bool mq_eligible(const Req &q) {
 
 // the pre-pass of q's activations in layout (kind, na_pad), shared with earlier products that read the same ones
 const Prep &get_prep(Batch &bt, const Req &q, const FmtInfo &f, int kind, int na_pad) {
-    const int nbk = q.cols / 256;
+    const bool q80 = kind == esq::PREP_KIND_Q80;
+    const int nbk = q.cols / (q80 ? 32 : 256);
     const uint64_t astride = q.astride ? q.astride : (uint64_t)nbk * f.ab;
     for (const Prep &p : bt.preps)
         if (p.act == q.act && p.arow == q.arow && p.astride == astride && p.na == q.na && p.nbk == nbk && p.kind == kind &&
@@ -342,9 +343,9 @@ const Prep &get_prep(Batch &bt, const Req &q, const FmtInfo &f, int kind, int na
             return p;
     Prep p{static_cast<const uint8_t *>(q.act), q.arow, astride, q.na, na_pad, nbk, kind, 0, 0};
     p.xq_off = bt.ws_bytes;
-    bt.ws_bytes += align256((size_t)nbk * na_pad * 256);
+    bt.ws_bytes += align256((size_t)nbk * na_pad * (q80 ? 32 : 256));
     p.xm_off = bt.ws_bytes;
-    bt.ws_bytes += align256((size_t)nbk * na_pad * (kind ? 36 : 20));   // meta, then the float scales
+    bt.ws_bytes += align256((size_t)nbk * na_pad * (q80 ? 4 : kind ? 36 : 20));   // meta, then the float scales
     bt.preps.push_back(p);
     return bt.preps.back();
 }
@@ -365,6 +366,7 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             if (!g) { bt.mbg.push_back(MbGroup{(int)q.type, mfma}); g = &bt.mbg.back(); }
             const int nbk32 = q.cols / 32;
             const int tstep = mfma ? esq::MB32M_TOKENS : 64;
+            const Prep *pp = mfma ? &get_prep(bt, q, f, esq::PREP_KIND_Q80, (q.na + 31) / 32 * 32) : nullptr;
             for (int t0 = 0; t0 < q.na; t0 += tstep) {
                 int ta = 1;
                 while (ta < std::min(64, q.na - t0)) ta <<= 1;
@@ -373,6 +375,10 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
                 j.W = static_cast<const uint8_t *>(q.W);
                 j.act = static_cast<const uint8_t *>(q.act);
                 j.arow = q.arow;
+                if (pp) {   // workspace offsets of this tile's planes until bind()
+                    j.xq = reinterpret_cast<const uint8_t *>(pp->xq_off + (size_t)(t0 / 32) * nbk32 * 1024);
+                    j.xm = reinterpret_cast<const uint8_t *>(pp->xm_off + (size_t)(t0 / 32) * nbk32 * 128);
+                }
                 j.y = q.y;
                 j.astride = q.astride ? q.astride : (uint64_t)nbk32 * f.ab;
                 j.ystride = q.ystride;
@@ -492,6 +498,12 @@ void bind(Batch &bt, uint8_t *ws) {
             j.xq = ws + reinterpret_cast<uintptr_t>(j.xq);
             j.xm = ws + reinterpret_cast<uintptr_t>(j.xm);
         }
+    for (MbGroup &g : bt.mbg)
+        if (g.mfma)
+            for (esq::MbJob &j : g.jobs) {
+                j.xq = ws + reinterpret_cast<uintptr_t>(j.xq);
+                j.xm = ws + reinterpret_cast<uintptr_t>(j.xm);
+            }
     bt.pj.clear();
     bt.prep_total = 0;
     for (Prep &p : bt.preps) {   // offsets become addresses too (kept as integers)
@@ -500,7 +512,7 @@ void bind(Batch &bt, uint8_t *ws) {
         esq::PrepJob j{p.act, p.arow, reinterpret_cast<uint8_t *>(p.xq_off), reinterpret_cast<uint8_t *>(p.xm_off), p.astride,
                        bt.prep_total, p.na, p.na_pad, p.nbk, p.kind};
         bt.pj.push_back(j);
-        const long n = (long)p.na_pad * p.nbk * 73;
+        const long n = (long)p.na_pad * p.nbk * esq::prep_words(p.kind);
         bt.prep_total += (n + esq::PREP_SPAN - 1) / esq::PREP_SPAN * esq::PREP_SPAN;
     }
 }
@@ -526,7 +538,7 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
         if (e != hipSuccess) return hip_fail(e, "pre-pass launch");
     } else {
         for (esq::PrepJob j : bt.pj) {
-            const long n = (long)j.na_pad * j.nbk * 73;
+            const long n = (long)j.na_pad * j.nbk * esq::prep_words(j.kind);
             j.start = 0;
             if ((e = esq::prep_launch(nullptr, 1, j, n, s)) != hipSuccess) return hip_fail(e, "pre-pass launch");
         }
