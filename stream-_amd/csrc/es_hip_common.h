@@ -80,9 +80,9 @@ struct MmJob {
 // One activation pre-pass: kind 0 writes 16 bytes of meta per activation and superblock (pair sums of the Q4_K
 // sub-blocks, low | high bytes), kind 1 32 bytes (the 16 bsums, low | high bytes), kind 2 32 bytes (the 16 bsums as
 // halves); xd follows the xm plane. Kind 3 takes Q8_0 rows (nbk blocks of 9 dwords: d, 32 int8) and writes, per tile of
-// 32 activations and block, the 32 x 32 values as xq[tile][block][half h][activation n][16 bytes] (values 16 h..16 h+15
-// of activation n: lane 32 h + n of the batched matrix-core kernel reads 16 bytes at 16 * lane) and the scales as
-// xm[tile][block][n] floats. All the
+// 32 activations and block, the 32 x 32 values as halves, xq[tile][block][q][h][activation n][8 halves] (values
+// 16 q + 8 h .. + 7 of activation n: lane 32 h + n of the batched matrix-core kernel reads 16 bytes at 1024 q + 16 * lane
+// for its instruction q) and the scales as xm[tile][block][n] floats. All the
 // pre-passes of a batch run in one launch over `total` items (one dword of an activation row each), pre-pass i taking
 // items [start, start + na_pad*nbk*W) (W = 73 dwords per Q8_K block, 9 per Q8_0 block); every start is a multiple of PREP_SPAN, the items of one workgroup.
 constexpr int PREP_BLOCK = 256, PREP_UNROLL = 8, PREP_SPAN = PREP_BLOCK * PREP_UNROLL;

@@ -98,8 +98,18 @@ __global__ __launch_bounds__(PREP_BLOCK) void act_prep_q8k(const PrepJob *__rest
         uint8_t *xm = P.xm;
         if (P.kind == PREP_KIND_Q80) {
             const uint32_t tb = (t >> 5) * (uint32_t)P.nbk + b, nn = t & 31u;   // (tile, block), activation in the tile
-            if (w == 0) stg<uint32_t>(xm + ((size_t)tb * 32 + nn) * 4, v[u]);
-            else stg<uint32_t>(P.xq + ((size_t)tb * 64 + 32 * ((w - 1) >> 2) + nn) * 16 + 4 * ((w - 1) & 3), v[u]);
+            if (w == 0) {
+                stg<uint32_t>(xm + ((size_t)tb * 32 + nn) * 4, v[u]);
+            } else {   // values e0 .. e0 + 3 as halves: instruction q = e0 / 16, lane half h = e0 % 16 / 8, halves e0 % 8 ..
+                const uint32_t e0 = 4 * (w - 1), q = e0 >> 4, hh = (e0 >> 3) & 1;
+                h2 lo, hi;
+                lo[0] = (_Float16)(int8_t)(v[u] & 0xff);
+                lo[1] = (_Float16)(int8_t)((v[u] >> 8) & 0xff);
+                hi[0] = (_Float16)(int8_t)((v[u] >> 16) & 0xff);
+                hi[1] = (_Float16)(int8_t)(v[u] >> 24);
+                const uint2 pr = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+                stg<uint2>(P.xq + ((((size_t)tb * 2 + q) * 2 + hh) * 32 + nn) * 16 + 2 * (e0 & 7), pr);
+            }
         } else if (w == 0) {
             stg<uint32_t>(xm + (size_t)P.nbk * P.na_pad * mb + bt * 4, v[u]);   // d
         } else if (w <= 64) {

@@ -343,7 +343,7 @@ const Prep &get_prep(Batch &bt, const Req &q, const FmtInfo &f, int kind, int na
             return p;
     Prep p{static_cast<const uint8_t *>(q.act), q.arow, astride, q.na, na_pad, nbk, kind, 0, 0};
     p.xq_off = bt.ws_bytes;
-    bt.ws_bytes += align256((size_t)nbk * na_pad * (q80 ? 32 : 256));
+    bt.ws_bytes += align256((size_t)nbk * na_pad * (q80 ? 64 : 256));
     p.xm_off = bt.ws_bytes;
     bt.ws_bytes += align256((size_t)nbk * na_pad * (q80 ? 4 : kind ? 36 : 20));   // meta, then the float scales
     bt.preps.push_back(p);
@@ -358,8 +358,8 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
         if (int rc = check_req(q, f)) return rc;
         if (mb_eligible(q)) {   // batched 32-wide: activation groups of at most 64
-            const int mm = g_mbm_min.load();
-            const bool mfma = mm > 0 && q.na >= mm;
+            const int mm = g_mbm_min.load();   // (the matrix-core kernel addresses a matrix with 32-bit offsets)
+            const bool mfma = mm > 0 && q.na >= mm && (size_t)q.r1 * (q.cols / 32) * f.bb < ((size_t)1 << 31);
             MbGroup *g = nullptr;
             for (MbGroup &x : bt.mbg)
                 if (x.type == (int)q.type && x.mfma == mfma) g = &x;
@@ -376,7 +376,7 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
                 j.act = static_cast<const uint8_t *>(q.act);
                 j.arow = q.arow;
                 if (pp) {   // workspace offsets of this tile's planes until bind()
-                    j.xq = reinterpret_cast<const uint8_t *>(pp->xq_off + (size_t)(t0 / 32) * nbk32 * 1024);
+                    j.xq = reinterpret_cast<const uint8_t *>(pp->xq_off + (size_t)(t0 / 32) * nbk32 * 2048);
                     j.xm = reinterpret_cast<const uint8_t *>(pp->xm_off + (size_t)(t0 / 32) * nbk32 * 128);
                 }
                 j.y = q.y;
