@@ -202,6 +202,22 @@ int es_hip_set_q6k_mfma_min_batch(int n);
 /* Q2_K products with at least n activations run on the Q2_K LDS-staged matrix-core kernel (default 2); below that, or
  * with it off, the small-batch kernel (es_hip_set_small_batch_min) or the vector kernel. */
 int es_hip_set_q2k_mfma_min_batch(int n);
+/* ---- activation preparation on the device ---------------------------------------------------------------------------
+ * es_act_prepare (src/es_quant.c:499-512) for `rows` rows of `cols` fp32 values in device memory: q80 (when non-NULL;
+ * cols % 32 == 0) receives cols/32 Q8_0 blocks per row exactly as quantize_q80 (src/es_quant.c:489-497) writes them, q8k
+ * (when non-NULL; cols % 256 == 0) cols/256 Q8_K blocks per row as es_quantize_q8_K (src/es_q2k.c:102-125), bsums
+ * included. Float strides are in floats, block strides in bytes; 0 means packed. Stream-ordered; nothing is allocated. */
+int es_hip_act_prepare_dev(const float *x, size_t xstride, int rows, int cols, void *q80, size_t q80_stride, void *q8k,
+                           size_t q8k_stride, void *stream);
+/* rmsnorm (src/es_engine.c:189-194: the sum of squares in double in element order, s = (float)(1 / sqrt(ss / cols + eps)),
+ * xn = x * s * w) fused with the same preparation of xn (the engine's `prep` after its rmsnorm, src/es_engine.c:1284-1292).
+ * w may be NULL (weights 1); xn (optional) receives the normalised rows. cols <= 16384. */
+int es_hip_rmsnorm_prepare_dev(const float *x, size_t xstride, const float *w, float eps, int rows, int cols, float *xn,
+                               size_t xn_stride, void *q80, size_t q80_stride, void *q8k, size_t q8k_stride, void *stream);
+/* SwiGLU of gate|up rows as dense_n / moe_n lay them out (gate at [r][0, ff), up at [r][ff, 2 ff); src/es_engine.c:957-972,
+ * 913-914), h = g / (1 + expf(-g)) * u, fused with the preparation of h; h (optional) receives the values. */
+int es_hip_swiglu_prepare_dev(const float *gu, size_t gu_stride, int rows, int ff, float *h, size_t h_stride, void *q80,
+                              size_t q80_stride, void *q8k, size_t q8k_stride, void *stream);
 /* The MoE SwiGLU alone on n device floats: h[i] = g[i] / (1 + expf(-g[i])) * u[i] as src/es_engine.c:913 computes it. */
 int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream);
 /* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`

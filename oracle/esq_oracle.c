@@ -643,6 +643,16 @@ void esq_swiglu(const float *g, const float *u, float *h, int n) {
     for (int i = 0; i < n; i++) h[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
 }
 
+/* src/es_engine.c:189-194: the sum of squares in double, in element order (each square is exact in double, each sum is
+ * rounded); s = (float)(1 / sqrt(ss / n + eps)) in double; o = (x * s) * w in float. The engine is built for baseline
+ * x86-64 (no FMA), and this file with -ffp-contract=off, so no operation here is fused. */
+void esq_rmsnorm(const float *x, const float *w, float *o, int n, float eps) {
+    double ss = 0;
+    for (int i = 0; i < n; i++) ss += (double)x[i] * x[i];
+    const float s = (float)(1.0 / sqrt(ss / n + eps));
+    for (int i = 0; i < n; i++) o[i] = x[i] * s * (w ? w[i] : 1.0f);
+}
+
 void esq_moe_combine(const float *ye, const int *rowof, const float *w, int n_tok, int k, int n, float *out) {
     for (int t = 0; t < n_tok; t++)
         for (int i = 0; i < n; i++) {

@@ -23,6 +23,9 @@
  *   route / grouping / SwiGLU / combine (moe_n restatement): golden vectors are not possible (the reference's engine
  *       needs a whole model), so these are pinned by invariants and textbook special cases in the tests
  *       (softmax of equal logits, ties to lowest index, norm_topk sums to one, grouping is a stable partition).
+ *   rmsnorm (es_engine.c is not buildable on its own): against an independent numpy restatement (float64 running sum
+ *       via cumsum, float32 products) on random rows, and the closed forms of a zero row (s = 1/sqrt(eps)), a constant
+ *       row (s = 1/sqrt(c^2 + eps)) and w = NULL equal to w = ones.
  *   Weight quantizers for Q4_0/Q5_0/Q4_K/Q6_K are this project's own (the reference has none); they are test-input
  *       generators, checked only for round-trip error bounds.
  */
@@ -101,6 +104,8 @@ int  esq_route_softmax(float *logits, int ne, int k, int norm_topk, int *sel, fl
 /* distinct experts in order of first use; start/cnt per expert; rowof[t*k + j] = grouped row of (t, j) */
 int  esq_moe_group(const int *sel, int n_tok, int k, int *uex, int *cnt, int *start, int *rowof, int *tok_of);
 void esq_swiglu(const float *g, const float *u, float *h, int n);  /* g/(1+expf(-g))*u, src/es_engine.c:913 */
+/* rmsnorm (src/es_engine.c:189-194): o = x * (float)(1/sqrt(sum of x^2 / n + eps)) * w; w may be NULL (weights 1) */
+void esq_rmsnorm(const float *x, const float *w, float *o, int n, float eps);
 /* out[t][i] = sum_j w[t][j] * ye[rowof[t][j]][i], sequential over j (src/es_engine.c:925-932) */
 void esq_moe_combine(const float *ye, const int *rowof, const float *w, int n_tok, int k, int n, float *out);
 

@@ -71,6 +71,7 @@ class Oracle:
             "esq_route_softmax": (i, [vp, i, i, i, vp, vp]),
             "esq_moe_group": (i, [vp, i, i, vp, vp, vp, vp, vp]),
             "esq_swiglu": (None, [vp, vp, vp, i]),
+            "esq_rmsnorm": (None, [vp, vp, vp, i, f]),
             "esq_moe_combine": (None, [vp, vp, vp, i, i, i, vp]),
             "esq_cpu_bench": (C.c_double, [vp, u32, vp, sz, i, i, i, vp, sz, i, vp, i, C.c_double, vp]),
             "esq_bind_reference": (None, [vp]),
@@ -193,6 +194,16 @@ class Oracle:
         h = np.zeros_like(g)
         self.lib.esq_swiglu(_p(g), _p(u), _p(h), g.size)
         return h
+
+    def rmsnorm(self, x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
+        """rows of x (2-D) normalised one by one"""
+        x = np.ascontiguousarray(x, np.float32)
+        x2 = x.reshape(-1, x.shape[-1])
+        o = np.zeros_like(x2)
+        wp = None if w is None else np.ascontiguousarray(w, np.float32)
+        for r in range(x2.shape[0]):
+            self.lib.esq_rmsnorm(_p(x2[r]), None if wp is None else _p(wp), _p(o[r]), x2.shape[1], eps)
+        return o.reshape(x.shape)
 
     def moe_combine(self, ye: np.ndarray, rowof: np.ndarray, w: np.ndarray) -> np.ndarray:
         n_tok, k = rowof.shape

@@ -125,6 +125,16 @@ hipError_t moe_combine_launch(const float *ye, const int *rowof, const float *w,
                               float *out, uint64_t ostride, hipStream_t s);
 hipError_t swiglu_plain_launch(const float *g, const float *u, float *h, long n, hipStream_t s);
 
+constexpr int ACT_RMS_MAX_COLS = 16384;   // rmsnorm rows are staged whole in LDS (64 KB)
+// Activation preparation (es_hip_act.hip): rows of fp32 values (plain, rmsnorm-ed, or the SwiGLU of gate|up rows) into
+// Q8_0 and / or Q8_K blocks (either output may be null). Float strides in floats, block strides in bytes.
+hipError_t act_prep_launch(const float *x, uint64_t xs, int rows, int cols, uint8_t *q80, uint64_t q80s, uint8_t *q8k,
+                           uint64_t q8ks, hipStream_t s);
+hipError_t act_prep_swiglu_launch(const float *gu, uint64_t gs, int rows, int ff, float *h, uint64_t hs, uint8_t *q80,
+                                  uint64_t q80s, uint8_t *q8k, uint64_t q8ks, hipStream_t s);
+hipError_t act_prep_rms_launch(const float *x, uint64_t xs, const float *w, float eps, int rows, int cols, float *xn,
+                               uint64_t xns, uint8_t *q80, uint64_t q80s, uint8_t *q8k, uint64_t q8ks, hipStream_t s);
+
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     // exact for every finite half, subnormals included (v_cvt_f32_f16)
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xffffu)));

@@ -1207,6 +1207,85 @@ int es_hip_moe_ffn(const es_hip_moe *m, int N, const int *k, const int *sel, con
     return rc;
 }
 
+}  // extern "C"
+
+namespace {
+// Checks of an activation preparation's block outputs (either may be null); fills in packed strides.
+int prep_blocks(int rows, int cols, const void *q80, size_t &q80s, const void *q8k, size_t &q8ks) {
+    if (rows < 0 || cols <= 0) return fail(ES_HIP_EINVAL, "bad shape: %d rows of %d values", rows, cols);
+    if (q80) {
+        const size_t packed = (size_t)(cols / 32) * 36;
+        if (cols % 32) return fail(ES_HIP_EINVAL, "Q8_0 blocks need cols %% 32 == 0 (cols %d)", cols);
+        if (!q80s) q80s = packed;
+        if (rows > 1 && q80s < packed) return fail(ES_HIP_EINVAL, "Q8_0 stride %zu < %zu bytes of one row", q80s, packed);
+        if ((reinterpret_cast<uintptr_t>(q80) & 3) || (q80s & 3)) return fail(ES_HIP_EINVAL, "Q8_0 blocks must be 4-byte aligned");
+    }
+    if (q8k) {
+        const size_t packed = (size_t)(cols / 256) * 292;
+        if (cols % 256) return fail(ES_HIP_EINVAL, "Q8_K blocks need cols %% 256 == 0 (cols %d)", cols);
+        if (!q8ks) q8ks = packed;
+        if (rows > 1 && q8ks < packed) return fail(ES_HIP_EINVAL, "Q8_K stride %zu < %zu bytes of one row", q8ks, packed);
+        if ((reinterpret_cast<uintptr_t>(q8k) & 3) || (q8ks & 3)) return fail(ES_HIP_EINVAL, "Q8_K blocks must be 4-byte aligned");
+    }
+    return ES_HIP_OK;
+}
+// a float row array: pointer, stride (0: packed) and row length
+int prep_floats(const char *what, const float *p, size_t &stride, int rows, size_t len) {
+    if (!stride) stride = len;
+    if (rows > 1 && stride < len) return fail(ES_HIP_EINVAL, "%s stride %zu < %zu floats of one row", what, stride, len);
+    if (reinterpret_cast<uintptr_t>(p) & 3) return fail(ES_HIP_EINVAL, "%s must be 4-byte aligned", what);
+    return ES_HIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int es_hip_act_prepare_dev(const float *x, size_t xstride, int rows, int cols, void *q80, size_t q80_stride, void *q8k,
+                           size_t q8k_stride, void *stream) {
+    if (int rc = need_device()) return rc;
+    if (int rc = prep_blocks(rows, cols, q80, q80_stride, q8k, q8k_stride)) return rc;
+    if (!q80 && !q8k) return fail(ES_HIP_EINVAL, "no output blocks asked for");
+    if (rows == 0) return ES_HIP_OK;
+    if (!x) return fail(ES_HIP_EINVAL, "null x");
+    if (int rc = prep_floats("x", x, xstride, rows, (size_t)cols)) return rc;
+    hipError_t e = esq::act_prep_launch(x, xstride, rows, cols, static_cast<uint8_t *>(q80), q80_stride,
+                                        static_cast<uint8_t *>(q8k), q8k_stride, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "activation preparation launch");
+}
+
+int es_hip_rmsnorm_prepare_dev(const float *x, size_t xstride, const float *w, float eps, int rows, int cols, float *xn,
+                               size_t xn_stride, void *q80, size_t q80_stride, void *q8k, size_t q8k_stride, void *stream) {
+    if (int rc = need_device()) return rc;
+    if (int rc = prep_blocks(rows, cols, q80, q80_stride, q8k, q8k_stride)) return rc;
+    if (!xn && !q80 && !q8k) return fail(ES_HIP_EINVAL, "no output asked for");
+    if (cols > esq::ACT_RMS_MAX_COLS) return fail(ES_HIP_EINVAL, "rmsnorm rows of %d values: above %d", cols, esq::ACT_RMS_MAX_COLS);
+    if (rows == 0) return ES_HIP_OK;
+    if (!x) return fail(ES_HIP_EINVAL, "null x");
+    if (int rc = prep_floats("x", x, xstride, rows, (size_t)cols)) return rc;
+    if (xn)
+        if (int rc = prep_floats("xn", xn, xn_stride, rows, (size_t)cols)) return rc;
+    if (reinterpret_cast<uintptr_t>(w) & 3) return fail(ES_HIP_EINVAL, "w must be 4-byte aligned");
+    hipError_t e = esq::act_prep_rms_launch(x, xstride, w, eps, rows, cols, xn, xn_stride, static_cast<uint8_t *>(q80),
+                                            q80_stride, static_cast<uint8_t *>(q8k), q8k_stride,
+                                            static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "rmsnorm preparation launch");
+}
+
+int es_hip_swiglu_prepare_dev(const float *gu, size_t gu_stride, int rows, int ff, float *h, size_t h_stride, void *q80,
+                              size_t q80_stride, void *q8k, size_t q8k_stride, void *stream) {
+    if (int rc = need_device()) return rc;
+    if (int rc = prep_blocks(rows, ff, q80, q80_stride, q8k, q8k_stride)) return rc;
+    if (!h && !q80 && !q8k) return fail(ES_HIP_EINVAL, "no output asked for");
+    if (rows == 0) return ES_HIP_OK;
+    if (!gu) return fail(ES_HIP_EINVAL, "null gate|up rows");
+    if (int rc = prep_floats("gate|up", gu, gu_stride, rows, 2 * (size_t)ff)) return rc;
+    if (h)
+        if (int rc = prep_floats("h", h, h_stride, rows, (size_t)ff)) return rc;
+    hipError_t e = esq::act_prep_swiglu_launch(gu, gu_stride, rows, ff, h, h_stride, static_cast<uint8_t *>(q80), q80_stride,
+                                               static_cast<uint8_t *>(q8k), q8k_stride, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "SwiGLU preparation launch");
+}
+
 int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream) {
     if (int rc = need_device()) return rc;
     if (n < 0 || (n > 0 && (!g || !u || !h))) return fail(ES_HIP_EINVAL, "bad SwiGLU arguments");

@@ -124,6 +124,9 @@ class Lib:
             ("es_hip_moe_plan_run", i, [vp, vp]), ("es_hip_moe_plan_destroy", None, [vp]),
             ("es_hip_step_time_ms", C.c_double, [vp, i, vp, i, i, i, vp]),
             ("es_hip_swiglu_dev", i, [vp, vp, vp, C.c_long, vp]),
+            ("es_hip_act_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp]),
+            ("es_hip_rmsnorm_prepare_dev", i, [vp, sz, vp, C.c_float, i, i, vp, sz, vp, sz, vp, sz, vp]),
+            ("es_hip_swiglu_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp, sz, vp]),
         ]:
             fn = getattr(L, name)
             fn.restype, fn.argtypes = res, args
@@ -245,6 +248,25 @@ class Lib:
 
     def swiglu_dev(self, g, u, h, n, stream=None):
         self._check(self._L.es_hip_swiglu_dev(int(g), int(u), int(h), n, stream))
+
+    # ---- activation preparation on the device (device pointers as DevBuf / ints; None for an output not wanted) ----
+    @staticmethod
+    def _ptr(b):
+        return None if b is None else int(b)
+
+    def act_prepare_dev(self, x, xstride, rows, cols, q80, q80_stride, q8k, q8k_stride, stream=None):
+        self._check(self._L.es_hip_act_prepare_dev(int(x), xstride, rows, cols, self._ptr(q80), q80_stride, self._ptr(q8k),
+                                                   q8k_stride, stream))
+
+    def rmsnorm_prepare_dev(self, x, xstride, w, eps, rows, cols, xn, xn_stride, q80, q80_stride, q8k, q8k_stride,
+                            stream=None):
+        self._check(self._L.es_hip_rmsnorm_prepare_dev(int(x), xstride, self._ptr(w), eps, rows, cols, self._ptr(xn),
+                                                       xn_stride, self._ptr(q80), q80_stride, self._ptr(q8k), q8k_stride,
+                                                       stream))
+
+    def swiglu_prepare_dev(self, gu, gu_stride, rows, ff, h, h_stride, q80, q80_stride, q8k, q8k_stride, stream=None):
+        self._check(self._L.es_hip_swiglu_prepare_dev(int(gu), gu_stride, rows, ff, self._ptr(h), h_stride, self._ptr(q80),
+                                                      q80_stride, self._ptr(q8k), q8k_stride, stream))
 
     def block_ints_dev(self, t, W, cols, rows, act):
         nb = cols // BLOCK_ELEMS[t]

@@ -261,3 +261,37 @@ def test_reference_adapter_for_cpu_baseline(orc):
         assert np.array_equal(_bits(orc.matvec_multi_reference(R, t, W, cols, rows, acts)), _bits(ref)), F
         sec, passes, y = orc.cpu_bench(orc.reference_fn_ptr(R), t, W, W.size, 1, rows, cols, acts, 3, 0.01)
         assert passes >= 1 and np.array_equal(_bits(y), _bits(ref)), F
+
+
+def _rmsnorm_numpy(x, w, eps):
+    """src/es_engine.c:189-194 restated with numpy: float64 running sum (cumsum adds in element order), double division,
+    sqrt and reciprocal, float32 products"""
+    x = np.asarray(x, np.float32)
+    sq = x.astype(np.float64) * x.astype(np.float64)   # exact in double
+    ss = np.cumsum(sq)[-1]
+    s = np.float32(1.0 / np.sqrt(ss / np.float64(x.size) + np.float64(np.float32(eps))))
+    o = x * s
+    return o * (np.ones_like(x) if w is None else np.asarray(w, np.float32))
+
+
+@pytest.mark.parametrize("n,eps,scale,weighted", [(2048, 1e-5, 1.0, True), (8192, 1e-6, 0.1, True), (896, 1e-5, 30.0, False),
+                                                  (256, 1e-6, 1e-3, True), (33, 1e-5, 1.0, False)])
+def test_rmsnorm_matches_numpy_restatement(orc, n, eps, scale, weighted):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((3, n)) * scale).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32) if weighted else None
+    mine = orc.rmsnorm(x, w, eps)
+    for r in range(3):
+        assert np.array_equal(_bits(mine[r]), _bits(_rmsnorm_numpy(x[r], w, eps)))
+
+
+def test_rmsnorm_closed_forms(orc):
+    n, eps = 512, np.float32(1e-5)
+    zero = orc.rmsnorm(np.zeros((1, n), np.float32), None, eps)
+    assert np.all(zero == 0.0)
+    c = np.float32(0.75)
+    const = orc.rmsnorm(np.full((1, n), c, np.float32), None, eps)
+    s = np.float32(1.0 / np.sqrt(np.float64(c) * np.float64(c) + np.float64(eps)))   # mean of c^2 is c^2 exactly
+    assert np.all(const == c * s)
+    x = np.random.default_rng(3).standard_normal((2, n)).astype(np.float32)
+    assert np.array_equal(_bits(orc.rmsnorm(x, None, eps)), _bits(orc.rmsnorm(x, np.ones(n, np.float32), eps)))
