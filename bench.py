@@ -231,6 +231,62 @@ def cpu_baseline(t, rows, cols, rng, seconds):
 Q4K_FFN = [(E.Q4_K, 8192, 2048), (E.Q4_K, 8192, 2048), (E.Q4_K, 2048, 8192)]
 
 
+class HipEvents:
+    """HIP events on the null stream (the one the activation-preparation calls below launch on), through the HIP runtime
+    the library itself loaded"""
+
+    def __init__(self):
+        import ctypes
+        self.C = ctypes
+        self.h = ctypes.CDLL("libamdhip64.so")
+
+    def time_ms(self, fn, warmup, iters):
+        C, h = self.C, self.h
+        for _ in range(warmup):
+            fn()
+        a, b = C.c_void_p(), C.c_void_p()
+        if h.hipEventCreate(C.byref(a)) or h.hipEventCreate(C.byref(b)):
+            raise RuntimeError("hipEventCreate failed")
+        h.hipEventRecord(a, None)
+        for _ in range(iters):
+            fn()
+        h.hipEventRecord(b, None)
+        h.hipEventSynchronize(b)
+        ms = C.c_float()
+        h.hipEventElapsedTime(C.byref(ms), a, b)
+        h.hipEventDestroy(a)
+        h.hipEventDestroy(b)
+        return ms.value / iters
+
+
+def act_prep_times(lib, rng, K, Wm):
+    """Device activation preparation at config 2's prefill shapes (T = 512): rmsnorm + Q8_K/Q8_0 of the 2048-wide layer
+    input, SwiGLU + Q8_K of the dense FFN's 8192-wide gate|up rows, and the plain Q8_K/Q8_0 quantizers. us per call
+    (HIP events around K back-to-back calls) and GB/s over the fp32 bytes read plus the block bytes written."""
+    T, n, ff = 512, 2048, 8192
+    ev = HipEvents()
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    gu = rng.standard_normal((T, 2 * ff)).astype(np.float32)
+    dx, dw, dgu = lib.upload(x), lib.upload(w), lib.upload(gu)
+    b80, b8k, h8k = lib.alloc(T * (n // 32) * 36), lib.alloc(T * (n // 256) * 292), lib.alloc(T * (ff // 256) * 292)
+    out = {}
+
+    def rec(name, fn, nbytes):
+        ms = ev.time_ms(fn, Wm, K)
+        out[name] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
+
+    blocks = T * ((n // 32) * 36 + (n // 256) * 292)
+    rec("rmsnorm_q8k_q80_512x2048", lambda: lib.rmsnorm_prepare_dev(dx, 0, dw, 1e-5, T, n, None, 0, b80, 0, b8k, 0),
+        x.nbytes + w.nbytes + blocks)
+    rec("plain_q8k_q80_512x2048", lambda: lib.act_prepare_dev(dx, 0, T, n, b80, 0, b8k, 0), x.nbytes + blocks)
+    rec("swiglu_q8k_512x8192", lambda: lib.swiglu_prepare_dev(dgu, 0, T, ff, None, 0, None, 0, h8k, 0),
+        gu.nbytes + T * (ff // 256) * 292)
+    for buf in (dx, dw, dgu, b80, b8k, h8k):
+        buf.close()
+    return out
+
+
 def only(lib, rng, name, K, Wm):
     """one workload of the bench, alone: the command profiler summaries are taken from"""
     if name == "copy":   # a plain device copy of known size, the reference for HBM byte counters
@@ -243,6 +299,8 @@ def only(lib, rng, name, K, Wm):
         a.close()
         b.close()
         return {"workload": "copy", "bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": Wm + K}
+    if name == "act":
+        return {"workload": "act", **act_prep_times(lib, rng, K, Wm)}
     if name in ("config4", "config5"):
         w = (MoeWorkload(lib, rng, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8) if name == "config4" else
              MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
@@ -268,7 +326,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=2.0)
-    ap.add_argument("--only", choices=["decode", "prefill", "config1", "config3b1", "config3b64", "config4", "config5", "copy"],
+    ap.add_argument("--only", choices=["decode", "prefill", "config1", "config3b1", "config3b64", "config4", "config5", "act",
+                                       "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -331,6 +390,8 @@ def main():
                                          "experts_used": c5.distinct,
                                          "hbm_frac": round(c5.weight_bytes / c5.copies / (e5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     c5.close()
+    # ---- device activation preparation at config 2's prefill shapes (rmsnorm / SwiGLU fused with the quantizers)
+    extra["act_prep_t512"] = act_prep_times(lib, rng, K, Wm)
 
     cpu = None
     if not args.no_cpu:

@@ -211,7 +211,7 @@ int es_hip_act_prepare_dev(const float *x, size_t xstride, int rows, int cols, v
                            size_t q8k_stride, void *stream);
 /* rmsnorm (src/es_engine.c:189-194: the sum of squares in double in element order, s = (float)(1 / sqrt(ss / cols + eps)),
  * xn = x * s * w) fused with the same preparation of xn (the engine's `prep` after its rmsnorm, src/es_engine.c:1284-1292).
- * w may be NULL (weights 1); xn (optional) receives the normalised rows. cols <= 16384. */
+ * w may be NULL (weights 1); xn (optional) receives the normalised rows. cols: a multiple of 32, at most 16384. */
 int es_hip_rmsnorm_prepare_dev(const float *x, size_t xstride, const float *w, float eps, int rows, int cols, float *xn,
                                size_t xn_stride, void *q80, size_t q80_stride, void *q8k, size_t q8k_stride, void *stream);
 /* SwiGLU of gate|up rows as dense_n / moe_n lay them out (gate at [r][0, ff), up at [r][ff, 2 ff); src/es_engine.c:957-972,

@@ -58,48 +58,97 @@ __device__ __forceinline__ void quant_chunk(float v, bool have, int e0, const Qu
     }
 }
 
-// Rows of fp32 values: grid (chunks of 256, rows).
+constexpr int CHUNKS = 4;   // 256-wide chunks per workgroup of the SwiGLU form (all loads issued first)
+
+// Rows of fp32 values: grid (groups of CHUNKS chunks of 256, rows).
+template <int CHUNKS>
 __global__ __launch_bounds__(256) void act_prep_plain(const float *__restrict__ x, uint64_t xs, int cols, uint8_t *q80,
                                                       uint64_t q80s, uint8_t *q8k, uint64_t q8ks) {
     __shared__ float wmax[4];
-    const int r = blockIdx.y, e0 = blockIdx.x * 256, e = e0 + threadIdx.x;
-    const bool have = e < cols;
-    const float v = have ? x[(size_t)r * xs + e] : 0.0f;
-    quant_chunk(v, have, e0, QuantOut{q80 ? q80 + (size_t)r * q80s : nullptr, q8k ? q8k + (size_t)r * q8ks : nullptr}, wmax);
+    const int r = blockIdx.y, c0 = blockIdx.x * CHUNKS;
+    const float *xr = x + (size_t)r * xs;
+    float v[CHUNKS];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) {
+        const int e = (c0 + c) * 256 + threadIdx.x;
+        v[c] = e < cols ? xr[e] : 0.0f;
+    }
+    const QuantOut o{q80 ? q80 + (size_t)r * q80s : nullptr, q8k ? q8k + (size_t)r * q8ks : nullptr};
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) {
+        const int e0 = (c0 + c) * 256;
+        if (e0 >= cols) break;   // uniform
+        quant_chunk(v[c], e0 + (int)threadIdx.x < cols, e0, o, wmax);
+    }
 }
 
-// SwiGLU of gate|up rows (gate at gu[r][0, ff), up at gu[r][ff, 2 ff)): grid (chunks of 256, rows).
+// SwiGLU of gate|up rows (gate at gu[r][0, ff), up at gu[r][ff, 2 ff)): grid (groups of CHUNKS chunks of 256, rows).
 __global__ __launch_bounds__(256) void act_prep_swiglu(const float *__restrict__ gu, uint64_t gs, int ff, float *h, uint64_t hs,
                                                        uint8_t *q80, uint64_t q80s, uint8_t *q8k, uint64_t q8ks) {
     __shared__ float wmax[4];
-    const int r = blockIdx.y, e0 = blockIdx.x * 256, e = e0 + threadIdx.x;
-    const bool have = e < ff;
-    float v = 0.0f;
-    if (have) {
-        const float *g = gu + (size_t)r * gs;
-        v = g[e] / (1.0f + esq_expf(-g[e])) * g[ff + e];
-        if (h) h[(size_t)r * hs + e] = v;
+    const int r = blockIdx.y, c0 = blockIdx.x * CHUNKS;
+    const float *g = gu + (size_t)r * gs;
+    float gv[CHUNKS], uv[CHUNKS];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) {
+        const int e = (c0 + c) * 256 + threadIdx.x;
+        gv[c] = e < ff ? g[e] : 0.0f;
+        uv[c] = e < ff ? g[ff + e] : 0.0f;
     }
-    quant_chunk(v, have, e0, QuantOut{q80 ? q80 + (size_t)r * q80s : nullptr, q8k ? q8k + (size_t)r * q8ks : nullptr}, wmax);
+    const QuantOut o{q80 ? q80 + (size_t)r * q80s : nullptr, q8k ? q8k + (size_t)r * q8ks : nullptr};
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) {
+        const int e0 = (c0 + c) * 256, e = e0 + threadIdx.x;
+        if (e0 >= ff) break;   // uniform
+        const bool have = e < ff;
+        float v = 0.0f;
+        if (have) {
+            v = gv[c] / (1.0f + esq_expf(-gv[c])) * uv[c];
+            if (h) h[(size_t)r * hs + e] = v;
+        }
+        quant_chunk(v, have, e0, o, wmax);
+    }
 }
 
-// rmsnorm, then the blocks: one workgroup per row. The row is staged in LDS; one thread forms the sum of squares in double
-// in element order (the reference's rounding), then every thread takes its elements of each 256-wide chunk.
+// rmsnorm, then the blocks: one workgroup per row. Every thread squares its elements in double (exact) into LDS; one
+// thread adds them in element order (the reference's rounding; the dependent adds are the kernel's critical path), then
+// every thread takes its elements of each 256-wide chunk.
 __global__ __launch_bounds__(256) void act_prep_rms(const float *__restrict__ x, uint64_t xs, const float *__restrict__ w,
                                                     float eps, int cols, float *xn, uint64_t xns, uint8_t *q80, uint64_t q80s,
                                                     uint8_t *q8k, uint64_t q8ks) {
-    extern __shared__ float row[];
+    extern __shared__ __align__(16) double sq[];   // cols squares (the host keeps cols a multiple of 32)
     __shared__ float wmax[4];
     __shared__ float scale;
     const int r = blockIdx.x, i = threadIdx.x;
     const float *xr = x + (size_t)r * xs;
-    for (int e = i; e < cols; e += 256) row[e] = xr[e];
+    for (int e = i; e < cols; e += 256) {
+        const double d = static_cast<double>(xr[e]);
+        sq[e] = d * d;   // exact: a float's square fits a double
+    }
     __syncthreads();
-    if (i == 0) {
+    if (i == 0) {   // two alternating batches of 16 squares: one batch's LDS reads are in flight while the other is added
         double ss = 0.0;
-        for (int e = 0; e < cols; e++) {
-            const double d = static_cast<double>(row[e]);
-            ss = ss + d * d;   // the square is exact in double; the sum rounds, in order
+        const double2 *s2 = reinterpret_cast<const double2 *>(sq);
+        double2 a[8], b[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) a[k] = s2[k];
+        for (int e = 0; e < cols; e += 32) {   // cols is a multiple of 32
+#pragma unroll
+            for (int k = 0; k < 8; k++) b[k] = s2[e / 2 + 8 + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                ss = ss + a[k].x;
+                ss = ss + a[k].y;
+            }
+            if (e + 32 < cols) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) a[k] = s2[e / 2 + 16 + k];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                ss = ss + b[k].x;
+                ss = ss + b[k].y;
+            }
         }
         scale = static_cast<float>(1.0 / __builtin_sqrt(ss / static_cast<double>(cols) + static_cast<double>(eps)));
     }
@@ -111,7 +160,7 @@ __global__ __launch_bounds__(256) void act_prep_rms(const float *__restrict__ x,
         const bool have = e < cols;
         float v = 0.0f;
         if (have) {
-            v = row[e] * s * (w ? w[e] : 1.0f);
+            v = xr[e] * s * (w ? w[e] : 1.0f);
             if (xn) xn[(size_t)r * xns + e] = v;
         }
         quant_chunk(v, have, e0, o, wmax);
@@ -123,23 +172,28 @@ __global__ __launch_bounds__(256) void act_prep_rms(const float *__restrict__ x,
 hipError_t act_prep_launch(const float *x, uint64_t xs, int rows, int cols, uint8_t *q80, uint64_t q80s, uint8_t *q8k,
                            uint64_t q8ks, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(act_prep_plain, dim3((cols + 255) / 256, rows), dim3(256), 0, s, x, xs, cols, q80, q80s, q8k, q8ks);
+    hipLaunchKernelGGL(act_prep_plain<1>, dim3((cols + 255) / 256, rows), dim3(256), 0, s, x, xs, cols, q80, q80s, q8k, q8ks);
     return hipGetLastError();
 }
 
 hipError_t act_prep_swiglu_launch(const float *gu, uint64_t gs, int rows, int ff, float *h, uint64_t hs, uint8_t *q80,
                                   uint64_t q80s, uint8_t *q8k, uint64_t q8ks, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(act_prep_swiglu, dim3((ff + 255) / 256, rows), dim3(256), 0, s, gu, gs, ff, h, hs, q80, q80s, q8k,
-                       q8ks);
+    hipLaunchKernelGGL(act_prep_swiglu, dim3((ff + 256 * CHUNKS - 1) / (256 * CHUNKS), rows), dim3(256), 0, s, gu, gs, ff, h, hs,
+                       q80, q80s, q8k, q8ks);
     return hipGetLastError();
 }
 
 hipError_t act_prep_rms_launch(const float *x, uint64_t xs, const float *w, float eps, int rows, int cols, float *xn,
                                uint64_t xns, uint8_t *q80, uint64_t q80s, uint8_t *q8k, uint64_t q8ks, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(act_prep_rms, dim3(rows), dim3(256), (size_t)cols * sizeof(float), s, x, xs, w, eps, cols, xn, xns,
-                       q80, q80s, q8k, q8ks);
+    const size_t lds = (size_t)cols * sizeof(double);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(act_prep_rms), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(act_prep_rms, dim3(rows), dim3(256), lds, s, x, xs, w, eps, cols, xn, xns, q80, q80s, q8k, q8ks);
     return hipGetLastError();
 }
 

@@ -125,7 +125,7 @@ hipError_t moe_combine_launch(const float *ye, const int *rowof, const float *w,
                               float *out, uint64_t ostride, hipStream_t s);
 hipError_t swiglu_plain_launch(const float *g, const float *u, float *h, long n, hipStream_t s);
 
-constexpr int ACT_RMS_MAX_COLS = 16384;   // rmsnorm rows are staged whole in LDS (64 KB)
+constexpr int ACT_RMS_MAX_COLS = 16384;   // rmsnorm rows' squares are staged whole in LDS (128 KB of doubles)
 // Activation preparation (es_hip_act.hip): rows of fp32 values (plain, rmsnorm-ed, or the SwiGLU of gate|up rows) into
 // Q8_0 and / or Q8_K blocks (either output may be null). Float strides in floats, block strides in bytes.
 hipError_t act_prep_launch(const float *x, uint64_t xs, int rows, int cols, uint8_t *q80, uint64_t q80s, uint8_t *q8k,

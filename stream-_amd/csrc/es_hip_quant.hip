@@ -1258,7 +1258,8 @@ int es_hip_rmsnorm_prepare_dev(const float *x, size_t xstride, const float *w, f
     if (int rc = need_device()) return rc;
     if (int rc = prep_blocks(rows, cols, q80, q80_stride, q8k, q8k_stride)) return rc;
     if (!xn && !q80 && !q8k) return fail(ES_HIP_EINVAL, "no output asked for");
-    if (cols > esq::ACT_RMS_MAX_COLS) return fail(ES_HIP_EINVAL, "rmsnorm rows of %d values: above %d", cols, esq::ACT_RMS_MAX_COLS);
+    if (cols > esq::ACT_RMS_MAX_COLS || cols % 32)
+        return fail(ES_HIP_EINVAL, "rmsnorm rows of %d values: a multiple of 32 up to %d is needed", cols, esq::ACT_RMS_MAX_COLS);
     if (rows == 0) return ES_HIP_OK;
     if (!x) return fail(ES_HIP_EINVAL, "null x");
     if (int rc = prep_floats("x", x, xstride, rows, (size_t)cols)) return rc;

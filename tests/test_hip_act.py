@@ -127,3 +127,5 @@ def test_act_prepare_rejects_bad_arguments(hip):
         hip.act_prepare_dev(dx, 0, 2, 256, None, 0, None, 0)       # nothing asked for
     with pytest.raises(E.EsHipError):
         hip.rmsnorm_prepare_dev(dx, 0, None, 1e-5, 1, 16640, None, 0, d, 0, None, 0)   # above the LDS-staged row length
+    with pytest.raises(E.EsHipError):
+        hip.rmsnorm_prepare_dev(dx, 0, None, 1e-5, 1, 100, d, 0, None, 0, None, 0)      # not a multiple of 32
