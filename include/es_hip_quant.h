@@ -218,6 +218,14 @@ int es_hip_rmsnorm_prepare_dev(const float *x, size_t xstride, const float *w, f
  * 913-914), h = g / (1 + expf(-g)) * u, fused with the preparation of h; h (optional) receives the values. */
 int es_hip_swiglu_prepare_dev(const float *gu, size_t gu_stride, int rows, int ff, float *h, size_t h_stride, void *q80,
                               size_t q80_stride, void *q8k, size_t q8k_stride, void *stream);
+/* route() for softmax gating on the device (src/es_engine.c:744-835, its GATE_SOFTMAX path: no gate bias, selection bias,
+ * expert groups, cache bonus or top-k override): for each of ntok tokens, the softmax of its n_exp logits (expf(l - max),
+ * summed in expert order, divided), the k largest probabilities by repeated argmax with ties to the lowest expert into
+ * sel[t * kmax + j] / w[t * kmax + j], and with norm_topk the weights divided by max(their sum, 2^-14). The results are the
+ * reference's bit for bit, so es_hip_moe_ffn / es_hip_moe_plan_create can take them as they are. Device pointers;
+ * n_exp <= 1024, k <= 64, k <= n_exp, k <= kmax; lstride in floats (0: n_exp). */
+int es_hip_route_softmax_dev(const float *logits, size_t lstride, int ntok, int n_exp, int k, int norm_topk, int *sel, float *w,
+                             int kmax, void *stream);
 /* The MoE SwiGLU alone on n device floats: h[i] = g[i] / (1 + expf(-g[i])) * u[i] as src/es_engine.c:913 computes it. */
 int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream);
 /* Average kernel time in milliseconds of `iters` back-to-back runs of a plan, measured with HIP events on `stream`

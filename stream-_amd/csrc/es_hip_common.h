@@ -124,6 +124,11 @@ hipError_t moe_swiglu_launch(const float *gu, int rows, int ff, bool q8k, uint8_
 hipError_t moe_combine_launch(const float *ye, const int *rowof, const float *w, const int *k, int kmax, int ntok, int n,
                               float *out, uint64_t ostride, hipStream_t s);
 hipError_t swiglu_plain_launch(const float *g, const float *u, float *h, long n, hipStream_t s);
+// route() with softmax gating for ntok tokens of ne <= ROUTE_MAX_EXPERTS logits (rows ls floats apart): sel / w rows of
+// kmax, the first k filled (k <= 64).
+constexpr int ROUTE_MAX_EXPERTS = 1024;
+hipError_t route_softmax_launch(const float *logits, uint64_t ls, int ntok, int ne, int k, int norm_topk, int *sel, float *w,
+                                int kmax, hipStream_t s);
 
 constexpr int ACT_RMS_MAX_COLS = 16384;   // rmsnorm rows' squares are staged whole in LDS (128 KB of doubles)
 // Activation preparation (es_hip_act.hip): rows of fp32 values (plain, rmsnorm-ed, or the SwiGLU of gate|up rows) into

@@ -68,6 +68,71 @@ __global__ __launch_bounds__(256) void moe_combine(const float *__restrict__ ye,
     out[(size_t)t * ostride + i] = s;
 }
 
+// route() for softmax gating (src/es_engine.c:744-835, the GATE_SOFTMAX path: no gate bias, selection bias, expert groups,
+// cache bonus or top-k override): one wave per token. The maximum and every argmax are exact in any order (ties go to the
+// lowest expert, as the reference's first-maximum scan does); the two sums (softmax denominator over the experts, chosen
+// weights over the picks) run on one lane in the reference's order.
+__global__ __launch_bounds__(64) void route_softmax(const float *__restrict__ logits, uint64_t ls, int ne, int k, int norm_topk,
+                                                    int *__restrict__ sel, float *__restrict__ w, int kmax) {
+    __shared__ float p[ROUTE_MAX_EXPERTS];
+    __shared__ float total;
+    const int t = blockIdx.x, l = threadIdx.x;
+    const float *r = logits + (size_t)t * ls;
+    float mx = -__builtin_inff();
+    for (int e = l; e < ne; e += 64) {
+        const float v = r[e];
+        p[e] = v;
+        mx = v > mx ? v : mx;   // mx = r[e] > mx ? r[e] : mx (:753)
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float m = __shfl_xor(mx, o);
+        mx = m > mx ? m : mx;
+    }
+    for (int e = l; e < ne; e += 64) p[e] = esq_expf(p[e] - mx);
+    __syncthreads();
+    if (l == 0) {
+        float sum = 0.0f;
+        for (int e = 0; e < ne; e++) sum += p[e];   // :754, in expert order
+        total = sum;
+    }
+    __syncthreads();
+    const float sum = total;
+    for (int e = l; e < ne; e += 64) p[e] /= sum;   // :755
+    __syncthreads();
+    // k rounds of argmax over the experts not yet taken (:794-804); taken experts are marked in a lane's own bit mask
+    uint32_t taken = 0;   // bit m: expert l + 64 m (ne <= 1024: 16 per lane)
+    float wsum = 0.0f, wj = 0.0f;
+    for (int j = 0; j < k; j++) {
+        float bv = 0.0f;
+        int be = -1;
+        for (int m = 0, e = l; e < ne; m++, e += 64) {
+            const float v = p[e];
+            if (!((taken >> m) & 1u) && (be < 0 || v > bv)) { bv = v; be = e; }
+        }
+        for (int o = 32; o > 0; o >>= 1) {   // the larger value, the lower expert on a tie; lanes without a candidate lose
+            const float ov = __shfl_xor(bv, o);
+            const int oe = __shfl_xor(be, o);
+            if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) { bv = ov; be = oe; }
+        }
+        if ((be & 63) == l) taken |= 1u << (be >> 6);
+        if (l == 0) {
+            sel[(size_t)t * kmax + j] = be;
+            wsum += bv;   // w[j] = r[best]; wsum += w[j] (:802-803)
+        }
+        if (l == j) wj = bv;
+    }
+    if (l == 0) total = norm_topk ? (wsum > 6.103515625e-5f ? wsum : 6.103515625e-5f) : 1.0f;   // :832
+    __syncthreads();
+    if (l < k) w[(size_t)t * kmax + l] = norm_topk ? wj / total : wj;
+}
+
+hipError_t route_softmax_launch(const float *logits, uint64_t ls, int ntok, int ne, int k, int norm_topk, int *sel, float *w,
+                                int kmax, hipStream_t s) {
+    if (ntok <= 0) return hipSuccess;
+    hipLaunchKernelGGL(route_softmax, dim3(ntok), dim3(64), 0, s, logits, ls, ne, k, norm_topk, sel, w, kmax);
+    return hipGetLastError();
+}
+
 hipError_t moe_swiglu_launch(const float *gu, int rows, int ff, bool q8k, uint8_t *ha, uint64_t hstride, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (q8k) hipLaunchKernelGGL(swiglu_q8k, dim3(ff / 256, rows), dim3(256), 0, s, gu, ff, ha, hstride);

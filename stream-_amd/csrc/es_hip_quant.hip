@@ -1287,6 +1287,22 @@ int es_hip_swiglu_prepare_dev(const float *gu, size_t gu_stride, int rows, int f
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "SwiGLU preparation launch");
 }
 
+int es_hip_route_softmax_dev(const float *logits, size_t lstride, int ntok, int n_exp, int k, int norm_topk, int *sel, float *w,
+                             int kmax, void *stream) {
+    if (int rc = need_device()) return rc;
+    if (ntok < 0 || n_exp <= 0 || n_exp > esq::ROUTE_MAX_EXPERTS || k <= 0 || k > 64 || k > n_exp || kmax < k)
+        return fail(ES_HIP_EINVAL, "bad routing shape: %d tokens, %d experts, top %d of rows of %d", ntok, n_exp, k, kmax);
+    if (ntok == 0) return ES_HIP_OK;
+    if (!logits || !sel || !w) return fail(ES_HIP_EINVAL, "null logits, sel or w");
+    if (!lstride) lstride = (size_t)n_exp;
+    if (ntok > 1 && lstride < (size_t)n_exp) return fail(ES_HIP_EINVAL, "logit stride %zu < %d", lstride, n_exp);
+    if ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(sel) | reinterpret_cast<uintptr_t>(w)) & 3)
+        return fail(ES_HIP_EINVAL, "logits, sel and w must be 4-byte aligned");
+    hipError_t e = esq::route_softmax_launch(logits, lstride, ntok, n_exp, k, norm_topk, sel, w, kmax,
+                                             static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "routing launch");
+}
+
 int es_hip_swiglu_dev(const float *g, const float *u, float *h, long n, void *stream) {
     if (int rc = need_device()) return rc;
     if (n < 0 || (n > 0 && (!g || !u || !h))) return fail(ES_HIP_EINVAL, "bad SwiGLU arguments");

@@ -125,6 +125,7 @@ class Lib:
             ("es_hip_step_time_ms", C.c_double, [vp, i, vp, i, i, i, vp]),
             ("es_hip_swiglu_dev", i, [vp, vp, vp, C.c_long, vp]),
             ("es_hip_act_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp]),
+            ("es_hip_route_softmax_dev", i, [vp, sz, i, i, i, i, vp, vp, i, vp]),
             ("es_hip_rmsnorm_prepare_dev", i, [vp, sz, vp, C.c_float, i, i, vp, sz, vp, sz, vp, sz, vp]),
             ("es_hip_swiglu_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp, sz, vp]),
         ]:
@@ -248,6 +249,10 @@ class Lib:
 
     def swiglu_dev(self, g, u, h, n, stream=None):
         self._check(self._L.es_hip_swiglu_dev(int(g), int(u), int(h), n, stream))
+
+    def route_softmax_dev(self, logits, lstride, ntok, n_exp, k, norm_topk, sel, w, kmax, stream=None):
+        self._check(self._L.es_hip_route_softmax_dev(int(logits), lstride, ntok, n_exp, k, int(norm_topk), int(sel), int(w),
+                                                     kmax, stream))
 
     # ---- activation preparation on the device (device pointers as DevBuf / ints; None for an output not wanted) ----
     @staticmethod
