@@ -6,8 +6,8 @@
  *   src/es_quant.h:25-49    es_act_prepare / es_matvec / es_matvec_multi / es_row_bytes / es_quant_supported
  *   src/es_q2k.h:24-86      the Q2_K / Q8_K block structs, es_quantize_q8_K, es_matvec_q2_K
  *   src/es_compute.h:10-25  the thread pool that fans a queue of row jobs out to cores (driven by src/es_engine.c:144-186)
- * This library computes the same products on one MI355X for the GGUF formats Q4_0, Q5_0, Q4_K, Q6_K and Q2_K against the
- * reference's Q8 activations, with the packed weight blocks kept byte-for-byte in device memory.
+ * This library computes the same products on one MI355X for the GGUF formats Q4_0, Q5_0, Q8_0, Q4_K, Q6_K and Q2_K against
+ * the reference's Q8 activations, with the packed weight blocks kept byte-for-byte in device memory.
  *
  * Results. The integer block dots are exact. The fp32 epilogue is evaluated in the reference's own order, so outputs are
  * bit-identical to the reference's CPU kernels in the selected build flavour (es_hip_set_order):
@@ -17,7 +17,7 @@
  *
  * Conventions (same as the reference): every buffer belongs to the caller; W points at row 0 of a row-major matrix whose row
  * stride is es_hip_row_bytes(type, cols); outputs are written only for rows [r0, r1), at absolute row indices, activation q's
- * result at y + q * ystride. Activation blocks are the reference's: Q8_0 (36 bytes: float d, int8 qs[32]) for Q4_0/Q5_0 and
+ * result at y + q * ystride. Activation blocks are the reference's: Q8_0 (36 bytes: float d, int8 qs[32]) for Q4_0/Q5_0/Q8_0 and
  * Q8_K (292 bytes: float d, int8 qs[256], int16 bsums[16]) for Q2_K/Q4_K/Q6_K.
  *
  * Errors. The reference's entry points return void and cannot fail. Here the device-pointer entry points return 0 on success
@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 /* GGML type ids of the formats computed here (reference src/es_quant.h:15-22) */
-enum { ES_HIP_Q4_0 = 2, ES_HIP_Q5_0 = 6, ES_HIP_Q2_K = 10, ES_HIP_Q4_K = 12, ES_HIP_Q6_K = 14 };
+enum { ES_HIP_Q4_0 = 2, ES_HIP_Q5_0 = 6, ES_HIP_Q8_0 = 8, ES_HIP_Q2_K = 10, ES_HIP_Q4_K = 12, ES_HIP_Q6_K = 14 };
 
 /* fp32 epilogue order, see the header comment */
 enum { ES_HIP_ORDER_X86_CONTRACT = 0, ES_HIP_ORDER_X86_STRICT = 1, ES_HIP_ORDER_SCALAR = 2 };
@@ -119,7 +119,7 @@ void         es_hip_plan_destroy(es_hip_plan *plan);
 int es_hip_register(const void *host, size_t bytes);
 int es_hip_update(const void *host);
 int es_hip_unregister(const void *host);
-/* es_matvec / es_matvec_multi (src/es_quant.h:44-47): host W, host activations (a->q80 for Q4_0/Q5_0, a->q8 for the K-quants),
+/* es_matvec / es_matvec_multi (src/es_quant.h:44-47): host W, host activations (a->q80 for Q4_0/Q5_0/Q8_0, a->q8 for the K-quants),
  * host y. Synchronous. The scratch argument is unused (kept for the prototype). They clear es_hip_last_error() on entry;
  * on failure y is left untouched and es_hip_last_error() says why (the reference's void prototype has no other error
  * channel). */
@@ -153,7 +153,7 @@ typedef struct {
 } es_hip_moe;
 /* The expert FFN of N tokens routed by route() (src/es_engine.c:744-835): token t's k[t] <= kmax experts are
  * sel[t * kmax + j] with weights w[t * kmax + j] (host arrays). x: device activation blocks of the N tokens (Q8_K for a
- * K-quant gate/up, Q8_0 for Q4_0/Q5_0), token t at x + t * xstride bytes (0: packed). out: device, token t's n outputs at
+ * K-quant gate/up, Q8_0 for Q4_0/Q5_0/Q8_0), token t at x + t * xstride bytes (0: packed). out: device, token t's n outputs at
  * out + t * ostride floats. In stream order on the device:
  *   the pairs (t, j) are grouped by expert in order of first use (:871-888);
  *   gate and up products of every pair into [pair][2 ff] (:899-903), one launch per format;
@@ -174,7 +174,7 @@ void   es_hip_moe_plan_destroy(es_hip_moe_plan *plan);
 
 /* ---- diagnostics ----------------------------------------------------------------------------------------------------- */
 /* The integer part of every (row, block) of rows [0, rows) against one activation, as the reference's kernels form it:
- * dots[r * nb + b] = the block's integer dot (Q4_0/Q5_0: the sum of the eight AVX2 lane sums; Q4_K: dot; Q6_K: tot;
+ * dots[r * nb + b] = the block's integer dot (Q4_0/Q5_0/Q8_0: the sum of the eight AVX2 lane sums; Q4_K: dot; Q6_K: tot;
  * Q2_K: isum) and aux[r * nb + b] = Q4_K mins or Q2_K summs (0 for the others). nb = cols / block elements. Device memory. */
 int es_hip_block_ints_dev(uint32_t type, const void *W, int cols, int rows, const void *act, int32_t *dots, int32_t *aux,
                           void *stream);
@@ -190,7 +190,7 @@ int es_hip_set_small_batch_min(int n);
  * waves, one of 128 x 128 x 8, 128 x 64 x 8, 64 x 64 x 8, 64 x 64 x 4, 32 x 128 x 4; (0, 0, 0) restores the automatic
  * choice (128 x 128 when that gives every CU a workgroup, else 64 x 64 x 8). Returns ES_HIP_OK or ES_HIP_EINVAL. */
 int es_hip_set_mfma_tile(int bm, int bn, int waves);
-/* Q4_0 / Q5_0 products with at least n activations run on the batched kernel (one lane per row and activation) instead of
+/* Q4_0 / Q5_0 / Q8_0 products with at least n activations run on the batched kernel (one lane per row and activation) instead of
  * the vector kernel (default 2). */
 int es_hip_set_batched32_min(int n);
 /* Of those, products with at least n activations run on the batched matrix-core kernel (one int8 MFMA per block forms the

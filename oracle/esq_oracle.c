@@ -19,7 +19,7 @@
 
 int esq_block_elems(uint32_t t) {
     switch (t) {
-    case ESQ_Q4_0: case ESQ_Q5_0: return 32;
+    case ESQ_Q4_0: case ESQ_Q5_0: case ESQ_Q8_0: return 32;
     case ESQ_Q2_K: case ESQ_Q4_K: case ESQ_Q6_K: return 256;
     }
     return 0;
@@ -29,6 +29,7 @@ int esq_block_bytes(uint32_t t) {
     switch (t) {
     case ESQ_Q4_0: return 18;   /* d f16, qs[16]                              src/es_quant.c:12 */
     case ESQ_Q5_0: return 22;   /* d f16, qh[4], qs[16]                       src/es_quant.c:14 */
+    case ESQ_Q8_0: return 34;   /* d f16, int8 qs[32]                         src/es_quant.c:11 */
     case ESQ_Q2_K: return 84;   /* scales[16], qs[64], d, dmin                src/es_q2k.h:24-29 */
     case ESQ_Q4_K: return 144;  /* d, dmin, scales[12], qs[128]               src/es_quant.c:17 */
     case ESQ_Q6_K: return 210;  /* ql[128], qh[64], int8 scales[16], d        src/es_quant.c:19 */
@@ -161,6 +162,21 @@ void esq_blkdot_q5_0(const uint8_t *blk, const esq_q80 *y, int32_t lane[8]) {
     }
 }
 
+void esq_blkdot_q8_0(const uint8_t *blk, const esq_q80 *y, int32_t lane[8]) {
+    const int8_t *qs = (const int8_t *)(blk + 2);
+    for (int i = 0; i < 8; i++) {   /* AVX2 lane i sums elements 4i..4i+3 (dot32_ss, src/es_quant.c:1198-1221) */
+        int32_t a = 0;
+        for (int m = 0; m < 4; m++) a += qs[4 * i + m] * y->qs[4 * i + m];
+        lane[i] = a;
+    }
+}
+
+static void blkdot_32(uint32_t t, const uint8_t *blk, const esq_q80 *y, int32_t lane[8]) {
+    if (t == ESQ_Q4_0) esq_blkdot_q4_0(blk, y, lane);
+    else if (t == ESQ_Q5_0) esq_blkdot_q5_0(blk, y, lane);
+    else esq_blkdot_q8_0(blk, y, lane);
+}
+
 void esq_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *mn) {
     if (j < 4) {
         *sc = q[j] & 63;
@@ -232,26 +248,26 @@ int32_t esq_blkdot_q2_K(const uint8_t *blk, const esq_q8K *y, int32_t *summs) {
 /* rows                                                                                                                */
 
 /* x86 AVX2 32-wide path: 8 fused lane accumulators per row, then the hsum_ps tree (src/es_quant.c:1185-1187,
- * 1262-1285, 1297-1323). _mm256_fmadd_ps is fused under either compiler, so order does not matter here. */
+ * 1198-1221, 1262-1285, 1297-1323). _mm256_fmadd_ps is fused under either compiler, so order does not matter here. */
 static float row_32_x86(uint32_t t, const uint8_t *w, int nb, const esq_q80 *y) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int b = 0; b < nb; b++) {
         const uint8_t *blk = w + (size_t)b * esq_block_bytes(t);
         int32_t lane[8];
-        if (t == ESQ_Q4_0) esq_blkdot_q4_0(blk, &y[b], lane); else esq_blkdot_q5_0(blk, &y[b], lane);
+        blkdot_32(t, blk, &y[b], lane);
         const float dyd = esq_half_to_float(rd16(blk)) * y[b].d;
         for (int i = 0; i < 8; i++) acc[i] = fmaf((float)lane[i], dyd, acc[i]);
     }
     return ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
 }
 
-/* scalar 32-wide path: one integer per block, s += (d*yd)*a (src/es_quant.c:1013-1055) */
+/* scalar 32-wide path: one integer per block, s += (d*yd)*a (src/es_quant.c:1005-1055) */
 static float row_32_scalar(uint32_t t, const uint8_t *w, int nb, const esq_q80 *y) {
     float s = 0.0f;
     for (int b = 0; b < nb; b++) {
         const uint8_t *blk = w + (size_t)b * esq_block_bytes(t);
         int32_t lane[8], a = 0;
-        if (t == ESQ_Q4_0) esq_blkdot_q4_0(blk, &y[b], lane); else esq_blkdot_q5_0(blk, &y[b], lane);
+        blkdot_32(t, blk, &y[b], lane);
         for (int i = 0; i < 8; i++) a += lane[i];
         const float dd = esq_half_to_float(rd16(blk)) * y[b].d;
         s = s + dd * (float)a;
@@ -320,6 +336,7 @@ void esq_block_ints(uint32_t t, const void *W, int cols, int rows, const void *a
             switch (t) {
             case ESQ_Q4_0: esq_blkdot_q4_0(blk, (const esq_q80 *)act + b, lane); for (int i = 0; i < 8; i++) v += lane[i]; break;
             case ESQ_Q5_0: esq_blkdot_q5_0(blk, (const esq_q80 *)act + b, lane); for (int i = 0; i < 8; i++) v += lane[i]; break;
+            case ESQ_Q8_0: esq_blkdot_q8_0(blk, (const esq_q80 *)act + b, lane); for (int i = 0; i < 8; i++) v += lane[i]; break;
             case ESQ_Q4_K: v = esq_blkdot_q4_K(blk, (const esq_q8K *)act + b, &x); break;
             case ESQ_Q6_K: v = esq_blkdot_q6_K(blk, (const esq_q8K *)act + b); break;
             case ESQ_Q2_K: v = esq_blkdot_q2_K(blk, (const esq_q8K *)act + b, &x); break;
@@ -340,6 +357,11 @@ void esq_dequant_row(uint32_t t, const void *src, float *y, int n) {
         case ESQ_Q4_0: {   /* (x-8)*d, src/es_quant.c:433-449 */
             const float d = esq_half_to_float(rd16(p));
             for (int e = 0; e < 32; e++) *y++ = (float)(nib32(p + 2, e) - 8) * d;
+            break;
+        }
+        case ESQ_Q8_0: {   /* d*q, src/es_quant.c:425-431 */
+            const float d = esq_half_to_float(rd16(p));
+            for (int e = 0; e < 32; e++) *y++ = d * (float)(int8_t)p[2 + e];
             break;
         }
         case ESQ_Q5_0: {   /* (x-16)*d, src/es_quant.c:451-468 */
@@ -441,6 +463,14 @@ void esq_quantize_row(uint32_t t, const float *x, void *dst, int n) {
     uint8_t *p = (uint8_t *)dst;
     switch (t) {
     case ESQ_Q2_K: esq_quantize_q2_K_ref(x, dst, n); return;
+    case ESQ_Q8_0:   /* symmetric: d = amax/127, code = round(x/d) */
+        for (int b = 0; b < n / 32; b++, x += 32, p += 34) {
+            const uint16_t dh = esq_float_to_half(absmax(x, 32) / 127.0f);
+            wr16(p, dh);
+            const float d = esq_half_to_float(dh);
+            for (int e = 0; e < 32; e++) p[2 + e] = (uint8_t)(int8_t)(d > 0 ? clampi(lrintf(x[e] / d), -127, 127) : 0);
+        }
+        return;
     case ESQ_Q4_0: case ESQ_Q5_0: {   /* symmetric: d = amax/(2^(bits-1)-1), code = round(x/d) + offset */
         const int five = t == ESQ_Q5_0, off = five ? 16 : 8, top = five ? 31 : 15, bb = five ? 22 : 18;
         for (int b = 0; b < n / 32; b++, x += 32, p += bb) {

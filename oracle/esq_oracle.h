@@ -5,7 +5,7 @@
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use. Every function restates the arithmetic of the
  * reference (Tharunmaks/Stream-, "ExpertStream") in plain C and cites the reference lines it follows.
  *
- * Formats covered: Q4_0, Q5_0, Q4_K, Q6_K, Q2_K weights against Q8_0 (float scale, 36 B) and Q8_K (292 B) activations.
+ * Formats covered: Q4_0, Q5_0, Q8_0, Q4_K, Q6_K, Q2_K weights against Q8_0 (float scale, 36 B) and Q8_K (292 B) activations.
  *
  * Float order. The reference's fp32 epilogues are compiler dependent (its Makefile defaults to clang, which contracts
  * a*b+c into an FMA inside the AVX2 functions; gcc in -std=c11 mode does not). Every matvec here takes
@@ -40,7 +40,7 @@ extern "C" {
 #endif
 
 /* GGML type ids used by the path (reference src/es_quant.h:15-22) */
-enum { ESQ_Q4_0 = 2, ESQ_Q5_0 = 6, ESQ_Q2_K = 10, ESQ_Q4_K = 12, ESQ_Q6_K = 14 };
+enum { ESQ_Q4_0 = 2, ESQ_Q5_0 = 6, ESQ_Q8_0 = 8, ESQ_Q2_K = 10, ESQ_Q4_K = 12, ESQ_Q6_K = 14 };
 enum { ESQ_STRICT = 0, ESQ_CONTRACT = 1 };
 enum { ESQ_PATH_X86 = 0, ESQ_PATH_SCALAR = 1 };
 
@@ -50,7 +50,7 @@ typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } esq_q8K;
 
 /* ---- format facts ---- */
 int    esq_block_elems(uint32_t type);          /* 32 or 256; 0 if unknown */
-int    esq_block_bytes(uint32_t type);          /* 18, 22, 144, 210, 84 */
+int    esq_block_bytes(uint32_t type);          /* 18, 22, 34, 144, 210, 84 */
 size_t esq_row_bytes(uint32_t type, int cols); /* src/es_quant.c:39-73 */
 int    esq_uses_q8K(uint32_t type);            /* 1: Q8_K activations, 0: Q8_0 */
 
@@ -66,6 +66,7 @@ void esq_quantize_q8_K(const float *x, esq_q8K *y, int n); /* src/es_q2k.c:102-1
 /* 32-wide: the eight AVX2 lane sums (4 weights each, offset already removed); their sum is the scalar integer dot */
 void    esq_blkdot_q4_0(const uint8_t *blk, const esq_q80 *y, int32_t lane[8]);
 void    esq_blkdot_q5_0(const uint8_t *blk, const esq_q80 *y, int32_t lane[8]);
+void    esq_blkdot_q8_0(const uint8_t *blk, const esq_q80 *y, int32_t lane[8]);
 int32_t esq_blkdot_q4_K(const uint8_t *blk, const esq_q8K *y, int32_t *mins);
 int32_t esq_blkdot_q6_K(const uint8_t *blk, const esq_q8K *y);
 int32_t esq_blkdot_q2_K(const uint8_t *blk, const esq_q8K *y, int32_t *summs);

@@ -1,4 +1,4 @@
-// Batched 32-wide formats (Q4_0 / Q5_0 against many activations) on the matrix cores.
+// Batched 32-wide formats (Q4_0 / Q5_0 / Q8_0 against many activations) on the matrix cores.
 //
 // The reference's AVX2 path forms, per 32-element block, eight integer lane sums lane_i = sum over elements 4i..4i+3 of
 // (code - offset) * y and folds them into eight fused chains acc_i = fma((float)lane_i, d * yd, acc_i) in block order,
@@ -34,10 +34,24 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 template <int F> struct Mb32Fmt;
 // Q4_0: d f16 @0, qs[16] @2; codes 0..15, offset 8. Q5_0: d f16 @0, qh u32 @2, qs[16] @6; codes 0..31, offset 16.
+// Q8_0: d f16 @0, int8 qs[32] @2 (BYTES: group i's four codes are dword i, taken as c + 128 in 0..255, offset 128).
 // NEG: the half pair -(1024 + offset): a code c under the exponent of 1024 (bits 0x6400 | c) is 1024 + c, so adding NEG
 // gives c - offset exactly.
-template <> struct Mb32Fmt<ES_HIP_Q4_0> { static constexpr int QS = 2, QH = -1; static constexpr uint32_t NEG = 0xe408e408u; };
-template <> struct Mb32Fmt<ES_HIP_Q5_0> { static constexpr int QS = 6, QH = 2; static constexpr uint32_t NEG = 0xe410e410u; };
+template <> struct Mb32Fmt<ES_HIP_Q4_0> {
+    static constexpr int QS = 2, QH = -1;
+    static constexpr bool BYTES = false;
+    static constexpr uint32_t NEG = 0xe408e408u;
+};
+template <> struct Mb32Fmt<ES_HIP_Q5_0> {
+    static constexpr int QS = 6, QH = 2;
+    static constexpr bool BYTES = false;
+    static constexpr uint32_t NEG = 0xe410e410u;
+};
+template <> struct Mb32Fmt<ES_HIP_Q8_0> {
+    static constexpr int QS = 2, QH = -1;
+    static constexpr bool BYTES = true;
+    static constexpr uint32_t NEG = 0xe480e480u;
+};
 
 struct Stage {
     uint32_t w0, w1;   // the aligned dwords at and after the block's start: d (and Q5_0 qh)
@@ -87,7 +101,8 @@ __global__ __launch_bounds__(256) void mb32m_kernel(const MbJob *__restrict__ jo
         const uint32_t start = rowoff + e * BB;   // block e of the row
         mis[e] = start & 2u;
         woff[e] = start - mis[e];
-        const uint32_t f = mis[e] + Mb32Fmt<F>::QS + 4 * gq, fa = f & ~3u, last = (mis[e] + BB - 1) & ~3u;
+        const uint32_t f = mis[e] + Mb32Fmt<F>::QS + 4 * (Mb32Fmt<F>::BYTES ? gi : gq), fa = f & ~3u,
+                       last = (mis[e] + BB - 1) & ~3u;
         qaoff[e] = woff[e] + fa;
         qboff[e] = woff[e] + (fa + 4 <= last ? fa + 4 : fa);
     }
@@ -112,7 +127,9 @@ __global__ __launch_bounds__(256) void mb32m_kernel(const MbJob *__restrict__ jo
     auto issue = [&](const Stage &c, int e, Issued &o) {
         const uint32_t m = mis[e];
         const uint32_t qs = alignbyte(c.qb, c.qa, m ^ 2u);   // the code dword is misaligned exactly when the block is not
-        uint32_t q = (qs >> nshift) & 0x0f0f0f0fu;
+        uint32_t q;
+        if constexpr (Mb32Fmt<F>::BYTES) q = qs ^ 0x80808080u;   // signed code + 128, per byte
+        else q = (qs >> nshift) & 0x0f0f0f0fu;
         if constexpr (F == ES_HIP_Q5_0) {   // bit e of qh -> bit 4 of byte e; qh starts 2 bytes into the block
             const uint64_t hw = (static_cast<uint64_t>(c.w1) << 32 | c.w0) >> (16 + 8 * m + 4 * gi);
             q |= (((static_cast<uint32_t>(hw) & 15u) * 0x00204081u) & 0x01010101u) << 4;
@@ -209,6 +226,7 @@ hipError_t mb32m_launch(int type, const MbJob *jobs, int njobs, const MbJob &sin
     const bool x86 = order != ES_HIP_ORDER_SCALAR;
     if (type == ES_HIP_Q4_0) launch<ES_HIP_Q4_0>(x86, jobs, njobs, single, grid, s);
     else if (type == ES_HIP_Q5_0) launch<ES_HIP_Q5_0>(x86, jobs, njobs, single, grid, s);
+    else if (type == ES_HIP_Q8_0) launch<ES_HIP_Q8_0>(x86, jobs, njobs, single, grid, s);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

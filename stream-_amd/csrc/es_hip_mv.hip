@@ -232,14 +232,14 @@ template <> struct Lane<ES_HIP_Q2_K> {
     }
 };
 
-// Q4_0 / Q5_0: one lane per 32-element block. AVX2 lane i of the reference sums elements 4i..4i+3 (one v_dot4 here):
-// lane_i = sum (code - offset) * y over those four elements, formed as dot(code, y) - offset * sum(y).
-// src/es_quant.c:1013-1055 (scalar), 1252-1323 (AVX2).
+// Q4_0 / Q5_0 / Q8_0: one lane per 32-element block. AVX2 lane i of the reference sums elements 4i..4i+3 (one v_dot4
+// here): lane_i = sum (code - offset) * y over those four elements, formed as dot(code, y) - offset * sum(y) (Q8_0: the
+// stored int8 codes, offset 0). src/es_quant.c:1005-1055 (scalar), 1198-1221, 1252-1323 (AVX2).
 template <int F> struct Lane32 {
-    static constexpr int OFF = F == ES_HIP_Q4_0 ? 8 : 16;
+    static constexpr int OFF = F == ES_HIP_Q4_0 ? 8 : F == ES_HIP_Q5_0 ? 16 : 0;   // Q8_0 codes are signed as stored
     // The block starts 2-aligned. A 16-byte load at the 4-aligned one of blk / blk+2 plus 2- and 4-byte loads for the
     // rest reads exactly the block's bytes.
-    struct Raw { uint4 v; uint32_t w4, u, par; };
+    struct Raw { uint4 v, v2; uint32_t w4, u, par; };
     struct Act { uint32_t y[8]; int ns[8]; float d; };   // ns[i] = -OFF * (sum of the four bytes of y[i])
     struct Wt { uint32_t q[8]; float d; };
     struct Ints { int lane[8]; };
@@ -258,7 +258,11 @@ template <int F> struct Lane32 {
     static __device__ __forceinline__ void load_raw(const uint8_t *blk, int, Raw &r) {
         r.par = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk) & 2);
         r.v = ldw4(blk + r.par);
-        if constexpr (F == ES_HIP_Q4_0) {   // d f16 @0, qs[16] @2
+        if constexpr (F == ES_HIP_Q8_0) {   // d f16 @0, int8 qs[32] @2: 34 bytes as 16 + 16 + 2
+            r.v2 = ldw4(blk + r.par + 16);
+            r.w4 = 0;
+            r.u = ldg<uint16_t>(r.par ? blk : blk + 32);
+        } else if constexpr (F == ES_HIP_Q4_0) {   // d f16 @0, qs[16] @2
             r.w4 = 0;
             r.u = ldg<uint16_t>(r.par ? blk : blk + 16);
         } else {                            // d f16 @0, qh u32 @2, qs[16] @6
@@ -269,6 +273,20 @@ template <int F> struct Lane32 {
     static __device__ __forceinline__ void unpack(const Raw &r, int, Wt &w) {
         uint32_t qs[4], d16, qh = 0;
         const uint4 v = r.v;
+        if constexpr (F == ES_HIP_Q8_0) {
+            const uint32_t s[9] = {v.x, v.y, v.z, v.w, r.v2.x, r.v2.y, r.v2.z, r.v2.w, r.u};
+            if (r.par == 0) {
+                d16 = v.x;
+#pragma unroll
+                for (int i = 0; i < 8; i++) w.q[i] = alignbyte(s[i + 1], s[i], 2);
+            } else {
+                d16 = r.u;
+#pragma unroll
+                for (int i = 0; i < 8; i++) w.q[i] = s[i];
+            }
+            w.d = half_bits_to_float(d16);
+            return;
+        }
         if constexpr (F == ES_HIP_Q4_0) {
             if (r.par == 0) {
                 d16 = v.x;
@@ -307,8 +325,9 @@ template <int F> struct Lane32 {
 };
 template <> struct Lane<ES_HIP_Q4_0> : Lane32<ES_HIP_Q4_0> {};
 template <> struct Lane<ES_HIP_Q5_0> : Lane32<ES_HIP_Q5_0> {};
+template <> struct Lane<ES_HIP_Q8_0> : Lane32<ES_HIP_Q8_0> {};
 
-template <int F> constexpr bool is32() { return F == ES_HIP_Q4_0 || F == ES_HIP_Q5_0; }
+template <int F> constexpr bool is32() { return F == ES_HIP_Q4_0 || F == ES_HIP_Q5_0 || F == ES_HIP_Q8_0; }
 
 // ---------------------------------------------------------------------------------------------------------------------
 // The kernel
@@ -500,6 +519,7 @@ hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJo
     switch (L.type) {
     case ES_HIP_Q4_0: fn = pick_nt<ES_HIP_Q4_0>(L.nt, L.waves); break;
     case ES_HIP_Q5_0: fn = pick_nt<ES_HIP_Q5_0>(L.nt, L.waves); break;
+    case ES_HIP_Q8_0: fn = pick_nt<ES_HIP_Q8_0>(L.nt, L.waves); break;
     case ES_HIP_Q2_K: fn = pick_nt<ES_HIP_Q2_K>(L.nt, L.waves); break;
     case ES_HIP_Q4_K: fn = pick_nt<ES_HIP_Q4_K>(L.nt, L.waves); break;
     case ES_HIP_Q6_K: fn = pick_nt<ES_HIP_Q6_K>(L.nt, L.waves); break;
@@ -574,6 +594,8 @@ hipError_t mb32_launch(int type, const MbJob *jobs, int njobs, const MbJob &sing
         hipLaunchKernelGGL(mb32_kernel<ES_HIP_Q4_0>, dim3(grid), dim3(256), 0, s, jobs, njobs, single, order);
     else if (type == ES_HIP_Q5_0)
         hipLaunchKernelGGL(mb32_kernel<ES_HIP_Q5_0>, dim3(grid), dim3(256), 0, s, jobs, njobs, single, order);
+    else if (type == ES_HIP_Q8_0)
+        hipLaunchKernelGGL(mb32_kernel<ES_HIP_Q8_0>, dim3(grid), dim3(256), 0, s, jobs, njobs, single, order);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -91,6 +91,7 @@ bool fmt_info(uint32_t t, FmtInfo &f) {
     switch (t) {
     case ES_HIP_Q4_0: f = {32, 18, 36, 1}; return true;
     case ES_HIP_Q5_0: f = {32, 22, 36, 1}; return true;
+    case ES_HIP_Q8_0: f = {32, 34, 36, 1}; return true;
     case ES_HIP_Q2_K: f = {256, 84, 292, 8}; return true;
     case ES_HIP_Q4_K: f = {256, 144, 292, 8}; return true;
     case ES_HIP_Q6_K: f = {256, 210, 292, 8}; return true;
@@ -324,7 +325,8 @@ bool mm_eligible(const Req &q) {
 
 bool mb_eligible(const Req &q) {
     const int mn = g_mb_min.load();
-    return (q.type == ES_HIP_Q4_0 || q.type == ES_HIP_Q5_0) && mn > 0 && q.na >= mn && !q.ints && q.r1 > q.r0;
+    return (q.type == ES_HIP_Q4_0 || q.type == ES_HIP_Q5_0 || q.type == ES_HIP_Q8_0) && mn > 0 && q.na >= mn && !q.ints &&
+           q.r1 > q.r0;
 }
 
 bool mq_eligible(const Req &q) {

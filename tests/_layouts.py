@@ -1,7 +1,7 @@
-"""Vectorised numpy decoders of the five block layouts, independent of the oracle's C code.
+"""Vectorised numpy decoders of the six block layouts, independent of the oracle's C code.
 
 Each decoder returns, per weight element, integer codes such that the weight equals
-    d * sc * q - dmin * m      (Q4_K, Q2_K)       or       d * sc * q      (Q6_K: q already minus 32; Q4_0/Q5_0: sc = 1)
+    d * sc * q - dmin * m      (Q4_K, Q2_K)   or   d * sc * q      (Q6_K: q already minus 32; Q4_0/Q5_0/Q8_0: sc = 1)
 and the tests pin the decoders by rebuilding the reference's dequantized floats (es_dequant_row) bit for bit.
 The integer block dot of a weight block against int8 activations is then sum(sc*q*y) (and sum(m*y) for the mins),
 computed here in int64 by brute force.
@@ -16,6 +16,13 @@ def _f16(u16):
 def decode(t, W, cols):
     """-> dict(q [rows, cols] int64, sc [rows, cols] int64, m [rows, cols] int64, d [rows, nb] f32, dmin [rows, nb])"""
     W = np.asarray(W, np.uint8)
+    if t == 8:   # Q8_0: d f16, int8 qs[32]
+        B = W.reshape(-1, 34)
+        d = _f16(B[:, 0:2].copy().view(np.uint16)[:, 0])
+        q = B[:, 2:34].copy().view(np.int8).astype(np.int64)
+        rows = W.size // (cols // 32 * 34)
+        return dict(q=q.reshape(rows, cols), sc=np.ones((rows, cols), np.int64), m=np.zeros((rows, cols), np.int64),
+                    d=d.reshape(rows, -1), dmin=np.zeros((rows, cols // 32), np.float32), bs=32)
     if t in (2, 6):
         bb = 18 if t == 2 else 22
         B = W.reshape(-1, bb)
@@ -85,7 +92,7 @@ def dequant_like_reference(t, dec):
     d = np.repeat(dec["d"], bs, axis=1)
     dm = np.repeat(dec["dmin"], bs, axis=1)
     q, sc, m = dec["q"], dec["sc"], dec["m"]
-    if t in (2, 6):
+    if t in (2, 6, 8):
         return q.astype(np.float32) * d
     if t == 14:
         return (d * sc.astype(np.float32)) * q.astype(np.float32)

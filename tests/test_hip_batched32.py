@@ -1,4 +1,4 @@
-"""GPU parity of the batched Q4_0 / Q5_0 kernels, the matrix-core one (es_hip_mb.hip: one int8 MFMA per block for 4 rows x
+"""GPU parity of the batched Q4_0 / Q5_0 / Q8_0 kernels, the matrix-core one (es_hip_mb.hip: one int8 MFMA per block for 4 rows x
 32 activations, chains in registers, 8 blocks in flight) and the one-lane-per-output one (es_hip_mv.hip): bit-identical to
 the oracle in every reference order and to the vector kernel, over activation counts that exercise every lane split and
 token tile (2 .. 64 per group, several groups), ragged row counts, rows of every block count around the load pipeline's
@@ -39,7 +39,7 @@ def inputs(orc, t, rows, cols, na, seed):
     return W, orc.quantize_act(t, x)
 
 
-@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0], ids=["q4_0", "q5_0"])
+@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0, O.Q8_0], ids=["q4_0", "q5_0", "q8_0"])
 @pytest.mark.parametrize("rows,cols,na", [(4096, 2048, 32), (512, 2048, 32), (37, 896, 2), (100, 320, 3), (65, 1024, 64),
                                           (33, 512, 70), (20, 256, 130)])
 @pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
@@ -51,7 +51,7 @@ def test_batched32_vs_oracle(hipb, orc, t, rows, cols, na, mode):
     assert np.array_equal(bits(y), bits(ref))
 
 
-@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0], ids=["q4_0", "q5_0"])
+@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0, O.Q8_0], ids=["q4_0", "q5_0", "q8_0"])
 def test_batched32_equals_vector_kernel_with_ranges(hipb, orc, t):
     rows, cols, na, r0, r1 = 150, 1024, 19, 9, 141
     W, acts = inputs(orc, t, rows, cols, na, 3)
@@ -74,7 +74,7 @@ def test_batched32_equals_vector_kernel_with_ranges(hipb, orc, t):
     assert np.all(out[0][:, :r0] == -555.0) and np.all(out[0][:, r1:] == -555.0)
 
 
-@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0], ids=["q4_0", "q5_0"])
+@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0, O.Q8_0], ids=["q4_0", "q5_0", "q8_0"])
 @pytest.mark.parametrize("cols", [32, 96, 224, 256, 288, 544, 2080])
 @pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
 def test_batched32_block_counts(hipb, orc, t, cols, mode):
@@ -88,19 +88,21 @@ def test_batched32_block_counts(hipb, orc, t, cols, mode):
     assert np.array_equal(bits(y), bits(ref))
 
 
-@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0], ids=["q4_0", "q5_0"])
+@pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0, O.Q8_0], ids=["q4_0", "q5_0", "q8_0"])
 def test_batched32_extreme_codes(hipb, orc, t):
-    """codes at both ends (0 and 15 / 31, every high bit set or clear) against activations of +-127"""
+    """codes at both ends (0 and 15 / 31, every high bit set or clear; Q8_0: -128 and 127) against activations of +-127"""
     rows, cols, na = 40, 512, 32
     rng = np.random.default_rng(11)
     W, acts = inputs(orc, t, rows, cols, na, 4)
-    bb = 18 if t == O.Q4_0 else 22
+    bb = O.BLOCK_BYTES[t]
     Wb = W.view(np.uint8).reshape(rows, -1).copy()
     for r in range(rows):
         for b in range(cols // 32):
             blk = Wb[r, bb * b:bb * (b + 1)]
             pat = rng.integers(0, 3)
-            if pat < 2:
+            if pat < 2 and t == O.Q8_0:
+                blk[2:] = 0x80 if pat == 0 else 0x7f          # int8 codes -128 / 127
+            elif pat < 2:
                 blk[bb - 16:] = 0xff if pat == 0 else 0x00
                 if t == O.Q5_0:
                     blk[2:6] = 0xff if pat == 0 else 0x00

@@ -12,7 +12,7 @@ import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K"]
+FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K", "Q8_0"]
 MODES = [(E.ORDER_X86_CONTRACT, "clang", O.CONTRACT, O.PATH_X86), (E.ORDER_X86_STRICT, "gcc", O.STRICT, O.PATH_X86),
          (E.ORDER_SCALAR, "scalar", O.STRICT, O.PATH_SCALAR)]
 
@@ -107,7 +107,8 @@ def test_baseline_shapes_vs_oracle(order, orc, F, rows, cols, na, mode):
 
 
 @pytest.mark.parametrize("F,rows,cols", [("Q4_K", 512, 2048), ("Q6_K", 300, 1024), ("Q2_K", 256, 2048),
-                                          ("Q4_0", 200, 896), ("Q5_0", 128, 2048), ("Q4_K", 64, 14336)])
+                                          ("Q4_0", 200, 896), ("Q5_0", 128, 2048), ("Q4_K", 64, 14336),
+                                          ("Q8_0", 300, 2048)])
 def test_multi_equals_single(hip, orc, F, rows, cols):
     """es_mtest's invariant on the device: one launch over na activations == na single-activation launches"""
     t = O.TYPES[F]
@@ -158,7 +159,7 @@ def test_edge_blocks(hip, orc, F):
     rng = np.random.default_rng(9)
     W[3] = rng.integers(0, 256, W[3].shape, dtype=np.uint8)
     W[4] = rng.integers(0, 256, W[4].shape, dtype=np.uint8)
-    dpos = {O.Q4_0: [0], O.Q5_0: [0], O.Q4_K: [0, 2], O.Q6_K: [208], O.Q2_K: [80, 82]}[t]
+    dpos = {O.Q4_0: [0], O.Q5_0: [0], O.Q8_0: [0], O.Q4_K: [0, 2], O.Q6_K: [208], O.Q2_K: [80, 82]}[t]
     for p in dpos:
         W[2, :, p:p + 2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)   # 1.0: extreme integers, sane scale
         W[3, :, p:p + 2] = np.frombuffer(np.uint16(0x0007).tobytes(), np.uint8)   # subnormal half
@@ -208,7 +209,8 @@ def test_run_jobs_and_plan_mixed_formats(hip, orc):
     """one queued batch over all five formats (the engine's run_jobs) == the products one by one"""
     specs, keep, refs = [], [], []
     for k, (F, rows, cols, na) in enumerate([("Q4_K", 256, 2048, 1), ("Q6_K", 130, 768, 3), ("Q2_K", 96, 1024, 2),
-                                             ("Q4_0", 77, 896, 1), ("Q5_0", 64, 2048, 5), ("Q4_K", 33, 512, 4)]):
+                                             ("Q4_0", 77, 896, 1), ("Q5_0", 64, 2048, 5), ("Q4_K", 33, 512, 4),
+                                             ("Q8_0", 50, 1024, 3)]):
         t = O.TYPES[F]
         W, acts = mtest_inputs(orc, t, rows, cols, na, 300 + k)
         dW, dA, dY = hip.upload(W), hip.upload(acts), hip.alloc(na * rows * 4)

@@ -6,7 +6,7 @@ import pytest
 import oracle as O
 import _layouts as L
 
-FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K"]
+FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K", "Q8_0"]
 CASES = ["mtest", "gauss"]
 
 
