@@ -35,7 +35,8 @@ INT8_PEAK_TOPS = 5000.0
 Q80 = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])
 Q8K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
 SETTLE_S = 0.3   # untimed runs before each workload's warmup steps: the GPU leaves its idle clocks
-SCALE_POS = {E.Q4_0: (0, None), E.Q5_0: (0, None), E.Q4_K: (0, 2), E.Q6_K: (208, None), E.Q2_K: (80, 82)}
+SCALE_POS = {E.Q4_0: (0, None), E.Q5_0: (0, None), E.Q8_0: (0, None), E.Q4_K: (0, 2), E.Q5_K: (0, 2), E.Q6_K: (208, None),
+             E.Q3_K: (108, None), E.Q2_K: (80, 82)}
 
 
 def random_blocks(t, rows, cols, rng):
@@ -309,8 +310,12 @@ def only(lib, rng, name, K, Wm):
         out = {"workload": name, "ms_per_layer": round(ms, 4), "weight_bytes_per_layer": w.weight_bytes // w.copies}
         w.close()
         return out
-    mats, na, copies = {"decode": (Q4K_FFN, 1, 38), "prefill": (Q4K_FFN, 512, 1), "config1": ([(E.Q4_0, 4864, 896)], 1, 410),
-                        "config3b1": ([(E.Q6_K, 151936, 1024)], 1, 8), "config3b64": ([(E.Q6_K, 151936, 1024)], 64, 8)}[name]
+    if name.startswith("decode_"):   # config 2's decode in another weight format (same shapes, same 38 layer copies)
+        t = E.TYPES[name[len("decode_"):].upper()]
+        mats, na, copies = [(t, r, c) for _, r, c in Q4K_FFN], 1, 38
+    else:
+        mats, na, copies = {"decode": (Q4K_FFN, 1, 38), "prefill": (Q4K_FFN, 512, 1), "config1": ([(E.Q4_0, 4864, 896)], 1, 410),
+                            "config3b1": ([(E.Q6_K, 151936, 1024)], 1, 8), "config3b64": ([(E.Q6_K, 151936, 1024)], 64, 8)}[name]
     w = Workload(lib, rng, mats, na, copies)
     _, ev = w.time(Wm, K)
     out = {"workload": name, "ms_per_launch": round(ev, 4), "weight_bytes_per_launch": w.weight_bytes,
@@ -327,7 +332,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=2.0)
     ap.add_argument("--only", choices=["decode", "prefill", "config1", "config3b1", "config3b64", "config4", "config5", "act",
-                                       "copy"],
+                                       "copy"] + [f"decode_{f.lower()}" for f in E.TYPES],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -6,19 +6,21 @@
  *   src/es_quant.h:25-49    es_act_prepare / es_matvec / es_matvec_multi / es_row_bytes / es_quant_supported
  *   src/es_q2k.h:24-86      the Q2_K / Q8_K block structs, es_quantize_q8_K, es_matvec_q2_K
  *   src/es_compute.h:10-25  the thread pool that fans a queue of row jobs out to cores (driven by src/es_engine.c:144-186)
- * This library computes the same products on one MI355X for the GGUF formats Q4_0, Q5_0, Q8_0, Q4_K, Q6_K and Q2_K against
+ * This library computes the same products on one MI355X for the GGUF formats Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K against
  * the reference's Q8 activations, with the packed weight blocks kept byte-for-byte in device memory.
  *
  * Results. The integer block dots are exact. The fp32 epilogue is evaluated in the reference's own order, so outputs are
  * bit-identical to the reference's CPU kernels in the selected build flavour (es_hip_set_order):
  *   ES_HIP_ORDER_X86_CONTRACT  the reference's default x86 build (clang, -ffp-contract=on; Makefile:1-4) — the default here
  *   ES_HIP_ORDER_X86_STRICT    the same AVX2 kernels built by gcc -std=c11 (no contraction)
- *   ES_HIP_ORDER_SCALAR        the scalar mv_* kernels (ES_NO_AVX2=1, src/es_quant.c:1013-1117)
+ *   ES_HIP_ORDER_SCALAR        the scalar mv_* kernels (ES_NO_AVX2=1, src/es_quant.c:1013-1175)
+ * Q5_K has no AVX2 kernel in the reference (its x86 build runs the scalar mv_q5_K, without FMA), so all three orders give
+ * the same Q5_K results.
  *
  * Conventions (same as the reference): every buffer belongs to the caller; W points at row 0 of a row-major matrix whose row
  * stride is es_hip_row_bytes(type, cols); outputs are written only for rows [r0, r1), at absolute row indices, activation q's
  * result at y + q * ystride. Activation blocks are the reference's: Q8_0 (36 bytes: float d, int8 qs[32]) for Q4_0/Q5_0/Q8_0 and
- * Q8_K (292 bytes: float d, int8 qs[256], int16 bsums[16]) for Q2_K/Q4_K/Q6_K.
+ * Q8_K (292 bytes: float d, int8 qs[256], int16 bsums[16]) for Q2_K/Q3_K/Q4_K/Q5_K/Q6_K.
  *
  * Errors. The reference's entry points return void and cannot fail. Here the device-pointer entry points return 0 on success
  * and a negative ES_HIP_E* code otherwise; es_hip_last_error() describes the most recent failure. There is no CPU fallback:
@@ -37,7 +39,10 @@ extern "C" {
 #endif
 
 /* GGML type ids of the formats computed here (reference src/es_quant.h:15-22) */
-enum { ES_HIP_Q4_0 = 2, ES_HIP_Q5_0 = 6, ES_HIP_Q8_0 = 8, ES_HIP_Q2_K = 10, ES_HIP_Q4_K = 12, ES_HIP_Q6_K = 14 };
+enum {
+    ES_HIP_Q4_0 = 2, ES_HIP_Q5_0 = 6, ES_HIP_Q8_0 = 8, ES_HIP_Q2_K = 10, ES_HIP_Q3_K = 11, ES_HIP_Q4_K = 12, ES_HIP_Q5_K = 13,
+    ES_HIP_Q6_K = 14
+};
 
 /* fp32 epilogue order, see the header comment */
 enum { ES_HIP_ORDER_X86_CONTRACT = 0, ES_HIP_ORDER_X86_STRICT = 1, ES_HIP_ORDER_SCALAR = 2 };

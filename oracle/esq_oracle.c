@@ -20,7 +20,7 @@
 int esq_block_elems(uint32_t t) {
     switch (t) {
     case ESQ_Q4_0: case ESQ_Q5_0: case ESQ_Q8_0: return 32;
-    case ESQ_Q2_K: case ESQ_Q4_K: case ESQ_Q6_K: return 256;
+    case ESQ_Q2_K: case ESQ_Q3_K: case ESQ_Q4_K: case ESQ_Q5_K: case ESQ_Q6_K: return 256;
     }
     return 0;
 }
@@ -31,7 +31,9 @@ int esq_block_bytes(uint32_t t) {
     case ESQ_Q5_0: return 22;   /* d f16, qh[4], qs[16]                       src/es_quant.c:14 */
     case ESQ_Q8_0: return 34;   /* d f16, int8 qs[32]                         src/es_quant.c:11 */
     case ESQ_Q2_K: return 84;   /* scales[16], qs[64], d, dmin                src/es_q2k.h:24-29 */
+    case ESQ_Q3_K: return 110;  /* hmask[32], qs[64], scales[12], d          src/es_quant.c:16 */
     case ESQ_Q4_K: return 144;  /* d, dmin, scales[12], qs[128]               src/es_quant.c:17 */
+    case ESQ_Q5_K: return 176;  /* d, dmin, scales[12], qh[32], qs[128]      src/es_quant.c:18 */
     case ESQ_Q6_K: return 210;  /* ql[128], qh[64], int8 scales[16], d        src/es_quant.c:19 */
     }
     return 0;
@@ -206,6 +208,51 @@ int32_t esq_blkdot_q4_K(const uint8_t *blk, const esq_q8K *y, int32_t *mins) {
     return dot;
 }
 
+int32_t esq_blkdot_q5_K(const uint8_t *blk, const esq_q8K *y, int32_t *mins) {
+    const uint8_t *scales = blk + 4, *qh = blk + 16, *q = blk + 48;
+    int32_t dot = 0, mm = 0;
+    for (int c = 0; c < 4; c++) {   /* Q4_K's chunks plus a fifth bit: qh bit 2c (low), 2c+1 (high) (src/es_quant.c:1153-1175) */
+        uint8_t s0, m0, s1, m1;
+        esq_scale_min_k4(2 * c, scales, &s0, &m0);
+        esq_scale_min_k4(2 * c + 1, scales, &s1, &m1);
+        int32_t lo = 0, hi = 0;
+        for (int l = 0; l < 32; l++) {
+            lo += ((q[32 * c + l] & 15) | (((qh[l] >> (2 * c)) & 1) << 4)) * y->qs[64 * c + l];
+            hi += ((q[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4)) * y->qs[64 * c + 32 + l];
+        }
+        dot += s0 * lo + s1 * hi;
+        mm += m0 * (y->bsums[4 * c] + y->bsums[4 * c + 1]) + m1 * (y->bsums[4 * c + 2] + y->bsums[4 * c + 3]);
+    }
+    *mins = mm;
+    return dot;
+}
+
+void esq_q3k_scales(const uint8_t *s12, int8_t sc[16]) {
+    /* sixteen 6-bit scales: low nibbles from bytes 0-7, high pairs from bytes 8-11 (src/es_quant.c:1125-1128) */
+    for (int g = 0; g < 16; g++) {
+        const int lo = g < 8 ? s12[g] & 15 : s12[g - 8] >> 4;
+        const int hi = (s12[8 + (g & 3)] >> (2 * (g >> 2))) & 3;
+        sc[g] = (int8_t)((lo | (hi << 4)) - 32);
+    }
+}
+
+int32_t esq_blkdot_q3_K(const uint8_t *blk, const esq_q8K *y) {
+    const uint8_t *hm = blk, *q = blk + 32;
+    int8_t sc[16];
+    esq_q3k_scales(blk + 96, sc);
+    int32_t tot = 0;
+    for (int g = 0; g < 16; g++) {   /* group g = 8n + 2j + half: bits 2j of qs[32n + 16half + l], hmask bit 4n+j (src/es_quant.c:1131-1146) */
+        const int n = g >> 3, j = (g >> 1) & 3, half = g & 1;
+        int32_t s16 = 0;
+        for (int l = 0; l < 16; l++) {
+            const int v = ((q[32 * n + 16 * half + l] >> (2 * j)) & 3) - (((hm[16 * half + l] >> (4 * n + j)) & 1) ? 0 : 4);
+            s16 += v * y->qs[16 * g + l];
+        }
+        tot += sc[g] * s16;
+    }
+    return tot;
+}
+
 int32_t esq_blkdot_q6_K(const uint8_t *blk, const esq_q8K *y) {
     const uint8_t *ql = blk, *qh = blk + 128;
     const int8_t *sc = (const int8_t *)(blk + 192);
@@ -287,9 +334,14 @@ static float row_k(uint32_t t, const uint8_t *w, int nb, const esq_q8K *y, int c
             const float q = dm * (float)mins;
             if (contract) s = fmaf(yd, fmaf(d, (float)dot, -q), s);
             else s = s + yd * (d * (float)dot - q);
-        } else if (t == ESQ_Q6_K) {   /* s += y.d * d * tot   (src/es_quant.c:1114, 1466) */
-            const int32_t tot = esq_blkdot_q6_K(blk, &y[b]);
-            const float yd_d = yd * esq_half_to_float(rd16(blk + 208));
+        } else if (t == ESQ_Q5_K) {   /* s += y.d * (d*dot - dmin*mins), the scalar kernel only: never fused (src/es_quant.c:1173) */
+            int32_t mins;
+            const int32_t dot = esq_blkdot_q5_K(blk, &y[b], &mins);
+            const float d = esq_half_to_float(rd16(blk)), dm = esq_half_to_float(rd16(blk + 2));
+            s = s + yd * (d * (float)dot - dm * (float)mins);
+        } else if (t == ESQ_Q6_K || t == ESQ_Q3_K) {   /* s += y.d * d * tot   (src/es_quant.c:1114, 1466; Q3_K 1147, 1391) */
+            const int32_t tot = t == ESQ_Q6_K ? esq_blkdot_q6_K(blk, &y[b]) : esq_blkdot_q3_K(blk, &y[b]);
+            const float yd_d = yd * esq_half_to_float(rd16(blk + (t == ESQ_Q6_K ? 208 : 108)));
             if (contract) s = fmaf(yd_d, (float)tot, s);
             else s = s + yd_d * (float)tot;
         } else {   /* Q2_K: s += dall*isum - dmin*summs   (src/es_q2k.c:142-146, src/es_quant.c:1364-1365) */
@@ -339,6 +391,8 @@ void esq_block_ints(uint32_t t, const void *W, int cols, int rows, const void *a
             case ESQ_Q8_0: esq_blkdot_q8_0(blk, (const esq_q80 *)act + b, lane); for (int i = 0; i < 8; i++) v += lane[i]; break;
             case ESQ_Q4_K: v = esq_blkdot_q4_K(blk, (const esq_q8K *)act + b, &x); break;
             case ESQ_Q6_K: v = esq_blkdot_q6_K(blk, (const esq_q8K *)act + b); break;
+            case ESQ_Q5_K: v = esq_blkdot_q5_K(blk, (const esq_q8K *)act + b, &x); break;
+            case ESQ_Q3_K: v = esq_blkdot_q3_K(blk, (const esq_q8K *)act + b); break;
             case ESQ_Q2_K: v = esq_blkdot_q2_K(blk, (const esq_q8K *)act + b, &x); break;
             }
             dots[(size_t)r * nb + b] = v;
@@ -379,6 +433,33 @@ void esq_dequant_row(uint32_t t, const void *src, float *y, int n) {
                 const float d1 = d * (float)s0, n1 = dm * (float)m0, d2 = d * (float)s1, n2 = dm * (float)m1;
                 for (int l = 0; l < 32; l++) *y++ = d1 * (float)(p[16 + 32 * c + l] & 15) - n1;
                 for (int l = 0; l < 32; l++) *y++ = d2 * (float)(p[16 + 32 * c + l] >> 4) - n2;
+            }
+            break;
+        }
+        case ESQ_Q5_K: {   /* d*sc*q - dmin*m, q with its fifth bit, src/es_quant.c:136-154 */
+            const float d = esq_half_to_float(rd16(p)), dm = esq_half_to_float(rd16(p + 2));
+            for (int c = 0; c < 4; c++) {
+                uint8_t s0, m0, s1, m1;
+                esq_scale_min_k4(2 * c, p + 4, &s0, &m0);
+                esq_scale_min_k4(2 * c + 1, p + 4, &s1, &m1);
+                const float d1 = d * (float)s0, n1 = dm * (float)m0, d2 = d * (float)s1, n2 = dm * (float)m1;
+                for (int l = 0; l < 32; l++)
+                    *y++ = d1 * (float)((p[48 + 32 * c + l] & 15) + ((p[16 + l] >> (2 * c)) & 1) * 16) - n1;
+                for (int l = 0; l < 32; l++)
+                    *y++ = d2 * (float)((p[48 + 32 * c + l] >> 4) + ((p[16 + l] >> (2 * c + 1)) & 1) * 16) - n2;
+            }
+            break;
+        }
+        case ESQ_Q3_K: {   /* d*(sc-32)*(q - (hbit ? 0 : 4)), src/es_quant.c:85-115 */
+            const float d = esq_half_to_float(rd16(p + 108));
+            int8_t sc[16];
+            esq_q3k_scales(p + 96, sc);
+            for (int g = 0; g < 16; g++) {
+                const int n = g >> 3, j = (g >> 1) & 3, half = g & 1;
+                const float dl = d * (float)sc[g];
+                for (int l = 0; l < 16; l++)
+                    *y++ = dl * (float)(((p[32 + 32 * n + 16 * half + l] >> (2 * j)) & 3) -
+                                        (((p[16 * half + l] >> (4 * n + j)) & 1) ? 0 : 4));
             }
             break;
         }
@@ -489,8 +570,9 @@ void esq_quantize_row(uint32_t t, const float *x, void *dst, int n) {
         }
         return;
     }
-    case ESQ_Q4_K: {   /* per 32: min (<= 0)/max -> 15 steps; 6-bit scale and min against fp16 d and dmin */
-        for (int b = 0; b < n / 256; b++, x += 256, p += 144) {
+    case ESQ_Q4_K: case ESQ_Q5_K: {   /* per 32: min (<= 0)/max -> 15 (31) steps; 6-bit scale and min against fp16 d and dmin */
+        const int five = t == ESQ_Q5_K, top = five ? 31 : 15, bb = five ? 176 : 144, qo = five ? 48 : 16;
+        for (int b = 0; b < n / 256; b++, x += 256, p += bb) {
             float sc[8], mn[8], smax = 0.0f, mmax = 0.0f;
             for (int j = 0; j < 8; j++) {
                 float lo = 0.0f, hi = x[32 * j];
@@ -499,12 +581,12 @@ void esq_quantize_row(uint32_t t, const float *x, void *dst, int n) {
                     if (x[32 * j + l] > hi) hi = x[32 * j + l];
                 }
                 if (hi < 0) hi = 0;
-                sc[j] = (hi - lo) / 15;
+                sc[j] = (hi - lo) / (float)top;
                 mn[j] = -lo;
                 if (sc[j] > smax) smax = sc[j];
                 if (mn[j] > mmax) mmax = mn[j];
             }
-            memset(p, 0, 144);
+            memset(p, 0, (size_t)bb);
             const uint16_t dh = esq_float_to_half(smax / 63), mh = esq_float_to_half(mmax / 63);
             wr16(p, dh);
             wr16(p + 2, mh);
@@ -523,8 +605,35 @@ void esq_quantize_row(uint32_t t, const float *x, void *dst, int n) {
             for (int j = 0; j < 8; j++) {
                 const float dl = d * (float)is[j], ml = dmin * (float)im[j];
                 for (int l = 0; l < 32; l++) {
-                    const int q = dl > 0 ? clampi(lrintf((x[32 * j + l] + ml) / dl), 0, 15) : 0;
-                    p[16 + 32 * (j >> 1) + l] |= (uint8_t)(q << ((j & 1) * 4));
+                    const int q = dl > 0 ? clampi(lrintf((x[32 * j + l] + ml) / dl), 0, top) : 0;
+                    p[qo + 32 * (j >> 1) + l] |= (uint8_t)((q & 15) << ((j & 1) * 4));
+                    if (five) p[16 + l] |= (uint8_t)(((q >> 4) & 1) << j);
+                }
+            }
+        }
+        return;
+    }
+    case ESQ_Q3_K: {   /* per 16: codes -4..3, 6-bit scale (stored + 32) against fp16 d */
+        for (int b = 0; b < n / 256; b++, x += 256, p += 110) {
+            float sc[16], smax = 0.0f;
+            for (int g = 0; g < 16; g++) {
+                sc[g] = absmax(x + 16 * g, 16) / 4;
+                if (sc[g] > smax) smax = sc[g];
+            }
+            memset(p, 0, 110);
+            const uint16_t dh = esq_float_to_half(smax / 31);
+            wr16(p + 108, dh);
+            const float d = esq_half_to_float(dh);
+            for (int g = 0; g < 16; g++) {   /* group g = 8n + 2j + half, as esq_q3k_scales reads it */
+                const int isc = clampi(d > 0 ? lrintf(sc[g] / d) : 0, 0, 31), u = isc + 32;
+                if (g < 8) p[96 + g] |= (uint8_t)(u & 15); else p[96 + g - 8] |= (uint8_t)((u & 15) << 4);
+                p[104 + (g & 3)] |= (uint8_t)((u >> 4) << (2 * (g >> 2)));
+                const int nn = g >> 3, j = (g >> 1) & 3, half = g & 1;
+                const float dl = d * (float)isc;
+                for (int l = 0; l < 16; l++) {
+                    const int q = dl > 0 ? clampi(lrintf(x[16 * g + l] / dl), -4, 3) : 0, c = q + 4;   /* c = low2 + 4*hbit */
+                    p[32 + 32 * nn + 16 * half + l] |= (uint8_t)((c & 3) << (2 * j));
+                    p[16 * half + l] |= (uint8_t)((c >> 2) << (4 * nn + j));
                 }
             }
         }
@@ -603,7 +712,8 @@ void esq_mtest_blocks(uint32_t t, uint64_t *state, uint8_t *W, int rows, int col
     const size_t rb = esq_row_bytes(t, cols);
     int dpos = 0, mpos = -1;
     if (t == ESQ_Q6_K) dpos = 208;
-    if (t == ESQ_Q4_K) mpos = 2;
+    if (t == ESQ_Q3_K) dpos = 108;
+    if (t == ESQ_Q4_K || t == ESQ_Q5_K) mpos = 2;   /* es_mtest sets dmin for Q4_K; Q5_K's is placed the same way */
     if (t == ESQ_Q2_K) { dpos = 80; mpos = 82; }
     for (size_t i = 0; i < rb * (size_t)rows; i++) W[i] = (uint8_t)mt_rnd(state);
     for (int r = 0; r < rows; r++)

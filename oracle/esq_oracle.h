@@ -5,14 +5,16 @@
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use. Every function restates the arithmetic of the
  * reference (Tharunmaks/Stream-, "ExpertStream") in plain C and cites the reference lines it follows.
  *
- * Formats covered: Q4_0, Q5_0, Q8_0, Q4_K, Q6_K, Q2_K weights against Q8_0 (float scale, 36 B) and Q8_K (292 B) activations.
+ * Formats covered: Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K weights against Q8_0 (float scale, 36 B) and Q8_K (292 B) activations.
  *
  * Float order. The reference's fp32 epilogues are compiler dependent (its Makefile defaults to clang, which contracts
  * a*b+c into an FMA inside the AVX2 functions; gcc in -std=c11 mode does not). Every matvec here takes
  *   order = ESQ_STRICT    : no contraction (gcc -std=c11 build of the reference),
  *   order = ESQ_CONTRACT  : clang -ffp-contract=on build of the reference,
  *   path  = ESQ_PATH_X86  : the x86 AVX2 dispatch (es_quant.c:1852-1884),
- *   path  = ESQ_PATH_SCALAR: the scalar mv_* kernels (ES_NO_AVX2=1, es_quant.c:1013-1117); order has no effect there.
+ *   path  = ESQ_PATH_SCALAR: the scalar mv_* kernels (ES_NO_AVX2=1, es_quant.c:1013-1175); order has no effect there.
+ * Q5_K has no AVX2 kernel: the x86 dispatch falls through to the scalar mv_q5_K (es_quant.c:1935), built without FMA, so
+ * its order is strict in every build and path. Q3_K's AVX2 epilogue has Q6_K's shape (s += y.d * d * tot).
  * Integer block dots are exact and order independent.
  *
  * Pinning (what checks each function; see tests/test_oracle.py):
@@ -26,7 +28,7 @@
  *   rmsnorm (es_engine.c is not buildable on its own): against an independent numpy restatement (float64 running sum
  *       via cumsum, float32 products) on random rows, and the closed forms of a zero row (s = 1/sqrt(eps)), a constant
  *       row (s = 1/sqrt(c^2 + eps)) and w = NULL equal to w = ones.
- *   Weight quantizers for Q4_0/Q5_0/Q4_K/Q6_K are this project's own (the reference has none); they are test-input
+ *   Weight quantizers for Q4_0/Q5_0/Q8_0/Q3_K/Q4_K/Q5_K/Q6_K are this project's own (the reference has none); they are test-input
  *       generators, checked only for round-trip error bounds.
  */
 #ifndef ESQ_ORACLE_H
@@ -40,7 +42,7 @@ extern "C" {
 #endif
 
 /* GGML type ids used by the path (reference src/es_quant.h:15-22) */
-enum { ESQ_Q4_0 = 2, ESQ_Q5_0 = 6, ESQ_Q8_0 = 8, ESQ_Q2_K = 10, ESQ_Q4_K = 12, ESQ_Q6_K = 14 };
+enum { ESQ_Q4_0 = 2, ESQ_Q5_0 = 6, ESQ_Q8_0 = 8, ESQ_Q2_K = 10, ESQ_Q3_K = 11, ESQ_Q4_K = 12, ESQ_Q5_K = 13, ESQ_Q6_K = 14 };
 enum { ESQ_STRICT = 0, ESQ_CONTRACT = 1 };
 enum { ESQ_PATH_X86 = 0, ESQ_PATH_SCALAR = 1 };
 
@@ -50,7 +52,7 @@ typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } esq_q8K;
 
 /* ---- format facts ---- */
 int    esq_block_elems(uint32_t type);          /* 32 or 256; 0 if unknown */
-int    esq_block_bytes(uint32_t type);          /* 18, 22, 34, 144, 210, 84 */
+int    esq_block_bytes(uint32_t type);          /* 18, 22, 34, 84, 110, 144, 176, 210 */
 size_t esq_row_bytes(uint32_t type, int cols); /* src/es_quant.c:39-73 */
 int    esq_uses_q8K(uint32_t type);            /* 1: Q8_K activations, 0: Q8_0 */
 
@@ -69,6 +71,10 @@ void    esq_blkdot_q5_0(const uint8_t *blk, const esq_q80 *y, int32_t lane[8]);
 void    esq_blkdot_q8_0(const uint8_t *blk, const esq_q80 *y, int32_t lane[8]);
 int32_t esq_blkdot_q4_K(const uint8_t *blk, const esq_q8K *y, int32_t *mins);
 int32_t esq_blkdot_q6_K(const uint8_t *blk, const esq_q8K *y);
+int32_t esq_blkdot_q5_K(const uint8_t *blk, const esq_q8K *y, int32_t *mins);
+int32_t esq_blkdot_q3_K(const uint8_t *blk, const esq_q8K *y);
+/* Q3_K's sixteen 6-bit scales, minus 32 (src/es_quant.c:1125-1129) */
+void    esq_q3k_scales(const uint8_t *s12, int8_t sc[16]);
 int32_t esq_blkdot_q2_K(const uint8_t *blk, const esq_q8K *y, int32_t *summs);
 /* Q4_K 6-bit scale/min unpack for sub-block j (src/es_quant.c:75-83) */
 void    esq_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *mn);
@@ -87,7 +93,7 @@ void esq_dequant_row(uint32_t type, const void *src, float *dst, int n);
 
 /* ---- weight quantizers ---- */
 void esq_quantize_q2_K_ref(const float *x, void *dst, int n); /* src/es_q2k.c:47-86 */
-/* this project's own min/max quantizers for Q4_0/Q5_0/Q4_K/Q6_K; Q2_K goes to the reference's method */
+/* this project's own min/max quantizers for Q4_0/Q5_0/Q8_0/Q3_K/Q4_K/Q5_K/Q6_K; Q2_K goes to the reference's method */
 void esq_quantize_row(uint32_t type, const float *x, void *dst, int n);
 
 /* ---- deterministic inputs ---- */

@@ -14,8 +14,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
-Q4_0, Q5_0, Q8_0, Q2_K, Q4_K, Q6_K = 2, 6, 8, 10, 12, 14
-TYPES = {"Q4_0": Q4_0, "Q5_0": Q5_0, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K}
+Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 2, 6, 8, 10, 11, 12, 13, 14
+TYPES = {"Q4_0": Q4_0, "Q5_0": Q5_0, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
 NAMES = {v: k for k, v in TYPES.items()}
 STRICT, CONTRACT = 0, 1
 PATH_X86, PATH_SCALAR = 0, 1
@@ -25,8 +25,8 @@ Q80 = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])
 Q8K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
 assert Q80.itemsize == 36 and Q8K.itemsize == 292
 
-BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q2_K: 256, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q2_K: 84, Q4_K: 144, Q6_K: 210}
+BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 
 
 def uses_q8k(t: int) -> bool:

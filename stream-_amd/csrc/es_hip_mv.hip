@@ -1,4 +1,4 @@
-// Decode / small-batch products on the vector ALU (v_dot4_i32_i8), all five formats.
+// Decode / small-batch products on the vector ALU (v_dot4_i32_i8), every format of the library.
 //
 // One workgroup of W waves owns `rows_per_wg` consecutive rows of one job. Two phases per batch of `chain_rows` rows:
 //
@@ -17,7 +17,7 @@
 // per batch of NT activations.
 //
 // Reference kernels restated (integer parts and float order): src/es_quant.c:1013-1117 (scalar mv_*), 1252-1343 and
-// 1443-1469 (AVX2 Q4_0/Q5_0/Q4_K/Q6_K), 1344-1368 and src/es_q2k.c:127-190 (Q2_K).
+// 1443-1469 (AVX2 Q4_0/Q5_0/Q4_K/Q6_K), 1344-1368 and src/es_q2k.c:127-190 (Q2_K), 1120-1175 and 1370-1394 (Q3_K, Q5_K).
 #include "es_hip_common.h"
 
 
@@ -99,6 +99,37 @@ template <> struct Lane<ES_HIP_Q4_K> {
     }
 };
 
+// Q5_K: Q4_K's lanes (same qs bytes at offset 48, same activation slice) plus the fifth bit of each element: qh byte
+// 16h + l holds bit 2c for low-nibble element 64c + 16h + l and bit 2c + 1 for high-nibble element 64c + 32 + 16h + l, so
+// lane k also takes qh[16h, 16h + 16). src/es_quant.c:1153-1175.
+template <> struct Lane<ES_HIP_Q5_K> : Lane<ES_HIP_Q4_K> {
+    struct Raw { uint4 hdr, qh, q; };
+    static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
+        r.hdr = ldw4(blk);
+        r.qh = ldw4(blk + 16 + 16 * (k & 1));
+        r.q = ldw4(blk + 48 + 16 * k);
+    }
+    static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
+        const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, hh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        const int c = k >> 1;
+        for (int i = 0; i < 4; i++) {
+            w.lo[i] = (qq[i] & 0x0f0f0f0fu) | (((hh[i] >> (2 * c)) & 0x01010101u) << 4);
+            w.hi[i] = ((qq[i] >> 4) & 0x0f0f0f0fu) | (((hh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+        }
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * c, w.sc0, w.mn0);
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * c + 1, w.sc1, w.mn1);
+        w.d = half_bits_to_float(r.hdr.x);
+        w.dmin = half_bits_to_float(r.hdr.x >> 16);
+    }
+    // s += y.d * (d * dot - dmin * mins). The reference has no AVX2 kernel for Q5_K: the x86 build runs the scalar mv_q5_K,
+    // compiled without FMA, in every configuration. The whole product is rounded here, so the chain's add (fused with a
+    // factor 1 or not) adds exactly that value in either order.
+    static __device__ __forceinline__ Term2 term(const Wt &w, const Act &x, Ints v, bool) {
+        const float in = w.d * static_cast<float>(v.dot) - w.dmin * static_cast<float>(v.aux);
+        return {1.0f, x.d * in};
+    }
+};
+
 // Q6_K: lane k of 8: half h = k/4, j = (k/2)%2, p = k%2. It takes ql[64h + 32p + 16j, +16) and qh[32h + 16j, +16);
 // low nibbles (with qh bits 2p, 2p+1) are group g1 = 8h + 2p + j, high nibbles (qh bits 2p+4, 2p+5) group g1 + 4, where a
 // group is 16 consecutive elements with one int8 scale. The 6-bit codes are dotted unsigned and corrected by
@@ -163,6 +194,77 @@ template <> struct Lane<ES_HIP_Q6_K> {
         return {w.sc1 * (s1 - 32 * x.bs1) + w.sc2 * (s2 - 32 * x.bs2), 0};
     }
     // s += y.d * d * tot   (src/es_quant.c:1114, 1466)
+    static __device__ __forceinline__ Term2 term(const Wt &w, const Act &x, Ints v, bool) {
+        return {x.d * w.d, static_cast<float>(v.dot)};
+    }
+};
+
+// Q3_K: group g = 8n + 2j + half holds elements 16g + [0,16): bits 2j of qs[32n + 16half + l] and hmask[16half + l] bit
+// 4n + j (absent: minus 4). Lane k of 8: n = k/4, jp = (k/2)%2, half = k%2 takes qs[32n + 16half, +16) and
+// hmask[16half, +16), groups g1 = 8n + 4jp + half (j = 2jp) and g1 + 2 (j = 2jp + 1). The codes low2 + 4*hbit (0..7) are
+// dotted unsigned and corrected by 4 * bsums; the 6-bit scales minus 32 come from the 12 packed bytes
+// (src/es_quant.c:1120-1151, 1370-1394). 16-byte fields at 2-byte aligned addresses are read as five aligned dwords, as
+// for Q6_K: the last one read (qs, offset 80) ends 12 bytes before the block does.
+template <> struct Lane<ES_HIP_Q3_K> {
+    struct Raw { uint4 qv, hv; uint32_t q4, h4, sel; uint32_t lo1, lo2, hi1, hi2; uint32_t d16; };
+    struct Act { uint32_t y1[4], y2[4]; int bs1, bs2; float d; };
+    struct Wt { uint32_t q1[4], q2[4]; int sc1, sc2; float d; };
+    struct Ints { int dot, aux; };
+
+    static __device__ __forceinline__ int g1_of(int k) { return 8 * (k >> 2) + 4 * ((k >> 1) & 1) + (k & 1); }
+    static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
+        const int g1 = g1_of(k), g2 = g1 + 2;
+        x.d = ldg<float>(a);
+        const uint4 v0 = ldg<uint4>(a + 4 + 16 * g1), v1 = ldg<uint4>(a + 4 + 16 * g2);
+        x.y1[0] = v0.x; x.y1[1] = v0.y; x.y1[2] = v0.z; x.y1[3] = v0.w;
+        x.y2[0] = v1.x; x.y2[1] = v1.y; x.y2[2] = v1.z; x.y2[3] = v1.w;
+        x.bs1 = ldg<int16_t>(a + 260 + 2 * g1);
+        x.bs2 = ldg<int16_t>(a + 260 + 2 * g2);
+    }
+    static __device__ __forceinline__ void zero_act(Act &x) {
+        for (int i = 0; i < 4; i++) x.y1[i] = x.y2[i] = 0;
+        x.bs1 = x.bs2 = 0;
+        x.d = 0.0f;
+    }
+    static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
+        const int n = k >> 2, half = k & 1, g1 = g1_of(k);
+        const uintptr_t aq = reinterpret_cast<uintptr_t>(blk + 32 + 32 * n + 16 * half);
+        const uintptr_t ah = reinterpret_cast<uintptr_t>(blk + 16 * half);
+        const uint8_t *bq = reinterpret_cast<const uint8_t *>(aq & ~static_cast<uintptr_t>(3));
+        const uint8_t *bh = reinterpret_cast<const uint8_t *>(ah & ~static_cast<uintptr_t>(3));
+        r.sel = static_cast<uint32_t>(aq & 3);   // same for both fields (offsets differ by multiples of 16)
+        r.qv = ldw4(bq);
+        r.q4 = ldg<uint32_t>(bq + 16);
+        r.hv = ldw4(bh);
+        r.h4 = ldg<uint32_t>(bh + 16);
+        // scale of group g: low nibble of byte g % 8 (g < 8: bits 0-3, else 4-7), high pair bits 2(g/4) of byte 8 + g % 4
+        r.lo1 = ldg<uint8_t>(blk + 96 + (g1 & 7));
+        r.lo2 = ldg<uint8_t>(blk + 96 + ((g1 + 2) & 7));
+        r.hi1 = ldg<uint8_t>(blk + 104 + (g1 & 3));
+        r.hi2 = ldg<uint8_t>(blk + 104 + ((g1 + 2) & 3));
+        r.d16 = ldg<uint16_t>(blk + 108);
+    }
+    static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
+        const uint32_t q[4] = {alignbyte(r.qv.y, r.qv.x, r.sel), alignbyte(r.qv.z, r.qv.y, r.sel),
+                               alignbyte(r.qv.w, r.qv.z, r.sel), alignbyte(r.q4, r.qv.w, r.sel)};
+        const uint32_t h[4] = {alignbyte(r.hv.y, r.hv.x, r.sel), alignbyte(r.hv.z, r.hv.y, r.sel),
+                               alignbyte(r.hv.w, r.hv.z, r.sel), alignbyte(r.h4, r.hv.w, r.sel)};
+        const int n = k >> 2, j1 = 2 * ((k >> 1) & 1), j2 = j1 + 1;
+        for (int i = 0; i < 4; i++) {
+            w.q1[i] = ((q[i] >> (2 * j1)) & 0x03030303u) | (((h[i] >> (4 * n + j1)) & 0x01010101u) << 2);
+            w.q2[i] = ((q[i] >> (2 * j2)) & 0x03030303u) | (((h[i] >> (4 * n + j2)) & 0x01010101u) << 2);
+        }
+        const int g1 = g1_of(k), g2 = g1 + 2;
+        w.sc1 = static_cast<int>(((r.lo1 >> (4 * (g1 >> 3))) & 15) | (((r.hi1 >> (2 * (g1 >> 2))) & 3) << 4)) - 32;
+        w.sc2 = static_cast<int>(((r.lo2 >> (4 * (g2 >> 3))) & 15) | (((r.hi2 >> (2 * (g2 >> 2))) & 3) << 4)) - 32;
+        w.d = half_bits_to_float(r.d16);
+    }
+    static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
+        int s1 = 0, s2 = 0;
+        for (int i = 0; i < 4; i++) { s1 = sdot4(w.q1[i], x.y1[i], s1); s2 = sdot4(w.q2[i], x.y2[i], s2); }
+        return {w.sc1 * (s1 - 4 * x.bs1) + w.sc2 * (s2 - 4 * x.bs2), 0};
+    }
+    // s += y.d * d * tot   (src/es_quant.c:1147, 1391)
     static __device__ __forceinline__ Term2 term(const Wt &w, const Act &x, Ints v, bool) {
         return {x.d * w.d, static_cast<float>(v.dot)};
     }
@@ -521,7 +623,9 @@ hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJo
     case ES_HIP_Q5_0: fn = pick_nt<ES_HIP_Q5_0>(L.nt, L.waves); break;
     case ES_HIP_Q8_0: fn = pick_nt<ES_HIP_Q8_0>(L.nt, L.waves); break;
     case ES_HIP_Q2_K: fn = pick_nt<ES_HIP_Q2_K>(L.nt, L.waves); break;
+    case ES_HIP_Q3_K: fn = pick_nt<ES_HIP_Q3_K>(L.nt, L.waves); break;
     case ES_HIP_Q4_K: fn = pick_nt<ES_HIP_Q4_K>(L.nt, L.waves); break;
+    case ES_HIP_Q5_K: fn = pick_nt<ES_HIP_Q5_K>(L.nt, L.waves); break;
     case ES_HIP_Q6_K: fn = pick_nt<ES_HIP_Q6_K>(L.nt, L.waves); break;
     }
     if (!fn) return hipErrorInvalidValue;

@@ -93,7 +93,9 @@ bool fmt_info(uint32_t t, FmtInfo &f) {
     case ES_HIP_Q5_0: f = {32, 22, 36, 1}; return true;
     case ES_HIP_Q8_0: f = {32, 34, 36, 1}; return true;
     case ES_HIP_Q2_K: f = {256, 84, 292, 8}; return true;
+    case ES_HIP_Q3_K: f = {256, 110, 292, 8}; return true;
     case ES_HIP_Q4_K: f = {256, 144, 292, 8}; return true;
+    case ES_HIP_Q5_K: f = {256, 176, 292, 8}; return true;
     case ES_HIP_Q6_K: f = {256, 210, 292, 8}; return true;
     }
     return false;

@@ -14,12 +14,12 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libes_hip_quant.so")
 
-Q4_0, Q5_0, Q8_0, Q2_K, Q4_K, Q6_K = 2, 6, 8, 10, 12, 14
-TYPES = {"Q4_0": Q4_0, "Q5_0": Q5_0, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K}
+Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 2, 6, 8, 10, 11, 12, 13, 14
+TYPES = {"Q4_0": Q4_0, "Q5_0": Q5_0, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
 ORDER_X86_CONTRACT, ORDER_X86_STRICT, ORDER_SCALAR = 0, 1, 2
-BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q2_K: 256, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q2_K: 84, Q4_K: 144, Q6_K: 210}
-ACT_BYTES = {Q4_0: 36, Q5_0: 36, Q8_0: 36, Q2_K: 292, Q4_K: 292, Q6_K: 292}
+BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+ACT_BYTES = {Q4_0: 36, Q5_0: 36, Q8_0: 36, Q2_K: 292, Q3_K: 292, Q4_K: 292, Q5_K: 292, Q6_K: 292}
 
 
 class EsHipError(RuntimeError):

@@ -34,7 +34,7 @@ def main():
     R = {"gcc": O.RefLib("gcc"), "clang": O.RefLib("clang"), "scalar": O.RefLib("gcc", scalar=True)}
     out = {}
     st = np.array([88172645463325252], np.uint64)   # tools/es_mtest.c:9
-    for t in (O.Q5_0, O.Q4_0, O.Q4_K, O.Q6_K, O.Q2_K, O.Q8_0):   # es_mtest's order, Q2_K and Q8_0 appended
+    for t in (O.Q5_0, O.Q4_0, O.Q4_K, O.Q6_K, O.Q2_K, O.Q8_0, O.Q5_K, O.Q3_K):   # es_mtest's order, then the rest appended
         F = O.NAMES[t]
         cases = {}
         cols, rows, na = 1024, 37, 13

@@ -38,7 +38,7 @@ def test_exports_are_c_symbols():
         assert re.search(rf"\sT\s{n}$", out, flags=re.M), n   # unmangled, extern "C"
 
 
-@pytest.mark.parametrize("F", ["Q4_0", "Q5_0", "Q8_0", "Q2_K", "Q4_K", "Q6_K"])
+@pytest.mark.parametrize("F", ["Q4_0", "Q5_0", "Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"])
 def test_row_bytes_match_reference(hiplib, F):
     t = O.TYPES[F]
     assert hiplib._L.es_hip_quant_supported(t) == 1
@@ -47,7 +47,7 @@ def test_row_bytes_match_reference(hiplib, F):
 
 
 def test_unsupported_types(hiplib):
-    for t in (0, 1, 3, 7, 11, 13, 16, 39):
+    for t in (0, 1, 3, 7, 9, 15, 16, 39):
         assert hiplib._L.es_hip_quant_supported(t) == 0
         assert hiplib._L.es_hip_row_bytes(t, 256) == 0
 

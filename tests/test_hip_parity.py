@@ -12,7 +12,7 @@ import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K", "Q8_0"]
+FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K", "Q8_0", "Q5_K", "Q3_K"]
 MODES = [(E.ORDER_X86_CONTRACT, "clang", O.CONTRACT, O.PATH_X86), (E.ORDER_X86_STRICT, "gcc", O.STRICT, O.PATH_X86),
          (E.ORDER_SCALAR, "scalar", O.STRICT, O.PATH_SCALAR)]
 
@@ -91,6 +91,10 @@ SHAPES = [
     ("Q6_K", 2048, 768, 3),     # config 5 expert down
     ("Q5_0", 4096, 2048, 4),    # config 5 attention q
     ("Q5_0", 512, 2048, 5),     # config 5 attention k/v
+    ("Q5_K", 2048, 768, 3),     # Q5_K / Q3_K tensors of the K-quant mixes, odd block count per row
+    ("Q5_K", 1024, 4096, 2),
+    ("Q3_K", 2048, 768, 3),
+    ("Q3_K", 1024, 4096, 2),
 ]
 
 
@@ -108,7 +112,7 @@ def test_baseline_shapes_vs_oracle(order, orc, F, rows, cols, na, mode):
 
 @pytest.mark.parametrize("F,rows,cols", [("Q4_K", 512, 2048), ("Q6_K", 300, 1024), ("Q2_K", 256, 2048),
                                           ("Q4_0", 200, 896), ("Q5_0", 128, 2048), ("Q4_K", 64, 14336),
-                                          ("Q8_0", 300, 2048)])
+                                          ("Q8_0", 300, 2048), ("Q5_K", 300, 2048), ("Q3_K", 257, 768)])
 def test_multi_equals_single(hip, orc, F, rows, cols):
     """es_mtest's invariant on the device: one launch over na activations == na single-activation launches"""
     t = O.TYPES[F]
@@ -159,7 +163,8 @@ def test_edge_blocks(hip, orc, F):
     rng = np.random.default_rng(9)
     W[3] = rng.integers(0, 256, W[3].shape, dtype=np.uint8)
     W[4] = rng.integers(0, 256, W[4].shape, dtype=np.uint8)
-    dpos = {O.Q4_0: [0], O.Q5_0: [0], O.Q8_0: [0], O.Q4_K: [0, 2], O.Q6_K: [208], O.Q2_K: [80, 82]}[t]
+    dpos = {O.Q4_0: [0], O.Q5_0: [0], O.Q8_0: [0], O.Q4_K: [0, 2], O.Q6_K: [208], O.Q2_K: [80, 82],
+            O.Q5_K: [0, 2], O.Q3_K: [108]}[t]
     for p in dpos:
         W[2, :, p:p + 2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)   # 1.0: extreme integers, sane scale
         W[3, :, p:p + 2] = np.frombuffer(np.uint16(0x0007).tobytes(), np.uint8)   # subnormal half
@@ -238,7 +243,7 @@ def test_invalid_arguments_are_rejected(hip):
     with pytest.raises(E.EsHipError):   # misaligned weights
         hip.matvec_multi_dev(E.Q4_K, buf.offset(2), 256, 0, 4, buf, 0, 1, buf, 0)
     with pytest.raises(E.EsHipError):   # unsupported type
-        hip.matvec_multi_dev(11, buf, 256, 0, 4, buf, 0, 1, buf, 0)
+        hip.matvec_multi_dev(7, buf, 256, 0, 4, buf, 0, 1, buf, 0)
     with pytest.raises(E.EsHipError):   # overlapping outputs
         hip.matvec_multi_dev(E.Q4_K, buf, 256, 0, 4, buf, 292, 2, buf, 2)
     hip.matvec_multi_dev(E.Q4_K, buf, 256, 4, 4, buf, 0, 1, buf, 0)   # empty range: nothing to do

@@ -6,7 +6,7 @@ import pytest
 import oracle as O
 import _layouts as L
 
-FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K", "Q8_0"]
+FMTS = ["Q5_0", "Q4_0", "Q4_K", "Q6_K", "Q2_K", "Q8_0", "Q5_K", "Q3_K"]
 CASES = ["mtest", "gauss"]
 
 
@@ -156,7 +156,8 @@ def test_fp16_conversions(orc, golden):
 def test_weight_quantizers_round_trip(orc):
     rows, cols = 8, 1024
     w = orc.gauss(5, 0.02, rows * cols).reshape(rows, cols)
-    for F, bound in (("Q4_0", 0.2), ("Q5_0", 0.1), ("Q4_K", 0.15), ("Q6_K", 0.05), ("Q2_K", 0.6)):
+    for F, bound in (("Q4_0", 0.2), ("Q5_0", 0.1), ("Q8_0", 0.01), ("Q4_K", 0.15), ("Q5_K", 0.08), ("Q6_K", 0.05),
+                     ("Q3_K", 0.3), ("Q2_K", 0.6)):
         t = O.TYPES[F]
         W = orc.quantize_rows(t, w)
         rb = O.row_bytes(t, cols)
