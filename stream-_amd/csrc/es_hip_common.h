@@ -16,11 +16,11 @@ template <int F> struct Fmt;
 template <> struct Fmt<ES_HIP_Q4_0> { static constexpr int BE = 32, BB = 18, AB = 36, LPB = 1; };
 template <> struct Fmt<ES_HIP_Q5_0> { static constexpr int BE = 32, BB = 22, AB = 36, LPB = 1; };
 template <> struct Fmt<ES_HIP_Q8_0> { static constexpr int BE = 32, BB = 34, AB = 36, LPB = 1; };
-template <> struct Fmt<ES_HIP_Q2_K> { static constexpr int BE = 256, BB = 84, AB = 292, LPB = 8; };
-template <> struct Fmt<ES_HIP_Q3_K> { static constexpr int BE = 256, BB = 110, AB = 292, LPB = 8; };
-template <> struct Fmt<ES_HIP_Q4_K> { static constexpr int BE = 256, BB = 144, AB = 292, LPB = 8; };
-template <> struct Fmt<ES_HIP_Q5_K> { static constexpr int BE = 256, BB = 176, AB = 292, LPB = 8; };
-template <> struct Fmt<ES_HIP_Q6_K> { static constexpr int BE = 256, BB = 210, AB = 292, LPB = 8; };
+template <> struct Fmt<ES_HIP_Q2_K> { static constexpr int BE = 256, BB = 84, AB = 292, LPB = 4; };
+template <> struct Fmt<ES_HIP_Q3_K> { static constexpr int BE = 256, BB = 110, AB = 292, LPB = 4; };
+template <> struct Fmt<ES_HIP_Q4_K> { static constexpr int BE = 256, BB = 144, AB = 292, LPB = 4; };
+template <> struct Fmt<ES_HIP_Q5_K> { static constexpr int BE = 256, BB = 176, AB = 292, LPB = 4; };
+template <> struct Fmt<ES_HIP_Q6_K> { static constexpr int BE = 256, BB = 210, AB = 292, LPB = 4; };
 
 // One product handed to a kernel: rows [r0, r1) of W against na activations. Tiles of `rows_per_wg` rows, one per
 // workgroup, numbered from tile0 across the jobs of a launch.

@@ -25,6 +25,15 @@
 #ifndef ESQ_UNITS
 #define ESQ_UNITS 4
 #endif
+#ifndef Q6K_UNITS1
+#define Q6K_UNITS1 2
+#endif
+#ifndef Q6K_UNITSN
+#define Q6K_UNITSN 1
+#endif
+#ifndef K_UNITSN
+#define K_UNITSN 2
+#endif
 // resident waves per SIMD the register allocation must allow
 #ifndef ESQ_MIN_WAVES
 #define ESQ_MIN_WAVES 1
@@ -44,31 +53,35 @@ enum { CH_FMA = 0, CH_MULADD = 1, CH_LANES = 2 };
 
 template <int F> struct Lane;
 
-// Q4_K: lane k of 8 takes qs bytes [16k, 16k+16): chunk c = k/2, half h = k%2; its low nibbles are elements
-// 64c + 16h + [0,16) (sub-block 2c), its high nibbles 64c + 32 + 16h + [0,16) (sub-block 2c+1). src/es_quant.c:1056-1080.
+// Q4_K: lane k of 4 takes qs chunk k, bytes [32k, 32k+32): its low nibbles are elements 64k + [0,32) (sub-block 2k),
+// its high nibbles 64k + 32 + [0,32) (sub-block 2k+1). src/es_quant.c:1056-1080.
 template <> struct Lane<ES_HIP_Q4_K> {
-    struct Raw { uint4 hdr, q; };
-    struct Act { uint32_t lo[4], hi[4]; int bs0, bs1; float d; };
-    struct Wt { uint32_t lo[4], hi[4]; int sc0, sc1, mn0, mn1; float d, dmin; };
+    struct Raw { uint4 hdr, q0, q1; };
+    struct Act { uint32_t lo[8], hi[8]; int bs0, bs1; float d; };
+    struct Wt { uint32_t lo[8], hi[8]; int sc0, sc1, mn0, mn1; float d, dmin; };
     struct Ints { int dot, aux; };
 
     static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
-        const int c = k >> 1, h = k & 1;
         x.d = ldg<float>(a);
-        const uint4 v0 = ldg<uint4>(a + 4 + 64 * c + 16 * h), v1 = ldg<uint4>(a + 4 + 64 * c + 32 + 16 * h);
-        x.lo[0] = v0.x; x.lo[1] = v0.y; x.lo[2] = v0.z; x.lo[3] = v0.w;
-        x.hi[0] = v1.x; x.hi[1] = v1.y; x.hi[2] = v1.z; x.hi[3] = v1.w;
-        x.bs0 = ldg<int16_t>(a + 260 + 2 * (4 * c + h));
-        x.bs1 = ldg<int16_t>(a + 260 + 2 * (4 * c + 2 + h));
+#pragma unroll
+        for (int v = 0; v < 2; v++) {
+            const uint4 l = ldg<uint4>(a + 4 + 64 * k + 16 * v), h = ldg<uint4>(a + 4 + 64 * k + 32 + 16 * v);
+            x.lo[4 * v] = l.x; x.lo[4 * v + 1] = l.y; x.lo[4 * v + 2] = l.z; x.lo[4 * v + 3] = l.w;
+            x.hi[4 * v] = h.x; x.hi[4 * v + 1] = h.y; x.hi[4 * v + 2] = h.z; x.hi[4 * v + 3] = h.w;
+        }
+        const uint2 b = ldg<uint2>(a + 260 + 8 * k);   // bsums 4k .. 4k+3, the last 8 bytes of the record for k = 3
+        x.bs0 = static_cast<int16_t>(b.x) + static_cast<int16_t>(b.x >> 16);
+        x.bs1 = static_cast<int16_t>(b.y) + static_cast<int16_t>(b.y >> 16);
     }
     static __device__ __forceinline__ void zero_act(Act &x) {
-        for (int i = 0; i < 4; i++) x.lo[i] = x.hi[i] = 0;
+        for (int i = 0; i < 8; i++) x.lo[i] = x.hi[i] = 0;
         x.bs0 = x.bs1 = 0;
         x.d = 0.0f;
     }
     static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
         r.hdr = ldw4(blk);
-        r.q = ldw4(blk + 16 + 16 * k);
+        r.q0 = ldw4(blk + 16 + 32 * k);
+        r.q1 = ldw4(blk + 32 + 32 * k);
     }
     // 6-bit scale and min of sub-block j from the 12 packed bytes (scale_min_k4, src/es_quant.c:75-83)
     static __device__ __forceinline__ void scale_min(uint32_t s03, uint32_t s47, uint32_t s811, int j, int &sc, int &mn) {
@@ -78,17 +91,16 @@ template <> struct Lane<ES_HIP_Q4_K> {
         else { sc = (c & 15) | ((a >> 6) << 4); mn = (c >> 4) | ((b >> 6) << 4); }
     }
     static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
-        const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-        for (int i = 0; i < 4; i++) { w.lo[i] = qq[i] & 0x0f0f0f0fu; w.hi[i] = (qq[i] >> 4) & 0x0f0f0f0fu; }
-        const int c = k >> 1;
-        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * c, w.sc0, w.mn0);
-        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * c + 1, w.sc1, w.mn1);
+        const uint32_t qq[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        for (int i = 0; i < 8; i++) { w.lo[i] = qq[i] & 0x0f0f0f0fu; w.hi[i] = (qq[i] >> 4) & 0x0f0f0f0fu; }
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * k, w.sc0, w.mn0);
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * k + 1, w.sc1, w.mn1);
         w.d = half_bits_to_float(r.hdr.x);
         w.dmin = half_bits_to_float(r.hdr.x >> 16);
     }
     static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
         int lo = 0, hi = 0;
-        for (int i = 0; i < 4; i++) { lo = sdot4(w.lo[i], x.lo[i], lo); hi = sdot4(w.hi[i], x.hi[i], hi); }
+        for (int i = 0; i < 8; i++) { lo = sdot4(w.lo[i], x.lo[i], lo); hi = sdot4(w.hi[i], x.hi[i], hi); }
         return {w.sc0 * lo + w.sc1 * hi, w.mn0 * x.bs0 + w.mn1 * x.bs1};
     }
     // s += y.d * (d * dot - dmin * mins)   (src/es_quant.c:1077, 1339)
@@ -99,25 +111,27 @@ template <> struct Lane<ES_HIP_Q4_K> {
     }
 };
 
-// Q5_K: Q4_K's lanes (same qs bytes at offset 48, same activation slice) plus the fifth bit of each element: qh byte
-// 16h + l holds bit 2c for low-nibble element 64c + 16h + l and bit 2c + 1 for high-nibble element 64c + 32 + 16h + l, so
-// lane k also takes qh[16h, 16h + 16). src/es_quant.c:1153-1175.
+// Q5_K: Q4_K's lanes (same qs chunks at offset 48, same activation slice) plus the fifth bit of each element: qh byte l
+// holds bit 2c for low-nibble element 64c + l and bit 2c + 1 for high-nibble element 64c + 32 + l, so every lane also
+// takes all 32 qh bytes. src/es_quant.c:1153-1175.
 template <> struct Lane<ES_HIP_Q5_K> : Lane<ES_HIP_Q4_K> {
-    struct Raw { uint4 hdr, qh, q; };
+    struct Raw { uint4 hdr, h0, h1, q0, q1; };
     static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
         r.hdr = ldw4(blk);
-        r.qh = ldw4(blk + 16 + 16 * (k & 1));
-        r.q = ldw4(blk + 48 + 16 * k);
+        r.h0 = ldw4(blk + 16);
+        r.h1 = ldw4(blk + 32);
+        r.q0 = ldw4(blk + 48 + 32 * k);
+        r.q1 = ldw4(blk + 64 + 32 * k);
     }
     static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
-        const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, hh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-        const int c = k >> 1;
-        for (int i = 0; i < 4; i++) {
-            w.lo[i] = (qq[i] & 0x0f0f0f0fu) | (((hh[i] >> (2 * c)) & 0x01010101u) << 4);
-            w.hi[i] = ((qq[i] >> 4) & 0x0f0f0f0fu) | (((hh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+        const uint32_t qq[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t hh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+        for (int i = 0; i < 8; i++) {
+            w.lo[i] = (qq[i] & 0x0f0f0f0fu) | (((hh[i] >> (2 * k)) & 0x01010101u) << 4);
+            w.hi[i] = ((qq[i] >> 4) & 0x0f0f0f0fu) | (((hh[i] >> (2 * k + 1)) & 0x01010101u) << 4);
         }
-        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * c, w.sc0, w.mn0);
-        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * c + 1, w.sc1, w.mn1);
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * k, w.sc0, w.mn0);
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * k + 1, w.sc1, w.mn1);
         w.d = half_bits_to_float(r.hdr.x);
         w.dmin = half_bits_to_float(r.hdr.x >> 16);
     }
@@ -130,68 +144,84 @@ template <> struct Lane<ES_HIP_Q5_K> : Lane<ES_HIP_Q4_K> {
     }
 };
 
-// Q6_K: lane k of 8: half h = k/4, j = (k/2)%2, p = k%2. It takes ql[64h + 32p + 16j, +16) and qh[32h + 16j, +16);
-// low nibbles (with qh bits 2p, 2p+1) are group g1 = 8h + 2p + j, high nibbles (qh bits 2p+4, 2p+5) group g1 + 4, where a
-// group is 16 consecutive elements with one int8 scale. The 6-bit codes are dotted unsigned and corrected by
-// 32 * bsums (the same integer as the signed form). src/es_quant.c:1081-1117, 1443-1469.
+// Q6_K: lane k of 4: half h = k/2, p = k%2. It takes ql[64h + 32p, +32) and qh[32h, +32); for j = 0, 1 the low nibbles
+// of ql bytes 16j + [0,16) (with qh bits 2p, 2p+1) are group 8h + 2p + j, the high nibbles (qh bits 2p+4, 2p+5) group
+// 8h + 2p + j + 4, where a group is 16 consecutive elements with one int8 scale. The 6-bit codes are dotted unsigned and
+// corrected by 32 * bsums (the same integer as the signed form). src/es_quant.c:1081-1117, 1443-1469.
 template <> struct Lane<ES_HIP_Q6_K> {
-    // 16-byte fields at 2-byte aligned addresses are read as five aligned dwords and realigned with v_alignbyte. All of it
+    // 32-byte fields at 2-byte aligned addresses are read as nine aligned dwords and realigned with v_alignbyte. All of it
     // lies inside the block: the block starts 4-byte aligned or 2 bytes past (then the dword before is the previous
-    // block's), and the last field read here (qh, offset 176) ends 18 bytes before the block does.
-    struct Raw { uint4 lv, hv; uint32_t l4, h4, sel; int s1, s2; uint32_t d16; };
-    struct Act { uint32_t y1[4], y2[4]; int bs1, bs2; float d; };
-    struct Wt { uint32_t q1[4], q2[4]; int sc1, sc2; float d; };
+    // block's), and the last field read here (d, offset 208) ends the block.
+    struct Raw { uint4 l0, l1, h0, h1; uint32_t l8, h8, sel, sa, sb, d16; };
+    struct Act { uint32_t y[4][4]; int bs[4]; float d; };   // groups g0, g0 + 1, g0 + 4, g0 + 5 with g0 = 8h + 2p
+    struct Wt { uint32_t c[4][4]; int sc[4]; float d; };
     struct Ints { int dot, aux; };
 
-    static __device__ __forceinline__ int g1_of(int k) { return 8 * (k >> 2) + 2 * (k & 1) + ((k >> 1) & 1); }
+    static __device__ __forceinline__ int grp(int k, int m) { return 8 * (k >> 1) + 2 * (k & 1) + (m & 1) + 4 * (m >> 1); }
     static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
-        const int g1 = g1_of(k), g2 = g1 + 4;
         x.d = ldg<float>(a);
-        const uint4 v0 = ldg<uint4>(a + 4 + 16 * g1), v1 = ldg<uint4>(a + 4 + 16 * g2);
-        x.y1[0] = v0.x; x.y1[1] = v0.y; x.y1[2] = v0.z; x.y1[3] = v0.w;
-        x.y2[0] = v1.x; x.y2[1] = v1.y; x.y2[2] = v1.z; x.y2[3] = v1.w;
-        x.bs1 = ldg<int16_t>(a + 260 + 2 * g1);
-        x.bs2 = ldg<int16_t>(a + 260 + 2 * g2);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int g = grp(k, m);
+            const uint4 v = ldg<uint4>(a + 4 + 16 * g);
+            x.y[m][0] = v.x; x.y[m][1] = v.y; x.y[m][2] = v.z; x.y[m][3] = v.w;
+            x.bs[m] = ldg<int16_t>(a + 260 + 2 * g);
+        }
     }
     static __device__ __forceinline__ void zero_act(Act &x) {
-        for (int i = 0; i < 4; i++) x.y1[i] = x.y2[i] = 0;
-        x.bs1 = x.bs2 = 0;
+        for (int m = 0; m < 4; m++) {
+            for (int i = 0; i < 4; i++) x.y[m][i] = 0;
+            x.bs[m] = 0;
+        }
         x.d = 0.0f;
     }
     static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
-        const int h = k >> 2, j = (k >> 1) & 1, p = k & 1;
-        const uintptr_t al = reinterpret_cast<uintptr_t>(blk + 64 * h + 32 * p + 16 * j);
-        const uintptr_t ah = reinterpret_cast<uintptr_t>(blk + 128 + 32 * h + 16 * j);
+        const int h = k >> 1, p = k & 1;
+        const uintptr_t al = reinterpret_cast<uintptr_t>(blk + 64 * h + 32 * p);
+        const uintptr_t ah = reinterpret_cast<uintptr_t>(blk + 128 + 32 * h);
         const uint8_t *bl = reinterpret_cast<const uint8_t *>(al & ~static_cast<uintptr_t>(3));
         const uint8_t *bh = reinterpret_cast<const uint8_t *>(ah & ~static_cast<uintptr_t>(3));
-        r.sel = static_cast<uint32_t>(al & 3);   // same for both fields (offsets differ by multiples of 16)
-        r.lv = ldw4(bl);
-        r.l4 = ldg<uint32_t>(bl + 16);
-        r.hv = ldw4(bh);
-        r.h4 = ldg<uint32_t>(bh + 16);
-        const int g1 = g1_of(k);
-        r.s1 = ldg<int8_t>(blk + 192 + g1);
-        r.s2 = ldg<int8_t>(blk + 192 + g1 + 4);
+        r.sel = static_cast<uint32_t>(al & 3);   // same for both fields (offsets differ by multiples of 32)
+        r.l0 = ldw4(bl);
+        r.l1 = ldw4(bl + 16);
+        r.l8 = ldg<uint32_t>(bl + 32);
+        r.h0 = ldw4(bh);
+        r.h1 = ldw4(bh + 16);
+        r.h8 = ldg<uint32_t>(bh + 32);
+        r.sa = ldg<uint16_t>(blk + 192 + 8 * h + 2 * p);       // scales of groups g0, g0 + 1
+        r.sb = ldg<uint16_t>(blk + 192 + 8 * h + 2 * p + 4);   // g0 + 4, g0 + 5
         r.d16 = ldg<uint16_t>(blk + 208);
     }
     static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
-        const uint32_t ql[4] = {alignbyte(r.lv.y, r.lv.x, r.sel), alignbyte(r.lv.z, r.lv.y, r.sel),
-                                alignbyte(r.lv.w, r.lv.z, r.sel), alignbyte(r.l4, r.lv.w, r.sel)};
-        const uint32_t qh[4] = {alignbyte(r.hv.y, r.hv.x, r.sel), alignbyte(r.hv.z, r.hv.y, r.sel),
-                                alignbyte(r.hv.w, r.hv.z, r.sel), alignbyte(r.h4, r.hv.w, r.sel)};
+        const uint32_t lw[9] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w, r.l1.x, r.l1.y, r.l1.z, r.l1.w, r.l8};
+        const uint32_t hw[9] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w, r.h8};
         const int p = k & 1, sl = 2 * p, sh = 2 * p + 4;
-        for (int i = 0; i < 4; i++) {
-            w.q1[i] = (ql[i] & 0x0f0f0f0fu) | (((qh[i] >> sl) & 0x03030303u) << 4);
-            w.q2[i] = ((ql[i] >> 4) & 0x0f0f0f0fu) | (((qh[i] >> sh) & 0x03030303u) << 4);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t ql = alignbyte(lw[4 * j + i + 1], lw[4 * j + i], r.sel);
+                const uint32_t qh = alignbyte(hw[4 * j + i + 1], hw[4 * j + i], r.sel);
+                w.c[j][i] = (ql & 0x0f0f0f0fu) | (((qh >> sl) & 0x03030303u) << 4);
+                w.c[2 + j][i] = ((ql >> 4) & 0x0f0f0f0fu) | (((qh >> sh) & 0x03030303u) << 4);
+            }
         }
-        w.sc1 = r.s1;
-        w.sc2 = r.s2;
+        w.sc[0] = static_cast<int8_t>(r.sa);
+        w.sc[1] = static_cast<int8_t>(r.sa >> 8);
+        w.sc[2] = static_cast<int8_t>(r.sb);
+        w.sc[3] = static_cast<int8_t>(r.sb >> 8);
         w.d = half_bits_to_float(r.d16);
     }
     static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
-        int s1 = 0, s2 = 0;
-        for (int i = 0; i < 4; i++) { s1 = sdot4(w.q1[i], x.y1[i], s1); s2 = sdot4(w.q2[i], x.y2[i], s2); }
-        return {w.sc1 * (s1 - 32 * x.bs1) + w.sc2 * (s2 - 32 * x.bs2), 0};
+        int dot = 0;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) s = sdot4(w.c[m][i], x.y[m][i], s);
+            dot += w.sc[m] * (s - 32 * x.bs[m]);
+        }
+        return {dot, 0};
     }
     // s += y.d * d * tot   (src/es_quant.c:1114, 1466)
     static __device__ __forceinline__ Term2 term(const Wt &w, const Act &x, Ints v, bool) {
@@ -200,48 +230,53 @@ template <> struct Lane<ES_HIP_Q6_K> {
 };
 
 // Q3_K: group g = 8n + 2j + half holds elements 16g + [0,16): bits 2j of qs[32n + 16half + l] and hmask[16half + l] bit
-// 4n + j (absent: minus 4). Lane k of 8: n = k/4, jp = (k/2)%2, half = k%2 takes qs[32n + 16half, +16) and
-// hmask[16half, +16), groups g1 = 8n + 4jp + half (j = 2jp) and g1 + 2 (j = 2jp + 1). The codes low2 + 4*hbit (0..7) are
-// dotted unsigned and corrected by 4 * bsums; the 6-bit scales minus 32 come from the 12 packed bytes
-// (src/es_quant.c:1120-1151, 1370-1394). 16-byte fields at 2-byte aligned addresses are read as five aligned dwords, as
-// for Q6_K: the last one read (qs, offset 80) ends 12 bytes before the block does.
+// 4n + j (absent: minus 4). Lane k of 4: n = k/2, half = k%2 takes qs[32n + 16half, +16) and hmask[16half, +16), and
+// with them the four groups 8n + 2j + half, j = 0..3. The codes low2 + 4*hbit (0..7) are dotted unsigned and corrected by
+// 4 * bsums; the 6-bit scales minus 32 come from the 12 packed bytes (src/es_quant.c:1120-1151, 1370-1394). Four lanes
+// per block keep the loads per block low: each 16-byte field is read as five aligned dwords (the block is 4-byte aligned
+// or 2 bytes past, as for Q6_K), the scales as three aligned dwords and a 2-byte load at 106; the last byte read is d's,
+// at 109, inside the block.
 template <> struct Lane<ES_HIP_Q3_K> {
-    struct Raw { uint4 qv, hv; uint32_t q4, h4, sel; uint32_t lo1, lo2, hi1, hi2; uint32_t d16; };
-    struct Act { uint32_t y1[4], y2[4]; int bs1, bs2; float d; };
-    struct Wt { uint32_t q1[4], q2[4]; int sc1, sc2; float d; };
+    struct Raw { uint4 qv, hv; uint32_t q4, h4, s0, s1, s2, s106, d16, sel; };
+    struct Act { uint32_t y[4][4]; int bs[4]; float d; };
+    struct Wt { uint32_t c[4][4]; int sc[4]; float d; };
     struct Ints { int dot, aux; };
 
-    static __device__ __forceinline__ int g1_of(int k) { return 8 * (k >> 2) + 4 * ((k >> 1) & 1) + (k & 1); }
     static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
-        const int g1 = g1_of(k), g2 = g1 + 2;
+        const int n = k >> 1, half = k & 1;
         x.d = ldg<float>(a);
-        const uint4 v0 = ldg<uint4>(a + 4 + 16 * g1), v1 = ldg<uint4>(a + 4 + 16 * g2);
-        x.y1[0] = v0.x; x.y1[1] = v0.y; x.y1[2] = v0.z; x.y1[3] = v0.w;
-        x.y2[0] = v1.x; x.y2[1] = v1.y; x.y2[2] = v1.z; x.y2[3] = v1.w;
-        x.bs1 = ldg<int16_t>(a + 260 + 2 * g1);
-        x.bs2 = ldg<int16_t>(a + 260 + 2 * g2);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int g = 8 * n + 2 * j + half;
+            const uint4 v = ldg<uint4>(a + 4 + 16 * g);
+            x.y[j][0] = v.x; x.y[j][1] = v.y; x.y[j][2] = v.z; x.y[j][3] = v.w;
+            x.bs[j] = ldg<int16_t>(a + 260 + 2 * g);
+        }
     }
     static __device__ __forceinline__ void zero_act(Act &x) {
-        for (int i = 0; i < 4; i++) x.y1[i] = x.y2[i] = 0;
-        x.bs1 = x.bs2 = 0;
+        for (int j = 0; j < 4; j++) {
+            for (int i = 0; i < 4; i++) x.y[j][i] = 0;
+            x.bs[j] = 0;
+        }
         x.d = 0.0f;
     }
     static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
-        const int n = k >> 2, half = k & 1, g1 = g1_of(k);
+        const int n = k >> 1, half = k & 1;
         const uintptr_t aq = reinterpret_cast<uintptr_t>(blk + 32 + 32 * n + 16 * half);
         const uintptr_t ah = reinterpret_cast<uintptr_t>(blk + 16 * half);
+        const uintptr_t as = reinterpret_cast<uintptr_t>(blk + 96);
         const uint8_t *bq = reinterpret_cast<const uint8_t *>(aq & ~static_cast<uintptr_t>(3));
         const uint8_t *bh = reinterpret_cast<const uint8_t *>(ah & ~static_cast<uintptr_t>(3));
-        r.sel = static_cast<uint32_t>(aq & 3);   // same for both fields (offsets differ by multiples of 16)
+        const uint8_t *bs = reinterpret_cast<const uint8_t *>(as & ~static_cast<uintptr_t>(3));
+        r.sel = static_cast<uint32_t>(aq & 3);   // the same for every field (their offsets differ by multiples of 16)
         r.qv = ldw4(bq);
         r.q4 = ldg<uint32_t>(bq + 16);
         r.hv = ldw4(bh);
         r.h4 = ldg<uint32_t>(bh + 16);
-        // scale of group g: low nibble of byte g % 8 (g < 8: bits 0-3, else 4-7), high pair bits 2(g/4) of byte 8 + g % 4
-        r.lo1 = ldg<uint8_t>(blk + 96 + (g1 & 7));
-        r.lo2 = ldg<uint8_t>(blk + 96 + ((g1 + 2) & 7));
-        r.hi1 = ldg<uint8_t>(blk + 104 + (g1 & 3));
-        r.hi2 = ldg<uint8_t>(blk + 104 + ((g1 + 2) & 3));
+        r.s0 = ldg<uint32_t>(bs);
+        r.s1 = ldg<uint32_t>(bs + 4);
+        r.s2 = ldg<uint32_t>(bs + 8);
+        r.s106 = ldg<uint16_t>(blk + 106);   // scale bytes 10, 11: the last aligned dword misses them when sel = 2
         r.d16 = ldg<uint16_t>(blk + 108);
     }
     static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
@@ -249,20 +284,38 @@ template <> struct Lane<ES_HIP_Q3_K> {
                                alignbyte(r.qv.w, r.qv.z, r.sel), alignbyte(r.q4, r.qv.w, r.sel)};
         const uint32_t h[4] = {alignbyte(r.hv.y, r.hv.x, r.sel), alignbyte(r.hv.z, r.hv.y, r.sel),
                                alignbyte(r.hv.w, r.hv.z, r.sel), alignbyte(r.h4, r.hv.w, r.sel)};
-        const int n = k >> 2, j1 = 2 * ((k >> 1) & 1), j2 = j1 + 1;
+        // scale bytes 0-3, 4-7, 8-11
+        const uint32_t S0 = alignbyte(r.s1, r.s0, r.sel), S1 = alignbyte(r.s2, r.s1, r.sel), S2 = alignbyte(r.s106, r.s2, r.sel);
+        const int n = k >> 1, half = k & 1;
+#pragma unroll
         for (int i = 0; i < 4; i++) {
-            w.q1[i] = ((q[i] >> (2 * j1)) & 0x03030303u) | (((h[i] >> (4 * n + j1)) & 0x01010101u) << 2);
-            w.q2[i] = ((q[i] >> (2 * j2)) & 0x03030303u) | (((h[i] >> (4 * n + j2)) & 0x01010101u) << 2);
+            const uint32_t hs = h[i] >> (4 * n);   // bits j of every byte: the high bits of group j
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t hb = j <= 2 ? (hs << (2 - j)) & 0x04040404u : (hs >> 1) & 0x04040404u;
+                w.c[j][i] = ((q[i] >> (2 * j)) & 0x03030303u) | hb;
+            }
         }
-        const int g1 = g1_of(k), g2 = g1 + 2;
-        w.sc1 = static_cast<int>(((r.lo1 >> (4 * (g1 >> 3))) & 15) | (((r.hi1 >> (2 * (g1 >> 2))) & 3) << 4)) - 32;
-        w.sc2 = static_cast<int>(((r.lo2 >> (4 * (g2 >> 3))) & 15) | (((r.hi2 >> (2 * (g2 >> 2))) & 3) << 4)) - 32;
+        // group g = 8n + 2j + half: low nibble of byte g % 8 (bits 4n), high pair of byte 8 + g % 4 (bits 2(g / 4))
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int bl = 8 * (2 * (j & 1) + half);
+            const uint32_t lo = ((j < 2 ? S0 : S1) >> (bl + 4 * n)) & 15u;
+            const uint32_t hi = (S2 >> (bl + 2 * (2 * n + (j >> 1)))) & 3u;
+            w.sc[j] = static_cast<int>(lo | (hi << 4)) - 32;
+        }
         w.d = half_bits_to_float(r.d16);
     }
     static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
-        int s1 = 0, s2 = 0;
-        for (int i = 0; i < 4; i++) { s1 = sdot4(w.q1[i], x.y1[i], s1); s2 = sdot4(w.q2[i], x.y2[i], s2); }
-        return {w.sc1 * (s1 - 4 * x.bs1) + w.sc2 * (s2 - 4 * x.bs2), 0};
+        int dot = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) s = sdot4(w.c[j][i], x.y[j][i], s);
+            dot += w.sc[j] * (s - 4 * x.bs[j]);
+        }
+        return {dot, 0};
     }
     // s += y.d * d * tot   (src/es_quant.c:1147, 1391)
     static __device__ __forceinline__ Term2 term(const Wt &w, const Act &x, Ints v, bool) {
@@ -270,41 +323,44 @@ template <> struct Lane<ES_HIP_Q3_K> {
     }
 };
 
-// Q2_K: lane k of 8: half h = k/4, part = (k/2)%2, sub = k%2. It takes qs[32h + 16part + 8sub, +8); shift 2s of those
-// bytes holds elements 16g + 8sub + [0,8) of group g = 8h + 2s + part (weight order of src/es_q2k.h:1-15).
-// isum = sum_g (sc[g] & 15) * sum q*y; summs = sum_g bsums[g] * (sc[g] >> 4), added once per group (sub 0 lanes).
-// src/es_q2k.c:127-148, src/es_quant.c:1344-1368.
+// Q2_K: lane k of 4: half h = k/2, part = k%2. It takes qs[32h + 16part, +16); shift 2s of those bytes holds the 16
+// elements 16g + [0,16) of group g = 8h + 2s + part (weight order of src/es_q2k.h:1-15), s = 0..3.
+// isum = sum_g (sc[g] & 15) * sum q*y; summs = sum_g bsums[g] * (sc[g] >> 4). src/es_q2k.c:127-148,
+// src/es_quant.c:1344-1368.
 template <> struct Lane<ES_HIP_Q2_K> {
-    struct Raw { uint2 q, sc; uint32_t dd; };
-    struct Act { uint32_t y[4][2]; int bs[4]; float d; };
-    struct Wt { uint32_t q[2]; int scl[4], mn[4]; float d, dmin; };
+    struct Raw { uint4 q; uint2 sc; uint32_t dd; };
+    struct Act { uint32_t y[4][4]; int bs[4]; float d; };
+    struct Wt { uint32_t q[4]; int scl[4], mn[4]; float d, dmin; };
     struct Ints { int dot, aux; };
 
     static __device__ __forceinline__ void load_act(const uint8_t *a, int k, Act &x) {
-        const int h = k >> 2, part = (k >> 1) & 1, sub = k & 1;
+        const int h = k >> 1, part = k & 1;
         x.d = ldg<float>(a);
+#pragma unroll
         for (int s = 0; s < 4; s++) {
             const int g = 8 * h + 2 * s + part;
-            const uint2 v = ldg<uint2>(a + 4 + 16 * g + 8 * sub);
-            x.y[s][0] = v.x;
-            x.y[s][1] = v.y;
-            x.bs[s] = sub == 0 ? ldg<int16_t>(a + 260 + 2 * g) : 0;
+            const uint4 v = ldg<uint4>(a + 4 + 16 * g);
+            x.y[s][0] = v.x; x.y[s][1] = v.y; x.y[s][2] = v.z; x.y[s][3] = v.w;
+            x.bs[s] = ldg<int16_t>(a + 260 + 2 * g);
         }
     }
     static __device__ __forceinline__ void zero_act(Act &x) {
-        for (int s = 0; s < 4; s++) { x.y[s][0] = x.y[s][1] = 0; x.bs[s] = 0; }
+        for (int s = 0; s < 4; s++) {
+            for (int i = 0; i < 4; i++) x.y[s][i] = 0;
+            x.bs[s] = 0;
+        }
         x.d = 0.0f;
     }
     static __device__ __forceinline__ void load_raw(const uint8_t *blk, int k, Raw &r) {
-        const int h = k >> 2, part = (k >> 1) & 1, sub = k & 1;
-        r.q = ldw2(blk + 16 + 32 * h + 16 * part + 8 * sub);
+        const int h = k >> 1, part = k & 1;
+        r.q = ldw4(blk + 16 + 32 * h + 16 * part);
         r.sc = ldg<uint2>(blk + 8 * h);   // scales[8h .. 8h+8): byte 2s + part is group 8h + 2s + part
         r.dd = ldg<uint32_t>(blk + 80);
     }
     static __device__ __forceinline__ void unpack(const Raw &r, int k, Wt &w) {
-        const int part = (k >> 1) & 1;
-        w.q[0] = r.q.x;
-        w.q[1] = r.q.y;
+        const int part = k & 1;
+        w.q[0] = r.q.x; w.q[1] = r.q.y; w.q[2] = r.q.z; w.q[3] = r.q.w;
+#pragma unroll
         for (int s = 0; s < 4; s++) {
             const int byte = 2 * s + part;
             const uint32_t v = ((byte < 4 ? r.sc.x : r.sc.y) >> (8 * (byte & 3))) & 0xff;
@@ -316,10 +372,11 @@ template <> struct Lane<ES_HIP_Q2_K> {
     }
     static __device__ __forceinline__ Ints ints(const Wt &w, const Act &x) {
         int isum = 0, summs = 0;
+#pragma unroll
         for (int s = 0; s < 4; s++) {
-            const uint32_t m = 0x03030303u;
-            int p = sdot4((w.q[0] >> (2 * s)) & m, x.y[s][0], 0);
-            p = sdot4((w.q[1] >> (2 * s)) & m, x.y[s][1], p);
+            int p = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) p = sdot4((w.q[i] >> (2 * s)) & 0x03030303u, x.y[s][i], p);
             isum += w.scl[s] * p;
             summs += x.bs[s] * w.mn[s];
         }
@@ -431,6 +488,14 @@ template <> struct Lane<ES_HIP_Q8_0> : Lane32<ES_HIP_Q8_0> {};
 
 template <int F> constexpr bool is32() { return F == ES_HIP_Q4_0 || F == ES_HIP_Q5_0 || F == ES_HIP_Q8_0; }
 
+// units whose raw loads a wave issues together (a power of two): ESQ_UNITS, fewer where a lane's unit (Q6_K) or the
+// activation slices held for NT activations are large enough that more would cost resident waves
+template <int F, int NT> constexpr int units() {
+    if constexpr (F == ES_HIP_Q6_K) return NT == 1 ? Q6K_UNITS1 : Q6K_UNITSN;
+    else if constexpr (!is32<F>()) return NT == 1 ? ESQ_UNITS : K_UNITSN;
+    else return ESQ_UNITS;
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // The kernel
 
@@ -446,7 +511,7 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
     constexpr int LPB = Fmt<F>::LPB, BE = Fmt<F>::BE, BB = Fmt<F>::BB, AB = Fmt<F>::AB;
     constexpr int SLOTS = WAVE / LPB;
     constexpr bool W32 = is32<F>();
-    constexpr int U = ESQ_UNITS;   // row passes whose raw loads a wave issues before using any of them
+    constexpr int U = units<F, NT>();   // row passes whose raw loads a wave issues before using any of them
 
     MvJob J;
     if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];

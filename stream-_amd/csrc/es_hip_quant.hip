@@ -92,11 +92,11 @@ bool fmt_info(uint32_t t, FmtInfo &f) {
     case ES_HIP_Q4_0: f = {32, 18, 36, 1}; return true;
     case ES_HIP_Q5_0: f = {32, 22, 36, 1}; return true;
     case ES_HIP_Q8_0: f = {32, 34, 36, 1}; return true;
-    case ES_HIP_Q2_K: f = {256, 84, 292, 8}; return true;
-    case ES_HIP_Q3_K: f = {256, 110, 292, 8}; return true;
-    case ES_HIP_Q4_K: f = {256, 144, 292, 8}; return true;
-    case ES_HIP_Q5_K: f = {256, 176, 292, 8}; return true;
-    case ES_HIP_Q6_K: f = {256, 210, 292, 8}; return true;
+    case ES_HIP_Q2_K: f = {256, 84, 292, 4}; return true;
+    case ES_HIP_Q3_K: f = {256, 110, 292, 4}; return true;
+    case ES_HIP_Q4_K: f = {256, 144, 292, 4}; return true;
+    case ES_HIP_Q5_K: f = {256, 176, 292, 4}; return true;
+    case ES_HIP_Q6_K: f = {256, 210, 292, 4}; return true;
     }
     return false;
 }
@@ -106,6 +106,7 @@ constexpr size_t LDS_TARGET = 32 * 1024;   // bytes of chain terms per workgroup
 constexpr size_t LDS_MAX = 160 * 1024;      // gfx950 LDS per workgroup
 constexpr size_t TARGET_WG = 8192;          // workgroups a launch aims for (256 CUs x 8 resident 4-wave groups x 4)
 constexpr int MIN_ITERS = 4;                // row passes per workgroup at least (one pipelined load group)
+constexpr size_t CHAIN_MAX = 256;           // rows per chain batch at most
 constexpr size_t MIN_WG_BLOCKS = 512;       // blocks per workgroup at least: a workgroup's set-up (job lookup, gathered
                                             // activation loads) is a chain of dependent loads that small launches (an
                                             // MoE layer's experts at a few tokens each) would otherwise repeat per 24 rows
@@ -198,7 +199,7 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
             const int rstep = (waves / seg) * rpi;   // rows one pass of the workgroup covers
             const size_t per_row = (size_t)nbk * nt * cw * sizeof(float);
             if (per_row > LDS_MAX) return fail(ES_HIP_EINVAL, "type %u cols %d: a row needs %zu bytes of LDS", q->type, q->cols, per_row);
-            int chain_cap = (int)std::min<size_t>(256, std::max<size_t>(1, LDS_TARGET / per_row));
+            int chain_cap = (int)std::min<size_t>(CHAIN_MAX, std::max<size_t>(1, LDS_TARGET / per_row));
             if (chain_cap >= rstep) chain_cap -= chain_cap % rstep;
             int rpw = (int)std::max<size_t>((size_t)MIN_ITERS * rstep, (wg_blocks + nbk - 1) / nbk);
             rpw = std::min(rpw, (rows + rstep - 1) / rstep * rstep);
