@@ -184,7 +184,7 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
         const int waves = kv.first.second;
         int max_na = 1;
         for (const Req *q : kv.second) max_na = std::max(max_na, q->na);
-        const int nt = max_na >= 4 ? 4 : max_na >= 2 ? 2 : 1;
+        const int nt = max_na >= 3 ? 4 : max_na;   // 3 activations in one pass of 4 rather than two passes of 2
         Group g;
         g.L.type = static_cast<int>(kv.first.first);
         g.L.nt = nt;
