@@ -53,7 +53,8 @@ enum {
     ES_HIP_ENODEV = -1,   /* no usable gfx950 device */
     ES_HIP_EINVAL = -2,   /* bad type, shape, stride, alignment or pointer */
     ES_HIP_ERUNTIME = -3, /* a HIP runtime call failed */
-    ES_HIP_ENOMEM = -4
+    ES_HIP_ENOMEM = -4,
+    ES_HIP_EBUSY = -5     /* expert cache: every slot is loading or protected (the reference exits "expert cache too small") */
 };
 
 /* Activation blocks and the prepared-activation record: the same byte layouts as the reference's es_blk_q80
@@ -240,6 +241,61 @@ double es_hip_plan_time_ms(es_hip_plan *plan, int warmup, int iters, void *strea
  * Returns milliseconds per iteration, or a negative value on failure. */
 double es_hip_step_time_ms(es_hip_plan *const *plans, int np, es_hip_moe_plan *const *moe, int nm, int warmup, int iters,
                            void *stream);
+
+/* ---- Device expert cache: the reference's hot-expert RAM cache (src/es_cache.h:1-56, src/es_cache.c:1-71) with its slots
+ * in HBM, so expert products read their weights from device memory. Same slot policy: nslots equal slots of slot_bytes,
+ * keyed by (layer, expert); a claim takes the first empty slot, else evicts the lowest last_use + freq_weight * min(uses,
+ * 16) among slots not loading and not protected (protect_until >= step), the first of equal scores. Loads are
+ * hipMemcpyAsync copies on the caller's stream; a slot stays LOADING until its copy has finished (a HIP event), and a
+ * loading slot is never evicted. slot_bytes = 0 creates a bookkeeping-only cache (no device memory, no GPU needed). One
+ * cache is used from one host thread. */
+typedef struct es_hip_cache es_hip_cache;
+enum { ES_HIP_SLOT_EMPTY = 0, ES_HIP_SLOT_LOADING = 1, ES_HIP_SLOT_READY = 2 };   /* ES_SLOT_*, src/es_cache.h:19 */
+typedef struct {   /* the policy fields of es_slot (src/es_cache.h:21-30) */
+    int layer, expert, state, prefetched;
+    uint64_t last_use;
+    uint32_t uses;
+    uint64_t protect_until;
+} es_hip_slot_info;
+typedef struct {   /* es_cache's counters (src/es_cache.h:40-41) and its step */
+    uint64_t hits, misses, prefetch_issued, prefetch_used, prefetch_wasted, evictions, step;
+} es_hip_cache_stats;
+/* Where an expert's bytes are on the host: part r (gate, up, down) of expert e is bytes[r] bytes at base[r] + e * stride[r]
+ * (a 3-D GGUF slab: stride = the per-expert size, src/es_engine.c:663-664), placed at offset[r] inside the slot (the
+ * reference's XOFF). Parts with bytes[r] = 0 are skipped. */
+typedef struct {
+    const void *base[3];
+    uint64_t stride[3], bytes[3], offset[3];
+} es_hip_expert_src;
+
+/* es_cache_init / es_cache_free (src/es_cache.h:44-46) */
+int  es_hip_cache_create(es_hip_cache **out, int nslots, size_t slot_bytes, int nlayers, int nexperts, double freq_weight);
+void es_hip_cache_destroy(es_hip_cache *c);
+/* es_cache_find (src/es_cache.h:48-49): the slot holding (layer, expert), or -1 */
+int  es_hip_cache_find(const es_hip_cache *c, int layer, int expert);
+/* es_cache_claim (src/es_cache.h:51-54): pick a victim, map it to (layer, expert) in state LOADING; the slot, or
+ * ES_HIP_EBUSY when every slot is loading or protected. (layer, expert) must not be cached already. */
+int  es_hip_cache_claim(es_hip_cache *c, int layer, int expert);
+/* device address of a slot (NULL for a bookkeeping-only cache) */
+void *es_hip_cache_slot_ptr(const es_hip_cache *c, int slot);
+/* copy bytes from host memory into the slot at offset, asynchronously on stream (es_submit / read_expert_part) */
+int  es_hip_cache_load(es_hip_cache *c, int slot, size_t offset, const void *host, size_t bytes, void *stream);
+/* wait for the slot's copies, then mark it READY (es_wait / gio_wait) */
+int  es_hip_cache_wait(es_hip_cache *c, int slot);
+/* advance the layer-step counter (C.step++) */
+int  es_hip_cache_step(es_hip_cache *c);
+/* load_experts for layer (src/es_engine.c:665-708): step += 1; for each selected expert a hit (clearing `prefetched`,
+ * counted as a used prefetch) or a miss that claims a slot and loads the expert's parts from src (NULL: bookkeeping only);
+ * then uses += 1, last_use = step, protect_until = step. slots[j] receives expert sel[j]'s slot (-1 where no slot was
+ * free: the call then returns ES_HIP_EBUSY after handling the others). */
+int  es_hip_cache_acquire(es_hip_cache *c, int layer, const int *sel, int k, const es_hip_expert_src *src, int *slots,
+                          void *stream);
+/* the router's prefetch of one expert (src/es_engine.c:606-611): *slot = the claimed slot, marked prefetched and protected
+ * for 3 more steps, its parts loading from src (NULL: bookkeeping only); *slot = -1 and ES_HIP_OK when the expert is cached
+ * already; ES_HIP_EBUSY (*slot = -1) when no slot is free (the reference then stops prefetching) */
+int  es_hip_cache_prefetch(es_hip_cache *c, int layer, int expert, const es_hip_expert_src *src, void *stream, int *slot);
+int  es_hip_cache_slot_info(const es_hip_cache *c, int slot, es_hip_slot_info *out);
+int  es_hip_cache_get_stats(const es_hip_cache *c, es_hip_cache_stats *out);
 
 #ifdef __cplusplus
 }

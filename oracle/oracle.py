@@ -73,6 +73,7 @@ class Oracle:
             "esq_swiglu": (None, [vp, vp, vp, i]),
             "esq_rmsnorm": (None, [vp, vp, vp, i, f]),
             "esq_moe_combine": (None, [vp, vp, vp, i, i, i, vp]),
+            "esq_cache_trace": (i, [i, i, i, C.c_double, vp, i, vp, vp, vp]),
             "esq_cpu_bench": (C.c_double, [vp, u32, vp, sz, i, i, i, vp, sz, i, vp, i, C.c_double, vp]),
             "esq_bind_reference": (None, [vp]),
             "esq_multi_reference": (None, [u32, vp, i, i, i, vp, sz, i, vp, sz]),
@@ -195,6 +196,10 @@ class Oracle:
         self.lib.esq_swiglu(_p(g), _p(u), _p(h), g.size)
         return h
 
+    def cache_trace(self, nslots, nlayers, nexperts, freq_weight, ops):
+        """the hot-expert cache policy restated (esq_cache.c): -> (res, slots [nslots, 7], stats [7])"""
+        return cache_trace_run(self.lib.esq_cache_trace, nslots, nlayers, nexperts, freq_weight, ops)
+
     def rmsnorm(self, x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
         """rows of x (2-D) normalised one by one"""
         x = np.ascontiguousarray(x, np.float32)
@@ -292,6 +297,58 @@ class Oracle:
 
 class _EsAct(C.Structure):   # es_act, src/es_quant.h:32-37
     _fields_ = [("x", C.c_void_p), ("q8", C.c_void_p), ("q80", C.c_void_p), ("cols", C.c_int)]
+
+
+# ---- expert cache traces (esq_cache.h) ----
+OP_STEP, OP_ACQUIRE, OP_PREFETCH = 1, 2, 3
+
+
+def cache_trace_run(fn, nslots, nlayers, nexperts, freq_weight, ops):
+    """run a trace [n, 3] int32 through fn (esq_cache_trace or esref_cache_trace) -> (res, slots [nslots, 7], stats [7])"""
+    ops = np.ascontiguousarray(ops, np.int32).reshape(-1, 3)
+    res = np.zeros(len(ops), np.int32)
+    slots = np.zeros((nslots, 7), np.int64)
+    stats = np.zeros(7, np.uint64)
+    rc = fn(nslots, nlayers, nexperts, float(freq_weight), _p(ops), len(ops), _p(res), _p(slots), _p(stats))
+    if rc:
+        raise ValueError("bad cache trace arguments")
+    return res, slots, stats
+
+
+def make_cache_trace(seed, nlayers, nexperts, k, tokens, passes, prefetch="top"):
+    """an engine-like trace: for each pass over the layers, each layer one load_experts call of k distinct experts drawn
+    with a skewed popularity (so some experts stay hot), followed by a prefetch of k/2 experts of the next layer: its
+    most popular ones (prefetch="top"), random ones (prefetch="random", many of them wasted) or none (None)"""
+    rng = np.random.default_rng(seed)
+    pop = rng.zipf(1.3, size=(nlayers, nexperts)).astype(np.float64)
+    pop /= pop.sum(axis=1, keepdims=True)
+    ops = []
+    for _ in range(passes):
+        for l in range(nlayers):
+            for _ in range(tokens):
+                sel = rng.choice(nexperts, size=k, replace=False, p=pop[l])
+                ops.append((OP_STEP, l, 0))
+                ops += [(OP_ACQUIRE, l, int(e)) for e in sel]
+                if prefetch and l + 1 < nlayers:
+                    guess = (np.argsort(-pop[l + 1], kind="stable")[: max(1, k // 2)] if prefetch == "top" else
+                             rng.choice(nexperts, size=max(1, k // 2), replace=False))
+                    ops += [(OP_PREFETCH, l + 1, int(e)) for e in guess]
+    return np.array(ops, np.int32)
+
+
+class RefCache:
+    """the reference's es_cache.c driven by esq_cache_ref.c (oracle/_ref/libesref_cache.so)"""
+
+    def __init__(self):
+        path = os.path.join(HERE, "_ref", "libesref_cache.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle ref` where /root/reference exists")
+        self.lib = C.CDLL(path)
+        self.lib.esref_cache_trace.restype = C.c_int
+        self.lib.esref_cache_trace.argtypes = [C.c_int, C.c_int, C.c_int, C.c_double] + [C.c_void_p, C.c_int] + [C.c_void_p] * 3
+
+    def trace(self, nslots, nlayers, nexperts, freq_weight, ops):
+        return cache_trace_run(self.lib.esref_cache_trace, nslots, nlayers, nexperts, freq_weight, ops)
 
 
 def ref_path(cc: str) -> str:

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "es_hip_common.h"
+#include "es_hip_host.h"
 
 using esq::MvJob;
 using esq::MvLaunch;
@@ -1145,6 +1146,13 @@ int moe_run(const es_hip_moe_plan *p, hipStream_t s) {
 }
 
 }  // namespace
+
+// error reporting and device discovery for the library's other host files (es_hip_host.h)
+namespace esq {
+int host_fail(int code, const char *msg) { return fail(code, "%s", msg); }
+int host_hip_fail(hipError_t e, const char *what) { return hip_fail(e, what); }
+int host_need_device() { return need_device(); }
+}  // namespace esq
 
 extern "C" {
 

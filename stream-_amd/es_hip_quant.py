@@ -92,6 +92,116 @@ class DevBuf:
         return int(self.ptr) + int(nbytes)
 
 
+class SlotInfo(C.Structure):
+    _fields_ = [("layer", C.c_int), ("expert", C.c_int), ("state", C.c_int), ("prefetched", C.c_int),
+                ("last_use", C.c_uint64), ("uses", C.c_uint32), ("protect_until", C.c_uint64)]
+
+
+class CacheStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("hits", "misses", "prefetch_issued", "prefetch_used", "prefetch_wasted",
+                                          "evictions", "step")]
+
+
+class ExpertSrc(C.Structure):
+    """es_hip_expert_src: part r of expert e is bytes[r] bytes at base[r] + e * stride[r], placed at offset[r] in the slot"""
+    _fields_ = [("base", C.c_void_p * 3), ("stride", C.c_uint64 * 3), ("bytes", C.c_uint64 * 3), ("offset", C.c_uint64 * 3)]
+
+
+EBUSY = -5
+ES_HIP_SLOT_EMPTY, ES_HIP_SLOT_LOADING, ES_HIP_SLOT_READY = 0, 1, 2
+
+
+class ExpertCache:
+    """es_hip_cache_*: the reference's hot-expert cache with its slots in HBM (slot_bytes = 0: bookkeeping only)"""
+
+    def __init__(self, lib, nslots, slot_bytes, nlayers, nexperts, freq_weight):
+        self.lib, self.nslots, self.h = lib, nslots, None
+        h = C.c_void_p()
+        lib._check(lib._L.es_hip_cache_create(C.byref(h), nslots, slot_bytes, nlayers, nexperts, float(freq_weight)))
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            self.lib._L.es_hip_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def find(self, layer, expert):
+        return self.lib._L.es_hip_cache_find(self.h, layer, expert)
+
+    def claim(self, layer, expert):
+        return self.lib._check(self.lib._L.es_hip_cache_claim(self.h, layer, expert))
+
+    def slot_ptr(self, slot):
+        return self.lib._L.es_hip_cache_slot_ptr(self.h, slot)
+
+    def load(self, slot, offset, host: np.ndarray, stream=None):
+        self.lib._check(self.lib._L.es_hip_cache_load(self.h, slot, offset, host.ctypes.data, host.nbytes, stream))
+
+    def wait(self, slot):
+        self.lib._check(self.lib._L.es_hip_cache_wait(self.h, slot))
+
+    def step(self):
+        self.lib._check(self.lib._L.es_hip_cache_step(self.h))
+
+    def acquire(self, layer, sel, src=None, stream=None, allow_busy=False):
+        sel = np.ascontiguousarray(sel, np.int32)
+        slots = np.zeros(len(sel), np.int32)
+        rc = self.lib._L.es_hip_cache_acquire(self.h, layer, sel.ctypes.data, len(sel), C.byref(src) if src else None,
+                                              slots.ctypes.data, stream)
+        if not (allow_busy and rc == EBUSY):
+            self.lib._check(rc)
+        return slots
+
+    def prefetch(self, layer, expert, src=None, stream=None):
+        """the claimed slot; -2 if the expert was cached already, -1 if no slot was free (the oracle's trace codes)"""
+        slot = C.c_int(-1)
+        rc = self.lib._L.es_hip_cache_prefetch(self.h, layer, expert, C.byref(src) if src else None, stream, C.byref(slot))
+        if rc == EBUSY:
+            return -1
+        self.lib._check(rc)
+        return slot.value if slot.value >= 0 else -2
+
+    def slot_info(self, slot):
+        o = SlotInfo()
+        self.lib._check(self.lib._L.es_hip_cache_slot_info(self.h, slot, C.byref(o)))
+        return o
+
+    def stats(self):
+        o = CacheStats()
+        self.lib._check(self.lib._L.es_hip_cache_get_stats(self.h, C.byref(o)))
+        return o
+
+    def run_trace(self, ops):
+        """replay an oracle cache trace (ops [n, 3]: 1 = step, 2 = acquire, 3 = prefetch; a step and the acquires after it
+        are one es_hip_cache_acquire call) -> (res, slots [nslots, 7], stats [7]) in the oracle's format"""
+        ops = np.asarray(ops, np.int32).reshape(-1, 3)
+        res = np.zeros(len(ops), np.int32)
+        i = 0
+        while i < len(ops):
+            op, l, e = (int(v) for v in ops[i])
+            if op == 1:
+                j = i + 1
+                while j < len(ops) and ops[j, 0] == 2 and ops[j, 1] == l:
+                    j += 1
+                res[i + 1:j] = self.acquire(l, ops[i + 1:j, 2], allow_busy=True)
+                i = j
+                continue
+            if op == 3:
+                res[i] = self.prefetch(l, e)
+            else:
+                raise ValueError(f"operation {op} outside a step")
+            i += 1
+        slots = np.array([[x.layer, x.expert, x.state, x.prefetched, x.last_use, x.uses, x.protect_until]
+                          for x in (self.slot_info(k) for k in range(self.nslots))], np.int64)
+        st = self.stats()
+        stats = np.array([st.hits, st.misses, st.prefetch_issued, st.prefetch_used, st.prefetch_wasted, st.evictions, st.step],
+                         np.uint64)
+        return res, slots, stats
+
+
 class Lib:
     def __init__(self, path: str | None = None):
         path = path or LIB_PATH
@@ -128,6 +238,12 @@ class Lib:
             ("es_hip_route_softmax_dev", i, [vp, sz, i, i, i, i, vp, vp, i, vp]),
             ("es_hip_rmsnorm_prepare_dev", i, [vp, sz, vp, C.c_float, i, i, vp, sz, vp, sz, vp, sz, vp]),
             ("es_hip_swiglu_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp, sz, vp]),
+            ("es_hip_cache_create", i, [vp, i, sz, i, i, C.c_double]), ("es_hip_cache_destroy", None, [vp]),
+            ("es_hip_cache_find", i, [vp, i, i]), ("es_hip_cache_claim", i, [vp, i, i]),
+            ("es_hip_cache_slot_ptr", vp, [vp, i]), ("es_hip_cache_load", i, [vp, i, sz, vp, sz, vp]),
+            ("es_hip_cache_wait", i, [vp, i]), ("es_hip_cache_step", i, [vp]),
+            ("es_hip_cache_acquire", i, [vp, i, vp, i, vp, vp, vp]), ("es_hip_cache_prefetch", i, [vp, i, i, vp, vp, vp]),
+            ("es_hip_cache_slot_info", i, [vp, i, vp]), ("es_hip_cache_get_stats", i, [vp, vp]),
         ]:
             fn = getattr(L, name)
             fn.restype, fn.argtypes = res, args

@@ -29,6 +29,17 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 import oracle as O  # noqa: E402
 
 
+# name: (seed, slots, layers, experts, k, calls per layer, passes, freq_weight, prefetch)
+CACHE_TRACES = {
+    "lru": (1, 8, 4, 16, 4, 2, 3, 0.0, "top"),
+    "engine": (2, 24, 6, 64, 8, 3, 2, 6.0, "top"),
+    "olmoe": (3, 40, 4, 64, 8, 4, 3, 4.0, "top"),
+    "wasted": (5, 20, 4, 64, 6, 2, 3, 4.0, "random"),
+    "tiny": (4, 6, 3, 16, 8, 1, 2, 1.0, "top"),
+    "noprefetch": (6, 12, 5, 32, 4, 3, 2, 2.5, None),
+}
+
+
 def main():
     o = O.Oracle()
     R = {"gcc": O.RefLib("gcc"), "clang": O.RefLib("clang"), "scalar": O.RefLib("gcc", scalar=True)}
@@ -91,6 +102,19 @@ def main():
     out["fp16/f"] = fl
     out["fp16/h"] = np.array([R["gcc"].fp32_to_fp16(float(v)) for v in fl], np.uint16)
 
+    # expert cache traces through the reference's own es_cache.c (oracle/esq_cache_ref.c): engine-like load_experts /
+    # prefetch sequences with plain LRU, the engine's frequency weight (1.0 * layers) and others; one with too few slots
+    RC = O.RefCache()
+    for name, (seed, ns, nl, ne, k, tok, ps, fw, pf) in CACHE_TRACES.items():
+        ops = O.make_cache_trace(seed, nl, ne, k, tok, ps, prefetch=pf)
+        res, slots, stats = RC.trace(ns, nl, ne, fw, ops)
+        out[f"cache/{name}/ops"] = ops
+        out[f"cache/{name}/params"] = np.array([ns, nl, ne], np.int32)
+        out[f"cache/{name}/freq_weight"] = np.array([fw], np.float64)
+        out[f"cache/{name}/res"] = res
+        out[f"cache/{name}/slots"] = slots
+        out[f"cache/{name}/stats"] = stats
+
     np.savez_compressed(os.path.join(HERE, "ref_vectors.npz"), **out)
     cc = {}
     for name, exe in (("gcc", "gcc"), ("clang", "/opt/rocm/lib/llvm/bin/clang")):
@@ -99,7 +123,8 @@ def main():
         except OSError:
             cc[name] = "unknown"
     manifest = {
-        "source": "reference src/es_quant.c, src/es_q2k.c, src/es_cpu.c built by oracle/Makefile (-O3 -std=c11)",
+        "source": "reference src/es_quant.c, src/es_q2k.c, src/es_cpu.c built by oracle/Makefile (-O3 -std=c11); "
+                  "cache/*: src/es_cache.c, es_io.c, es_cpu.c with oracle/esq_cache_ref.c",
         "compilers": cc,
         "gcc": "x86 AVX2 path, no contraction", "clang": "x86 AVX2 path, -ffp-contract=on (the reference default CC)",
         "scalar": "gcc build with ES_NO_AVX2=1",
