@@ -260,6 +260,35 @@ class HipEvents:
         return ms.value / iters
 
 
+def cache_load_rate(lib, rng, K, Wm):
+    """Expert loads through the device expert cache (es_hip_cache_acquire) at config 5's expert size: gate/up Q4_K 768x2048
+    and down Q6_K 2048x768 (3,059,712 bytes), from pageable host slabs of 64 experts, 16 slots. Every call takes 8 experts
+    that are not cached (the cycle through 64 experts with 16 slots always misses), so each call copies 8 experts host ->
+    HBM and evicts 8; timed to the end of the copies. Host-to-device bound (PCIe), not an HBM figure."""
+    ne, nslots, k = 64, 16, 8
+    parts = [768 * 8 * 144, 768 * 8 * 144, 2048 * 3 * 210]
+    slabs = [rng.integers(0, 256, (ne, b), dtype=np.uint8) for b in parts]
+    src = E.ExpertSrc()
+    off = 0
+    for r in range(3):
+        src.base[r], src.stride[r], src.bytes[r], src.offset[r] = slabs[r].ctypes.data, parts[r], parts[r], off
+        off += parts[r]
+    c = E.ExpertCache(lib, nslots, off, 1, ne, 1.0)
+    calls = [np.arange(k * i, k * i + k) % ne for i in range(Wm + K)]
+    for sel in calls[:Wm]:
+        c.acquire(0, sel, src)
+    lib.synchronize()
+    t0 = time.perf_counter()
+    for sel in calls[Wm:]:
+        c.acquire(0, sel, src)
+    lib.synchronize()
+    dt = (time.perf_counter() - t0) / K
+    st = c.stats()
+    c.close()
+    return {"expert_bytes": off, "experts_per_call": k, "ms_per_call": round(dt * 1e3, 4),
+            "gbs": round(k * off / dt / 1e9, 2), "misses": st.misses, "evictions": st.evictions}
+
+
 def act_prep_times(lib, rng, K, Wm):
     """Device activation preparation at config 2's prefill shapes (T = 512): rmsnorm + Q8_K/Q8_0 of the 2048-wide layer
     input, SwiGLU + Q8_K of the dense FFN's 8192-wide gate|up rows, and the plain Q8_K/Q8_0 quantizers. us per call
@@ -302,6 +331,8 @@ def only(lib, rng, name, K, Wm):
         return {"workload": "copy", "bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": Wm + K}
     if name == "act":
         return {"workload": "act", **act_prep_times(lib, rng, K, Wm)}
+    if name == "cache":
+        return {"workload": "cache", **cache_load_rate(lib, rng, K, Wm)}
     if name in ("config4", "config5"):
         w = (MoeWorkload(lib, rng, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8) if name == "config4" else
              MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
@@ -332,7 +363,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=2.0)
     ap.add_argument("--only", choices=["decode", "prefill", "config1", "config3b1", "config3b64", "config4", "config5", "act",
-                                       "copy"] + [f"decode_{f.lower()}" for f in E.TYPES],
+                                       "cache", "copy"] + [f"decode_{f.lower()}" for f in E.TYPES],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -397,6 +428,7 @@ def main():
     c5.close()
     # ---- device activation preparation at config 2's prefill shapes (rmsnorm / SwiGLU fused with the quantizers)
     extra["act_prep_t512"] = act_prep_times(lib, rng, K, Wm)
+    extra["expert_cache_load"] = cache_load_rate(lib, rng, K, Wm)
 
     cpu = None
     if not args.no_cpu:
