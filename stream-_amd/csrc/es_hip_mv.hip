@@ -488,10 +488,11 @@ template <> struct Lane<ES_HIP_Q8_0> : Lane32<ES_HIP_Q8_0> {};
 
 template <int F> constexpr bool is32() { return F == ES_HIP_Q4_0 || F == ES_HIP_Q5_0 || F == ES_HIP_Q8_0; }
 
-// units whose raw loads a wave issues together (a power of two): ESQ_UNITS, fewer where a lane's unit (Q6_K) or the
-// activation slices held for NT activations are large enough that more would cost resident waves
+// units whose raw loads a wave issues together (a power of two): ESQ_UNITS, fewer where a lane's unit (Q6_K, Q3_K: four
+// and three realigned fields) or the activation slices held for NT activations are large enough that more would cost
+// resident waves
 template <int F, int NT> constexpr int units() {
-    if constexpr (F == ES_HIP_Q6_K) return NT == 1 ? Q6K_UNITS1 : Q6K_UNITSN;
+    if constexpr (F == ES_HIP_Q6_K || F == ES_HIP_Q3_K) return NT == 1 ? Q6K_UNITS1 : Q6K_UNITSN;
     else if constexpr (!is32<F>()) return NT == 1 ? ESQ_UNITS : K_UNITSN;
     else return ESQ_UNITS;
 }
