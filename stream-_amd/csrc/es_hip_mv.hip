@@ -541,6 +541,20 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
     constexpr int CW = W32 ? 9 : 2;   // floats per (row, block, activation) in LDS
     extern __shared__ float lds[];
 
+    typename L::Raw raw[U];
+    bool ok[U];
+    // the first unit batch's weight loads go out before the activation loads, so their latencies overlap (Q4_K at one
+    // activation per pass; elsewhere keeping these registers live across the activation loads cost more than it saved)
+    constexpr bool PRE = NT == 1 && F == ES_HIP_Q4_K;
+    bool pre = PRE && ra0 < rend;
+    if (pre) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int row = ra0 + rfirst + u * rstep;
+            ok[u] = live && row < min(ra0 + J.chain_rows, rend);
+            L::load_raw(ok[u] ? J.W + (size_t)row * J.row_bytes + (size_t)b * BB : dummy, k, raw[u]);
+        }
+    }
     for (int t0 = 0; t0 < J.na; t0 += NT) {
         const int nt = min(NT, J.na - t0);
         typename L::Act act[NT];
@@ -557,14 +571,15 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
             const int rb = min(ra + J.chain_rows, rend);
             // ---- phase 1: integers per block, float terms to LDS
             for (int r0 = ra + rfirst; r0 - rowoff < rb; r0 += U * rstep) {
-                typename L::Raw raw[U];
-                bool ok[U];
+                if (!pre) {
 #pragma unroll
-                for (int u = 0; u < U; u++) {
-                    const int row = r0 + u * rstep;
-                    ok[u] = live && row < rb;
-                    L::load_raw(ok[u] ? J.W + (size_t)row * J.row_bytes + (size_t)b * BB : dummy, k, raw[u]);
+                    for (int u = 0; u < U; u++) {
+                        const int row = r0 + u * rstep;
+                        ok[u] = live && row < rb;
+                        L::load_raw(ok[u] ? J.W + (size_t)row * J.row_bytes + (size_t)b * BB : dummy, k, raw[u]);
+                    }
                 }
+                pre = false;
 #pragma unroll
                 for (int u = 0; u < U; u++) {
                     const int row = r0 + u * rstep;
