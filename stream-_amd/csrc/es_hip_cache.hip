@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdint>
 #include <vector>
 
 #include "es_hip_common.h"
@@ -102,13 +103,27 @@ int load(es_hip_cache *c, int slot, size_t offset, const void *host, size_t byte
     return ES_HIP_OK;
 }
 
+// a slot whose expert could not be loaded is emptied, so it can never be found holding partial bytes
+void unmap(es_hip_cache *c, int slot) {
+    es_hip_cache::Slot &s = c->slots[slot];
+    if (s.layer >= 0) c->where[(size_t)s.layer * c->nexperts + s.expert] = -1;
+    s.layer = s.expert = -1;
+    s.state = ES_HIP_SLOT_EMPTY;
+    s.prefetched = 0;
+    s.uses = 0;
+}
+
 // the expert's parts from their host slabs into the slot (read_expert_part / the expert file, src/es_engine.c:686-699)
 int load_parts(es_hip_cache *c, int slot, int expert, const es_hip_expert_src *src, hipStream_t stream) {
     for (int r = 0; r < 3; r++) {
         if (!src->bytes[r]) continue;
         const uint8_t *h = static_cast<const uint8_t *>(src->base[r]);
-        if (!h) return host_fail(ES_HIP_EINVAL, "expert source part without a base pointer");
-        if (int rc = load(c, slot, src->offset[r], h + (size_t)expert * src->stride[r], src->bytes[r], stream)) return rc;
+        int rc = h ? load(c, slot, src->offset[r], h + (size_t)expert * src->stride[r], src->bytes[r], stream)
+                   : host_fail(ES_HIP_EINVAL, "expert source part without a base pointer");
+        if (rc) {
+            unmap(c, slot);
+            return rc;
+        }
     }
     return ES_HIP_OK;
 }
@@ -123,6 +138,8 @@ int es_hip_cache_create(es_hip_cache **out, int nslots, size_t slot_bytes, int n
     if (nslots <= 0 || nlayers <= 0 || nexperts <= 0 || (long long)nlayers * nexperts > (1LL << 30))
         return host_fail(ES_HIP_EINVAL, "nslots, nlayers and nexperts must be positive (nlayers * nexperts <= 2^30)");
     if (!std::isfinite(freq_weight) || freq_weight < 0.0) return host_fail(ES_HIP_EINVAL, "freq_weight must be finite and >= 0");
+    if (slot_bytes > (SIZE_MAX - 255) / 2 || (slot_bytes + 255) / 256 * 256 > SIZE_MAX / (size_t)nslots)
+        return host_fail(ES_HIP_EINVAL, "nslots x slot_bytes overflows");
     es_hip_cache *c = new es_hip_cache;
     c->nslots = nslots;
     c->nlayers = nlayers;

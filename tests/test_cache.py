@@ -101,6 +101,9 @@ def test_cache_rejects_bad_arguments(hiplib):
         E.ExpertCache(hiplib, 0, 0, 1, 4, 0.0)
     with pytest.raises(E.EsHipError):
         E.ExpertCache(hiplib, 2, 0, 1, 4, -1.0)
+    with pytest.raises(E.EsHipError) as err:
+        E.ExpertCache(hiplib, 1 << 20, 1 << 62, 1, 4, 0.0)   # nslots x slot_bytes overflows: refused before any device use
+    assert err.value.code == -2
     c = E.ExpertCache(hiplib, 2, 0, 2, 4, 1.0)
     try:
         with pytest.raises(E.EsHipError):
