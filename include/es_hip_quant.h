@@ -170,6 +170,13 @@ typedef struct {
  * situ activations. es_hip_moe_ffn is synchronous. */
 int es_hip_moe_ffn(const es_hip_moe *m, int N, const int *k, const int *sel, const float *w, int kmax, const void *x,
                    size_t xstride, float *out, size_t ostride, void *stream);
+/* The MoE layer from the router's logits (device, token t's n_exp logits at logits + t * lstride floats, 0: packed):
+ * route() for softmax gating on the device (es_hip_route_softmax_dev: top k, norm_topk), the k choices and weights of every
+ * token copied to the host for the grouping, then es_hip_moe_ffn with them. sel_out / w_out (host, N * k each, optional)
+ * receive the routing. Synchronous. */
+int es_hip_moe_ffn_logits(const es_hip_moe *m, int N, const float *logits, size_t lstride, int k, int norm_topk,
+                          const void *x, size_t xstride, float *out, size_t ostride, int *sel_out, float *w_out,
+                          void *stream);
 /* The same as a prepared plan: grouping, job tables and workspace are made once; runs are asynchronous on `stream`. The
  * routing (k, sel, w) is captured at creation; x, out and the expert bytes may change between runs. */
 typedef struct es_hip_moe_plan es_hip_moe_plan;

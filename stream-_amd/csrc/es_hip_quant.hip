@@ -1220,6 +1220,34 @@ int es_hip_moe_ffn(const es_hip_moe *m, int N, const int *k, const int *sel, con
     return rc;
 }
 
+int es_hip_moe_ffn_logits(const es_hip_moe *m, int N, const float *logits, size_t lstride, int k, int norm_topk,
+                          const void *x, size_t xstride, float *out, size_t ostride, int *sel_out, float *w_out,
+                          void *stream) {
+    if (int rc = need_device()) return rc;
+    if (!m) return fail(ES_HIP_EINVAL, "null MoE description");
+    if (N < 0 || k <= 0) return fail(ES_HIP_EINVAL, "bad token count %d or top-k %d", N, k);
+    if (N == 0) return ES_HIP_OK;
+    const size_t pairs = (size_t)N * k;
+    void *buf = nullptr;
+    hipError_t e = hipMalloc(&buf, pairs * (sizeof(int) + sizeof(float)));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc (routing)");
+    int *dsel = static_cast<int *>(buf);
+    float *dw = reinterpret_cast<float *>(dsel + pairs);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<int> sel(pairs), kk((size_t)N, k);
+    std::vector<float> w(pairs);
+    int rc = es_hip_route_softmax_dev(logits, lstride, N, m->n_exp, k, norm_topk, dsel, dw, k, stream);
+    if (!rc && ((e = hipMemcpyAsync(sel.data(), dsel, pairs * sizeof(int), hipMemcpyDeviceToHost, s)) != hipSuccess ||
+                (e = hipMemcpyAsync(w.data(), dw, pairs * sizeof(float), hipMemcpyDeviceToHost, s)) != hipSuccess ||
+                (e = hipStreamSynchronize(s)) != hipSuccess))
+        rc = hip_fail(e, "routing copy to the host");
+    (void)hipFree(buf);
+    if (rc) return rc;
+    if (sel_out) std::memcpy(sel_out, sel.data(), pairs * sizeof(int));
+    if (w_out) std::memcpy(w_out, w.data(), pairs * sizeof(float));
+    return es_hip_moe_ffn(m, N, kk.data(), sel.data(), w.data(), k, x, xstride, out, ostride, stream);
+}
+
 }  // extern "C"
 
 namespace {

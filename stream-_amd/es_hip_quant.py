@@ -232,6 +232,7 @@ class Lib:
             ("es_hip_moe_ffn", i, [vp, i, vp, vp, vp, i, vp, sz, vp, sz, vp]),
             ("es_hip_moe_plan_create", vp, [vp, i, vp, vp, vp, i, vp, sz, vp, sz]),
             ("es_hip_moe_plan_run", i, [vp, vp]), ("es_hip_moe_plan_destroy", None, [vp]),
+            ("es_hip_moe_ffn_logits", i, [vp, i, vp, sz, i, i, vp, sz, vp, sz, vp, vp, vp]),
             ("es_hip_step_time_ms", C.c_double, [vp, i, vp, i, i, i, vp]),
             ("es_hip_swiglu_dev", i, [vp, vp, vp, C.c_long, vp]),
             ("es_hip_act_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp]),
@@ -347,6 +348,14 @@ class Lib:
     # ---- MoE expert FFN ----
     def moe_ffn(self, args: "MoeArgs", x, xstride, out, ostride, stream=None):
         self._check(self._L.es_hip_moe_ffn(*args.c_args(), int(x), xstride, int(out), ostride, stream))
+
+    def moe_ffn_logits(self, args: "MoeArgs", N, logits, lstride, k, norm_topk, x, xstride, out, ostride, stream=None):
+        """the MoE layer from device logits (es_hip_moe_ffn_logits); args' routing arrays are ignored. -> (sel, w) [N, k]"""
+        sel = np.zeros((N, k), np.int32)
+        w = np.zeros((N, k), np.float32)
+        self._check(self._L.es_hip_moe_ffn_logits(C.byref(args.m), N, int(logits), lstride, k, int(norm_topk), int(x), xstride,
+                                                  int(out), ostride, sel.ctypes.data, w.ctypes.data, stream))
+        return sel, w
 
     def moe_plan(self, args: "MoeArgs", x, xstride, out, ostride) -> "Plan":
         h = self._L.es_hip_moe_plan_create(*args.c_args(), int(x), xstride, int(out), ostride)

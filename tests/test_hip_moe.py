@@ -150,3 +150,23 @@ def test_moe_rejects_bad_routing(hip, orc):
         sel = np.array(sel, np.int32)
         with pytest.raises(E.EsHipError):
             hip.moe_ffn(ex.args(np.array(k), sel, np.ones(sel.shape, np.float32)), dx, 0, dout, n)
+
+
+@pytest.mark.parametrize("types,n_exp,N,k,norm", [((E.Q2_K, E.Q2_K, E.Q2_K), 64, 40, 8, False),
+                                                  ((E.Q4_K, E.Q4_K, E.Q6_K), 128, 32, 8, True)])
+def test_moe_from_device_logits(hipo, orc, types, n_exp, N, k, norm):
+    """es_hip_moe_ffn_logits: routing on the device from the router's logits, then the expert FFN; the routing equals the
+    oracle's route() and the outputs its moe_n restatement, bit for bit"""
+    n, ff = 2048, 768 if types[0] == E.Q4_K else 1024
+    ex = Experts(hipo, orc, types, n_exp, n, ff, 60 + n_exp)
+    logits = orc.gauss(1300 + N, 1.0, N * n_exp).reshape(N, n_exp)
+    want_sel, want_w = routed(orc, N, n_exp, k, norm, 1300 + N)
+    x = orc.quantize_act(types[0], orc.gauss(17, 1.0, N * n).reshape(N, n))
+    dl, dx = hipo.upload(logits), hipo.upload(x)
+    dout = hipo.upload(np.full((N, n), -777.0, np.float32))
+    args = ex.args(np.zeros(1, np.int32), np.zeros((1, k), np.int32), np.zeros((1, k), np.float32))
+    sel, w = hipo.moe_ffn_logits(args, N, dl, 0, k, norm, dx, x.strides[0], dout, n)
+    assert np.array_equal(sel, want_sel) and np.array_equal(bits(w), bits(want_w))
+    out = hipo.download(dout, np.zeros((N, n), np.float32))
+    ref = orc.moe_ffn(types, ex.host, n, ff, x, want_sel, want_w)
+    assert np.array_equal(bits(out), bits(ref))
