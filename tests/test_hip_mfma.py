@@ -1,5 +1,5 @@
 """GPU parity of the batched (matrix-core) Q4_K path: bit-identical to the oracle, and to the vector kernels, in every
-reference order, at the BASELINE prefill shapes and at ragged edges (rows not a multiple of the 64-row tile, activation
+reference order, at config 2's prefill shapes and at ragged edges (rows not a multiple of the 64-row tile, activation
 counts not a multiple of the 128-activation tile, row sub-ranges, padded strides)."""
 import numpy as np
 import pytest
@@ -63,7 +63,7 @@ def test_mfma_vs_oracle(hipm, orc, rows, cols, na, gauss, mode):
 
 @pytest.mark.parametrize("rows,cols,na", [(8192, 2048, 512), (2048, 8192, 512), (1000, 1024, 200)])
 def test_mfma_equals_vector_path(hipm, orc, rows, cols, na):
-    """the full BASELINE prefill shape (T=512): matrix-core result == vector-kernel result, bit for bit"""
+    """config 2's full prefill shape (T=512): matrix-core result == vector-kernel result, bit for bit"""
     W, acts = inputs(orc, rows, cols, na, 7 * rows + na)
     y_mm = hipm.matvec_multi(O.Q4_K, W, cols, rows, acts)
     y_mv = vector_path(hipm, lambda: hipm.matvec_multi(O.Q4_K, W, cols, rows, acts))

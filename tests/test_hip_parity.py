@@ -79,7 +79,7 @@ def mtest_inputs(orc, t, rows, cols, na, seed):
     return W, orc.quantize_act(t, x)
 
 
-# BASELINE.json shapes (rows x cols), at token counts the oracle finishes in seconds
+# the benchmark configurations' shapes (rows x cols), at token counts the oracle finishes in seconds
 SHAPES = [
     ("Q4_0", 4864, 896, 1),     # config 1
     ("Q4_K", 8192, 2048, 3),    # config 2 gate/up

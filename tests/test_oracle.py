@@ -233,7 +233,7 @@ def test_cpu_bench_harness_runs(orc):
 
 @pytest.mark.skipif(not O.ref_available("clang"), reason="reference not built here (no /root/reference)")
 def test_live_reference_wide_shapes(orc):
-    """the live reference build on the BASELINE shapes' column counts, many rows, contract and strict orders"""
+    """the live reference build on the benchmark configurations' column counts, many rows, contract and strict orders"""
     for F, cols in (("Q4_0", 896), ("Q5_0", 2048), ("Q4_K", 2048), ("Q4_K", 8192), ("Q6_K", 1024), ("Q2_K", 2048),
                     ("Q6_K", 768)):
         t = O.TYPES[F]
