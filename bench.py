@@ -260,14 +260,22 @@ class HipEvents:
         return ms.value / iters
 
 
-def cache_load_rate(lib, rng, K, Wm):
+def cache_load_rate(lib, rng, K, Wm, pinned=False):
     """Expert loads through the device expert cache (es_hip_cache_acquire) at config 5's expert size: gate/up Q4_K 768x2048
     and down Q6_K 2048x768 (3,059,712 bytes), from pageable host slabs of 64 experts, 16 slots. Every call takes 8 experts
     that are not cached (the cycle through 64 experts with 16 slots always misses), so each call copies 8 experts host ->
-    HBM and evicts 8; timed to the end of the copies. Host-to-device bound (PCIe), not an HBM figure."""
+    HBM and evicts 8, and waits for its copies as load_experts does. Host-to-device bound (PCIe), not an HBM figure.
+    pinned: the slabs in page-locked memory (es_hip_host_alloc), else pageable numpy arrays."""
     ne, nslots, k = 64, 16, 8
     parts = [768 * 8 * 144, 768 * 8 * 144, 2048 * 3 * 210]
     slabs = [rng.integers(0, 256, (ne, b), dtype=np.uint8) for b in parts]
+    if pinned:   # the same bytes in page-locked memory (es_hip_host_alloc)
+        pinned_slabs = []
+        for s in slabs:
+            h = lib.host_array(s.shape, np.uint8)
+            h[...] = s
+            pinned_slabs.append(h)
+        slabs = pinned_slabs
     src = E.ExpertSrc()
     off = 0
     for r in range(3):
@@ -275,12 +283,17 @@ def cache_load_rate(lib, rng, K, Wm):
         off += parts[r]
     c = E.ExpertCache(lib, nslots, off, 1, ne, 1.0)
     calls = [np.arange(k * i, k * i + k) % ne for i in range(Wm + K)]
+
+    def step(sel):   # load_experts: the experts of the call, then a wait for their copies (gio_wait)
+        for s in c.acquire(0, sel, src):
+            c.wait(int(s))
+
     for sel in calls[:Wm]:
-        c.acquire(0, sel, src)
+        step(sel)
     lib.synchronize()
     t0 = time.perf_counter()
     for sel in calls[Wm:]:
-        c.acquire(0, sel, src)
+        step(sel)
     lib.synchronize()
     dt = (time.perf_counter() - t0) / K
     st = c.stats()
@@ -332,7 +345,8 @@ def only(lib, rng, name, K, Wm):
     if name == "act":
         return {"workload": "act", **act_prep_times(lib, rng, K, Wm)}
     if name == "cache":
-        return {"workload": "cache", **cache_load_rate(lib, rng, K, Wm)}
+        return {"workload": "cache", "pageable": cache_load_rate(lib, rng, K, Wm),
+                "pinned": cache_load_rate(lib, rng, K, Wm, pinned=True)}
     if name in ("config4", "config5"):
         w = (MoeWorkload(lib, rng, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8) if name == "config4" else
              MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
@@ -429,6 +443,7 @@ def main():
     # ---- device activation preparation at config 2's prefill shapes (rmsnorm / SwiGLU fused with the quantizers)
     extra["act_prep_t512"] = act_prep_times(lib, rng, K, Wm)
     extra["expert_cache_load"] = cache_load_rate(lib, rng, K, Wm)
+    extra["expert_cache_load_pinned"] = cache_load_rate(lib, rng, K, Wm, pinned=True)
 
     cpu = None
     if not args.no_cpu:

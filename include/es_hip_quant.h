@@ -82,6 +82,10 @@ size_t es_hip_row_bytes(uint32_t type, int cols);
 /* ---- device memory helpers (plumbing for callers without their own HIP allocator) ---------------------------------- */
 void *es_hip_malloc(size_t bytes);                            /* NULL on failure */
 int   es_hip_free(void *dev);
+/* page-locked host memory (hipHostMalloc): expert slabs staged here load into the expert cache asynchronously at the
+ * link's full rate; pageable sources are staged by the runtime */
+void *es_hip_host_alloc(size_t bytes);                        /* NULL on failure */
+int   es_hip_host_free(void *host);
 int   es_hip_memcpy_h2d(void *dev, const void *host, size_t bytes);
 int   es_hip_memcpy_d2h(void *host, const void *dev, size_t bytes);
 int   es_hip_memcpy_d2d(void *dst, const void *src, size_t bytes);
@@ -254,7 +258,9 @@ double es_hip_step_time_ms(es_hip_plan *const *plans, int np, es_hip_moe_plan *c
  * keyed by (layer, expert); a claim takes the first empty slot, else evicts the lowest last_use + freq_weight * min(uses,
  * 16) among slots not loading and not protected (protect_until >= step), the first of equal scores. Loads are
  * hipMemcpyAsync copies on the caller's stream; a slot stays LOADING until its copy has finished (a HIP event), and a
- * loading slot is never evicted. slot_bytes = 0 creates a bookkeeping-only cache (no device memory, no GPU needed). One
+ * loading slot is never evicted: like load_experts, which waits for its reads before it returns, wait for a call's slots
+ * (es_hip_cache_wait, or a stream synchronisation) before claims that may need them, or a cache of in-flight copies
+ * answers ES_HIP_EBUSY. slot_bytes = 0 creates a bookkeeping-only cache (no device memory, no GPU needed). One
  * cache is used from one host thread. */
 typedef struct es_hip_cache es_hip_cache;
 enum { ES_HIP_SLOT_EMPTY = 0, ES_HIP_SLOT_LOADING = 1, ES_HIP_SLOT_READY = 2 };   /* ES_SLOT_*, src/es_cache.h:19 */

@@ -673,6 +673,18 @@ int es_hip_free(void *dev) {
     hipError_t e = hipFree(dev);
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipFree");
 }
+void *es_hip_host_alloc(size_t bytes) {
+    if (need_device()) return nullptr;
+    void *p = nullptr;
+    hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
+    if (e != hipSuccess) { hip_fail(e, "hipHostMalloc"); return nullptr; }
+    return p;
+}
+int es_hip_host_free(void *host) {
+    if (!host) return ES_HIP_OK;
+    hipError_t e = hipHostFree(host);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipHostFree");
+}
 int es_hip_memcpy_h2d(void *dev, const void *host, size_t bytes) {
     if (int rc = need_device()) return rc;
     hipError_t e = hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice);

@@ -9,6 +9,8 @@ from __future__ import annotations
 import ctypes as C
 import os
 
+import weakref
+
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -214,6 +216,7 @@ class Lib:
             ("es_hip_set_order", i, [i]), ("es_hip_get_order", i, []),
             ("es_hip_quant_supported", i, [u32]), ("es_hip_row_bytes", sz, [u32, i]),
             ("es_hip_malloc", vp, [sz]), ("es_hip_free", i, [vp]),
+            ("es_hip_host_alloc", vp, [sz]), ("es_hip_host_free", i, [vp]),
             ("es_hip_memcpy_h2d", i, [vp, vp, sz]), ("es_hip_memcpy_d2h", i, [vp, vp, sz]),
             ("es_hip_memcpy_d2d", i, [vp, vp, sz]), ("es_hip_memset", i, [vp, i, sz]), ("es_hip_synchronize", i, []),
             ("es_hip_matvec_dev", i, [u32, vp, i, i, i, vp, vp, vp]),
@@ -292,6 +295,18 @@ class Lib:
         return rc
 
     # ---- memory ----
+    def host_array(self, shape, dtype) -> np.ndarray:
+        """a numpy array over page-locked host memory (es_hip_host_alloc), freed when the array is collected"""
+        dtype = np.dtype(dtype)
+        n = int(np.prod(shape)) * dtype.itemsize
+        p = self._L.es_hip_host_alloc(n)
+        if not p:
+            raise EsHipError(-4, self.last_error())
+        buf = (C.c_uint8 * max(n, 1)).from_address(p)
+        arr = np.frombuffer(buf, np.uint8, count=n).view(dtype).reshape(shape)
+        weakref.finalize(arr, self._L.es_hip_host_free, p)
+        return arr
+
     def alloc(self, nbytes: int) -> DevBuf:
         return DevBuf(self, nbytes)
 

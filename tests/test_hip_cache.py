@@ -146,3 +146,22 @@ def test_load_bounds(hip):
         assert c.slot_ptr(1) - c.slot_ptr(0) == 1024   # slots 256-byte aligned
     finally:
         c.close()
+
+
+def test_pinned_host_slabs(hip, orc):
+    """expert slabs in page-locked memory (es_hip_host_alloc) load like pageable ones"""
+    nl, ne = 1, 4
+    slabs = make_slabs(orc, nl, ne, 41)
+    pinned = []
+    for part in slabs[0]:
+        h = hip.host_array(part.shape, np.uint8)
+        h[...] = part
+        pinned.append(h)
+    c = E.ExpertCache(hip, 2, sum(part_bytes()), nl, ne, 0.0)
+    try:
+        slots = c.acquire(0, [3, 1], src_of(pinned))
+        hip.synchronize()
+        check_resident(hip, c, [pinned], 2)
+        assert [c.slot_info(int(s)).expert for s in slots] == [3, 1]
+    finally:
+        c.close()
