@@ -136,6 +136,13 @@ int es_hip_unregister(const void *host);
 void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch);
 void es_hip_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
                          size_t ystride, float *scratch);
+/* es_q2k.h's Q2_K drop-ins (src/es_q2k.h:78-86): es_matvec_q2_K over host rows of es_block_q2_K and one activation's
+ * Q8_K blocks (xq, cols / 256 of them), y[r] for r in [r0, r1), in the reference's portable order (sumf += dall * isum -
+ * dmin * summs per block, no fusion) whatever es_hip_set_order says, as es_matvec_q2_K computes on every build; the
+ * kernel name, and a scalar switch kept for A/B scripts (the reference's scalar and portable dots give the same floats). */
+void        es_hip_matvec_q2_K(const void *W, int cols, int r0, int r1, const void *xq, float *y);
+const char *es_hip_q2k_kernel_name(void);
+void        es_hip_q2k_force_scalar(int on);
 /* The engine's queued job on host memory: mv_job (src/es_engine.c:144) field for field. */
 typedef struct {
     uint32_t type;

@@ -616,7 +616,7 @@ void *reg_lookup(const void *h, size_t n) {
 
 // Plan, upload the job tables (and bind the pre-pass workspace) in scratch, launch, wait: the synchronous path shared by
 // run_jobs, run_jobs_host and the host drop-ins. The caller holds g_call_mu.
-int run_sync(const std::vector<Req> &reqs, hipStream_t s) {
+int run_sync(const std::vector<Req> &reqs, hipStream_t s, int order = -1) {   // order -1: es_hip_set_order's
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
     if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty()) return ES_HIP_OK;
@@ -629,7 +629,7 @@ int run_sync(const std::vector<Req> &reqs, hipStream_t s) {
     const std::vector<uint8_t> img = table_image(bt);
     if (!img.empty() && (e = hipMemcpyAsync(dev, img.data(), img.size(), hipMemcpyHostToDevice, s)) != hipSuccess)
         return hip_fail(e, "job table upload");
-    if (int rc = launch_batch(bt, static_cast<const uint8_t *>(dev), g_order.load(), s)) return rc;
+    if (int rc = launch_batch(bt, static_cast<const uint8_t *>(dev), order >= 0 ? order : g_order.load(), s)) return rc;
     e = hipStreamSynchronize(s);   // like the reference's run_jobs: every product is done on return
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipStreamSynchronize");
 }
@@ -888,7 +888,7 @@ int es_hip_unregister(const void *host) {
 }
 
 static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
-                      size_t ystride) {
+                      size_t ystride, int order = -1) {
     g_err.clear();   // the void drop-ins report failure only through es_hip_last_error()
     if (int rc = need_device()) return rc;
     FmtInfo f;
@@ -922,7 +922,7 @@ static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, co
     if ((e = hipMemcpy(at, pack.data(), pack.size(), hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
     if (int rc = g_ytmp.get(sizeof(float) * n * na, &yt)) return rc;
     std::vector<Req> reqs{{type, dW, at, static_cast<float *>(yt), nullptr, nullptr, 0, n, cols, na, ab, (size_t)n}};
-    if (int rc = run_sync(reqs, nullptr)) return rc;
+    if (int rc = run_sync(reqs, nullptr, order)) return rc;
     std::vector<float> out((size_t)n * na);
     if ((e = hipMemcpy(out.data(), yt, out.size() * sizeof(float), hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
     for (int q = 0; q < na; q++) memcpy(y + ystride * q + r0, out.data() + (size_t)n * q, sizeof(float) * n);
@@ -1010,6 +1010,19 @@ void es_hip_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1,
     (void)scratch;
     host_multi(type, W, cols, r0, r1, a, na, y, ystride);
 }
+
+// es_matvec_q2_K (src/es_q2k.c:223-229) runs the portable dot (or, forced, es_dot_q2_K_q8_K_ref: the same float order,
+// src/es_q2k.c:127-148, 160-190) in every build: per block sumf += dall * isum - dmin * summs, nothing fused
+static std::atomic<int> g_q2k_scalar{0};
+
+void es_hip_matvec_q2_K(const void *W, int cols, int r0, int r1, const void *xq, float *y) {
+    es_hip_act a{nullptr, static_cast<es_hip_block_q8_K *>(const_cast<void *>(xq)), nullptr, cols};
+    host_multi(ES_HIP_Q2_K, W, cols, r0, r1, &a, 1, y, 0, ES_HIP_ORDER_X86_STRICT);
+}
+
+const char *es_hip_q2k_kernel_name(void) { return g_q2k_scalar.load() ? "hip-gfx950 (scalar order)" : "hip-gfx950"; }
+
+void es_hip_q2k_force_scalar(int on) { g_q2k_scalar.store(on ? 1 : 0); }
 
 }  // extern "C"
 

@@ -217,6 +217,8 @@ class Lib:
             ("es_hip_quant_supported", i, [u32]), ("es_hip_row_bytes", sz, [u32, i]),
             ("es_hip_malloc", vp, [sz]), ("es_hip_free", i, [vp]),
             ("es_hip_host_alloc", vp, [sz]), ("es_hip_host_free", i, [vp]),
+            ("es_hip_matvec_q2_K", None, [vp, i, i, i, vp, vp]), ("es_hip_q2k_kernel_name", C.c_char_p, []),
+            ("es_hip_q2k_force_scalar", None, [i]),
             ("es_hip_memcpy_h2d", i, [vp, vp, sz]), ("es_hip_memcpy_d2h", i, [vp, vp, sz]),
             ("es_hip_memcpy_d2d", i, [vp, vp, sz]), ("es_hip_memset", i, [vp, i, sz]), ("es_hip_synchronize", i, []),
             ("es_hip_matvec_dev", i, [u32, vp, i, i, i, vp, vp, vp]),
@@ -295,6 +297,16 @@ class Lib:
         return rc
 
     # ---- memory ----
+    def matvec_q2_K(self, W: np.ndarray, cols: int, r0: int, r1: int, xq: np.ndarray, rows: int) -> np.ndarray:
+        """es_matvec_q2_K's drop-in on host arrays: y[rows] with rows [r0, r1) written (the rest stay zero)"""
+        y = np.zeros(rows, np.float32)
+        self._L.es_hip_matvec_q2_K(np.ascontiguousarray(W).ctypes.data, cols, r0, r1, np.ascontiguousarray(xq).ctypes.data,
+                                   y.ctypes.data)
+        err = self.last_error()
+        if err:
+            raise EsHipError(-3, err)
+        return y
+
     def host_array(self, shape, dtype) -> np.ndarray:
         """a numpy array over page-locked host memory (es_hip_host_alloc), freed when the array is collected"""
         dtype = np.dtype(dtype)

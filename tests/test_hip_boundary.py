@@ -77,3 +77,13 @@ def test_no_device_means_no_compute(hiplib):
     with pytest.raises(E.EsHipError):
         hiplib.host_matvec_multi(E.Q4_K, W, 256, 0, 1, acts, y)
     assert y[0, 0] == 7.0
+
+
+def test_q2k_kernel_name_and_switch(hiplib):
+    """es_q2k.h's kernel name and scalar switch (src/es_q2k.h:83-86), usable without a device"""
+    L = hiplib._L
+    assert L.es_hip_q2k_kernel_name() == b"hip-gfx950"
+    L.es_hip_q2k_force_scalar(1)
+    assert b"scalar" in L.es_hip_q2k_kernel_name()
+    L.es_hip_q2k_force_scalar(0)
+    assert L.es_hip_q2k_kernel_name() == b"hip-gfx950"

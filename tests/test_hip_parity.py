@@ -266,3 +266,21 @@ def test_run_jobs_host_is_the_engine_queue(hip, orc):
     assert np.array_equal(bits(gu[:, ff:]), bits(orc.matvec_multi(O.Q4_K, Wu, n, ff, acts)))
     assert np.array_equal(bits(yd), bits(orc.matvec_multi(O.Q6_K, Wh, ff, n, hacts)))
     hip.unregister(Wu)
+
+
+def test_matvec_q2_K_drop_in(hip, golden):
+    """es_matvec_q2_K's drop-in: the reference's own es_dot_q2_K_q8_K_ref values (kbench's correctness rows) and its scalar
+    build's outputs, bit for bit, under every es_hip_set_order setting (es_matvec_q2_K never takes the AVX2 path)"""
+    W, xq, want = golden["q2k/W"], golden["q2k/xq"], golden["q2k/dot_ref"]
+    cols, rows = golden["q2k/x"].size, want.size
+    try:
+        for order in (E.ORDER_X86_CONTRACT, E.ORDER_X86_STRICT, E.ORDER_SCALAR):
+            hip.set_order(order)
+            y = hip.matvec_q2_K(W, cols, 0, rows, xq, rows)
+            assert np.array_equal(bits(y), bits(want)), order
+            cols2, rows2 = (int(v) for v in golden["Q2_K/mtest_shape"])
+            acts = golden_acts(golden, "Q2_K", "mtest")
+            y2 = hip.matvec_q2_K(golden["Q2_K/mtest_W"], cols2, 3, rows2, acts[0], rows2)
+            assert np.array_equal(bits(y2[3:]), bits(golden["Q2_K/mtest_y_scalar"][0][3:])) and np.all(y2[:3] == 0)
+    finally:
+        hip.set_order(E.ORDER_X86_CONTRACT)
