@@ -242,6 +242,9 @@ int es_hip_rmsnorm_prepare_dev(const float *x, size_t xstride, const float *w, f
  * 913-914), h = g / (1 + expf(-g)) * u, fused with the preparation of h; h (optional) receives the values. */
 int es_hip_swiglu_prepare_dev(const float *gu, size_t gu_stride, int rows, int ff, float *h, size_t h_stride, void *q80,
                               size_t q80_stride, void *q8k, size_t q8k_stride, void *stream);
+/* es_dequant_row (src/es_quant.h:28, src/es_quant.c:425-476) on the device: n weights (a whole number of blocks, any byte
+ * alignment) of src to fp32 at dst, each by its format's formula in the reference's operation order (bit-identical). */
+int es_hip_dequant_row_dev(uint32_t type, const void *src, float *dst, long n, void *stream);
 /* route() for softmax gating on the device (src/es_engine.c:744-835, its GATE_SOFTMAX path: no gate bias, selection bias,
  * expert groups, cache bonus or top-k override): for each of ntok tokens, the softmax of its n_exp logits (expf(l - max),
  * summed in expert order, divided), the k largest probabilities by repeated argmax with ties to the lowest expert into

@@ -130,6 +130,7 @@ hipError_t swiglu_plain_launch(const float *g, const float *u, float *h, long n,
 // route() with softmax gating for ntok tokens of ne <= ROUTE_MAX_EXPERTS logits (rows ls floats apart): sel / w rows of
 // kmax, the first k filled (k <= 64).
 constexpr int ROUTE_MAX_EXPERTS = 1024;
+hipError_t dequant_launch(uint32_t type, const void *src, float *dst, long n, hipStream_t s);
 hipError_t route_softmax_launch(const float *logits, uint64_t ls, int ntok, int ne, int k, int norm_topk, int *sel, float *w,
                                 int kmax, hipStream_t s);
 

@@ -1353,6 +1353,18 @@ int es_hip_swiglu_prepare_dev(const float *gu, size_t gu_stride, int rows, int f
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "SwiGLU preparation launch");
 }
 
+int es_hip_dequant_row_dev(uint32_t type, const void *src, float *dst, long n, void *stream) {
+    if (int rc = need_device()) return rc;
+    FmtInfo f;
+    if (!fmt_info(type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", type);
+    if (n < 0 || n % f.be) return fail(ES_HIP_EINVAL, "n = %ld is not a whole number of %d-element blocks", n, f.be);
+    if (n == 0) return ES_HIP_OK;
+    if (!src || !dst) return fail(ES_HIP_EINVAL, "null source or output");
+    if (reinterpret_cast<uintptr_t>(dst) & 3) return fail(ES_HIP_EINVAL, "dst must be 4-byte aligned");
+    hipError_t e = esq::dequant_launch(type, src, dst, n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "dequant launch");
+}
+
 int es_hip_route_softmax_dev(const float *logits, size_t lstride, int ntok, int n_exp, int k, int norm_topk, int *sel, float *w,
                              int kmax, void *stream) {
     if (int rc = need_device()) return rc;

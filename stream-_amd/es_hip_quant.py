@@ -242,6 +242,7 @@ class Lib:
             ("es_hip_swiglu_dev", i, [vp, vp, vp, C.c_long, vp]),
             ("es_hip_act_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp]),
             ("es_hip_route_softmax_dev", i, [vp, sz, i, i, i, i, vp, vp, i, vp]),
+            ("es_hip_dequant_row_dev", i, [u32, vp, vp, C.c_long, vp]),
             ("es_hip_rmsnorm_prepare_dev", i, [vp, sz, vp, C.c_float, i, i, vp, sz, vp, sz, vp, sz, vp]),
             ("es_hip_swiglu_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp, sz, vp]),
             ("es_hip_cache_create", i, [vp, i, sz, i, i, C.c_double]), ("es_hip_cache_destroy", None, [vp]),
@@ -401,6 +402,9 @@ class Lib:
 
     def swiglu_dev(self, g, u, h, n, stream=None):
         self._check(self._L.es_hip_swiglu_dev(int(g), int(u), int(h), n, stream))
+
+    def dequant_row_dev(self, t, src, dst, n, stream=None):
+        self._check(self._L.es_hip_dequant_row_dev(t, int(src), int(dst), n, stream))
 
     def route_softmax_dev(self, logits, lstride, ntok, n_exp, k, norm_topk, sel, w, kmax, stream=None):
         self._check(self._L.es_hip_route_softmax_dev(int(logits), lstride, ntok, n_exp, k, int(norm_topk), int(sel), int(w),
