@@ -336,6 +336,44 @@ def make_cache_trace(seed, nlayers, nexperts, k, tokens, passes, prefetch="top")
     return np.array(ops, np.int32)
 
 
+class RefEngine:
+    """the reference engine's own route() and rmsnorm() (src/es_engine.c:744-835, 189-194), compiled from its source by
+    oracle/Makefile into oracle/_ref/libesref_engine_{clang,gcc}.so through esq_engine_ref.c"""
+
+    def __init__(self, cc: str = "clang"):
+        path = os.path.join(HERE, "_ref", f"libesref_engine_{cc}.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle ref` where /root/reference exists")
+        self.lib = C.CDLL(path)
+        self.lib.esref_route.restype = C.c_int
+        self.lib.esref_route.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        self.lib.esref_rmsnorm.restype = None
+        self.lib.esref_rmsnorm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_float]
+
+    def route(self, logits: np.ndarray, k: int, norm_topk: bool):
+        """softmax gating over rows of logits -> (sel [n_tok, k] int32, w [n_tok, k] fp32)"""
+        lg = np.ascontiguousarray(logits, np.float32)
+        n_tok, ne = lg.shape
+        sel = np.zeros((n_tok, k), np.int32)
+        w = np.zeros((n_tok, k), np.float32)
+        got = self.lib.esref_route(n_tok, ne, k, int(norm_topk), _p(lg), _p(sel), _p(w))
+        if got != k:
+            raise RuntimeError(f"reference route() returned k={got}, expected {k}")
+        return sel, w
+
+    def rmsnorm(self, x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        x2 = x.reshape(-1, x.shape[-1])
+        o = np.zeros_like(x2)
+        wp = None if w is None else np.ascontiguousarray(w, np.float32)
+        self.lib.esref_rmsnorm(_p(o), _p(x2), None if wp is None else _p(wp), x2.shape[0], x2.shape[1], eps)
+        return o.reshape(x.shape)
+
+
+def ref_engine_available(cc: str = "clang") -> bool:
+    return os.path.exists(os.path.join(HERE, "_ref", f"libesref_engine_{cc}.so"))
+
+
 class RefCache:
     """the reference's es_cache.c driven by esq_cache_ref.c (oracle/_ref/libesref_cache.so)"""
 

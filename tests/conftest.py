@@ -10,6 +10,7 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, os.path.join(ROOT, "stream-_amd"))
 
 GOLDEN = os.path.join(ROOT, "tests", "golden", "ref_vectors.npz")
+ENGINE_GOLDEN = os.path.join(ROOT, "tests", "golden", "engine_vectors.npz")
 
 
 def pytest_configure(config):
@@ -34,6 +35,18 @@ def orc():
 def golden():
     with np.load(GOLDEN, allow_pickle=False) as z:
         return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope="session")
+def engine_golden():
+    """route() / rmsnorm() inputs and outputs of the reference engine built from its source (make_engine_golden.py)"""
+    with np.load(ENGINE_GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def golden_cases(g, prefix):
+    """case names under prefix/ in a golden dict"""
+    return sorted({k.split("/")[1] for k in g if k.startswith(prefix + "/")})
 
 
 @pytest.fixture(scope="session")

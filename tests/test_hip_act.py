@@ -129,3 +129,18 @@ def test_act_prepare_rejects_bad_arguments(hip):
         hip.rmsnorm_prepare_dev(dx, 0, None, 1e-5, 1, 16640, None, 0, d, 0, None, 0)   # above the LDS-staged row length
     with pytest.raises(E.EsHipError):
         hip.rmsnorm_prepare_dev(dx, 0, None, 1e-5, 1, 100, d, 0, None, 0, None, 0)      # not a multiple of 32
+
+
+def test_rmsnorm_matches_reference_engine_goldens(hip, engine_golden):
+    """device rmsnorm on the rows the reference engine's own rmsnorm() was run on (tests/golden/engine_vectors.npz):
+    bit-identical floats, weighted and unweighted, n = 896, 2048, 8192, tiny / huge / zero rows"""
+    from conftest import golden_cases
+    for c in golden_cases(engine_golden, "rms"):
+        x = engine_golden[f"rms/{c}/x"]
+        w = engine_golden.get(f"rms/{c}/w")
+        rows, cols = x.shape
+        dx, dxn = hip.upload(x), hip.alloc(x.nbytes)
+        dw = hip.upload(w) if w is not None else None
+        d80 = hip.alloc(rows * (cols // 32) * 36)
+        hip.rmsnorm_prepare_dev(dx, 0, dw, float(engine_golden[f"rms/{c}/eps"][0]), rows, cols, dxn, 0, d80, 0, None, 0)
+        assert np.array_equal(bits(hip.download(dxn, np.zeros_like(x))), bits(engine_golden[f"rms/{c}/o"])), c

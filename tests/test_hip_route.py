@@ -53,3 +53,15 @@ def test_route_rejects_bad_shapes(hip):
         hip.route_softmax_dev(d, 0, 2, 2048, 8, True, d, d, 8)   # more experts than the kernel stages
     with pytest.raises(E.EsHipError):
         hip.route_softmax_dev(d, 0, 2, 64, 8, True, d, d, 4)     # kmax < k
+
+
+def test_route_matches_reference_engine_goldens(hip, engine_golden):
+    """device route() on the logits the reference engine's own route() was run on (tests/golden/engine_vectors.npz):
+    the same experts and bit-identical weights, without the oracle in between"""
+    from conftest import golden_cases
+    for c in golden_cases(engine_golden, "route"):
+        g = lambda n: engine_golden[f"route/{c}/{n}"]
+        k, norm = (int(v) for v in g("params"))
+        sel, w = device_route(hip, g("logits"), k, bool(norm))
+        assert np.array_equal(sel, g("sel")), c
+        assert np.array_equal(bits(w), bits(g("w"))), c

@@ -296,3 +296,71 @@ def test_rmsnorm_closed_forms(orc):
     assert np.all(const == c * s)
     x = np.random.default_rng(3).standard_normal((2, n)).astype(np.float32)
     assert np.array_equal(_bits(orc.rmsnorm(x, None, eps)), _bits(orc.rmsnorm(x, np.ones(n, np.float32), eps)))
+
+
+# ---- engine glue pinned to the reference engine's own route() / rmsnorm() (tests/golden/engine_vectors.npz) ----------
+def test_route_matches_reference_engine_goldens(orc, engine_golden):
+    from conftest import golden_cases
+    cases = golden_cases(engine_golden, "route")
+    assert {"olmoe", "qwen3", "ties", "ties_norm", "underflow", "underflow_norm", "k1", "k32", "wide"} <= set(cases)
+    for c in cases:
+        g = lambda n: engine_golden[f"route/{c}/{n}"]
+        k, norm = (int(v) for v in g("params"))
+        sel, w, _ = orc.route_softmax(g("logits"), k, bool(norm))
+        assert np.array_equal(sel, g("sel")), c
+        assert np.array_equal(_bits(w), _bits(g("w"))), c
+
+
+def test_rmsnorm_matches_reference_engine_goldens(orc, engine_golden):
+    from conftest import golden_cases
+    cases = golden_cases(engine_golden, "rms")
+    assert {"n896", "n896_w", "n2048", "n2048_w", "n8192", "n8192_w", "tiny", "huge", "zero"} <= set(cases)
+    for c in cases:
+        w = engine_golden.get(f"rms/{c}/w")
+        o = orc.rmsnorm(engine_golden[f"rms/{c}/x"], w, float(engine_golden[f"rms/{c}/eps"][0]))
+        assert np.array_equal(_bits(o), _bits(engine_golden[f"rms/{c}/o"])), c
+
+
+def test_engine_goldens_catch_planted_mistakes(engine_golden):
+    """the goldens tell apart the plausible slips of a restatement: a float (not double) sum of squares, a dropped eps,
+    the weight applied before the scale, top-k by logits with ties to the highest index, renormalising without the clamp"""
+    x = engine_golden["rms/n2048_w/x"][0]
+    w = engine_golden["rms/n2048_w/w"]
+    eps = float(engine_golden["rms/n2048_w/eps"][0])
+    want = engine_golden["rms/n2048_w/o"][0]
+    ssf = np.float32(0)
+    for v in x:
+        ssf = np.float32(ssf + v * v)
+    s_f = np.float32(1.0 / np.sqrt(np.float64(ssf) / x.size + eps))
+    ss = float(np.cumsum(x.astype(np.float64) ** 2)[-1])
+    s = np.float32(1.0 / np.sqrt(ss / x.size + np.float64(np.float32(eps))))
+    s_noeps = np.float32(1.0 / np.sqrt(ss / x.size))
+    right = x * s * w
+    assert np.array_equal(_bits(right), _bits(want))
+    assert not np.array_equal(_bits(x * s_f * w), _bits(want))
+    assert not np.array_equal(_bits(x * s_noeps * w), _bits(want))
+    assert not np.array_equal(_bits(x * (s * w)), _bits(want))
+    t = engine_golden["route/ties/logits"]
+    sel = engine_golden["route/ties/sel"]
+    last_max = np.stack([np.argsort(-row[::-1], kind="stable")[:8] for row in t])
+    last_max = t.shape[1] - 1 - last_max
+    assert not np.array_equal(last_max, sel)
+
+
+@pytest.mark.skipif(not O.ref_engine_available("clang"), reason="reference engine not built here (no /root/reference)")
+def test_route_and_rmsnorm_live_reference_engine(orc):
+    """the live reference engine against the oracle on fresh inputs (shapes of configs 4 and 5, both compilers)"""
+    rng = np.random.default_rng(77)
+    for cc in ("clang", "gcc"):
+        R = O.RefEngine(cc)
+        for ntok, ne, k, norm in ((64, 64, 8, False), (16, 128, 8, True), (5, 300, 32, True), (8, 64, 1, True)):
+            lg = rng.standard_normal((ntok, ne)).astype(np.float32)
+            lg[0, ::5] = 2.0
+            sel, w = R.route(lg, k, norm)
+            osel, ow, _ = orc.route_softmax(lg, k, norm)
+            assert np.array_equal(sel, osel) and np.array_equal(_bits(w), _bits(ow)), (cc, ntok, ne, k, norm)
+        for n in (256, 1024, 4096):
+            x = rng.standard_normal((2, n)).astype(np.float32) * 5
+            wv = rng.random(n).astype(np.float32)
+            for ww in (None, wv):
+                assert np.array_equal(_bits(R.rmsnorm(x, ww, 1e-5)), _bits(orc.rmsnorm(x, ww, 1e-5))), (cc, n)
