@@ -226,6 +226,14 @@ int es_hip_set_q6k_mfma_min_batch(int n);
 /* Q2_K products with at least n activations run on the Q2_K LDS-staged matrix-core kernel (default 2); below that, or
  * with it off, the small-batch kernel (es_hip_set_small_batch_min) or the vector kernel. */
 int es_hip_set_q2k_mfma_min_batch(int n);
+/* Q4_K products with at least n activations (default 32) and at least es_hip_set_direct_mfma_min_tiles tiles run on the
+ * direct-activation matrix-core kernel: it reads the activations' Q8_K rows itself (no pre-pass) in tiles of 64 rows x 128
+ * activations. Otherwise, or with it off (n <= 0), the pre-pass kernels of es_hip_set_mfma_min_batch /
+ * es_hip_set_small_batch_min or the vector kernel. Results are identical on every kernel. Returns the previous value. */
+int es_hip_set_direct_mfma_min_batch(int n);
+/* The direct-activation kernel's minimum tile count per product (default 128; twice that for rows longer than 4096):
+ * below it a product has too few workgroups to fill the device. Returns the previous value. */
+int es_hip_set_direct_mfma_min_tiles(int n);
 /* ---- activation preparation on the device ---------------------------------------------------------------------------
  * es_act_prepare (src/es_quant.c:499-512) for `rows` rows of `cols` fp32 values in device memory: q80 (when non-NULL;
  * cols % 32 == 0) receives cols/32 Q8_0 blocks per row exactly as quantize_q80 (src/es_quant.c:489-497) writes them, q8k

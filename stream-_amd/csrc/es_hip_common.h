@@ -80,6 +80,24 @@ struct MmJob {
     int r0, r1, cols, na, na_pad;
     int tile0, ntok_tiles;
 };
+// The batched form reading the activations' Q8_K rows directly (es_hip_mk.hip, no pre-pass): rows [r0, r1) against na
+// activations, activation q at act + (arow ? arow[q] : q) * astride. Workgroup tiles of MK_ROWS rows x MK_TOK
+// activations, numbered from tile0; ntok_tiles activation tiles per row tile. The activation rows of a product must lie
+// within 4 GiB of act (32-bit offsets; checked by the host).
+constexpr int MK_TOK = 128, MK_ROWS = 64;
+struct MkJob {
+    const uint8_t *W;     // row 0
+    const uint8_t *act;   // activation 0's first block
+    const int *arow;      // optional gather
+    float *y;
+    uint64_t astride, ystride, row_bytes;
+    int r0, r1, cols, na;
+    int tile0, ntok_tiles;
+};
+// gather: some job of the launch reads its activation rows through arow (a separate kernel build; the others need not)
+hipError_t mk_launch(int type, bool gather, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
+                     hipStream_t s);
+
 // One activation pre-pass: kind 0 writes 16 bytes of meta per activation and superblock (pair sums of the Q4_K
 // sub-blocks, low | high bytes), kind 1 32 bytes (the 16 bsums, low | high bytes), kind 2 32 bytes (the 16 bsums as
 // halves); xd follows the xm plane. Kind 3 takes Q8_0 rows (nbk blocks of 9 dwords: d, 32 int8) and writes, per tile of

@@ -125,6 +125,7 @@ struct Req {   // one product as the launch planner sees it
     int r0, r1, cols, na;
     size_t astride, ystride;
     const int *arow;   // optional device gather table: activation q is row arow[q] of act
+    int act_rows = 0;  // rows of act a gather may index (0: na)
 };
 
 int check_req(const Req &q, const FmtInfo &f) {
@@ -247,6 +248,8 @@ std::atomic<int> g_mb_min{2};    // activations per Q4_0/Q5_0 product from which
 std::atomic<int> g_mbm_min{2};   // ... and from which that batched kernel is the matrix-core one (<= 0: never)
 std::atomic<int> g_mm6_min{16};  // activations per Q6_K product from which its matrix-core kernel is used (<= 0: never)
 std::atomic<int> g_mm2_min{2};   // activations per Q2_K product from which its LDS-staged matrix-core kernel is used
+std::atomic<int> g_mk_min{32};   // activations per Q4_K product from which the direct-activation matrix-core kernel is used
+std::atomic<int> g_mk_min_tiles{128};   // ... and its 64 x 128 tiles per product from which it is (twice that for K > 4096)
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
@@ -276,8 +279,17 @@ struct MmGroup {   // one matrix-core launch: products of one format sharing a w
     size_t off = 0;   // byte offset of the job table in the device image
 };
 
+struct MkGroup {   // one direct-activation matrix-core launch: products of one format, gathered activations or not
+    int type;
+    bool gather;
+    int grid = 0;
+    std::vector<esq::MkJob> jobs;
+    size_t off = 0;
+};
+
 struct Batch {
     std::vector<Group> mv;
+    std::vector<MkGroup> mkg;
     std::vector<Prep> preps;
     std::vector<std::pair<int, esq::MmJob>> mm;   // (type, job); xq / xm hold workspace offsets until bind(); copied into mmg
     std::vector<MmGroup> mmg;
@@ -325,6 +337,28 @@ bool mm_eligible(const Req &q) {
     if (q.type == ES_HIP_Q6_K && (q.cols / 256) % 2) return false;   // rows must be 4-byte aligned
     return (q.type == ES_HIP_Q4_K || q.type == ES_HIP_Q6_K || q.type == ES_HIP_Q2_K) && mn > 0 && q.na >= mn && !q.ints &&
            q.r1 > q.r0;
+}
+
+// the direct-activation kernel: Q4_K batches of at least g_mk_min, every activation row within 4 GiB of act
+// the output stride the direct kernel uses: any stride >= r1 serves a single activation (only its row 0 is written)
+size_t mk_ystride(const Req &q) { return q.na > 1 ? q.ystride : std::max(q.ystride, (size_t)q.r1); }
+
+bool mk_eligible(const Req &q) {
+    const int mn = g_mk_min.load();
+    if (q.type != ES_HIP_Q4_K || mn <= 0 || q.na < mn || q.ints || q.r1 <= q.r0) return false;
+    const size_t rows = q.arow ? (size_t)std::max(q.act_rows, 0) : (size_t)q.na;
+    const size_t stride = q.astride ? q.astride : (size_t)(q.cols / 256) * 292;
+    // Tiles (64 rows x 128 activations, one workgroup each) against the K loop each runs: measured on config 2's shapes,
+    // this kernel wins from 128 tiles of 8 superblocks (8192 x 2048 at 128 activations: 17 us against 28 us) and loses
+    // with 128 tiles of 32 superblocks (2048 x 8192 at 512: 60 us against 45 us, a quarter of the chip's workgroup slots
+    // each running a long chain); from 256 tiles it wins or ties at every depth.
+    const int mt = g_mk_min_tiles.load();
+    const size_t tiles = (size_t)((q.r1 - q.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS) * ((q.na + esq::MK_TOK - 1) / esq::MK_TOK);
+    if (tiles < (size_t)mt || (tiles < 2 * (size_t)mt && q.cols > 16 * 256)) return false;
+    // 32-bit offsets: activation rows within 4 GiB of the activation pointer; outputs (with a tile of activations past
+    // the last) below 2^31 bytes, the range the kernel's buffer stores are checked against
+    return (!q.arow || q.act_rows > 0) && rows * stride < ((size_t)1 << 32) - 65536 &&
+           ((size_t)q.na + esq::MK_TOK) * mk_ystride(q) * sizeof(float) < ((size_t)1 << 31);
 }
 
 bool mb_eligible(const Req &q) {
@@ -403,6 +437,30 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             continue;
         }
         const int nbk = q.cols / 256;
+        if (mk_eligible(q)) {   // one launch per format; MK_ROWS x MK_TOK tiles, 8 consecutive ids per row tile group
+            MkGroup *g = nullptr;
+            for (MkGroup &x : bt.mkg)
+                if (x.type == (int)q.type && x.gather == (q.arow != nullptr)) g = &x;
+            if (!g) { bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr}); g = &bt.mkg.back(); }
+            esq::MkJob j{};
+            j.W = static_cast<const uint8_t *>(q.W);
+            j.act = static_cast<const uint8_t *>(q.act);
+            j.arow = q.arow;
+            j.y = q.y;
+            j.astride = q.astride ? q.astride : (uint64_t)nbk * f.ab;
+            j.ystride = mk_ystride(q);
+            j.row_bytes = (uint64_t)nbk * f.bb;
+            j.r0 = q.r0;
+            j.r1 = q.r1;
+            j.cols = q.cols;
+            j.na = q.na;
+            j.tile0 = g->grid;
+            j.ntok_tiles = (q.na + esq::MK_TOK - 1) / esq::MK_TOK;
+            const int row_tiles = (q.r1 - q.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS;
+            g->grid += 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
+            g->jobs.push_back(j);
+            continue;
+        }
         if (!mm_eligible(q)) {
             if (!mq_eligible(q)) { mv.push_back(q); continue; }
             // small batch: activation groups of at most 64, one launch per (format, 16-wide tiles per group)
@@ -478,6 +536,10 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         g.off = off;
         off += align256(g.jobs.size() * sizeof(esq::MmJob));
     }
+    for (MkGroup &g : bt.mkg) {
+        g.off = off;
+        off += align256(g.jobs.size() * sizeof(esq::MkJob));
+    }
     for (MqGroup &g : bt.mqg) {
         g.off = off;
         off += align256(g.jobs.size() * sizeof(esq::MqJob));
@@ -528,6 +590,7 @@ std::vector<uint8_t> table_image(const Batch &bt) {
     for (size_t i = 0; i < bt.mv.size(); i++)
         memcpy(img.data() + bt.mv_off[i], bt.mv[i].jobs.data(), bt.mv[i].jobs.size() * sizeof(MvJob));
     for (const MmGroup &g : bt.mmg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MmJob));
+    for (const MkGroup &g : bt.mkg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MkJob));
     for (const MqGroup &g : bt.mqg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MqJob));
     for (const MbGroup &g : bt.mbg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MbJob));
     if (!bt.pj.empty()) memcpy(img.data() + bt.prep_off, bt.pj.data(), bt.pj.size() * sizeof(esq::PrepJob));
@@ -557,6 +620,11 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
     for (const MmGroup &g : bt.mmg) {
         const esq::MmJob *dj = tables ? reinterpret_cast<const esq::MmJob *>(tables + g.off) : nullptr;
         if ((e = esq::mm_launch(g.type, g.bm, g.bn, g.nw, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+            return hip_fail(e, "matrix-core launch");
+    }
+    for (const MkGroup &g : bt.mkg) {
+        const esq::MkJob *dj = tables ? reinterpret_cast<const esq::MkJob *>(tables + g.off) : nullptr;
+        if ((e = esq::mk_launch(g.type, g.gather, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
             return hip_fail(e, "matrix-core launch");
     }
     for (const MbGroup &g : bt.mbg) {
@@ -619,7 +687,7 @@ void *reg_lookup(const void *h, size_t n) {
 int run_sync(const std::vector<Req> &reqs, hipStream_t s, int order = -1) {   // order -1: es_hip_set_order's
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
-    if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty()) return ES_HIP_OK;
+    if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty()) return ES_HIP_OK;
     hipError_t e = hipStreamSynchronize(s);   // the scratch may still be read by an earlier call's kernels
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     void *dev = nullptr;
@@ -719,7 +787,8 @@ int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int 
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty()) return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
+    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty())
+        return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
     // other kernels (possibly several jobs per launch, pre-passes): a stream-ordered allocation for the job tables and the
     // pre-pass workspace. The tables are copied from pageable memory, which the copy has consumed when it returns.
     void *dev = nullptr;
@@ -834,6 +903,8 @@ int es_hip_set_batched32_min(int n) { return g_mb_min.exchange(n); }
 int es_hip_set_batched32_mfma_min(int n) { return g_mbm_min.exchange(n); }
 int es_hip_set_q6k_mfma_min_batch(int n) { return g_mm6_min.exchange(n); }
 int es_hip_set_q2k_mfma_min_batch(int n) { return g_mm2_min.exchange(n); }
+int es_hip_set_direct_mfma_min_batch(int n) { return g_mk_min.exchange(n); }
+int es_hip_set_direct_mfma_min_tiles(int n) { return g_mk_min_tiles.exchange(n); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
@@ -1140,8 +1211,8 @@ int moe_build(es_hip_moe_plan *p, const es_hip_moe *m, int N, const int *k, cons
     for (size_t u = 0; u < uex.size(); u++) {
         const int ex = uex[u], s0 = start[u], c = cnt[u];
         float *y = p->bgu + (size_t)s0 * 2 * ff;
-        gu.push_back({m->gate_type, m->gate[ex], x, y, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0});
-        gu.push_back({m->up_type, m->up[ex], x, y + ff, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0});
+        gu.push_back({m->gate_type, m->gate[ex], x, y, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0, N});
+        gu.push_back({m->up_type, m->up[ex], x, y + ff, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0, N});
         dn.push_back({m->down_type, m->down[ex], p->ha + (size_t)s0 * p->hstride, p->bye + (size_t)s0 * n, nullptr, nullptr, 0, n,
                       ff, c, p->hstride, (size_t)n, nullptr});
     }

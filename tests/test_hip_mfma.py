@@ -30,23 +30,27 @@ def inputs(orc, rows, cols, na, seed, gauss=False):
 
 @pytest.fixture(params=[8, 32], ids=["lds", "regs"])
 def hipm(hip, request):
-    """Q4_K batches of 8..31 on the LDS-staged kernel (threshold 8) or on the register-streaming one (threshold 32)"""
+    """Q4_K batches of 8..31 on the LDS-staged kernel (threshold 8) or on the register-streaming one (threshold 32); the
+    direct-activation kernel (tests/test_hip_direct.py) switched off"""
     prev = hip.set_mfma_min_batch(request.param)
     prev_s = hip.set_small_batch_min(8)
+    prev_d = hip.set_direct_mfma_min_batch(0)
     yield hip
     hip.set_mfma_min_batch(prev)
     hip.set_small_batch_min(prev_s)
+    hip.set_direct_mfma_min_batch(prev_d)
     hip.set_order(E.ORDER_X86_CONTRACT)
 
 
 def vector_path(hip, fn):
-    """fn() with both matrix-core kernels switched off"""
-    a, b = hip.set_mfma_min_batch(0), hip.set_small_batch_min(0)
+    """fn() with every Q4_K matrix-core kernel switched off"""
+    a, b, c = hip.set_mfma_min_batch(0), hip.set_small_batch_min(0), hip.set_direct_mfma_min_batch(0)
     try:
         return fn()
     finally:
         hip.set_mfma_min_batch(a)
         hip.set_small_batch_min(b)
+        hip.set_direct_mfma_min_batch(c)
 
 
 @pytest.mark.parametrize("rows,cols,na,gauss", [(8192, 2048, 40, True), (2048, 8192, 33, False), (768, 2048, 130, False),
@@ -83,11 +87,13 @@ def test_mfma_every_tile(hip, orc, tile, mode):
     W, acts = inputs(orc, rows, cols, na, 4242)
     hip.set_order(mode[0])
     hip.set_mfma_tile(*tile)
+    prev_d = hip.set_direct_mfma_min_batch(0)
     try:
         y = hip.matvec_multi(O.Q4_K, W, cols, rows, acts)
     finally:
         hip.set_mfma_tile(0, 0, 0)
         hip.set_order(E.ORDER_X86_CONTRACT)
+        hip.set_direct_mfma_min_batch(prev_d)
     pick = np.array([0, 1, 63, 64, 127, 128, 149])
     ref = orc.matvec_multi(O.Q4_K, W, cols, rows, acts[pick], mode[1], mode[2])
     assert np.array_equal(bits(y[pick]), bits(ref))
