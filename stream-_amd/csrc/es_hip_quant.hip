@@ -806,6 +806,57 @@ int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int 
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipFreeAsync");
 }
 
+// ---- the product entry point that allocates nothing ----------------------------------------------------------------
+// es_hip_matvec_multi_dev's job tables and pre-pass workspace, for callers that cannot allocate, live in this file-scope
+// device array instead of a stream-ordered allocation: each device the library runs on holds its own copy until the
+// process ends. Host code never passes the array's name (a host-side stand-in) to a kernel or a copy: it uses the device
+// address hipGetSymbolAddress returns, looked up once per device with that device current.
+constexpr size_t NOALLOC_SCRATCH = (size_t)ES_HIP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH];
+
+std::mutex g_scratch_mu;
+std::vector<uint8_t *> g_scratch_dev;   // per device id: scratch's device address there (null: not looked up yet)
+
+int scratch_address(uint8_t **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((size_t)dev >= g_scratch_dev.size()) g_scratch_dev.resize(dev + 1, nullptr);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return hip_fail(e, "hipGetSymbolAddress (scratch)");
+        g_scratch_dev[dev] = static_cast<uint8_t *>(p);
+    }
+    *out = g_scratch_dev[dev];
+    return ES_HIP_OK;
+}
+
+int es_hip_matvec_multi_dev_noalloc(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride,
+                                    int na, float *y, size_t ystride, void *stream) {
+    if (int rc = need_device()) return rc;
+    std::vector<Req> reqs{{type, W, act, y, nullptr, nullptr, r0, r1, cols, na, astride, ystride}};
+    Batch bt;
+    if (int rc = plan_batch(reqs, bt)) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty())
+        return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
+    const size_t ws_at = align256(bt.table_bytes), need = ws_at + bt.ws_bytes;
+    if (need > NOALLOC_SCRATCH)
+        return fail(ES_HIP_EINVAL, "this product needs %zu bytes of job tables and workspace, more than the %zu bytes of the "
+                                   "no-allocation scratch (use es_hip_matvec_multi_dev)", need, NOALLOC_SCRATCH);
+    uint8_t *dev = nullptr;
+    if (int rc = scratch_address(&dev)) return rc;
+    bind(bt, dev + ws_at);
+    // Every pre-pass writes all of its padded planes (zeros past na), so nothing in the scratch needs clearing; the
+    // tables are copied from pageable memory, which the copy has consumed when it returns.
+    const std::vector<uint8_t> img = table_image(bt);
+    hipError_t e;
+    if (!img.empty() && (e = hipMemcpyAsync(dev, img.data(), img.size(), hipMemcpyHostToDevice, s)) != hipSuccess)
+        return hip_fail(e, "job table upload");
+    return launch_batch(bt, dev, g_order.load(), s);
+}
+
 int es_hip_matvec_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, float *y, void *stream) {
     return es_hip_matvec_multi_dev(type, W, cols, r0, r1, act, 0, 1, y, 0, stream);
 }

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "libes_hip_quant.so")
 Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 2, 6, 8, 10, 11, 12, 13, 14
 TYPES = {"Q4_0": Q4_0, "Q5_0": Q5_0, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
 ORDER_X86_CONTRACT, ORDER_X86_STRICT, ORDER_SCALAR = 0, 1, 2
+NOALLOC_SCRATCH_BYTES = 32 << 20   # ES_HIP_NOALLOC_SCRATCH_BYTES
 BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
 BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 ACT_BYTES = {Q4_0: 36, Q5_0: 36, Q8_0: 36, Q2_K: 292, Q3_K: 292, Q4_K: 292, Q5_K: 292, Q6_K: 292}
@@ -223,6 +224,7 @@ class Lib:
             ("es_hip_memcpy_d2d", i, [vp, vp, sz]), ("es_hip_memset", i, [vp, i, sz]), ("es_hip_synchronize", i, []),
             ("es_hip_matvec_dev", i, [u32, vp, i, i, i, vp, vp, vp]),
             ("es_hip_matvec_multi_dev", i, [u32, vp, i, i, i, vp, sz, i, vp, sz, vp]),
+            ("es_hip_matvec_multi_dev_noalloc", i, [u32, vp, i, i, i, vp, sz, i, vp, sz, vp]),
             ("es_hip_run_jobs", i, [vp, i, vp]),
             ("es_hip_plan_create", vp, [vp, i]), ("es_hip_plan_run", i, [vp, vp]), ("es_hip_plan_destroy", None, [vp]),
             ("es_hip_plan_time_ms", C.c_double, [vp, i, i, vp]),
@@ -354,6 +356,11 @@ class Lib:
     # ---- device-pointer products ----
     def matvec_multi_dev(self, t, W, cols, r0, r1, act, astride, na, y, ystride, stream=None):
         self._check(self._L.es_hip_matvec_multi_dev(t, int(W), cols, r0, r1, int(act), astride, na, int(y), ystride, stream))
+
+    def matvec_multi_dev_noalloc(self, t, W, cols, r0, r1, act, astride, na, y, ystride, stream=None):
+        """es_hip_matvec_multi_dev with its tables and workspace in the library's static device scratch (no allocation)"""
+        self._check(self._L.es_hip_matvec_multi_dev_noalloc(t, int(W), cols, r0, r1, int(act), astride, na, int(y), ystride,
+                                                            stream))
 
     def matvec_dev(self, t, W, cols, r0, r1, act, y, stream=None):
         self._check(self._L.es_hip_matvec_dev(t, int(W), cols, r0, r1, int(act), int(y), stream))
