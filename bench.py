@@ -200,33 +200,90 @@ class MoeWorkload:
             b.close()
 
 
-def cpu_baseline(t, rows, cols, rng, seconds):
+class CpuRef:
     """The reference's es_matvec_multi (oracle/_ref/libesref_clang.so, built from its sources) or, where that build is
-    absent, the oracle's restatement, timed es_kbench-style on this host: a rotating set larger than the host LLC,
-    pinned threads taking 16-row chunks, >= `seconds` per point."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
+    absent, the oracle's restatement, timed es_kbench-style on this host: pinned threads taking 16-row chunks of a rotating
+    set of matrices, activations in the engine's batches of at most 64 (src/es_engine.c:43, 152-171)."""
 
-    orc = O.Oracle()
-    if O.ref_available("clang"):
-        ref = O.RefLib("clang")
-        fn, kind = orc.reference_fn_ptr(ref), "reference"
-    else:
-        fn, kind = orc.multi_fn_ptr(), "port"
-    W1 = random_blocks(t, rows, cols, rng)
-    nmat = max(1, (288 << 20) // W1.nbytes + 1)
-    W = np.tile(W1, nmat)
-    acts = quantize_acts(t, rng.standard_normal((1, cols)).astype(np.float32))
-    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    allc = max(1, min(16, avail))
-    points = {}
-    for nt in sorted({1, min(8, allc), allc}):
-        sec, passes, _ = orc.cpu_bench(fn, t, W, W1.nbytes, nmat, rows, cols, acts, nt, seconds)
-        points[nt] = W1.nbytes * nmat / sec / 1e9
-    return {"value": round(points[allc], 2), "unit": "GB/s", "cores": allc, "kind": kind,
-            "sample": f"Q4_K {rows}x{cols} matvec (T=1), {nmat} matrices = {W1.nbytes * nmat / 2**20:.0f} MiB rotating, "
-                      f">= {seconds:.1f} s per point, 16-row chunks (src/es_engine.c:152-171)",
-            "by_threads_gbs": {str(k): round(v, 2) for k, v in points.items()}, "host_cpus_visible": avail}
+    def __init__(self):
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+
+        self.orc = O.Oracle()
+        if O.ref_available("clang"):
+            self.ref = O.RefLib("clang")
+            self.fn, self.kind = self.orc.reference_fn_ptr(self.ref), "reference"
+        else:
+            self.fn, self.kind = self.orc.multi_fn_ptr(), "port"
+        avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+        self.avail, self.allc = avail, max(1, min(16, avail))
+        self.threads = sorted({1, min(8, self.allc), self.allc})
+
+    def seconds(self, t, rows, cols, na, rng, seconds, nt, min_bytes=288 << 20):
+        """seconds per pass of one matrix against na activations at nt threads (the rotating set at least min_bytes)"""
+        W1 = random_blocks(t, rows, cols, rng)
+        nmat = max(1, min_bytes // W1.nbytes + (1 if min_bytes else 0))
+        W = np.tile(W1, nmat) if nmat > 1 else W1
+        acts = quantize_acts(t, rng.standard_normal((na, cols)).astype(np.float32))
+        sec, _, _ = self.orc.cpu_bench(self.fn, t, W, W1.nbytes, nmat, rows, cols, acts, nt, seconds)
+        return sec / nmat, W1.nbytes
+
+    def point(self, t, rows, cols, na, rng, seconds, min_bytes=288 << 20):
+        """{threads: (weight GB/s, TOPS)} for one matrix shape"""
+        out = {}
+        for nt in self.threads:
+            sec, wb = self.seconds(t, rows, cols, na, rng, seconds, nt, min_bytes)
+            out[nt] = (wb / sec / 1e9, 2.0 * na * rows * cols / sec / 1e12)
+        return out
+
+    def record(self, pts, unit, sample):
+        k = 0 if unit == "GB/s" else 1
+        return {"value": round(pts[self.allc][k], 3), "unit": unit, "cores": self.allc, "kind": self.kind, "sample": sample,
+                "by_threads": {str(n): round(v[k], 3) for n, v in pts.items()}, "host_cpus_visible": self.avail}
+
+
+def cpu_baseline(rng, seconds):
+    """the headline's CPU figure: config 2 decode (Q4_K 8192x2048, T=1) in weight GB/s"""
+    c = CpuRef()
+    pts = c.point(E.Q4_K, 8192, 2048, 1, rng, seconds)
+    return c.record(pts, "GB/s", f"Q4_K 8192x2048 matvec (T=1), rotating set >= 288 MiB, >= {seconds:.1f} s per point, "
+                                 "16-row chunks (src/es_engine.c:152-171)")
+
+
+def cpu_configs(rng, seconds):
+    """the other configurations' CPU figures (the reference's kernels on this host), each a bounded sample"""
+    c = CpuRef()
+    out = {}
+    pts = c.point(E.Q4_0, 4864, 896, 1, rng, seconds)
+    out["config1_q4_0_decode"] = c.record(pts, "GB/s", "Q4_0 4864x896 matvec (T=1), rotating set >= 288 MiB")
+    pts = c.point(E.Q4_K, 8192, 2048, 512, rng, seconds, min_bytes=0)
+    out["prefill"] = c.record(pts, "TOPS", "Q4_K 8192x2048 against 512 activations (gate/up shape), batches of 64, 16-row "
+                                           "chunks; int8 TOPS = 2 x 512 x rows x cols / time")
+    for b in (1, 64):
+        pts = c.point(E.Q6_K, 151936, 1024, b, rng, seconds, min_bytes=(288 << 20) if b == 1 else 0)
+        out[f"config3_q6_k_head_b{b}"] = c.record(pts, "GB/s", f"Q6_K 151936x1024 head against {b} activation(s)")
+    # MoE layers through moe_n's job pattern (src/es_engine.c:871-918): per distinct expert, gate and up against the
+    # tokens routed to it, then down; the per-expert products are timed at the mean tokens per expert, over a rotating
+    # set of expert matrices
+    for name, (t3, n, ff, n_exp, k, n_tok, norm) in {
+            "config4_q2_k_moe": ((E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False),
+            "config5_mixed_moe_decode": ((E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True)}.items():
+        sel, _ = route_topk(rng, n_tok, n_exp, k, norm)   # the same synthetic routing as the device legs
+        used = len(set(sel.reshape(-1).tolist()))
+        per = max(1, round(n_tok * k / used))
+        pts, ms = {}, {}
+        for nt in c.threads:
+            sg, bg = c.seconds(t3[0], ff, n, per, rng, seconds, nt)
+            su, bu = c.seconds(t3[1], ff, n, per, rng, seconds, nt)
+            sd, bd = c.seconds(t3[2], n, ff, per, rng, seconds, nt)
+            layer = used * (sg + su + sd)
+            ms[nt] = layer * 1e3
+            pts[nt] = (used * (bg + bu + bd) / layer / 1e9, 2.0 * used * per * 3 * n * ff / layer / 1e12)
+        rec = c.record(pts, "GB/s", f"{used} experts x (gate, up {ff}x{n}, down {n}x{ff}) at {per} tokens each "
+                                    f"({n_tok} tokens top-{k}); expert bytes / layer time")
+        rec["ms_per_layer"] = round(ms[c.allc], 4)
+        out[name] = rec
+    return out
 
 
 Q4K_FFN = [(E.Q4_K, 8192, 2048), (E.Q4_K, 8192, 2048), (E.Q4_K, 2048, 8192)]
@@ -330,6 +387,29 @@ def act_prep_times(lib, rng, K, Wm):
     return out
 
 
+def dense_ffn_time(lib, rng, K, Wm, T=512, n=2048, ff=8192):
+    """dense_n on the device (es_hip_dense_ffn_dev) at config 2's prefill shape: gate/up Q4_K ff x n into [T][2 ff], SwiGLU
+    + Q8_K of h, down Q4_K n x ff. us per layer (HIP events on the null stream around K calls) and int8 TOPS over the three
+    products."""
+    t = E.Q4_K
+    W = [random_blocks(t, ff, n, rng), random_blocks(t, ff, n, rng), random_blocks(t, n, ff, rng)]
+    x = quantize_acts(t, rng.standard_normal((T, n)).astype(np.float32))
+    d = [lib.upload(a) for a in W + [x]]
+    gu, hq, out = lib.alloc(T * 2 * ff * 4), lib.alloc(T * (ff // 256) * 292), lib.alloc(T * n * 4)
+    fn = lambda: lib.dense_ffn_dev(t, d[0], t, d[1], t, d[2], n, ff, T, d[3], x.strides[0], gu, hq, out, n)
+    t_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_end:
+        fn()
+        lib.synchronize()
+    ms = HipEvents().time_ms(fn, Wm, K)
+    for b in d + [gu, hq, out]:
+        b.close()
+    ops = 2 * T * 3 * n * ff
+    return {"us": round(ms * 1e3, 2), "tops": round(ops / (ms * 1e-3) / 1e12, 2),
+            "frac": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+            "workload": f"dense_n T={T}: gate/up {ff}x{n} + SwiGLU/Q8_K + down {n}x{ff}, Q4_K, three dependent steps"}
+
+
 def only(lib, rng, name, K, Wm):
     """one workload of the bench, alone: the command profiler summaries are taken from"""
     if name == "copy":   # a plain device copy of known size, the reference for HBM byte counters
@@ -344,6 +424,8 @@ def only(lib, rng, name, K, Wm):
         return {"workload": "copy", "bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": Wm + K}
     if name == "act":
         return {"workload": "act", **act_prep_times(lib, rng, K, Wm)}
+    if name == "dense":
+        return {"workload": "dense", **dense_ffn_time(lib, rng, K, Wm)}
     if name == "cache":
         return {"workload": "cache", "pageable": cache_load_rate(lib, rng, K, Wm),
                 "pinned": cache_load_rate(lib, rng, K, Wm, pinned=True)}
@@ -376,7 +458,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=2.0)
-    ap.add_argument("--only", choices=["decode", "prefill", "config1", "config3b1", "config3b64", "config4", "config5", "act",
+    ap.add_argument("--only", choices=["decode", "prefill", "dense", "config1", "config3b1", "config3b64", "config4", "config5", "act",
                                        "cache", "copy"] + [f"decode_{f.lower()}" for f in E.TYPES],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
@@ -409,6 +491,8 @@ def main():
     pre.close()
 
     extra = {}
+    # ---- config 2 dense_n on the device (gate/up, SwiGLU + Q8_K, down), T=512
+    extra["config2_dense_ffn_t512"] = dense_ffn_time(lib, rng, max(3, K // 4), Wm)
     # ---- config 1: Q4_0 4864x896, b=1, 410 copies (1.0 GB)
     c1 = Workload(lib, rng, [(E.Q4_0, 4864, 896)], 1, 410)
     _, e1 = c1.time(Wm, K)
@@ -447,7 +531,12 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(E.Q4_K, 8192, 2048, rng, args.cpu_seconds)
+        cpu = cpu_baseline(rng, args.cpu_seconds)
+        cfg_cpu = cpu_configs(rng, args.cpu_seconds / 2)
+        for key, rec in cfg_cpu.items():
+            if key == "prefill":
+                continue
+            extra.setdefault(key, {})["cpu"] = rec
 
     # HBM bytes per launch of the same workloads, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summaries
     traffic = {}
@@ -468,6 +557,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": {"workload": "Q4_K prefill T=512: gate/up 8192x2048 and down 2048x8192, one batched launch",
                     "value": round(tops, 2), "unit": "TOPS", "ms": round(pev, 4),
+                    "cpu": None if args.no_cpu else cfg_cpu["prefill"],
                     "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                                  "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": traffic.get("prefill")}},
         "configs": extra,

@@ -166,6 +166,19 @@ typedef struct {
  * launch per format, outputs come back in one copy. Synchronous, like the reference's. Returns 0 or ES_HIP_E*. */
 int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs);
 
+/* ---- dense FFN: dense_n (src/es_engine.c:957-972) ------------------------------------------------------------------- */
+/* The SwiGLU FFN of N tokens on the device, as dense_n computes it for a layer without LoRA or the situ activation:
+ *   gate and up products into gu, token t's gate at gu[t * 2 ff + i], up at gu[t * 2 ff + ff + i] (the engine's BGU);
+ *   h = g / (1 + expf(-g)) * u, prepared as es_act_prepare does for the down type (Q8_K for K-quants, Q8_0 otherwise) into
+ *   hq, token t's ff / 256 Q8_K (or ff / 32 Q8_0) blocks packed at hq + t * (that many blocks' bytes);
+ *   down products into out, token t's n outputs at out + t * ostride floats.
+ * Weights: device pointers to row 0 (gate, up: ff rows of n; down: n rows of ff). x: the N tokens' activation blocks
+ * (Q8_K for K-quant gate/up, Q8_0 otherwise), token t at x + t * xstride bytes (0: packed). gu (N * 2 ff floats) and hq
+ * are the caller's device workspaces. Stream-ordered; bit-identical to dense_n's outputs (and to its BGU rows). */
+int es_hip_dense_ffn_dev(uint32_t gate_type, const void *wg, uint32_t up_type, const void *wu, uint32_t down_type,
+                         const void *wd, int n, int ff, int N, const void *x, size_t xstride, float *gu, void *hq,
+                         float *out, size_t ostride, void *stream);
+
 /* ---- MoE expert FFN: the expert part of moe_n (src/es_engine.c:848-942) --------------------------------------------- */
 /* The routed experts of one layer, resident on the device. Experts whose pointers are NULL must not be routed. */
 typedef struct {

@@ -919,8 +919,11 @@ double esq_cpu_bench(esq_multi_fn fn, uint32_t type, const void *W, size_t mat_b
         args[i].tid = i;
         if (i) pthread_create(&th[i], NULL, bench_worker, &args[i]);
     }
+    cpu_set_t keep;   /* worker 0 is the calling thread: its own affinity comes back afterwards */
+    const int have = sched_getaffinity(0, sizeof keep, &keep) == 0;
     bench_worker(&args[0]);
     for (int i = 1; i < nthreads; i++) pthread_join(th[i], NULL);
+    if (have) sched_setaffinity(0, sizeof keep, &keep);
     pthread_barrier_destroy(&c.bar);
     free(th);
     free(args);

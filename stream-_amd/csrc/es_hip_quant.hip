@@ -780,17 +780,15 @@ int es_hip_synchronize(void) {
 }
 
 // ---- products on device memory ----------------------------------------------------------------------------------------
-int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride, int na,
-                            float *y, size_t ystride, void *stream) {
-    if (int rc = need_device()) return rc;
-    std::vector<Req> reqs{{type, W, act, y, nullptr, nullptr, r0, r1, cols, na, astride, ystride}};
+// Plan and launch a batch in stream order: a single decode job by value; anything else (several jobs per launch,
+// pre-passes) with a stream-ordered allocation for the job tables and the pre-pass workspace, freed in stream order. The
+// tables are copied from pageable memory, which the copy has consumed when it returns.
+static int run_async(const std::vector<Req> &reqs, hipStream_t s) {
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty())
+    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.mv.size() <= 1 &&
+        (bt.mv.empty() || bt.mv[0].jobs.size() == 1))
         return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
-    // other kernels (possibly several jobs per launch, pre-passes): a stream-ordered allocation for the job tables and the
-    // pre-pass workspace. The tables are copied from pageable memory, which the copy has consumed when it returns.
     void *dev = nullptr;
     const size_t ws_at = align256(bt.table_bytes);
     hipError_t e = hipMallocAsync(&dev, std::max<size_t>(ws_at + bt.ws_bytes, 256), s);
@@ -806,6 +804,39 @@ int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int 
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipFreeAsync");
 }
 
+int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride, int na,
+                            float *y, size_t ystride, void *stream) {
+    if (int rc = need_device()) return rc;
+    return run_async({{type, W, act, y, nullptr, nullptr, r0, r1, cols, na, astride, ystride}}, static_cast<hipStream_t>(stream));
+}
+
+// dense_n (src/es_engine.c:957-972): gate and up into the engine's [token][2 ff] rows in one batch, SwiGLU fused with the
+// preparation of h for the down product's activation kind, then down.
+int es_hip_dense_ffn_dev(uint32_t gate_type, const void *wg, uint32_t up_type, const void *wu, uint32_t down_type,
+                         const void *wd, int n, int ff, int N, const void *x, size_t xstride, float *gu, void *hq,
+                         float *out, size_t ostride, void *stream) {
+    if (int rc = need_device()) return rc;
+    FmtInfo fg, fu, fd;
+    if (!fmt_info(gate_type, fg) || !fmt_info(up_type, fu) || !fmt_info(down_type, fd))
+        return fail(ES_HIP_EINVAL, "a weight type is not computed by this library");
+    if (fg.ab != fu.ab) return fail(ES_HIP_EINVAL, "gate and up must take the same kind of activation blocks");
+    if (n <= 0 || ff <= 0 || N < 0) return fail(ES_HIP_EINVAL, "bad shape n %d ff %d N %d", n, ff, N);
+    const bool dq8k = fd.ab == 292;   // K-quant down: Q8_K activations; Q4_0/Q5_0/Q8_0: Q8_0
+    if (ff % (dq8k ? 256 : 32)) return fail(ES_HIP_EINVAL, "ff %d is not a whole number of the down type's blocks", ff);
+    if (N == 0) return ES_HIP_OK;
+    if (!wg || !wu || !wd || !x || !gu || !hq || !out) return fail(ES_HIP_EINVAL, "null pointer");
+    if (ostride < (size_t)n) return fail(ES_HIP_EINVAL, "ostride %zu < n %d", ostride, n);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t gus = 2 * (size_t)ff;
+    if (int rc = run_async({{gate_type, wg, x, gu, nullptr, nullptr, 0, ff, n, N, xstride, gus},
+                            {up_type, wu, x, gu + ff, nullptr, nullptr, 0, ff, n, N, xstride, gus}}, s))
+        return rc;
+    const size_t hs = (size_t)(ff / (dq8k ? 256 : 32)) * fd.ab;   // packed activation blocks of h, per token
+    if (int rc = es_hip_swiglu_prepare_dev(gu, gus, N, ff, nullptr, 0, dq8k ? nullptr : hq, hs, dq8k ? hq : nullptr, hs, stream))
+        return rc;
+    return run_async({{down_type, wd, hq, out, nullptr, nullptr, 0, n, ff, N, hs, ostride}}, s);
+}
+
 // ---- the product entry point that allocates nothing ----------------------------------------------------------------
 // es_hip_matvec_multi_dev's job tables and pre-pass workspace, for callers that cannot allocate, live in this file-scope
 // device array instead of a stream-ordered allocation: each device the library runs on holds its own copy until the
@@ -814,10 +845,10 @@ int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int 
 constexpr size_t NOALLOC_SCRATCH = (size_t)ES_HIP_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH];
 
-std::mutex g_scratch_mu;
-std::vector<uint8_t *> g_scratch_dev;   // per device id: scratch's device address there (null: not looked up yet)
+static std::mutex g_scratch_mu;
+static std::vector<uint8_t *> g_scratch_dev;   // per device id: scratch's device address there (null: not looked up yet)
 
-int scratch_address(uint8_t **out) {
+static int scratch_address(uint8_t **out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");

@@ -225,6 +225,7 @@ class Lib:
             ("es_hip_matvec_dev", i, [u32, vp, i, i, i, vp, vp, vp]),
             ("es_hip_matvec_multi_dev", i, [u32, vp, i, i, i, vp, sz, i, vp, sz, vp]),
             ("es_hip_matvec_multi_dev_noalloc", i, [u32, vp, i, i, i, vp, sz, i, vp, sz, vp]),
+            ("es_hip_dense_ffn_dev", i, [u32, vp, u32, vp, u32, vp, i, i, i, vp, sz, vp, vp, vp, sz, vp]),
             ("es_hip_run_jobs", i, [vp, i, vp]),
             ("es_hip_plan_create", vp, [vp, i]), ("es_hip_plan_run", i, [vp, vp]), ("es_hip_plan_destroy", None, [vp]),
             ("es_hip_plan_time_ms", C.c_double, [vp, i, i, vp]),
@@ -361,6 +362,11 @@ class Lib:
         """es_hip_matvec_multi_dev with its tables and workspace in the library's static device scratch (no allocation)"""
         self._check(self._L.es_hip_matvec_multi_dev_noalloc(t, int(W), cols, r0, r1, int(act), astride, na, int(y), ystride,
                                                             stream))
+
+    def dense_ffn_dev(self, tg, wg, tu, wu, td, wd, n, ff, N, x, xstride, gu, hq, out, ostride, stream=None):
+        """dense_n on the device (es_hip_dense_ffn_dev); every pointer a device buffer"""
+        self._check(self._L.es_hip_dense_ffn_dev(tg, int(wg), tu, int(wu), td, int(wd), n, ff, N, int(x), xstride, int(gu),
+                                                 int(hq), int(out), ostride, stream))
 
     def matvec_dev(self, t, W, cols, r0, r1, act, y, stream=None):
         self._check(self._L.es_hip_matvec_dev(t, int(W), cols, r0, r1, int(act), int(y), stream))

@@ -38,6 +38,19 @@ def test_exports_are_c_symbols():
         assert re.search(rf"\sT\s{n}$", out, flags=re.M), n   # unmangled, extern "C"
 
 
+def test_no_other_c_symbols_exported():
+    """every unmangled symbol the library defines is a declared es_hip_* entry point (helpers stay internal)"""
+    declared = set(declared_functions())
+    stray = []
+    for line in os.popen(f"nm -D --defined-only {E.LIB_PATH}").read().splitlines():
+        parts = line.split()
+        if len(parts) != 3 or parts[2].startswith(("_Z", "__hip_cuid_", "_init", "_fini", "_edata", "_end", "__bss")):
+            continue
+        if parts[2] not in declared:
+            stray.append(parts[2])
+    assert not stray, stray
+
+
 @pytest.mark.parametrize("F", ["Q4_0", "Q5_0", "Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"])
 def test_row_bytes_match_reference(hiplib, F):
     t = O.TYPES[F]
