@@ -141,7 +141,8 @@ class MoeWorkload:
     optionally the attention products of the same tokens (one job-batch plan per copy). A step runs every copy once."""
 
     def __init__(self, lib, rng, types, n, ff, n_exp, k, n_tok, norm_topk, copies, attn=()):
-        self.lib, self.keep, self.plans, self.moe = lib, [], [], []
+        self.lib, self.keep, self.plans, self.moe, self.ctx_args = lib, [], [], [], []
+        self.n_tok, self.n_exp, self.n, self.norm = n_tok, n_exp, n, norm_topk
         gt, ut, dt = types
         sel, w = route_topk(rng, n_tok, n_exp, k, norm_topk)
         used = sorted(set(sel.reshape(-1).tolist()))
@@ -151,6 +152,10 @@ class MoeWorkload:
         x = quantize_acts(gt, rng.standard_normal((n_tok, n)).astype(np.float32))
         dx = lib.upload(x)
         self.keep.append(dx)
+        self.dx, self.xstride = dx, x.strides[0]
+        # router logits for the device-routed leg: a fresh routing every step (8 sets in rotation)
+        self.logits = [lib.upload(rng.standard_normal((n_tok, n_exp)).astype(np.float32)) for _ in range(8)]
+        self.keep += self.logits
         xa = quantize_acts(E.Q5_0, rng.standard_normal((n_tok, n)).astype(np.float32)) if attn else None
         dxa = lib.upload(xa) if attn else None
         for c in range(copies):
@@ -172,6 +177,7 @@ class MoeWorkload:
             self.keep.append(out)
             args = E.MoeArgs(gt, ut, dt, n, ff, experts, np.full(n_tok, k), sel, w)
             self.moe.append(lib.moe_plan(args, dx, x.strides[0], out, n))
+            self.ctx_args.append((lib.moe_ctx(args, n_tok, k), out))
             if attn:
                 specs = []
                 for (rows, cols) in attn:
@@ -193,9 +199,31 @@ class MoeWorkload:
             self.lib.step_time_ms(self.plans, self.moe, 0, 2)
         return self.lib.step_time_ms(self.plans, self.moe, warmup, steps) / self.copies
 
+    def time_device_routed(self, warmup, steps):
+        """ms per copy (one layer) with the routing computed on the device from fresh logits every step and the layer run
+        through its context (es_hip_moe_ctx_run_logits: grouping and job tables on the device, no host round trip), the
+        attention plans as in time(); HIP events on the null stream around `steps` steps"""
+        it = [0]
+
+        def step():
+            for i, (ctx, out) in enumerate(self.ctx_args):
+                if self.plans:
+                    self.plans[i].run()
+                ctx.run_logits(self.n_tok, self.logits[it[0] % len(self.logits)], 0, self.norm, self.dx, self.xstride, out,
+                               self.n)
+            it[0] += 1
+
+        t_end = time.perf_counter() + SETTLE_S
+        while time.perf_counter() < t_end:
+            step()
+            self.lib.synchronize()
+        return HipEvents().time_ms(step, warmup, steps) / self.copies
+
     def close(self):
         for p in self.plans + self.moe:
             p.close()
+        for ctx, _ in self.ctx_args:
+            ctx.close()
         for b in self.keep:
             b.close()
 
@@ -434,7 +462,8 @@ def only(lib, rng, name, K, Wm):
              MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
                          attn=((4096, 2048), (512, 2048), (512, 2048))))
         ms = w.time(Wm, K)
-        out = {"workload": name, "ms_per_layer": round(ms, 4), "weight_bytes_per_layer": w.weight_bytes // w.copies}
+        out = {"workload": name, "ms_per_layer": round(ms, 4), "weight_bytes_per_layer": w.weight_bytes // w.copies,
+               "device_routed_ms_per_layer": round(w.time_device_routed(Wm, K), 4)}
         w.close()
         return out
     if name.startswith("decode_"):   # config 2's decode in another weight format (same shapes, same 38 layer copies)
@@ -510,19 +539,23 @@ def main():
     # ---- config 4: OLMoE Q2_K experts (64 x gate/up 1024x2048, down 2048x1024), 128 tokens top-8; 8 layer copies
     c4 = MoeWorkload(lib, rng, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8)
     e4 = c4.time(Wm, max(3, K // 2))
+    d4 = c4.time_device_routed(Wm, max(3, K // 2))
     extra["config4_q2_k_moe"] = {"gbs": round(c4.weight_bytes / c4.copies / (e4 * 1e-3) / 1e9, 1), "ms": round(e4, 4),
                                  "weight_bytes": c4.weight_bytes // c4.copies, "experts_used": c4.distinct,
-                                 "hbm_frac": round(c4.weight_bytes / c4.copies / (e4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                                 "hbm_frac": round(c4.weight_bytes / c4.copies / (e4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                 "device_routed_ms": round(d4, 4), "device_routed_vs_plan": round(d4 / e4, 3)}
     c4.close()
     # ---- config 5: Qwen3-30B-A3B-like decode batch of 32: Q5_0 attention q/k/v + 128 experts (Q4_K gate/up 768x2048,
     # Q6_K down 2048x768) top-8 renormalised; 3 layer copies
     c5 = MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
                      attn=((4096, 2048), (512, 2048), (512, 2048)))
     e5 = c5.time(Wm, max(3, K // 2))
+    d5 = c5.time_device_routed(Wm, max(3, K // 2))
     extra["config5_mixed_moe_decode"] = {"gbs": round(c5.weight_bytes / c5.copies / (e5 * 1e-3) / 1e9, 1),
                                          "ms": round(e5, 4), "weight_bytes": c5.weight_bytes // c5.copies,
                                          "experts_used": c5.distinct,
-                                         "hbm_frac": round(c5.weight_bytes / c5.copies / (e5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                                         "hbm_frac": round(c5.weight_bytes / c5.copies / (e5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                         "device_routed_ms": round(d5, 4), "device_routed_vs_plan": round(d5 / e5, 3)}
     c5.close()
     # ---- device activation preparation at config 2's prefill shapes (rmsnorm / SwiGLU fused with the quantizers)
     extra["act_prep_t512"] = act_prep_times(lib, rng, K, Wm)

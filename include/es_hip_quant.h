@@ -218,6 +218,27 @@ es_hip_moe_plan *es_hip_moe_plan_create(const es_hip_moe *m, int N, const int *k
 int    es_hip_moe_plan_run(es_hip_moe_plan *plan, void *stream);
 void   es_hip_moe_plan_destroy(es_hip_moe_plan *plan);
 
+/* ---- device-routed MoE layer: no allocation, no host round trip per call -------------------------------------------- */
+typedef struct es_hip_moe_ctx es_hip_moe_ctx;
+/* A context for one layer's expert set (the es_hip_moe arrays are copied; the expert weights must stay resident and
+ * unrouted experts may be NULL) and up to max_tokens tokens of k choices each (max_tokens * k <= 16384, k <= 64):
+ * every buffer and job table of a layer is allocated here, once. NULL on failure (es_hip_last_error). */
+es_hip_moe_ctx *es_hip_moe_ctx_create(const es_hip_moe *m, int max_tokens, int k);
+/* moe_n's expert part (src/es_engine.c:848-942) for N <= max_tokens tokens whose k choices and weights are in device
+ * memory (sel: int [N][k], valid expert ids; w: float [N][k]): the grouping of :871-888 (distinct experts in order of
+ * first use, each expert's rows in choice order) and the job tables are computed on the device, then gate/up, SwiGLU +
+ * requantization, down and the combine run as in es_hip_moe_ffn, with the same outputs bit for bit. x / out as for
+ * es_hip_moe_ffn (device). Stream-ordered and asynchronous: no allocation, no copy to or from the host, no wait. Calls on
+ * one context share its buffers: order them on one stream (or synchronise between streams). */
+int es_hip_moe_ctx_run(es_hip_moe_ctx *c, int N, const int *sel, const float *w, const void *x, size_t xstride, float *out,
+                       size_t ostride, void *stream);
+/* The layer from the router's logits (device, token t's n_exp logits at logits + t * lstride floats, 0: packed): route()
+ * for softmax gating on the device (as es_hip_route_softmax_dev), then es_hip_moe_ctx_run's work. sel_out / w_out
+ * (device, N * k each, optional) receive the routing. Asynchronous as es_hip_moe_ctx_run. */
+int es_hip_moe_ctx_run_logits(es_hip_moe_ctx *c, int N, const float *logits, size_t lstride, int norm_topk, const void *x,
+                              size_t xstride, float *out, size_t ostride, int *sel_out, float *w_out, void *stream);
+void es_hip_moe_ctx_destroy(es_hip_moe_ctx *c);
+
 /* ---- diagnostics ----------------------------------------------------------------------------------------------------- */
 /* The integer part of every (row, block) of rows [0, rows) against one activation, as the reference's kernels form it:
  * dots[r * nb + b] = the block's integer dot (Q4_0/Q5_0/Q8_0: the sum of the eight AVX2 lane sums; Q4_K: dot; Q6_K: tot;

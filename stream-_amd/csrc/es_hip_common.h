@@ -152,6 +152,43 @@ hipError_t dequant_launch(uint32_t type, const void *src, float *dst, long n, hi
 hipError_t route_softmax_launch(const float *logits, uint64_t ls, int ntok, int ne, int k, int norm_topk, int *sel, float *w,
                                 int kmax, hipStream_t s);
 
+// Device-routed MoE (es_hip_moe.hip): moe_n's grouping (src/es_engine.c:871-888) and the job tables of one layer's
+// gate/up and down launches built on the device from a routing in device memory, so a layer needs no host round trip.
+// Every expert product of a launch runs on one kernel family, chosen by the host from the expected tokens per expert:
+//   MOE_FAM_MV: the decode kernel (one job per expert slot and product, a fixed number of row tiles each);
+//   MOE_FAM_MM: a pre-pass of the expert's gathered activations into its planes (packed one expert after another), then
+//               the matrix-core kernel (tiles of 128 rows x bn activations, as many activation tiles as the expert's
+//               count needs).
+// Slots u >= the number of experts used, and one sentinel job at the end of every table, are empty jobs placed after the
+// last real tile (the host launches upper-bound grids; their workgroups find an empty job and exit).
+constexpr int MOE_FAM_MV = 0, MOE_FAM_MM = 1, MOE_GROUP_THREADS = 1024, MOE_MAX_PAIRS = 16384;
+struct MoeFamily {
+    int kind;
+    MvJob mv;              // MV: template job (rows, cols, strides, rows_per_wg, chain_rows); mv_tiles row tiles per job
+    int mv_tiles;
+    MmJob mm;              // MM: template job; bn activations per tile; row tiles (rounded up to 8, the XCD map)
+    PrepJob pj;            // MM: template pre-pass (nbk, kind)
+    int bn, row_tiles8;
+};
+struct MoeDevArgs {
+    const int *sel;         // [ntok][k] routing (experts)
+    const float *w;         // [ntok][k] routing weights
+    int ntok, k, n_exp, umax, ff, n;
+    const uint8_t *const *gate, *const *up, *const *down;   // device arrays of n_exp expert pointers
+    const uint8_t *x;       // gate/up activation blocks, token t at x + t * xstride
+    uint64_t xstride, hstride;
+    float *bgu;             // [pair row][2 ff]
+    uint8_t *ha;            // [pair row] requantized h, hstride bytes apart
+    float *bye;             // [pair row][n]
+    int *tok_of;            // [pair row] token of the row (the gate/up gather table)
+    int *rowof;             // [ntok][k] pair row of each choice
+    float *wv;              // [ntok][k] weights as the combine reads them
+    void *gu_jobs, *dn_jobs;         // MvJob or MmJob tables: gate/up 2 umax + 1 entries, down umax + 1
+    PrepJob *gu_prep, *dn_prep;      // MM: umax + 1 entries each
+    uint8_t *gu_ws, *dn_ws;          // MM: the experts' planes, packed in slot order (256-byte aligned)
+};
+hipError_t moe_group_build_launch(const MoeDevArgs &a, const MoeFamily &gu, const MoeFamily &dn, hipStream_t s);
+
 constexpr int ACT_RMS_MAX_COLS = 16384;   // rmsnorm rows' squares are staged whole in LDS (128 KB of doubles)
 // Activation preparation (es_hip_act.hip): rows of fp32 values (plain, rmsnorm-ed, or the SwiGLU of gate|up rows) into
 // Q8_0 and / or Q8_K blocks (either output may be null). Float strides in floats, block strides in bytes.

@@ -12,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <array>
 #include <map>
 #include <mutex>
 #include <string>
@@ -1424,6 +1425,328 @@ int es_hip_moe_ffn_logits(const es_hip_moe *m, int N, const float *logits, size_
     if (sel_out) std::memcpy(sel_out, sel.data(), pairs * sizeof(int));
     if (w_out) std::memcpy(w_out, w.data(), pairs * sizeof(float));
     return es_hip_moe_ffn(m, N, kk.data(), sel.data(), w.data(), k, x, xstride, out, ostride, stream);
+}
+
+}  // extern "C"
+
+// ---- device-routed MoE context ----------------------------------------------------------------------------------------
+// Buffers for up to max_tokens tokens and every table of the two launches, allocated once; a layer then runs in stream
+// order with no allocation, no copy to or from the host and no wait: routing (optional), grouping and job tables on the
+// device (moe_group_build), gate/up, SwiGLU + requantization, down, combine.
+struct es_hip_moe_ctx {
+    uint32_t gt, ut, dt;
+    int n, ff, n_exp, max_tokens, k;
+    uint8_t *buf = nullptr;
+    int *sel = nullptr, *tok_of = nullptr, *rowof = nullptr, *kk = nullptr;
+    float *w = nullptr, *wv = nullptr, *bgu = nullptr, *bye = nullptr;
+    uint8_t *ha = nullptr;
+    const uint8_t **dgate = nullptr, **dup = nullptr, **ddown = nullptr;
+    void *gu_jobs = nullptr, *dn_jobs = nullptr;
+    esq::PrepJob *gu_prep = nullptr, *dn_prep = nullptr;
+    uint8_t *gu_ws = nullptr, *dn_ws = nullptr;
+    uint64_t hstride = 0, gu_slot = 0, dn_slot = 0;   // gu_slot / dn_slot: plane workspace bytes
+    const uint8_t *w_gate0 = nullptr, *w_down0 = nullptr;   // a valid weight pointer for empty jobs
+    bool h_q8k = true;
+    std::map<std::array<int, 6>, std::pair<MvLaunch, MvJob>> mv_cache;   // decode-kernel sizing by (type, rows, cols, ...)
+};
+
+namespace {
+
+// na_pad and tile activations of a matrix-core product of about `na` activations (the planner's rule for one product)
+bool moe_mm_family(uint32_t type, int cols, double expect, int &bn) {
+    const Req q{type, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 1, cols, std::max(1, (int)(expect + 0.5)), 0, 0};
+    if (!mm_eligible(q)) return false;
+    const int na = q.na;
+    if (type == ES_HIP_Q2_K) bn = na <= 32 ? 32 : 64;
+    else if (type == ES_HIP_Q6_K) bn = na <= 16 ? 16 : na <= 32 ? 32 : 64;
+    else bn = na <= 16 ? 16 : na <= 32 ? 32 : na <= 64 ? 64 : 128;
+    return esq::mm_tile_ok(128, bn, 8);
+}
+
+// the planes of every expert of a layer of R choices over at most umax experts, packed: at most R + 127 umax padded
+// activations (tiles of up to 128), each expert's two planes rounded up to 256 bytes
+size_t moe_ws_bytes(int cols, int R, int umax) {
+    const size_t nbk = cols / 256, rows = (size_t)R + 127 * (size_t)umax;
+    return nbk * rows * (256 + 36) + 2 * 256 * (size_t)umax;
+}
+
+// one product's family and launch: rows x cols weights of `type`, umax expert slots of `njob` products each, R choices
+struct MoeLaunch {
+    esq::MoeFamily F{};
+    MvLaunch L{};
+    int bn = 0, grid = 0, njobs = 0, nprep = 0;   // tile upper bound; job table entries; pre-pass entries (MM)
+    long items = 0;                               // pre-pass item upper bound (MM)
+};
+
+int moe_family(es_hip_moe_ctx *c, uint32_t type, int rows, int cols, int umax, int njob, int R, double expect,
+               const uint8_t *w0, const uint8_t *act, const int *arow, uint64_t astride, float *y, uint64_t ystride,
+               uint8_t *ws, MoeLaunch &M) {
+    FmtInfo f;
+    fmt_info(type, f);
+    const int nbk = cols / f.be;
+    M.F = esq::MoeFamily{};
+    M.njobs = njob * umax + 1;
+    M.nprep = umax + 1;
+    int bn = 0;
+    if (ws && moe_mm_family(type, cols, expect, bn)) {
+        M.F.kind = esq::MOE_FAM_MM;
+        M.bn = M.F.bn = bn;
+        const int row_tiles = (rows + 127) / 128;
+        M.F.row_tiles8 = 8 * ((row_tiles + 7) / 8);
+        esq::MmJob &j = M.F.mm;
+        j.W = w0;
+        j.xq = ws;
+        j.xm = ws;
+        j.y = y;
+        j.ystride = ystride;
+        j.row_bytes = (uint64_t)nbk * f.bb;
+        j.r0 = 0;
+        j.r1 = rows;
+        j.cols = cols;
+        j.ntok_tiles = 1;
+        esq::PrepJob &p = M.F.pj;
+        p.act = act;
+        p.arow = arow;
+        p.xq = ws;
+        p.xm = ws;
+        p.astride = astride;
+        p.nbk = nbk;
+        p.kind = 2;
+        const long ntok_ub = (R + bn - 1) / bn + umax;   // sum over experts of ceil(count / bn)
+        M.grid = njob * M.F.row_tiles8 * (int)ntok_ub;
+        M.items = ntok_ub * bn * nbk * (long)esq::prep_words(2) + (long)umax * esq::PREP_SPAN;
+        return ES_HIP_OK;
+    }
+    // the decode kernel, sized as the planner sizes umax * njob products of about `expect` activations each (the sizing
+    // depends on the shapes only: kept per context)
+    M.F.kind = esq::MOE_FAM_MV;
+    const int na = std::max(1, (int)std::ceil(expect));
+    const std::array<int, 6> key{(int)type, rows, cols, umax, njob, na};
+    auto it = c->mv_cache.find(key);
+    if (it == c->mv_cache.end()) {
+        std::vector<Req> reqs((size_t)umax * njob,
+                              Req{type, w0, act, y, nullptr, nullptr, 0, rows, cols, na, astride, ystride, arow, 1});
+        std::vector<Group> groups;
+        if (int rc = plan_groups(reqs, groups)) return rc;
+        if (groups.size() != 1) return fail(ES_HIP_EINVAL, "MoE product planned as %zu launches", groups.size());
+        it = c->mv_cache.emplace(key, std::make_pair(groups[0].L, groups[0].jobs[0])).first;
+    }
+    M.L = it->second.first;
+    M.F.mv = it->second.second;   // this call's pointers: the template must point at live buffers (empty jobs keep them)
+    M.F.mv.W = w0;
+    M.F.mv.act = act;
+    M.F.mv.arow = arow;
+    M.F.mv.astride = astride;
+    M.F.mv.y = y;
+    M.F.mv.ystride = ystride;
+    M.F.mv.na = 0;
+    M.F.mv.tile0 = 0;
+    M.F.mv_tiles = (rows + M.F.mv.rows_per_wg - 1) / M.F.mv.rows_per_wg;
+    M.grid = M.L.grid = njob * umax * M.F.mv_tiles;
+    return ES_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+es_hip_moe_ctx *es_hip_moe_ctx_create(const es_hip_moe *m, int max_tokens, int k) {
+    if (need_device()) return nullptr;
+    if (!m) { fail(ES_HIP_EINVAL, "null MoE description"); return nullptr; }
+    FmtInfo fg, fu, fd;
+    if (!fmt_info(m->gate_type, fg) || !fmt_info(m->up_type, fu) || !fmt_info(m->down_type, fd)) {
+        fail(ES_HIP_EINVAL, "an expert type is not computed by this library");
+        return nullptr;
+    }
+    if (m->gate_type != m->up_type) { fail(ES_HIP_EINVAL, "the device-routed MoE needs gate and up of one type"); return nullptr; }
+    if (m->n <= 0 || m->ff <= 0 || m->n % fg.be || m->ff % fd.be) { fail(ES_HIP_EINVAL, "bad widths n %d, ff %d", m->n, m->ff); return nullptr; }
+    if (m->n_exp <= 0 || m->n_exp > esq::ROUTE_MAX_EXPERTS || !m->gate || !m->up || !m->down) {
+        fail(ES_HIP_EINVAL, "bad expert table (1 to %d experts)", esq::ROUTE_MAX_EXPERTS);
+        return nullptr;
+    }
+    if (max_tokens <= 0 || k <= 0 || k > 64 || k > m->n_exp || (long)max_tokens * k > esq::MOE_MAX_PAIRS) {
+        fail(ES_HIP_EINVAL, "bad max_tokens %d or k %d (at most %d choices)", max_tokens, k, esq::MOE_MAX_PAIRS);
+        return nullptr;
+    }
+    auto *c = new es_hip_moe_ctx();
+    c->gt = m->gate_type; c->ut = m->up_type; c->dt = m->down_type;
+    c->n = m->n; c->ff = m->ff; c->n_exp = m->n_exp; c->max_tokens = max_tokens; c->k = k;
+    c->h_q8k = fd.be == 256;
+    c->hstride = (uint64_t)(m->ff / fd.be) * fd.ab;
+    std::vector<const uint8_t *> hg(m->n_exp), hu(m->n_exp), hd(m->n_exp);
+    for (int e = 0; e < m->n_exp; e++) {
+        hg[e] = static_cast<const uint8_t *>(m->gate[e]);
+        hu[e] = static_cast<const uint8_t *>(m->up[e]);
+        hd[e] = static_cast<const uint8_t *>(m->down[e]);
+        if (!c->w_gate0 && hg[e] && hu[e] && hd[e]) { c->w_gate0 = hg[e]; c->w_down0 = hd[e]; }
+    }
+    if (!c->w_gate0) { fail(ES_HIP_EINVAL, "no expert has weights"); delete c; return nullptr; }
+    for (int e = 0; e < m->n_exp; e++)   // experts without weights point at one that has them (they must not be routed)
+        if (!hg[e] || !hu[e] || !hd[e]) { hg[e] = hu[e] = c->w_gate0; hd[e] = c->w_down0; }
+    const int R = max_tokens * k, umax = std::min(m->n_exp, R), n = m->n, ff = m->ff;
+    const bool gu_mm = m->gate_type == ES_HIP_Q2_K || m->gate_type == ES_HIP_Q4_K || (m->gate_type == ES_HIP_Q6_K && (n / 256) % 2 == 0);
+    const bool dn_mm = m->down_type == ES_HIP_Q2_K || m->down_type == ES_HIP_Q4_K || (m->down_type == ES_HIP_Q6_K && (ff / 256) % 2 == 0);
+    c->gu_slot = gu_mm ? moe_ws_bytes(n, R, umax) : 0;
+    c->dn_slot = dn_mm ? moe_ws_bytes(ff, R, umax) : 0;
+    const size_t job = std::max(sizeof(MvJob), sizeof(esq::MmJob));
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off += align256(std::max<size_t>(bytes, 1)); return o; };
+    const size_t o_sel = take(sizeof(int) * R), o_w = take(sizeof(float) * R), o_tok = take(sizeof(int) * R),
+                 o_rowof = take(sizeof(int) * R), o_wv = take(sizeof(float) * R), o_kk = take(sizeof(int) * max_tokens),
+                 o_g = take(sizeof(void *) * m->n_exp), o_u = take(sizeof(void *) * m->n_exp), o_d = take(sizeof(void *) * m->n_exp),
+                 o_bgu = take(sizeof(float) * 2 * ff * (size_t)R), o_ha = take(c->hstride * R), o_bye = take(sizeof(float) * n * (size_t)R),
+                 o_guj = take(job * (2 * (size_t)umax + 1)), o_dnj = take(job * ((size_t)umax + 1)),
+                 o_gup = take(sizeof(esq::PrepJob) * (umax + 1)), o_dnp = take(sizeof(esq::PrepJob) * (umax + 1)),
+                 o_guw = take(c->gu_slot), o_dnw = take(c->dn_slot);
+    hipError_t e = hipMalloc(&c->buf, off);
+    if (e != hipSuccess) { hip_fail(e, "hipMalloc (MoE context)"); delete c; return nullptr; }
+    uint8_t *b = c->buf;
+    c->sel = reinterpret_cast<int *>(b + o_sel);
+    c->w = reinterpret_cast<float *>(b + o_w);
+    c->tok_of = reinterpret_cast<int *>(b + o_tok);
+    c->rowof = reinterpret_cast<int *>(b + o_rowof);
+    c->wv = reinterpret_cast<float *>(b + o_wv);
+    c->kk = reinterpret_cast<int *>(b + o_kk);
+    c->dgate = reinterpret_cast<const uint8_t **>(b + o_g);
+    c->dup = reinterpret_cast<const uint8_t **>(b + o_u);
+    c->ddown = reinterpret_cast<const uint8_t **>(b + o_d);
+    c->bgu = reinterpret_cast<float *>(b + o_bgu);
+    c->ha = b + o_ha;
+    c->bye = reinterpret_cast<float *>(b + o_bye);
+    c->gu_jobs = b + o_guj;
+    c->dn_jobs = b + o_dnj;
+    c->gu_prep = reinterpret_cast<esq::PrepJob *>(b + o_gup);
+    c->dn_prep = reinterpret_cast<esq::PrepJob *>(b + o_dnp);
+    c->gu_ws = gu_mm ? b + o_guw : nullptr;
+    c->dn_ws = dn_mm ? b + o_dnw : nullptr;
+    std::vector<int> kk(max_tokens, k);
+    if ((e = hipMemcpy(c->kk, kk.data(), sizeof(int) * max_tokens, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(c->dgate, hg.data(), sizeof(void *) * m->n_exp, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(c->dup, hu.data(), sizeof(void *) * m->n_exp, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(c->ddown, hd.data(), sizeof(void *) * m->n_exp, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemset(c->bye, 0, sizeof(float) * n)) != hipSuccess) {
+        hip_fail(e, "MoE context set-up");
+        (void)hipFree(c->buf);
+        delete c;
+        return nullptr;
+    }
+    return c;
+}
+
+void es_hip_moe_ctx_destroy(es_hip_moe_ctx *c) {
+    if (!c) return;
+    if (c->buf) (void)hipFree(c->buf);
+    delete c;
+}
+
+}  // extern "C"
+
+namespace {
+
+// one layer from a routing already in the context's sel / w (device), in stream order
+int moe_ctx_layer(es_hip_moe_ctx *c, int N, const void *x, size_t xstride, float *out, size_t ostride, hipStream_t s) {
+    const int R = N * c->k, umax = std::min(c->n_exp, R), n = c->n, ff = c->ff;
+    FmtInfo fg, fd;
+    fmt_info(c->gt, fg);
+    fmt_info(c->dt, fd);
+    const uint64_t xs = xstride ? xstride : (uint64_t)(n / fg.be) * fg.ab;
+    const double expect = (double)R / umax;   // choices per expert if every slot were used
+    MoeLaunch G, D;
+    if (int rc = moe_family(c, c->gt, ff, n, umax, 2, R, expect, c->w_gate0, static_cast<const uint8_t *>(x), c->tok_of, xs,
+                            c->bgu, 2 * (uint64_t)ff, c->gu_ws, G))
+        return rc;
+    if (int rc = moe_family(c, c->dt, n, ff, umax, 1, R, expect, c->w_down0, c->ha, nullptr, c->hstride, c->bye, (uint64_t)n,
+                            c->dn_ws, D))
+        return rc;
+    esq::MoeDevArgs a{};
+    a.sel = c->sel;
+    a.w = c->w;
+    a.ntok = N;
+    a.k = c->k;
+    a.n_exp = c->n_exp;
+    a.umax = umax;
+    a.ff = ff;
+    a.n = n;
+    a.gate = c->dgate;
+    a.up = c->dup;
+    a.down = c->ddown;
+    a.x = static_cast<const uint8_t *>(x);
+    a.xstride = xs;
+    a.hstride = c->hstride;
+    a.bgu = c->bgu;
+    a.ha = c->ha;
+    a.bye = c->bye;
+    a.tok_of = c->tok_of;
+    a.rowof = c->rowof;
+    a.wv = c->wv;
+    a.gu_jobs = c->gu_jobs;
+    a.dn_jobs = c->dn_jobs;
+    a.gu_prep = c->gu_prep;
+    a.dn_prep = c->dn_prep;
+    a.gu_ws = c->gu_ws;
+    a.dn_ws = c->dn_ws;
+    hipError_t e = esq::moe_group_build_launch(a, G.F, D.F, s);
+    if (e != hipSuccess) return hip_fail(e, "MoE grouping launch");
+    const int order = g_order.load();
+    auto run = [&](const MoeLaunch &M, uint32_t type, void *jobs, esq::PrepJob *prep) -> int {
+        if (M.F.kind == esq::MOE_FAM_MV) {
+            e = esq::mv_launch(M.L, static_cast<const MvJob *>(jobs), M.njobs, M.F.mv, order, s);
+            return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "MoE decode-kernel launch");
+        }
+        if ((e = esq::prep_launch(prep, M.nprep, M.F.pj, M.items, s)) != hipSuccess) return hip_fail(e, "MoE pre-pass launch");
+        e = esq::mm_launch((int)type, 128, M.bn, 8, static_cast<const esq::MmJob *>(jobs), M.njobs, M.F.mm, M.grid, order, s);
+        return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "MoE matrix-core launch");
+    };
+    if (int rc = run(G, c->gt, c->gu_jobs, c->gu_prep)) return rc;
+    if ((e = esq::moe_swiglu_launch(c->bgu, R, ff, c->h_q8k, c->ha, c->hstride, s)) != hipSuccess) return hip_fail(e, "SwiGLU launch");
+    if (int rc = run(D, c->dt, c->dn_jobs, c->dn_prep)) return rc;
+    e = esq::moe_combine_launch(c->bye, c->rowof, c->wv, c->kk, c->k, N, n, out, ostride ? ostride : (uint64_t)n, s);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "combine launch");
+}
+
+int moe_ctx_check(const es_hip_moe_ctx *c, int N, const void *x, const float *out, size_t ostride) {
+    if (!c) return fail(ES_HIP_EINVAL, "null MoE context");
+    if (N < 0 || N > c->max_tokens) return fail(ES_HIP_EINVAL, "N %d outside [0, %d]", N, c->max_tokens);
+    if (N > 0 && (!x || !out)) return fail(ES_HIP_EINVAL, "null activations or outputs");
+    if (N > 1 && ostride && ostride < (size_t)c->n) return fail(ES_HIP_EINVAL, "ostride %zu < n %d", ostride, c->n);
+    return ES_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int es_hip_moe_ctx_run_logits(es_hip_moe_ctx *c, int N, const float *logits, size_t lstride, int norm_topk, const void *x,
+                              size_t xstride, float *out, size_t ostride, int *sel_out, float *w_out, void *stream) {
+    if (int rc = need_device()) return rc;
+    if (int rc = moe_ctx_check(c, N, x, out, ostride)) return rc;
+    if (N == 0) return ES_HIP_OK;
+    if (!logits) return fail(ES_HIP_EINVAL, "null logits");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = esq::route_softmax_launch(logits, lstride ? lstride : (uint64_t)c->n_exp, N, c->n_exp, c->k, norm_topk,
+                                             c->sel, c->w, c->k, s);
+    if (e != hipSuccess) return hip_fail(e, "routing launch");
+    const size_t pairs = (size_t)N * c->k;
+    if (sel_out && (e = hipMemcpyAsync(sel_out, c->sel, pairs * sizeof(int), hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_fail(e, "routing copy");
+    if (w_out && (e = hipMemcpyAsync(w_out, c->w, pairs * sizeof(float), hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_fail(e, "routing copy");
+    return moe_ctx_layer(c, N, x, xstride, out, ostride, s);
+}
+
+int es_hip_moe_ctx_run(es_hip_moe_ctx *c, int N, const int *sel, const float *w, const void *x, size_t xstride, float *out,
+                       size_t ostride, void *stream) {
+    if (int rc = need_device()) return rc;
+    if (int rc = moe_ctx_check(c, N, x, out, ostride)) return rc;
+    if (N == 0) return ES_HIP_OK;
+    if (!sel || !w) return fail(ES_HIP_EINVAL, "null routing");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t pairs = (size_t)N * c->k;
+    hipError_t e;
+    if ((e = hipMemcpyAsync(c->sel, sel, pairs * sizeof(int), hipMemcpyDeviceToDevice, s)) != hipSuccess ||
+        (e = hipMemcpyAsync(c->w, w, pairs * sizeof(float), hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_fail(e, "routing copy");
+    return moe_ctx_layer(c, N, x, xstride, out, ostride, s);
 }
 
 }  // extern "C"

@@ -226,6 +226,9 @@ class Lib:
             ("es_hip_matvec_multi_dev", i, [u32, vp, i, i, i, vp, sz, i, vp, sz, vp]),
             ("es_hip_matvec_multi_dev_noalloc", i, [u32, vp, i, i, i, vp, sz, i, vp, sz, vp]),
             ("es_hip_dense_ffn_dev", i, [u32, vp, u32, vp, u32, vp, i, i, i, vp, sz, vp, vp, vp, sz, vp]),
+            ("es_hip_moe_ctx_create", vp, [vp, i, i]), ("es_hip_moe_ctx_destroy", None, [vp]),
+            ("es_hip_moe_ctx_run", i, [vp, i, vp, vp, vp, sz, vp, sz, vp]),
+            ("es_hip_moe_ctx_run_logits", i, [vp, i, vp, sz, i, vp, sz, vp, sz, vp, vp, vp]),
             ("es_hip_run_jobs", i, [vp, i, vp]),
             ("es_hip_plan_create", vp, [vp, i]), ("es_hip_plan_run", i, [vp, vp]), ("es_hip_plan_destroy", None, [vp]),
             ("es_hip_plan_time_ms", C.c_double, [vp, i, i, vp]),
@@ -410,6 +413,13 @@ class Lib:
             raise EsHipError(-2, self.last_error())
         return Plan(self, h, moe=True)
 
+    def moe_ctx(self, args: "MoeArgs", max_tokens: int, k: int) -> "MoeCtx":
+        """a device-routed MoE context for args' expert set (es_hip_moe_ctx_create); args' routing arrays are unused"""
+        h = self._L.es_hip_moe_ctx_create(C.byref(args.m), max_tokens, k)
+        if not h:
+            raise EsHipError(-2, self.last_error())
+        return MoeCtx(self, h, args)
+
     def step_time_ms(self, plans, moe_plans, warmup: int, iters: int, stream=None) -> float:
         """ms per iteration of: every plan in `plans`, then every MoE plan in `moe_plans`, timed with HIP events"""
         P = (C.c_void_p * max(len(plans), 1))(*[p.h for p in plans])
@@ -532,6 +542,29 @@ class MoeArgs:
     def c_args(self):
         return (C.byref(self.m), self.N, self.k.ctypes.data, self.sel.ctypes.data, self.w.ctypes.data, self.kmax)
 
+
+
+class MoeCtx:
+    """es_hip_moe_ctx: run(N, sel, w, x, xstride, out, ostride) with device routing arrays, or run_logits(...)"""
+
+    def __init__(self, lib: Lib, handle, args):
+        self.lib, self.h, self.args = lib, handle, args   # args keeps the expert pointer arrays alive
+
+    def run(self, N, sel, w, x, xstride, out, ostride, stream=None):
+        self.lib._check(self.lib._L.es_hip_moe_ctx_run(self.h, N, int(sel), int(w), int(x), xstride, int(out), ostride, stream))
+
+    def run_logits(self, N, logits, lstride, norm_topk, x, xstride, out, ostride, sel_out=None, w_out=None, stream=None):
+        L = self.lib
+        L._check(L._L.es_hip_moe_ctx_run_logits(self.h, N, int(logits), lstride, int(norm_topk), int(x), xstride, int(out),
+                                                ostride, L._ptr(sel_out), L._ptr(w_out), stream))
+
+    def close(self):
+        if self.h:
+            self.lib._L.es_hip_moe_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 class Plan:
