@@ -76,7 +76,7 @@ int         es_hip_set_order(int order);     /* select the epilogue order; retur
 int         es_hip_get_order(void);
 
 /* ---- format facts (reference src/es_quant.h:24-26, 48-49; src/es_quant.c:39-73) ------------------------------------- */
-int    es_hip_quant_supported(uint32_t type);   /* 1 for the five formats above */
+int    es_hip_quant_supported(uint32_t type);   /* 1 for the eight formats above */
 size_t es_hip_row_bytes(uint32_t type, int cols);
 
 /* ---- device memory helpers (plumbing for callers without their own HIP allocator) ---------------------------------- */
@@ -141,7 +141,12 @@ int es_hip_unregister(const void *host);
 /* es_matvec / es_matvec_multi (src/es_quant.h:44-47): host W, host activations (a->q80 for Q4_0/Q5_0/Q8_0, a->q8 for the K-quants),
  * host y. Synchronous. The scratch argument is unused (kept for the prototype). They clear es_hip_last_error() on entry;
  * on failure y is left untouched and es_hip_last_error() says why (the reference's void prototype has no other error
- * channel). */
+ * channel). Row length limit (every product entry point): at most ES_HIP_MAX_COLS_32 columns for the 32-element formats
+ * (Q4_0, Q5_0, Q8_0) and ES_HIP_MAX_COLS_256 for the K-quants; a longer row is refused with ES_HIP_EINVAL (the decode
+ * kernel splits a row over at most 8 waves of one block group each), where the reference takes any multiple of the block
+ * size. */
+#define ES_HIP_MAX_COLS_32 16384
+#define ES_HIP_MAX_COLS_256 32768
 void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch);
 void es_hip_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
                          size_t ystride, float *scratch);

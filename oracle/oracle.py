@@ -49,7 +49,8 @@ class Oracle:
     """The CPU restatement (esq_oracle.c)."""
 
     def __init__(self, path: str | None = None):
-        path = path or os.path.join(HERE, "liboracle.so")
+        # ESQ_ORACLE_LIB: another build of the oracle (the sanitizer build of the CPU sanitizer test)
+        path = path or os.environ.get("ESQ_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
         if not os.path.exists(path):
             raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
         L = self.lib = C.CDLL(path)

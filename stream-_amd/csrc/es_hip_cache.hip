@@ -103,9 +103,15 @@ int load(es_hip_cache *c, int slot, size_t offset, const void *host, size_t byte
     return ES_HIP_OK;
 }
 
-// a slot whose expert could not be loaded is emptied, so it can never be found holding partial bytes
+// a slot whose expert could not be loaded is emptied, so it can never be found holding partial bytes; copies of its
+// earlier parts still in flight are waited for first (a reload into the slot, perhaps on another stream, must not be
+// overwritten by them)
 void unmap(es_hip_cache *c, int slot) {
     es_hip_cache::Slot &s = c->slots[slot];
+    if (s.pending) {
+        (void)hipEventSynchronize(s.ev);
+        s.pending = false;
+    }
     if (s.layer >= 0) c->where[(size_t)s.layer * c->nexperts + s.expert] = -1;
     s.layer = s.expert = -1;
     s.state = ES_HIP_SLOT_EMPTY;

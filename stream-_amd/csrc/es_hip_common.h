@@ -9,7 +9,7 @@ namespace esq {
 
 constexpr int WAVE = 64;
 
-// Block geometry of the five formats (reference src/es_quant.c:11-19, src/es_q2k.h:24-38):
+// Block geometry of the eight formats (reference src/es_quant.c:11-19, src/es_q2k.h:24-38):
 //   BE elements per block, BB bytes per block, AB bytes of the matching activation block (Q8_0 36, Q8_K 292),
 //   LPB lanes that share one block in the decode kernels.
 template <int F> struct Fmt;

@@ -143,7 +143,10 @@ int check_req(const Req &q, const FmtInfo &f) {
     if ((q.na > 1 || q.arow) && q.astride < packed) return fail(ES_HIP_EINVAL, "activation stride %zu < %zu bytes of one activation", q.astride, packed);
     if (q.na > 1 && q.ystride < (size_t)q.r1) return fail(ES_HIP_EINVAL, "ystride %zu < r1 %d: outputs of activations overlap", q.ystride, q.r1);
     const int slots = 64 / f.lpb, nbk = q.cols / f.be;
-    if (nbk > 8 * slots) return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this kernel handles", q.type, q.cols, 8 * slots * f.be);   // 8 waves x one segment each
+    static_assert(8 * 64 * 32 == ES_HIP_MAX_COLS_32 && 8 * 16 * 256 == ES_HIP_MAX_COLS_256, "the header's row limits");
+    if (nbk > 8 * slots)   // 8 waves x one block group each
+        return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this library handles (ES_HIP_MAX_COLS_*)", q.type, q.cols,
+                    8 * slots * f.be);
     if ((long)q.na * nbk * 73 > (1L << 30)) return fail(ES_HIP_EINVAL, "%d activations of %d columns: above 2^30 words per product", q.na, q.cols);
     return ES_HIP_OK;
 }
@@ -336,6 +339,8 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 bool mm_eligible(const Req &q) {
     const int mn = q.type == ES_HIP_Q6_K ? g_mm6_min.load() : q.type == ES_HIP_Q2_K ? g_mm2_min.load() : g_mm_min.load();
     if (q.type == ES_HIP_Q6_K && (q.cols / 256) % 2) return false;   // rows must be 4-byte aligned
+    // the Q2_K kernel addresses its weights with 32-bit offsets from row 0 of the matrix
+    if (q.type == ES_HIP_Q2_K && (size_t)q.r1 * (size_t)(q.cols / 256) * 84 + 64 >= ((size_t)1 << 32)) return false;
     return (q.type == ES_HIP_Q4_K || q.type == ES_HIP_Q6_K || q.type == ES_HIP_Q2_K) && mn > 0 && q.na >= mn && !q.ints &&
            q.r1 > q.r0;
 }

@@ -14,7 +14,8 @@ import weakref
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libes_hip_quant.so")
+# ES_HIP_LIB: another build of the same library (the host-sanitizer build of the CPU sanitizer test)
+LIB_PATH = os.environ.get("ES_HIP_LIB") or os.path.join(HERE, "libes_hip_quant.so")
 
 Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 2, 6, 8, 10, 11, 12, 13, 14
 TYPES = {"Q4_0": Q4_0, "Q5_0": Q5_0, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}

@@ -44,7 +44,8 @@ def test_no_other_c_symbols_exported():
     stray = []
     for line in os.popen(f"nm -D --defined-only {E.LIB_PATH}").read().splitlines():
         parts = line.split()
-        if len(parts) != 3 or parts[2].startswith(("_Z", "__hip_cuid_", "_init", "_fini", "_edata", "_end", "__bss")):
+        if len(parts) != 3 or parts[2].startswith(("_Z", "__hip_cuid_", "_init", "_fini", "_edata", "_end", "__bss",
+                                                   "__odr_asan", "__asan")):   # (the last two: sanitizer builds)
             continue
         if parts[2] not in declared:
             stray.append(parts[2])

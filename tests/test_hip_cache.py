@@ -165,3 +165,24 @@ def test_pinned_host_slabs(hip, orc):
         assert [c.slot_info(int(s)).expert for s in slots] == [3, 1]
     finally:
         c.close()
+
+
+def test_failed_part_empties_the_slot_after_its_copies(hip, orc):
+    """an expert whose second part cannot be read (no base pointer) leaves its slot EMPTY, and only after the first part's
+    copy has landed: the next expert acquired into that slot holds its own bytes, nothing of the failed load"""
+    slabs = make_slabs(orc, 1, 3, 31)
+    good = src_of(slabs[0])
+    bad = src_of(slabs[0])
+    bad.base[1] = None
+    c = E.ExpertCache(hip, 1, sum(part_bytes()), 1, 3, 0.0)
+    try:
+        with pytest.raises(E.EsHipError):
+            c.acquire(0, np.array([0], np.int32), bad)
+        assert c.slot_info(0).layer == -1 and c.find(0, 0) == -1
+        c.step()
+        for s in c.acquire(0, np.array([1], np.int32), good):
+            c.wait(int(s))
+        check_resident(hip, c, slabs, 1)
+        assert c.slot_info(0).expert == 1
+    finally:
+        c.close()

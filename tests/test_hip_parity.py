@@ -284,3 +284,34 @@ def test_matvec_q2_K_drop_in(hip, golden):
             assert np.array_equal(bits(y2[3:]), bits(golden["Q2_K/mtest_y_scalar"][0][3:])) and np.all(y2[:3] == 0)
     finally:
         hip.set_order(E.ORDER_X86_CONTRACT)
+
+
+@pytest.mark.parametrize("F", ["Q8_0", "Q4_0", "Q4_K", "Q2_K"])
+def test_longest_rows_and_the_limit(hip, orc, F):
+    """the longest rows the library takes (ES_HIP_MAX_COLS_32 = 16384 columns for the 32-element formats, 32768 for the
+    K-quants) match the oracle at one and several activations; one block more is refused with EINVAL, y untouched, on the
+    device path and the host drop-in (whose void prototype reports through es_hip_last_error)"""
+    t = O.TYPES[F]
+    cmax = 16384 if O.BLOCK_ELEMS[t] == 32 else 32768
+    rows = 48
+    W, acts = mtest_inputs(orc, t, rows, cmax, 3, 99 + t)
+    y = hip.matvec_multi(t, W, cmax, rows, acts)
+    assert np.array_equal(bits(y), bits(orc.matvec_multi(t, W, cmax, rows, acts)))
+    y1 = hip.matvec_multi(t, W, cmax, rows, acts[:1])
+    assert np.array_equal(bits(y1[0]), bits(y[0]))
+    c = cmax + O.BLOCK_ELEMS[t]
+    nbk = c // O.BLOCK_ELEMS[t]
+    dW, dA = hip.alloc(4 * E.row_bytes(t, c)), hip.alloc(nbk * E.ACT_BYTES[t])
+    dY = hip.upload(np.full(4, -5.0, np.float32))
+    with pytest.raises(E.EsHipError) as ei:
+        hip.matvec_multi_dev(t, dW, c, 0, 4, dA, 0, 1, dY, 0)
+    assert "above" in str(ei.value)
+    assert np.all(hip.download(dY, np.zeros(4, np.float32)) == -5.0)
+    for b in (dW, dA, dY):
+        b.close()
+    Wh = np.zeros(4 * E.row_bytes(t, c), np.uint8)
+    ah = np.zeros((1, nbk * E.ACT_BYTES[t]), np.uint8)
+    yh = np.full((1, 4), -5.0, np.float32)
+    with pytest.raises(E.EsHipError):   # the host drop-in: void, the error in es_hip_last_error
+        hip.host_matvec_multi(t, Wh, c, 0, 4, ah, yh)
+    assert np.all(yh == -5.0)
