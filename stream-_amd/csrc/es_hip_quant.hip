@@ -338,7 +338,6 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 bool mm_eligible(const Req &q) {
     const int mn = q.type == ES_HIP_Q6_K ? g_mm6_min.load() : q.type == ES_HIP_Q2_K ? g_mm2_min.load() : g_mm_min.load();
-    if (q.type == ES_HIP_Q6_K && (q.cols / 256) % 2) return false;   // rows must be 4-byte aligned
     // the Q2_K kernel addresses its weights with 32-bit offsets from row 0 of the matrix
     if (q.type == ES_HIP_Q2_K && (size_t)q.r1 * (size_t)(q.cols / 256) * 84 + 64 >= ((size_t)1 << 32)) return false;
     return (q.type == ES_HIP_Q4_K || q.type == ES_HIP_Q6_K || q.type == ES_HIP_Q2_K) && mn > 0 && q.na >= mn && !q.ints &&
@@ -1589,8 +1588,8 @@ es_hip_moe_ctx *es_hip_moe_ctx_create(const es_hip_moe *m, int max_tokens, int k
     for (int e = 0; e < m->n_exp; e++)   // experts without weights point at one that has them (they must not be routed)
         if (!hg[e] || !hu[e] || !hd[e]) { hg[e] = hu[e] = c->w_gate0; hd[e] = c->w_down0; }
     const int R = max_tokens * k, umax = std::min(m->n_exp, R), n = m->n, ff = m->ff;
-    const bool gu_mm = m->gate_type == ES_HIP_Q2_K || m->gate_type == ES_HIP_Q4_K || (m->gate_type == ES_HIP_Q6_K && (n / 256) % 2 == 0);
-    const bool dn_mm = m->down_type == ES_HIP_Q2_K || m->down_type == ES_HIP_Q4_K || (m->down_type == ES_HIP_Q6_K && (ff / 256) % 2 == 0);
+    const bool gu_mm = m->gate_type == ES_HIP_Q2_K || m->gate_type == ES_HIP_Q4_K || m->gate_type == ES_HIP_Q6_K;
+    const bool dn_mm = m->down_type == ES_HIP_Q2_K || m->down_type == ES_HIP_Q4_K || m->down_type == ES_HIP_Q6_K;
     c->gu_slot = gu_mm ? moe_ws_bytes(n, R, umax) : 0;
     c->dn_slot = dn_mm ? moe_ws_bytes(ff, R, umax) : 0;
     const size_t job = std::max(sizeof(MvJob), sizeof(esq::MmJob));

@@ -1,7 +1,7 @@
 """GPU parity of the Q6_K matrix-core path (es_hip_mm6.hip): bit-identical to the oracle in every reference order and to
 the vector kernel, at the config 3 head shape and at ragged edges (rows not a multiple of the 128-row tile, activation
-counts between the 16/32/64-wide tiles and above 64, row sub-ranges, padded strides), plus the vector fallback for rows
-with an odd number of superblocks (2-byte aligned rows)."""
+counts between the 16/32/64-wide tiles and above 64, row sub-ranges, padded strides), and rows of an odd number of
+superblocks (2-byte aligned rows)."""
 import numpy as np
 import pytest
 
@@ -89,13 +89,17 @@ def test_q6k_mfma_row_range_and_strides(hip6, orc):
     assert np.all(y[:, :r0] == sentinel) and np.all(y[:, r1:rows] == sentinel) and np.all(y[:, rows:] == sentinel)
 
 
-def test_q6k_odd_superblock_rows_use_the_vector_kernel(hip6, orc):
-    """768 columns: 630-byte rows, only 2-byte aligned; the product stays on the vector kernel and is still exact"""
-    rows, cols, na = 200, 768, 40
-    W, acts = inputs(orc, rows, cols, na, 77)
+@pytest.mark.parametrize("cols,na", [(768, 40), (256, 17), (1280, 64), (768, 130)])
+def test_q6k_odd_superblock_rows_on_the_matrix_cores(hip6, orc, cols, na):
+    """an odd number of superblocks: 210-byte blocks make every other row start 2 bytes past a dword (config 5's
+    2048 x 768 down experts); the matrix-core kernel reads them at that alignment and stays exact against the oracle
+    and the vector kernel"""
+    rows = 200
+    W, acts = inputs(orc, rows, cols, na, 77 + cols)
     y = hip6.matvec_multi(O.Q6_K, W, cols, rows, acts)
-    ref = orc.matvec_multi(O.Q6_K, W, cols, rows, acts[[0, 39]])
-    assert np.array_equal(bits(y[[0, 39]]), bits(ref))
+    ref = orc.matvec_multi(O.Q6_K, W, cols, rows, acts[[0, na // 2, na - 1]])
+    assert np.array_equal(bits(y[[0, na // 2, na - 1]]), bits(ref))
+    assert np.array_equal(bits(y), bits(vector_path(hip6, lambda: hip6.matvec_multi(O.Q6_K, W, cols, rows, acts))))
 
 
 def test_q6k_mfma_extreme_codes(hip6, orc):
