@@ -136,6 +136,12 @@ def route_topk(rng, n_tok, n_exp, k, norm_topk):
     return sel, w
 
 
+def moe_rng(config):
+    """each MoE workload's own generator: the same routing (and so the same experts and counts, which move the layer time
+    by over 10%) whether the workload runs alone (--only) or after the others"""
+    return np.random.default_rng(20260100 + config)
+
+
 class MoeWorkload:
     """`copies` copies of one MoE layer (experts in device memory) with one routing of N tokens, one MoE plan per copy, and
     optionally the attention products of the same tokens (one job-batch plan per copy). A step runs every copy once."""
@@ -438,7 +444,7 @@ def dense_ffn_time(lib, rng, K, Wm, T=512, n=2048, ff=8192):
             "workload": f"dense_n T={T}: gate/up {ff}x{n} + SwiGLU/Q8_K + down {n}x{ff}, Q4_K, three dependent steps"}
 
 
-def only(lib, rng, name, K, Wm):
+def only(lib, rng, name, K, Wm, moe_leg="both"):
     """one workload of the bench, alone: the command profiler summaries are taken from"""
     if name == "copy":   # a plain device copy of known size, the reference for HBM byte counters
         n = 1 << 30
@@ -458,12 +464,14 @@ def only(lib, rng, name, K, Wm):
         return {"workload": "cache", "pageable": cache_load_rate(lib, rng, K, Wm),
                 "pinned": cache_load_rate(lib, rng, K, Wm, pinned=True)}
     if name in ("config4", "config5"):
-        w = (MoeWorkload(lib, rng, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8) if name == "config4" else
-             MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
+        w = (MoeWorkload(lib, moe_rng(4), (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8) if name == "config4" else
+             MoeWorkload(lib, moe_rng(5), (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
                          attn=((4096, 2048), (512, 2048), (512, 2048))))
-        ms = w.time(Wm, K)
-        out = {"workload": name, "ms_per_layer": round(ms, 4), "weight_bytes_per_layer": w.weight_bytes // w.copies,
-               "device_routed_ms_per_layer": round(w.time_device_routed(Wm, K), 4)}
+        out = {"workload": name, "weight_bytes_per_layer": w.weight_bytes // w.copies}
+        if moe_leg in ("both", "plan"):
+            out["ms_per_layer"] = round(w.time(Wm, K), 4)
+        if moe_leg in ("both", "device"):
+            out["device_routed_ms_per_layer"] = round(w.time_device_routed(Wm, K), 4)
         w.close()
         return out
     if name.startswith("decode_"):   # config 2's decode in another weight format (same shapes, same 38 layer copies)
@@ -490,6 +498,8 @@ def main():
     ap.add_argument("--only", choices=["decode", "prefill", "dense", "config1", "config3b1", "config3b64", "config4", "config5", "act",
                                        "cache", "copy"] + [f"decode_{f.lower()}" for f in E.TYPES],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
+    ap.add_argument("--moe-leg", choices=["both", "plan", "device"], default="both",
+                    help="with --only config4/config5: time the prepared plan, the device-routed context, or both")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the path shards by output rows or by "
@@ -502,7 +512,7 @@ def main():
     rng = np.random.default_rng(20260101)
     K, Wm = args.steps, args.warmup
     if args.only:
-        print(json.dumps(only(lib, rng, args.only, K, Wm)), flush=True)
+        print(json.dumps(only(lib, rng, args.only, K, Wm, args.moe_leg)), flush=True)
         return
 
     # ---- headline: config 2 decode, Q4_K, T=1, 1.08 GB rotating set
@@ -537,7 +547,7 @@ def main():
         c3.close()
 
     # ---- config 4: OLMoE Q2_K experts (64 x gate/up 1024x2048, down 2048x1024), 128 tokens top-8; 8 layer copies
-    c4 = MoeWorkload(lib, rng, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8)
+    c4 = MoeWorkload(lib, moe_rng(4), (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8)
     e4 = c4.time(Wm, max(3, K // 2))
     d4 = c4.time_device_routed(Wm, max(3, K // 2))
     extra["config4_q2_k_moe"] = {"gbs": round(c4.weight_bytes / c4.copies / (e4 * 1e-3) / 1e9, 1), "ms": round(e4, 4),
@@ -547,7 +557,7 @@ def main():
     c4.close()
     # ---- config 5: Qwen3-30B-A3B-like decode batch of 32: Q5_0 attention q/k/v + 128 experts (Q4_K gate/up 768x2048,
     # Q6_K down 2048x768) top-8 renormalised; 3 layer copies
-    c5 = MoeWorkload(lib, rng, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
+    c5 = MoeWorkload(lib, moe_rng(5), (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True, 3,
                      attn=((4096, 2048), (512, 2048), (512, 2048)))
     e5 = c5.time(Wm, max(3, K // 2))
     d5 = c5.time_device_routed(Wm, max(3, K // 2))
