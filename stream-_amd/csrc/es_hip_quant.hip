@@ -1482,7 +1482,7 @@ struct MoeLaunch {
     long items = 0;                               // pre-pass item upper bound (MM)
 };
 
-int moe_family(es_hip_moe_ctx *c, uint32_t type, int rows, int cols, int umax, int njob, int R, double expect,
+int moe_family(es_hip_moe_ctx *c, uint32_t type, int rows, int cols, int umax, int njob, int R, double expect, int maxc,
                const uint8_t *w0, const uint8_t *act, const int *arow, uint64_t astride, float *y, uint64_t ystride,
                uint8_t *ws, MoeLaunch &M) {
     FmtInfo f;
@@ -1522,9 +1522,12 @@ int moe_family(es_hip_moe_ctx *c, uint32_t type, int rows, int cols, int umax, i
         return ES_HIP_OK;
     }
     // the decode kernel, sized as the planner sizes umax * njob products of about `expect` activations each (the sizing
-    // depends on the shapes only: kept per context)
+    // depends on the shapes only: kept per context). The activations per pass cover the counts routing can produce: an
+    // expert takes at most maxc (the layer's tokens) and usually a few more than the mean, so the planner's four-wide pass
+    // whenever three or more are possible (sized at the mean, 32 tokens over 128 experts ran two-wide passes and lost
+    // 11.6 us per layer re-reading the weights of the experts above it)
     M.F.kind = esq::MOE_FAM_MV;
-    const int na = std::max(1, (int)std::ceil(expect));
+    const int na = std::min(std::max(1, maxc), std::max(4, (int)std::ceil(expect)));
     const std::array<int, 6> key{(int)type, rows, cols, umax, njob, na};
     auto it = c->mv_cache.find(key);
     if (it == c->mv_cache.end()) {
@@ -1656,10 +1659,10 @@ int moe_ctx_layer(es_hip_moe_ctx *c, int N, const void *x, size_t xstride, float
     const uint64_t xs = xstride ? xstride : (uint64_t)(n / fg.be) * fg.ab;
     const double expect = (double)R / umax;   // choices per expert if every slot were used
     MoeLaunch G, D;
-    if (int rc = moe_family(c, c->gt, ff, n, umax, 2, R, expect, c->w_gate0, static_cast<const uint8_t *>(x), c->tok_of, xs,
+    if (int rc = moe_family(c, c->gt, ff, n, umax, 2, R, expect, N, c->w_gate0, static_cast<const uint8_t *>(x), c->tok_of, xs,
                             c->bgu, 2 * (uint64_t)ff, c->gu_ws, G))
         return rc;
-    if (int rc = moe_family(c, c->dt, n, ff, umax, 1, R, expect, c->w_down0, c->ha, nullptr, c->hstride, c->bye, (uint64_t)n,
+    if (int rc = moe_family(c, c->dt, n, ff, umax, 1, R, expect, N, c->w_down0, c->ha, nullptr, c->hstride, c->bye, (uint64_t)n,
                             c->dn_ws, D))
         return rc;
     esq::MoeDevArgs a{};
