@@ -86,6 +86,11 @@ __global__ __launch_bounds__(256) void act_prep_plain(const float *__restrict__ 
 __global__ __launch_bounds__(256) void act_prep_swiglu(const float *__restrict__ gu, uint64_t gs, int ff, float *h, uint64_t hs,
                                                        uint8_t *q80, uint64_t q80s, uint8_t *q8k, uint64_t q8ks) {
     __shared__ float wmax[4];
+    __shared__ uint64_t tab[32];   // expf's table in LDS: its load goes out beside the row's
+    {
+        static constexpr uint64_t T[32] = ESQ_EXPF_TABLE;
+        if (threadIdx.x < 32) tab[threadIdx.x] = T[threadIdx.x];
+    }
     const int r = blockIdx.y, c0 = blockIdx.x * CHUNKS;
     const float *g = gu + (size_t)r * gs;
     float gv[CHUNKS], uv[CHUNKS];
@@ -95,6 +100,7 @@ __global__ __launch_bounds__(256) void act_prep_swiglu(const float *__restrict__
         gv[c] = e < ff ? g[e] : 0.0f;
         uv[c] = e < ff ? g[ff + e] : 0.0f;
     }
+    __syncthreads();
     const QuantOut o{q80 ? q80 + (size_t)r * q80s : nullptr, q8k ? q8k + (size_t)r * q8ks : nullptr};
 #pragma unroll
     for (int c = 0; c < CHUNKS; c++) {
@@ -103,7 +109,7 @@ __global__ __launch_bounds__(256) void act_prep_swiglu(const float *__restrict__
         const bool have = e < ff;
         float v = 0.0f;
         if (have) {
-            v = gv[c] / (1.0f + esq_expf(-gv[c])) * uv[c];
+            v = gv[c] / (1.0f + esq_expf_tab(-gv[c], tab)) * uv[c];
             if (h) h[(size_t)r * hs + e] = v;
         }
         quant_chunk(v, have, e0, o, wmax);

@@ -22,17 +22,19 @@
 #define ESQ_EXPF_QUAL __device__ __forceinline__
 #endif
 
-ESQ_EXPF_QUAL float esq_expf(float x) {
-    // T[i] = bits(2^(i/32)) - (i << 47)
-    static constexpr uint64_t T[32] = {
-        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+// T[i] = bits(2^(i/32)) - (i << 47)
+#define ESQ_EXPF_TABLE                                                                         \
+    {0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull, \
+     0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull, \
+     0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull, \
+     0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull, \
+     0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull, \
+     0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull, \
+     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull, \
+     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull}
+
+// the routine with its table passed in (a kernel may keep a copy in LDS): T is indexed as T[i]
+template <typename TAB> ESQ_EXPF_QUAL float esq_expf_tab(float x, const TAB &T) {
     if (x != x) return x + x;
     if (x > 0x1.62e42ep6f) return __builtin_inff();   // > log(2^128)
     if (x < -0x1.9fe368p6f) return 0.0f;              // < log(2^-150)
@@ -44,11 +46,16 @@ ESQ_EXPF_QUAL float esq_expf(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    const double s = __builtin_bit_cast(double, T[ki % 32] + (ki << 47));
+    const double s = __builtin_bit_cast(double, (uint64_t)T[ki % 32] + (ki << 47));
     const double z = __builtin_fma(C0, r, C1), r2 = r * r;
     double y = __builtin_fma(C2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return static_cast<float>(y * s);
+}
+
+ESQ_EXPF_QUAL float esq_expf(float x) {
+    static constexpr uint64_t T[32] = ESQ_EXPF_TABLE;
+    return esq_expf_tab(x, T);
 }
 
 #endif

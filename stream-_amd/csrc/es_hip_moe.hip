@@ -11,14 +11,36 @@
 
 namespace esq {
 
+// A workgroup barrier that orders LDS only: every wave's LDS accesses before it are complete, and nothing waits for the
+// wave's global loads and stores (no wave of these kernels reads global memory another wave of it wrote).
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + esq_expf(-g)) * u; }
+template <typename TAB> __device__ __forceinline__ float swiglu_tab(float g, float u, const TAB &T) {
+    return g / (1.0f + esq_expf_tab(-g, T)) * u;
+}
+// expf's table copied into LDS by the first 32 threads, its load issued beside the kernel's own (the caller synchronises
+// before the first expf)
+#define ESQ_EXPF_LDS_TABLE(tab, i)                    \
+    __shared__ uint64_t tab[32];                      \
+    {                                                 \
+        static constexpr uint64_t T_[32] = ESQ_EXPF_TABLE; \
+        if ((i) < 32) tab[(i)] = T_[(i)];             \
+    }
 
 // One workgroup of 256 threads per (pair row, 256-wide block): h, amax, the Q8_K block (d, qs, bsums).
 __global__ __launch_bounds__(256) void swiglu_q8k(const float *__restrict__ gu, int ff, uint8_t *__restrict__ ha,
                                                    uint64_t hstride) {
     const int r = blockIdx.y, b = blockIdx.x, i = threadIdx.x;
+    ESQ_EXPF_LDS_TABLE(tab, i)
     const float *g = gu + (size_t)r * 2 * ff + (size_t)b * 256;
-    const float h = swiglu(g[i], g[ff + i]);
+    const float gv = g[i], uv = g[ff + i];
+    __syncthreads();
+    const float h = swiglu_tab(gv, uv, tab);
     __shared__ float wmax[4];
     float a = __builtin_fabsf(h);
     for (int o = 32; o > 0; o >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, o));   // max is exact in any order
@@ -43,9 +65,11 @@ __global__ __launch_bounds__(256) void swiglu_q8k(const float *__restrict__ gu, 
 __global__ __launch_bounds__(256) void swiglu_q80(const float *__restrict__ gu, int ff, uint8_t *__restrict__ ha,
                                                    uint64_t hstride) {
     const int r = blockIdx.y, i = threadIdx.x, e = blockIdx.x * 256 + i;
+    ESQ_EXPF_LDS_TABLE(tab, i)
+    __syncthreads();
     if (e >= ff) return;   // ff is a multiple of 32: whole blocks drop out together
     const float *g = gu + (size_t)r * 2 * ff;
-    const float h = swiglu(g[e], g[ff + e]);
+    const float h = swiglu_tab(g[e], g[ff + e], tab);
     float a = __builtin_fabsf(h);
     for (int o = 16; o > 0; o >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, o, 32));
     const float d = a / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
@@ -69,60 +93,157 @@ __global__ __launch_bounds__(256) void moe_combine(const float *__restrict__ ye,
 }
 
 // route() for softmax gating (src/es_engine.c:744-835, the GATE_SOFTMAX path: no gate bias, selection bias, expert groups,
-// cache bonus or top-k override): one wave per token. The maximum and every argmax are exact in any order (ties go to the
-// lowest expert, as the reference's first-maximum scan does); the two sums (softmax denominator over the experts, chosen
-// weights over the picks) run on one lane in the reference's order.
+// cache bonus or top-k override): one wave per token. The maximum is exact in any order; the two sums (softmax
+// denominator over the experts, chosen weights over the picks) run in the reference's order.
+//
+// The k picks: each lane keeps the best of its own untaken experts (e = l + 64 m); per pick the wave takes the largest
+// value (probabilities are non-negative, so their bits order as the values do), then the lowest expert holding it (the
+// reference's first-maximum scan), and only the lane that owned the pick rescans its experts. Both reductions are DPP
+// moves within the wave (no LDS). A probability that is NaN (only from a NaN or infinite logit) takes the reference's
+// scan order instead, one comparison per expert as it writes it.
+constexpr int ROUTE_PER_LANE = ROUTE_MAX_EXPERTS / 64;
+
+// the wave's maximum (MAX) or minimum of v in every lane: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror
+// (each row of 16 holds its own), row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3; lane 63 is read out
+template <bool MAX, int CTRL, int ROW_MASK> __device__ __forceinline__ uint32_t dpp_step(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
+    return MAX ? (o > v ? o : v) : (o < v ? o : v);
+}
+template <bool MAX> __device__ __forceinline__ uint32_t wave_reduce(uint32_t v) {
+    v = dpp_step<MAX, 0xB1, 0xF>(v);
+    v = dpp_step<MAX, 0x4E, 0xF>(v);
+    v = dpp_step<MAX, 0x141, 0xF>(v);
+    v = dpp_step<MAX, 0x140, 0xF>(v);
+    v = dpp_step<MAX, 0x142, 0xA>(v);
+    v = dpp_step<MAX, 0x143, 0xC>(v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+// the same for a float maximum that skips NaN as the reference's mx = r[e] > mx ? r[e] : mx does
+template <int CTRL, int ROW_MASK> __device__ __forceinline__ float dpp_fmax(float v) {
+    const float o = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+    return o > v ? o : v;
+}
+__device__ __forceinline__ float wave_fmax(float v) {
+    v = dpp_fmax<0xB1, 0xF>(v);
+    v = dpp_fmax<0x4E, 0xF>(v);
+    v = dpp_fmax<0x141, 0xF>(v);
+    v = dpp_fmax<0x140, 0xF>(v);
+    v = dpp_fmax<0x142, 0xA>(v);
+    v = dpp_fmax<0x143, 0xC>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __global__ __launch_bounds__(64) void route_softmax(const float *__restrict__ logits, uint64_t ls, int ne, int k, int norm_topk,
                                                     int *__restrict__ sel, float *__restrict__ w, int kmax) {
-    __shared__ float p[ROUTE_MAX_EXPERTS];
+    __shared__ __align__(16) float p[ROUTE_MAX_EXPERTS];
+    __shared__ uint64_t tab[32];
     __shared__ float total;
+    static constexpr uint64_t T[32] = ESQ_EXPF_TABLE;
     const int t = blockIdx.x, l = threadIdx.x;
+    const int mc = (ne + 63) >> 6;   // experts per lane, wave-uniform
+    if (l < 32) tab[l] = T[l];      // expf's table in LDS: its load overlaps the logits'
     const float *r = logits + (size_t)t * ls;
+    float v[ROUTE_PER_LANE];
     float mx = -__builtin_inff();
-    for (int e = l; e < ne; e += 64) {
-        const float v = r[e];
-        p[e] = v;
-        mx = v > mx ? v : mx;   // mx = r[e] > mx ? r[e] : mx (:753)
+#pragma unroll
+    for (int m = 0; m < ROUTE_PER_LANE; m++) {
+        if (m >= mc) break;
+        const int e = l + 64 * m;
+        v[m] = e < ne ? r[e] : -__builtin_inff();
+        mx = v[m] > mx ? v[m] : mx;   // mx = r[e] > mx ? r[e] : mx (:753)
     }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float m = __shfl_xor(mx, o);
-        mx = m > mx ? m : mx;
+    mx = wave_fmax(mx);
+    lds_sync();   // the table
+#pragma unroll
+    for (int m = 0; m < ROUTE_PER_LANE; m++) {
+        if (m >= mc) break;
+        const int e = l + 64 * m;
+        if (e < ne) p[e] = esq_expf_tab(v[m] - mx, tab);
     }
-    for (int e = l; e < ne; e += 64) p[e] = esq_expf(p[e] - mx);
-    __syncthreads();
-    if (l == 0) {
+    lds_sync();
+    if (l == 0) {   // :754, in expert order: 32 values per batch of LDS reads
         float sum = 0.0f;
-        for (int e = 0; e < ne; e++) sum += p[e];   // :754, in expert order
+        int e = 0;
+        for (; e + 32 <= ne; e += 32) {
+            float4 q[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[i] = *reinterpret_cast<const float4 *>(&p[e + 4 * i]);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                sum += q[i].x;
+                sum += q[i].y;
+                sum += q[i].z;
+                sum += q[i].w;
+            }
+        }
+        for (; e < ne; e++) sum += p[e];
         total = sum;
     }
-    __syncthreads();
+    lds_sync();
     const float sum = total;
-    for (int e = l; e < ne; e += 64) p[e] /= sum;   // :755
-    __syncthreads();
-    // k rounds of argmax over the experts not yet taken (:794-804); taken experts are marked in a lane's own bit mask
-    uint32_t taken = 0;   // bit m: expert l + 64 m (ne <= 1024: 16 per lane)
+    bool nan = false;
+#pragma unroll
+    for (int m = 0; m < ROUTE_PER_LANE; m++) {
+        if (m >= mc) break;
+        const int e = l + 64 * m;
+        if (e < ne) {
+            const float q = p[e] / sum;   // :755
+            p[e] = q;
+            v[m] = q;
+            nan = nan || q != q;
+        }
+    }
+    uint32_t taken = 0;   // bit m: expert l + 64 m
     float wsum = 0.0f, wj = 0.0f;
-    for (int j = 0; j < k; j++) {
-        float bv = 0.0f;
-        int be = -1;
-        for (int m = 0, e = l; e < ne; m++, e += 64) {
-            const float v = p[e];
-            if (!((taken >> m) & 1u) && (be < 0 || v > bv)) { bv = v; be = e; }
-        }
-        for (int o = 32; o > 0; o >>= 1) {   // the larger value, the lower expert on a tie; lanes without a candidate lose
-            const float ov = __shfl_xor(bv, o);
-            const int oe = __shfl_xor(be, o);
-            if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) { bv = ov; be = oe; }
-        }
-        if ((be & 63) == l) taken |= 1u << (be >> 6);
-        if (l == 0) {
-            sel[(size_t)t * kmax + j] = be;
+    int sj = 0;
+    if (__ballot(nan) == 0) {
+        uint32_t bvb = 0;   // this lane's best untaken value: its bits + 1 (0: none left)
+        int bve = 0xffff;   // and its expert (the lowest of that value)
+        auto rescan = [&]() {
+            bvb = 0;
+            bve = 0xffff;
+#pragma unroll
+            for (int m = 0; m < ROUTE_PER_LANE; m++) {
+                if (m >= mc) break;
+                const int e = l + 64 * m;
+                const uint32_t b = __float_as_uint(v[m]) + 1u;
+                if (e < ne && !((taken >> m) & 1u) && b > bvb) { bvb = b; bve = e; }
+            }
+        };
+        rescan();
+        for (int j = 0; j < k; j++) {
+            const uint32_t vmax = wave_reduce<true>(bvb);
+            const int be = (int)wave_reduce<false>(bvb == vmax ? (uint32_t)bve : 0xffffu);
+            const float bv = __uint_as_float(vmax - 1u);
+            if ((be & 63) == l) {   // the owner drops the pick and finds its next best
+                taken |= 1u << (be >> 6);
+                rescan();
+            }
             wsum += bv;   // w[j] = r[best]; wsum += w[j] (:802-803)
+            if (l == j) { wj = bv; sj = be; }
         }
-        if (l == j) wj = bv;
+        if (l < k) sel[(size_t)t * kmax + l] = sj;
+    } else {
+        lds_sync();
+        for (int j = 0; j < k; j++) {   // the reference's scan (:794-804), on one lane
+            if (l == 0) {
+                int be = -1;
+                for (int e = 0; e < ne; e++) {
+                    bool used = false;
+                    for (int i = 0; i < j; i++) used = used || sel[(size_t)t * kmax + i] == e;
+                    if (!used && (be < 0 || p[e] > p[be])) be = e;
+                }
+                sel[(size_t)t * kmax + j] = be;
+                wsum += p[be];
+                total = p[be];
+            }
+            lds_sync();
+            if (l == j) wj = total;
+            lds_sync();
+        }
     }
     if (l == 0) total = norm_topk ? (wsum > 6.103515625e-5f ? wsum : 6.103515625e-5f) : 1.0f;   // :832
-    __syncthreads();
+    lds_sync();
     if (l < k) w[(size_t)t * kmax + l] = norm_topk ? wj / total : wj;
 }
 
@@ -150,30 +271,35 @@ hipError_t moe_combine_launch(const float *ye, const int *rowof, const float *w,
 // ---- device-routed MoE: grouping and job tables --------------------------------------------------------------------
 namespace {
 
-// Exclusive prefix sums of three values per thread of the block (MOE_GROUP_THREADS threads, 16 waves): shuffles within
-// each wave, then the 16 wave totals on one wave. tot receives the three sums.
+// Inclusive prefix sum over the wave's 64 lanes by DPP moves: row_shr 1, 2, 4, 8 (lanes shifted in from outside the row
+// add 0), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2 and 3.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+    return x;
+}
+
+// Exclusive prefix sums of three values per thread of the block (MOE_GROUP_THREADS threads, 16 waves): each wave's scan,
+// then the 16 wave totals scanned on one wave. tot receives the three sums.
 __device__ int3 block_excl_scan3(int3 v, int3 *wsum, int3 *tot) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    int3 x = v;
-    for (int off = 1; off < 64; off <<= 1) {
-        const int a = __shfl_up(x.x, off), b = __shfl_up(x.y, off), c = __shfl_up(x.z, off);
-        if (lane >= off) { x.x += a; x.y += b; x.z += c; }
-    }
+    const int3 x = make_int3(wave_incl_scan(v.x), wave_incl_scan(v.y), wave_incl_scan(v.z));
     if (lane == 63) wsum[w] = x;
-    __syncthreads();
+    lds_sync();
     if (w == 0) {
         constexpr int NW = MOE_GROUP_THREADS / 64;
-        int3 y = lane < NW ? wsum[lane] : make_int3(0, 0, 0);
-        for (int off = 1; off < NW; off <<= 1) {
-            const int a = __shfl_up(y.x, off), b = __shfl_up(y.y, off), c = __shfl_up(y.z, off);
-            if (lane >= off) { y.x += a; y.y += b; y.z += c; }
-        }
+        const int3 y0 = lane < NW ? wsum[lane] : make_int3(0, 0, 0);
+        const int3 y = make_int3(wave_incl_scan(y0.x), wave_incl_scan(y0.y), wave_incl_scan(y0.z));
         if (lane < NW) wsum[lane] = y;
         if (lane == NW - 1) *tot = y;
     }
-    __syncthreads();
+    lds_sync();
     const int3 pre = w > 0 ? wsum[w - 1] : make_int3(0, 0, 0);
-    __syncthreads();   // wsum is reused by the next scan
+    lds_sync();   // wsum is reused by the next scan
     return make_int3(pre.x + x.x - v.x, pre.y + x.y - v.y, pre.z + x.z - v.z);
 }
 
@@ -181,25 +307,50 @@ __device__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // One workgroup: moe_n's grouping (src/es_engine.c:871-888) of the ntok * k choices, then every job of the layer's two
 // launches. Experts take slots in order of first use; an expert's rows follow its choices in (token, j) order.
-__global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeDevArgs A, MoeFamily GU, MoeFamily DN) {
+// The kernel's arguments as one block (its first and only parameter, at offset 0 of the argument segment).
+struct MoeBuildArgs {
+    MoeDevArgs A;
+    MoeFamily GU, DN;
+};
+static_assert(sizeof(MoeBuildArgs) % 4 == 0 && sizeof(MoeBuildArgs) / 4 <= MOE_GROUP_THREADS, "one dword per thread");
+
+__global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArgs P) {
     __shared__ int first[ROUTE_MAX_EXPERTS], cnt[ROUTE_MAX_EXPERTS], slot[ROUTE_MAX_EXPERTS], taken[ROUTE_MAX_EXPERTS];
     __shared__ int uex[ROUTE_MAX_EXPERTS], ustart[ROUTE_MAX_EXPERTS];
     __shared__ int wcnt[MOE_GROUP_THREADS / 64][ROUTE_MAX_EXPERTS];   // per wave of a chunk: choices of each expert
     __shared__ int3 wsum[MOE_GROUP_THREADS / 64];
     __shared__ int3 s_tot;
-    __shared__ int s_used;
-    const int tid = threadIdx.x, T = MOE_GROUP_THREADS, NE = A.n_exp, R = A.ntok * A.k;
+    __shared__ int wfl[MOE_GROUP_THREADS / 64];
+    __shared__ __align__(16) MoeBuildArgs sa;
+    __shared__ const uint8_t *pg[ROUTE_MAX_EXPERTS], *pu[ROUTE_MAX_EXPERTS], *pd[ROUTE_MAX_EXPERTS];
+    const int tid = threadIdx.x, T = MOE_GROUP_THREADS, NE = P.A.n_exp, R = P.A.ntok * P.A.k;
+    const int lane = tid & 63, wv = tid >> 6;
+    constexpr int NW = MOE_GROUP_THREADS / 64;
+    const uint64_t lt = (1ull << lane) - 1;
     // the first chunk's choices and weights, loaded before anything waits on them
-    const int sel0 = tid < R ? A.sel[tid] : -1;
-    const float w0_ = tid < R ? A.w[tid] : 0.0f;
-    if (tid == 0) s_used = 0;
+    const int sel0 = tid < R ? P.A.sel[tid] : -1;
+    const float w0_ = tid < R ? P.A.w[tid] : 0.0f;
+    // the arguments into LDS, one dword per thread through vector loads (read as plain scalars, the two families'
+    // templates would be loaded in several dependent rounds where the job tables use them), and the experts' matrix
+    // pointers: all of these loads are in flight together
+    const uint32_t arg = tid < (int)(sizeof(MoeBuildArgs) / 4)
+                             ? ((const uint32_t *)__builtin_amdgcn_kernarg_segment_ptr())[tid] : 0u;
+    const uint8_t *eg = tid < NE ? P.A.gate[tid] : nullptr, *eu = tid < NE ? P.A.up[tid] : nullptr,
+                  *ed = tid < NE ? P.A.down[tid] : nullptr;
     for (int e = tid; e < NE; e += T) {
         first[e] = R;
         cnt[e] = 0;
         taken[e] = 0;
         slot[e] = -1;
     }
-    __syncthreads();
+    if (tid < (int)(sizeof(MoeBuildArgs) / 4)) reinterpret_cast<uint32_t *>(&sa)[tid] = arg;
+    if (tid < NE) {
+        pg[tid] = eg;
+        pu[tid] = eu;
+        pd[tid] = ed;
+    }
+    const MoeDevArgs &A = P.A;   // pointers from the arguments themselves: the compiler knows them as global memory
+    lds_sync();
     for (int p = tid; p < R; p += T) {
         const int e = p < T ? sel0 : A.sel[p];
         if (e >= 0 && e < NE) {
@@ -207,28 +358,43 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeDevArgs 
             atomicAdd(&cnt[e], 1);
         }
     }
-    __syncthreads();
-    // slot of a used expert: the number of used experts first chosen before it (first uses are distinct choices)
-    for (int e = tid; e < NE; e += T)
-        if (first[e] < R) {
-            int r = 0;
-            for (int e2 = 0; e2 < NE; e2++) r += first[e2] < first[e];
-            slot[e] = r;
-            uex[r] = e;
-            atomicAdd(&s_used, 1);
+    lds_sync();
+    // slot of a used expert: the number of first uses before its own, a running count over the choices in order (one
+    // ballot per wave, then the wave totals)
+    int U = 0;
+    for (int c0 = 0; c0 < R; c0 += T) {
+        const int p = c0 + tid;
+        const int e0 = c0 == 0 ? sel0 : p < R ? A.sel[p] : -1;
+        const bool fu = p < R && e0 >= 0 && e0 < NE && first[e0] == p;
+        const uint64_t b = __ballot(fu);
+        if (lane == 0) wfl[wv] = __popcll(b);
+        lds_sync();
+        int before = U, total = U;
+#pragma unroll
+        for (int i = 0; i < NW; i++) {
+            const int x = wfl[i];
+            before += i < wv ? x : 0;
+            total += x;
         }
-    __syncthreads();
-    const int U = s_used;
-    const int c_me = tid < U ? cnt[uex[tid]] : 0;   // thread u: slot u's expert's count
+        if (fu) {
+            const int r = before + __popcll(b & lt);
+            slot[e0] = r;
+            uex[r] = e0;
+        }
+        U = total;
+        lds_sync();   // wfl is rewritten by the next chunk; slot and uex are complete
+    }
+    // slot u's expert and its matrices
+    const int ue = tid < U ? uex[tid] : 0;
+    const uint8_t *wgate = pg[ue], *wup = pu[ue], *wdown = pd[ue];
+    const int c_me = tid < U ? cnt[ue] : 0;   // thread u: slot u's expert's count
     const int st = block_excl_scan3(make_int3(c_me, 0, 0), wsum, &s_tot).x;
     if (tid < NE) ustart[tid] = st;
     // pair rows: the slot's first row + the choices of the same expert before this one, counted in chunks of one choice
     // per thread: earlier chunks (taken), earlier waves of the chunk (wcnt), earlier lanes of the wave (a match mask
     // from ballots over the expert id's bits)
-    const int lane = tid & 63, wv = tid >> 6;
-    const uint64_t lt = (1ull << lane) - 1;
     for (int c0 = 0; c0 < R; c0 += T) {
-        for (int i = tid; i < (T / 64) * NE; i += T) wcnt[i / NE][i % NE] = 0;
+        for (int i = tid; i < NW * NE; i += T) wcnt[i / NE][i % NE] = 0;
         const int p = c0 + tid;
         const int e0 = c0 == 0 ? sel0 : p < R ? A.sel[p] : -1;
         const int e = e0 >= 0 && e0 < NE ? e0 : -1;
@@ -237,9 +403,9 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeDevArgs 
             const uint64_t m = __ballot(e >= 0 && ((e >> b) & 1));
             same &= ((e >> b) & 1) ? m : ~m;
         }
-        __syncthreads();
+        lds_sync();
         if (e >= 0 && (same & lt) == 0) wcnt[wv][e] = __popcll(same);   // the wave's first lane with e
-        __syncthreads();
+        lds_sync();
         if (p < R) {
             int row = 0;
             float wt = 0.0f;
@@ -253,17 +419,17 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeDevArgs 
             A.rowof[p] = row;   // an invalid expert id contributes 0 * row 0
             A.wv[p] = wt;
         }
-        __syncthreads();
+        lds_sync();
         if (p < R && e >= 0 && (same & lt) == 0) atomicAdd(&taken[e], __popcll(same));
-        __syncthreads();
+        lds_sync();
     }
     // ---- job tables. Thread u writes slot u's jobs; tiles and pre-pass items are prefix sums over the slots.
     const int u = tid;
     const bool real = u < U;
-    const int e = real ? uex[u] : 0, c = real ? cnt[e] : 0, s0 = real ? ustart[u] : 0;
+    const int c = c_me, s0 = real ? ustart[u] : 0;
     const int ff = A.ff, n = A.n;
     for (int prod = 0; prod < 2; prod++) {   // 0: gate/up, 1: down
-        const MoeFamily &F = prod ? DN : GU;
+        const MoeFamily &F = prod ? sa.DN : sa.GU;
         const int njob = prod ? 1 : 2;
         int ntok = 0, tiles = 0, items = 0, units = 0;
         if (F.kind == MOE_FAM_MM && real) {
@@ -284,7 +450,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeDevArgs 
             w0 = sc.z;
         }
         const int t0 = tiles, i0 = items;
-        const uint8_t *const *wsrc = prod ? A.down : A.gate;
+        const uint8_t *wsrc = prod ? wdown : wgate;
         if (F.kind == MOE_FAM_MV) {
             MvJob *jobs = static_cast<MvJob *>(prod ? A.dn_jobs : A.gu_jobs);
             const int end = njob * U * F.mv_tiles;
@@ -292,7 +458,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeDevArgs 
                 for (int g = 0; g < njob; g++) {
                     MvJob J = F.mv;
                     if (real) {
-                        J.W = (g ? A.up : wsrc)[e];
+                        J.W = g ? wup : wsrc;
                         if (prod) {
                             J.act = A.ha + (size_t)s0 * A.hstride;
                             J.arow = nullptr;
@@ -343,7 +509,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeDevArgs 
                 for (int g = 0; g < njob; g++) {
                     MmJob J = F.mm;
                     if (real) {
-                        J.W = (g ? A.up : wsrc)[e];
+                        J.W = g ? wup : wsrc;
                         J.xq = xq;
                         J.xm = xm;
                         J.y = prod ? A.bye + (size_t)s0 * n : A.bgu + (size_t)s0 * 2 * ff + (size_t)g * ff;
@@ -373,14 +539,15 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeDevArgs 
                 jobs[njob * A.umax] = J;
             }
         }
-        __syncthreads();
+        lds_sync();
     }
 }
 
 }  // namespace
 
 hipError_t moe_group_build_launch(const MoeDevArgs &a, const MoeFamily &gu, const MoeFamily &dn, hipStream_t s) {
-    hipLaunchKernelGGL(moe_group_build, dim3(1), dim3(MOE_GROUP_THREADS), 0, s, a, gu, dn);
+    const MoeBuildArgs P{a, gu, dn};
+    hipLaunchKernelGGL(moe_group_build, dim3(1), dim3(MOE_GROUP_THREADS), 0, s, P);
     return hipGetLastError();
 }
 
