@@ -278,19 +278,29 @@ __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
 
 // The job of workgroup bid in a launch whose jobs hold consecutive tile ranges from tile0 (the last job with
 // tile0 <= bid). When the jobs are of equal size (an MoE layer's experts, copies of one matrix) the proportional guess
-// is that job, found in one round trip (its two bounds are independent loads); otherwise a binary search follows.
-template <typename JobT> __device__ __forceinline__ int find_tile_job(const JobT *jobs, int njobs, int bid) {
-    {
-        const int g = min(njobs - 1, static_cast<int>((static_cast<long>(bid) * njobs) / static_cast<long>(gridDim.x)));
-        const int a = jobs[g].tile0, b = g + 1 < njobs ? jobs[g + 1].tile0 : 0x7fffffff;
-        if (a <= bid && bid < b) return g;
-    }
+// is that job: the guessed job itself and the next job's tile0 are independent loads, so the job arrives in the same
+// round trip that checks it; otherwise a binary search and a second load follow.
+template <typename JobT> __device__ __forceinline__ JobT load_tile_job(const JobT *jobs, int njobs, int bid) {
+    static_assert(sizeof(JobT) % 8 == 0, "jobs are read as 8-byte pieces");
+    constexpr int N = sizeof(JobT) / 8;
+    const int g = min(njobs - 1, static_cast<int>((static_cast<long>(bid) * njobs) / static_cast<long>(gridDim.x)));
+    const int b = g + 1 < njobs ? jobs[g + 1].tile0 : 0x7fffffff;
+    uint64_t v[N];
+    const uint64_t *src = reinterpret_cast<const uint64_t *>(jobs + g);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = src[i];
+    // every piece is needed here, before the check: otherwise the compiler loads the guessed job's tile0 alone, checks
+    // it, and only then the rest of the job (a second round trip)
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" ::"s"(v[i]));
+    const JobT J = __builtin_bit_cast(JobT, v);
+    if (J.tile0 <= bid && bid < b) return J;
     int lo = 0, hi = njobs - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
         if (jobs[mid].tile0 <= bid) lo = mid; else hi = mid - 1;
     }
-    return lo;
+    return jobs[lo];
 }
 
 // One wave's 64 x 16 bytes from global memory straight into LDS: lane l's 16 bytes at base + off land at lds + 16*l

@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void mb32m_kernel(const MbJob *__restrict__ jo
     constexpr int BB = Fmt<F>::BB;
     static_assert(P % 2 == 0, "block parity is the stage's");
     MbJob J;
-    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = lane & 31, h = lane >> 5;

@@ -171,7 +171,7 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_q4k_kernel(const MkJob *_
     __shared__ __align__(16) uint8_t smem[2 * ST_BYTES];
 
     MkJob J;
-    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
     // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs (id % 8); all activation tiles of row tile rt go to
     // ids with id % 8 == rt % 8, so a row tile's weights are read into one XCD's L2. Each job's tiles start at a multiple

@@ -161,7 +161,7 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q4k_kernel(const MmJob *__res
     __shared__ __align__(16) uint8_t smem[G::LDS];
 
     MmJob J;
-    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
     // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs (id % 8), so all activation tiles of row tile rt
     // are given to ids with id % 8 == rt % 8 and the rows' weight blocks are read into a single XCD's L2. Each job's

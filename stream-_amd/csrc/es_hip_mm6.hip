@@ -51,7 +51,7 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
     __shared__ __align__(16) uint8_t smem[G::LDS];
 
     MmJob J;
-    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
     // XCD-aware tile order, as in the Q4_K kernel: all activation tiles of row tile rt on one XCD
     const int tile = blockIdx.x - J.tile0;

@@ -142,7 +142,7 @@ template <int F, int WN, bool CONTRACT>
 __global__ __launch_bounds__(256, 2) void mq_kernel(const MqJob *__restrict__ jobs, int njobs, MqJob single) {
     using M = Mq<F>;
     MqJob J;
-    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int lr = lane & 15, lg = lane >> 4;

@@ -515,7 +515,7 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
     constexpr int U = units<F, NT>();   // row passes whose raw loads a wave issues before using any of them
 
     MvJob J;
-    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
     const int nbk = J.cols / BE;
     const int tile = blockIdx.x - J.tile0;
@@ -732,7 +732,7 @@ __global__ __launch_bounds__(256) void mb32_kernel(const MbJob *__restrict__ job
     using L = Lane32<F>;
     constexpr int BB = Fmt<F>::BB, AB = Fmt<F>::AB;
     MbJob J;
-    if (jobs) J = jobs[find_tile_job(jobs, njobs, blockIdx.x)];
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rows_per_wave = 64 / J.ta;
