@@ -142,11 +142,10 @@ int es_hip_unregister(const void *host);
  * host y. Synchronous. The scratch argument is unused (kept for the prototype). They clear es_hip_last_error() on entry;
  * on failure y is left untouched and es_hip_last_error() says why (the reference's void prototype has no other error
  * channel). Row length limit (every product entry point): at most ES_HIP_MAX_COLS_32 columns for the 32-element formats
- * (Q4_0, Q5_0, Q8_0) and ES_HIP_MAX_COLS_256 for the K-quants; a longer row is refused with ES_HIP_EINVAL (the decode
- * kernel splits a row over at most 8 waves of one block group each), where the reference takes any multiple of the block
- * size. */
-#define ES_HIP_MAX_COLS_32 16384
-#define ES_HIP_MAX_COLS_256 32768
+ * (Q4_0, Q5_0, Q8_0) and ES_HIP_MAX_COLS_256 for the K-quants (one row's float terms stay in a workgroup's LDS in the decode
+ * kernel); a longer row is refused with ES_HIP_EINVAL, where the reference takes any multiple of the block size. */
+#define ES_HIP_MAX_COLS_32 131072
+#define ES_HIP_MAX_COLS_256 1048576
 void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch);
 void es_hip_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
                          size_t ystride, float *scratch);

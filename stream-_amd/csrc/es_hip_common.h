@@ -44,6 +44,7 @@ struct MvLaunch {
     int type, nt, waves;
     int grid;
     size_t lds;
+    bool seg_loop = false;   // some row of the launch needs more than `waves` block groups (each wave takes several)
 };
 hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s);
 

@@ -502,10 +502,11 @@ template <int F, int NT> constexpr int units() {
 
 // W waves per workgroup. A row of nbk blocks is cut into seg = ceil(nbk / slots) segments of `slots` blocks, one wave
 // each, so every lane keeps one fixed block position and its activation slice stays in registers; when seg < W the
-// W / seg wave groups take different rows. All waves write their blocks' float terms to the workgroup's LDS, then the
+// W / seg wave groups take different rows, and when seg > W each wave takes seg / W segments in turn (reloading its
+// activation slices for each). All waves write their blocks' float terms to the workgroup's LDS, then the
 // whole workgroup runs the per-row chains. order: ES_HIP_ORDER_*; NT activations per pass. One workgroup per tile
 // (rows_per_wg rows of one job).
-template <int F, int NT, int W>
+template <int F, int NT, int W, bool SEGLOOP>
 __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob *__restrict__ jobs, int njobs, MvJob single,
                                                                      int order) {
     using L = Lane<F>;
@@ -525,13 +526,16 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
 
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int slot = lane / LPB, k = lane % LPB;
-    int seg = 1;                                      // waves per row, a power of two (the planner keeps seg <= W)
+    int seg = 1;                                      // groups of SLOTS blocks per row, a power of two
     while (seg * SLOTS < nbk) seg <<= 1;
-    const int my_seg = wave % seg, rowgrp = wave / seg, nrowgrp = W / seg;
+    const int segw = seg < W ? seg : W;               // waves per row
+    const int spw = SEGLOOP ? seg / segw : 1;         // groups per wave: rows of more than W groups give each wave
+                                                      // groups my_seg, my_seg + W, ... in turn (SEGLOOP launches)
+    const int my_seg = wave % segw, rowgrp = wave / segw, nrowgrp = W / segw;
     int rpi, rowoff, b;
     if (nbk <= SLOTS) { rpi = SLOTS / nbk; rowoff = slot / nbk; b = slot % nbk; }
     else { rpi = 1; rowoff = 0; b = my_seg * SLOTS + slot; }
-    const bool live = rowoff < rpi && b < nbk;
+    bool live = rowoff < rpi && b < nbk;
     const int rstep = nrowgrp * rpi;                  // rows advanced by one pass of the whole workgroup
     const int rfirst = rowgrp * rpi + rowoff;
 
@@ -558,76 +562,86 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
     for (int t0 = 0; t0 < J.na; t0 += NT) {
         const int nt = min(NT, J.na - t0);
         typename L::Act act[NT];
+        auto load_acts = [&]() {   // the activation slices of this lane's block position b
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (live && t < nt) {
-                const int q = J.arow ? ldg<int>(J.arow + t0 + t) : t0 + t;
-                L::load_act(J.act + (size_t)q * J.astride + (size_t)b * AB, k, act[t]);
+            for (int t = 0; t < NT; t++) {
+                if (live && t < nt) {
+                    const int q = J.arow ? ldg<int>(J.arow + t0 + t) : t0 + t;
+                    L::load_act(J.act + (size_t)q * J.astride + (size_t)b * AB, k, act[t]);
+                }
+                else L::zero_act(act[t]);
             }
-            else L::zero_act(act[t]);
-        }
+        };
+        if (spw == 1) load_acts();
 
         for (int ra = ra0; ra < rend; ra += J.chain_rows) {
             const int rb = min(ra + J.chain_rows, rend);
-            // ---- phase 1: integers per block, float terms to LDS
-            for (int r0 = ra + rfirst; r0 - rowoff < rb; r0 += U * rstep) {
-                if (!pre) {
+            for (int si = 0; si < spw; si++) {
+                if (spw > 1) {   // the wave's next group of blocks: its block position and activation slices
+                    b = (my_seg + si * W) * SLOTS + slot;
+                    live = b < nbk;
+                    load_acts();
+                }
+                // ---- phase 1: integers per block, float terms to LDS
+                for (int r0 = ra + rfirst; r0 - rowoff < rb; r0 += U * rstep) {
+                    if (!pre) {
+#pragma unroll
+                        for (int u = 0; u < U; u++) {
+                            const int row = r0 + u * rstep;
+                            ok[u] = live && row < rb;
+                            L::load_raw(ok[u] ? J.W + (size_t)row * J.row_bytes + (size_t)b * BB : dummy, k, raw[u]);
+                        }
+                    }
+                    pre = false;
 #pragma unroll
                     for (int u = 0; u < U; u++) {
                         const int row = r0 + u * rstep;
-                        ok[u] = live && row < rb;
-                        L::load_raw(ok[u] ? J.W + (size_t)row * J.row_bytes + (size_t)b * BB : dummy, k, raw[u]);
-                    }
-                }
-                pre = false;
+                        typename L::Wt w;
+                        L::unpack(raw[u], k, w);
+                        typename L::Ints v[NT];
 #pragma unroll
-                for (int u = 0; u < U; u++) {
-                    const int row = r0 + u * rstep;
-                    typename L::Wt w;
-                    L::unpack(raw[u], k, w);
-                    typename L::Ints v[NT];
+                        for (int t = 0; t < NT; t++) {   // activations past nt (a uniform bound) are skipped
+                            if (t < nt) v[t] = ok[u] ? L::ints(w, act[t]) : typename L::Ints{};
+                            else v[t] = typename L::Ints{};
+                        }
+                        if constexpr (!W32) {
 #pragma unroll
-                    for (int t = 0; t < NT; t++) {   // activations past nt (a uniform bound) are skipped
-                        if (t < nt) v[t] = ok[u] ? L::ints(w, act[t]) : typename L::Ints{};
-                        else v[t] = typename L::Ints{};
-                    }
-                    if constexpr (!W32) {
+                            for (int t = 0; t < NT; t++)
+                                if (t < nt) { v[t].dot = group_sum<LPB>(v[t].dot); v[t].aux = group_sum<LPB>(v[t].aux); }
+                        }
+                        if (ok[u] && k == 0) {
+                            float *e = lds + ((size_t)(row - ra) * nbk + b) * NT * CW;
+                            if constexpr (W32) {
 #pragma unroll
-                        for (int t = 0; t < NT; t++)
-                            if (t < nt) { v[t].dot = group_sum<LPB>(v[t].dot); v[t].aux = group_sum<LPB>(v[t].aux); }
-                    }
-                    if (ok[u] && k == 0) {
-                        float *e = lds + ((size_t)(row - ra) * nbk + b) * NT * CW;
-                        if constexpr (W32) {
-#pragma unroll
-                            for (int t = 0; t < NT; t++) {
-                                if (t >= nt) continue;
-                                e[t * CW] = w.d * act[t].d;
-                                if (cmode == CH_LANES) {
-                                    for (int i = 0; i < 8; i++) e[t * CW + 1 + i] = static_cast<float>(v[t].lane[i]);
-                                } else {
-                                    int a = 0;
-                                    for (int i = 0; i < 8; i++) a += v[t].lane[i];
-                                    e[t * CW + 1] = static_cast<float>(a);
+                                for (int t = 0; t < NT; t++) {
+                                    if (t >= nt) continue;
+                                    e[t * CW] = w.d * act[t].d;
+                                    if (cmode == CH_LANES) {
+                                        for (int i = 0; i < 8; i++) e[t * CW + 1 + i] = static_cast<float>(v[t].lane[i]);
+                                    } else {
+                                        int a = 0;
+                                        for (int i = 0; i < 8; i++) a += v[t].lane[i];
+                                        e[t * CW + 1] = static_cast<float>(a);
+                                    }
                                 }
-                            }
-                            if (J.ints && t0 == 0) {
-                                int a = 0;
-                                for (int i = 0; i < 8; i++) a += v[0].lane[i];
-                                stg<int32_t>(J.ints + (size_t)row * nbk + b, a);
-                                stg<int32_t>(J.ints_aux + (size_t)row * nbk + b, 0);
-                            }
-                        } else {
+                                if (J.ints && t0 == 0) {
+                                    int a = 0;
+                                    for (int i = 0; i < 8; i++) a += v[0].lane[i];
+                                    stg<int32_t>(J.ints + (size_t)row * nbk + b, a);
+                                    stg<int32_t>(J.ints_aux + (size_t)row * nbk + b, 0);
+                                }
+                            } else {
 #pragma unroll
-                            for (int t = 0; t < NT; t++) {
-                                if (t >= nt) continue;
-                                const Term2 tm = L::term(w, act[t], v[t], contract);
-                                e[t * CW] = tm.a;
-                                e[t * CW + 1] = tm.b;
-                            }
-                            if (J.ints && t0 == 0) {
-                                stg<int32_t>(J.ints + (size_t)row * nbk + b, v[0].dot);
-                                stg<int32_t>(J.ints_aux + (size_t)row * nbk + b, v[0].aux);
+                                for (int t = 0; t < NT; t++) {
+                                    if (t >= nt) continue;
+                                    const Term2 tm = L::term(w, act[t], v[t], contract);
+                                    e[t * CW] = tm.a;
+                                    e[t * CW + 1] = tm.b;
+                                }
+                                if (J.ints && t0 == 0) {
+                                    stg<int32_t>(J.ints + (size_t)row * nbk + b, v[0].dot);
+                                    stg<int32_t>(J.ints_aux + (size_t)row * nbk + b, v[0].aux);
+                                }
                             }
                         }
                     }
@@ -681,18 +695,18 @@ namespace esq {
 using MvFn = void (*)(const MvJob *, int, MvJob, int);
 
 // Only the (NT, W) pairs the planner uses are instantiated.
-template <int F, int NT> static MvFn pick_w(int w) {
+template <int F, int NT> static MvFn pick_w(int w, bool seg_loop) {
     switch (w) {
-    case 4: return mv_kernel<F, NT, 4>;
-    case 8: return mv_kernel<F, NT, 8>;
+    case 4: return seg_loop ? nullptr : mv_kernel<F, NT, 4, false>;
+    case 8: return seg_loop ? mv_kernel<F, NT, 8, true> : mv_kernel<F, NT, 8, false>;
     }
     return nullptr;
 }
-template <int F> static MvFn pick_nt(int nt, int w) {
+template <int F> static MvFn pick_nt(int nt, int w, bool seg_loop) {
     switch (nt) {
-    case 1: return pick_w<F, 1>(w);
-    case 2: return pick_w<F, 2>(w);
-    case 4: return pick_w<F, 4>(w);
+    case 1: return pick_w<F, 1>(w, seg_loop);
+    case 2: return pick_w<F, 2>(w, seg_loop);
+    case 4: return pick_w<F, 4>(w, seg_loop);
     }
     return nullptr;
 }
@@ -700,14 +714,14 @@ template <int F> static MvFn pick_nt(int nt, int w) {
 hipError_t mv_launch(const MvLaunch &L, const MvJob *jobs, int njobs, const MvJob &single, int order, hipStream_t s) {
     MvFn fn = nullptr;
     switch (L.type) {
-    case ES_HIP_Q4_0: fn = pick_nt<ES_HIP_Q4_0>(L.nt, L.waves); break;
-    case ES_HIP_Q5_0: fn = pick_nt<ES_HIP_Q5_0>(L.nt, L.waves); break;
-    case ES_HIP_Q8_0: fn = pick_nt<ES_HIP_Q8_0>(L.nt, L.waves); break;
-    case ES_HIP_Q2_K: fn = pick_nt<ES_HIP_Q2_K>(L.nt, L.waves); break;
-    case ES_HIP_Q3_K: fn = pick_nt<ES_HIP_Q3_K>(L.nt, L.waves); break;
-    case ES_HIP_Q4_K: fn = pick_nt<ES_HIP_Q4_K>(L.nt, L.waves); break;
-    case ES_HIP_Q5_K: fn = pick_nt<ES_HIP_Q5_K>(L.nt, L.waves); break;
-    case ES_HIP_Q6_K: fn = pick_nt<ES_HIP_Q6_K>(L.nt, L.waves); break;
+    case ES_HIP_Q4_0: fn = pick_nt<ES_HIP_Q4_0>(L.nt, L.waves, L.seg_loop); break;
+    case ES_HIP_Q5_0: fn = pick_nt<ES_HIP_Q5_0>(L.nt, L.waves, L.seg_loop); break;
+    case ES_HIP_Q8_0: fn = pick_nt<ES_HIP_Q8_0>(L.nt, L.waves, L.seg_loop); break;
+    case ES_HIP_Q2_K: fn = pick_nt<ES_HIP_Q2_K>(L.nt, L.waves, L.seg_loop); break;
+    case ES_HIP_Q3_K: fn = pick_nt<ES_HIP_Q3_K>(L.nt, L.waves, L.seg_loop); break;
+    case ES_HIP_Q4_K: fn = pick_nt<ES_HIP_Q4_K>(L.nt, L.waves, L.seg_loop); break;
+    case ES_HIP_Q5_K: fn = pick_nt<ES_HIP_Q5_K>(L.nt, L.waves, L.seg_loop); break;
+    case ES_HIP_Q6_K: fn = pick_nt<ES_HIP_Q6_K>(L.nt, L.waves, L.seg_loop); break;
     }
     if (!fn) return hipErrorInvalidValue;
     if (L.lds > 64 * 1024) {

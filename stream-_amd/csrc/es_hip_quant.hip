@@ -142,11 +142,14 @@ int check_req(const Req &q, const FmtInfo &f) {
     const size_t packed = (size_t)(q.cols / f.be) * f.ab;
     if ((q.na > 1 || q.arow) && q.astride < packed) return fail(ES_HIP_EINVAL, "activation stride %zu < %zu bytes of one activation", q.astride, packed);
     if (q.na > 1 && q.ystride < (size_t)q.r1) return fail(ES_HIP_EINVAL, "ystride %zu < r1 %d: outputs of activations overlap", q.ystride, q.r1);
-    const int slots = 64 / f.lpb, nbk = q.cols / f.be;
-    static_assert(8 * 64 * 32 == ES_HIP_MAX_COLS_32 && 8 * 16 * 256 == ES_HIP_MAX_COLS_256, "the header's row limits");
-    if (nbk > 8 * slots)   // 8 waves x one block group each
-        return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this library handles (ES_HIP_MAX_COLS_*)", q.type, q.cols,
-                    8 * slots * f.be);
+    const int nbk = q.cols / f.be;
+    // the decode kernel keeps one row's float terms in LDS (at one activation per pass: 9 floats per block for the
+    // 32-element formats, 2 per superblock for the K-quants)
+    static_assert((size_t)ES_HIP_MAX_COLS_32 / 32 * 9 * 4 <= LDS_MAX && (size_t)ES_HIP_MAX_COLS_256 / 256 * 2 * 4 <= LDS_MAX,
+                  "the header's row limits fit one row's terms");
+    const int cmax = f.be == 32 ? ES_HIP_MAX_COLS_32 : ES_HIP_MAX_COLS_256;
+    if (q.cols > cmax)
+        return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this library handles (ES_HIP_MAX_COLS_*)", q.type, q.cols, cmax);
     if ((long)q.na * nbk * 73 > (1L << 30)) return fail(ES_HIP_EINVAL, "%d activations of %d columns: above 2^30 words per product", q.na, q.cols);
     return ES_HIP_OK;
 }
@@ -188,10 +191,15 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
         const bool w32 = f.be == 32;
         const int slots = 64 / f.lpb;
         const int waves = kv.first.second;
-        int max_na = 1;
-        for (const Req *q : kv.second) max_na = std::max(max_na, q->na);
-        const int nt = max_na >= 3 ? 4 : max_na;   // 3 activations in one pass of 4 rather than two passes of 2
         Group g;
+        int max_na = 1, max_nbk = 1;
+        for (const Req *q : kv.second) {
+            max_na = std::max(max_na, q->na);
+            max_nbk = std::max(max_nbk, q->cols / f.be);
+        }
+        g.L.seg_loop = segments(max_nbk, slots) > waves;
+        int nt = max_na >= 3 ? 4 : max_na;   // 3 activations in one pass of 4 rather than two passes of 2
+        while (nt > 1 && (size_t)max_nbk * nt * (w32 ? 9 : 2) * sizeof(float) > LDS_MAX) nt /= 2;   // one row's terms fit
         g.L.type = static_cast<int>(kv.first.first);
         g.L.nt = nt;
         g.L.waves = waves;
@@ -202,7 +210,7 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
             const int nbk = q->cols / f.be, rows = q->r1 - q->r0;
             const int rpi = nbk <= slots ? slots / nbk : 1;
             const int seg = segments(nbk, slots);
-            const int rstep = (waves / seg) * rpi;   // rows one pass of the workgroup covers
+            const int rstep = std::max(1, waves / seg) * rpi;   // rows one pass of the workgroup covers
             const size_t per_row = (size_t)nbk * nt * cw * sizeof(float);
             if (per_row > LDS_MAX) return fail(ES_HIP_EINVAL, "type %u cols %d: a row needs %zu bytes of LDS", q->type, q->cols, per_row);
             int chain_cap = (int)std::min<size_t>(CHAIN_MAX, std::max<size_t>(1, LDS_TARGET / per_row));

@@ -286,19 +286,28 @@ def test_matvec_q2_K_drop_in(hip, golden):
         hip.set_order(E.ORDER_X86_CONTRACT)
 
 
-@pytest.mark.parametrize("F", ["Q8_0", "Q4_0", "Q4_K", "Q2_K"])
-def test_longest_rows_and_the_limit(hip, orc, F):
-    """the longest rows the library takes (ES_HIP_MAX_COLS_32 = 16384 columns for the 32-element formats, 32768 for the
-    K-quants) match the oracle at one and several activations; one block more is refused with EINVAL, y untouched, on the
-    device path and the host drop-in (whose void prototype reports through es_hip_last_error)"""
+@pytest.mark.parametrize("F,cols", [("Q8_0", 28672), ("Q4_0", 28672), ("Q5_0", 29568), ("Q4_K", 53248), ("Q6_K", 28672),
+                                    ("Q2_K", 53248), ("Q8_0", 131072), ("Q4_0", 131072), ("Q4_K", 1048576), ("Q2_K", 1048576)])
+def test_long_rows(hip, orc, F, cols):
+    """rows longer than the decode kernel's 8 waves cover in one pass (each wave then takes several groups of blocks in
+    turn): Llama-3-70B's 28672-wide and Qwen2.5-72B's 29568-wide down projections, Llama-3.1-405B's 53248, and the longest
+    rows the library takes (ES_HIP_MAX_COLS_32 = 131072 columns, ES_HIP_MAX_COLS_256 = 1048576), against the oracle at one
+    and several activations"""
     t = O.TYPES[F]
-    cmax = 16384 if O.BLOCK_ELEMS[t] == 32 else 32768
-    rows = 48
-    W, acts = mtest_inputs(orc, t, rows, cmax, 3, 99 + t)
-    y = hip.matvec_multi(t, W, cmax, rows, acts)
-    assert np.array_equal(bits(y), bits(orc.matvec_multi(t, W, cmax, rows, acts)))
-    y1 = hip.matvec_multi(t, W, cmax, rows, acts[:1])
+    rows = 48 if cols < 131072 else 8
+    W, acts = mtest_inputs(orc, t, rows, cols, 3, 99 + t + cols)
+    y = hip.matvec_multi(t, W, cols, rows, acts)
+    assert np.array_equal(bits(y), bits(orc.matvec_multi(t, W, cols, rows, acts)))
+    y1 = hip.matvec_multi(t, W, cols, rows, acts[:1])
     assert np.array_equal(bits(y1[0]), bits(y[0]))
+
+
+@pytest.mark.parametrize("F", ["Q8_0", "Q4_0", "Q4_K", "Q2_K"])
+def test_row_limit(hip, orc, F):
+    """one block past the longest row the library takes is refused with EINVAL, y untouched, on the device path and the
+    host drop-in (whose void prototype reports through es_hip_last_error)"""
+    t = O.TYPES[F]
+    cmax = 131072 if O.BLOCK_ELEMS[t] == 32 else 1048576
     c = cmax + O.BLOCK_ELEMS[t]
     nbk = c // O.BLOCK_ELEMS[t]
     dW, dA = hip.alloc(4 * E.row_bytes(t, c)), hip.alloc(nbk * E.ACT_BYTES[t])
