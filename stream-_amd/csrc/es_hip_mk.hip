@@ -36,6 +36,11 @@
 // reference order (src/es_quant.c:1056-1080, 1324-1343, 1564-1602), so the outputs are bit-identical to the CPU kernels.
 // MFMA lane layouts (A: lane l holds row l%16, k 16*(l/16)..+15 for the i8 form and k 4*(l/16)..+3 for the f16 form;
 // D: lane l, register i holds D[4*(l/16)+i][l%16]) are those of the device, checked by the parity tests.
+//
+// Q5_K (src/es_quant.c:1153-1175): Q4_K's layout plus qh[32] after the scales, bit 2c (2c + 1) of qh[l] the fifth bit of
+// element l of sub-block 2c (2c + 1), so q = q4 + 16 q5. A third int8 plane q5 * sc (<= 63) goes through the matrix cores
+// and dot = D_lo + 8 D_hi + 16 D_q5, exact. Its epilogue is the reference's scalar mv_q5_K (the x86 build has no AVX2
+// Q5_K kernel and no FMA in it): s += y.d * (d * dot - dmin * mins) with every product and sum rounded, in every order.
 #include "es_hip_common.h"
 
 namespace esq {
@@ -70,18 +75,31 @@ static_assert(MK_TOK == 128, "the staging assignment below is written for 128 ac
 
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
-struct WRaw {   // this lane's fields of one row tile's superblock: header, qs chunks lg and lg + 4
+template <int F> struct MkFmt;
+template <> struct MkFmt<ES_HIP_Q4_K> { static constexpr int BB = 144, QS = 16, QH = -1; };
+template <> struct MkFmt<ES_HIP_Q5_K> { static constexpr int BB = 176, QS = 48, QH = 16; };
+
+template <int F> struct WRaw {   // this lane's fields of one row tile's superblock: header, qs chunks lg and lg + 4
     uint4 h, q0, q1;
 };
+template <> struct WRaw<ES_HIP_Q5_K> {   // ... and the qh bytes of its elements, 16 (lg & 1) .. + 15
+    uint4 h, q0, q1, qh;
+};
 
-struct BOps {   // one row tile's B operands for one superblock
+template <int F> struct BOps {   // one row tile's B operands for one superblock
     v4i lo[4], hi[4];
     v4h mn;
     float d, dm;
 };
+template <> struct BOps<ES_HIP_Q5_K> {
+    v4i lo[4], hi[4], q5[4];
+    v4h mn;
+    float d, dm;
+};
 
-// scale_min_k4 (src/es_quant.c:75-83) byte-parallel: the two int8 planes of the four slices and the mins operand
-__device__ __forceinline__ void build_b(const WRaw &w, int lg, BOps &B) {
+// scale_min_k4 (src/es_quant.c:75-83) byte-parallel: the two int8 planes of the four slices (three for Q5_K) and the
+// mins operand
+template <int F> __device__ __forceinline__ void build_b(const WRaw<F> &w, int lg, BOps<F> &B) {
     const uint4 h = w.h;
     const uint32_t sc0 = h.y & 0x3f3f3f3fu, sc1 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
     const uint32_t mn0 = h.z & 0x3f3f3f3fu, mn1 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
@@ -103,6 +121,17 @@ __device__ __forceinline__ void build_b(const WRaw &w, int lg, BOps &B) {
             B.lo[s][i] = (int)pk_mul_u16(nib, slw[s]);   // byte * scale <= 105: no carry between bytes
             B.hi[s][i] = (int)pk_mul_u16(nib, shw[s]);
         }
+    if constexpr (F == ES_HIP_Q5_K) {   // slice s takes sub-block j = 2 (lg >> 1) + 4 (s >> 1) + (s & 1): bit j of its qh bytes
+        const uint32_t scw[4] = {__builtin_amdgcn_perm(0, sc0, sel0), __builtin_amdgcn_perm(0, sc0, sel1),
+                                 __builtin_amdgcn_perm(0, sc1, sel0), __builtin_amdgcn_perm(0, sc1, sel1)};
+        const uint32_t hw[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const uint32_t j = 2 * (lg >> 1) + 4 * (s >> 1) + (s & 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) B.q5[s][i] = (int)pk_mul_u16((hw[i] >> j) & 0x01010101u, scw[s]);   // <= 63
+        }
+    }
     // mins operand: k positions 4lg .. 4lg+3 meet bsums 4lg .. 4lg+3, i.e. sub-blocks 2lg and 2lg+1, each twice. Each half
     // is built as 1024 + m (byte m under the exponent of 1024) and 1024 subtracted exactly.
     const uint32_t mw = lg < 2 ? mn0 : mn1, kb = 2u * (uint32_t)(lg & 1);
@@ -120,33 +149,40 @@ struct AOps {   // one activation tile's A operands for one superblock, and the 
     v4f yd;     // y.d of activations 4*lg .. 4*lg+3 of the tile
 };
 
-struct MAcc {   // the matrix-core results of one 16 x 16 tile and superblock
+template <int F> struct MAcc {   // the matrix-core results of one 16 x 16 tile and superblock
     v4i lo, hi;
     v4f mn;
 };
+template <> struct MAcc<ES_HIP_Q5_K> {
+    v4i lo, hi, q5;
+    v4f mn;
+};
 
-struct Pend {   // a tile's results waiting for their epilogue, with the scales of their superblock
-    MAcc m;
+template <int F> struct Pend {   // a tile's results waiting for their epilogue, with the scales of their superblock
+    MAcc<F> m;
     v4f yd;
     float d, dm;
 };
 
-__device__ __forceinline__ void mma(const AOps &a, const BOps &B, MAcc &m) {
+template <int F> __device__ __forceinline__ void mma(const AOps &a, const BOps<F> &B, MAcc<F> &m) {
     m.lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[0], B.lo[0], v4i{0, 0, 0, 0}, 0, 0, 0);
     m.hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[0], B.hi[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+    if constexpr (F == ES_HIP_Q5_K) m.q5 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[0], B.q5[0], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
     for (int s = 1; s < 4; s++) {
         m.lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[s], B.lo[s], m.lo, 0, 0, 0);
         m.hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[s], B.hi[s], m.hi, 0, 0, 0);
+        if constexpr (F == ES_HIP_Q5_K) m.q5 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[s], B.q5[s], m.q5, 0, 0, 0);
     }
     m.mn = __builtin_amdgcn_mfma_f32_16x16x16f16(a.bs, B.mn, v4f{0, 0, 0, 0}, 0, 0, 0);
 }
 
-template <bool CONTRACT>
-__device__ __forceinline__ void epilogue(const MAcc &m, float d, float dm, const v4f &yd, v4f &s) {
+template <int F, bool CONTRACT>
+__device__ __forceinline__ void epilogue(const MAcc<F> &m, float d, float dm, const v4f &yd, v4f &s) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int dot = m.lo[i] + 8 * m.hi[i];
+        int dot = m.lo[i] + 8 * m.hi[i];
+        if constexpr (F == ES_HIP_Q5_K) dot += 16 * m.q5[i];
         const float q = dm * m.mn[i];   // the mins are exact integers in the f32 accumulator
         if constexpr (CONTRACT)
             s[i] = __builtin_fmaf(yd[i], __builtin_fmaf(d, static_cast<float>(dot), -q), s[i]);
@@ -155,19 +191,21 @@ __device__ __forceinline__ void epilogue(const MAcc &m, float d, float dm, const
     }
 }
 
-// One tile step: 9 MFMAs interleaved with the step's vector work (the previous tile's epilogue) and the next tile's LDS
-// reads: 1 MFMA : 3 VALU : 1 LDS read.
-__device__ __forceinline__ void step_schedule() {
+// One tile step: 9 MFMAs (13 for Q5_K) interleaved with the step's vector work (the previous tile's epilogue) and the
+// next tile's LDS reads: 1 MFMA : 3 VALU : 1 LDS read.
+template <int NMFMA> __device__ __forceinline__ void step_schedule() {
 #pragma unroll
-    for (int k = 0; k < 9; k++) {
+    for (int k = 0; k < NMFMA; k++) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
         if (k < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
     }
 }
 
-template <bool CONTRACT, bool GATHER>
-__global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_q4k_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
+template <int F, bool CONTRACT, bool GATHER>
+__global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
+    using FM = MkFmt<F>;
+    constexpr bool FUSED = CONTRACT && F == ES_HIP_Q4_K;   // Q5_K's reference epilogue never fuses
     __shared__ __align__(16) uint8_t smem[2 * ST_BYTES];
 
     MkJob J;
@@ -238,11 +276,12 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_q4k_kernel(const MkJob *_
     // ---- this wave's weight rows (rows past the end repeat the last one; their results are not stored)
     const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
     const uint32_t woff = (uint32_t)min(16 * wave + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
-    auto wload = [&](int b, WRaw &W) {
-        const uint8_t *p = wbase + woff + 144u * (uint32_t)b;
+    auto wload = [&](int b, WRaw<F> &W) {
+        const uint8_t *p = wbase + woff + (uint32_t)FM::BB * (uint32_t)b;
         W.h = ldg<uint4>(p);
-        W.q0 = ldg<uint4>(p + 16 + 16 * lg);
-        W.q1 = ldg<uint4>(p + 80 + 16 * lg);
+        W.q0 = ldg<uint4>(p + FM::QS + 16 * lg);
+        W.q1 = ldg<uint4>(p + FM::QS + 64 + 16 * lg);
+        if constexpr (F == ES_HIP_Q5_K) W.qh = ldg<uint4>(p + FM::QH + 16 * (lg & 1));
     };
 
     // ---- A operand offsets in a slot: activation tile tt adds 16 rows (values), 16 * 8 (bsums), 64 (scales)
@@ -275,12 +314,12 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_q4k_kernel(const MkJob *_
     // A tile's epilogue runs two tile steps after its MFMAs (a step's vector work then never waits for the matrix cores),
     // across superblock boundaries: steps 0 and 1 of superblock b finish tiles 6 and 7 of superblock b - 1. The two
     // pending slots start as zeros (all scales 0), whose epilogues add +0 to the +0 of acc[6] and acc[7]: the same bits.
-    Pend p0, p1;   // the tiles two and one steps back
-    p0.m = MAcc{v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}, v4f{0, 0, 0, 0}};
+    Pend<F> p0, p1;   // the tiles two and one steps back
+    p0.m = MAcc<F>{};
     p0.yd = v4f{0, 0, 0, 0};
     p0.d = p0.dm = 0.f;
     p1 = p0;
-    WRaw W;
+    WRaw<F> W;
     stage_dma(0, 0);
     wload(0, W);
     bs_write(bs_load(0), 0);
@@ -288,8 +327,8 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_q4k_kernel(const MkJob *_
         const int sl = b & 1;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's copies into LDS (not tracked by the compiler)
         __syncthreads();
-        BOps B;
-        build_b(W, lg, B);
+        BOps<F> B;
+        build_b<F>(W, lg, B);
         const int bn = min(b + 1, nbk - 1);
         uint4 bsn;
         const uint32_t so = smem0 + (uint32_t)sl * ST_BYTES;
@@ -299,15 +338,15 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_q4k_kernel(const MkJob *_
 #pragma unroll
         for (int tt = 0; tt < MK_TT; tt++) {
             if (tt + 1 < MK_TT) aload(xa, ba, ya, tt + 1, A[(tt + 1) & 1]);
-            MAcc cur;
-            mma(A[tt & 1], B, cur);
-            epilogue<CONTRACT>(p0.m, p0.d, p0.dm, p0.yd, acc[(tt + MK_TT - 2) % MK_TT]);
+            MAcc<F> cur;
+            mma<F>(A[tt & 1], B, cur);
+            epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[(tt + MK_TT - 2) % MK_TT]);
             p0 = p1;
             p1.m = cur;
             p1.yd = A[tt & 1].yd;
             p1.d = B.d;
             p1.dm = B.dm;
-            step_schedule();
+            step_schedule<F == ES_HIP_Q5_K ? 13 : 9>();
             __builtin_amdgcn_sched_barrier(0);
             if (tt == 1) {
                 // the next load group, once this superblock's weights are unpacked (the first MFMAs used them)
@@ -319,8 +358,8 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_q4k_kernel(const MkJob *_
         }
         bs_write(bsn, 1 - sl);
     }
-    epilogue<CONTRACT>(p0.m, p0.d, p0.dm, p0.yd, acc[MK_TT - 2]);
-    epilogue<CONTRACT>(p1.m, p1.d, p1.dm, p1.yd, acc[MK_TT - 1]);
+    epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[MK_TT - 2]);
+    epilogue<F, FUSED>(p1.m, p1.d, p1.dm, p1.yd, acc[MK_TT - 1]);
 
     // ---- outputs: lane l, register i holds activation tok0 + 16 tt + 4 lg + i, row row0 + 16 wave + lr. Buffer stores
     // over y[0, (na - 1) * ystride + r1): the hardware's range check drops those of activations past na (ystride >= r1),
@@ -343,17 +382,25 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_q4k_kernel(const MkJob *_
 
 }  // namespace
 
+template <int F>
+static void mk_launch_fmt(bool gather, bool contract, const MkJob *jobs, int njobs, const MkJob &single, int grid,
+                          hipStream_t s) {
+    const dim3 g(grid), b(64 * MK_WAVES);
+    if (gather) {
+        if (contract) hipLaunchKernelGGL((mk_kernel<F, true, true>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mk_kernel<F, false, true>), g, b, 0, s, jobs, njobs, single);
+    } else {
+        if (contract) hipLaunchKernelGGL((mk_kernel<F, true, false>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mk_kernel<F, false, false>), g, b, 0, s, jobs, njobs, single);
+    }
+}
+
 hipError_t mk_launch(int type, bool gather, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
                      hipStream_t s) {
-    if (type != ES_HIP_Q4_K) return hipErrorInvalidValue;
     const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
-    if (gather) {
-        if (contract) hipLaunchKernelGGL((mk_q4k_kernel<true, true>), dim3(grid), dim3(64 * MK_WAVES), 0, s, jobs, njobs, single);
-        else hipLaunchKernelGGL((mk_q4k_kernel<false, true>), dim3(grid), dim3(64 * MK_WAVES), 0, s, jobs, njobs, single);
-    } else {
-        if (contract) hipLaunchKernelGGL((mk_q4k_kernel<true, false>), dim3(grid), dim3(64 * MK_WAVES), 0, s, jobs, njobs, single);
-        else hipLaunchKernelGGL((mk_q4k_kernel<false, false>), dim3(grid), dim3(64 * MK_WAVES), 0, s, jobs, njobs, single);
-    }
+    if (type == ES_HIP_Q4_K) mk_launch_fmt<ES_HIP_Q4_K>(gather, contract, jobs, njobs, single, grid, s);
+    else if (type == ES_HIP_Q5_K) mk_launch_fmt<ES_HIP_Q5_K>(gather, false, jobs, njobs, single, grid, s);   // never fused
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
