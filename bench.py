@@ -477,8 +477,9 @@ def only(lib, rng, name, K, Wm, moe_leg="both"):
     if name.startswith("decode_"):   # config 2's decode in another weight format (same shapes, same 38 layer copies)
         t = E.TYPES[name[len("decode_"):].upper()]
         mats, na, copies = [(t, r, c) for _, r, c in Q4K_FFN], 1, 38
-    elif name == "prefill_q5k":      # config 2's prefill with the weights in Q5_K
-        mats, na, copies = [(E.Q5_K, r, c) for _, r, c in Q4K_FFN], 512, 1
+    elif name in ("prefill_q5k", "prefill_q3k"):   # config 2's prefill with the weights in Q5_K / Q3_K
+        t = E.Q5_K if name == "prefill_q5k" else E.Q3_K
+        mats, na, copies = [(t, r, c) for _, r, c in Q4K_FFN], 512, 1
     else:
         mats, na, copies = {"decode": (Q4K_FFN, 1, 38), "prefill": (Q4K_FFN, 512, 1), "config1": ([(E.Q4_0, 4864, 896)], 1, 410),
                             "config3b1": ([(E.Q6_K, 151936, 1024)], 1, 8), "config3b64": ([(E.Q6_K, 151936, 1024)], 64, 8)}[name]
@@ -497,7 +498,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=2.0)
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill_q5k", "dense", "config1", "config3b1", "config3b64", "config4", "config5", "act",
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill_q5k", "prefill_q3k", "dense", "config1", "config3b1", "config3b64", "config4", "config5", "act",
                                        "cache", "copy"] + [f"decode_{f.lower()}" for f in E.TYPES],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     ap.add_argument("--moe-leg", choices=["both", "plan", "device"], default="both",
@@ -532,12 +533,13 @@ def main():
     pre.close()
 
     extra = {}
-    # ---- config 2 prefill with the weights in Q5_K (the matrix-core kernel's third plane), T=512
-    p5 = Workload(lib, rng, [(E.Q5_K, r, c) for _, r, c in Q4K_FFN], 512, 1)
-    _, p5ev = p5.time(Wm, max(3, K // 4))
-    p5tops = p5.ops / (p5ev * 1e-3) / 1e12
-    extra["prefill_q5k_t512"] = {"tops": round(p5tops, 2), "ms": round(p5ev, 4), "frac": round(p5tops / INT8_PEAK_TOPS, 4)}
-    p5.close()
+    # ---- config 2 prefill with the weights in Q5_K (the matrix-core kernel's third plane) and in Q3_K, T=512
+    for key, t in (("prefill_q5k_t512", E.Q5_K), ("prefill_q3k_t512", E.Q3_K)):
+        pk = Workload(lib, rng, [(t, r, c) for _, r, c in Q4K_FFN], 512, 1)
+        _, pkev = pk.time(Wm, max(3, K // 4))
+        pktops = pk.ops / (pkev * 1e-3) / 1e12
+        extra[key] = {"tops": round(pktops, 2), "ms": round(pkev, 4), "frac": round(pktops / INT8_PEAK_TOPS, 4)}
+        pk.close()
     # ---- config 2 dense_n on the device (gate/up, SwiGLU + Q8_K, down), T=512
     extra["config2_dense_ffn_t512"] = dense_ffn_time(lib, rng, max(3, K // 4), Wm)
     # ---- config 1: Q4_0 4864x896, b=1, 410 copies (1.0 GB)

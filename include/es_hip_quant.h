@@ -285,6 +285,10 @@ int es_hip_set_direct_mfma_min_tiles(int n);
  * plane for the fifth bit); below it, or with it off (n <= 0), on the vector kernel. Results are identical on both. Returns
  * the previous value. */
 int es_hip_set_q5k_mfma_min_batch(int n);
+/* Q3_K products with at least n activations (default 8) run on the direct-activation matrix-core kernel (two int8 planes of
+ * the signed codes against the split scales); below it, or with it off (n <= 0), on the vector kernel. Results are
+ * identical on both. Returns the previous value. */
+int es_hip_set_q3k_mfma_min_batch(int n);
 /* ---- activation preparation on the device ---------------------------------------------------------------------------
  * es_act_prepare (src/es_quant.c:499-512) for `rows` rows of `cols` fp32 values in device memory: q80 (when non-NULL;
  * cols % 32 == 0) receives cols/32 Q8_0 blocks per row exactly as quantize_q80 (src/es_quant.c:489-497) writes them, q8k

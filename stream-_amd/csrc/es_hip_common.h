@@ -225,6 +225,12 @@ template <typename T> __device__ __forceinline__ T ldg(const void *p) {   // 8- 
     else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, *(const ESQ_GLOBAL u32x2 *)p);
     else return *(const ESQ_GLOBAL T *)p;
 }
+// 16 bytes of global memory at a 2-byte aligned address (Q3_K and Q6_K superblocks: the hardware's unaligned access)
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+__device__ __forceinline__ uint4 ldg_u128_a2(const uint8_t *p) {
+    const u32x4_a2 v = *(const ESQ_GLOBAL u32x4_a2 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 template <typename T> __device__ __forceinline__ void stg(void *p, const T &v) {
     if constexpr (sizeof(T) == 16) *(ESQ_GLOBAL u32x4 *)p = __builtin_bit_cast(u32x4, v);
     else if constexpr (sizeof(T) == 8) *(ESQ_GLOBAL u32x2 *)p = __builtin_bit_cast(u32x2, v);

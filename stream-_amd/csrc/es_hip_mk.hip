@@ -1,5 +1,5 @@
-// Batched Q4_K products on the int8 matrix cores that read the activations' Q8_K rows directly (no pre-pass): the
-// prompt-reading form of es_matvec_multi (src/es_quant.c:1818-1850, 1564-1602) for Q4_K.
+// Batched Q4_K products (and Q5_K, Q3_K: below) on the int8 matrix cores that read the activations' Q8_K rows directly
+// (no pre-pass): the prompt-reading form of es_matvec_multi (src/es_quant.c:1818-1850, 1564-1602) for Q4_K.
 //
 // Work split. A workgroup of 4 waves computes MK_ROWS = 64 rows x MK_TOK = 128 activations; wave w takes the 16 rows
 // 16w .. 16w+15 and all 128 activations (eight 16-activation tiles), so a row tile's unpacked weights serve eight MFMA
@@ -41,6 +41,16 @@
 // element l of sub-block 2c (2c + 1), so q = q4 + 16 q5. A third int8 plane q5 * sc (<= 63) goes through the matrix cores
 // and dot = D_lo + 8 D_hi + 16 D_q5, exact. Its epilogue is the reference's scalar mv_q5_K (the x86 build has no AVX2
 // Q5_K kernel and no FMA in it): s += y.d * (d * dot - dmin * mins) with every product and sum rounded, in every order.
+//
+// Q3_K (src/es_quant.c:1120-1150, 1369-1395): 110-byte superblocks hmask[32] | qs[64] | scales[12] | d, 2-byte aligned,
+// read with unaligned 16-byte loads (the header as bytes 94..109: qs[62..63], the scales and d, so no load passes the
+// superblock's end). Group g = 8n + 2j + half holds the 16 elements v = ((qs[32n + 16 half + l] >> 2j) & 3) - 4 (plus 4
+// when bit 4n + j of hmask[16 half + l] is set), v in -4..3, with the scale sc_g = code_g - 32 in -32..31. Split
+// code = 8 h + l (h, l in 0..7): sc = l + 8 (h - 4), and v * l (-28..21) and v * (h - 4) (-12..16) both fit int8, so
+// tot = sum_g sc_g * sum v y = D_lo + 8 D_hi with no bsums term (the reference sums the codes against the values too).
+// Slice s and lane group lg take group g = 8 (lg >> 1) + 2 s + (lg & 1); the planes' bytes come from two 8-entry tables
+// per slice (v * l and v * (h - 4) for v + 4 = 0..7) through v_perm_b32, indexed by the 3-bit code v + 4. Epilogue: the
+// reference's s += y.d * d * tot (fused in the clang order).
 #include "es_hip_common.h"
 
 namespace esq {
@@ -78,12 +88,16 @@ typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 template <int F> struct MkFmt;
 template <> struct MkFmt<ES_HIP_Q4_K> { static constexpr int BB = 144, QS = 16, QH = -1; };
 template <> struct MkFmt<ES_HIP_Q5_K> { static constexpr int BB = 176, QS = 48, QH = 16; };
+template <> struct MkFmt<ES_HIP_Q3_K> { static constexpr int BB = 110, QS = 32, QH = 0; };
 
 template <int F> struct WRaw {   // this lane's fields of one row tile's superblock: header, qs chunks lg and lg + 4
     uint4 h, q0, q1;
 };
 template <> struct WRaw<ES_HIP_Q5_K> {   // ... and the qh bytes of its elements, 16 (lg & 1) .. + 15
     uint4 h, q0, q1, qh;
+};
+template <> struct WRaw<ES_HIP_Q3_K> {   // bytes 94..109 (qs[62..63] | scales | d), qs chunk lg, hmask chunk lg & 1
+    uint4 h, q, hm;
 };
 
 template <int F> struct BOps {   // one row tile's B operands for one superblock
@@ -94,6 +108,10 @@ template <int F> struct BOps {   // one row tile's B operands for one superblock
 template <> struct BOps<ES_HIP_Q5_K> {
     v4i lo[4], hi[4], q5[4];
     v4h mn;
+    float d, dm;
+};
+template <> struct BOps<ES_HIP_Q3_K> {   // dm unused (0)
+    v4i lo[4], hi[4];
     float d, dm;
 };
 
@@ -143,6 +161,41 @@ template <int F> __device__ __forceinline__ void build_b(const WRaw<F> &w, int l
     B.dm = half_bits_to_float(h.x >> 16);
 }
 
+// Q3_K: the two planes of every slice from the 3-bit codes c = v + 4 and per-slice tables (see the file comment)
+template <> __device__ __forceinline__ void build_b<ES_HIP_Q3_K>(const WRaw<ES_HIP_Q3_K> &w, int lg, BOps<ES_HIP_Q3_K> &B) {
+    const uint4 h = w.h;
+    const uint32_t n4 = 4u * (uint32_t)(lg >> 1), half8 = 8u * (uint32_t)(lg & 1);
+    // scale bytes 0-3, 4-7, 8-11 (bytes 2.. of the header load)
+    const uint32_t S0 = __builtin_amdgcn_alignbyte(h.y, h.x, 2), S1 = __builtin_amdgcn_alignbyte(h.z, h.y, 2),
+                   S2 = __builtin_amdgcn_alignbyte(h.w, h.z, 2);
+    // 6-bit codes of groups 8n + 4p + i, byte i of C[p]: nibble n of scales[4p + i], bits 4n + 2p of scales[8 + i]
+    // (src/es_quant.c:1125-1128); then the lane's two groups of each, bytes lg & 1 and 2 + (lg & 1), shifted down
+    const uint32_t hs = S2 >> n4;
+    const uint32_t C0 = (((S0 >> n4) & 0x0f0f0f0fu) | ((hs << 4) & 0x30303030u)) >> half8;
+    const uint32_t C1 = (((S1 >> n4) & 0x0f0f0f0fu) | ((hs << 2) & 0x30303030u)) >> half8;
+    const uint32_t hd[4] = {w.hm.x >> n4, w.hm.y >> n4, w.hm.z >> n4, w.hm.w >> n4};   // bit j of byte l: group 8n + 2j + half
+    const uint32_t qd[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        // slice s: group 8n + 2s + half, code byte 2 (s & 1) of C[s >> 1]: l = bits 0-2, h = bits 3-5
+        const uint32_t C = s < 2 ? C0 : C1, sh = 16u * (uint32_t)(s & 1);
+        const uint32_t cl = (C >> sh) & 7u, ch = (C >> (sh + 3)) & 7u;
+        // tables: byte c of (T1:T0) = (c - 4) * l, of (U1:U0) = (c - 4) * (h - 4); bytes are formed biased by 0x80 (every
+        // partial result stays in 0..255, no borrow between bytes) and the bias flipped back
+        const uint32_t T1 = cl * 0x03020100u, T0 = (0x80808080u - cl * 0x01020304u) ^ 0x80808080u;
+        const uint32_t U1 = (ch * 0x03020100u + 0x74787c80u) ^ 0x80808080u, U0 = (0x84888c90u - ch * 0x01020304u) ^ 0x80808080u;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t hb = s <= 2 ? hd[i] << (2 - s) : hd[i] >> 1;   // the high bit to bit 2 of each byte
+            const uint32_t c = ((qd[i] >> (2 * s)) & 0x03030303u) | (hb & 0x04040404u);
+            B.lo[s][i] = (int)__builtin_amdgcn_perm(T1, T0, c);
+            B.hi[s][i] = (int)__builtin_amdgcn_perm(U1, U0, c);
+        }
+    }
+    B.d = half_bits_to_float(h.w >> 16);
+    B.dm = 0.f;
+}
+
 struct AOps {   // one activation tile's A operands for one superblock, and the tile's activation scales
     v4i x[4];
     v4h bs;
@@ -156,6 +209,9 @@ template <int F> struct MAcc {   // the matrix-core results of one 16 x 16 tile 
 template <> struct MAcc<ES_HIP_Q5_K> {
     v4i lo, hi, q5;
     v4f mn;
+};
+template <> struct MAcc<ES_HIP_Q3_K> {
+    v4i lo, hi;
 };
 
 template <int F> struct Pend {   // a tile's results waiting for their epilogue, with the scales of their superblock
@@ -174,7 +230,7 @@ template <int F> __device__ __forceinline__ void mma(const AOps &a, const BOps<F
         m.hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[s], B.hi[s], m.hi, 0, 0, 0);
         if constexpr (F == ES_HIP_Q5_K) m.q5 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[s], B.q5[s], m.q5, 0, 0, 0);
     }
-    m.mn = __builtin_amdgcn_mfma_f32_16x16x16f16(a.bs, B.mn, v4f{0, 0, 0, 0}, 0, 0, 0);
+    if constexpr (F != ES_HIP_Q3_K) m.mn = __builtin_amdgcn_mfma_f32_16x16x16f16(a.bs, B.mn, v4f{0, 0, 0, 0}, 0, 0, 0);
 }
 
 template <int F, bool CONTRACT>
@@ -182,16 +238,22 @@ __device__ __forceinline__ void epilogue(const MAcc<F> &m, float d, float dm, co
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         int dot = m.lo[i] + 8 * m.hi[i];
-        if constexpr (F == ES_HIP_Q5_K) dot += 16 * m.q5[i];
-        const float q = dm * m.mn[i];   // the mins are exact integers in the f32 accumulator
-        if constexpr (CONTRACT)
-            s[i] = __builtin_fmaf(yd[i], __builtin_fmaf(d, static_cast<float>(dot), -q), s[i]);
-        else
-            s[i] = s[i] + yd[i] * (d * static_cast<float>(dot) - q);
+        if constexpr (F == ES_HIP_Q3_K) {   // s += (y.d * d) * tot
+            const float a = yd[i] * d;
+            if constexpr (CONTRACT) s[i] = __builtin_fmaf(a, static_cast<float>(dot), s[i]);
+            else s[i] = s[i] + a * static_cast<float>(dot);
+        } else {
+            if constexpr (F == ES_HIP_Q5_K) dot += 16 * m.q5[i];
+            const float q = dm * m.mn[i];   // the mins are exact integers in the f32 accumulator
+            if constexpr (CONTRACT)
+                s[i] = __builtin_fmaf(yd[i], __builtin_fmaf(d, static_cast<float>(dot), -q), s[i]);
+            else
+                s[i] = s[i] + yd[i] * (d * static_cast<float>(dot) - q);
+        }
     }
 }
 
-// One tile step: 9 MFMAs (13 for Q5_K) interleaved with the step's vector work (the previous tile's epilogue) and the
+// One tile step: 9 MFMAs (13 for Q5_K, 8 for Q3_K) interleaved with the step's vector work (the previous tile's epilogue) and the
 // next tile's LDS reads: 1 MFMA : 3 VALU : 1 LDS read.
 template <int NMFMA> __device__ __forceinline__ void step_schedule() {
 #pragma unroll
@@ -205,7 +267,8 @@ template <int NMFMA> __device__ __forceinline__ void step_schedule() {
 template <int F, bool CONTRACT, bool GATHER>
 __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
     using FM = MkFmt<F>;
-    constexpr bool FUSED = CONTRACT && F == ES_HIP_Q4_K;   // Q5_K's reference epilogue never fuses
+    constexpr bool FUSED = CONTRACT && F != ES_HIP_Q5_K;   // Q5_K's reference epilogue never fuses
+    constexpr bool BSUMS = F != ES_HIP_Q3_K;              // the mins term reads the activations' bsums
     __shared__ __align__(16) uint8_t smem[2 * ST_BYTES];
 
     MkJob J;
@@ -278,17 +341,23 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
     const uint32_t woff = (uint32_t)min(16 * wave + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
     auto wload = [&](int b, WRaw<F> &W) {
         const uint8_t *p = wbase + woff + (uint32_t)FM::BB * (uint32_t)b;
-        W.h = ldg<uint4>(p);
-        W.q0 = ldg<uint4>(p + FM::QS + 16 * lg);
-        W.q1 = ldg<uint4>(p + FM::QS + 64 + 16 * lg);
-        if constexpr (F == ES_HIP_Q5_K) W.qh = ldg<uint4>(p + FM::QH + 16 * (lg & 1));
+        if constexpr (F == ES_HIP_Q3_K) {
+            W.h = ldg_u128_a2(p + 94);
+            W.q = ldg_u128_a2(p + FM::QS + 16 * lg);
+            W.hm = ldg_u128_a2(p + FM::QH + 16 * (lg & 1));
+        } else {
+            W.h = ldg<uint4>(p);
+            W.q0 = ldg<uint4>(p + FM::QS + 16 * lg);
+            W.q1 = ldg<uint4>(p + FM::QS + 64 + 16 * lg);
+            if constexpr (F == ES_HIP_Q5_K) W.qh = ldg<uint4>(p + FM::QH + 16 * (lg & 1));
+        }
     };
 
     // ---- A operand offsets in a slot: activation tile tt adds 16 rows (values), 16 * 8 (bsums), 64 (scales)
     uint32_t xo[4];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        const int nat = 4 * (lg >> 1) + 8 * (s >> 1) + 2 * (s & 1) + (lg & 1);
+        const int nat = F == ES_HIP_Q3_K ? 8 * (lg >> 1) + 2 * s + (lg & 1) : 4 * (lg >> 1) + 8 * (s >> 1) + 2 * (s & 1) + (lg & 1);
         xo[s] = ST_QS + lr * TROW + 16 * (nat ^ lr);   // rows 16 tt + lr: the swizzle key is lr
     }
     const uint32_t bso = ST_BS + lg * (MK_TOK * 8) + lr * 8, ydo = ST_D + 16 * lg;
@@ -297,7 +366,7 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
     auto aload = [&](const uint32_t (&xa)[4], uint32_t ba, uint32_t ya, int tt, AOps &A) {
 #pragma unroll
         for (int s = 0; s < 4; s++) A.x[s] = lds_ld<v4i>(xa[s] + 16 * TROW * tt);
-        A.bs = lds_ld<v4h>(ba + 128 * tt);
+        if constexpr (BSUMS) A.bs = lds_ld<v4h>(ba + 128 * tt);
         A.yd = lds_ld<v4f>(ya + 64 * tt);
     };
 
@@ -322,7 +391,7 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
     WRaw<F> W;
     stage_dma(0, 0);
     wload(0, W);
-    bs_write(bs_load(0), 0);
+    if constexpr (BSUMS) bs_write(bs_load(0), 0);
     for (int b = 0; b < nbk; b++) {
         const int sl = b & 1;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's copies into LDS (not tracked by the compiler)
@@ -346,17 +415,17 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
             p1.yd = A[tt & 1].yd;
             p1.d = B.d;
             p1.dm = B.dm;
-            step_schedule<F == ES_HIP_Q5_K ? 13 : 9>();
+            step_schedule<F == ES_HIP_Q5_K ? 13 : F == ES_HIP_Q3_K ? 8 : 9>();
             __builtin_amdgcn_sched_barrier(0);
             if (tt == 1) {
                 // the next load group, once this superblock's weights are unpacked (the first MFMAs used them)
                 stage_dma(bn, 1 - sl);
                 wload(bn, W);
-                bsn = bs_load(bn);
+                if constexpr (BSUMS) bsn = bs_load(bn);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        bs_write(bsn, 1 - sl);
+        if constexpr (BSUMS) bs_write(bsn, 1 - sl);
     }
     epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[MK_TT - 2]);
     epilogue<F, FUSED>(p1.m, p1.d, p1.dm, p1.yd, acc[MK_TT - 1]);
@@ -400,6 +469,7 @@ hipError_t mk_launch(int type, bool gather, const MkJob *jobs, int njobs, const 
     const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
     if (type == ES_HIP_Q4_K) mk_launch_fmt<ES_HIP_Q4_K>(gather, contract, jobs, njobs, single, grid, s);
     else if (type == ES_HIP_Q5_K) mk_launch_fmt<ES_HIP_Q5_K>(gather, false, jobs, njobs, single, grid, s);   // never fused
+    else if (type == ES_HIP_Q3_K) mk_launch_fmt<ES_HIP_Q3_K>(gather, contract, jobs, njobs, single, grid, s);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

@@ -35,14 +35,6 @@ template <int RW, int TW, int WN> struct Mm6Geom {
     static_assert(BM <= NT, "one d per thread");
 };
 
-// 16 bytes of global memory at a 2-byte aligned address
-typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
-__device__ __forceinline__ uint4 ldg_u128_a2(const uint8_t *p) {
-    const u32x4_a2 v = *(const ESQ_GLOBAL u32x4_a2 *)p;
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-
 // RW x TW waves: RW along the rows, TW along the activations; WN: 16 x 16 MFMA tiles per wave along the activations.
 // CONTRACT: the clang order (fused multiply-adds), else the gcc / scalar order.
 template <int RW, int TW, int WN, bool CONTRACT>

@@ -263,6 +263,7 @@ std::atomic<int> g_mm2_min{2};   // activations per Q2_K product from which its 
 std::atomic<int> g_mk_min{32};   // activations per Q4_K product from which the direct-activation matrix-core kernel is used
 std::atomic<int> g_mk_min_tiles{128};   // ... and its 64 x 128 tiles per product from which it is (twice that for K > 4096)
 std::atomic<int> g_mk5_min{8};          // activations per Q5_K product from which the direct-activation kernel is used
+std::atomic<int> g_mk3_min{8};          // ... per Q3_K product
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
@@ -353,25 +354,27 @@ bool mm_eligible(const Req &q) {
            q.r1 > q.r0;
 }
 
-// the direct-activation kernel: Q4_K batches of at least g_mk_min (Q5_K: of at least g_mk5_min), every activation row
+// the direct-activation kernel: Q4_K batches of at least g_mk_min (Q5_K, Q3_K: of at least g_mk5_min, g_mk3_min), every
+// activation row
 // within 4 GiB of act
 // the output stride the direct kernel uses: any stride >= r1 serves a single activation (only its row 0 is written)
 size_t mk_ystride(const Req &q) { return q.na > 1 ? q.ystride : std::max(q.ystride, (size_t)q.r1); }
 
 bool mk_eligible(const Req &q) {
-    const bool q5 = q.type == ES_HIP_Q5_K;
-    const int mn = q5 ? g_mk5_min.load() : g_mk_min.load();
-    if ((q.type != ES_HIP_Q4_K && !q5) || mn <= 0 || q.na < mn || q.ints || q.r1 <= q.r0) return false;
+    const bool q5 = q.type == ES_HIP_Q5_K, q3 = q.type == ES_HIP_Q3_K;
+    const int mn = q5 ? g_mk5_min.load() : q3 ? g_mk3_min.load() : g_mk_min.load();
+    if ((q.type != ES_HIP_Q4_K && !q5 && !q3) || mn <= 0 || q.na < mn || q.ints || q.r1 <= q.r0) return false;
     const size_t rows = q.arow ? (size_t)std::max(q.act_rows, 0) : (size_t)q.na;
     const size_t stride = q.astride ? q.astride : (size_t)(q.cols / 256) * 292;
     // Tiles (64 rows x 128 activations, one workgroup each) against the K loop each runs: measured on config 2's shapes,
     // this kernel wins from 128 tiles of 8 superblocks (8192 x 2048 at 128 activations: 17 us against 28 us) and loses
     // with 128 tiles of 32 superblocks (2048 x 8192 at 512: 60 us against 45 us, a quarter of the chip's workgroup slots
     // each running a long chain); from 256 tiles it wins or ties at every depth.
-    // Q5_K has no other matrix-core kernel: against the decode kernel's passes of 4 activations it wins at any tile count.
+    // Q5_K and Q3_K have no other matrix-core kernel: against the decode kernel's passes of 4 activations it wins at any
+    // tile count.
     const int mt = g_mk_min_tiles.load();
     const size_t tiles = (size_t)((q.r1 - q.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS) * ((q.na + esq::MK_TOK - 1) / esq::MK_TOK);
-    if (!q5 && (tiles < (size_t)mt || (tiles < 2 * (size_t)mt && q.cols > 16 * 256))) return false;
+    if (!q5 && !q3 && (tiles < (size_t)mt || (tiles < 2 * (size_t)mt && q.cols > 16 * 256))) return false;
     // 32-bit offsets: activation rows within 4 GiB of the activation pointer; outputs (with a tile of activations past
     // the last) below 2^31 bytes, the range the kernel's buffer stores are checked against
     return (!q.arow || q.act_rows > 0) && rows * stride < ((size_t)1 << 32) - 65536 &&
@@ -1005,6 +1008,7 @@ int es_hip_set_q2k_mfma_min_batch(int n) { return g_mm2_min.exchange(n); }
 int es_hip_set_direct_mfma_min_batch(int n) { return g_mk_min.exchange(n); }
 int es_hip_set_direct_mfma_min_tiles(int n) { return g_mk_min_tiles.exchange(n); }
 int es_hip_set_q5k_mfma_min_batch(int n) { return g_mk5_min.exchange(n); }
+int es_hip_set_q3k_mfma_min_batch(int n) { return g_mk3_min.exchange(n); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
