@@ -289,6 +289,11 @@ int es_hip_set_q5k_mfma_min_batch(int n);
  * the signed codes against the split scales); below it, or with it off (n <= 0), on the vector kernel. Results are
  * identical on both. Returns the previous value. */
 int es_hip_set_q3k_mfma_min_batch(int n);
+/* Q2_K products with 2 to n activations (default 64) and rows of at most 4096 columns run on the expert-sized matrix-core
+ * kernel: it copies the activations' Q8_K rows into LDS once per tile of 256 rows x 32 activations and streams the weights
+ * (no pre-pass). Larger batches, or all with n < 2, run on the LDS-staged Q2_K kernel of es_hip_set_q2k_mfma_min_batch.
+ * Results are identical on every kernel. Returns the previous value. */
+int es_hip_set_q2k_expert_max_batch(int n);
 /* ---- activation preparation on the device ---------------------------------------------------------------------------
  * es_act_prepare (src/es_quant.c:499-512) for `rows` rows of `cols` fp32 values in device memory: q80 (when non-NULL;
  * cols % 32 == 0) receives cols/32 Q8_0 blocks per row exactly as quantize_q80 (src/es_quant.c:489-497) writes them, q8k

@@ -95,6 +95,14 @@ struct MkJob {
     int r0, r1, cols, na;
     int tile0, ntok_tiles;
 };
+// Expert-sized Q2_K products (es_hip_mx.hip): the same jobs, workgroup tiles of MX_ROWS rows x MX_TOK activations (ntok_tiles
+// per row tile; with one, tile ids are the row tiles themselves), rows of at most MX_NBK superblocks (the whole row's
+// activations sit in LDS). nbk_max: the longest row of the launch; mx_nbk_max gives the LDS size class it runs in (0: too
+// long).
+constexpr int MX_TOK = 32, MX_ROWS = 256, MX_NBK = 16;
+int mx_nbk_max(int nbk);
+hipError_t mx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single,
+                     int grid, int order, hipStream_t s);
 // gather: some job of the launch reads its activation rows through arow (a separate kernel build; the others need not)
 hipError_t mk_launch(int type, bool gather, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
                      hipStream_t s);
@@ -324,6 +332,15 @@ __device__ __forceinline__ void load_lds4(const uint8_t *base, uint32_t off, uin
 }
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+
+// A workgroup barrier that orders LDS only: every wave's LDS accesses before it are complete, and nothing waits for the
+// wave's global loads and stores (for kernels where no wave reads global memory another wave of it wrote; copies into LDS
+// by global_load_lds are waited for separately, with s_waitcnt vmcnt).
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 template <int N> __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }

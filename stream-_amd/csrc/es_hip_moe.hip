@@ -11,14 +11,6 @@
 
 namespace esq {
 
-// A workgroup barrier that orders LDS only: every wave's LDS accesses before it are complete, and nothing waits for the
-// wave's global loads and stores (no wave of these kernels reads global memory another wave of it wrote).
-__device__ __forceinline__ void lds_sync() {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 __device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + esq_expf(-g)) * u; }
 template <typename TAB> __device__ __forceinline__ float swiglu_tab(float g, float u, const TAB &T) {
     return g / (1.0f + esq_expf_tab(-g, T)) * u;

@@ -1,0 +1,324 @@
+// Expert-sized Q2_K products on the int8 matrix cores, reading the activations' Q8_K rows directly (no pre-pass): the
+// form of es_matvec_multi (src/es_quant.c:1818-1850, 1344-1368; src/es_q2k.c:127-148) for a MoE expert's few to few tens
+// of activations (config 4: 128 tokens over 64 experts, top 8, about 16 per expert).
+//
+// Work split. A workgroup of 4 waves takes MX_ROWS = 256 rows x MX_TOK = 32 activations: two 16-activation MFMA tiles, the
+// second skipped (wave-uniform) when 16 or fewer activations are left. Every activation value, bsum and scale of the
+// tile's whole row (at most NBKM superblocks) is copied into LDS once, at the start (the activations the tile has: 16 or
+// 32); after that one barrier each wave streams its rows' superblocks from HBM into registers, one superblock ahead per
+// row group (the first already in flight while the activations are copied), with no further barrier.
+// Wave w owns the four row groups 16 (4j + w) .. + 15 (j = 0..3) and runs superblock-major: superblock b of its four row
+// groups in turn, so the A operands of superblock b, read from LDS once, serve four row groups.
+//
+// LDS (NBKM superblocks): values [b][32][256] (activation t's 16-byte chunk c at position c ^ (t & 15), so the 16 lanes
+// that read chunk c of 16 activations hit 16 different bank groups), bsums as halves [b][lg][32][4] (k group lg holds
+// bsums 4lg .. 4lg + 3: exact, |bsums| <= 16 * 127), scales [b][32]. Values go from the Q8_K rows straight into LDS with
+// global_load_lds_dwordx4 (the swizzle in the per-lane source offsets); bsums and scales pass through registers.
+//
+// B operands (weights). Q2_K element order (src/es_q2k.h:1-15): group g = 8n + 2j + half holds bits 2j of
+// qs[32n + 16 half + l], l = 0..15, with the scale byte scales[g] (low nibble sc, high nibble min). Slice s and lane group
+// lg take g = 8 (lg >> 1) + 2s + (lg & 1): the lane's 16 qs bytes 16 lg .. 16 lg + 15 at shift 2s, against the natural
+// 16-element chunk g of the activation row. One int8 plane q * sc (<= 45): isum = D exactly. summs = sum_g bsums_g * min_g
+// through one v_mfma_f32_16x16x16_f16 (k positions 4lg .. 4lg + 3 meet bsums 4lg .. 4lg + 3; mins <= 15 and the bsums are
+// exact halves, every partial sum an integer below 2^24: exact).
+//
+// MFMA operands: A = activations (16 x 64 k), B = weights (64 k x 16 rows): D[activation][row] sits in lane l, register i
+// as activation 4 (l / 16) + i of the tile and row l % 16, the row whose weights the lane unpacked, so d and dmin need no
+// cross-lane moves. Each item's epilogue runs one item later (under the next item's matrix work).
+//
+// Epilogue per (row, activation) and superblock, in superblock order (src/es_q2k.c:142-146, src/es_quant.c:1364-1365):
+// dall = y.d * d, dmin = y.d * dmin, s += dall * isum - dmin * summs, with the product and difference fused as the clang
+// build fuses them (s + fma(dall, isum, -(dmin * summs))) or every operation rounded (the gcc and portable builds).
+#include "es_hip_common.h"
+
+namespace esq {
+namespace {
+
+constexpr int MX_WAVES = 4, MX_RG = MX_ROWS / (16 * MX_WAVES);
+static_assert(MX_RG == 4 && MX_TOK == 32, "four row groups per wave, two activation tiles");
+// LDS bytes per superblock: values, bsums, scales
+constexpr int XV = MX_TOK * 256, XB = 4 * MX_TOK * 8, XD = MX_TOK * 4;
+
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+template <typename T> __device__ __forceinline__ T lds_ld(uint32_t a) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) T *>(a);
+}
+
+struct WRaw {      // this lane's bytes of one row's superblock: qs chunk lg, scale dwords 2 (lg >> 1) and + 1, d | dmin
+    uint4 q;
+    uint32_t s0, s1, dd;
+};
+struct BOps {
+    v4i q[4];
+    v4h mn;
+    float d, dm;
+};
+struct AOps {      // one activation tile's operands for one superblock
+    v4i x[4];
+    v4h bs;
+    v4f yd;        // y.d of activations 4 lg .. 4 lg + 3 of the tile
+};
+struct MRes {
+    v4i i;
+    v4f m;
+};
+
+__device__ __forceinline__ void build_b(const WRaw &w, int lg, BOps &B) {
+    // slice s: scale byte g = 8 (lg >> 1) + 2s + (lg & 1), i.e. byte 2 (s & 1) + (lg & 1) of scale dword 2 (lg >> 1) + (s >> 1),
+    // put into both 16-bit halves for the byte-pair multiplies
+    const uint32_t selA = 0x0c000c00u + (uint32_t)(lg & 1) * 0x00010001u, selB = selA + 0x00020002u;
+    const uint32_t scw[4] = {__builtin_amdgcn_perm(0, w.s0, selA) & 0x000f000fu, __builtin_amdgcn_perm(0, w.s0, selB) & 0x000f000fu,
+                             __builtin_amdgcn_perm(0, w.s1, selA) & 0x000f000fu, __builtin_amdgcn_perm(0, w.s1, selB) & 0x000f000fu};
+    const uint32_t qa[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) B.q[s][i] = (int)pk_mul_u16((qa[i] >> (2 * s)) & 0x03030303u, scw[s]);   // <= 45
+    // mins of groups 4lg .. 4lg + 3: the high nibbles of scale dword lg (= 2 (lg >> 1) + (lg & 1)), as halves built as
+    // 1024 + m (byte m under the exponent of 1024) with 1024 subtracted exactly
+    const uint32_t mw = ((lg & 1) ? w.s1 : w.s0) >> 4 & 0x0f0f0f0fu;
+    const h2 m1024 = __builtin_bit_cast(h2, 0xe400e400u);
+    const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u)) + m1024;
+    const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u)) + m1024;
+    B.mn = v4h{a[0], a[1], b[0], b[1]};
+    B.d = half_bits_to_float(w.dd);
+    B.dm = half_bits_to_float(w.dd >> 16);
+}
+
+__device__ __forceinline__ void mma(const AOps &a, const BOps &B, MRes &m) {
+    m.i = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[0], B.q[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+    for (int s = 1; s < 4; s++) m.i = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.x[s], B.q[s], m.i, 0, 0, 0);
+    m.m = __builtin_amdgcn_mfma_f32_16x16x16f16(a.bs, B.mn, v4f{0, 0, 0, 0}, 0, 0, 0);
+}
+
+template <bool CONTRACT> __device__ __forceinline__ void epilogue(const MRes &m, float d, float dm, const v4f &yd, v4f &s) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float dall = yd[i] * d, dmn = yd[i] * dm;
+        const float q = dmn * m.m[i];   // summs: an exact integer in the f32 accumulator
+        if constexpr (CONTRACT) s[i] = s[i] + __builtin_fmaf(dall, static_cast<float>(m.i[i]), -q);
+        else s[i] = s[i] + (dall * static_cast<float>(m.i[i]) - q);
+    }
+}
+
+template <int NBKM, bool CONTRACT, bool GATHER>
+__global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
+    constexpr uint32_t V0 = 0, BS0 = NBKM * XV, D0 = BS0 + NBKM * XB;
+    __shared__ __align__(16) uint8_t smem[NBKM * (XV + XB + XD)];
+
+    MkJob J;
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
+    else J = single;
+    // tiles: row tile rt, activation tile tt. With several activation tiles, ids go round-robin over the 8 XCDs (id % 8)
+    // with all activation tiles of row tile rt on ids with id % 8 == rt % 8 (one XCD's L2 serves the repeated weight
+    // reads); each job's tiles then start at a multiple of 8 and ids past the last row tile exit at once.
+    const int tile = blockIdx.x - J.tile0;
+    int rt = tile, tt = 0;
+    if (J.ntok_tiles > 1) {
+        const int xcd = tile & 7, kq = tile >> 3;
+        rt = xcd + 8 * (kq / J.ntok_tiles);
+        tt = kq % J.ntok_tiles;
+    }
+    if (rt * MX_ROWS >= J.r1 - J.r0) return;
+    const int row0 = J.r0 + rt * MX_ROWS, tok0 = tt * MX_TOK;
+    const bool two = J.na - tok0 > 16;   // the second 16-activation tile has activations
+    const int nbk = J.cols / 256;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+    const uint32_t smem0 = lds_addr(smem);
+
+    // ---- staging sources: 32-bit offsets from J.act (the host keeps every activation row within 4 GiB of it)
+    auto act_off = [&](int t) -> uint32_t {   // activation t of the tile (clamped to the last one)
+        const int q = min(tok0 + t, J.na - 1);
+        const int r = (GATHER && J.arow) ? ldg<int>(J.arow + q) : q;
+        return (uint32_t)r * (uint32_t)J.astride;
+    };
+    auto sb_base = [&](int b) {   // superblock b's base, kept opaque in scalar registers
+        uint32_t sb = 292u * (uint32_t)b;
+        asm volatile("" : "+s"(sb));
+        return J.act + sb;
+    };
+    // values: wave w copies activations 4w .. 4w + 3 (and 16 + 4w .. + 3 when the second tile is live) of every superblock,
+    // one instruction each (lane l: activation t = 4w + l/16 (+ 16), LDS position l % 16 of its row, source chunk
+    // (l % 16) ^ (t & 15))
+    {
+        const int t0 = 4 * wave + (lane >> 4), t1 = t0 + 16;
+        const uint32_t o0 = act_off(t0) + 4 + 16 * ((lane & 15) ^ (t0 & 15));
+        const uint32_t o1 = act_off(t1) + 4 + 16 * ((lane & 15) ^ (t1 & 15));
+        const uint32_t l0 = smem0 + V0 + (uint32_t)(4 * wave) * 256;
+        for (int b = 0; b < nbk; b++) {
+            const uint8_t *ab = sb_base(b);
+            load_lds16(ab, o0, l0 + (uint32_t)b * XV);
+            if (two) load_lds16(ab, o1, l0 + (uint32_t)b * XV + 16 * 256);
+        }
+    }
+    // bsums: thread tid, activation tb = (tid >> 1) & 31, bsums 8 hb .. 8 hb + 7 of superblocks wave + 4k;
+    // scales: activation td = tid & 31 of superblocks (tid >> 5) + 8k (activations 16..31 only when the second tile is live)
+    constexpr int KB = (NBKM + 3) / 4, KD = (NBKM + 7) / 8;
+    const int tb = (tid >> 1) & 31, hb = tid & 1, td = tid & 31;
+    const bool bs_live = two || tb < 16, d_live = two || td < 16;
+    uint4 bsv[KB];
+    float dv[KD];
+    {
+        const uint32_t ob = act_off(tb) + 260 + 16 * hb, od = act_off(td);
+#pragma unroll
+        for (int k = 0; k < KB; k++)
+            if (wave + 4 * k < nbk && bs_live) bsv[k] = ldg<uint4>(sb_base(wave + 4 * k) + ob);
+#pragma unroll
+        for (int k = 0; k < KD; k++) {
+            const int b = (tid >> 5) + 8 * k;
+            if (b < nbk && d_live) dv[k] = ldg<float>(J.act + (size_t)(292u * (uint32_t)b + od));
+        }
+    }
+
+    // ---- this wave's weight rows (rows past r1 repeat the last one; their results are not stored)
+    const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
+    uint32_t woff[MX_RG];
+#pragma unroll
+    for (int j = 0; j < MX_RG; j++)
+        woff[j] = (uint32_t)min(16 * (4 * j + wave) + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
+    auto wload = [&](int j, int b, WRaw &w) {
+        const uint8_t *p = wbase + woff[j] + 84u * (uint32_t)b;
+        w.q = ldg_u128_a2(p + 16 + 16 * lg);
+        const u32x2_a4 sc = *(const ESQ_GLOBAL u32x2_a4 *)(p + 8 * (lg >> 1));
+        w.s0 = sc.x;
+        w.s1 = sc.y;
+        w.dd = ldg<uint32_t>(p + 80);
+    };
+    // one register set per row group, a superblock ahead. Every load is unconditional (the superblock past the last
+    // repeats it, unused): with no branch around a load, the compiler's waits count exactly which loads a use needs
+    // instead of draining the queue.
+    WRaw R[MX_RG];
+#pragma unroll
+    for (int j = 0; j < MX_RG; j++) wload(j, 0, R[j]);
+    // the staged copies are older than the 3 * MX_RG weight loads just issued
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * MX_RG) : "memory");
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+        const int b = wave + 4 * k;
+        if (b >= nbk || !bs_live) continue;
+        const uint32_t w[4] = {bsv[k].x, bsv[k].y, bsv[k].z, bsv[k].w};
+        uint32_t hv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {   // two int16 bsums -> two halves (exact)
+            const _Float16 e0 = (_Float16)(int16_t)(w[i] & 0xffffu), e1 = (_Float16)(int16_t)(w[i] >> 16);
+            hv[i] = (uint32_t)__builtin_bit_cast(uint16_t, e0) | (uint32_t)__builtin_bit_cast(uint16_t, e1) << 16;
+        }
+        uint8_t *base = smem + BS0 + b * XB + tb * 8;
+        *reinterpret_cast<uint2 *>(base + (2 * hb) * (MX_TOK * 8)) = make_uint2(hv[0], hv[1]);
+        *reinterpret_cast<uint2 *>(base + (2 * hb + 1) * (MX_TOK * 8)) = make_uint2(hv[2], hv[3]);
+    }
+#pragma unroll
+    for (int k = 0; k < KD; k++) {
+        const int b = (tid >> 5) + 8 * k;
+        if (b < nbk && d_live) *reinterpret_cast<float *>(smem + D0 + b * XD + td * 4) = dv[k];
+    }
+    lds_sync();
+
+    // ---- A operand addresses: tile u adds 16 rows (values), 16 * 8 bytes (bsums), 64 bytes (scales)
+    uint32_t xo[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int nat = 8 * (lg >> 1) + 2 * s + (lg & 1);
+        xo[s] = smem0 + V0 + lr * 256 + 16 * (nat ^ lr);
+    }
+    const uint32_t bso = smem0 + BS0 + lg * (MX_TOK * 8) + lr * 8, ydo = smem0 + D0 + 16 * lg;
+    auto aload = [&](int b, int u, AOps &A) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) A.x[s] = lds_ld<v4i>(xo[s] + (uint32_t)b * XV + 16 * 256 * u);
+        A.bs = lds_ld<v4h>(bso + (uint32_t)b * XB + 128 * u);
+        A.yd = lds_ld<v4f>(ydo + (uint32_t)b * XD + 64 * u);
+    };
+
+    v4f acc[MX_RG][2];
+#pragma unroll
+    for (int j = 0; j < MX_RG; j++) acc[j][0] = acc[j][1] = v4f{0, 0, 0, 0};
+    // the previous item's results (starting as zeros: their epilogue adds +0 to the +0 of acc[3])
+    MRes pm[2];
+    pm[0].i = pm[1].i = v4i{0, 0, 0, 0};
+    pm[0].m = pm[1].m = v4f{0, 0, 0, 0};
+    v4f pyd[2] = {v4f{0, 0, 0, 0}, v4f{0, 0, 0, 0}};
+    float pd = 0.f, pdm = 0.f;
+    for (int b = 0; b < nbk; b++) {   // superblock b of the four row groups; their superblock b + 1 loaded in turn
+        AOps A[2];
+        aload(b, 0, A[0]);
+        if (two) aload(b, 1, A[1]);
+#pragma unroll
+        for (int j = 0; j < MX_RG; j++) {
+            BOps B;
+            build_b(R[j], lg, B);
+            wload(j, min(b + 1, nbk - 1), R[j]);
+            MRes m[2];
+            mma(A[0], B, m[0]);
+            if (two) mma(A[1], B, m[1]);
+            // the previous item: row group j - 1 of this superblock, or row group 3 of the previous one
+            epilogue<CONTRACT>(pm[0], pd, pdm, pyd[0], acc[(j + MX_RG - 1) % MX_RG][0]);
+            if (two) epilogue<CONTRACT>(pm[1], pd, pdm, pyd[1], acc[(j + MX_RG - 1) % MX_RG][1]);
+            pm[0] = m[0];
+            pm[1] = m[1];
+            pd = B.d;
+            pdm = B.dm;
+            pyd[0] = A[0].yd;
+            pyd[1] = A[1].yd;
+        }
+    }
+    epilogue<CONTRACT>(pm[0], pd, pdm, pyd[0], acc[MX_RG - 1][0]);
+    if (two) epilogue<CONTRACT>(pm[1], pd, pdm, pyd[1], acc[MX_RG - 1][1]);
+
+    // ---- outputs: lane l, register i of tile u holds activation tok0 + 16u + 4lg + i, row row0 + 16 (4j + wave) + lr.
+    // Buffer stores over y[0, (na - 1) * ystride + r1): the hardware's range check drops those of activations past na
+    // (ystride >= r1), and rows past r1 get an offset above the range. The host keeps (na + MX_TOK) * ystride * 4 below
+    // 2^31, so no offset wraps.
+    const uint32_t ys4 = 4u * (uint32_t)J.ystride;
+    const uint32_t yrange = (uint32_t)(J.na - 1) * ys4 + 4u * (uint32_t)J.r1;
+    const __amdgpu_buffer_rsrc_t yrsrc = __builtin_amdgcn_make_buffer_rsrc((void *)J.y, (short)0, (int)yrange, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < MX_RG; j++) {
+        const int r = row0 + 16 * (4 * j + wave) + lr;
+        uint32_t yoff = r < J.r1 ? (uint32_t)(tok0 + 4 * lg) * ys4 + 4u * (uint32_t)r : 0x80000000u;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            if (u == 1 && !two) break;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float v = acc[j][u][i];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrsrc, (int)yoff, 0, 0);
+                yoff += i < 3 ? ys4 : 13 * ys4;   // the next activation: + 1, or + 13 to the next tile's first
+            }
+        }
+    }
+}
+
+template <int NBKM>
+void mx_launch_nbk(bool gather, bool contract, const MkJob *jobs, int njobs, const MkJob &single, int grid, hipStream_t s) {
+    const dim3 g(grid), b(64 * MX_WAVES);
+    if (gather) {
+        if (contract) hipLaunchKernelGGL((mx_q2k_kernel<NBKM, true, true>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mx_q2k_kernel<NBKM, false, true>), g, b, 0, s, jobs, njobs, single);
+    } else {
+        if (contract) hipLaunchKernelGGL((mx_q2k_kernel<NBKM, true, false>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mx_q2k_kernel<NBKM, false, false>), g, b, 0, s, jobs, njobs, single);
+    }
+}
+
+}  // namespace
+
+int mx_nbk_max(int nbk) { return nbk <= 4 ? 4 : nbk <= 8 ? 8 : nbk <= MX_NBK ? MX_NBK : 0; }
+
+hipError_t mx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single, int grid,
+                     int order, hipStream_t s) {
+    if (type != ES_HIP_Q2_K) return hipErrorInvalidValue;
+    const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
+    switch (mx_nbk_max(nbk_max)) {
+    case 4: mx_launch_nbk<4>(gather, contract, jobs, njobs, single, grid, s); break;
+    case 8: mx_launch_nbk<8>(gather, contract, jobs, njobs, single, grid, s); break;
+    case MX_NBK: mx_launch_nbk<MX_NBK>(gather, contract, jobs, njobs, single, grid, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace esq

@@ -264,6 +264,7 @@ std::atomic<int> g_mk_min{32};   // activations per Q4_K product from which the 
 std::atomic<int> g_mk_min_tiles{128};   // ... and its 64 x 128 tiles per product from which it is (twice that for K > 4096)
 std::atomic<int> g_mk5_min{8};          // activations per Q5_K product from which the direct-activation kernel is used
 std::atomic<int> g_mk3_min{8};          // ... per Q3_K product
+std::atomic<int> g_mx_max{64};          // activations per Q2_K product up to which the expert-sized kernel is used (2+)
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
@@ -296,6 +297,7 @@ struct MmGroup {   // one matrix-core launch: products of one format sharing a w
 struct MkGroup {   // one direct-activation matrix-core launch: products of one format, gathered activations or not
     int type;
     bool gather;
+    int nbkm = 0;     // > 0: the expert-sized kernel (es_hip_mx.hip) in LDS size class nbkm
     int grid = 0;
     std::vector<esq::MkJob> jobs;
     size_t off = 0;
@@ -359,6 +361,17 @@ bool mm_eligible(const Req &q) {
 // within 4 GiB of act
 // the output stride the direct kernel uses: any stride >= r1 serves a single activation (only its row 0 is written)
 size_t mk_ystride(const Req &q) { return q.na > 1 ? q.ystride : std::max(q.ystride, (size_t)q.r1); }
+
+// the expert-sized kernel: Q2_K products of 2 .. g_mx_max activations, rows of at most MX_NBK superblocks, every
+// activation row within 4 GiB of act
+bool mx_eligible(const Req &q) {
+    const int mx = g_mx_max.load();
+    if (q.type != ES_HIP_Q2_K || q.na < 2 || q.na > mx || q.ints || q.r1 <= q.r0 || q.cols / 256 > esq::MX_NBK) return false;
+    const size_t rows = q.arow ? (size_t)std::max(q.act_rows, 0) : (size_t)q.na;
+    const size_t stride = q.astride ? q.astride : (size_t)(q.cols / 256) * 292;
+    return (!q.arow || q.act_rows > 0) && rows * stride < ((size_t)1 << 32) - 65536 &&
+           ((size_t)q.na + esq::MX_TOK) * mk_ystride(q) * sizeof(float) < ((size_t)1 << 31);
+}
 
 bool mk_eligible(const Req &q) {
     const bool q5 = q.type == ES_HIP_Q5_K, q3 = q.type == ES_HIP_Q3_K;
@@ -457,10 +470,35 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             continue;
         }
         const int nbk = q.cols / 256;
+        if (mx_eligible(q)) {   // one launch per LDS size class; MX_ROWS x MX_TOK tiles
+            const int nbkm = esq::mx_nbk_max(nbk);
+            MkGroup *g = nullptr;
+            for (MkGroup &x : bt.mkg)
+                if (x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == nbkm) g = &x;
+            if (!g) { bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr, nbkm}); g = &bt.mkg.back(); }
+            esq::MkJob j{};
+            j.W = static_cast<const uint8_t *>(q.W);
+            j.act = static_cast<const uint8_t *>(q.act);
+            j.arow = q.arow;
+            j.y = q.y;
+            j.astride = q.astride ? q.astride : (uint64_t)nbk * f.ab;
+            j.ystride = mk_ystride(q);
+            j.row_bytes = (uint64_t)nbk * f.bb;
+            j.r0 = q.r0;
+            j.r1 = q.r1;
+            j.cols = q.cols;
+            j.na = q.na;
+            j.tile0 = g->grid;
+            j.ntok_tiles = (q.na + esq::MX_TOK - 1) / esq::MX_TOK;
+            const int row_tiles = (q.r1 - q.r0 + esq::MX_ROWS - 1) / esq::MX_ROWS;
+            g->grid += j.ntok_tiles == 1 ? row_tiles : 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
+            g->jobs.push_back(j);
+            continue;
+        }
         if (mk_eligible(q)) {   // one launch per format; MK_ROWS x MK_TOK tiles, 8 consecutive ids per row tile group
             MkGroup *g = nullptr;
             for (MkGroup &x : bt.mkg)
-                if (x.type == (int)q.type && x.gather == (q.arow != nullptr)) g = &x;
+                if (x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == 0) g = &x;
             if (!g) { bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr}); g = &bt.mkg.back(); }
             esq::MkJob j{};
             j.W = static_cast<const uint8_t *>(q.W);
@@ -644,7 +682,8 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
     }
     for (const MkGroup &g : bt.mkg) {
         const esq::MkJob *dj = tables ? reinterpret_cast<const esq::MkJob *>(tables + g.off) : nullptr;
-        if ((e = esq::mk_launch(g.type, g.gather, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+        if ((e = g.nbkm ? esq::mx_launch(g.type, g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
+                        : esq::mk_launch(g.type, g.gather, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
             return hip_fail(e, "matrix-core launch");
     }
     for (const MbGroup &g : bt.mbg) {
@@ -1009,6 +1048,7 @@ int es_hip_set_direct_mfma_min_batch(int n) { return g_mk_min.exchange(n); }
 int es_hip_set_direct_mfma_min_tiles(int n) { return g_mk_min_tiles.exchange(n); }
 int es_hip_set_q5k_mfma_min_batch(int n) { return g_mk5_min.exchange(n); }
 int es_hip_set_q3k_mfma_min_batch(int n) { return g_mk3_min.exchange(n); }
+int es_hip_set_q2k_expert_max_batch(int n) { return g_mx_max.exchange(n); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }

@@ -1,7 +1,9 @@
-"""GPU parity of the Q2_K LDS-staged matrix-core path (es_hip_mm2.hip): bit-identical to the oracle in every reference
-order and to the vector kernel, at the config 4 expert shapes and at ragged edges (rows not a multiple of the 128-row tile,
-activation counts between the 16/32/64-wide tiles and above 64, row sub-ranges, padded strides, matrices at any 4-byte
-offset), with codes and scales at their extremes."""
+"""GPU parity of the Q2_K matrix-core kernels, each test run on both: the LDS-staged kernel (es_hip_mm2.hip, "lds") and the
+expert-sized kernel that copies the activations' Q8_K rows into LDS once and streams the weights (es_hip_mx.hip, "expert",
+for 2 to 64 activations; larger batches stay on the LDS-staged kernel). Bit-identical to the oracle in every reference
+order and to the vector kernel, at the config 4 expert shapes and at ragged edges (rows not a multiple of the row tiles,
+activation counts between the 16/32/64-wide tiles and above 64, rows of 1 to 16 superblocks, row sub-ranges, padded
+strides, matrices at any 4-byte offset), with codes and scales at their extremes."""
 import numpy as np
 import pytest
 
@@ -29,28 +31,32 @@ def inputs(orc, rows, cols, na, seed, gauss=False):
     return W, orc.quantize_act(O.Q2_K, x)
 
 
-@pytest.fixture
-def hip2(hip):
+@pytest.fixture(params=["lds", "expert"])
+def hip2(hip, request):
     prev = hip.set_q2k_mfma_min_batch(2)
+    prev_x = hip.set_q2k_expert_max_batch(64 if request.param == "expert" else 1)
     yield hip
     hip.set_q2k_mfma_min_batch(prev)
+    hip.set_q2k_expert_max_batch(prev_x)
     hip.set_order(E.ORDER_X86_CONTRACT)
 
 
 def vector_path(hip, fn):
     """fn() with the Q2_K matrix-core kernels switched off"""
-    a, b = hip.set_q2k_mfma_min_batch(0), hip.set_small_batch_min(0)
+    a, b, c = hip.set_q2k_mfma_min_batch(0), hip.set_small_batch_min(0), hip.set_q2k_expert_max_batch(1)
     try:
         return fn()
     finally:
         hip.set_q2k_mfma_min_batch(a)
         hip.set_small_batch_min(b)
+        hip.set_q2k_expert_max_batch(c)
 
 
 @pytest.mark.parametrize("rows,cols,na,gauss", [(1024, 2048, 2, True), (300, 1024, 5, False), (1024, 2048, 16, True),
                                                 (2048, 1024, 24, True), (300, 1024, 64, False),
                                                 (200, 2048, 40, False), (77, 768, 9, False), (150, 1024, 130, False),
-                                                (64, 4096, 33, True)])
+                                                (64, 4096, 33, True), (1, 256, 17, False), (257, 1280, 31, False),
+                                                (130, 3328, 48, True)])
 @pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
 def test_q2k_mfma_vs_oracle(hip2, orc, rows, cols, na, gauss, mode):
     hip2.set_order(mode[0])
@@ -72,8 +78,9 @@ def test_q2k_mfma_equals_vector_path(hip2, orc, rows, cols, na):
     assert np.array_equal(bits(y_mm[:2]), bits(ref))
 
 
-def test_q2k_mfma_row_range_and_strides(hip2, orc):
-    rows, cols, na, r0, r1 = 300, 1024, 70, 37, 251
+@pytest.mark.parametrize("na", [70, 40, 7])
+def test_q2k_mfma_row_range_and_strides(hip2, orc, na):
+    rows, cols, r0, r1 = 300, 1024, 37, 251
     W, acts = inputs(orc, rows, cols, na, 98)
     ab = cols // 256 * 292
     astride = ab + 52
@@ -86,8 +93,8 @@ def test_q2k_mfma_row_range_and_strides(hip2, orc):
     dY = hip2.upload(np.full(na * ystride, sentinel, np.float32))
     hip2.matvec_multi_dev(O.Q2_K, dW, cols, r0, r1, dA, astride, na, dY, ystride)
     y = hip2.download(dY, np.zeros((na, ystride), np.float32))
-    ref = orc.matvec_multi(O.Q2_K, W, cols, rows, acts[[0, 69]])
-    assert np.array_equal(bits(y[[0, 69], r0:r1]), bits(ref[:, r0:r1]))
+    ref = orc.matvec_multi(O.Q2_K, W, cols, rows, acts[[0, na - 1]])
+    assert np.array_equal(bits(y[[0, na - 1], r0:r1]), bits(ref[:, r0:r1]))
     assert np.all(y[:, :r0] == sentinel) and np.all(y[:, r1:rows] == sentinel) and np.all(y[:, rows:] == sentinel)
 
 
