@@ -167,10 +167,13 @@ hipError_t route_softmax_launch(const float *logits, uint64_t ls, int ntok, int 
 //   MOE_FAM_MV: the decode kernel (one job per expert slot and product, a fixed number of row tiles each);
 //   MOE_FAM_MM: a pre-pass of the expert's gathered activations into its planes (packed one expert after another), then
 //               the matrix-core kernel (tiles of 128 rows x bn activations, as many activation tiles as the expert's
-//               count needs).
+//               count needs);
+//   MOE_FAM_MX: the expert-sized Q2_K kernel on the gathered Q8_K rows themselves (tiles of MX_ROWS rows x MX_TOK
+//               activations: mx_tiles row tiles for an expert of one activation tile, row_tiles8 per activation tile for
+//               an expert of several).
 // Slots u >= the number of experts used, and one sentinel job at the end of every table, are empty jobs placed after the
 // last real tile (the host launches upper-bound grids; their workgroups find an empty job and exit).
-constexpr int MOE_FAM_MV = 0, MOE_FAM_MM = 1, MOE_GROUP_THREADS = 1024, MOE_MAX_PAIRS = 16384;
+constexpr int MOE_FAM_MV = 0, MOE_FAM_MM = 1, MOE_FAM_MX = 2, MOE_GROUP_THREADS = 1024, MOE_MAX_PAIRS = 16384;
 struct MoeFamily {
     int kind;
     MvJob mv;              // MV: template job (rows, cols, strides, rows_per_wg, chain_rows); mv_tiles row tiles per job
@@ -178,6 +181,8 @@ struct MoeFamily {
     MmJob mm;              // MM: template job; bn activations per tile; row tiles (rounded up to 8, the XCD map)
     PrepJob pj;            // MM: template pre-pass (nbk, kind)
     int bn, row_tiles8;
+    MkJob mk;              // MX: template job
+    int mx_tiles;
 };
 struct MoeDevArgs {
     const int *sel;         // [ntok][k] routing (experts)

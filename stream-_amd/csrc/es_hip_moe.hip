@@ -424,6 +424,10 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
         const MoeFamily &F = prod ? sa.DN : sa.GU;
         const int njob = prod ? 1 : 2;
         int ntok = 0, tiles = 0, items = 0, units = 0;
+        if (F.kind == MOE_FAM_MX && real) {
+            ntok = ceil_div(c, MX_TOK);
+            tiles = njob * (ntok == 1 ? F.mx_tiles : F.row_tiles8 * ntok);
+        }
         if (F.kind == MOE_FAM_MM && real) {
             ntok = ceil_div(c, F.bn);
             tiles = njob * F.row_tiles8 * ntok;
@@ -433,7 +437,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
             units = ceil_div(F.pj.nbk * ntok * F.bn * 256, 256) + ceil_div(F.pj.nbk * ntok * F.bn * 36, 256);
         }
         int tot_tiles = 0, tot_items = 0, w0 = 0;
-        if (F.kind == MOE_FAM_MM) {   // uniform across the block: every thread takes part in the scan
+        if (F.kind != MOE_FAM_MV) {   // uniform across the block: every thread takes part in the scan
             const int3 sc = block_excl_scan3(make_int3(tiles, items, units), wsum, &s_tot);
             tot_tiles = s_tot.x;
             tot_items = s_tot.y;
@@ -474,6 +478,35 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
                 J.na = 0;
                 J.r0 = J.r1 = 0;
                 J.tile0 = end;
+                jobs[njob * A.umax] = J;
+            }
+        } else if (F.kind == MOE_FAM_MX) {
+            MkJob *jobs = static_cast<MkJob *>(prod ? A.dn_jobs : A.gu_jobs);
+            if (u < A.umax)
+                for (int g = 0; g < njob; g++) {
+                    MkJob J = F.mk;
+                    if (real) {
+                        J.W = g ? wup : wsrc;
+                        J.act = prod ? A.ha + (size_t)s0 * A.hstride : A.x;
+                        J.arow = prod ? nullptr : A.tok_of + s0;
+                        J.y = prod ? A.bye + (size_t)s0 * n : A.bgu + (size_t)s0 * 2 * ff + (size_t)g * ff;
+                        J.na = c;
+                        J.ntok_tiles = ntok;
+                        J.tile0 = t0 + g * (ntok == 1 ? F.mx_tiles : F.row_tiles8 * ntok);
+                    } else {
+                        J.na = 0;
+                        J.r0 = J.r1 = 0;
+                        J.ntok_tiles = 1;
+                        J.tile0 = tot_tiles;
+                    }
+                    jobs[njob * u + g] = J;
+                }
+            if (tid == 0) {
+                MkJob J = F.mk;
+                J.na = 0;
+                J.r0 = J.r1 = 0;
+                J.ntok_tiles = 1;
+                J.tile0 = tot_tiles;
                 jobs[njob * A.umax] = J;
             }
         } else {

@@ -175,18 +175,27 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
     }
 
     // ---- this wave's weight rows (rows past r1 repeat the last one; their results are not stored)
+    // Buffer loads from the tile's first row: per-lane offsets per row group (q chunk, scale pair, d | dmin) and the
+    // superblock's 84 b in the scalar offset, so a load needs no address arithmetic.
     const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
-    uint32_t woff[MX_RG];
+    const uint32_t wrange = (uint32_t)min(MX_ROWS, J.r1 - row0) * (uint32_t)J.row_bytes;
+    const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc((void *)wbase, (short)0, (int)wrange, 0x00020000);
+    uint32_t vq[MX_RG], vs[MX_RG], vd[MX_RG];
 #pragma unroll
-    for (int j = 0; j < MX_RG; j++)
-        woff[j] = (uint32_t)min(16 * (4 * j + wave) + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
+    for (int j = 0; j < MX_RG; j++) {
+        const uint32_t o = (uint32_t)min(16 * (4 * j + wave) + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
+        vq[j] = o + 16 + 16 * lg;
+        vs[j] = o + 8 * (lg >> 1);
+        vd[j] = o + 80;
+    }
     auto wload = [&](int j, int b, WRaw &w) {
-        const uint8_t *p = wbase + woff[j] + 84u * (uint32_t)b;
-        w.q = ldg_u128_a2(p + 16 + 16 * lg);
-        const u32x2_a4 sc = *(const ESQ_GLOBAL u32x2_a4 *)(p + 8 * (lg >> 1));
+        const int so = 84 * b;
+        const u32x4 q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)vq[j], so, 0));
+        const u32x2 sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrsrc, (int)vs[j], so, 0));
+        w.q = make_uint4(q.x, q.y, q.z, q.w);
         w.s0 = sc.x;
         w.s1 = sc.y;
-        w.dd = ldg<uint32_t>(p + 80);
+        w.dd = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)vd[j], so, 0);
     };
     // one register set per row group, a superblock ahead. Every load is unconditional (the superblock past the last
     // repeats it, unused): with no branch around a load, the compiler's waits count exactly which loads a use needs
@@ -237,36 +246,38 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
 #pragma unroll
     for (int j = 0; j < MX_RG; j++) acc[j][0] = acc[j][1] = v4f{0, 0, 0, 0};
     // the previous item's results (starting as zeros: their epilogue adds +0 to the +0 of acc[3])
-    MRes pm[2];
-    pm[0].i = pm[1].i = v4i{0, 0, 0, 0};
-    pm[0].m = pm[1].m = v4f{0, 0, 0, 0};
-    v4f pyd[2] = {v4f{0, 0, 0, 0}, v4f{0, 0, 0, 0}};
-    float pd = 0.f, pdm = 0.f;
+    // Results and row scales by item parity (j & 1): item j's epilogue reads those of item j - 1 in place, no copies.
+    // Item (b - 1, 3), whose epilogue runs at (b, 0), keeps its activation scales in ydl. Its slots start as zeros (all
+    // scales 0): the first epilogue adds +0 to the +0 of acc[3].
+    MRes mr[2][2];
+    mr[1][0].i = mr[1][1].i = v4i{0, 0, 0, 0};
+    mr[1][0].m = mr[1][1].m = v4f{0, 0, 0, 0};
+    float bd[2] = {0.f, 0.f}, bdm[2] = {0.f, 0.f};
+    v4f ydl[2] = {v4f{0, 0, 0, 0}, v4f{0, 0, 0, 0}};
     for (int b = 0; b < nbk; b++) {   // superblock b of the four row groups; their superblock b + 1 loaded in turn
         AOps A[2];
         aload(b, 0, A[0]);
         if (two) aload(b, 1, A[1]);
 #pragma unroll
         for (int j = 0; j < MX_RG; j++) {
+            const int pc = j & 1, pp = pc ^ 1;
             BOps B;
             build_b(R[j], lg, B);
             wload(j, min(b + 1, nbk - 1), R[j]);
-            MRes m[2];
-            mma(A[0], B, m[0]);
-            if (two) mma(A[1], B, m[1]);
+            bd[pc] = B.d;
+            bdm[pc] = B.dm;
+            mma(A[0], B, mr[pc][0]);
+            if (two) mma(A[1], B, mr[pc][1]);
             // the previous item: row group j - 1 of this superblock, or row group 3 of the previous one
-            epilogue<CONTRACT>(pm[0], pd, pdm, pyd[0], acc[(j + MX_RG - 1) % MX_RG][0]);
-            if (two) epilogue<CONTRACT>(pm[1], pd, pdm, pyd[1], acc[(j + MX_RG - 1) % MX_RG][1]);
-            pm[0] = m[0];
-            pm[1] = m[1];
-            pd = B.d;
-            pdm = B.dm;
-            pyd[0] = A[0].yd;
-            pyd[1] = A[1].yd;
+            v4f &a0 = acc[(j + MX_RG - 1) % MX_RG][0], &a1 = acc[(j + MX_RG - 1) % MX_RG][1];
+            epilogue<CONTRACT>(mr[pp][0], bd[pp], bdm[pp], j ? A[0].yd : ydl[0], a0);
+            if (two) epilogue<CONTRACT>(mr[pp][1], bd[pp], bdm[pp], j ? A[1].yd : ydl[1], a1);
         }
+        ydl[0] = A[0].yd;
+        ydl[1] = A[1].yd;
     }
-    epilogue<CONTRACT>(pm[0], pd, pdm, pyd[0], acc[MX_RG - 1][0]);
-    if (two) epilogue<CONTRACT>(pm[1], pd, pdm, pyd[1], acc[MX_RG - 1][1]);
+    epilogue<CONTRACT>(mr[1][0], bd[1], bdm[1], ydl[0], acc[MX_RG - 1][0]);
+    if (two) epilogue<CONTRACT>(mr[1][1], bd[1], bdm[1], ydl[1], acc[MX_RG - 1][1]);
 
     // ---- outputs: lane l, register i of tile u holds activation tok0 + 16u + 4lg + i, row row0 + 16 (4j + wave) + lr.
     // Buffer stores over y[0, (na - 1) * ystride + r1): the hardware's range check drops those of activations past na

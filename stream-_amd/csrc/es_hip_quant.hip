@@ -1524,6 +1524,17 @@ bool moe_mm_family(uint32_t type, int cols, double expect, int &bn) {
     return esq::mm_tile_ok(128, bn, 8);
 }
 
+// the expert-sized kernel for a MoE product when plan_batch would pick it at the expected count per expert, with its
+// 32-bit offsets in range: the act_rows activation rows within 4 GiB of the first, the outputs (R + MX_TOK activations
+// past any expert's first) within 2 GiB
+bool moe_mx_family(uint32_t type, int rows, int cols, double expect, int R, size_t act_rows, uint64_t astride,
+                   uint64_t ystride) {
+    const int na = std::max(1, (int)(expect + 0.5));
+    return type == ES_HIP_Q2_K && na >= 2 && na <= g_mx_max.load() && cols / 256 <= esq::MX_NBK && rows > 0 &&
+           act_rows * astride < ((size_t)1 << 32) - 65536 &&
+           ((size_t)R + esq::MX_TOK) * ystride * sizeof(float) < ((size_t)1 << 31);
+}
+
 // the planes of every expert of a layer of R choices over at most umax experts, packed: at most R + 127 umax padded
 // activations (tiles of up to 128), each expert's two planes rounded up to 256 bytes
 size_t moe_ws_bytes(int cols, int R, int umax) {
@@ -1549,6 +1560,30 @@ int moe_family(es_hip_moe_ctx *c, uint32_t type, int rows, int cols, int umax, i
     M.njobs = njob * umax + 1;
     M.nprep = umax + 1;
     int bn = 0;
+    // activation rows: the layer's tokens (gate/up, gathered) or its pair rows (down)
+    if (moe_mx_family(type, rows, cols, expect, R, arow ? (size_t)std::max(maxc, 1) : (size_t)R, astride, ystride)) {
+        M.F.kind = esq::MOE_FAM_MX;
+        const int row_tiles = (rows + esq::MX_ROWS - 1) / esq::MX_ROWS;
+        M.F.mx_tiles = row_tiles;
+        M.F.row_tiles8 = 8 * ((row_tiles + 7) / 8);
+        esq::MkJob &j = M.F.mk;
+        j.W = w0;
+        j.act = act;
+        j.arow = arow;
+        j.y = y;
+        j.astride = astride;
+        j.ystride = ystride;
+        j.row_bytes = (uint64_t)nbk * f.bb;
+        j.r0 = 0;
+        j.r1 = rows;
+        j.cols = cols;
+        j.na = 0;
+        j.tile0 = 0;
+        j.ntok_tiles = 1;
+        // sum over experts of ceil(count / MX_TOK) activation tiles, each at most row_tiles8 tiles
+        M.grid = njob * M.F.row_tiles8 * ((R + esq::MX_TOK - 1) / esq::MX_TOK + umax);
+        return ES_HIP_OK;
+    }
     if (ws && moe_mm_family(type, cols, expect, bn)) {
         M.F.kind = esq::MOE_FAM_MM;
         M.bn = M.F.bn = bn;
@@ -1652,7 +1687,7 @@ es_hip_moe_ctx *es_hip_moe_ctx_create(const es_hip_moe *m, int max_tokens, int k
     const bool dn_mm = m->down_type == ES_HIP_Q2_K || m->down_type == ES_HIP_Q4_K || m->down_type == ES_HIP_Q6_K;
     c->gu_slot = gu_mm ? moe_ws_bytes(n, R, umax) : 0;
     c->dn_slot = dn_mm ? moe_ws_bytes(ff, R, umax) : 0;
-    const size_t job = std::max(sizeof(MvJob), sizeof(esq::MmJob));
+    const size_t job = std::max({sizeof(MvJob), sizeof(esq::MmJob), sizeof(esq::MkJob)});
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += align256(std::max<size_t>(bytes, 1)); return o; };
     const size_t o_sel = take(sizeof(int) * R), o_w = take(sizeof(float) * R), o_tok = take(sizeof(int) * R),
@@ -1756,6 +1791,11 @@ int moe_ctx_layer(es_hip_moe_ctx *c, int N, const void *x, size_t xstride, float
         if (M.F.kind == esq::MOE_FAM_MV) {
             e = esq::mv_launch(M.L, static_cast<const MvJob *>(jobs), M.njobs, M.F.mv, order, s);
             return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "MoE decode-kernel launch");
+        }
+        if (M.F.kind == esq::MOE_FAM_MX) {
+            e = esq::mx_launch((int)type, M.F.mk.arow != nullptr, M.F.mk.cols / 256, static_cast<const esq::MkJob *>(jobs),
+                               M.njobs, M.F.mk, M.grid, order, s);
+            return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "MoE expert-kernel launch");
         }
         if ((e = esq::prep_launch(prep, M.nprep, M.F.pj, M.items, s)) != hipSuccess) return hip_fail(e, "MoE pre-pass launch");
         e = esq::mm_launch((int)type, 128, M.bn, 8, static_cast<const esq::MmJob *>(jobs), M.njobs, M.F.mm, M.grid, order, s);

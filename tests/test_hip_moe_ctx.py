@@ -1,8 +1,8 @@
 """GPU parity of the device-routed MoE layer (es_hip_moe_ctx_*): moe_n's grouping (src/es_engine.c:871-888) and the job
 tables built on the device from a routing in device memory, then the expert FFN, with no allocation and no host round
 trip per call. Outputs must equal the oracle's moe_n restatement bit for bit: configs 4 and 5 from device logits (the
-routing equal to the oracle's route()), every reference order, both kernel families (decode kernel, pre-pass +
-matrix-core kernel), skewed routings where one expert takes every token, fresh routings and token counts call after call
+routing equal to the oracle's route()), every reference order, every kernel family (decode kernel, pre-pass +
+matrix-core kernel, expert-sized Q2_K kernel), skewed routings where one expert takes every token, fresh routings and token counts call after call
 on one context without a wait between them, and the rejected shapes."""
 import numpy as np
 import pytest
@@ -35,20 +35,26 @@ def run_logits(hip, ctx, orc, ex, N, n_exp, k, norm, seed, xseed):
     return x, out, sel, w
 
 
+@pytest.mark.parametrize("family", ["expert", "prepass"])
 @pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
-def test_ctx_config4_olmoe_q2k_from_logits(hipo, orc, mode):
-    """config 4: 64 Q2_K experts (gate/up 1024x2048, down 2048x1024), 128 tokens top-8: the pre-pass + matrix-core family"""
+def test_ctx_config4_olmoe_q2k_from_logits(hipo, orc, mode, family):
+    """config 4: 64 Q2_K experts (gate/up 1024x2048, down 2048x1024), 128 tokens top-8: the expert-sized kernel family
+    (default) and the pre-pass + matrix-core family (the expert kernel switched off)"""
     hipo.set_order(mode[0])
-    n, ff, n_exp, k, N = 2048, 1024, 64, 8, 128
-    types = (E.Q2_K, E.Q2_K, E.Q2_K)
-    ex = Experts(hipo, orc, types, n_exp, n, ff, 46)
-    ctx = hipo.moe_ctx(ex.args(np.zeros(1, np.int32), np.zeros((1, k), np.int32), np.zeros((1, k), np.float32)), N, k)
-    x, out, sel, w = run_logits(hipo, ctx, orc, ex, N, n_exp, k, False, 1238, 11)
-    want_sel, want_w = routed(orc, N, n_exp, k, False, 1238)
-    assert np.array_equal(sel, want_sel) and np.array_equal(bits(w), bits(want_w))
-    ref = orc.moe_ffn(types, ex.host, n, ff, x, want_sel, want_w, order=mode[1], path=mode[2])
-    assert np.array_equal(bits(out), bits(ref))
-    ctx.close()
+    prev = hipo.set_q2k_expert_max_batch(64 if family == "expert" else 1)
+    try:
+        n, ff, n_exp, k, N = 2048, 1024, 64, 8, 128
+        types = (E.Q2_K, E.Q2_K, E.Q2_K)
+        ex = Experts(hipo, orc, types, n_exp, n, ff, 46)
+        ctx = hipo.moe_ctx(ex.args(np.zeros(1, np.int32), np.zeros((1, k), np.int32), np.zeros((1, k), np.float32)), N, k)
+        x, out, sel, w = run_logits(hipo, ctx, orc, ex, N, n_exp, k, False, 1238, 11)
+        want_sel, want_w = routed(orc, N, n_exp, k, False, 1238)
+        assert np.array_equal(sel, want_sel) and np.array_equal(bits(w), bits(want_w))
+        ref = orc.moe_ffn(types, ex.host, n, ff, x, want_sel, want_w, order=mode[1], path=mode[2])
+        assert np.array_equal(bits(out), bits(ref))
+        ctx.close()
+    finally:
+        hipo.set_q2k_expert_max_batch(prev)
 
 
 def test_ctx_config5_qwen3_mixed_from_logits(hipo, orc):
