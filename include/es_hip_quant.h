@@ -294,6 +294,11 @@ int es_hip_set_q3k_mfma_min_batch(int n);
  * (no pre-pass). Larger batches, or all with n < 2, run on the LDS-staged Q2_K kernel of es_hip_set_q2k_mfma_min_batch.
  * Results are identical on every kernel. Returns the previous value. */
 int es_hip_set_q2k_expert_max_batch(int n);
+/* Q4_0 / Q5_0 / Q8_0 batches that run on the matrix cores (es_hip_set_batched32_mfma_min) and have rows of at most 4096
+ * columns use, with on != 0 (the default), the kernel that copies the activations' Q8_0 rows into LDS once per tile of
+ * 16 rows x 32 activations (no pre-pass); with 0, the one that reads them from a pre-pass layout. Results are identical
+ * on both. Returns the previous setting. */
+int es_hip_set_batched32_direct(int on);
 /* ---- activation preparation on the device ---------------------------------------------------------------------------
  * es_act_prepare (src/es_quant.c:499-512) for `rows` rows of `cols` fp32 values in device memory: q80 (when non-NULL;
  * cols % 32 == 0) receives cols/32 Q8_0 blocks per row exactly as quantize_q80 (src/es_quant.c:489-497) writes them, q8k

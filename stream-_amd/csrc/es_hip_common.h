@@ -103,6 +103,13 @@ constexpr int MX_TOK = 32, MX_ROWS = 256, MX_NBK = 16;
 int mx_nbk_max(int nbk);
 hipError_t mx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single,
                      int grid, int order, hipStream_t s);
+// Batched 32-wide formats reading the activations' Q8_0 rows directly (es_hip_mbx.hip): the same jobs, workgroup tiles of
+// MBX_ROWS rows x MBX_TOK activations (tile ids as in the expert-sized kernel), rows of at most MBX_NBK blocks (the whole
+// row's activations sit in LDS); mbx_nbk_max gives the LDS size class of a launch's longest row (0: too long).
+constexpr int MBX_TOK = 32, MBX_ROWS = 16, MBX_NBK = 128;
+int mbx_nbk_max(int nbk);
+hipError_t mbx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single, int grid,
+                      int order, hipStream_t s);
 // gather: some job of the launch reads its activation rows through arow (a separate kernel build; the others need not)
 hipError_t mk_launch(int type, bool gather, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
                      hipStream_t s);

@@ -172,9 +172,14 @@ __global__ __launch_bounds__(256) void mb32m_kernel(const MbJob *__restrict__ jo
     // p's MFMAs are issued before block p - 1's chains; the stage is refilled with block b0 + p + P right after its issue.
     Stage st[P];
     Issued io[2];
+    // The first P loads are unconditional (stages past the last block load the last block again, unused): with a branch
+    // around them the compiler's waits at the top of the main loop drained every load in flight (vmcnt(0)), exposing the
+    // full memory latency once per chunk.
 #pragma unroll
-    for (int p = 0; p < P; p++)
-        if (p < nbk) load(st[p], p, p & 1);
+    for (int p = 0; p < P; p++) {
+        const int b = min(p, nbk - 1);
+        load(st[p], b, b & 1);
+    }
     int b0 = 0;
     for (; b0 + 2 * P <= nbk; b0 += P) {   // every refill in range: no conditions
 #pragma unroll

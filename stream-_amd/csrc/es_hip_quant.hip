@@ -265,6 +265,7 @@ std::atomic<int> g_mk_min_tiles{128};   // ... and its 64 x 128 tiles per produc
 std::atomic<int> g_mk5_min{8};          // activations per Q5_K product from which the direct-activation kernel is used
 std::atomic<int> g_mk3_min{8};          // ... per Q3_K product
 std::atomic<int> g_mx_max{64};          // activations per Q2_K product up to which the expert-sized kernel is used (2+)
+std::atomic<int> g_mbx_on{1};           // batched 32-wide products on the kernel reading Q8_0 rows (0: the pre-pass one)
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
     const uint8_t *act;
@@ -298,6 +299,7 @@ struct MkGroup {   // one direct-activation matrix-core launch: products of one 
     int type;
     bool gather;
     int nbkm = 0;     // > 0: the expert-sized kernel (es_hip_mx.hip) in LDS size class nbkm
+    bool b32 = false; // ... or with nbkm, the 32-wide kernel reading Q8_0 rows (es_hip_mbx.hip)
     int grid = 0;
     std::vector<esq::MkJob> jobs;
     size_t off = 0;
@@ -431,13 +433,46 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
         if (int rc = check_req(q, f)) return rc;
         if (mb_eligible(q)) {   // batched 32-wide: activation groups of at most 64
-            const int mm = g_mbm_min.load();   // (the matrix-core kernel addresses a matrix with 32-bit offsets)
+            const int mm = g_mbm_min.load();   // (the matrix-core kernels address a matrix with 32-bit offsets)
             const bool mfma = mm > 0 && q.na >= mm && (size_t)q.r1 * (q.cols / 32) * f.bb < ((size_t)1 << 31);
+            const int nbk32 = q.cols / 32;
+            const size_t arows = q.arow ? (size_t)std::max(q.act_rows, 0) : (size_t)q.na;
+            const size_t astride = q.astride ? q.astride : (size_t)nbk32 * f.ab;
+            if (mfma && g_mbx_on.load() && esq::mbx_nbk_max(nbk32) && (!q.arow || q.act_rows > 0) &&
+                arows * astride < ((size_t)1 << 32) - 65536) {
+                // the matrix-core kernel reading the Q8_0 rows: MBX_ROWS x MBX_TOK tiles, no pre-pass
+                const int nbkm = esq::mbx_nbk_max(nbk32);
+                MkGroup *g = nullptr;
+                for (MkGroup &x : bt.mkg)
+                    if (x.b32 && x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == nbkm) g = &x;
+                if (!g) {
+                    bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr, nbkm});
+                    g = &bt.mkg.back();
+                    g->b32 = true;
+                }
+                esq::MkJob j{};
+                j.W = static_cast<const uint8_t *>(q.W);
+                j.act = static_cast<const uint8_t *>(q.act);
+                j.arow = q.arow;
+                j.y = q.y;
+                j.astride = astride;
+                j.ystride = q.ystride;
+                j.row_bytes = (uint64_t)nbk32 * f.bb;
+                j.r0 = q.r0;
+                j.r1 = q.r1;
+                j.cols = q.cols;
+                j.na = q.na;
+                j.tile0 = g->grid;
+                j.ntok_tiles = (q.na + esq::MBX_TOK - 1) / esq::MBX_TOK;
+                const int row_tiles = (q.r1 - q.r0 + esq::MBX_ROWS - 1) / esq::MBX_ROWS;
+                g->grid += j.ntok_tiles == 1 ? row_tiles : 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
+                g->jobs.push_back(j);
+                continue;
+            }
             MbGroup *g = nullptr;
             for (MbGroup &x : bt.mbg)
                 if (x.type == (int)q.type && x.mfma == mfma) g = &x;
             if (!g) { bt.mbg.push_back(MbGroup{(int)q.type, mfma}); g = &bt.mbg.back(); }
-            const int nbk32 = q.cols / 32;
             const int tstep = mfma ? esq::MB32M_TOKENS : 64;
             const Prep *pp = mfma ? &get_prep(bt, q, f, esq::PREP_KIND_Q80, (q.na + 31) / 32 * 32) : nullptr;
             for (int t0 = 0; t0 < q.na; t0 += tstep) {
@@ -474,7 +509,7 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             const int nbkm = esq::mx_nbk_max(nbk);
             MkGroup *g = nullptr;
             for (MkGroup &x : bt.mkg)
-                if (x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == nbkm) g = &x;
+                if (!x.b32 && x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == nbkm) g = &x;
             if (!g) { bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr, nbkm}); g = &bt.mkg.back(); }
             esq::MkJob j{};
             j.W = static_cast<const uint8_t *>(q.W);
@@ -498,7 +533,7 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         if (mk_eligible(q)) {   // one launch per format; MK_ROWS x MK_TOK tiles, 8 consecutive ids per row tile group
             MkGroup *g = nullptr;
             for (MkGroup &x : bt.mkg)
-                if (x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == 0) g = &x;
+                if (!x.b32 && x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == 0) g = &x;
             if (!g) { bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr}); g = &bt.mkg.back(); }
             esq::MkJob j{};
             j.W = static_cast<const uint8_t *>(q.W);
@@ -682,8 +717,9 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
     }
     for (const MkGroup &g : bt.mkg) {
         const esq::MkJob *dj = tables ? reinterpret_cast<const esq::MkJob *>(tables + g.off) : nullptr;
-        if ((e = g.nbkm ? esq::mx_launch(g.type, g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
-                        : esq::mk_launch(g.type, g.gather, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+        if ((e = g.b32    ? esq::mbx_launch(g.type, g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
+                 : g.nbkm ? esq::mx_launch(g.type, g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
+                          : esq::mk_launch(g.type, g.gather, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
             return hip_fail(e, "matrix-core launch");
     }
     for (const MbGroup &g : bt.mbg) {
@@ -1049,6 +1085,7 @@ int es_hip_set_direct_mfma_min_tiles(int n) { return g_mk_min_tiles.exchange(n);
 int es_hip_set_q5k_mfma_min_batch(int n) { return g_mk5_min.exchange(n); }
 int es_hip_set_q3k_mfma_min_batch(int n) { return g_mk3_min.exchange(n); }
 int es_hip_set_q2k_expert_max_batch(int n) { return g_mx_max.exchange(n); }
+int es_hip_set_batched32_direct(int on) { return g_mbx_on.exchange(on ? 1 : 0); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }

@@ -1,8 +1,10 @@
-"""GPU parity of the batched Q4_0 / Q5_0 / Q8_0 kernels, the matrix-core one (es_hip_mb.hip: one int8 MFMA per block for 4 rows x
-32 activations, chains in registers, 8 blocks in flight) and the one-lane-per-output one (es_hip_mv.hip): bit-identical to
-the oracle in every reference order and to the vector kernel, over activation counts that exercise every lane split and
-token tile (2 .. 64 per group, several groups), ragged row counts, rows of every block count around the load pipeline's
-depth, 2-byte aligned rows, extreme codes and padded strides."""
+"""GPU parity of the batched Q4_0 / Q5_0 / Q8_0 kernels, each test run on all three: the matrix-core one reading the
+activations' Q8_0 rows from LDS ("direct", es_hip_mbx.hip: one int8 MFMA per block for 4 rows x 32 activations), the
+matrix-core one reading a pre-pass layout ("mfma", es_hip_mb.hip) and the one-lane-per-output one ("lanes",
+es_hip_mv.hip): bit-identical to the oracle in every reference order and to the vector kernel, over activation counts that
+exercise every lane split and token tile (2 .. 64 per group, several groups, 130), ragged row counts, rows of every block
+count around the load pipeline's depth and across the direct kernel's LDS size classes (up to 128 blocks, and past them,
+where the pre-pass kernel takes over), 2-byte aligned rows, extreme codes and padded strides."""
 import numpy as np
 import pytest
 
@@ -19,16 +21,18 @@ def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-KERNELS = {"mfma": 2, "lanes": 0}   # es_hip_set_batched32_mfma_min for each kernel
+KERNELS = {"direct": (2, 1), "mfma": (2, 0), "lanes": (0, 0)}   # (es_hip_set_batched32_mfma_min, _direct) per kernel
 
 
 @pytest.fixture(params=list(KERNELS))
 def hipb(hip, request):
     prev = hip.set_batched32_min(2)
-    prevm = hip.set_batched32_mfma_min(KERNELS[request.param])
+    prevm = hip.set_batched32_mfma_min(KERNELS[request.param][0])
+    prevd = hip.set_batched32_direct(KERNELS[request.param][1])
     yield hip
     hip.set_batched32_min(prev)
     hip.set_batched32_mfma_min(prevm)
+    hip.set_batched32_direct(prevd)
     hip.set_order(E.ORDER_X86_CONTRACT)
 
 
@@ -75,11 +79,12 @@ def test_batched32_equals_vector_kernel_with_ranges(hipb, orc, t):
 
 
 @pytest.mark.parametrize("t", [O.Q4_0, O.Q5_0, O.Q8_0], ids=["q4_0", "q5_0", "q8_0"])
-@pytest.mark.parametrize("cols", [32, 96, 224, 256, 288, 544, 2080])
+@pytest.mark.parametrize("cols", [32, 96, 224, 256, 288, 544, 2080, 3104, 4096, 4128])
 @pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
 def test_batched32_block_counts(hipb, orc, t, cols, mode):
-    """1 .. 65 blocks per row: fewer than, exactly and just past the 8 blocks the matrix-core kernel keeps in flight; odd
-    block counts give rows that start only 2-byte aligned"""
+    """1 .. 129 blocks per row: fewer than, exactly and just past the 8 blocks the matrix-core kernels keep in flight, the
+    direct kernel's LDS size classes (32, 64, 128 blocks) and one block past the last; odd block counts give rows that
+    start only 2-byte aligned"""
     hipb.set_order(mode[0])
     rows, na = 45, 33
     W, acts = inputs(orc, t, rows, cols, na, cols + t)
