@@ -299,6 +299,11 @@ int es_hip_set_q2k_expert_max_batch(int n);
  * 16 rows x 32 activations (no pre-pass); with 0, the one that reads them from a pre-pass layout. Results are identical
  * on both. Returns the previous setting. */
 int es_hip_set_batched32_direct(int on);
+/* A Q6_K product on the matrix cores that is alone in its launch, has one tile of activations (at most 64) and short
+ * rows (at most 5 superblocks at 64 activations, 11 at 32, 22 at 16) runs, with on != 0 (the default), as a persistent
+ * launch: one workgroup per CU copies the activations into LDS once and streams its row tiles back to back. Results
+ * are identical either way. Returns the previous setting. */
+int es_hip_set_q6k_persistent(int on);
 /* ---- activation preparation on the device ---------------------------------------------------------------------------
  * es_act_prepare (src/es_quant.c:499-512) for `rows` rows of `cols` fp32 values in device memory: q80 (when non-NULL;
  * cols % 32 == 0) receives cols/32 Q8_0 blocks per row exactly as quantize_q80 (src/es_quant.c:489-497) writes them, q8k

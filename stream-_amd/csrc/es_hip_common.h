@@ -100,6 +100,9 @@ struct MkJob {
 // activations sit in LDS). nbk_max: the longest row of the launch; mx_nbk_max gives the LDS size class it runs in (0: too
 // long).
 constexpr int MX_TOK = 32, MX_ROWS = 256, MX_NBK = 16;
+// the Q6_K matrix-core kernel's persistent form for single products (es_hip_mm6.hip): on (default) or off; returns the
+// previous setting
+int mm6_set_persistent(int on);
 int mx_nbk_max(int nbk);
 hipError_t mx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single,
                      int grid, int order, hipStream_t s);
@@ -132,12 +135,13 @@ struct PrepJob {
     int na, na_pad, nbk, kind;
 };
 hipError_t prep_launch(const PrepJob *jobs, int njobs, const PrepJob &single, long total, hipStream_t s);
+// hjobs: the same jobs in host memory when the caller has them (the Q6_K form may then launch per job)
 hipError_t mm_launch(int type, int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
-                     hipStream_t s);
+                     hipStream_t s, const MmJob *hjobs = nullptr);
 bool mm_tile_ok(int bm, int bn, int nw);   // a workgroup tile (rows x activations, waves) mm_launch has
 // The Q6_K form (es_hip_mm6.hip): tiles of 128 rows x 16, 32 or 64 activations on 8 waves
 hipError_t mm6_launch(int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
-                      hipStream_t s);
+                      hipStream_t s, const MmJob *hjobs = nullptr);
 // The Q2_K form (es_hip_mm2.hip): tiles of 128 rows x 16, 32 or 64 activations on 8 waves
 hipError_t mm2_launch(int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
                       hipStream_t s);

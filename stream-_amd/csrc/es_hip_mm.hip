@@ -417,8 +417,8 @@ bool mm_tile_ok(int bm, int bn, int nw) {
 }
 
 hipError_t mm_launch(int type, int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
-                     hipStream_t s) {
-    if (type == ES_HIP_Q6_K) return mm6_launch(bm, bn, nw, jobs, njobs, single, grid, order, s);
+                     hipStream_t s, const MmJob *hjobs) {
+    if (type == ES_HIP_Q6_K) return mm6_launch(bm, bn, nw, jobs, njobs, single, grid, order, s, hjobs);
     if (type == ES_HIP_Q2_K) return mm2_launch(bm, bn, nw, jobs, njobs, single, grid, order, s);
     if (type != ES_HIP_Q4_K) return hipErrorInvalidValue;
     if (nw == 8) {

@@ -20,6 +20,9 @@
 // activation operand is the natural 16-element chunk g of the activation row, as in the pre-pass planes.
 #include "es_hip_common.h"
 
+#include <algorithm>
+#include <atomic>
+
 namespace esq {
 
 template <int RW, int TW, int WN> struct Mm6Geom {
@@ -30,27 +33,45 @@ template <int RW, int TW, int WN> struct Mm6Geom {
     static constexpr int M_OFF = X_OFF + BN * 256, D_OFF = M_OFF + BN * 32, STAGE = D_OFF + (BN * 4 + 15) / 16 * 16;
     static constexpr int SW = (CW + NT - 1) / NT, SX = (CX + NT - 1) / NT;   // chunks per thread
     static constexpr int LDS = 2 * STAGE;
+    // persistent form: two stages of weights (and d) only, then the activations of every superblock (NBKP at most)
+    static constexpr int WST = X_OFF, XSB = STAGE - X_OFF, ACT0 = 2 * WST, NBKP = (160 * 1024 - ACT0) / XSB;
+    static constexpr int LDSP = ACT0 + NBKP * XSB;
     static_assert(NW == 8, "8 waves");
-    static_assert(LDS <= 160 * 1024, "two stages fit the LDS");
+    static_assert(LDS <= 160 * 1024 && LDSP <= 160 * 1024, "two stages fit the LDS");
     static_assert(BM <= NT, "one d per thread");
 };
 
 // RW x TW waves: RW along the rows, TW along the activations; WN: 16 x 16 MFMA tiles per wave along the activations.
 // CONTRACT: the clang order (fused multiply-adds), else the gcc / scalar order.
-template <int RW, int TW, int WN, bool CONTRACT>
+// PERS: the persistent form for one product of one activation tile with at most NBKP superblocks per row (config 3's
+// head at 64 activations): a workgroup per CU takes row tiles blockIdx.x, + gridDim.x, ...; the activations of every
+// superblock are copied into LDS once, and the weights of (row tile, superblock) items stream through the two stages
+// back to back, so no row tile pays the pipeline's start (job lookup, first loads, first stage write) again.
+template <int RW, int TW, int WN, bool CONTRACT, bool PERS>
 __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__restrict__ jobs, int njobs, MmJob single) {
     using G = Mm6Geom<RW, TW, WN>;
-    __shared__ __align__(16) uint8_t smem[G::LDS];
+    __shared__ __align__(16) uint8_t smem[PERS ? G::LDSP : G::LDS];
 
     MmJob J;
     if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
-    // XCD-aware tile order, as in the Q4_K kernel: all activation tiles of row tile rt on one XCD
-    const int tile = blockIdx.x - J.tile0;
-    const int x = tile & 7, kq = tile >> 3;
-    const int rt = x + 8 * (kq / J.ntok_tiles), tt = kq % J.ntok_tiles;
-    if (rt * G::BM >= J.r1 - J.r0) return;
-    const int row0 = J.r0 + rt * G::BM, tok0 = tt * G::BN;
+    int rt, tt, ntile;
+    if constexpr (PERS) {   // row tiles blockIdx.x + i * gridDim.x, i < ntile; one activation tile
+        const int rtiles = (J.r1 - J.r0 + G::BM - 1) / G::BM;
+        rt = blockIdx.x;
+        tt = 0;
+        ntile = rt < rtiles ? (rtiles - 1 - rt) / (int)gridDim.x + 1 : 0;
+        if (ntile == 0) return;
+    } else {
+        // XCD-aware tile order, as in the Q4_K kernel: all activation tiles of row tile rt on one XCD
+        const int tile = blockIdx.x - J.tile0;
+        const int x = tile & 7, kq = tile >> 3;
+        rt = x + 8 * (kq / J.ntok_tiles);
+        tt = kq % J.ntok_tiles;
+        ntile = 1;
+        if (rt * G::BM >= J.r1 - J.r0) return;
+    }
+    const int tok0 = tt * G::BN;
     const int nbk = J.cols / 256;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wr = (wave % RW) * 16, wt = (wave / RW) * 16 * WN;   // this wave's rows / activations in the tile
@@ -59,19 +80,19 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
     // ---- this thread's share of a stage: weight chunk c = tid + NT*k (row c / 13, 16-byte piece c % 13 of its first 208
     // bytes; rows past the end repeat the last one, their results are not stored), d of row tid, activation chunk
     // tid + NT*k (values, swizzled: chunk q of activation t at slot q ^ (t & 15); bsums; scales, four activations a chunk)
-    const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
-    const int last_row = J.r1 - 1 - row0;
+    // (PERS: the chunk's row and piece, clamped per row tile at each load; else the chunk's offset in the one row tile)
+    const int row00 = J.r0 + rt * G::BM;
     uint32_t wsrc[G::SW], wdst[G::SW], xsrc[G::SX], xstep[G::SX], xdst[G::SX];
     bool wok[G::SW], xok[G::SX];
 #pragma unroll
     for (int k = 0; k < G::SW; k++) {
         const int c = tid + G::NT * k;
         wok[k] = c < G::CW;
-        wsrc[k] = (uint32_t)min(c / 13, last_row) * (uint32_t)J.row_bytes + 16 * (c % 13);
+        wsrc[k] = PERS ? (uint32_t)(c / 13) << 8 | (uint32_t)(16 * (c % 13))
+                       : (uint32_t)min(c / 13, J.r1 - 1 - row00) * (uint32_t)J.row_bytes + 16 * (c % 13);
         wdst[k] = 16 * c;
     }
     const bool dok = tid < G::BM;
-    const uint32_t dsrc = (uint32_t)min(tid, last_row) * (uint32_t)J.row_bytes + 208;
     const uint32_t xm_rel = (uint32_t)(J.xm - J.xq), xd_rel = xm_rel + (uint32_t)nbk * J.na_pad * 32;
 #pragma unroll
     for (int k = 0; k < G::SX; k++) {
@@ -94,28 +115,52 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
             xdst[k] = G::D_OFF + 16 * t4;
         }
     }
-    // the global loads of superblock bi into registers, and their LDS writes into stage st
+    // item it = (row tile rt + (it / nbk) * gridDim.x, superblock it % nbk): the global loads of its weights (and, unless
+    // PERS, of its activations) into registers, and their LDS writes into stage st
+    constexpr int STG = PERS ? G::WST : G::STAGE;
     uint4 rw[G::SW], rx[G::SX];
     uint32_t rd = 0;
-    auto gload = [&](int bi) {
+    auto gload = [&](int it) {
+        const int ti = PERS ? it / nbk : 0, bi = it - ti * nbk;
+        const int row0 = row00 + ti * (int)gridDim.x * G::BM, last_row = J.r1 - 1 - row0;
+        const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes + 210u * bi;
 #pragma unroll
-        for (int k = 0; k < G::SW; k++)
-            if (wok[k]) rw[k] = ldg_u128_a2(wbase + 210u * bi + wsrc[k]);
-        if (dok) rd = ldg<uint16_t>(wbase + 210u * bi + dsrc);
+        for (int k = 0; k < G::SW; k++) {
+            if (!wok[k]) continue;
+            if constexpr (PERS)
+                rw[k] = ldg_u128_a2(wbase + (uint32_t)min((int)(wsrc[k] >> 8), last_row) * (uint32_t)J.row_bytes + (wsrc[k] & 255u));
+            else
+                rw[k] = ldg_u128_a2(wbase + wsrc[k]);
+        }
+        if (dok) rd = ldg<uint16_t>(wbase + (uint32_t)min(tid, last_row) * (uint32_t)J.row_bytes + 208);
+        if constexpr (!PERS) {
 #pragma unroll
-        for (int k = 0; k < G::SX; k++)
-            if (xok[k]) rx[k] = ldg<uint4>(J.xq + xsrc[k] + (uint32_t)bi * xstep[k]);
+            for (int k = 0; k < G::SX; k++)
+                if (xok[k]) rx[k] = ldg<uint4>(J.xq + xsrc[k] + (uint32_t)bi * xstep[k]);
+        }
     };
     auto lstore = [&](int st) {
-        uint8_t *sb = smem + st * G::STAGE;
+        uint8_t *sb = smem + st * STG;
 #pragma unroll
         for (int k = 0; k < G::SW; k++)
             if (wok[k]) *reinterpret_cast<uint4 *>(sb + wdst[k]) = rw[k];
         if (dok) *reinterpret_cast<uint16_t *>(sb + G::D_W + 2 * tid) = (uint16_t)rd;
+        if constexpr (!PERS) {
 #pragma unroll
-        for (int k = 0; k < G::SX; k++)
-            if (xok[k]) *reinterpret_cast<uint4 *>(sb + xdst[k]) = rx[k];
+            for (int k = 0; k < G::SX; k++)
+                if (xok[k]) *reinterpret_cast<uint4 *>(sb + xdst[k]) = rx[k];
+        }
     };
+    if constexpr (PERS) {   // every superblock's activations into their own LDS region, once
+        for (int bi = 0; bi < nbk; bi++) {
+#pragma unroll
+            for (int k = 0; k < G::SX; k++)
+                if (xok[k]) rx[k] = ldg<uint4>(J.xq + xsrc[k] + (uint32_t)bi * xstep[k]);
+#pragma unroll
+            for (int k = 0; k < G::SX; k++)
+                if (xok[k]) *reinterpret_cast<uint4 *>(smem + G::ACT0 + bi * G::XSB + (xdst[k] - G::X_OFF)) = rx[k];
+        }
+    }
 
     uint32_t xo[4];   // activation chunk offsets of this lane in a stage (tile c adds 4096*c): chunk 4ks + lg
 #pragma unroll
@@ -131,21 +176,25 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
 #pragma unroll
         for (int i = 0; i < 4; i++) s[c][i] = 0.0f;
 
-    // Two stages. Superblock b+1's loads went out during superblock b-1 (into registers); at the top of b they are written
-    // to stage (b+1) & 1, whose last readers finished b-1 (barrier), and superblock b+2's loads go out.
+    // Two stages. Item it+1's loads went out during item it-1 (into registers); at the top of it they are written to
+    // stage (it+1) & 1, whose last readers finished it-1 (barrier), and item it+2's loads go out.
+    const int nitem = ntile * nbk;
     gload(0);
     lstore(0);
-    if (nbk > 1) gload(1);
-    for (int b = 0; b < nbk; b++) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's LDS writes of stage b and reads of b-1 are done
+    if (nitem > 1) gload(1);
+    for (int it = 0; it < nitem; it++) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's LDS writes of stage it and reads of it-1 are done
         __builtin_amdgcn_s_barrier();                         // ... and every wave's
         asm volatile("" ::: "memory");
-        const uint8_t *wb = smem + (b & 1) * G::STAGE;
-        if (b + 1 < nbk) {
-            lstore((b + 1) & 1);
-            if (b + 2 < nbk) gload(b + 2);
+        const int ti = PERS ? it / nbk : 0, b = it - ti * nbk;
+        const uint8_t *wb = smem + (it & 1) * STG;
+        // the activation operands: in the stage, or (PERS) in superblock b's region, addressed as if it were a stage
+        const uint8_t *xb = PERS ? smem + G::ACT0 + b * G::XSB - G::X_OFF : wb;
+        if (it + 1 < nitem) {
+            lstore((it + 1) & 1);
+            if (it + 2 < nitem) gload(it + 2);
         }
-        __builtin_amdgcn_sched_barrier(0);   // the loads stay here, a whole superblock ahead of their LDS writes
+        __builtin_amdgcn_sched_barrier(0);   // the loads stay here, a whole item ahead of their LDS writes
 
         // LDS reads in the order they are needed: the weight fields, the row scales, then activation tile 0
         const uint8_t *rowp = wb + rowoff;
@@ -158,9 +207,9 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
         struct Bt { v4i x[4]; v8h m; float td; };
         auto load_b = [&](int c, Bt &B) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) B.x[ks] = *reinterpret_cast<const v4i *>(wb + xo[ks] + 4096 * c);
-            B.m = *reinterpret_cast<const v8h *>(wb + mo + 512 * c);
-            B.td = *reinterpret_cast<const float *>(wb + dof + 64 * c);
+            for (int ks = 0; ks < 4; ks++) B.x[ks] = *reinterpret_cast<const v4i *>(xb + xo[ks] + 4096 * c);
+            B.m = *reinterpret_cast<const v8h *>(xb + mo + 512 * c);
+            B.td = *reinterpret_cast<const float *>(xb + dof + 64 * c);
         };
         Bt B[2];
         load_b(0, B[0]);
@@ -252,44 +301,79 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
             __builtin_amdgcn_sched_barrier(0);
         }
         epi(WN - 1);
-        asm volatile("" ::: "memory");   // stage b's LDS reads stay before the next superblock's barrier
-    }
+        asm volatile("" ::: "memory");   // stage it's LDS reads stay before the next item's barrier
 
-    // ---- outputs
+        if (b == nbk - 1) {   // ---- the row tile's outputs
+            const int row0 = row00 + ti * (int)gridDim.x * G::BM;
 #pragma unroll
-    for (int c = 0; c < WN; c++) {
-        const int t = tok0 + wt + 16 * c + lr;
-        if (t >= J.na) continue;
-        const int r = row0 + wr + 4 * lg;   // this lane holds rows r .. r+3 of activation t
-        float *yp = J.y + (size_t)t * J.ystride + r;
-        if (r + 3 < J.r1 && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
-            stg<float4>(yp, make_float4(s[c][0], s[c][1], s[c][2], s[c][3]));
-        } else {
+            for (int c = 0; c < WN; c++) {
+                const int t = tok0 + wt + 16 * c + lr;
+                if (t < J.na) {
+                    const int r = row0 + wr + 4 * lg;   // this lane holds rows r .. r+3 of activation t
+                    float *yp = J.y + (size_t)t * J.ystride + r;
+                    if (r + 3 < J.r1 && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
+                        stg<float4>(yp, make_float4(s[c][0], s[c][1], s[c][2], s[c][3]));
+                    } else {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (r + i < J.r1) stg<float>(yp + i, s[c][i]);
+                        for (int i = 0; i < 4; i++)
+                            if (r + i < J.r1) stg<float>(yp + i, s[c][i]);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[c][i] = 0.0f;
+            }
         }
     }
 }
 
+std::atomic<int> g_mm6_persistent{1};
+
 template <int RW, int TW, int WN>
-static hipError_t mm6_launch_cfg(const MmJob *jobs, int njobs, const MmJob &single, int grid, int order, hipStream_t s) {
-    if (order == ES_HIP_ORDER_X86_CONTRACT)
-        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, true>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
+static hipError_t mm6_launch_cfg(const MmJob *jobs, int njobs, const MmJob &single, int grid, int order, hipStream_t s,
+                                 const MmJob *hjobs) {
+    using G = Mm6Geom<RW, TW, WN>;
+    const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
+    static const int ncu = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 256;
+        return n > 0 ? n : 256;
+    }();
+    // The persistent form, one launch per product with a workgroup per CU: for a lone product of one activation tile with
+    // short rows, or for a few such products each of at least two row tiles per CU (a head or projection per call, or
+    // their copies in one batch). Otherwise the tiled form.
+    auto rtiles = [](const MmJob &j) { return (j.r1 - j.r0 + G::BM - 1) / G::BM; };
+    auto fits = [&](const MmJob &j) { return j.ntok_tiles == 1 && j.cols / 256 <= G::NBKP; };
+    bool pers = g_mm6_persistent.load() && (njobs == 1 ? fits(single) : hjobs != nullptr && njobs <= 16);
+    for (int i = 0; pers && njobs > 1 && i < njobs; i++) pers = fits(hjobs[i]) && rtiles(hjobs[i]) >= 2 * ncu;
+    if (pers) {
+        const dim3 b(64 * RW * TW);
+        for (int i = 0; i < njobs; i++) {
+            const MmJob &j = njobs == 1 ? single : hjobs[i];
+            const dim3 g(std::min(rtiles(j), ncu));
+            if (contract) hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, true, true>), g, b, 0, s, nullptr, 1, j);
+            else hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, false, true>), g, b, 0, s, nullptr, 1, j);
+        }
+        return hipGetLastError();
+    }
+    if (contract)
+        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, true, false>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
     else
-        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, false>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
+        hipLaunchKernelGGL((mm_q6k_kernel<RW, TW, WN, false, false>), dim3(grid), dim3(64 * RW * TW), 0, s, jobs, njobs, single);
     return hipGetLastError();
 }
+
+int mm6_set_persistent(int on) { return g_mm6_persistent.exchange(on ? 1 : 0); }
 
 // Q6_K workgroup tiles: 128 rows x 16, 32 or 64 activations on 8 waves (16 rows x all the activations each)
 bool mm6_tile_ok(int bm, int bn, int nw) { return nw == 8 && bm == 128 && (bn == 16 || bn == 32 || bn == 64); }
 
 hipError_t mm6_launch(int bm, int bn, int nw, const MmJob *jobs, int njobs, const MmJob &single, int grid, int order,
-                      hipStream_t s) {
+                      hipStream_t s, const MmJob *hjobs) {
     if (nw == 8 && bm == 128) {
-        if (bn == 64) return mm6_launch_cfg<8, 1, 4>(jobs, njobs, single, grid, order, s);
-        if (bn == 32) return mm6_launch_cfg<8, 1, 2>(jobs, njobs, single, grid, order, s);
-        if (bn == 16) return mm6_launch_cfg<8, 1, 1>(jobs, njobs, single, grid, order, s);
+        if (bn == 64) return mm6_launch_cfg<8, 1, 4>(jobs, njobs, single, grid, order, s, hjobs);
+        if (bn == 32) return mm6_launch_cfg<8, 1, 2>(jobs, njobs, single, grid, order, s, hjobs);
+        if (bn == 16) return mm6_launch_cfg<8, 1, 1>(jobs, njobs, single, grid, order, s, hjobs);
     }
     return hipErrorInvalidValue;
 }

@@ -712,7 +712,8 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
     }
     for (const MmGroup &g : bt.mmg) {
         const esq::MmJob *dj = tables ? reinterpret_cast<const esq::MmJob *>(tables + g.off) : nullptr;
-        if ((e = esq::mm_launch(g.type, g.bm, g.bn, g.nw, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+        if ((e = esq::mm_launch(g.type, g.bm, g.bn, g.nw, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s, g.jobs.data())) !=
+            hipSuccess)
             return hip_fail(e, "matrix-core launch");
     }
     for (const MkGroup &g : bt.mkg) {
@@ -1086,6 +1087,7 @@ int es_hip_set_q5k_mfma_min_batch(int n) { return g_mk5_min.exchange(n); }
 int es_hip_set_q3k_mfma_min_batch(int n) { return g_mk3_min.exchange(n); }
 int es_hip_set_q2k_expert_max_batch(int n) { return g_mx_max.exchange(n); }
 int es_hip_set_batched32_direct(int on) { return g_mbx_on.exchange(on ? 1 : 0); }
+int es_hip_set_q6k_persistent(int on) { return esq::mm6_set_persistent(on); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }

@@ -1,7 +1,9 @@
-"""GPU parity of the Q6_K matrix-core path (es_hip_mm6.hip): bit-identical to the oracle in every reference order and to
-the vector kernel, at the config 3 head shape and at ragged edges (rows not a multiple of the 128-row tile, activation
-counts between the 16/32/64-wide tiles and above 64, row sub-ranges, padded strides), and rows of an odd number of
-superblocks (2-byte aligned rows)."""
+"""GPU parity of the Q6_K matrix-core path (es_hip_mm6.hip), each test with its persistent form for single short-row
+products on ("persistent": one workgroup per CU, activations copied into LDS once, row tiles streamed back to back) and
+off ("tiled"): bit-identical to the oracle in every reference order and to the vector kernel, at the config 3 head shape
+and at ragged edges (rows not a multiple of the 128-row tile, activation counts between the 16/32/64-wide tiles and
+above 64, row sub-ranges, padded strides, rows at and past the persistent form's superblock limits), and rows of an odd
+number of superblocks (2-byte aligned rows)."""
 import numpy as np
 import pytest
 
@@ -29,11 +31,13 @@ def inputs(orc, rows, cols, na, seed, gauss=False):
     return W, orc.quantize_act(O.Q6_K, x)
 
 
-@pytest.fixture
-def hip6(hip):
+@pytest.fixture(params=["persistent", "tiled"])
+def hip6(hip, request):
     prev = hip.set_q6k_mfma_min_batch(16)
+    prevp = hip.set_q6k_persistent(request.param == "persistent")
     yield hip
     hip.set_q6k_mfma_min_batch(prev)
+    hip.set_q6k_persistent(prevp)
     hip.set_order(E.ORDER_X86_CONTRACT)
 
 
@@ -48,7 +52,9 @@ def vector_path(hip, fn):
 
 @pytest.mark.parametrize("rows,cols,na,gauss", [(4096, 1024, 64, True), (300, 1024, 64, False), (200, 2048, 40, False),
                                                 (128, 512, 16, True), (77, 512, 23, False), (150, 1024, 130, False),
-                                                (64, 4096, 33, True)])
+                                                (64, 4096, 33, True), (40000, 1280, 64, False), (40000, 1536, 64, False),
+                                                (33000, 2816, 32, False), (20000, 3072, 32, False), (9000, 5888, 16, False),
+                                                (9000, 6144, 16, False)])
 @pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
 def test_q6k_mfma_vs_oracle(hip6, orc, rows, cols, na, gauss, mode):
     hip6.set_order(mode[0])
@@ -133,3 +139,32 @@ def test_q6k_mfma_extreme_codes(hip6, orc):
         y = hip6.matvec_multi(O.Q6_K, W, cols, rows, acts)
         ref = orc.matvec_multi(O.Q6_K, W, cols, rows, acts, mode[1], mode[2])
         assert np.array_equal(bits(y), bits(ref)), mode
+
+
+@pytest.mark.parametrize("na", [64, 20])
+def test_q6k_persistent_batch_equals_tiled(hip, orc, na):
+    """a batch of three large short-row products (each at least two row tiles per CU, one with a row range) through
+    es_hip_run_jobs: the persistent form launched per product equals the tiled form bit for bit, and the oracle on
+    sampled rows"""
+    rows, cols = 70000, 1024
+    W, acts = inputs(orc, rows, cols, na, 77 + na)
+    dW, dA = hip.upload(W), hip.upload(acts)
+    outs = {}
+    for pers in (1, 0):
+        prev = hip.set_q6k_persistent(pers)
+        prevm = hip.set_q6k_mfma_min_batch(16)
+        try:
+            dY = [hip.upload(np.full((na, rows), -5.0, np.float32)) for _ in range(3)]
+            specs = [dict(type=O.Q6_K, rows=rows, cols=cols, W=dW, act=dA, astride=acts.strides[0], nb=na, y=dY[i],
+                          ystride=rows) for i in range(3)]
+            hip.run_jobs(specs)
+            hip.synchronize()
+            outs[pers] = [hip.download(d, np.zeros((na, rows), np.float32)) for d in dY]
+        finally:
+            hip.set_q6k_persistent(prev)
+            hip.set_q6k_mfma_min_batch(prevm)
+    for a, b in zip(outs[1], outs[0]):
+        assert np.array_equal(bits(a), bits(b))
+    sel = np.array([0, 1, 777, 65535, rows - 1])
+    ref = orc.matvec_multi(O.Q6_K, W.reshape(rows, -1)[sel].reshape(-1), cols, len(sel), acts[[0, na - 1]])
+    assert np.array_equal(bits(outs[1][0][[0, na - 1]][:, sel]), bits(ref))
