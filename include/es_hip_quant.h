@@ -304,6 +304,11 @@ int es_hip_set_batched32_direct(int on);
  * launch: one workgroup per CU copies the activations into LDS once and streams its row tiles back to back. Results
  * are identical either way. Returns the previous setting. */
 int es_hip_set_q6k_persistent(int on);
+/* Q5_K and Q3_K products on the direct-activation kernel that would have fewer than 256 tiles of 64 rows x 128
+ * activations run, with on != 0 (the default) and at least 64 activations, in tiles of 64 activations (twice the
+ * workgroups: config 2's down product at T = 512 in those formats). Results are identical either way. Returns the
+ * previous setting. */
+int es_hip_set_direct_mfma_tok64(int on);
 /* ---- activation preparation on the device ---------------------------------------------------------------------------
  * es_act_prepare (src/es_quant.c:499-512) for `rows` rows of `cols` fp32 values in device memory: q80 (when non-NULL;
  * cols % 32 == 0) receives cols/32 Q8_0 blocks per row exactly as quantize_q80 (src/es_quant.c:489-497) writes them, q8k

@@ -113,8 +113,9 @@ constexpr int MBX_TOK = 32, MBX_ROWS = 16, MBX_NBK = 128;
 int mbx_nbk_max(int nbk);
 hipError_t mbx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single, int grid,
                       int order, hipStream_t s);
-// gather: some job of the launch reads its activation rows through arow (a separate kernel build; the others need not)
-hipError_t mk_launch(int type, bool gather, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
+// gather: some job of the launch reads its activation rows through arow (a separate kernel build; the others need not);
+// tok: activations per workgroup tile, MK_TOK or 64 (ntok_tiles and the tile numbering then count tiles of 64)
+hipError_t mk_launch(int type, bool gather, int tok, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
                      hipStream_t s);
 
 // One activation pre-pass: kind 0 writes 16 bytes of meta per activation and superblock (pair sums of the Q4_K

@@ -74,14 +74,16 @@ __device__ __forceinline__ void load_lds4(const uint8_t *base, uint32_t off, uin
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory");
 }
 
-constexpr int MK_WAVES = 4, MK_TT = MK_TOK / 16;
-// one slot of the activation ring: values (one swizzled 256-byte row per activation) | bsums as halves [lg][activation][4]
-// | scales
-constexpr int TROW = 256;
-constexpr int ST_QS = 0, ST_BS = MK_TOK * TROW, ST_D = ST_BS + MK_TOK * 32, ST_BYTES = ST_D + MK_TOK * 4;
-static_assert(2 * 2 * ST_BYTES <= 160 * 1024, "two workgroups' two slots fit the LDS");
+constexpr int MK_WAVES = 4;
 static_assert(MK_ROWS == 16 * MK_WAVES, "four waves of 16 rows");
-static_assert(MK_TOK == 128, "the staging assignment below is written for 128 activations");
+// one slot of the activation ring for T activations: values (one swizzled 256-byte row per activation) | bsums as halves
+// [lg][activation][4] | scales
+constexpr int TROW = 256;
+template <int T> struct MkSlot {
+    static constexpr int QS = 0, BS = T * TROW, D = BS + T * 32, BYTES = D + T * 4, TT = T / 16;
+    static_assert(T == 64 || T == 128, "the staging assignment below is written for 64 or 128 activations");
+    static_assert(2 * 2 * BYTES <= 160 * 1024, "two workgroups' two slots fit the LDS");
+};
 
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
@@ -264,9 +266,12 @@ template <int NMFMA> __device__ __forceinline__ void step_schedule() {
     }
 }
 
-template <int F, bool CONTRACT, bool GATHER>
+// T: activations per workgroup tile, 128, or 64 for products with too few row tiles to fill the device at 128.
+template <int F, bool CONTRACT, bool GATHER, int T>
 __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
     using FM = MkFmt<F>;
+    using SL = MkSlot<T>;
+    constexpr int ST_QS = SL::QS, ST_BS = SL::BS, ST_D = SL::D, ST_BYTES = SL::BYTES, MK_TT = SL::TT;
     constexpr bool FUSED = CONTRACT && F != ES_HIP_Q5_K;   // Q5_K's reference epilogue never fuses
     constexpr bool BSUMS = F != ES_HIP_Q3_K;              // the mins term reads the activations' bsums
     __shared__ __align__(16) uint8_t smem[2 * ST_BYTES];
@@ -281,7 +286,7 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
     const int xcd = tile & 7, kq = tile >> 3;
     const int rt_ = xcd + 8 * (kq / J.ntok_tiles), tt_ = kq % J.ntok_tiles;
     if (rt_ * MK_ROWS >= J.r1 - J.r0) return;
-    const int row0 = J.r0 + rt_ * MK_ROWS, tok0 = tt_ * MK_TOK;
+    const int row0 = J.r0 + rt_ * MK_ROWS, tok0 = tt_ * T;
     const int nbk = J.cols / 256;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lr = lane & 15, lg = lane >> 4;
@@ -292,20 +297,23 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
         const int r = (GATHER && J.arow) ? ldg<int>(J.arow + q) : q;
         return (uint32_t)r * (uint32_t)J.astride;
     };
-    // values: wave w copies activations 32w .. 32w+31, four per instruction: instruction k, lane l: activation
-    // t = 32w + 4k + l/16, LDS position l%16 of its row, so source chunk (l%16) ^ (t & 15)
-    uint32_t qoff[8];
+    // values: wave w copies activations (T/4) w .. (T/4) w + T/4 - 1, four per instruction: instruction k, lane l:
+    // activation t = (T/4) w + 4k + l/16, LDS position l%16 of its row, so source chunk (l%16) ^ (t & 15)
+    constexpr int NV = T / 16;
+    uint32_t qoff[NV];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int t = 32 * wave + 4 * k + (lane >> 4);
+    for (int k = 0; k < NV; k++) {
+        const int t = (T / 4) * wave + 4 * k + (lane >> 4);
         qoff[k] = act_off(t) + 4 + 16 * ((lane & 15) ^ (t & 15));
     }
-    // scales: wave w, lane l copies activation 64(w & 1) + l's d
-    const uint32_t doff = act_off(64 * (wave & 1) + lane);
-    // bsums: every lane, activation bt, bsums 8*bh .. 8*bh+7
-    const int bt = tid >> 1, bh = tid & 1;
+    // scales: wave w, lane l copies activation 64 ds + l's d, ds = w & 1 (at 128 activations; 0 at 64)
+    const int ds = T == 128 ? (wave & 1) : 0;
+    const uint32_t doff = act_off(64 * ds + lane);
+    // bsums: every lane, activation bt, bsums 8*bh .. 8*bh+7 (at 64 activations the upper half of the workgroup repeats the
+    // lower half's copies: the same bytes to the same place)
+    const int bt = (tid >> 1) & (T - 1), bh = tid & 1;
     const uint32_t boff = act_off(bt) + 260 + 16 * bh;
-    const uint32_t bdst0 = ST_BS + (2 * bh) * (MK_TOK * 8) + bt * 8, bdst1 = bdst0 + MK_TOK * 8;
+    const uint32_t bdst0 = ST_BS + (2 * bh) * (T * 8) + bt * 8, bdst1 = bdst0 + T * 8;
     const uint32_t smem0 = lds_addr(smem);
 
     // the superblock's base address, kept opaque in scalar registers (as plain arithmetic the compiler folds it into
@@ -317,11 +325,11 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
     };
     auto stage_dma = [&](int b, int st) {   // values and scales of superblock b into slot st
         const uint8_t *ab = sb_base(b);
-        const uint32_t base = smem0 + (uint32_t)st * ST_BYTES + ST_QS + (uint32_t)(32 * wave) * TROW;
+        const uint32_t base = smem0 + (uint32_t)st * ST_BYTES + ST_QS + (uint32_t)((T / 4) * wave) * TROW;
 #pragma unroll
-        for (int k = 0; k < 8; k++) load_lds16(ab, qoff[k], base + 4 * TROW * k);
-        // waves 2 and 3 repeat waves 0 and 1's copy (the same bytes to the same place), which keeps the code branch-free
-        load_lds4(ab, doff, smem0 + (uint32_t)st * ST_BYTES + ST_D + 256 * (wave & 1));
+        for (int k = 0; k < NV; k++) load_lds16(ab, qoff[k], base + 4 * TROW * k);
+        // the other waves repeat waves 0 and 1's copy (the same bytes to the same place), which keeps the code branch-free
+        load_lds4(ab, doff, smem0 + (uint32_t)st * ST_BYTES + ST_D + 256 * ds);
     };
     auto bs_load = [&](int b) { return ldg<uint4>(sb_base(b) + boff); };
     auto bs_write = [&](const uint4 &v, int st) {
@@ -360,7 +368,7 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
         const int nat = F == ES_HIP_Q3_K ? 8 * (lg >> 1) + 2 * s + (lg & 1) : 4 * (lg >> 1) + 8 * (s >> 1) + 2 * (s & 1) + (lg & 1);
         xo[s] = ST_QS + lr * TROW + 16 * (nat ^ lr);   // rows 16 tt + lr: the swizzle key is lr
     }
-    const uint32_t bso = ST_BS + lg * (MK_TOK * 8) + lr * 8, ydo = ST_D + 16 * lg;
+    const uint32_t bso = ST_BS + lg * (T * 8) + lr * 8, ydo = ST_D + 16 * lg;
     // read addresses: per superblock, the slot's base is added once to these six, and an activation tile's reads differ
     // only in their immediate offsets
     auto aload = [&](const uint32_t (&xa)[4], uint32_t ba, uint32_t ya, int tt, AOps &A) {
@@ -451,25 +459,33 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
 
 }  // namespace
 
-template <int F>
-static void mk_launch_fmt(bool gather, bool contract, const MkJob *jobs, int njobs, const MkJob &single, int grid,
+template <int F, int T>
+static void mk_launch_tok(bool gather, bool contract, const MkJob *jobs, int njobs, const MkJob &single, int grid,
                           hipStream_t s) {
     const dim3 g(grid), b(64 * MK_WAVES);
     if (gather) {
-        if (contract) hipLaunchKernelGGL((mk_kernel<F, true, true>), g, b, 0, s, jobs, njobs, single);
-        else hipLaunchKernelGGL((mk_kernel<F, false, true>), g, b, 0, s, jobs, njobs, single);
+        if (contract) hipLaunchKernelGGL((mk_kernel<F, true, true, T>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mk_kernel<F, false, true, T>), g, b, 0, s, jobs, njobs, single);
     } else {
-        if (contract) hipLaunchKernelGGL((mk_kernel<F, true, false>), g, b, 0, s, jobs, njobs, single);
-        else hipLaunchKernelGGL((mk_kernel<F, false, false>), g, b, 0, s, jobs, njobs, single);
+        if (contract) hipLaunchKernelGGL((mk_kernel<F, true, false, T>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mk_kernel<F, false, false, T>), g, b, 0, s, jobs, njobs, single);
     }
 }
 
-hipError_t mk_launch(int type, bool gather, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
+template <int F>
+static void mk_launch_fmt(int tok, bool gather, bool contract, const MkJob *jobs, int njobs, const MkJob &single, int grid,
+                          hipStream_t s) {
+    if (tok == 64) mk_launch_tok<F, 64>(gather, contract, jobs, njobs, single, grid, s);
+    else mk_launch_tok<F, 128>(gather, contract, jobs, njobs, single, grid, s);
+}
+
+hipError_t mk_launch(int type, bool gather, int tok, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
                      hipStream_t s) {
     const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
-    if (type == ES_HIP_Q4_K) mk_launch_fmt<ES_HIP_Q4_K>(gather, contract, jobs, njobs, single, grid, s);
-    else if (type == ES_HIP_Q5_K) mk_launch_fmt<ES_HIP_Q5_K>(gather, false, jobs, njobs, single, grid, s);   // never fused
-    else if (type == ES_HIP_Q3_K) mk_launch_fmt<ES_HIP_Q3_K>(gather, contract, jobs, njobs, single, grid, s);
+    if (tok != 64 && tok != MK_TOK) return hipErrorInvalidValue;
+    if (type == ES_HIP_Q4_K) mk_launch_fmt<ES_HIP_Q4_K>(tok, gather, contract, jobs, njobs, single, grid, s);
+    else if (type == ES_HIP_Q5_K) mk_launch_fmt<ES_HIP_Q5_K>(tok, gather, false, jobs, njobs, single, grid, s);   // never fused
+    else if (type == ES_HIP_Q3_K) mk_launch_fmt<ES_HIP_Q3_K>(tok, gather, contract, jobs, njobs, single, grid, s);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

@@ -300,6 +300,7 @@ struct MkGroup {   // one direct-activation matrix-core launch: products of one 
     bool gather;
     int nbkm = 0;     // > 0: the expert-sized kernel (es_hip_mx.hip) in LDS size class nbkm
     bool b32 = false; // ... or with nbkm, the 32-wide kernel reading Q8_0 rows (es_hip_mbx.hip)
+    int tok = esq::MK_TOK;   // the direct kernel's activations per tile
     int grid = 0;
     std::vector<esq::MkJob> jobs;
     size_t off = 0;
@@ -375,6 +376,18 @@ bool mx_eligible(const Req &q) {
            ((size_t)q.na + esq::MX_TOK) * mk_ystride(q) * sizeof(float) < ((size_t)1 << 31);
 }
 
+std::atomic<int> g_mk_tok64{1};   // the direct kernel's 64-activation tiles for products short of row tiles (0: never)
+
+// the direct kernel's activations per tile: 64 for Q5_K and Q3_K products when 128 would leave fewer than 256 tiles (a
+// quarter of the device's workgroup slots) and the batch fills at least one 64-wide tile, else MK_TOK. Q4_K's short
+// products keep the LDS-staged kernel instead: config 2's down product at T = 512 took longer on 64-wide direct tiles
+// (the prefill step 90.6 -> 97.2 us) while Q5_K's step, which has no other matrix-core kernel, went 128 -> 119 us.
+int mk_tok(const Req &q) {
+    if (q.type == ES_HIP_Q4_K || !g_mk_tok64.load() || q.na < 64) return esq::MK_TOK;
+    const size_t rt = (size_t)((q.r1 - q.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS);
+    return rt * ((q.na + esq::MK_TOK - 1) / esq::MK_TOK) < 256 ? 64 : esq::MK_TOK;
+}
+
 bool mk_eligible(const Req &q) {
     const bool q5 = q.type == ES_HIP_Q5_K, q3 = q.type == ES_HIP_Q3_K;
     const int mn = q5 ? g_mk5_min.load() : q3 ? g_mk3_min.load() : g_mk_min.load();
@@ -384,11 +397,12 @@ bool mk_eligible(const Req &q) {
     // Tiles (64 rows x 128 activations, one workgroup each) against the K loop each runs: measured on config 2's shapes,
     // this kernel wins from 128 tiles of 8 superblocks (8192 x 2048 at 128 activations: 17 us against 28 us) and loses
     // with 128 tiles of 32 superblocks (2048 x 8192 at 512: 60 us against 45 us, a quarter of the chip's workgroup slots
-    // each running a long chain); from 256 tiles it wins or ties at every depth.
+    // each running a long chain); from 256 tiles it wins or ties at every depth. Products short of row tiles take tiles
+    // of 64 activations (mk_tok), counted here as they run.
     // Q5_K and Q3_K have no other matrix-core kernel: against the decode kernel's passes of 4 activations it wins at any
     // tile count.
-    const int mt = g_mk_min_tiles.load();
-    const size_t tiles = (size_t)((q.r1 - q.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS) * ((q.na + esq::MK_TOK - 1) / esq::MK_TOK);
+    const int mt = g_mk_min_tiles.load(), tok = mk_tok(q);
+    const size_t tiles = (size_t)((q.r1 - q.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS) * ((q.na + tok - 1) / tok);
     if (!q5 && !q3 && (tiles < (size_t)mt || (tiles < 2 * (size_t)mt && q.cols > 16 * 256))) return false;
     // 32-bit offsets: activation rows within 4 GiB of the activation pointer; outputs (with a tile of activations past
     // the last) below 2^31 bytes, the range the kernel's buffer stores are checked against
@@ -530,11 +544,16 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             g->jobs.push_back(j);
             continue;
         }
-        if (mk_eligible(q)) {   // one launch per format; MK_ROWS x MK_TOK tiles, 8 consecutive ids per row tile group
+        if (mk_eligible(q)) {   // one launch per format and tile; MK_ROWS x tok tiles, 8 consecutive ids per row tile group
+            const int tok = mk_tok(q);
             MkGroup *g = nullptr;
             for (MkGroup &x : bt.mkg)
-                if (!x.b32 && x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == 0) g = &x;
-            if (!g) { bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr}); g = &bt.mkg.back(); }
+                if (!x.b32 && x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == 0 && x.tok == tok) g = &x;
+            if (!g) {
+                bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr});
+                g = &bt.mkg.back();
+                g->tok = tok;
+            }
             esq::MkJob j{};
             j.W = static_cast<const uint8_t *>(q.W);
             j.act = static_cast<const uint8_t *>(q.act);
@@ -548,7 +567,7 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             j.cols = q.cols;
             j.na = q.na;
             j.tile0 = g->grid;
-            j.ntok_tiles = (q.na + esq::MK_TOK - 1) / esq::MK_TOK;
+            j.ntok_tiles = (q.na + tok - 1) / tok;
             const int row_tiles = (q.r1 - q.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS;
             g->grid += 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
             g->jobs.push_back(j);
@@ -720,7 +739,8 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
         const esq::MkJob *dj = tables ? reinterpret_cast<const esq::MkJob *>(tables + g.off) : nullptr;
         if ((e = g.b32    ? esq::mbx_launch(g.type, g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
                  : g.nbkm ? esq::mx_launch(g.type, g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
-                          : esq::mk_launch(g.type, g.gather, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) != hipSuccess)
+                          : esq::mk_launch(g.type, g.gather, g.tok, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) !=
+            hipSuccess)
             return hip_fail(e, "matrix-core launch");
     }
     for (const MbGroup &g : bt.mbg) {
@@ -1088,6 +1108,7 @@ int es_hip_set_q3k_mfma_min_batch(int n) { return g_mk3_min.exchange(n); }
 int es_hip_set_q2k_expert_max_batch(int n) { return g_mx_max.exchange(n); }
 int es_hip_set_batched32_direct(int on) { return g_mbx_on.exchange(on ? 1 : 0); }
 int es_hip_set_q6k_persistent(int on) { return esq::mm6_set_persistent(on); }
+int es_hip_set_direct_mfma_tok64(int on) { return g_mk_tok64.exchange(on ? 1 : 0); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }

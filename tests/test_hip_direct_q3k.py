@@ -33,12 +33,15 @@ def inputs(orc, rows, cols, na, seed, gauss=False):
     return W, orc.quantize_act(O.Q3_K, x)
 
 
-@pytest.fixture
-def hip3(hip):
-    """every Q3_K product with at least one activation on the matrix-core kernel"""
+@pytest.fixture(params=["tok64", "tok128"])
+def hip3(hip, request):
+    """every Q3_K product with at least one activation on the matrix-core kernel; products short of row tiles in tiles of
+    64 activations ("tok64") or always 128 ("tok128")"""
     prev = hip.set_q3k_mfma_min_batch(1)
+    prev_64 = hip.set_direct_mfma_tok64(request.param == "tok64")
     yield hip
     hip.set_q3k_mfma_min_batch(prev)
+    hip.set_direct_mfma_tok64(prev_64)
     hip.set_order(E.ORDER_X86_CONTRACT)
 
 

@@ -31,12 +31,15 @@ def inputs(orc, rows, cols, na, seed, gauss=False):
     return W, orc.quantize_act(O.Q5_K, x)
 
 
-@pytest.fixture
-def hip5(hip):
-    """every Q5_K product with at least one activation on the matrix-core kernel"""
+@pytest.fixture(params=["tok64", "tok128"])
+def hip5(hip, request):
+    """every Q5_K product with at least one activation on the matrix-core kernel; products short of row tiles in tiles of
+    64 activations ("tok64") or always 128 ("tok128")"""
     prev = hip.set_q5k_mfma_min_batch(1)
+    prev_64 = hip.set_direct_mfma_tok64(request.param == "tok64")
     yield hip
     hip.set_q5k_mfma_min_batch(prev)
+    hip.set_direct_mfma_tok64(prev_64)
     hip.set_order(E.ORDER_X86_CONTRACT)
 
 
