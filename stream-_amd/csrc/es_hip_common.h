@@ -65,7 +65,7 @@ hipError_t mb32_launch(int type, const MbJob *jobs, int njobs, const MbJob &sing
 // The same products on the matrix cores (es_hip_mb.hip): workgroups of 16 rows x activations [t0, t0 + 32), the
 // activations read from a kind 3 pre-pass.
 constexpr int MB32M_ROWS = 16, MB32M_TOKENS = 32, PREP_KIND_Q80 = 3;
-__host__ __device__ constexpr uint32_t prep_words(int kind) { return kind == PREP_KIND_Q80 ? 9u : 73u; }   // per block
+__host__ __device__ constexpr uint32_t prep_words(int kind) { return kind == PREP_KIND_Q80 ? 9u : 19u; }   // items per block
 hipError_t mb32m_launch(int type, const MbJob *jobs, int njobs, const MbJob &single, int grid, int order, hipStream_t s);
 
 // The batched (matrix-core) form: rows [r0, r1) against na activations that a pre-pass has re-laid out as
@@ -125,8 +125,8 @@ hipError_t mk_launch(int type, bool gather, int tok, const MkJob *jobs, int njob
 // 16 q + 8 h .. + 7 of activation n: lane 32 h + n of the batched matrix-core kernel reads 16 bytes at 1024 q + 16 * lane
 // for its instruction q) and the scales as xm[tile][block][n] floats. All the
 // pre-passes of a batch run in one launch over `total` items (one dword of an activation row each), pre-pass i taking
-// items [start, start + na_pad*nbk*W) (W = 73 dwords per Q8_K block, 9 per Q8_0 block); every start is a multiple of PREP_SPAN, the items of one workgroup.
-constexpr int PREP_BLOCK = 256, PREP_UNROLL = 8, PREP_SPAN = PREP_BLOCK * PREP_UNROLL;
+// items [start, start + na_pad*nbk*W) (W = 19 16-byte items per Q8_K block, 9 dwords per Q8_0 block); every start is a multiple of PREP_SPAN, the items of one workgroup.
+constexpr int PREP_BLOCK = 256, PREP_UNROLL = 4, PREP_SPAN = PREP_BLOCK * PREP_UNROLL;
 struct PrepJob {
     const uint8_t *act;
     const int *arow;

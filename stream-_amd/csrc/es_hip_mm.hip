@@ -35,17 +35,22 @@ namespace esq {
 
 
 // ---- pre-pass --------------------------------------------------------------------------------------------------------
-// One item per dword of an activation's Q8_K row (nbk blocks of 73 dwords: d, 64 of qs, 8 of bsums pairs), consecutive
-// items on consecutive threads so the reads are coalesced, PREP_UNROLL items per thread with every load issued before
-// the first store; padding activations t >= na get zeros. Activation t is row arow[t] of act when arow is given.
+// Items of an activation's row, consecutive items on consecutive threads so the reads are coalesced, PREP_UNROLL items
+// per thread with every load issued before the first store; padding activations t >= na get zeros. Activation t is row
+// arow[t] of act when arow is given. A Q8_K block (292 bytes: d, qs[256], bsums[16]) is 19 items of 16 bytes: item 0 at
+// byte 0 (d and the first qs, of which only d is used), item w = 1 .. 18 at byte 16w - 12 (qs for w <= 16, then bsums
+// 0..7 and 8..15); the rows are only dword-aligned, so the loads are dword-aligned 16-byte loads. A Q8_0 block is 9 dword
+// items (d, 8 words of qs).
 // kind 0 writes the pair sums (Q4_K sub-blocks) and kind 1 the 16 bsums, both split as 128*hi + lo, one byte each; kind 2
 // writes the 16 bsums as halves (exact: a Q8_K block's bsums are sums of 16 int8 values, |bsums| <= 2048). Kind 3 reads
-// Q8_0 rows (9 dwords per block) and writes the batched 32-wide matrix-core layout (tiles of 32 activations).
+// Q8_0 rows and writes the batched 32-wide matrix-core layout (tiles of 32 activations).
 // Index arithmetic is 32-bit within a pre-pass (the host keeps every pre-pass below 2^31 threads).
-// the loads of one thread's items: row indices (for a gather), then the activation words
-template <bool GATHER>
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// the loads of one thread's items: row indices (for a gather), then the activation items (WIDE: 16 bytes, else a dword)
+template <bool GATHER, bool WIDE>
 __device__ __forceinline__ void prep_loads(const PrepJob &P, uint32_t base, uint32_t per, const bool (&ok)[PREP_UNROLL],
-                                           uint32_t (&row)[PREP_UNROLL], uint32_t (&v)[PREP_UNROLL]) {
+                                           uint32_t (&row)[PREP_UNROLL], uint4 (&v)[PREP_UNROLL]) {
     if constexpr (GATHER) {
 #pragma unroll
         for (int u = 0; u < PREP_UNROLL; u++) row[u] = (uint32_t)ldg<int>(P.arow + row[u]);
@@ -53,7 +58,110 @@ __device__ __forceinline__ void prep_loads(const PrepJob &P, uint32_t base, uint
 #pragma unroll
     for (int u = 0; u < PREP_UNROLL; u++) {
         const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x, t = lid / per, k = ok[u] ? lid - t * per : 0u;
-        v[u] = ldg<uint32_t>(P.act + (size_t)row[u] * P.astride + 4 * (size_t)k);
+        const uint8_t *src = P.act + (size_t)row[u] * P.astride;
+        if constexpr (WIDE) {
+            const uint32_t b = k / 19u, w = k - 19u * b, off = 292u * b + (w ? 16u * w - 12u : 0u);
+            const u32x4_a4 x = *(const ESQ_GLOBAL u32x4_a4 *)(src + off);
+            v[u] = make_uint4(x.x, x.y, x.z, x.w);
+        } else {
+            v[u].x = ldg<uint32_t>(src + 4 * (size_t)k);
+        }
+    }
+}
+
+// the stores of one Q8_K item (d, 16 bytes of qs, or 8 bsums)
+__device__ __forceinline__ void prep_store_q8k(const PrepJob &P, uint32_t t, uint32_t k, const uint4 &v) {
+    const uint32_t b = k / 19u, w = k - 19u * b;
+    const size_t bt = (size_t)b * P.na_pad + t;
+    uint8_t *xm = P.xm;
+    const int mb = P.kind == 0 ? 16 : 32;   // meta bytes per (activation, superblock)
+    if (w == 0) {
+        stg<uint32_t>(xm + (size_t)P.nbk * P.na_pad * mb + bt * 4, v.x);   // d
+        return;
+    }
+    if (w <= 16) {
+        stg<uint4>(P.xq + bt * 256 + 16 * (w - 1), v);   // qs
+        return;
+    }
+    const int h = (int)w - 17;   // bsums 8h .. 8h+7
+    const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+    int bs[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        bs[2 * i] = (int16_t)(wd[i] & 0xffff);
+        bs[2 * i + 1] = (int16_t)(wd[i] >> 16);
+    }
+    if (P.kind == 0) {   // pair sums p_jj = bsums[2jj] + bsums[2jj+1], jj = 4h .. 4h+3
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = bs[2 * i] + bs[2 * i + 1];
+            lo |= (uint32_t)(p & 127) << (8 * i);
+            hi |= (uint32_t)((p >> 7) & 0xff) << (8 * i);
+        }
+        stg<uint32_t>(xm + bt * 16 + 4 * h, lo);
+        stg<uint32_t>(xm + bt * 16 + 8 + 4 * h, hi);
+    } else if (P.kind == 1) {   // bsums g = 8h .. 8h+7: low bytes, then high bytes
+        uint32_t lo[2] = {0, 0}, hi[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            lo[i >> 2] |= (uint32_t)(bs[i] & 127) << (8 * (i & 3));
+            hi[i >> 2] |= (uint32_t)((bs[i] >> 7) & 0xff) << (8 * (i & 3));
+        }
+        stg<uint2>(xm + bt * 32 + 8 * h, make_uint2(lo[0], lo[1]));
+        stg<uint2>(xm + bt * 32 + 16 + 8 * h, make_uint2(hi[0], hi[1]));
+    } else {   // kind 2: halves
+        uint32_t hv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            hv[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)bs[2 * i]) |
+                    (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)bs[2 * i + 1]) << 16;
+        stg<uint4>(xm + bt * 32 + 16 * h, make_uint4(hv[0], hv[1], hv[2], hv[3]));
+    }
+}
+
+// the stores of one Q8_0 dword item (kind 3)
+__device__ __forceinline__ void prep_store_q80(const PrepJob &P, uint32_t t, uint32_t k, uint32_t v) {
+    const uint32_t b = k / 9u, w = k - 9u * b;
+    const uint32_t tb = (t >> 5) * (uint32_t)P.nbk + b, nn = t & 31u;   // (tile, block), activation in the tile
+    if (w == 0) {
+        stg<uint32_t>(P.xm + ((size_t)tb * 32 + nn) * 4, v);
+    } else {   // values e0 .. e0 + 3 as halves: instruction q = e0 / 16, lane half h = e0 % 16 / 8, halves e0 % 8 ..
+        const uint32_t e0 = 4 * (w - 1), q = e0 >> 4, hh = (e0 >> 3) & 1;
+        h2 lo, hi;
+        lo[0] = (_Float16)(int8_t)(v & 0xff);
+        lo[1] = (_Float16)(int8_t)((v >> 8) & 0xff);
+        hi[0] = (_Float16)(int8_t)((v >> 16) & 0xff);
+        hi[1] = (_Float16)(int8_t)(v >> 24);
+        const uint2 pr = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+        stg<uint2>(P.xq + ((((size_t)tb * 2 + q) * 2 + hh) * 32 + nn) * 16 + 2 * (e0 & 7), pr);
+    }
+}
+
+template <bool WIDE>
+__device__ __forceinline__ void prep_items(const PrepJob &P, uint32_t base, uint32_t per, uint32_t n) {
+    // every load of the span first, unconditionally (items past the end read the first item and keep 0), so they are all
+    // in flight together; then the stores
+    uint4 v[PREP_UNROLL];
+    uint32_t row[PREP_UNROLL];
+    bool ok[PREP_UNROLL];
+#pragma unroll
+    for (int u = 0; u < PREP_UNROLL; u++) {
+        const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x, t = lid / per;
+        ok[u] = lid < n && (int)t < P.na;
+        row[u] = ok[u] ? t : 0u;
+    }
+    if (P.arow) prep_loads<true, WIDE>(P, base, per, ok, row, v);   // two copies of the loads, so no branch splits them
+    else prep_loads<false, WIDE>(P, base, per, ok, row, v);
+#pragma unroll
+    for (int u = 0; u < PREP_UNROLL; u++) v[u] = ok[u] ? v[u] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < PREP_UNROLL; u++) {
+        const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x;
+        if (lid >= n) break;
+        const uint32_t t = lid / per, k = lid - t * per;
+        if constexpr (WIDE) prep_store_q8k(P, t, k, v[u]);
+        else prep_store_q80(P, t, k, v[u].x);
     }
 }
 
@@ -72,64 +180,9 @@ __global__ __launch_bounds__(PREP_BLOCK) void act_prep_q8k(const PrepJob *__rest
     PrepJob P;
     if (jobs) P = jobs[j];
     else P = single;
-    const uint32_t words = prep_words(P.kind);
-    const uint32_t per = (uint32_t)P.nbk * words, n = (uint32_t)P.na_pad * per, base = (uint32_t)(id0 - P.start);
-    const int mb = P.kind == 0 ? 16 : 32;   // meta bytes per (activation, superblock)
-    // every load of the span first, unconditionally (items past the end read the first word and keep 0), so they are all
-    // in flight together; then the stores
-    uint32_t v[PREP_UNROLL], row[PREP_UNROLL];
-    bool ok[PREP_UNROLL];
-#pragma unroll
-    for (int u = 0; u < PREP_UNROLL; u++) {
-        const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x, t = lid / per;
-        ok[u] = lid < n && (int)t < P.na;
-        row[u] = ok[u] ? t : 0u;
-    }
-    if (P.arow) prep_loads<true>(P, base, per, ok, row, v);   // two copies of the loads, so no branch splits them
-    else prep_loads<false>(P, base, per, ok, row, v);
-#pragma unroll
-    for (int u = 0; u < PREP_UNROLL; u++) v[u] = ok[u] ? v[u] : 0u;
-#pragma unroll
-    for (int u = 0; u < PREP_UNROLL; u++) {
-        const uint32_t lid = base + u * PREP_BLOCK + threadIdx.x;
-        if (lid >= n) break;
-        const uint32_t t = lid / per, k = lid - t * per, b = k / words, w = k - words * b;
-        const size_t bt = (size_t)b * P.na_pad + t;
-        uint8_t *xm = P.xm;
-        if (P.kind == PREP_KIND_Q80) {
-            const uint32_t tb = (t >> 5) * (uint32_t)P.nbk + b, nn = t & 31u;   // (tile, block), activation in the tile
-            if (w == 0) {
-                stg<uint32_t>(xm + ((size_t)tb * 32 + nn) * 4, v[u]);
-            } else {   // values e0 .. e0 + 3 as halves: instruction q = e0 / 16, lane half h = e0 % 16 / 8, halves e0 % 8 ..
-                const uint32_t e0 = 4 * (w - 1), q = e0 >> 4, hh = (e0 >> 3) & 1;
-                h2 lo, hi;
-                lo[0] = (_Float16)(int8_t)(v[u] & 0xff);
-                lo[1] = (_Float16)(int8_t)((v[u] >> 8) & 0xff);
-                hi[0] = (_Float16)(int8_t)((v[u] >> 16) & 0xff);
-                hi[1] = (_Float16)(int8_t)(v[u] >> 24);
-                const uint2 pr = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-                stg<uint2>(P.xq + ((((size_t)tb * 2 + q) * 2 + hh) * 32 + nn) * 16 + 2 * (e0 & 7), pr);
-            }
-        } else if (w == 0) {
-            stg<uint32_t>(xm + (size_t)P.nbk * P.na_pad * mb + bt * 4, v[u]);   // d
-        } else if (w <= 64) {
-            stg<uint32_t>(P.xq + bt * 256 + 4 * (w - 1), v[u]);                 // qs
-        } else if (P.kind == 2) {
-            const _Float16 h0 = (_Float16)(int16_t)(v[u] & 0xffff), h1 = (_Float16)(int16_t)(v[u] >> 16);
-            stg<uint32_t>(xm + bt * 32 + 4 * (w - 65),
-                          (uint32_t)__builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-        } else if (P.kind == 0) {
-            const int jj = w - 65, p = (int16_t)(v[u] & 0xffff) + (int16_t)(v[u] >> 16);   // bsums[2jj] + bsums[2jj+1]
-            stg<uint8_t>(xm + bt * 16 + jj, (uint8_t)(p & 127));
-            stg<uint8_t>(xm + bt * 16 + 8 + jj, (uint8_t)((p >> 7) & 0xff));
-        } else {
-            const int g = 2 * (w - 65), p0 = (int16_t)(v[u] & 0xffff), p1 = (int16_t)(v[u] >> 16);   // bsums[g], bsums[g+1]
-            stg<uint8_t>(xm + bt * 32 + g, (uint8_t)(p0 & 127));
-            stg<uint8_t>(xm + bt * 32 + g + 1, (uint8_t)(p1 & 127));
-            stg<uint8_t>(xm + bt * 32 + 16 + g, (uint8_t)((p0 >> 7) & 0xff));
-            stg<uint8_t>(xm + bt * 32 + 16 + g + 1, (uint8_t)((p1 >> 7) & 0xff));
-        }
-    }
+    const uint32_t per = (uint32_t)P.nbk * prep_words(P.kind), n = (uint32_t)P.na_pad * per, base = (uint32_t)(id0 - P.start);
+    if (P.kind == PREP_KIND_Q80) prep_items<false>(P, base, per, n);
+    else prep_items<true>(P, base, per, n);
 }
 
 // ---- main kernel ---------------------------------------------------------------------------------------------------

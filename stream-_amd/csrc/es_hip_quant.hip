@@ -713,7 +713,7 @@ std::vector<uint8_t> table_image(const Batch &bt) {
 // single jobs by value.
 int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t s) {
     hipError_t e;
-    if (tables && !bt.pj.empty()) {   // every pre-pass in one launch
+    if (tables && bt.pj.size() > 1) {   // every pre-pass in one launch (a single one goes by value: no table read first)
         e = esq::prep_launch(reinterpret_cast<const esq::PrepJob *>(tables + bt.prep_off), (int)bt.pj.size(), bt.pj[0],
                              bt.prep_total, s);
         if (e != hipSuccess) return hip_fail(e, "pre-pass launch");
