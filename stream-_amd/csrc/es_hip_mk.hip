@@ -74,8 +74,10 @@ __device__ __forceinline__ void load_lds4(const uint8_t *base, uint32_t off, uin
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory");
 }
 
-constexpr int MK_WAVES = 4;
-static_assert(MK_ROWS == 16 * MK_WAVES, "four waves of 16 rows");
+constexpr int MK_WAVES = MK_ROWS / 16;
+static_assert(MK_WAVES == 4 || MK_WAVES == 8, "four or eight waves of 16 rows");
+// workgroups per CU: two of four waves (each with its own LDS ring and barriers), or one of eight
+constexpr int MK_WG_PER_CU = MK_WAVES == 4 ? 2 : 1;
 // one slot of the activation ring for T activations: values (one swizzled 256-byte row per activation) | bsums as halves
 // [lg][activation][4] | scales
 constexpr int TROW = 256;
@@ -268,7 +270,7 @@ template <int NMFMA> __device__ __forceinline__ void step_schedule() {
 
 // T: activations per workgroup tile, 128, or 64 for products with too few row tiles to fill the device at 128.
 template <int F, bool CONTRACT, bool GATHER, int T>
-__global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
+__global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
     using FM = MkFmt<F>;
     using SL = MkSlot<T>;
     constexpr int ST_QS = SL::QS, ST_BS = SL::BS, ST_D = SL::D, ST_BYTES = SL::BYTES, MK_TT = SL::TT;
@@ -297,13 +299,13 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
         const int r = (GATHER && J.arow) ? ldg<int>(J.arow + q) : q;
         return (uint32_t)r * (uint32_t)J.astride;
     };
-    // values: wave w copies activations (T/4) w .. (T/4) w + T/4 - 1, four per instruction: instruction k, lane l:
-    // activation t = (T/4) w + 4k + l/16, LDS position l%16 of its row, so source chunk (l%16) ^ (t & 15)
-    constexpr int NV = T / 16;
+    // values: wave w of NW copies activations TW w .. TW w + TW - 1 (TW = T / NW), four per instruction: instruction k,
+    // lane l: activation t = TW w + 4k + l/16, LDS position l%16 of its row, so source chunk (l%16) ^ (t & 15)
+    constexpr int TW = T / MK_WAVES, NV = TW / 4;
     uint32_t qoff[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int t = (T / 4) * wave + 4 * k + (lane >> 4);
+        const int t = TW * wave + 4 * k + (lane >> 4);
         qoff[k] = act_off(t) + 4 + 16 * ((lane & 15) ^ (t & 15));
     }
     // scales: wave w, lane l copies activation 64 ds + l's d, ds = w & 1 (at 128 activations; 0 at 64)
@@ -325,7 +327,7 @@ __global__ __launch_bounds__(64 * MK_WAVES, 2) void mk_kernel(const MkJob *__res
     };
     auto stage_dma = [&](int b, int st) {   // values and scales of superblock b into slot st
         const uint8_t *ab = sb_base(b);
-        const uint32_t base = smem0 + (uint32_t)st * ST_BYTES + ST_QS + (uint32_t)((T / 4) * wave) * TROW;
+        const uint32_t base = smem0 + (uint32_t)st * ST_BYTES + ST_QS + (uint32_t)(TW * wave) * TROW;
 #pragma unroll
         for (int k = 0; k < NV; k++) load_lds16(ab, qoff[k], base + 4 * TROW * k);
         // the other waves repeat waves 0 and 1's copy (the same bytes to the same place), which keeps the code branch-free
