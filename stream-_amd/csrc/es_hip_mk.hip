@@ -4,7 +4,9 @@
 // Work split. A workgroup of 4 waves computes MK_ROWS = 64 rows x MK_TOK = 128 activations; wave w takes the 16 rows
 // 16w .. 16w+15 and all 128 activations (eight 16-activation tiles), so a row tile's unpacked weights serve eight MFMA
 // tiles. Two workgroups share a CU (one wave of each per SIMD), each with its own LDS ring and barriers, so one
-// workgroup's vector work (unpacking weights, the float epilogue) overlaps the other's matrix work.
+// workgroup's vector work (unpacking weights, the float epilogue) overlaps the other's matrix work. The code is written
+// for MK_WAVES = MK_ROWS / 16 waves: a build with MK_ROWS = 128 runs one workgroup of 8 waves per CU (the same results;
+// measured no faster for Q4_K and slower for Q5_K and Q3_K, whose short products then get half the tiles).
 //
 // Activations. Superblock b of the 128 activations passes through a two-slot LDS ring: the Q8_K values (each activation's
 // 256 bytes in one LDS row, its 16-byte chunk c at position c ^ (t & 15), so the 16 lanes that read chunk c of 16
