@@ -72,7 +72,6 @@ __global__ __launch_bounds__(256, NBKM <= 64 ? 2 : 1) void mbx_kernel(const MkJo
     using BF = BxFmt<F>;
     constexpr int BB = Fmt<F>::BB;
     constexpr uint32_t V0 = 0, D0 = NBKM * 1024;
-    constexpr int NLD = BF::QH >= 0 ? 4 : 3;   // weight loads per block
     static_assert(P % 2 == 0 && NBKM % 2 == 0, "block parity is the stage's; scale copies cover two blocks");
     __shared__ __align__(16) uint8_t smem[NBKM * (1024 + 128)];
 
@@ -153,8 +152,10 @@ __global__ __launch_bounds__(256, NBKM <= 64 ? 2 : 1) void mbx_kernel(const MkJo
     // the compiler's waits count exactly which loads a use needs
 #pragma unroll
     for (int p = 0; p < P; p++) load(st[p], min(p, nbk - 1));
-    // the staging copies are older than the NLD * P weight loads just issued
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD * P) : "memory");
+    // Every staging copy must have landed before the barrier publishes the LDS. The wait drains the weight prefetch too:
+    // counting only the weight loads would depend on how the compiler merges them (Q5_0's d|qh dwords become one
+    // 8-byte load), and the first block needs its loads now anyway.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_sync();
 
     const uint32_t xo = smem0 + V0 + (uint32_t)n * 32 + 16u * (uint32_t)(h ^ ((n >> 3) & 1)), yo = smem0 + D0 + 4u * n;
