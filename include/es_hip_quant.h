@@ -304,6 +304,12 @@ int es_hip_set_batched32_direct(int on);
  * launch: one workgroup per CU copies the activations into LDS once and streams its row tiles back to back. Results
  * are identical either way. Returns the previous setting. */
 int es_hip_set_q6k_persistent(int on);
+/* Q4_K and Q3_K products that take the direct-activation kernel and have an even number (at least 2) of superblocks per
+ * row, with no gathered activations, run, with on != 0 (the default), in one persistent launch per format: two
+ * workgroups per CU, each computing a host-scheduled list of tiles (64 rows x 128 or 64 activations) with its loads
+ * running ahead across tile boundaries. Q4_K products of this kind then take it at any tile count (config 2's 2048 x 8192
+ * down product shares the launch with gate and up). Results are identical either way. Returns the previous setting. */
+int es_hip_set_direct_persistent(int on);
 /* Q5_K and Q3_K products on the direct-activation kernel that would have fewer than 256 tiles of 64 rows x 128
  * activations run, with on != 0 (the default) and at least 64 activations, in tiles of 64 activations (twice the
  * workgroups: config 2's down product at T = 512 in those formats). Results are identical either way. Returns the

@@ -85,7 +85,11 @@ struct MmJob {
 // activations, activation q at act + (arow ? arow[q] : q) * astride. Workgroup tiles of MK_ROWS rows x MK_TOK
 // activations, numbered from tile0; ntok_tiles activation tiles per row tile. The activation rows of a product must lie
 // within 4 GiB of act (32-bit offsets; checked by the host).
-constexpr int MK_TOK = 128, MK_ROWS = 64;
+// rows per workgroup tile: 64 (two workgroups of 4 waves per CU) or, built with ESQ_MK_ROWS=128, 128 (one of 8 waves)
+#ifndef ESQ_MK_ROWS
+#define ESQ_MK_ROWS 64
+#endif
+constexpr int MK_TOK = 128, MK_ROWS = ESQ_MK_ROWS;
 struct MkJob {
     const uint8_t *W;     // row 0
     const uint8_t *act;   // activation 0's first block
@@ -117,6 +121,30 @@ hipError_t mbx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int
 // tok: activations per workgroup tile, MK_TOK or 64 (ntok_tiles and the tile numbering then count tiles of 64)
 hipError_t mk_launch(int type, bool gather, int tok, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
                      hipStream_t s);
+
+// The persistent form of the direct kernel (es_hip_mk.hip): a launch of `grid` workgroups (two per CU) in which workgroup
+// g computes the tiles tiles[wgptr[g] .. wgptr[g + 1]) one after another, its loads running ahead across tile
+// boundaries. A tile is MK_ROWS rows x 128 (or 64) activations of one product, every address it needs written by the
+// host. Products of any row length of at least 2 superblocks (no gathered activations) share one launch.
+struct PkTile {
+    const uint8_t *w;       // the tile's first weight row
+    const uint8_t *act;     // the product's activation 0 (every activation row within 4 GiB of it)
+    float *y;               // output of the tile's first activation and first row
+    uint32_t astride;       // bytes between activations
+    uint32_t ystride4;      // bytes between the outputs of consecutive activations
+    uint32_t row_bytes;
+    int32_t nbk;            // superblocks per row (>= 2)
+    int32_t t64;            // 1: a tile of 64 activations, else 128
+    int32_t tok0;           // the tile's first activation
+    int32_t na;             // activations of the product (sources past the last repeat it)
+    int32_t rows;           // rows of the tile (<= MK_ROWS; rows past them repeat the last and are not stored)
+    int32_t ntok;           // activations of the tile (those past it are not stored)
+    int32_t pad_;
+};
+static_assert(sizeof(PkTile) == 64, "tile records are copied into LDS as 16-byte pieces");
+constexpr int PK_MAX_TILES = 48;   // tiles per workgroup (their records sit in LDS beside the ring: 80 KB a workgroup)
+// workgroups [0, g64) take the tiles of 64 activations, the rest those of 128
+hipError_t pk_launch(int type, const PkTile *tiles, const int *wgptr, int grid, int g64, int order, hipStream_t s);
 
 // One activation pre-pass: kind 0 writes 16 bytes of meta per activation and superblock (pair sums of the Q4_K
 // sub-blocks, low | high bytes), kind 1 32 bytes (the 16 bsums, low | high bytes), kind 2 32 bytes (the 16 bsums as

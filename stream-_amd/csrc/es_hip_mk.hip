@@ -53,6 +53,8 @@
 // Slice s and lane group lg take group g = 8 (lg >> 1) + 2 s + (lg & 1); the planes' bytes come from two 8-entry tables
 // per slice (v * l and v * (h - 4) for v + 4 = 0..7) through v_perm_b32, indexed by the 3-bit code v + 4. Epilogue: the
 // reference's s += y.d * d * tot (fused in the clang order).
+#include <type_traits>
+
 #include "es_hip_common.h"
 
 namespace esq {
@@ -81,12 +83,13 @@ static_assert(MK_WAVES == 4 || MK_WAVES == 8, "four or eight waves of 16 rows");
 // workgroups per CU: two of four waves (each with its own LDS ring and barriers), or one of eight
 constexpr int MK_WG_PER_CU = MK_WAVES == 4 ? 2 : 1;
 // one slot of the activation ring for T activations: values (one swizzled 256-byte row per activation) | bsums as halves
-// [lg][activation][4] | scales
+// [lg][activation][4] | scales. After the two slots, one landing area for the next superblock's raw int16 bsums
+// [activation][16] (RAW bytes), converted into a slot's halves by the wave that copied them.
 constexpr int TROW = 256;
 template <int T> struct MkSlot {
-    static constexpr int QS = 0, BS = T * TROW, D = BS + T * 32, BYTES = D + T * 4, TT = T / 16;
+    static constexpr int QS = 0, BS = T * TROW, D = BS + T * 32, BYTES = D + T * 4, TT = T / 16, RAW = T * 32;
     static_assert(T == 64 || T == 128, "the staging assignment below is written for 64 or 128 activations");
-    static_assert(2 * 2 * BYTES <= 160 * 1024, "two workgroups' two slots fit the LDS");
+    static_assert(MK_WG_PER_CU * (2 * BYTES + RAW) <= 160 * 1024, "the workgroups of a CU fit its LDS");
 };
 
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
@@ -202,6 +205,19 @@ template <> __device__ __forceinline__ void build_b<ES_HIP_Q3_K>(const WRaw<ES_H
     B.dm = 0.f;
 }
 
+// An empty statement that takes every B operand as an input: placed before the next load group's copies (volatile
+// statements keep their order), it keeps the unpacking, and the compiler's wait for the weight registers it reads, above
+// the copies. The compiler counts only its own loads: its wait placed after the copies would wait for most of them too.
+template <int F> __device__ __forceinline__ void b_ready(const BOps<F> &B) {
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        asm volatile("" ::"v"(B.lo[s]), "v"(B.hi[s]));
+        if constexpr (F == ES_HIP_Q5_K) asm volatile("" ::"v"(B.q5[s]));
+    }
+    if constexpr (F != ES_HIP_Q3_K) asm volatile("" ::"v"(B.mn));
+    asm volatile("" ::"v"(B.d), "v"(B.dm));
+}
+
 struct AOps {   // one activation tile's A operands for one superblock, and the tile's activation scales
     v4i x[4];
     v4h bs;
@@ -278,7 +294,10 @@ __global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const M
     constexpr int ST_QS = SL::QS, ST_BS = SL::BS, ST_D = SL::D, ST_BYTES = SL::BYTES, MK_TT = SL::TT;
     constexpr bool FUSED = CONTRACT && F != ES_HIP_Q5_K;   // Q5_K's reference epilogue never fuses
     constexpr bool BSUMS = F != ES_HIP_Q3_K;              // the mins term reads the activations' bsums
-    __shared__ __align__(16) uint8_t smem[2 * ST_BYTES];
+    // weight loads per superblock and lane (one 16-byte load each, so the count is exact: no load merges into another)
+    constexpr int NW = F == ES_HIP_Q5_K ? 4 : 3;
+    constexpr uint32_t RAW0 = 2 * ST_BYTES;
+    __shared__ __align__(16) uint8_t smem[2 * ST_BYTES + (BSUMS ? SL::RAW : 0)];
 
     MkJob J;
     if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
@@ -313,12 +332,15 @@ __global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const M
     // scales: wave w, lane l copies activation 64 ds + l's d, ds = w & 1 (at 128 activations; 0 at 64)
     const int ds = T == 128 ? (wave & 1) : 0;
     const uint32_t doff = act_off(64 * ds + lane);
-    // bsums: every lane, activation bt, bsums 8*bh .. 8*bh+7 (at 64 activations the upper half of the workgroup repeats the
-    // lower half's copies: the same bytes to the same place)
+    // bsums: the raw int16 rows go into the landing area by LDS DMA, one instruction per wave (wave w, lane l: activation
+    // 32 (w % RW) + l / 2, bsums 8 (l & 1) .. + 7; at 64 activations waves 2 and 3 repeat waves 0 and 1: the same bytes to
+    // the same place); every thread then converts the 8 bsums it copied (activation bt, bsums 8*bh .. 8*bh+7) to halves.
+    constexpr int RW = T / 32;
     const int bt = (tid >> 1) & (T - 1), bh = tid & 1;
-    const uint32_t boff = act_off(bt) + 260 + 16 * bh;
+    const uint32_t rawoff = act_off(32 * (wave % RW) + (lane >> 1)) + 260 + 16 * (lane & 1);
     const uint32_t bdst0 = ST_BS + (2 * bh) * (T * 8) + bt * 8, bdst1 = bdst0 + T * 8;
     const uint32_t smem0 = lds_addr(smem);
+    const uint32_t rawdst = smem0 + RAW0 + 1024u * (uint32_t)(wave % RW), rawsrc = smem0 + RAW0 + 16u * (uint32_t)(tid & (2 * T - 1));
 
     // the superblock's base address, kept opaque in scalar registers (as plain arithmetic the compiler folds it into
     // per-lane 64-bit pointers)
@@ -327,16 +349,26 @@ __global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const M
         asm volatile("" : "+s"(sb));
         return J.act + sb;
     };
-    auto stage_dma = [&](int b, int st) {   // values and scales of superblock b into slot st
+    // piece k (0 .. NP - 1) of superblock b's copies into slot st: value chunks, then scales, then raw bsums
+    constexpr int NP = NV + 1 + (BSUMS ? 1 : 0);
+    auto stage_part = [&](int b, int st, int k) {
         const uint8_t *ab = sb_base(b);
-        const uint32_t base = smem0 + (uint32_t)st * ST_BYTES + ST_QS + (uint32_t)(TW * wave) * TROW;
-#pragma unroll
-        for (int k = 0; k < NV; k++) load_lds16(ab, qoff[k], base + 4 * TROW * k);
-        // the other waves repeat waves 0 and 1's copy (the same bytes to the same place), which keeps the code branch-free
-        load_lds4(ab, doff, smem0 + (uint32_t)st * ST_BYTES + ST_D + 256 * ds);
+        if (k < NV) {
+            load_lds16(ab, qoff[k], smem0 + (uint32_t)st * ST_BYTES + ST_QS + (uint32_t)(TW * wave) * TROW + 4 * TROW * k);
+        } else if (k == NV) {
+            // the other waves repeat waves 0 and 1's copy (the same bytes to the same place): the code stays branch-free
+            load_lds4(ab, doff, smem0 + (uint32_t)st * ST_BYTES + ST_D + 256 * ds);
+        } else if constexpr (BSUMS) {
+            load_lds16(ab, rawoff, rawdst);
+        }
     };
-    auto bs_load = [&](int b) { return ldg<uint4>(sb_base(b) + boff); };
-    auto bs_write = [&](const uint4 &v, int st) {
+    auto stage_dma = [&](int b, int st) {
+#pragma unroll
+        for (int k = 0; k < NP; k++) stage_part(b, st, k);
+    };
+    // the bsums this thread copied (landed: its wave waited for its copies) as halves into slot st
+    auto bs_convert = [&](int st) {
+        const u32x4 v = lds_ld<u32x4>(rawsrc);
         uint8_t *base = smem + st * ST_BYTES;
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
         uint32_t hv[4];
@@ -351,18 +383,23 @@ __global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const M
     // ---- this wave's weight rows (rows past the end repeat the last one; their results are not stored)
     const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
     const uint32_t woff = (uint32_t)min(16 * wave + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
-    auto wload = [&](int b, WRaw<F> &W) {
+    // field f (0 .. NW - 1) of superblock b's weights: one 16-byte load
+    auto wload_part = [&](int b, WRaw<F> &W, int f) {
         const uint8_t *p = wbase + woff + (uint32_t)FM::BB * (uint32_t)b;
         if constexpr (F == ES_HIP_Q3_K) {
-            W.h = ldg_u128_a2(p + 94);
-            W.q = ldg_u128_a2(p + FM::QS + 16 * lg);
-            W.hm = ldg_u128_a2(p + FM::QH + 16 * (lg & 1));
+            if (f == 0) W.h = ldg_u128_a2(p + 94);
+            else if (f == 1) W.q = ldg_u128_a2(p + FM::QS + 16 * lg);
+            else W.hm = ldg_u128_a2(p + FM::QH + 16 * (lg & 1));
         } else {
-            W.h = ldg<uint4>(p);
-            W.q0 = ldg<uint4>(p + FM::QS + 16 * lg);
-            W.q1 = ldg<uint4>(p + FM::QS + 64 + 16 * lg);
-            if constexpr (F == ES_HIP_Q5_K) W.qh = ldg<uint4>(p + FM::QH + 16 * (lg & 1));
+            if (f == 0) W.h = ldg<uint4>(p);
+            else if (f == 1) W.q0 = ldg<uint4>(p + FM::QS + 16 * lg);
+            else if (f == 2) W.q1 = ldg<uint4>(p + FM::QS + 64 + 16 * lg);
+            else if constexpr (F == ES_HIP_Q5_K) W.qh = ldg<uint4>(p + FM::QH + 16 * (lg & 1));
         }
+    };
+    auto wload = [&](int b, WRaw<F> &W) {
+#pragma unroll
+        for (int f = 0; f < NW; f++) wload_part(b, W, f);
     };
 
     // ---- A operand offsets in a slot: activation tile tt adds 16 rows (values), 16 * 8 (bsums), 64 (scales)
@@ -386,11 +423,17 @@ __global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const M
 #pragma unroll
     for (int tt = 0; tt < MK_TT; tt++) acc[tt] = v4f{0, 0, 0, 0};
 
-    // Per superblock b: wait for every load of the previous group and the barrier (slot b & 1 complete, the other slot
-    // free); the B operands of superblock b from its weights; the matrix work over the 8 activation tiles, with the next
-    // load group (values and scales of superblock b + 1 into the free slot, its weights and bsums into registers) issued
-    // after the second tile; the bsums of superblock b + 1 into LDS. The last iteration repeats the last superblock's
-    // loads into a slot nobody reads.
+    // Per superblock b (slot b & 1, weights in one of two register sets): the barrier (slot b & 1 complete and its bsums
+    // converted, the other slot free); the B operands of superblock b from its weights; the copies of superblock b + 1
+    // into the free slot and the landing area, then the weights of superblock b + 2 into the register set just unpacked;
+    // the matrix work over the 8 activation tiles; a wait for this wave's copies (every load but the NW weight loads
+    // issued last) and the conversion of the bsums it copied. So the copies have a whole superblock of matrix work to
+    // arrive and the weights two, and no wait drains the weight loads in flight. Loads past the last superblock repeat
+    // it into a slot or register set nobody reads.
+    //
+    // The loop is unrolled by two so that the slot and the register set of each half are compile-time choices (a register
+    // set picked at run time would move in-flight load destinations, and the compiler would wait for them first); with
+    // an odd number of superblocks the last one follows the loop.
     //
     // A tile's epilogue runs two tile steps after its MFMAs (a step's vector work then never waits for the matrix cores),
     // across superblock boundaries: steps 0 and 1 of superblock b finish tiles 6 and 7 of superblock b - 1. The two
@@ -400,20 +443,24 @@ __global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const M
     p0.yd = v4f{0, 0, 0, 0};
     p0.d = p0.dm = 0.f;
     p1 = p0;
-    WRaw<F> W;
+    WRaw<F> Wa, Wb;   // superblocks of even / odd index
     stage_dma(0, 0);
-    wload(0, W);
-    if constexpr (BSUMS) bs_write(bs_load(0), 0);
-    for (int b = 0; b < nbk; b++) {
-        const int sl = b & 1;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's copies into LDS (not tracked by the compiler)
-        __syncthreads();
+    wload(0, Wa);
+    wload(min(1, nbk - 1), Wb);
+    wait_vmcnt<NW>();   // superblock 0's copies and weights (superblock 1's weights may still be in flight)
+    if constexpr (BSUMS) bs_convert(0);
+    auto iter = [&](auto slc, int b, WRaw<F> &Wc) {
+        constexpr int sl = decltype(slc)::value;
+        lds_sync();
         BOps<F> B;
-        build_b<F>(W, lg, B);
-        const int bn = min(b + 1, nbk - 1);
-        uint4 bsn;
-        const uint32_t so = smem0 + (uint32_t)sl * ST_BYTES;
-        const uint32_t xa[4] = {so + xo[0], so + xo[1], so + xo[2], so + xo[3]}, ba = so + bso, ya = so + ydo;
+        build_b<F>(Wc, lg, B);
+        b_ready<F>(B);
+        stage_dma(min(b + 1, nbk - 1), 1 - sl);
+        wload(min(b + 2, nbk - 1), Wc);
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr uint32_t so = (uint32_t)sl * ST_BYTES;
+        const uint32_t xa[4] = {smem0 + so + xo[0], smem0 + so + xo[1], smem0 + so + xo[2], smem0 + so + xo[3]};
+        const uint32_t ba = smem0 + so + bso, ya = smem0 + so + ydo;
         AOps A[2];
         aload(xa, ba, ya, 0, A[0]);
 #pragma unroll
@@ -429,16 +476,16 @@ __global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const M
             p1.dm = B.dm;
             step_schedule<F == ES_HIP_Q5_K ? 13 : F == ES_HIP_Q3_K ? 8 : 9>();
             __builtin_amdgcn_sched_barrier(0);
-            if (tt == 1) {
-                // the next load group, once this superblock's weights are unpacked (the first MFMAs used them)
-                stage_dma(bn, 1 - sl);
-                wload(bn, W);
-                if constexpr (BSUMS) bsn = bs_load(bn);
-                __builtin_amdgcn_sched_barrier(0);
-            }
         }
-        if constexpr (BSUMS) bs_write(bsn, 1 - sl);
+        wait_vmcnt<NW>();   // this wave's copies of superblock b + 1 (the weights of b + 2 may still be in flight)
+        if constexpr (BSUMS) bs_convert(1 - sl);
+    };
+    int b = 0;
+    for (; b + 1 < nbk; b += 2) {
+        iter(std::integral_constant<int, 0>{}, b, Wa);
+        iter(std::integral_constant<int, 1>{}, b + 1, Wb);
     }
+    if (b < nbk) iter(std::integral_constant<int, 0>{}, b, Wa);
     epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[MK_TT - 2]);
     epilogue<F, FUSED>(p1.m, p1.d, p1.dm, p1.yd, acc[MK_TT - 1]);
 
@@ -459,6 +506,293 @@ __global__ __launch_bounds__(64 * MK_WAVES, MK_WG_PER_CU) void mk_kernel(const M
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrsrc, (int)yoff, 0, 0);
             yoff += i < 3 ? ys4 : 13 * ys4;   // the next activation: + 1, or + 13 to the next tile's first
         }
+}
+
+// ---- the persistent form ----------------------------------------------------------------------------------------------
+// Workgroup g computes tiles tiles[wgptr[g] .. wgptr[g + 1]) (64 rows x 128 or 64 activations each, records written by
+// the host and copied into LDS at the start) as one stream of (tile, superblock) items: the mk_kernel loop above, whose
+// copies (one item ahead) and weight loads (two items ahead) run across tile boundaries, so a workgroup waits for its
+// first loads once. The ring keeps the 128-activation layout for both tile widths (a 64-wide tile uses the first half of
+// every region). At a tile's last item the two pending epilogues run at once, the outputs are stored and the accumulators
+// cleared; then the next tile's sources become current.
+template <int F, bool CONTRACT> struct PkGeom {
+    using SL = MkSlot<128>;
+    static constexpr uint32_t RAW0 = 2 * SL::BYTES, REC0 = RAW0 + SL::RAW, BYTES = REC0 + PK_MAX_TILES * sizeof(PkTile);
+    static_assert(2 * BYTES <= 160 * 1024, "two workgroups fit a CU's LDS");
+};
+
+// the tiles of one workgroup, all of one width (T64: 64 activations); smem: PkGeom's LDS
+template <int F, bool CONTRACT, bool T64>
+__device__ __forceinline__ void pk_body(const PkTile *__restrict__ tiles, int k0, int nt, uint8_t *smem) {
+    using FM = MkFmt<F>;
+    using SL = MkSlot<128>;
+    constexpr int ST_QS = SL::QS, ST_BS = SL::BS, ST_D = SL::D, ST_BYTES = SL::BYTES;
+    constexpr bool FUSED = CONTRACT && F != ES_HIP_Q5_K;
+    constexpr bool BSUMS = F != ES_HIP_Q3_K;
+    constexpr int NW = F == ES_HIP_Q5_K ? 4 : 3;
+    constexpr uint32_t RAW0 = PkGeom<F, CONTRACT>::RAW0, REC0 = PkGeom<F, CONTRACT>::REC0;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+    const uint32_t smem0 = lds_addr(smem);
+    for (int i = tid; i < nt * (int)(sizeof(PkTile) / 16); i += 256)
+        *reinterpret_cast<uint4 *>(smem + REC0 + 16 * i) = ldg<uint4>(reinterpret_cast<const uint8_t *>(tiles + k0) + 16 * i);
+    __syncthreads();
+
+    struct Rec {
+        const uint8_t *w, *act;
+        float *y;
+        uint32_t astride, ystride4, row_bytes;
+        int nbk, t64, tok0, na, rows, ntok;
+    };
+    auto rec = [&](int k) {   // tile k of the workgroup, in scalar registers
+        const uint32_t a = smem0 + REC0 + (uint32_t)k * (uint32_t)sizeof(PkTile);
+        const u32x4 v0 = lds_ld<u32x4>(a), v1 = lds_ld<u32x4>(a + 16), v2 = lds_ld<u32x4>(a + 32), v3 = lds_ld<u32x4>(a + 48);
+        auto u = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
+        auto p = [&](uint32_t lo, uint32_t hi) { return (uint64_t)u(lo) | (uint64_t)u(hi) << 32; };
+        Rec r;
+        r.w = reinterpret_cast<const uint8_t *>(p(v0.x, v0.y));
+        r.act = reinterpret_cast<const uint8_t *>(p(v0.z, v0.w));
+        r.y = reinterpret_cast<float *>(p(v1.x, v1.y));
+        r.astride = u(v1.z);
+        r.ystride4 = u(v1.w);
+        r.row_bytes = u(v2.x);
+        r.nbk = (int)u(v2.y);
+        r.t64 = (int)u(v2.z);
+        r.tok0 = (int)u(v2.w);
+        r.na = (int)u(v3.x);
+        r.rows = (int)u(v3.y);
+        r.ntok = (int)u(v3.z);
+        return r;
+    };
+    // the per-lane sources of a tile (see mk_kernel): value chunks (NVt = 8, or 4 for 64 activations), scale, raw bsums,
+    // weight row
+    struct Src {
+        uint32_t q[8], d, raw, w;
+    };
+    auto sources = [&](const Rec &r) {
+        auto act_off = [&](int t) { return (uint32_t)min(r.tok0 + t, r.na - 1) * r.astride; };
+        const int tw = r.t64 ? 16 : 32, rw = r.t64 ? 2 : 4;
+        Src c;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int t = tw * wave + 4 * (k & (r.t64 ? 3 : 7)) + (lane >> 4);
+            c.q[k] = act_off(t) + 4 + 16 * ((lane & 15) ^ (t & 15));
+        }
+        c.d = act_off(64 * (r.t64 ? 0 : (wave & 1)) + lane);
+        c.raw = act_off(32 * (wave % rw) + (lane >> 1)) + 260 + 16 * (lane & 1);
+        c.w = (uint32_t)min(16 * wave + lr, r.rows - 1) * r.row_bytes;
+        return c;
+    };
+    auto sb_base = [&](const uint8_t *act, int b) {
+        uint32_t sb = 292u * (uint32_t)b;
+        asm volatile("" : "+s"(sb));
+        return act + sb;
+    };
+    // the copies of superblock b of a tile into slot st (values, scale, raw bsums) from its sources c
+    auto stage = [&](const Rec &r, const Src &c, int b, int st) {
+        const uint8_t *ab = sb_base(r.act, b);
+        const uint32_t so = smem0 + (uint32_t)st * ST_BYTES;
+        if (r.t64) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) load_lds16(ab, c.q[k], so + ST_QS + (uint32_t)(16 * wave) * TROW + 4 * TROW * k);
+            load_lds4(ab, c.d, so + ST_D);
+            if constexpr (BSUMS) load_lds16(ab, c.raw, smem0 + RAW0 + 1024u * (uint32_t)(wave & 1));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) load_lds16(ab, c.q[k], so + ST_QS + (uint32_t)(32 * wave) * TROW + 4 * TROW * k);
+            load_lds4(ab, c.d, so + ST_D + 256 * (wave & 1));
+            if constexpr (BSUMS) load_lds16(ab, c.raw, smem0 + RAW0 + 1024u * (uint32_t)wave);
+        }
+    };
+    // the same for a tile's first superblock while the previous tile is current: each source offset formed as it is issued
+    auto stage_first = [&](const Rec &r, int st) {
+        const uint8_t *ab = r.act;
+        const uint32_t so = smem0 + (uint32_t)st * ST_BYTES;
+        auto act_off = [&](int t) { return (uint32_t)min(r.tok0 + t, r.na - 1) * r.astride; };
+        const int tw = r.t64 ? 16 : 32, nv = r.t64 ? 4 : 8, rw = r.t64 ? 2 : 4, ds = r.t64 ? 0 : (wave & 1);
+        for (int k = 0; k < nv; k++) {
+            const int t = tw * wave + 4 * k + (lane >> 4);
+            load_lds16(ab, act_off(t) + 4 + 16 * ((lane & 15) ^ (t & 15)), so + ST_QS + (uint32_t)(tw * wave) * TROW + 4 * TROW * k);
+        }
+        load_lds4(ab, act_off(64 * ds + lane), so + ST_D + 256 * ds);
+        if constexpr (BSUMS)
+            load_lds16(ab, act_off(32 * (wave % rw) + (lane >> 1)) + 260 + 16 * (lane & 1), smem0 + RAW0 + 1024u * (uint32_t)(wave % rw));
+    };
+    // the raw bsums this thread copied (its wave waited for them) as halves into slot st
+    auto bs_convert = [&](int st, int t64) {
+        const int T = t64 ? 64 : 128;
+        const int bt = (tid >> 1) & (T - 1), bh = tid & 1;
+        const u32x4 v = lds_ld<u32x4>(smem0 + RAW0 + 16u * (uint32_t)(tid & (2 * T - 1)));
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t hv[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const _Float16 e0 = (_Float16)(int16_t)(w[k] & 0xffffu), e1 = (_Float16)(int16_t)(w[k] >> 16);
+            hv[k] = (uint32_t)__builtin_bit_cast(uint16_t, e0) | (uint32_t)__builtin_bit_cast(uint16_t, e1) << 16;
+        }
+        uint8_t *base = smem + st * ST_BYTES + ST_BS + (2 * bh) * (128 * 8) + bt * 8;
+        *reinterpret_cast<uint2 *>(base) = make_uint2(hv[0], hv[1]);
+        *reinterpret_cast<uint2 *>(base + 128 * 8) = make_uint2(hv[2], hv[3]);
+    };
+    auto wload = [&](const uint8_t *wrow, uint32_t woff, int b, WRaw<F> &W) {
+        const uint8_t *p = wrow + woff + (uint32_t)FM::BB * (uint32_t)b;
+        if constexpr (F == ES_HIP_Q3_K) {
+            W.h = ldg_u128_a2(p + 94);
+            W.q = ldg_u128_a2(p + FM::QS + 16 * lg);
+            W.hm = ldg_u128_a2(p + FM::QH + 16 * (lg & 1));
+        } else {
+            W.h = ldg<uint4>(p);
+            W.q0 = ldg<uint4>(p + FM::QS + 16 * lg);
+            W.q1 = ldg<uint4>(p + FM::QS + 64 + 16 * lg);
+            if constexpr (F == ES_HIP_Q5_K) W.qh = ldg<uint4>(p + FM::QH + 16 * (lg & 1));
+        }
+    };
+
+    // A operand offsets in a slot (the 128-activation layout)
+    uint32_t xo[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int nat = F == ES_HIP_Q3_K ? 8 * (lg >> 1) + 2 * s + (lg & 1) : 4 * (lg >> 1) + 8 * (s >> 1) + 2 * (s & 1) + (lg & 1);
+        xo[s] = ST_QS + lr * TROW + 16 * (nat ^ lr);
+    }
+    const uint32_t bso = ST_BS + lg * (128 * 8) + lr * 8, ydo = ST_D + 16 * lg;
+    auto aload = [&](const uint32_t (&xa)[4], uint32_t ba, uint32_t ya, int tt, AOps &A) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) A.x[s] = lds_ld<v4i>(xa[s] + 16 * TROW * tt);
+        if constexpr (BSUMS) A.bs = lds_ld<v4h>(ba + 128 * tt);
+        A.yd = lds_ld<v4f>(ya + 64 * tt);
+    };
+
+    v4f acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) acc[t] = v4f{0, 0, 0, 0};
+    Pend<F> p0, p1;
+    p0.m = MAcc<F>{};
+    p0.yd = v4f{0, 0, 0, 0};
+    p0.d = p0.dm = 0.f;
+    p1 = p0;
+    const Pend<F> pzero = p0;
+
+    // The matrix work of one item over its activation tiles (slot base so). A 64-activation tile leaves after four
+    // steps: its last two epilogues run there and the pending slots are cleared (the next item's first two steps then
+    // add +0 to accumulators 6 and 7, which such a tile never stores).
+    auto steps = [&](auto t64c, uint32_t so, const BOps<F> &B) {
+        constexpr bool t64 = decltype(t64c)::value;
+        const uint32_t xa[4] = {smem0 + so + xo[0], smem0 + so + xo[1], smem0 + so + xo[2], smem0 + so + xo[3]};
+        const uint32_t ba = smem0 + so + bso, ya = smem0 + so + ydo;
+        AOps A[2];
+        aload(xa, ba, ya, 0, A[0]);
+#pragma unroll
+        for (int tt = 0; tt < (t64 ? 4 : 8); tt++) {
+            if (tt + 1 < (t64 ? 4 : 8)) aload(xa, ba, ya, tt + 1, A[(tt + 1) & 1]);
+            MAcc<F> cur;
+            mma<F>(A[tt & 1], B, cur);
+            epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[(tt + 6) % 8]);
+            p0 = p1;
+            p1.m = cur;
+            p1.yd = A[tt & 1].yd;
+            p1.d = B.d;
+            p1.dm = B.dm;
+            step_schedule<F == ES_HIP_Q5_K ? 13 : F == ES_HIP_Q3_K ? 8 : 9>();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (t64) {
+            epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[2]);
+            epilogue<F, FUSED>(p1.m, p1.d, p1.dm, p1.yd, acc[3]);
+            p0 = pzero;
+            p1 = pzero;
+        }
+    };
+    // a finished tile: the two pending epilogues, the outputs of all eight activation tiles (buffer stores checked against
+    // the tile's range: activations past ntok, among them every one of a 64-wide tile's upper half, and rows past rows
+    // are dropped), the accumulators and pending slots cleared
+    auto flush = [&](const Rec &r) {
+        epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[6]);
+        epilogue<F, FUSED>(p1.m, p1.d, p1.dm, p1.yd, acc[7]);
+        p0 = pzero;
+        p1 = pzero;
+        const int row = 16 * wave + lr;
+        const uint32_t yrange = (uint32_t)(r.ntok - 1) * r.ystride4 + 4u * (uint32_t)r.rows;
+        const __amdgpu_buffer_rsrc_t yrsrc = __builtin_amdgcn_make_buffer_rsrc((void *)r.y, (short)0, (int)yrange, 0x00020000);
+        uint32_t yoff = row < r.rows ? (uint32_t)(4 * lg) * r.ystride4 + 4u * (uint32_t)row : 0x80000000u;
+#pragma unroll
+        for (int tt = 0; tt < 8; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float v = acc[tt][i];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrsrc, (int)yoff, 0, 0);
+                yoff += i < 3 ? r.ystride4 : 13 * r.ystride4;
+            }
+#pragma unroll
+        for (int t = 0; t < 8; t++) acc[t] = v4f{0, 0, 0, 0};
+    };
+
+    // ---- the item stream. rc: the current tile (k), rn: the next (or rc again past the last); C: rc's sources
+    int k = 0;
+    Rec rc = rec(0), rn = rec(nt > 1 ? 1 : 0);
+    Src C = sources(rc);
+    WRaw<F> Wa, Wb;
+    stage(rc, C, 0, 0);
+    wload(rc.w, C.w, 0, Wa);
+    wload(rc.w, C.w, 1, Wb);
+    wait_vmcnt<NW>();
+    if constexpr (BSUMS) bs_convert(0, rc.t64);
+
+    // One item: superblock j of the current tile in slot j & 1, its weights in register set Wc (tiles have an even number
+    // of superblocks, so every tile starts at j = 0 in slot 0 with its weights in Wa, and a pair of items never spans two
+    // tiles). At the tile's last item its outputs are stored and the next tile becomes current.
+    int j = 0;
+    auto item = [&](auto t64c, auto slc, WRaw<F> &Wc) {
+        constexpr int sl = decltype(slc)::value;
+        lds_sync();
+        BOps<F> B;
+        build_b<F>(Wc, lg, B);
+        b_ready<F>(B);
+        // the copies of the next item: superblock j + 1 of this tile, else the next tile's first
+        const bool more = k + 1 < nt;
+        int t64n = rc.t64;
+        if (j + 1 < rc.nbk || !more) {
+            stage(rc, C, min(j + 1, rc.nbk - 1), 1 - sl);
+        } else {
+            stage_first(rn, 1 - sl);
+            t64n = rn.t64;
+        }
+        // the weights of the item after: superblock j + 2 of this tile, else of the next (every tile has >= 2)
+        {
+            const bool here = j + 2 < rc.nbk || !more;
+            const uint8_t *wr = here ? rc.w : rn.w;
+            const uint32_t wo = here ? C.w : (uint32_t)min(16 * wave + lr, rn.rows - 1) * rn.row_bytes;
+            const int bw = j + 2 < rc.nbk ? j + 2 : more ? j + 2 - rc.nbk : rc.nbk - 1;
+            wload(wr, wo, bw, Wc);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        steps(t64c, (uint32_t)sl * ST_BYTES, B);
+        wait_vmcnt<NW>();   // this wave's copies of the next item (the weights after it may still be in flight)
+        if constexpr (BSUMS) bs_convert(1 - sl, t64n);
+        if (++j == rc.nbk) {
+            flush(rc);
+            j = 0;
+            if (++k < nt) {
+                rc = rn;
+                rn = rec(k + 1 < nt ? k + 1 : k);
+                C = sources(rc);
+            }
+        }
+    };
+    while (k < nt) {
+        item(std::integral_constant<bool, T64>{}, std::integral_constant<int, 0>{}, Wa);
+        item(std::integral_constant<bool, T64>{}, std::integral_constant<int, 1>{}, Wb);
+    }
+}
+
+// Workgroups [0, g64) take tiles of 64 activations, the others tiles of 128: two separate bodies, chosen once.
+template <int F, bool CONTRACT>
+__global__ __launch_bounds__(256, 2) void pk_kernel(const PkTile *__restrict__ tiles, const int *__restrict__ wgptr, int g64) {
+    __shared__ __align__(16) uint8_t smem[PkGeom<F, CONTRACT>::BYTES];
+    const int k0 = wgptr[blockIdx.x], nt = wgptr[blockIdx.x + 1] - k0;
+    if (nt <= 0) return;
+    if ((int)blockIdx.x < g64) pk_body<F, CONTRACT, true>(tiles, k0, nt, smem);
+    else pk_body<F, CONTRACT, false>(tiles, k0, nt, smem);
 }
 
 }  // namespace
@@ -490,6 +824,20 @@ hipError_t mk_launch(int type, bool gather, int tok, const MkJob *jobs, int njob
     if (type == ES_HIP_Q4_K) mk_launch_fmt<ES_HIP_Q4_K>(tok, gather, contract, jobs, njobs, single, grid, s);
     else if (type == ES_HIP_Q5_K) mk_launch_fmt<ES_HIP_Q5_K>(tok, gather, false, jobs, njobs, single, grid, s);   // never fused
     else if (type == ES_HIP_Q3_K) mk_launch_fmt<ES_HIP_Q3_K>(tok, gather, contract, jobs, njobs, single, grid, s);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+template <int F>
+static void pk_launch_fmt(bool contract, const PkTile *tiles, const int *wgptr, int grid, int g64, hipStream_t s) {
+    if (contract) hipLaunchKernelGGL((pk_kernel<F, true>), dim3(grid), dim3(256), 0, s, tiles, wgptr, g64);
+    else hipLaunchKernelGGL((pk_kernel<F, false>), dim3(grid), dim3(256), 0, s, tiles, wgptr, g64);
+}
+
+hipError_t pk_launch(int type, const PkTile *tiles, const int *wgptr, int grid, int g64, int order, hipStream_t s) {
+    const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
+    if (type == ES_HIP_Q4_K) pk_launch_fmt<ES_HIP_Q4_K>(contract, tiles, wgptr, grid, g64, s);
+    else if (type == ES_HIP_Q3_K) pk_launch_fmt<ES_HIP_Q3_K>(contract, tiles, wgptr, grid, g64, s);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

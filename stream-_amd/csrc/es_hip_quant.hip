@@ -47,6 +47,7 @@ int hip_fail(hipError_t e, const char *what) {
 struct Device {
     int ok = 0;
     int id = -1;
+    int cus = 256;   // compute units (the persistent kernels' grids)
     std::string arch, why;
 };
 
@@ -73,6 +74,7 @@ Device &device() {
             return;
         }
         d.id = cur;
+        d.cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
         d.ok = 1;
     });
     return d;
@@ -306,9 +308,27 @@ struct MkGroup {   // one direct-activation matrix-core launch: products of one 
     size_t off = 0;
 };
 
+// One launch of the persistent direct kernel (es_hip_mk.hip): every eligible product of one format, cut into tiles of
+// MK_ROWS rows x 128 or 64 activations and scheduled over the workgroups by the host (pk_schedule).
+struct PkGroup {
+    int type;
+    struct Prod {
+        const uint8_t *W, *act;
+        float *y;
+        uint32_t astride, ystride, row_bytes;
+        int r0, r1, nbk, na;
+    };
+    std::vector<Prod> prods;
+    std::vector<esq::PkTile> tiles;   // in workgroup order
+    std::vector<int> wgptr;           // grid + 1 entries: workgroup g takes tiles[wgptr[g] .. wgptr[g + 1])
+    int grid = 0, g64 = 0;            // workgroups [0, g64) take the 64-wide tiles
+    size_t off = 0;                   // byte offset of the tiles in the device image; wgptr follows them
+};
+
 struct Batch {
     std::vector<Group> mv;
     std::vector<MkGroup> mkg;
+    std::vector<PkGroup> pkg;
     std::vector<Prep> preps;
     std::vector<std::pair<int, esq::MmJob>> mm;   // (type, job); xq / xm hold workspace offsets until bind(); copied into mmg
     std::vector<MmGroup> mmg;
@@ -410,6 +430,155 @@ bool mk_eligible(const Req &q) {
            ((size_t)q.na + esq::MK_TOK) * mk_ystride(q) * sizeof(float) < ((size_t)1 << 31);
 }
 
+std::atomic<int> g_pk_on{1};   // the persistent direct kernel (0: products take the per-tile launches)
+
+// The persistent direct kernel: Q4_K / Q3_K products that the direct kernels take (at least g_mk_min / g_mk3_min
+// activations), with an even number (>= 2) of superblocks per row and no gathered activations, every activation row
+// within 4 GiB of act and a tile's outputs (128 activations) within 2^31 bytes of its first.
+bool pk_eligible(const Req &q) {
+    if (!g_pk_on.load() || q.arow || q.ints || q.r1 <= q.r0) return false;
+    if (q.type != ES_HIP_Q4_K && q.type != ES_HIP_Q3_K) return false;
+    const int mn = q.type == ES_HIP_Q3_K ? g_mk3_min.load() : g_mk_min.load(), nbk = q.cols / 256;
+    if (mn <= 0 || q.na < mn || nbk < 2 || (nbk & 1)) return false;
+    const size_t stride = q.astride ? q.astride : (size_t)nbk * 292;
+    // (a tile's stores past its activations fall outside its range only when consecutive activations' outputs are at
+    // least a tile's rows apart)
+    return (size_t)q.na * stride < ((size_t)1 << 32) - 65536 && mk_ystride(q) >= (size_t)std::min(esq::MK_ROWS, q.r1 - q.r0) &&
+           (size_t)esq::MK_TOK * mk_ystride(q) * sizeof(float) < ((size_t)1 << 31);
+}
+
+// Relative cost of a tile: its superblocks (a 64-wide one does ~0.6 of a 128-wide one's work: the same unpacking and
+// weight loads for half the matrix work) and a fixed part for its first loads and its stores.
+double pk_cost(int nbk, bool t64) { return nbk * (t64 ? 0.6 : 1.0) + 1.0; }
+
+// The schedule of a persistent launch: grid = 2 workgroups per CU; workgroups [0, g64) take 64-wide tiles, the rest
+// 128-wide ones. A product takes 64-wide tiles when it has at most 64 activations or when one 128-wide tile would cost
+// more than a workgroup's mean load (a long row against few row tiles: config 2's down product). Some 128-wide tiles are
+// then cut in two and moved to the 64-wide workgroups until both sets of workgroups carry about the same load. Within
+// each set, all tiles of a row tile go to one XCD (workgroup g runs on XCD g % 8: its L2 reads the row tile's weights
+// once), row tiles are spread over the XCDs and tiles over an XCD's workgroups longest first, each to the least loaded.
+// Returns false when some workgroup would get more than PK_MAX_TILES tiles.
+bool pk_schedule(PkGroup &g, int cus) {
+    const int G = 2 * std::max(cus, 8) / 8 * 8;
+    struct Tl { int p, rt, t0, nt; bool t64; double c; };
+    std::vector<Tl> v128, v64;
+    double mean = 0;
+    for (const PkGroup::Prod &p : g.prods)
+        mean += (double)((p.r1 - p.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS) * ((p.na + 127) / 128) * pk_cost(p.nbk, false);
+    mean /= G;
+    for (int pi = 0; pi < (int)g.prods.size(); pi++) {
+        const PkGroup::Prod &p = g.prods[pi];
+        const int rts = (p.r1 - p.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS;
+        const bool t64 = p.na <= 64 || pk_cost(p.nbk, false) > mean;
+        const int T = t64 ? 64 : 128;
+        for (int rt = 0; rt < rts; rt++)
+            for (int t0 = 0; t0 < p.na; t0 += T)
+                (t64 ? v64 : v128).push_back(Tl{pi, rt, t0, std::min(T, p.na - t0), t64, pk_cost(p.nbk, t64)});
+    }
+    // LPT of a tile set over workgroups [base, base + n) (n a multiple of 8), row tiles kept on one XCD
+    auto lpt = [&](const std::vector<Tl> &ts, int base, int n, std::vector<std::vector<int>> &own, std::vector<double> &load) {
+        std::map<std::pair<int, int>, double> rtc;   // (product, row tile) -> cost
+        for (const Tl &t : ts) rtc[{t.p, t.rt}] += t.c;
+        std::vector<std::pair<double, std::pair<int, int>>> order;
+        for (auto &e : rtc) order.push_back({e.second, e.first});
+        std::stable_sort(order.begin(), order.end(), [](const auto &a, const auto &b) { return a.first > b.first; });
+        double xl[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        std::map<std::pair<int, int>, int> xcd;
+        for (auto &o : order) {
+            int x = 0;
+            for (int i = 1; i < 8; i++)
+                if (xl[i] < xl[x]) x = i;
+            xcd[o.second] = x;
+            xl[x] += o.first;
+        }
+        std::vector<int> idx(ts.size());
+        for (size_t i = 0; i < ts.size(); i++) idx[i] = (int)i;
+        std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return ts[a].c > ts[b].c; });
+        for (int i : idx) {
+            const int x = xcd[{ts[i].p, ts[i].rt}];
+            int best = -1;
+            for (int w = base + ((x - base) % 8 + 8) % 8; w < base + n; w += 8)
+                if (best < 0 || load[w] < load[best]) best = w;
+            own[best].push_back(i);
+            load[best] += ts[i].c;
+        }
+    };
+    // choose g64 (and the 128-wide tiles cut in two) for the smallest makespan
+    double best_ms = 1e300;
+    int best_g64 = 0, best_h = 0;
+    const double w64 = [&] { double w = 0; for (const Tl &t : v64) w += t.c; return w; }();
+    const double w128 = [&] { double w = 0; for (const Tl &t : v128) w += t.c; return w; }();
+    std::vector<int> cands;
+    if (v64.empty()) cands.push_back(0);
+    else if (v128.empty()) cands.push_back(G);
+    else
+        for (int c = 8; c <= G - 8; c += 8) cands.push_back(c);
+    auto build = [&](int g64, int h, std::vector<Tl> &a64, std::vector<Tl> &a128) {
+        a64 = v64;
+        a128.assign(v128.begin(), v128.end() - h);
+        for (auto it = v128.end() - h; it != v128.end(); ++it) {   // cut in two 64-wide tiles
+            const PkGroup::Prod &p = g.prods[it->p];
+            for (int t0 = it->t0; t0 < it->t0 + it->nt; t0 += 64)
+                a64.push_back(Tl{it->p, it->rt, t0, std::min(64, it->t0 + it->nt - t0), true, pk_cost(p.nbk, true)});
+        }
+        (void)g64;
+    };
+    for (int g64 : cands) {
+        int h = 0;
+        if (g64 > 0 && g64 < G && !v128.empty()) {
+            const double c128 = v128.back().c, c64 = pk_cost(g.prods[v128.back().p].nbk, true);
+            const double hh = (w128 * g64 - w64 * (G - g64)) / (2 * c64 * (G - g64) + c128 * g64);
+            h = std::max(0, std::min((int)v128.size(), (int)std::lround(hh)));
+        }
+        std::vector<Tl> a64, a128;
+        build(g64, h, a64, a128);
+        if ((!a64.empty() && g64 == 0) || (!a128.empty() && g64 == G)) continue;
+        std::vector<std::vector<int>> own(G);
+        std::vector<double> load(G, 0.0);
+        if (!a64.empty()) lpt(a64, 0, g64, own, load);
+        if (!a128.empty()) lpt(a128, g64, G - g64, own, load);
+        const double ms = *std::max_element(load.begin(), load.end());
+        if (ms < best_ms - 1e-9) { best_ms = ms; best_g64 = g64; best_h = h; }
+    }
+    std::vector<Tl> a64, a128;
+    build(best_g64, best_h, a64, a128);
+    std::vector<std::vector<int>> own(G);
+    std::vector<double> load(G, 0.0);
+    if (!a64.empty()) lpt(a64, 0, best_g64, own, load);
+    std::vector<std::vector<int>> own128(G);
+    if (!a128.empty()) lpt(a128, best_g64, G - best_g64, own128, load);
+    g.grid = G;
+    g.g64 = best_g64;
+    g.tiles.clear();
+    g.wgptr.assign(1, 0);
+    for (int w = 0; w < G; w++) {
+        const bool is64 = w < best_g64;
+        const std::vector<int> &mine = is64 ? own[w] : own128[w];
+        if ((int)mine.size() > esq::PK_MAX_TILES) return false;
+        for (int i : mine) {
+            const Tl &t = is64 ? a64[i] : a128[i];
+            const PkGroup::Prod &p = g.prods[t.p];
+            const int row0 = p.r0 + esq::MK_ROWS * t.rt;
+            esq::PkTile r{};
+            r.w = p.W + (size_t)row0 * p.row_bytes;
+            r.act = p.act;
+            r.y = p.y + (size_t)t.t0 * p.ystride + row0;
+            r.astride = p.astride;
+            r.ystride4 = 4u * p.ystride;
+            r.row_bytes = p.row_bytes;
+            r.nbk = p.nbk;
+            r.t64 = t.t64 ? 1 : 0;
+            r.tok0 = t.t0;
+            r.na = p.na;
+            r.rows = std::min(esq::MK_ROWS, p.r1 - row0);
+            r.ntok = t.nt;
+            g.tiles.push_back(r);
+        }
+        g.wgptr.push_back((int)g.tiles.size());
+    }
+    return true;
+}
+
 bool mb_eligible(const Req &q) {
     const int mn = g_mb_min.load();
     return (q.type == ES_HIP_Q4_0 || q.type == ES_HIP_Q5_0 || q.type == ES_HIP_Q8_0) && mn > 0 && q.na >= mn && !q.ints &&
@@ -439,7 +608,7 @@ const Prep &get_prep(Batch &bt, const Req &q, const FmtInfo &f, int kind, int na
     return bt.preps.back();
 }
 
-int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
+int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
     bt = Batch();
     std::vector<Req> mv;
     for (const Req &q : reqs) {
@@ -544,6 +713,17 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
             g->jobs.push_back(j);
             continue;
         }
+        if (allow_pk && pk_eligible(q)) {   // the persistent direct kernel: one launch per format, scheduled below
+            PkGroup *g = nullptr;
+            for (PkGroup &x : bt.pkg)
+                if (x.type == (int)q.type) g = &x;
+            if (!g) { bt.pkg.push_back(PkGroup{(int)q.type}); g = &bt.pkg.back(); }
+            const int nbk = q.cols / 256;
+            g->prods.push_back(PkGroup::Prod{static_cast<const uint8_t *>(q.W), static_cast<const uint8_t *>(q.act), q.y,
+                                             (uint32_t)(q.astride ? q.astride : (size_t)nbk * 292), (uint32_t)mk_ystride(q),
+                                             (uint32_t)((size_t)nbk * f.bb), q.r0, q.r1, nbk, q.na});
+            continue;
+        }
         if (mk_eligible(q)) {   // one launch per format and tile; MK_ROWS x tok tiles, 8 consecutive ids per row tile group
             const int tok = mk_tok(q);
             MkGroup *g = nullptr;
@@ -638,11 +818,17 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt) {
         g->grid += 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
         g->jobs.push_back(j);
     }
+    for (PkGroup &g : bt.pkg)
+        if (!pk_schedule(g, device().cus)) return plan_batch(reqs, bt, false);   // too many tiles for one launch
     if (int rc = plan_groups(mv, bt.mv)) return rc;
     size_t off = 0;
     for (const Group &g : bt.mv) {
         bt.mv_off.push_back(off);
         off += align256(g.jobs.size() * sizeof(MvJob));
+    }
+    for (PkGroup &g : bt.pkg) {
+        g.off = off;
+        off += align256(g.tiles.size() * sizeof(esq::PkTile)) + align256(g.wgptr.size() * sizeof(int));
     }
     for (MmGroup &g : bt.mmg) {
         g.off = off;
@@ -703,6 +889,10 @@ std::vector<uint8_t> table_image(const Batch &bt) {
         memcpy(img.data() + bt.mv_off[i], bt.mv[i].jobs.data(), bt.mv[i].jobs.size() * sizeof(MvJob));
     for (const MmGroup &g : bt.mmg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MmJob));
     for (const MkGroup &g : bt.mkg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MkJob));
+    for (const PkGroup &g : bt.pkg) {
+        memcpy(img.data() + g.off, g.tiles.data(), g.tiles.size() * sizeof(esq::PkTile));
+        memcpy(img.data() + g.off + align256(g.tiles.size() * sizeof(esq::PkTile)), g.wgptr.data(), g.wgptr.size() * sizeof(int));
+    }
     for (const MqGroup &g : bt.mqg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MqJob));
     for (const MbGroup &g : bt.mbg) memcpy(img.data() + g.off, g.jobs.data(), g.jobs.size() * sizeof(esq::MbJob));
     if (!bt.pj.empty()) memcpy(img.data() + bt.prep_off, bt.pj.data(), bt.pj.size() * sizeof(esq::PrepJob));
@@ -734,6 +924,12 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
         if ((e = esq::mm_launch(g.type, g.bm, g.bn, g.nw, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s, g.jobs.data())) !=
             hipSuccess)
             return hip_fail(e, "matrix-core launch");
+    }
+    for (const PkGroup &g : bt.pkg) {   // (always from the uploaded tables)
+        if (!tables) return fail(ES_HIP_EINVAL, "the persistent kernel needs its tile tables on the device");
+        const esq::PkTile *tl = reinterpret_cast<const esq::PkTile *>(tables + g.off);
+        const int *wp = reinterpret_cast<const int *>(tables + g.off + align256(g.tiles.size() * sizeof(esq::PkTile)));
+        if ((e = esq::pk_launch(g.type, tl, wp, g.grid, g.g64, order, s)) != hipSuccess) return hip_fail(e, "matrix-core launch");
     }
     for (const MkGroup &g : bt.mkg) {
         const esq::MkJob *dj = tables ? reinterpret_cast<const esq::MkJob *>(tables + g.off) : nullptr;
@@ -803,7 +999,7 @@ void *reg_lookup(const void *h, size_t n) {
 int run_sync(const std::vector<Req> &reqs, hipStream_t s, int order = -1) {   // order -1: es_hip_set_order's
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
-    if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty()) return ES_HIP_OK;
+    if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.pkg.empty()) return ES_HIP_OK;
     hipError_t e = hipStreamSynchronize(s);   // the scratch may still be read by an earlier call's kernels
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     void *dev = nullptr;
@@ -902,7 +1098,7 @@ int es_hip_synchronize(void) {
 static int run_async(const std::vector<Req> &reqs, hipStream_t s) {
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
-    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.mv.size() <= 1 &&
+    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.pkg.empty() && bt.mv.size() <= 1 &&
         (bt.mv.empty() || bt.mv[0].jobs.size() == 1))
         return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
     void *dev = nullptr;
@@ -986,7 +1182,7 @@ int es_hip_matvec_multi_dev_noalloc(uint32_t type, const void *W, int cols, int 
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty())
+    if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.pkg.empty())
         return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
     const size_t ws_at = align256(bt.table_bytes), need = ws_at + bt.ws_bytes;
     if (need > NOALLOC_SCRATCH)
@@ -1105,6 +1301,7 @@ int es_hip_set_direct_mfma_min_batch(int n) { return g_mk_min.exchange(n); }
 int es_hip_set_direct_mfma_min_tiles(int n) { return g_mk_min_tiles.exchange(n); }
 int es_hip_set_q5k_mfma_min_batch(int n) { return g_mk5_min.exchange(n); }
 int es_hip_set_q3k_mfma_min_batch(int n) { return g_mk3_min.exchange(n); }
+int es_hip_set_direct_persistent(int on) { return g_pk_on.exchange(on ? 1 : 0); }
 int es_hip_set_q2k_expert_max_batch(int n) { return g_mx_max.exchange(n); }
 int es_hip_set_batched32_direct(int on) { return g_mbx_on.exchange(on ? 1 : 0); }
 int es_hip_set_q6k_persistent(int on) { return esq::mm6_set_persistent(on); }
