@@ -299,10 +299,11 @@ def cpu_configs(rng, seconds):
     # MoE layers through moe_n's job pattern (src/es_engine.c:871-918): per distinct expert, gate and up against the
     # tokens routed to it, then down; the per-expert products are timed at the mean tokens per expert, over a rotating
     # set of expert matrices
-    for name, (t3, n, ff, n_exp, k, n_tok, norm) in {
-            "config4_q2_k_moe": ((E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False),
-            "config5_mixed_moe_decode": ((E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True)}.items():
-        sel, _ = route_topk(rng, n_tok, n_exp, k, norm)   # the same synthetic routing as the device legs
+    for name, (cfg, t3, n, ff, n_exp, k, n_tok, norm) in {
+            "config4_q2_k_moe": (4, (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False),
+            "config5_mixed_moe_decode": (5, (E.Q4_K, E.Q4_K, E.Q6_K), 2048, 768, 128, 8, 32, True)}.items():
+        # the same synthetic routing as the device legs: their generator's first draw (MoeWorkload routes first)
+        sel, _ = route_topk(moe_rng(cfg), n_tok, n_exp, k, norm)
         used = len(set(sel.reshape(-1).tolist()))
         per = max(1, round(n_tok * k / used))
         pts, ms = {}, {}

@@ -100,11 +100,12 @@ int es_hip_matvec_dev(uint32_t type, const void *W, int cols, int r0, int r1, co
 int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride, int na,
                             float *y, size_t ystride, void *stream);
 /* es_hip_matvec_multi_dev without any device allocation. No counterpart in the reference: it is for callers that cannot
- * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The job tables and the
- * activation pre-pass workspace live in a static device array of ES_HIP_NOALLOC_SCRATCH_BYTES per device, held until the
- * process ends; a product that needs more fails with ES_HIP_EINVAL (es_hip_matvec_multi_dev serves it). Every call on a
- * device shares that array: calls that overlap on one device (different streams, or threads) race; calls ordered on one
- * stream do not. Same outputs as es_hip_matvec_multi_dev, bit for bit. */
+ * allocate (tight serving loops, harnesses that forbid hipMalloc). The job tables and the activation pre-pass workspace
+ * live in a static device array of ES_HIP_NOALLOC_SCRATCH_BYTES per device, held until the process ends; a product that
+ * needs more fails with ES_HIP_EINVAL (es_hip_matvec_multi_dev serves it). Every call on a device shares that array: calls
+ * that overlap on one device (different streams, or threads) race; calls ordered on one stream do not. Not for HIP graph
+ * capture: the tables are copied from host memory at the call, so a capturing stream is refused with ES_HIP_EINVAL.
+ * Same outputs as es_hip_matvec_multi_dev, bit for bit. */
 #define ES_HIP_NOALLOC_SCRATCH_BYTES (32u << 20)
 int es_hip_matvec_multi_dev_noalloc(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride,
                                     int na, float *y, size_t ystride, void *stream);

@@ -152,7 +152,7 @@ int check_req(const Req &q, const FmtInfo &f) {
     const int cmax = f.be == 32 ? ES_HIP_MAX_COLS_32 : ES_HIP_MAX_COLS_256;
     if (q.cols > cmax)
         return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this library handles (ES_HIP_MAX_COLS_*)", q.type, q.cols, cmax);
-    if ((long)q.na * nbk * 73 > (1L << 30)) return fail(ES_HIP_EINVAL, "%d activations of %d columns: above 2^30 words per product", q.na, q.cols);
+    (void)nbk;
     return ES_HIP_OK;
 }
 
@@ -820,6 +820,10 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
     }
     for (PkGroup &g : bt.pkg)
         if (!pk_schedule(g, device().cus)) return plan_batch(reqs, bt, false);   // too many tiles for one launch
+    // a pre-pass numbers its 16-byte items with 32-bit indices
+    for (const Prep &p : bt.preps)
+        if ((long)p.na_pad * p.nbk * esq::prep_words(p.kind) > (1L << 30))
+            return fail(ES_HIP_EINVAL, "%d activations of %d blocks: above 2^30 pre-pass items per product", p.na, p.nbk);
     if (int rc = plan_groups(mv, bt.mv)) return rc;
     size_t off = 0;
     for (const Group &g : bt.mv) {
@@ -1178,10 +1182,16 @@ static int scratch_address(uint8_t **out) {
 int es_hip_matvec_multi_dev_noalloc(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride,
                                     int na, float *y, size_t ystride, void *stream) {
     if (int rc = need_device()) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // Not for graph capture: the job tables are copied from host memory that is gone when the call returns, and every
+    // replay would share the one scratch array.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+        return fail(ES_HIP_EINVAL, "es_hip_matvec_multi_dev_noalloc on a capturing stream: its job tables are copied from host "
+                                   "memory at the call, so it cannot be recorded into a graph");
     std::vector<Req> reqs{{type, W, act, y, nullptr, nullptr, r0, r1, cols, na, astride, ystride}};
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.pkg.empty())
         return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
     const size_t ws_at = align256(bt.table_bytes), need = ws_at + bt.ws_bytes;
@@ -2072,6 +2082,18 @@ int moe_ctx_check(const es_hip_moe_ctx *c, int N, const void *x, const float *ou
     if (N > 1 && ostride && ostride < (size_t)c->n) return fail(ES_HIP_EINVAL, "ostride %zu < n %d", ostride, c->n);
     return ES_HIP_OK;
 }
+// the token rows x as check_req checks a product's activations: dword-aligned rows at least one row's blocks apart
+int moe_ctx_check_x(const es_hip_moe_ctx *c, int N, const void *x, size_t xstride) {
+    if (N == 0) return ES_HIP_OK;
+    FmtInfo fg;
+    fmt_info(c->gt, fg);
+    const size_t packed = (size_t)(c->n / fg.be) * fg.ab;
+    if ((reinterpret_cast<uintptr_t>(x) & 3) || (xstride & 3))
+        return fail(ES_HIP_EINVAL, "activation rows must be 4-byte aligned (pointer and stride)");
+    if (N > 1 && xstride && xstride < packed)
+        return fail(ES_HIP_EINVAL, "activation stride %zu < %zu bytes of one token's blocks", xstride, packed);
+    return ES_HIP_OK;
+}
 
 }  // namespace
 
@@ -2081,6 +2103,7 @@ int es_hip_moe_ctx_run_logits(es_hip_moe_ctx *c, int N, const float *logits, siz
                               size_t xstride, float *out, size_t ostride, int *sel_out, float *w_out, void *stream) {
     if (int rc = need_device()) return rc;
     if (int rc = moe_ctx_check(c, N, x, out, ostride)) return rc;
+    if (int rc = moe_ctx_check_x(c, N, x, xstride)) return rc;
     if (N == 0) return ES_HIP_OK;
     if (!logits) return fail(ES_HIP_EINVAL, "null logits");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -2099,6 +2122,7 @@ int es_hip_moe_ctx_run(es_hip_moe_ctx *c, int N, const int *sel, const float *w,
                        size_t ostride, void *stream) {
     if (int rc = need_device()) return rc;
     if (int rc = moe_ctx_check(c, N, x, out, ostride)) return rc;
+    if (int rc = moe_ctx_check_x(c, N, x, xstride)) return rc;
     if (N == 0) return ES_HIP_OK;
     if (!sel || !w) return fail(ES_HIP_EINVAL, "null routing");
     hipStream_t s = static_cast<hipStream_t>(stream);

@@ -132,6 +132,12 @@ def test_ctx_rejects_bad_shapes(hip, orc):
     d = hip.alloc(1 << 16)
     with pytest.raises(E.EsHipError):
         ctx.run(9, d, d, d, 0, d, n)         # more tokens than the context holds
+    with pytest.raises(E.EsHipError):
+        ctx.run(2, d, d, d.offset(2), 0, d, n)   # token rows not 4-byte aligned
+    with pytest.raises(E.EsHipError):
+        ctx.run(2, d, d, d, 580, d, n)       # token stride below one token's Q8_K blocks (2 x 292 bytes)
+    with pytest.raises(E.EsHipError):
+        ctx.run(2, d, d, d, 586, d, n)       # token stride not a multiple of 4
     ctx.run(0, d, d, d, 0, d, n)             # nothing to do
     ctx.close()
     bad = E.MoeArgs(E.Q4_K, E.Q4_0, E.Q4_K, n, ff, ex.dev, np.zeros(1, np.int32), np.zeros((1, k), np.int32),

@@ -99,3 +99,31 @@ def test_noalloc_refuses_more_than_the_scratch(hip):
     assert (y == 0x7f7f7f7f).all()
     for b in (dW, dA, dY):
         b.close()
+
+
+def test_noalloc_refuses_graph_capture(hip, orc):
+    """on a stream under HIP graph capture the call is refused with EINVAL (its job tables are copied from host memory at
+    the call, which a captured graph could not replay); the capture ends cleanly and the entry point works after it"""
+    import ctypes as C
+    import glob
+    hiprt = C.CDLL(sorted(glob.glob("/opt/rocm/lib/libamdhip64.so*"))[0])
+    rows, cols, na = 1024, 2048, 40
+    W, acts = make(orc, O.Q4_K, rows, cols, na, 77)
+    dW, dA, dY = hip.upload(W), hip.upload(acts), hip.alloc(na * rows * 4)
+    s, g = C.c_void_p(), C.c_void_p()
+    assert hiprt.hipStreamCreate(C.byref(s)) == 0
+    assert hiprt.hipStreamBeginCapture(s, 2) == 0   # hipStreamCaptureModeRelaxed
+    try:
+        with pytest.raises(E.EsHipError):
+            hip.matvec_multi_dev_noalloc(O.Q4_K, dW, cols, 0, rows, dA, acts.strides[0], na, dY, rows, stream=s.value)
+    finally:
+        rc = hiprt.hipStreamEndCapture(s, C.byref(g))
+        if g.value:
+            hiprt.hipGraphDestroy(g)
+        hiprt.hipStreamDestroy(s)
+    assert rc == 0
+    assert "capturing stream" in hip.last_error()
+    for b in (dW, dA, dY):
+        b.close()
+    y = run(hip, hip.matvec_multi_dev_noalloc, O.Q4_K, W, cols, rows, acts)
+    assert np.array_equal(bits(y), bits(run(hip, hip.matvec_multi_dev, O.Q4_K, W, cols, rows, acts)))
