@@ -98,6 +98,8 @@ struct MkJob {
     uint64_t astride, ystride, row_bytes;
     int r0, r1, cols, na;
     int tile0, ntok_tiles;
+    int rows_per_wg;      // the batched 32-wide kernel's rows per workgroup tile (1 .. MBX_ROWS), set per job by the host
+    int pad_;
 };
 // Expert-sized Q2_K products (es_hip_mx.hip): the same jobs, workgroup tiles of MX_ROWS rows x MX_TOK activations (ntok_tiles
 // per row tile; with one, tile ids are the row tiles themselves), rows of at most MX_NBK superblocks (the whole row's
@@ -111,9 +113,10 @@ int mx_nbk_max(int nbk);
 hipError_t mx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single,
                      int grid, int order, hipStream_t s);
 // Batched 32-wide formats reading the activations' Q8_0 rows directly (es_hip_mbx.hip): the same jobs, workgroup tiles of
-// MBX_ROWS rows x MBX_TOK activations (tile ids as in the expert-sized kernel), rows of at most MBX_NBK blocks (the whole
-// row's activations sit in LDS); mbx_nbk_max gives the LDS size class of a launch's longest row (0: too long).
-constexpr int MBX_TOK = 32, MBX_ROWS = 16, MBX_NBK = 128;
+// rows_per_wg (<= MBX_ROWS) rows x MBX_TOK activations on MBX_WAVES waves (tile ids as in the expert-sized kernel), rows of
+// at most MBX_NBK blocks (the whole row's activations sit in LDS); mbx_nbk_max gives the LDS size class of a launch's
+// longest row (0: too long).
+constexpr int MBX_TOK = 32, MBX_ROWS = 32, MBX_NBK = 128, MBX_WAVES = 8;
 int mbx_nbk_max(int nbk);
 hipError_t mbx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single, int grid,
                       int order, hipStream_t s);

@@ -6,16 +6,20 @@
 // summed at the end as ((0+4)+(2+6))+((1+5)+(3+7)) (src/es_quant.c:1185-1187, 1252-1323); its scalar path adds
 // (d * yd) * (float)sum-of-all-32 to one chain (src/es_quant.c:1013-1055).
 //
-// Work split. A workgroup of 4 waves takes 16 rows x 32 activations; wave w the 4 rows 4w .. 4w + 3. Every activation
-// value and scale of the tile's whole row (at most NBKM blocks) is copied into LDS once, at the start; after one barrier
-// each wave streams its rows' blocks from HBM into registers, P blocks ahead, with no further barrier. (The matrix-core
-// kernel of es_hip_mb.hip read each block's activations from L2 in every wave: 2 KB of activation halves per block and
-// wave against 88 bytes of weights.)
+// Work split. A workgroup of 8 waves (two per SIMD) takes RW <= 32 rows x 32 activations, RW set per job by the host so
+// that a launch's workgroups about fill the CUs once (config 5's q/k/v: 5120 rows in 246 workgroups of 21, instead of
+// 320 of 16 on 256 CUs, which left 64 CUs with twice the work). The RW rows are cut into 8 contiguous runs of 1..4 rows,
+// the longer runs to waves 0, 1, 2, ... so the two waves of a SIMD (w and w + 4) carry about RW / 4 rows between them.
+// Every activation value and scale of the tile's whole row (at most NBKM blocks) is copied into LDS once, at the start;
+// after one barrier each wave streams its rows' blocks from HBM into registers, P blocks ahead, with no further barrier.
+// (The matrix-core kernel of es_hip_mb.hip read each block's activations from L2 in every wave: 2 KB of activation
+// halves per block and wave against 88 bytes of weights.)
 //
-// One v_mfma_i32_32x32x32_i8 per block and wave produces every lane sum of its 4 rows x 32 activations: output row
-// m = 8r + i is (weight row r, group i), and A row m holds only group i's four codes (code - offset, int8) at the four k
-// positions where B (the activation's 32 int8 values) holds that group's values; every other A element is zero. So
-// D[8r + i][n] is lane_i of row r against activation n, exactly, as an int32.
+// One v_mfma_i32_32x32x32_i8 per block and wave produces every lane sum of its (up to) 4 rows x 32 activations: output
+// row m = 8r + i is (weight row r, group i), and A row m holds only group i's four codes (code - offset, int8) at the
+// four k positions where B (the activation's 32 int8 values) holds that group's values; every other A element is zero.
+// So D[8r + i][n] is lane_i of row r against activation n, exactly, as an int32. Rows past the wave's run repeat its last
+// row; their chains are not run and their outputs not stored.
 //
 // Operand layouts of v_mfma_i32_32x32x32_i8 (wave64): lane l supplies A row l % 32 and B column l % 32, both for the 16 k
 // positions 16 (l / 32) .. + 15; D register j of lane l is element [8 (j / 4) + 4 (l / 32) + j % 4][l % 32]. So a lane
@@ -29,6 +33,8 @@
 // Weights: per block a lane reads the aligned dwords around its row's d (and Q5_0 high bits) and its group's code dword
 // (blocks are 18, 22 or 34 bytes, so fields sit at 2-byte alignment; every dword read holds at least one of the block's
 // bytes, so none crosses past the matrix).
+#include <type_traits>
+
 #include "es_hip_common.h"
 
 namespace esq {
@@ -65,10 +71,10 @@ struct Stage {
     uint32_t qa, qb;   // the aligned dwords at and after this lane's code dword
 };
 
-// Tiles of 4 waves x 4 rows against MBX_TOK activations. P: blocks in flight per wave (even). X86: the AVX2 order (else
-// the scalar one).
+// Tiles of 8 waves x J.rows_per_wg (<= MBX_ROWS) rows against MBX_TOK activations. P: blocks in flight per wave (even).
+// X86: the AVX2 order (else the scalar one).
 template <int F, int NBKM, int P, bool X86, bool GATHER>
-__global__ __launch_bounds__(256, NBKM <= 64 ? 2 : 1) void mbx_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
+__global__ __launch_bounds__(64 * MBX_WAVES, 1) void mbx_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
     using BF = BxFmt<F>;
     constexpr int BB = Fmt<F>::BB;
     constexpr uint32_t V0 = 0, D0 = NBKM * 1024;
@@ -86,10 +92,15 @@ __global__ __launch_bounds__(256, NBKM <= 64 ? 2 : 1) void mbx_kernel(const MkJo
         rt = xcd + 8 * (kq / J.ntok_tiles);
         tt = kq % J.ntok_tiles;
     }
-    if (rt * MBX_ROWS >= J.r1 - J.r0) return;
+    const int RW = J.rows_per_wg;
+    if (rt * RW >= J.r1 - J.r0) return;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int n = lane & 31, h = lane >> 5;
-    const int row0 = J.r0 + rt * MBX_ROWS + 4 * wave, tok0 = tt * MBX_TOK;
+    // this wave's run of rows: R (0..4) rows from row0, the longer runs to the first waves (waves w and w + 4 share a SIMD)
+    const int rbase = RW / MBX_WAVES, rext = RW % MBX_WAVES;
+    const int R = rbase + (wave < rext ? 1 : 0);
+    const int row0 = J.r0 + rt * RW + wave * rbase + min(wave, rext), tok0 = tt * MBX_TOK;
+    const int rlast = max(min(row0 + R, J.r1) - 1, J.r0);   // the run's last row (rows past it repeat it)
     const int nbk = J.cols / 32;
     const uint32_t smem0 = lds_addr(smem);
 
@@ -105,21 +116,21 @@ __global__ __launch_bounds__(256, NBKM <= 64 ? 2 : 1) void mbx_kernel(const MkJo
         return J.act + o;
     };
     {
-        // values: block b is one instruction of wave b % 4; lane l writes LDS slot l: activation l / 2, position l % 2,
-        // source chunk (l % 2) ^ ((n >> 3) & 1)
+        // values: block b is one instruction of wave b % MBX_WAVES; lane l writes LDS slot l: activation l / 2, position
+        // l % 2, source chunk (l % 2) ^ ((n >> 3) & 1)
         const int tv = lane >> 1;
         const uint32_t ov = act_off(tv) + 4 + 16 * ((lane & 1) ^ ((tv >> 3) & 1));
-        for (int b = wave; b < nbk; b += 4) load_lds16(blk_base(b), ov, smem0 + V0 + (uint32_t)b * 1024);
+        for (int b = wave; b < nbk; b += MBX_WAVES) load_lds16(blk_base(b), ov, smem0 + V0 + (uint32_t)b * 1024);
         // scales: instruction q covers blocks 2q and 2q + 1 (lane l: block 2q + l / 32, activation l % 32; a block past
         // the last reads the last one again into a slot nobody reads)
         const uint32_t od0 = act_off(n);
-        for (int q = wave; 2 * q < nbk; q += 4) {
+        for (int q = wave; 2 * q < nbk; q += MBX_WAVES) {
             const int b = min(2 * q + h, nbk - 1);
             load_lds4(blk_base(2 * q), od0 + 36u * (uint32_t)(b - 2 * q), smem0 + D0 + (uint32_t)q * 256);
         }
     }
 
-    // ---- this lane's weights: group gi = n % 8 of row row0 + n / 8 (rows past r1 repeat the last; not stored)
+    // ---- this lane's weights: group gi = n % 8 of row row0 + n / 8 (rows past the run repeat its last; not stored)
     const int gi = n & 7, gq = gi & 3;
     const bool mine = (gi >> 2) == h;
     const int nshift = 4 * (gi >> 2);
@@ -128,7 +139,7 @@ __global__ __launch_bounds__(256, NBKM <= 64 ? 2 : 1) void mbx_kernel(const MkJo
     // sit at fixed distances from it: the block's first two aligned dwords (a block is at least 18 bytes), the aligned
     // dword holding the code field's first byte, and the next one unless that would pass the block's last aligned dword
     // (then the field is 4-byte aligned and the second dword is not used).
-    const uint32_t rowoff = static_cast<uint32_t>(min(row0 + (n >> 3), J.r1 - 1)) * static_cast<uint32_t>(J.row_bytes);
+    const uint32_t rowoff = static_cast<uint32_t>(min(row0 + (n >> 3), rlast)) * static_cast<uint32_t>(J.row_bytes);
     uint32_t mis[2], woff[2], qaoff[2], qboff[2];
 #pragma unroll
     for (int e = 0; e < 2; e++) {
@@ -157,93 +168,112 @@ __global__ __launch_bounds__(256, NBKM <= 64 ? 2 : 1) void mbx_kernel(const MkJo
     // 8-byte load), and the first block needs its loads now anyway.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_sync();
+    if (R == 0) return;   // (a tile of fewer than 8 rows; no barrier follows)
+    // the rest for a run of NR rows (a compile-time count: uniform branches per row inside the block loop kept the
+    // compiler from overlapping one block's chains with the next block's matrix work)
+    auto run = [&](auto nrc) {
+        constexpr int NR = decltype(nrc)::value;
 
-    const uint32_t xo = smem0 + V0 + (uint32_t)n * 32 + 16u * (uint32_t)(h ^ ((n >> 3) & 1)), yo = smem0 + D0 + 4u * n;
-    float acc[16];   // x86: acc[4 r + jj] = chain of group 4 h + jj of row r; scalar: acc[r] = the row's chain
-#pragma unroll
-    for (int j = 0; j < 16; j++) acc[j] = 0.0f;
+        const uint32_t xo = smem0 + V0 + (uint32_t)n * 32 + 16u * (uint32_t)(h ^ ((n >> 3) & 1)), yo = smem0 + D0 + 4u * n;
+        float acc[16];   // x86: acc[4 r + jj] = chain of group 4 h + jj of row r; scalar: acc[r] = the row's chain
+    #pragma unroll
+        for (int j = 0; j < 16; j++) acc[j] = 0.0f;
 
-    struct Issued { v16i d; float dy[4]; };
-    auto issue = [&](const Stage &c, int b, Issued &o) {   // block b's MFMA and its d * yd for rows 0..3
-        const uint32_t m = mis[b & 1];
-        const uint32_t qs = alignbyte(c.qb, c.qa, m ^ 2u);   // the code dword is misaligned exactly when the block is not
-        uint32_t q;
-        if constexpr (BF::BYTES) {
-            q = qs;
-        } else {
-            q = (qs >> nshift) & 0x0f0f0f0fu;
-            if constexpr (F == ES_HIP_Q5_0) {   // bit e of qh -> bit 4 of byte e; qh starts 2 bytes into the block
-                const uint64_t hw = (static_cast<uint64_t>(c.w1) << 32 | c.w0) >> (16 + 8 * m + 4 * gi);
-                q |= (((static_cast<uint32_t>(hw) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+        struct Issued { v16i d; float dy[4]; };
+        auto issue = [&](const Stage &c, int b, Issued &o) {   // block b's MFMA and its d * yd for the run's rows
+            const uint32_t m = mis[b & 1];
+            const uint32_t qs = alignbyte(c.qb, c.qa, m ^ 2u);   // the code dword is misaligned exactly when the block is not
+            uint32_t q;
+            if constexpr (BF::BYTES) {
+                q = qs;
+            } else {
+                q = (qs >> nshift) & 0x0f0f0f0fu;
+                if constexpr (F == ES_HIP_Q5_0) {   // bit e of qh -> bit 4 of byte e; qh starts 2 bytes into the block
+                    const uint64_t hw = (static_cast<uint64_t>(c.w1) << 32 | c.w0) >> (16 + 8 * m + 4 * gi);
+                    q |= (((static_cast<uint32_t>(hw) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+                }
+                q = (q + BF::ADD) ^ 0x80808080u;   // c - offset as signed bytes
             }
-            q = (q + BF::ADD) ^ 0x80808080u;   // c - offset as signed bytes
+            q = mine ? q : 0u;
+            const v4i a = v4i{gq == 0 ? (int)q : 0, gq == 1 ? (int)q : 0, gq == 2 ? (int)q : 0, gq == 3 ? (int)q : 0};
+            const v4i x = lds_ld<v4i>(xo + (uint32_t)b * 1024);
+            o.d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, x, v16i{}, 0, 0, 0);
+            const float yd = lds_ld<float>(yo + (uint32_t)b * 128);
+            // d of rows 0..NR-1 (float), read from lanes 0, 8, 16, 24, which loaded them
+            const float wd = half_bits_to_float(alignbyte(c.w0, c.w0, m));
+    #pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (r < NR) o.dy[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wd), 8 * r)) * yd;
+        };
+        auto chain = [&](const Issued &o) {   // the chains of the run's rows (R is wave-uniform)
+            if constexpr (X86) {
+    #pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (r < NR) {
+    #pragma unroll
+                        for (int jj = 0; jj < 4; jj++)
+                            acc[4 * r + jj] = __builtin_fmaf(static_cast<float>(o.d[4 * r + jj]), o.dy[r], acc[4 * r + jj]);
+                    }
+            } else {
+    #pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (r < NR) {
+                        // the block's integer sum: this lane's four groups, then the other four
+                        int s4 = (o.d[4 * r] + o.d[4 * r + 1]) + (o.d[4 * r + 2] + o.d[4 * r + 3]);
+                        s4 += __shfl_xor(s4, 32);
+                        acc[r] = acc[r] + o.dy[r] * static_cast<float>(s4);
+                    }
+            }
+        };
+
+        // Chunks of P blocks: block b0 + p is in st[p] (b0 is a multiple of P) and its results in io[p & 1]. Block b's MFMA is
+        // issued before block b - 1's chains, and the last block's chains follow its own issue; the stage is refilled with
+        // block b + P (or the last block again) right after. Every index is a compile-time constant (a runtime index would put
+        // io in scratch memory).
+        Issued io[2];
+        for (int b0 = 0; b0 < nbk; b0 += P) {
+    #pragma unroll
+            for (int p = 0; p < P; p++) {
+                const int b = b0 + p;
+                if (b < nbk) {
+                    issue(st[p], b, io[p & 1]);
+                    if (b > 0) chain(io[(p + 1) & 1]);
+                    if (b == nbk - 1) chain(io[p & 1]);
+                }
+                load(st[p], min(b + P, nbk - 1));
+            }
         }
-        q = mine ? q : 0u;
-        const v4i a = v4i{gq == 0 ? (int)q : 0, gq == 1 ? (int)q : 0, gq == 2 ? (int)q : 0, gq == 3 ? (int)q : 0};
-        const v4i x = lds_ld<v4i>(xo + (uint32_t)b * 1024);
-        o.d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, x, v16i{}, 0, 0, 0);
-        const float yd = lds_ld<float>(yo + (uint32_t)b * 128);
-        // d of rows 0..3 (float), read from lanes 0, 8, 16, 24, which loaded them
-        const float wd = half_bits_to_float(alignbyte(c.w0, c.w0, m));
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            o.dy[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wd), 8 * r)) * yd;
+
+        const int t = tok0 + n;
+        const bool tok_ok = t < J.na;
+    #pragma unroll
+        for (int r = 0; r < 4; r++) {
+            if (r >= NR) break;
+            float s;
+            if constexpr (X86) {
+                float u[4];
+    #pragma unroll
+                for (int jj = 0; jj < 4; jj++) u[jj] = acc[4 * r + jj] + __shfl_xor(acc[4 * r + jj], 32);   // acc_jj + acc_(jj+4)
+                s = (u[0] + u[2]) + (u[1] + u[3]);
+            } else {
+                s = acc[r];
+            }
+            const int row = row0 + r;
+            if (h == 0 && tok_ok && row < J.r1) stg<float>(J.y + (size_t)t * J.ystride + row, s);
+        }
     };
-    auto chain = [&](const Issued &o) {
-        if constexpr (X86) {
-#pragma unroll
-            for (int j = 0; j < 16; j++) acc[j] = __builtin_fmaf(static_cast<float>(o.d[j]), o.dy[j >> 2], acc[j]);
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                // the block's integer sum: this lane's four groups, then the other four
-                int s4 = (o.d[4 * r] + o.d[4 * r + 1]) + (o.d[4 * r + 2] + o.d[4 * r + 3]);
-                s4 += __shfl_xor(s4, 32);
-                acc[r] = acc[r] + o.dy[r] * static_cast<float>(s4);
-            }
-        }
-    };
-
-    // Chunks of P blocks: block b0 + p is in st[p] (b0 is a multiple of P) and its results in io[p & 1]. Block b's MFMA is
-    // issued before block b - 1's chains, and the last block's chains follow its own issue; the stage is refilled with
-    // block b + P (or the last block again) right after. Every index is a compile-time constant (a runtime index would put
-    // io in scratch memory).
-    Issued io[2];
-    for (int b0 = 0; b0 < nbk; b0 += P) {
-#pragma unroll
-        for (int p = 0; p < P; p++) {
-            const int b = b0 + p;
-            if (b < nbk) {
-                issue(st[p], b, io[p & 1]);
-                if (b > 0) chain(io[(p + 1) & 1]);
-                if (b == nbk - 1) chain(io[p & 1]);
-            }
-            load(st[p], min(b + P, nbk - 1));
-        }
-    }
-
-    const int t = tok0 + n;
-    const bool tok_ok = t < J.na;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        float s;
-        if constexpr (X86) {
-            float u[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) u[jj] = acc[4 * r + jj] + __shfl_xor(acc[4 * r + jj], 32);   // acc_jj + acc_(jj+4)
-            s = (u[0] + u[2]) + (u[1] + u[3]);
-        } else {
-            s = acc[r];
-        }
-        const int row = row0 + r;
-        if (h == 0 && tok_ok && row < J.r1) stg<float>(J.y + (size_t)t * J.ystride + row, s);
+    switch (R) {
+    case 1: run(std::integral_constant<int, 1>{}); break;
+    case 2: run(std::integral_constant<int, 2>{}); break;
+    case 3: run(std::integral_constant<int, 3>{}); break;
+    default: run(std::integral_constant<int, 4>{}); break;
     }
 }
 
 template <int F, int NBKM>
 void launch_nbk(bool x86, bool gather, const MkJob *jobs, int njobs, const MkJob &single, int grid, hipStream_t s) {
     constexpr int P = 8;
-    const dim3 g(grid), b(256);
+    const dim3 g(grid), b(64 * MBX_WAVES);
     if (x86) {
         if (gather) hipLaunchKernelGGL((mbx_kernel<F, NBKM, P, true, true>), g, b, 0, s, jobs, njobs, single);
         else hipLaunchKernelGGL((mbx_kernel<F, NBKM, P, true, false>), g, b, 0, s, jobs, njobs, single);

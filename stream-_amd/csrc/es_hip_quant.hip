@@ -608,6 +608,25 @@ const Prep &get_prep(Batch &bt, const Req &q, const FmtInfo &f, int kind, int na
     return bt.preps.back();
 }
 
+// Rows per workgroup tile of a batched 32-wide launch (es_hip_mbx.hip): the kernel is VALU-bound per SIMD, so the
+// launch's row x activation-tile units are spread over about one workgroup per CU, each job taking its share of the
+// workgroups; a tile holds 8 .. MBX_ROWS rows (one to four per wave). Then the tile numbering (with several activation
+// tiles, a job's tiles start at a multiple of 8 so that a row tile's activation tiles share an XCD).
+void mbx_tiles(MkGroup &g, int cus) {
+    double units = 0;
+    for (const esq::MkJob &j : g.jobs) units += (double)(j.r1 - j.r0) * j.ntok_tiles;
+    g.grid = 0;
+    for (esq::MkJob &j : g.jobs) {
+        const int rows = j.r1 - j.r0;
+        const int wg = std::max(1, (int)((double)cus * rows * j.ntok_tiles / units));
+        const int rt = std::max(1, wg / j.ntok_tiles);
+        j.rows_per_wg = std::min(esq::MBX_ROWS, std::max(esq::MBX_WAVES, (rows + rt - 1) / rt));
+        j.tile0 = g.grid;
+        const int row_tiles = (rows + j.rows_per_wg - 1) / j.rows_per_wg;
+        g.grid += j.ntok_tiles == 1 ? row_tiles : 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
+    }
+}
+
 int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
     bt = Batch();
     std::vector<Req> mv;
@@ -623,7 +642,8 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
             const size_t astride = q.astride ? q.astride : (size_t)nbk32 * f.ab;
             if (mfma && g_mbx_on.load() && esq::mbx_nbk_max(nbk32) && (!q.arow || q.act_rows > 0) &&
                 arows * astride < ((size_t)1 << 32) - 65536) {
-                // the matrix-core kernel reading the Q8_0 rows: MBX_ROWS x MBX_TOK tiles, no pre-pass
+                // the matrix-core kernel reading the Q8_0 rows: rows_per_wg x MBX_TOK tiles, no pre-pass (tiles numbered
+                // once the launch's jobs are known, mbx_tiles)
                 const int nbkm = esq::mbx_nbk_max(nbk32);
                 MkGroup *g = nullptr;
                 for (MkGroup &x : bt.mkg)
@@ -645,10 +665,7 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
                 j.r1 = q.r1;
                 j.cols = q.cols;
                 j.na = q.na;
-                j.tile0 = g->grid;
                 j.ntok_tiles = (q.na + esq::MBX_TOK - 1) / esq::MBX_TOK;
-                const int row_tiles = (q.r1 - q.r0 + esq::MBX_ROWS - 1) / esq::MBX_ROWS;
-                g->grid += j.ntok_tiles == 1 ? row_tiles : 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
                 g->jobs.push_back(j);
                 continue;
             }
@@ -818,6 +835,8 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
         g->grid += 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
         g->jobs.push_back(j);
     }
+    for (MkGroup &g : bt.mkg)
+        if (g.b32) mbx_tiles(g, device().cus);
     for (PkGroup &g : bt.pkg)
         if (!pk_schedule(g, device().cus)) return plan_batch(reqs, bt, false);   // too many tiles for one launch
     // a pre-pass numbers its 16-byte items with 32-bit indices

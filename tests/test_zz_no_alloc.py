@@ -80,19 +80,20 @@ def test_noalloc_back_to_back_on_one_stream(hip, orc):
 
 
 def test_noalloc_refuses_more_than_the_scratch(hip):
-    """64 rows x 8192 columns against 8192 activations: the pre-pass planes alone (8192 x 32 superblocks x ~292 bytes)
-    exceed the scratch; the call fails with EINVAL before launching anything"""
+    """Q6_K, 64 rows x 8192 columns against 8192 activations (the pre-pass matrix-core kernel): the pre-pass planes alone
+    (8192 x 32 superblocks x ~292 bytes) exceed the scratch; the call fails with EINVAL before launching anything. (A Q4_K
+    product of that shape runs on the direct kernel, whose tile tables fit.)"""
     rows, cols, na = 64, 8192, 8192
     nbk = cols // 256
     assert na * nbk * 292 > E.NOALLOC_SCRATCH_BYTES
-    dW = hip.alloc(rows * nbk * 144)
+    dW = hip.alloc(rows * nbk * 210)
     dA = hip.alloc(na * nbk * 292)
-    hip.memset(dW, 0, rows * nbk * 144)
+    hip.memset(dW, 0, rows * nbk * 210)
     hip.memset(dA, 0, na * nbk * 292)
     dY = hip.alloc(na * rows * 4)
     hip.memset(dY, 0x7f, na * rows * 4)
     with pytest.raises(E.EsHipError) as ei:
-        hip.matvec_multi_dev_noalloc(O.Q4_K, dW, cols, 0, rows, dA, nbk * 292, na, dY, rows)
+        hip.matvec_multi_dev_noalloc(O.Q6_K, dW, cols, 0, rows, dA, nbk * 292, na, dY, rows)
     assert "no-allocation scratch" in str(ei.value) or "no-allocation scratch" in hip.last_error()
     hip.synchronize()
     y = hip.download(dY, np.zeros(na * rows, np.uint32))
