@@ -110,6 +110,15 @@ int es_hip_matvec_multi_dev(uint32_t type, const void *W, int cols, int r0, int 
 int es_hip_matvec_multi_dev_noalloc(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride,
                                     int na, float *y, size_t ystride, void *stream);
 
+/* The float path of es_matvec (src/es_quant.c:1941-1944) on device memory: an activation prepared without blocks
+ * (es_act_prepare without a Q8_K buffer, with its Q8_0 arena exhausted, or under ES_FLOAT_ACT; src/es_quant.c:499-512) is
+ * multiplied by dequantizing each weight row (es_dequant_row) and taking dot_f32 against its floats (src/es_quant.c:514-526:
+ * four running sums over i mod 4, products and sums rounded separately, then (s0 + s1) + (s2 + s3)). x: na activations of
+ * cols floats, activation q at x + q * xstride floats (0: cols); y as es_hip_matvec_multi_dev. W at 2-byte alignment, x and
+ * y at 4. The same floats as the reference's in every build (dot_f32 has no FMA target on x86). No row length limit. */
+int es_hip_matvec_float_dev(uint32_t type, const void *W, int cols, int r0, int r1, const float *x, size_t xstride, int na,
+                            float *y, size_t ystride, void *stream);
+
 /* One queued product: the reference engine's mv_job (src/es_engine.c:144) with device pointers. rows are [0, rows). */
 typedef struct {
     uint32_t type;
@@ -139,10 +148,11 @@ void         es_hip_plan_destroy(es_hip_plan *plan);
 int es_hip_register(const void *host, size_t bytes);
 int es_hip_update(const void *host);
 int es_hip_unregister(const void *host);
-/* es_matvec / es_matvec_multi (src/es_quant.h:44-47): host W, host activations (a->q80 for Q4_0/Q5_0/Q8_0, a->q8 for the K-quants),
- * host y. Synchronous. The scratch argument is unused (kept for the prototype). They clear es_hip_last_error() on entry;
- * on failure y is left untouched and es_hip_last_error() says why (the reference's void prototype has no other error
- * channel). Row length limit (every product entry point): at most ES_HIP_MAX_COLS_32 columns for the 32-element formats
+/* es_matvec / es_matvec_multi (src/es_quant.h:44-47): host W, host activations (a->q80 for Q4_0/Q5_0/Q8_0, a->q8 for the
+ * K-quants; an activation without them takes the float path from a->x, as in the reference), host y. Synchronous. The
+ * scratch argument is unused (kept for the prototype). They clear es_hip_last_error() on entry; on failure y is left
+ * untouched and es_hip_last_error() says why (the reference's void prototype has no other error channel). Row length
+ * limit (every product entry point but the float path's): at most ES_HIP_MAX_COLS_32 columns for the 32-element formats
  * (Q4_0, Q5_0, Q8_0) and ES_HIP_MAX_COLS_256 for the K-quants (one row's float terms stay in a workgroup's LDS in the decode
  * kernel); a longer row is refused with ES_HIP_EINVAL, where the reference takes any multiple of the block size. */
 #define ES_HIP_MAX_COLS_32 131072
@@ -168,7 +178,8 @@ typedef struct {
     size_t ys;
 } es_hip_host_job;
 /* run_jobs (src/es_engine.c:177-186) for a queue on host memory: activations go up in one copy, every job runs in one
- * launch per format, outputs come back in one copy. Synchronous, like the reference's. Returns 0 or ES_HIP_E*. */
+ * launch per format (activations without blocks in the float path's launch, from a->x), outputs come back in one copy.
+ * Synchronous, like the reference's. Returns 0 or ES_HIP_E*. */
 int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs);
 
 /* ---- dense FFN: dense_n (src/es_engine.c:957-972) ------------------------------------------------------------------- */

@@ -378,6 +378,30 @@ void esq_matvec_multi(uint32_t t, const void *W, int cols, int r0, int r1, const
         esq_matvec(t, W, cols, r0, r1, (const uint8_t *)act + (size_t)q * astride, y + (size_t)q * ystride, order, path);
 }
 
+/* The float path (src/es_quant.c:1941-1944): an activation prepared without its blocks (es_act_prepare with no Q8_K
+ * buffer, an exhausted Q8_0 arena, or ES_FLOAT_ACT; src/es_quant.c:499-512) is multiplied by dequantizing each row and
+ * taking dot_f32 (src/es_quant.c:514-526): four running sums over the elements i = 0, 1, 2, 3 (mod 4), each product and
+ * sum rounded on its own (the function has no FMA target on x86, so no build contracts it), then (s0 + s1) + (s2 + s3). */
+static float dot_f32_4(const float *a, const float *b, int n) {
+    float s[4] = {0, 0, 0, 0};
+    int i = 0;
+    for (; i + 4 <= n; i += 4)
+        for (int j = 0; j < 4; j++) s[j] += a[i + j] * b[i + j];
+    for (; i < n; i++) s[0] += a[i] * b[i];
+    return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+void esq_matvec_float(uint32_t t, const void *W, int cols, int r0, int r1, const float *x, float *y) {
+    const size_t rb = esq_row_bytes(t, cols);
+    float *row = (float *)malloc(sizeof(float) * (size_t)cols);
+    if (!row) return;
+    for (int r = r0; r < r1; r++) {
+        esq_dequant_row(t, (const uint8_t *)W + rb * (size_t)r, row, cols);
+        y[r] = dot_f32_4(row, x, cols);
+    }
+    free(row);
+}
+
 void esq_block_ints(uint32_t t, const void *W, int cols, int rows, const void *act, int32_t *dots, int32_t *aux) {
     const int nb = cols / esq_block_elems(t);
     const size_t rb = esq_row_bytes(t, cols);

@@ -85,6 +85,9 @@ void esq_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const vo
 /* na activations, activation q at act + q*astride bytes, output y[q*ystride + r] (src/es_quant.c:1818-1850) */
 void esq_matvec_multi(uint32_t type, const void *W, int cols, int r0, int r1, const void *act, size_t astride, int na,
                       float *y, size_t ystride, int order, int path);
+/* the float path for activations without blocks: es_dequant_row + dot_f32 per row (src/es_quant.c:514-526, 1941-1944),
+ * y[r] for r in [r0, r1); x holds cols floats. The same in every build and path. */
+void esq_matvec_float(uint32_t type, const void *W, int cols, int r0, int r1, const float *x, float *y);
 /* integer parts of every (row, block): dots[r*nb + b] (Q4_0/Q5_0: sum of lanes), aux = mins/summs (0 otherwise) */
 void esq_block_ints(uint32_t type, const void *W, int cols, int rows, const void *act, int32_t *dots, int32_t *aux);
 

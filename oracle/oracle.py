@@ -63,6 +63,7 @@ class Oracle:
             "esq_matvec": (None, [u32, vp, i, i, i, vp, vp, i, i]),
             "esq_matvec_multi": (None, [u32, vp, i, i, i, vp, sz, i, vp, sz, i, i]),
             "esq_block_ints": (None, [u32, vp, i, i, vp, vp, vp]),
+            "esq_matvec_float": (None, [u32, vp, i, i, i, vp, vp]),
             "esq_dequant_row": (None, [u32, vp, vp, i]),
             "esq_quantize_q2_K_ref": (None, [vp, vp, i]),
             "esq_quantize_row": (None, [u32, vp, vp, i]),
@@ -123,6 +124,15 @@ class Oracle:
         na = acts.shape[0]
         y = np.zeros((na, rows), np.float32)
         self.lib.esq_matvec_multi(t, _p(W), cols, 0, rows, _p(acts), acts.strides[0], na, _p(y), rows, order, path)
+        return y
+
+    def matvec_float(self, t, W, cols, rows, x, r0=0):
+        """the float path (dequantized rows . fp32 activations): x [na, cols] -> y [na, rows], rows [r0, rows) written"""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+        y = np.zeros((x.shape[0], rows), np.float32)
+        for q in range(x.shape[0]):
+            self.lib.esq_matvec_float(t, _p(W), cols, r0, rows, C.c_void_p(x.ctypes.data + q * cols * 4),
+                                      C.c_void_p(y.ctypes.data + q * rows * 4))
         return y
 
     def block_ints(self, t, W, cols, rows, act):
@@ -481,6 +491,24 @@ class RefLib:
                 self.lib.es_matvec(t, _p(W), cols, r0, rows, C.byref(acts[q]), C.c_void_p(y.ctypes.data + q * rows * 4),
                                    _p(scratch))
         del keep
+        return y
+
+    def matvec_float(self, t, W, cols, rows, x: np.ndarray, r0=0, multi=False):
+        """x [na, cols] fp32 as activations prepared without blocks (es_act.q8 = q80 = NULL, what es_act_prepare leaves
+        under ES_FLOAT_ACT or an exhausted arena): es_matvec's float path, one call per activation or es_matvec_multi"""
+        x = np.ascontiguousarray(x, np.float32)
+        na = x.shape[0]
+        acts = (_EsAct * na)()
+        for q in range(na):
+            acts[q].x, acts[q].q8, acts[q].q80, acts[q].cols = x.ctypes.data + q * cols * 4, None, None, cols
+        y = np.zeros((na, rows), np.float32)
+        scratch = np.zeros(cols, np.float32)
+        if multi:
+            self.lib.es_matvec_multi(t, _p(W), cols, r0, rows, acts, na, _p(y), rows, _p(scratch))
+        else:
+            for q in range(na):
+                self.lib.es_matvec(t, _p(W), cols, r0, rows, C.byref(acts[q]), C.c_void_p(y.ctypes.data + q * rows * 4),
+                                   _p(scratch))
         return y
 
     def quantize_q8_K(self, x):

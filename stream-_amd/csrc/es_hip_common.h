@@ -201,6 +201,10 @@ hipError_t swiglu_plain_launch(const float *g, const float *u, float *h, long n,
 // kmax, the first k filled (k <= 64).
 constexpr int ROUTE_MAX_EXPERTS = 1024;
 hipError_t dequant_launch(uint32_t type, const void *src, float *dst, long n, hipStream_t s);
+// the float path: rows [r0, r1) of W (row stride rb bytes) against na fp32 activations (x + q * xstride floats), into
+// y + q * ystride; es_dequant_row + dot_f32 per output (src/es_quant.c:514-526, 1941-1944)
+hipError_t fdot_launch(uint32_t type, const void *W, size_t rb, int r0, int r1, int cols, const float *x, size_t xstride,
+                       int na, float *y, size_t ystride, hipStream_t s);
 hipError_t route_softmax_launch(const float *logits, uint64_t ls, int ntok, int ne, int k, int norm_topk, int *sel, float *w,
                                 int kmax, hipStream_t s);
 

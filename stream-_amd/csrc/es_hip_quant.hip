@@ -1388,6 +1388,33 @@ int es_hip_unregister(const void *host) {
     return ES_HIP_OK;
 }
 
+// The activation blocks the format takes (Q8_0 for the 32-element formats, Q8_K for the K-quants), or NULL when the
+// activation was prepared without them: es_act_prepare without a Q8_K buffer, with its Q8_0 arena exhausted, or under
+// ES_FLOAT_ACT (src/es_quant.c:499-512). Such an activation takes the reference's float path (src/es_quant.c:1941-1944).
+static const void *act_blocks(const FmtInfo &f, const es_hip_act &a) {
+    return f.be == 32 ? static_cast<const void *>(a.q80) : static_cast<const void *>(a.q8);
+}
+
+// Splits a host activation list into those with blocks (integer path) and those without (float path, which needs x).
+static int split_acts(const FmtInfo &f, const es_hip_act *a, int na, std::vector<int> &qi, std::vector<int> &qf, int job) {
+    qi.clear();
+    qf.clear();
+    for (int q = 0; q < na; q++) {
+        if (act_blocks(f, a[q])) qi.push_back(q);
+        else if (a[q].x) qf.push_back(q);
+        else if (job < 0) return fail(ES_HIP_EINVAL, "activation %d has neither %s blocks nor floats", q, f.be == 32 ? "Q8_0" : "Q8_K");
+        else return fail(ES_HIP_EINVAL, "job %d activation %d has neither %s blocks nor floats", job, q, f.be == 32 ? "Q8_0" : "Q8_K");
+    }
+    return ES_HIP_OK;
+}
+
+static int float_launch(uint32_t type, const void *dW, size_t rb, int rows, int cols, const float *x, int na, float *y,
+                        hipStream_t s) {
+    if (reinterpret_cast<uintptr_t>(dW) & 1) return fail(ES_HIP_EINVAL, "W must be 2-byte aligned");
+    hipError_t e = esq::fdot_launch(type, dW, rb, 0, rows, cols, x, (size_t)cols, na, y, (size_t)rows, s);
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "float-path launch");
+}
+
 static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, int na, float *y,
                       size_t ystride, int order = -1) {
     g_err.clear();   // the void drop-ins report failure only through es_hip_last_error()
@@ -1400,10 +1427,8 @@ static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, co
     const int nbk = cols / f.be;
     const size_t rb = (size_t)nbk * f.bb, ab = (size_t)nbk * f.ab;
     const int n = r1 - r0;
-    for (int q = 0; q < na; q++) {
-        const void *blk = f.be == 32 ? static_cast<const void *>(a[q].q80) : static_cast<const void *>(a[q].q8);
-        if (!blk) return fail(ES_HIP_EINVAL, "activation %d has no %s blocks (the reference's float fallback is not provided)", q, f.be == 32 ? "Q8_0" : "Q8_K");
-    }
+    std::vector<int> qi, qf;   // activations with blocks, then those on the float path; outputs in that order
+    if (int rc = split_acts(f, a, na, qi, qf, -1)) return rc;
     std::lock_guard<std::mutex> lk(g_call_mu);
     const uint8_t *wsub = static_cast<const uint8_t *>(W) + rb * r0;
     const void *dW = reg_lookup(wsub, rb * n);
@@ -1414,27 +1439,35 @@ static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, co
         if ((e = hipMemcpy(wt, wsub, rb * n, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "weight upload");
         dW = wt;
     }
-    if (int rc = g_atmp.get(ab * na, &at)) return rc;
-    std::vector<uint8_t> pack(ab * na);
-    for (int q = 0; q < na; q++) {
-        const void *blk = f.be == 32 ? static_cast<const void *>(a[q].q80) : static_cast<const void *>(a[q].q8);
-        memcpy(pack.data() + ab * q, blk, ab);
-    }
+    const size_t ibytes = align256(ab * qi.size()), xbytes = sizeof(float) * cols * qf.size();
+    if (int rc = g_atmp.get(ibytes + xbytes, &at)) return rc;
+    std::vector<uint8_t> pack(ibytes + xbytes);
+    for (size_t k = 0; k < qi.size(); k++) memcpy(pack.data() + ab * k, act_blocks(f, a[qi[k]]), ab);
+    for (size_t k = 0; k < qf.size(); k++) memcpy(pack.data() + ibytes + sizeof(float) * cols * k, a[qf[k]].x, sizeof(float) * cols);
     if ((e = hipMemcpy(at, pack.data(), pack.size(), hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
     if (int rc = g_ytmp.get(sizeof(float) * n * na, &yt)) return rc;
-    std::vector<Req> reqs{{type, dW, at, static_cast<float *>(yt), nullptr, nullptr, 0, n, cols, na, ab, (size_t)n}};
-    if (int rc = run_sync(reqs, nullptr, order)) return rc;
+    float *yd = static_cast<float *>(yt);
+    if (!qf.empty())
+        if (int rc = float_launch(type, dW, rb, n, cols, reinterpret_cast<const float *>(static_cast<uint8_t *>(at) + ibytes),
+                                  (int)qf.size(), yd + (size_t)n * qi.size(), nullptr))
+            return rc;
+    if (!qi.empty()) {
+        std::vector<Req> reqs{{type, dW, at, yd, nullptr, nullptr, 0, n, cols, (int)qi.size(), ab, (size_t)n}};
+        if (int rc = run_sync(reqs, nullptr, order)) return rc;
+    }
+    if ((e = hipStreamSynchronize(nullptr)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     std::vector<float> out((size_t)n * na);
     if ((e = hipMemcpy(out.data(), yt, out.size() * sizeof(float), hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
-    for (int q = 0; q < na; q++) memcpy(y + ystride * q + r0, out.data() + (size_t)n * q, sizeof(float) * n);
+    qi.insert(qi.end(), qf.begin(), qf.end());
+    for (int k = 0; k < na; k++) memcpy(y + ystride * qi[k] + r0, out.data() + (size_t)n * k, sizeof(float) * n);
     return ES_HIP_OK;
 }
 
 int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
     if (int rc = need_device()) return rc;
     if (njobs < 0 || (njobs > 0 && !jobs)) return fail(ES_HIP_EINVAL, "bad job list");
-    // sizes of the staged activations, outputs and unregistered weights
-    struct Stage { size_t aoff, yoff, woff; const void *dW; size_t ab, rb; };
+    // sizes of the staged activations (blocks, then the float-path activations' floats), outputs and unregistered weights
+    struct Stage { size_t aoff, xoff, yoff, woff; const void *dW; size_t ab, rb; std::vector<int> qi, qf; };
     std::vector<Stage> st(njobs);
     size_t abytes = 0, ybytes = 0, wbytes = 0;
     for (int i = 0; i < njobs; i++) {
@@ -1447,16 +1480,15 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
         const int nbk = j.cols / f.be;
         st[i].ab = (size_t)nbk * f.ab;
         st[i].rb = (size_t)nbk * f.bb;
-        for (int q = 0; q < j.nb; q++) {
-            const void *blk = f.be == 32 ? static_cast<const void *>(j.a[q].q80) : static_cast<const void *>(j.a[q].q8);
-            if (!blk) return fail(ES_HIP_EINVAL, "job %d activation %d has no %s blocks", i, q, f.be == 32 ? "Q8_0" : "Q8_K");
-        }
+        if (int rc = split_acts(f, j.a, j.nb, st[i].qi, st[i].qf, i)) return rc;
         st[i].aoff = abytes;
-        abytes += (st[i].ab * j.nb + 255) / 256 * 256;
+        abytes += align256(st[i].ab * st[i].qi.size());
+        st[i].xoff = abytes;
+        abytes += align256(sizeof(float) * j.cols * st[i].qf.size());
         st[i].yoff = ybytes;
-        ybytes += ((size_t)j.rows * j.nb * sizeof(float) + 255) / 256 * 256;
+        ybytes += align256((size_t)j.rows * j.nb * sizeof(float));
         st[i].dW = reg_lookup(j.w, st[i].rb * j.rows);
-        if (!st[i].dW) { st[i].woff = wbytes; wbytes += (st[i].rb * j.rows + 255) / 256 * 256; }
+        if (!st[i].dW) { st[i].woff = wbytes; wbytes += align256(st[i].rb * j.rows); }
     }
     std::lock_guard<std::mutex> lk(g_call_mu);
     void *at = nullptr, *yt = nullptr, *wt = nullptr;
@@ -1474,29 +1506,44 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
         if (j.rows == 0 || j.nb == 0) continue;
         FmtInfo f;
         fmt_info(j.type, f);
-        for (int q = 0; q < j.nb; q++) {
-            const void *blk = f.be == 32 ? static_cast<const void *>(j.a[q].q80) : static_cast<const void *>(j.a[q].q8);
-            memcpy(pack.data() + st[i].aoff + st[i].ab * q, blk, st[i].ab);
-        }
-        const void *dW = st[i].dW;
+        const Stage &g = st[i];
+        for (size_t k = 0; k < g.qi.size(); k++) memcpy(pack.data() + g.aoff + g.ab * k, act_blocks(f, j.a[g.qi[k]]), g.ab);
+        for (size_t k = 0; k < g.qf.size(); k++)
+            memcpy(pack.data() + g.xoff + sizeof(float) * j.cols * k, j.a[g.qf[k]].x, sizeof(float) * j.cols);
+        const void *dW = g.dW;
         if (!dW) {
-            dW = static_cast<uint8_t *>(wt) + st[i].woff;
-            if ((e = hipMemcpy(const_cast<void *>(dW), j.w, st[i].rb * j.rows, hipMemcpyHostToDevice)) != hipSuccess)
+            dW = static_cast<uint8_t *>(wt) + g.woff;
+            if ((e = hipMemcpy(const_cast<void *>(dW), j.w, g.rb * j.rows, hipMemcpyHostToDevice)) != hipSuccess)
                 return hip_fail(e, "weight upload");
         }
-        reqs.push_back({j.type, dW, static_cast<uint8_t *>(at) + st[i].aoff,
-                        reinterpret_cast<float *>(static_cast<uint8_t *>(yt) + st[i].yoff), nullptr, nullptr, 0, j.rows, j.cols,
-                        j.nb, st[i].ab, (size_t)j.rows});
+        float *yd = reinterpret_cast<float *>(static_cast<uint8_t *>(yt) + g.yoff);
+        if (!g.qi.empty())
+            reqs.push_back({j.type, dW, static_cast<uint8_t *>(at) + g.aoff, yd, nullptr, nullptr, 0, j.rows, j.cols,
+                            (int)g.qi.size(), g.ab, (size_t)j.rows});
     }
     if (abytes && (e = hipMemcpy(at, pack.data(), abytes, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
+    for (int i = 0; i < njobs; i++) {   // the float-path activations, stream-ordered before the batch's launches
+        const es_hip_host_job &j = jobs[i];
+        const Stage &g = st[i];
+        if (j.rows == 0 || j.nb == 0 || g.qf.empty()) continue;
+        const void *dW = g.dW ? g.dW : static_cast<uint8_t *>(wt) + g.woff;
+        float *yd = reinterpret_cast<float *>(static_cast<uint8_t *>(yt) + g.yoff) + (size_t)j.rows * g.qi.size();
+        if (int rc = float_launch(j.type, dW, g.rb, j.rows, j.cols,
+                                  reinterpret_cast<const float *>(static_cast<uint8_t *>(at) + g.xoff), (int)g.qf.size(), yd,
+                                  nullptr))
+            return rc;
+    }
     if (int rc = run_sync(reqs, nullptr)) return rc;
+    if ((e = hipStreamSynchronize(nullptr)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     std::vector<uint8_t> out(ybytes);
     if (ybytes && (e = hipMemcpy(out.data(), yt, ybytes, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
     for (int i = 0; i < njobs; i++) {
         const es_hip_host_job &j = jobs[i];
         if (j.rows == 0 || j.nb == 0) continue;
         const float *src = reinterpret_cast<const float *>(out.data() + st[i].yoff);
-        for (int q = 0; q < j.nb; q++) memcpy(j.y + j.ys * q, src + (size_t)j.rows * q, sizeof(float) * j.rows);
+        int k = 0;
+        for (int q : st[i].qi) memcpy(j.y + j.ys * q, src + (size_t)j.rows * k++, sizeof(float) * j.rows);
+        for (int q : st[i].qf) memcpy(j.y + j.ys * q, src + (size_t)j.rows * k++, sizeof(float) * j.rows);
     }
     return ES_HIP_OK;
 }
@@ -2243,6 +2290,26 @@ int es_hip_dequant_row_dev(uint32_t type, const void *src, float *dst, long n, v
     if (reinterpret_cast<uintptr_t>(dst) & 3) return fail(ES_HIP_EINVAL, "dst must be 4-byte aligned");
     hipError_t e = esq::dequant_launch(type, src, dst, n, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "dequant launch");
+}
+
+int es_hip_matvec_float_dev(uint32_t type, const void *W, int cols, int r0, int r1, const float *x, size_t xstride, int na,
+                            float *y, size_t ystride, void *stream) {
+    if (int rc = need_device()) return rc;
+    FmtInfo f;
+    if (!fmt_info(type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", type);
+    if (cols <= 0 || cols % f.be) return fail(ES_HIP_EINVAL, "type %u: cols %d is not a positive multiple of %d", type, cols, f.be);
+    if (r0 < 0 || r1 < r0 || na < 0) return fail(ES_HIP_EINVAL, "bad row range [%d, %d) or activation count %d", r0, r1, na);
+    if (r1 == r0 || na == 0) return ES_HIP_OK;
+    if (!W || !x || !y) return fail(ES_HIP_EINVAL, "null W, x or y");
+    if (reinterpret_cast<uintptr_t>(W) & 1) return fail(ES_HIP_EINVAL, "W must be 2-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 3) return fail(ES_HIP_EINVAL, "x and y must be 4-byte aligned");
+    if (!xstride) xstride = (size_t)cols;
+    if (na > 1 && xstride < (size_t)cols) return fail(ES_HIP_EINVAL, "x stride %zu < cols %d", xstride, cols);
+    if (na > 1 && ystride < (size_t)r1) return fail(ES_HIP_EINVAL, "ystride %zu < r1 %d: outputs of activations overlap", ystride, r1);
+    if (na > 65535 * 8) return fail(ES_HIP_EINVAL, "%d activations in one call (at most %d)", na, 65535 * 8);
+    const size_t rb = (size_t)(cols / f.be) * f.bb;
+    hipError_t e = esq::fdot_launch(type, W, rb, r0, r1, cols, x, xstride, na, y, ystride, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "float-path launch");
 }
 
 int es_hip_route_softmax_dev(const float *logits, size_t lstride, int ntok, int n_exp, int k, int norm_topk, int *sel, float *w,

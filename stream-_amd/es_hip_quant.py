@@ -51,13 +51,19 @@ class HostJob(C.Structure):   # es_hip_host_job (= the reference engine's mv_job
                 ("y", C.c_void_p), ("nb", C.c_int), ("ys", C.c_size_t)]
 
 
-def act_records(t: int, acts: np.ndarray, cols: int):
-    """es_act records pointing at the rows of `acts` [na, nblocks] (q8 for K-quants, q80 for Q4_0/Q5_0)"""
-    na = acts.shape[0]
+def act_records(t: int, acts, cols: int, x=None, floats=()):
+    """es_act records pointing at the rows of `acts` [na, nblocks] (q8 for K-quants, q80 for Q4_0/Q5_0/Q8_0) and of x
+    [na, cols] fp32 when given; the activations listed in `floats` (all of them when acts is None) carry no blocks, as
+    es_act_prepare leaves them without a Q8_K buffer or Q8_0 arena room, and take the float path"""
+    na = acts.shape[0] if acts is not None else x.shape[0]
     recs = (Act * max(na, 1))()
     for q in range(na):
+        px = x.ctypes.data + q * x.strides[0] if x is not None else None
+        if acts is None or q in floats:
+            recs[q] = Act(px, None, None, cols)
+            continue
         p = acts.ctypes.data + q * acts.strides[0]
-        recs[q] = Act(None, p if BLOCK_ELEMS[t] == 256 else None, p if BLOCK_ELEMS[t] == 32 else None, cols)
+        recs[q] = Act(px, p if BLOCK_ELEMS[t] == 256 else None, p if BLOCK_ELEMS[t] == 32 else None, cols)
     return recs
 
 
@@ -250,6 +256,7 @@ class Lib:
             ("es_hip_act_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp]),
             ("es_hip_route_softmax_dev", i, [vp, sz, i, i, i, i, vp, vp, i, vp]),
             ("es_hip_dequant_row_dev", i, [u32, vp, vp, C.c_long, vp]),
+            ("es_hip_matvec_float_dev", i, [u32, vp, i, i, i, vp, sz, i, vp, sz, vp]),
             ("es_hip_rmsnorm_prepare_dev", i, [vp, sz, vp, C.c_float, i, i, vp, sz, vp, sz, vp, sz, vp]),
             ("es_hip_swiglu_prepare_dev", i, [vp, sz, i, i, vp, sz, vp, sz, vp, sz, vp]),
             ("es_hip_cache_create", i, [vp, i, sz, i, i, C.c_double]), ("es_hip_cache_destroy", None, [vp]),
@@ -457,6 +464,9 @@ class Lib:
     def dequant_row_dev(self, t, src, dst, n, stream=None):
         self._check(self._L.es_hip_dequant_row_dev(t, int(src), int(dst), n, stream))
 
+    def matvec_float_dev(self, t, W, cols, r0, r1, x, xstride, na, y, ystride, stream=None):
+        self._check(self._L.es_hip_matvec_float_dev(t, int(W), cols, r0, r1, int(x), xstride, na, int(y), ystride, stream))
+
     def route_softmax_dev(self, logits, lstride, ntok, n_exp, k, norm_topk, sel, w, kmax, stream=None):
         self._check(self._L.es_hip_route_softmax_dev(int(logits), lstride, ntok, n_exp, k, int(norm_topk), int(sel), int(w),
                                                      kmax, stream))
@@ -515,11 +525,13 @@ class Lib:
     def unregister(self, W: np.ndarray):
         return self._L.es_hip_unregister(W.ctypes.data)
 
-    def host_matvec_multi(self, t, W: np.ndarray, cols: int, r0: int, r1: int, acts: np.ndarray, y: np.ndarray):
-        """es_hip_matvec_multi with es_act records pointing at `acts` [na, nblocks]; y [na, ystride] updated in place"""
-        acts = np.ascontiguousarray(acts)
-        na = acts.shape[0]
-        recs = act_records(t, acts, cols)
+    def host_matvec_multi(self, t, W: np.ndarray, cols: int, r0: int, r1: int, acts, y: np.ndarray, x=None, floats=()):
+        """es_hip_matvec_multi with es_act records pointing at `acts` [na, nblocks] (and at x [na, cols] fp32, if given);
+        the activations in `floats` (all when acts is None) carry no blocks; y [na, ystride] updated in place"""
+        acts = None if acts is None else np.ascontiguousarray(acts)
+        x = None if x is None else np.ascontiguousarray(x, np.float32)
+        recs = act_records(t, acts, cols, x, floats)
+        na = acts.shape[0] if acts is not None else x.shape[0]
         if na == 1:
             self._L.es_hip_matvec(t, W.ctypes.data, cols, r0, r1, recs, y.ctypes.data, None)
         else:
@@ -529,17 +541,20 @@ class Lib:
             raise EsHipError(-1, err)
         return y
 
-
     def run_jobs_host(self, jobs):
-        """jobs: list of (type, W host uint8, rows, cols, acts [nb, nblocks], y [nb, ys] float32 written in place)"""
+        """jobs: list of (type, W host uint8, rows, cols, acts [nb, nblocks], y [nb, ys] float32 written in place), each
+        optionally extended by (x [nb, cols] fp32, floats): the activations listed in floats carry no blocks (float path)"""
         arr = (HostJob * max(len(jobs), 1))()
         keep = []
-        for k, (t, W, rows, cols, acts, y) in enumerate(jobs):
-            acts = np.ascontiguousarray(acts)
-            recs = act_records(t, acts, cols)
-            keep += [acts, recs]
-            arr[k] = HostJob(t, W.ctypes.data, rows, cols, C.cast(recs, C.c_void_p), y.ctypes.data, acts.shape[0],
-                             y.strides[0] // 4)
+        for k, job in enumerate(jobs):
+            t, W, rows, cols, acts, y = job[:6]
+            x, floats = (job[6], job[7]) if len(job) > 6 else (None, ())
+            acts = None if acts is None else np.ascontiguousarray(acts)
+            x = None if x is None else np.ascontiguousarray(x, np.float32)
+            recs = act_records(t, acts, cols, x, floats)
+            keep += [acts, x, recs]
+            nb = acts.shape[0] if acts is not None else x.shape[0]
+            arr[k] = HostJob(t, W.ctypes.data, rows, cols, C.cast(recs, C.c_void_p), y.ctypes.data, nb, y.strides[0] // 4)
         self._check(self._L.es_hip_run_jobs_host(arr, len(jobs)))
         del keep
 

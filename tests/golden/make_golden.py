@@ -12,6 +12,8 @@ the generated inputs are stored, so the fixture does not depend on the generator
     F/{case}_y_{gcc,clang}     es_matvec over rows [3, rows) on the x86 AVX2 path, per compiler
     F/{case}_y_scalar          the same with ES_NO_AVX2=1 (scalar mv_* kernels)
     F/{case}_ymulti_clang      es_matvec_multi (bit-identical to single in the reference: es_mtest's invariant)
+    F/{case}_yfloat            es_matvec over rows [3, rows) with activations prepared without blocks (q8 = q80 = NULL):
+                               es_dequant_row + dot_f32; checked equal across gcc, clang, scalar and es_matvec_multi
     F/dequant                  es_dequant_row of the first gauss row
 plus Q2_K quantizer bytes (es_quantize_q2_K_ref), Q8_K quantizer edge cases, es_fp32_to_fp16 on edge floats and
 es_dot_q2_K_q8_K_ref values (the kbench correctness test, tools/es_kbench.c:154-192, at 8 rows).
@@ -66,6 +68,13 @@ def main():
             for cc, lib in R.items():
                 out[f"{F}/{name}_y_{cc}"] = lib.matvec_f32(t, W, cols, rows, x, r0=3)
             out[f"{F}/{name}_ymulti_clang"] = R["clang"].matvec_f32(t, W, cols, rows, x, r0=3, multi=True)
+            # the float path (activations without blocks): the same in every build, single and multi
+            yf = R["clang"].matvec_float(t, W, cols, rows, x, r0=3)
+            for cc, lib in R.items():
+                assert np.array_equal(yf.view(np.uint32), lib.matvec_float(t, W, cols, rows, x, r0=3).view(np.uint32))
+            assert np.array_equal(yf.view(np.uint32), R["clang"].matvec_float(t, W, cols, rows, x, r0=3, multi=True)
+                                  .view(np.uint32))
+            out[f"{F}/{name}_yfloat"] = yf
         Wg, _, cols, _ = cases["gauss"]
         out[f"{F}/dequant"] = R["gcc"].dequant(t, Wg[: O.row_bytes(t, cols)], cols)
 

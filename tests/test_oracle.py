@@ -231,6 +231,69 @@ def test_cpu_bench_harness_runs(orc):
     assert np.array_equal(y, orc.matvec_multi(t, W, cols, rows, acts))
 
 
+@pytest.mark.parametrize("F", FMTS)
+@pytest.mark.parametrize("case", CASES)
+def test_float_path_vs_reference(orc, golden, F, case):
+    """activations prepared without blocks: es_dequant_row + dot_f32 per row, as the reference computed it (the fixture
+    was checked equal across its gcc, clang and scalar builds and es_matvec_multi when it was written)"""
+    t = O.TYPES[F]
+    cols, rows = (int(v) for v in golden[f"{F}/{case}_shape"])
+    y = orc.matvec_float(t, golden[f"{F}/{case}_W"], cols, rows, golden[f"{F}/{case}_x"], r0=3)
+    assert np.array_equal(_bits(y), _bits(golden[f"{F}/{case}_yfloat"]))
+
+
+def _chain_variants(w, x):
+    """dot products of rows w [rows, n] with x [n] summed three wrong ways: one running sum; four running sums added
+    left to right; four running sums with each product fused into its sum (rounded once, through float64)"""
+    one = np.zeros(w.shape[0], np.float32)
+    four = np.zeros((4, w.shape[0]), np.float32)
+    fused = np.zeros((4, w.shape[0]), np.float32)
+    for i in range(w.shape[1]):
+        p = w[:, i] * x[i]
+        one = (one + p).astype(np.float32)
+        four[i % 4] = (four[i % 4] + p).astype(np.float32)
+        fused[i % 4] = (fused[i % 4].astype(np.float64) + w[:, i].astype(np.float64) * np.float64(x[i])).astype(np.float32)
+    left = (((four[0] + four[1]) + four[2]) + four[3]).astype(np.float32)
+    return one, left, ((fused[0] + fused[1]) + (fused[2] + fused[3])).astype(np.float32)
+
+
+@pytest.mark.parametrize("F", ["Q4_K", "Q8_0", "Q6_K"])
+def test_float_path_fixture_pins_the_summation_order(orc, golden, F):
+    """the fixture rejects the plausible mistakes in dot_f32's order: each wrong summation differs from it somewhere"""
+    t = O.TYPES[F]
+    cols, rows = (int(v) for v in golden[f"{F}/gauss_shape"])
+    W, x = golden[f"{F}/gauss_W"], golden[f"{F}/gauss_x"]
+    w = np.stack([orc.dequant(t, W[r * O.row_bytes(t, cols):(r + 1) * O.row_bytes(t, cols)], cols) for r in range(rows)])
+    ref = golden[f"{F}/gauss_yfloat"]
+    for q in range(x.shape[0]):
+        for wrong in _chain_variants(w, x[q]):
+            assert not np.array_equal(_bits(wrong[3:]), _bits(ref[q, 3:]))
+
+
+@pytest.mark.parametrize("F", ["Q8_0", "Q4_0", "Q4_K"])
+def test_float_path_exact_integers(orc, F):
+    """weights and activations that are small integers (block scales 1.0, integer mins) make every product and partial sum
+    exact, so the float path must equal the int64 dot of the dequantized integers"""
+    t = O.TYPES[F]
+    rows, cols = 9, 1024
+    rng = np.random.default_rng(5)
+    bb, be = O.BLOCK_BYTES[t], O.BLOCK_ELEMS[t]
+    W = rng.integers(0, 256, rows * cols // be * bb, dtype=np.uint8).reshape(rows, cols // be, bb)
+    if F in ("Q8_0", "Q4_0"):
+        W[:, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)   # d = 1.0
+    else:   # Q4_K: d = 1.0, dmin = 1.0; 6-bit scales and mins are small integers already
+        W[:, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+        W[:, :, 2:4] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    W = W.reshape(-1)
+    x = rng.integers(-6, 7, (2, cols)).astype(np.float32)
+    rb = O.row_bytes(t, cols)
+    wi = np.stack([orc.dequant(t, W[r * rb:(r + 1) * rb], cols) for r in range(rows)]).astype(np.int64)
+    assert np.array_equal(wi.astype(np.float32), np.stack([orc.dequant(t, W[r * rb:(r + 1) * rb], cols) for r in range(rows)]))
+    exact = x.astype(np.int64) @ wi.T
+    assert np.abs(exact).max() < 1 << 24
+    assert np.array_equal(orc.matvec_float(t, W, cols, rows, x), exact.astype(np.float32))
+
+
 @pytest.mark.skipif(not O.ref_available("clang"), reason="reference not built here (no /root/reference)")
 def test_live_reference_wide_shapes(orc):
     """the live reference build on the benchmark configurations' column counts, many rows, contract and strict orders"""
@@ -245,6 +308,9 @@ def test_live_reference_wide_shapes(orc):
             R = O.RefLib(cc)
             ref = R.matvec_f32(t, W, cols, rows, x, multi=True)
             assert np.array_equal(_bits(orc.matvec_multi(t, W, cols, rows, acts, order)), _bits(ref)), (F, cols, cc)
+            # the float path (activations prepared without blocks)
+            assert np.array_equal(_bits(orc.matvec_float(t, W, cols, rows, x)),
+                                  _bits(R.matvec_float(t, W, cols, rows, x, multi=True))), (F, cols, cc)
 
 
 @pytest.mark.skipif(not O.ref_available("clang"), reason="reference not built here (no /root/reference)")
