@@ -445,6 +445,44 @@ def dense_ffn_time(lib, rng, K, Wm, T=512, n=2048, ff=8192):
             "workload": f"dense_n T={T}: gate/up {ff}x{n} + SwiGLU/Q8_K + down {n}x{ff}, Q4_K, three dependent steps"}
 
 
+def host_queue_time(lib, rng, K, Wm, T):
+    """es_hip_run_jobs_host, the engine-facing binding (run_jobs over host buffers, src/es_engine.c:177-186), at config 2's
+    FFN shapes: the engine's two queues per layer around SwiGLU, gate + up (Q4_K 8192x2048) in one call and down (Q4_K
+    2048x8192) in a second, weights registered (resident in HBM, as es_hip_register keeps them), activation blocks and
+    outputs in host memory. Each call is synchronous: activations up, launches, outputs down. ms per layer by the wall
+    clock over K layers, and the PCIe bytes moved per layer (activation blocks up, fp32 outputs down)."""
+    t, n, ff = E.Q4_K, 2048, 8192
+    W = [random_blocks(t, ff, n, rng), random_blocks(t, ff, n, rng), random_blocks(t, n, ff, rng)]
+    for w in W:
+        lib.register(w)
+    x = quantize_acts(t, rng.standard_normal((T, n)).astype(np.float32))
+    h = quantize_acts(t, rng.standard_normal((T, ff)).astype(np.float32))
+    gu = np.zeros((T, 2 * ff), np.float32)
+    out = np.zeros((T, n), np.float32)
+    q1, k1 = lib.host_jobs([(t, W[0], ff, n, x, gu[:, :ff]), (t, W[1], ff, n, x, gu[:, ff:])])
+    q2, k2 = lib.host_jobs([(t, W[2], n, ff, h, out)])
+    run = lib._L.es_hip_run_jobs_host
+
+    def layer():
+        if run(q1, 2) or run(q2, 1):
+            raise RuntimeError("es_hip_run_jobs_host: " + lib.last_error())
+
+    for _ in range(Wm):
+        layer()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        layer()
+    dt = (time.perf_counter() - t0) / K
+    for w in W:
+        lib.unregister(w)
+    del k1, k2
+    pcie = x.nbytes + h.nbytes + gu.nbytes + out.nbytes
+    wbytes = sum(w.nbytes for w in W)
+    return {"ms_per_layer": round(dt * 1e3, 4), "pcie_bytes_per_layer": pcie,
+            "pcie_gbs": round(pcie / dt / 1e9, 2), "weight_gbs": round(wbytes / dt / 1e9, 1),
+            "workload": f"run_jobs_host T={T}: [gate, up] then [down], Q4_K, registered weights, host activations/outputs"}
+
+
 def only(lib, rng, name, K, Wm, moe_leg="both"):
     """one workload of the bench, alone: the command profiler summaries are taken from"""
     if name == "copy":   # a plain device copy of known size, the reference for HBM byte counters
@@ -461,6 +499,9 @@ def only(lib, rng, name, K, Wm, moe_leg="both"):
         return {"workload": "act", **act_prep_times(lib, rng, K, Wm)}
     if name == "dense":
         return {"workload": "dense", **dense_ffn_time(lib, rng, K, Wm)}
+    if name == "host_queue":
+        return {"workload": "host_queue", "t1": host_queue_time(lib, rng, K, Wm, 1),
+                "t512": host_queue_time(lib, rng, max(3, K // 4), Wm, 512)}
     if name == "cache":
         return {"workload": "cache", "pageable": cache_load_rate(lib, rng, K, Wm),
                 "pinned": cache_load_rate(lib, rng, K, Wm, pinned=True)}
@@ -500,7 +541,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=2.0)
     ap.add_argument("--only", choices=["decode", "prefill", "prefill_q5k", "prefill_q3k", "dense", "config1", "config3b1", "config3b64", "config4", "config5", "act",
-                                       "cache", "copy"] + [f"decode_{f.lower()}" for f in E.TYPES],
+                                       "cache", "copy", "host_queue"] + [f"decode_{f.lower()}" for f in E.TYPES],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     ap.add_argument("--moe-leg", choices=["both", "plan", "device"], default="both",
                     help="with --only config4/config5: time the prepared plan, the device-routed context, or both")
@@ -582,6 +623,9 @@ def main():
     extra["act_prep_t512"] = act_prep_times(lib, rng, K, Wm)
     extra["expert_cache_load"] = cache_load_rate(lib, rng, K, Wm)
     extra["expert_cache_load_pinned"] = cache_load_rate(lib, rng, K, Wm, pinned=True)
+    # ---- the engine-facing host binding (es_hip_run_jobs_host) at config 2 decode and prefill: PCIe-inclusive
+    extra["host_queue_t1"] = host_queue_time(lib, rng, K, Wm, 1)
+    extra["host_queue_t512"] = host_queue_time(lib, rng, max(3, K // 4), Wm, 512)
 
     cpu = None
     if not args.no_cpu:

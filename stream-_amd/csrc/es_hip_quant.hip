@@ -16,6 +16,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "es_hip_common.h"
@@ -998,6 +999,65 @@ struct Scratch {
 Scratch g_table, g_wtmp, g_atmp, g_ytmp;
 std::mutex g_call_mu;   // serialises the synchronous convenience entry points that share scratch
 
+// ---- page-locked host staging for the entry points on host memory ----------------------------------------------------
+// Activations are packed here before one copy up and outputs land here before they are spread to the caller's arrays:
+// copies from and to page-locked memory run at the link's rate, and the buffers persist, so a call neither allocates nor
+// faults in fresh pages. Used under g_call_mu.
+struct HostStage {
+    void *p = nullptr;
+    size_t n = 0;
+    int get(size_t bytes, void **out) {
+        if (bytes > n) {
+            if (p) (void)hipHostFree(p);
+            p = nullptr;
+            n = 0;
+            const size_t want = std::max(bytes, (size_t)1 << 20);
+            hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+            if (e != hipSuccess) return hip_fail(e, "hipHostMalloc staging");
+            n = want;
+        }
+        *out = p;
+        return ES_HIP_OK;
+    }
+};
+HostStage g_hin, g_hout;
+
+// The host-to-host copies of one call (packing activations, spreading outputs), over up to 8 threads when they add up to
+// more than 8 MB: a prefill-sized queue returns tens of MB of outputs, which one core copies at a fraction of the link's rate.
+struct HCopy {
+    void *dst;
+    const void *src;
+    size_t bytes;
+};
+void host_copies(const std::vector<HCopy> &v) {
+    size_t total = 0;
+    for (const HCopy &c : v) total += c.bytes;
+    const unsigned nt = std::min(8u, std::max(1u, std::thread::hardware_concurrency()));
+    auto run = [](const std::vector<HCopy> &w) { for (const HCopy &c : w) memcpy(c.dst, c.src, c.bytes); };
+    if (total < ((size_t)8 << 20) || nt == 1) return run(v);
+    const size_t piece = (total + nt - 1) / nt;   // each thread takes a contiguous share of about total / nt bytes
+    std::vector<std::vector<HCopy>> work(nt);
+    size_t acc = 0;
+    for (HCopy c : v)
+        while (c.bytes) {
+            const unsigned w = (unsigned)std::min<size_t>(acc / piece, nt - 1);
+            const size_t b = w == nt - 1 ? c.bytes : std::min(c.bytes, (w + 1) * piece - acc);
+            work[w].push_back({c.dst, c.src, b});
+            c.dst = static_cast<uint8_t *>(c.dst) + b;
+            c.src = static_cast<const uint8_t *>(c.src) + b;
+            c.bytes -= b;
+            acc += b;
+        }
+    std::vector<std::thread> th;
+    try {
+        for (unsigned w = 1; w < nt; w++) th.emplace_back(run, std::cref(work[w]));
+    } catch (...) {   // no thread to be had: the remaining shares run here
+        for (unsigned w = 1 + (unsigned)th.size(); w < nt; w++) run(work[w]);
+    }
+    run(work[0]);
+    for (std::thread &t : th) t.join();
+}
+
 // ---- weight registry ------------------------------------------------------------------------------------------------
 struct Reg {
     size_t bytes;
@@ -1017,24 +1077,55 @@ void *reg_lookup(const void *h, size_t n) {
     return static_cast<uint8_t *>(it->second.dev) + (a - it->first);
 }
 
-// Plan, upload the job tables (and bind the pre-pass workspace) in scratch, launch, wait: the synchronous path shared by
-// run_jobs, run_jobs_host and the host drop-ins. The caller holds g_call_mu.
-int run_sync(const std::vector<Req> &reqs, hipStream_t s, int order = -1) {   // order -1: es_hip_set_order's
+// Plan, upload the job tables (and bind the pre-pass workspace) in scratch, launch: the path shared by run_jobs,
+// run_jobs_host and the host drop-ins. The caller holds g_call_mu. The tables go up from page-locked staging, stream-ordered
+// behind the caller's earlier work on s; every call waits for its kernels before it returns (with sync here, or, for the
+// host entry points, after their output copy), so no earlier call's kernels still read the scratch. A call that failed
+// between its first copy or launch and that wait leaves g_table_pending set, and the next call first waits for the device.
+HostStage g_htab;
+bool g_table_pending = false;
+
+int settle() {   // before the staging or the scratch is reused: the wait a failed call skipped
+    if (!g_table_pending) return ES_HIP_OK;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+    g_table_pending = false;
+    return ES_HIP_OK;
+}
+
+int run_launch(const std::vector<Req> &reqs, hipStream_t s, int order) {   // order -1: es_hip_set_order's
     Batch bt;
     if (int rc = plan_batch(reqs, bt)) return rc;
     if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.pkg.empty()) return ES_HIP_OK;
-    hipError_t e = hipStreamSynchronize(s);   // the scratch may still be read by an earlier call's kernels
-    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    void *dev = nullptr;
+    hipError_t e;
+    if (int rc = settle()) return rc;
+    void *dev = nullptr, *htab = nullptr;
     const size_t ws_at = align256(bt.table_bytes);
     if (int rc = g_table.get(ws_at + bt.ws_bytes, &dev)) return rc;
     bind(bt, static_cast<uint8_t *>(dev) + ws_at);
     const std::vector<uint8_t> img = table_image(bt);
-    if (!img.empty() && (e = hipMemcpyAsync(dev, img.data(), img.size(), hipMemcpyHostToDevice, s)) != hipSuccess)
-        return hip_fail(e, "job table upload");
-    if (int rc = launch_batch(bt, static_cast<const uint8_t *>(dev), order >= 0 ? order : g_order.load(), s)) return rc;
-    e = hipStreamSynchronize(s);   // like the reference's run_jobs: every product is done on return
-    return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipStreamSynchronize");
+    if (!img.empty()) {
+        if (int rc = g_htab.get(img.size(), &htab)) return rc;
+        memcpy(htab, img.data(), img.size());
+        g_table_pending = true;
+        if ((e = hipMemcpyAsync(dev, htab, img.size(), hipMemcpyHostToDevice, s)) != hipSuccess) return hip_fail(e, "job table upload");
+    }
+    g_table_pending = true;
+    return launch_batch(bt, static_cast<const uint8_t *>(dev), order >= 0 ? order : g_order.load(), s);
+}
+
+// the caller's wait after run_launch (and whatever it queued behind it on s)
+int finish(hipStream_t s) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    g_table_pending = false;
+    return ES_HIP_OK;
+}
+
+// run_launch and wait: like the reference's run_jobs, every product is done on return
+int run_sync(const std::vector<Req> &reqs, hipStream_t s, int order = -1) {
+    if (int rc = run_launch(reqs, s, order)) return rc;
+    return finish(s);
 }
 
 }  // namespace
@@ -1430,6 +1521,7 @@ static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, co
     std::vector<int> qi, qf;   // activations with blocks, then those on the float path; outputs in that order
     if (int rc = split_acts(f, a, na, qi, qf, -1)) return rc;
     std::lock_guard<std::mutex> lk(g_call_mu);
+    if (int rc = settle()) return rc;
     const uint8_t *wsub = static_cast<const uint8_t *>(W) + rb * r0;
     const void *dW = reg_lookup(wsub, rb * n);
     void *wt = nullptr, *at = nullptr, *yt = nullptr;
@@ -1440,11 +1532,16 @@ static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, co
         dW = wt;
     }
     const size_t ibytes = align256(ab * qi.size()), xbytes = sizeof(float) * cols * qf.size();
+    void *hin = nullptr, *hout = nullptr;
     if (int rc = g_atmp.get(ibytes + xbytes, &at)) return rc;
-    std::vector<uint8_t> pack(ibytes + xbytes);
-    for (size_t k = 0; k < qi.size(); k++) memcpy(pack.data() + ab * k, act_blocks(f, a[qi[k]]), ab);
-    for (size_t k = 0; k < qf.size(); k++) memcpy(pack.data() + ibytes + sizeof(float) * cols * k, a[qf[k]].x, sizeof(float) * cols);
-    if ((e = hipMemcpy(at, pack.data(), pack.size(), hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
+    if (int rc = g_hin.get(ibytes + xbytes, &hin)) return rc;
+    std::vector<HCopy> cp;
+    uint8_t *pack = static_cast<uint8_t *>(hin);
+    for (size_t k = 0; k < qi.size(); k++) cp.push_back({pack + ab * k, act_blocks(f, a[qi[k]]), ab});
+    for (size_t k = 0; k < qf.size(); k++) cp.push_back({pack + ibytes + sizeof(float) * cols * k, a[qf[k]].x, sizeof(float) * cols});
+    host_copies(cp);
+    g_table_pending = true;
+    if ((e = hipMemcpyAsync(at, hin, ibytes + xbytes, hipMemcpyHostToDevice, nullptr)) != hipSuccess) return hip_fail(e, "activation upload");
     if (int rc = g_ytmp.get(sizeof(float) * n * na, &yt)) return rc;
     float *yd = static_cast<float *>(yt);
     if (!qf.empty())
@@ -1453,13 +1550,17 @@ static int host_multi(uint32_t type, const void *W, int cols, int r0, int r1, co
             return rc;
     if (!qi.empty()) {
         std::vector<Req> reqs{{type, dW, at, yd, nullptr, nullptr, 0, n, cols, (int)qi.size(), ab, (size_t)n}};
-        if (int rc = run_sync(reqs, nullptr, order)) return rc;
+        if (int rc = run_launch(reqs, nullptr, order)) return rc;
     }
-    if ((e = hipStreamSynchronize(nullptr)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    std::vector<float> out((size_t)n * na);
-    if ((e = hipMemcpy(out.data(), yt, out.size() * sizeof(float), hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
+    if (int rc = g_hout.get(sizeof(float) * n * na, &hout)) return rc;
+    if ((e = hipMemcpyAsync(hout, yt, sizeof(float) * n * na, hipMemcpyDeviceToHost, nullptr)) != hipSuccess)
+        return hip_fail(e, "output download");
+    if (int rc = finish(nullptr)) return rc;
     qi.insert(qi.end(), qf.begin(), qf.end());
-    for (int k = 0; k < na; k++) memcpy(y + ystride * qi[k] + r0, out.data() + (size_t)n * k, sizeof(float) * n);
+    const float *out = static_cast<const float *>(hout);
+    cp.clear();
+    for (int k = 0; k < na; k++) cp.push_back({y + ystride * qi[k] + r0, out + (size_t)n * k, sizeof(float) * n});
+    host_copies(cp);
     return ES_HIP_OK;
 }
 
@@ -1491,6 +1592,7 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
         if (!st[i].dW) { st[i].woff = wbytes; wbytes += align256(st[i].rb * j.rows); }
     }
     std::lock_guard<std::mutex> lk(g_call_mu);
+    if (int rc = settle()) return rc;
     void *at = nullptr, *yt = nullptr, *wt = nullptr;
     if (abytes)
         if (int rc = g_atmp.get(abytes, &at)) return rc;
@@ -1498,7 +1600,13 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
         if (int rc = g_ytmp.get(ybytes, &yt)) return rc;
     if (wbytes)
         if (int rc = g_wtmp.get(wbytes, &wt)) return rc;
-    std::vector<uint8_t> pack(abytes);
+    void *hin = nullptr, *hout = nullptr;
+    if (abytes)
+        if (int rc = g_hin.get(abytes, &hin)) return rc;
+    if (ybytes)
+        if (int rc = g_hout.get(ybytes, &hout)) return rc;
+    uint8_t *pack = static_cast<uint8_t *>(hin);
+    std::vector<HCopy> cp;
     std::vector<Req> reqs;
     hipError_t e;
     for (int i = 0; i < njobs; i++) {
@@ -1507,9 +1615,9 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
         FmtInfo f;
         fmt_info(j.type, f);
         const Stage &g = st[i];
-        for (size_t k = 0; k < g.qi.size(); k++) memcpy(pack.data() + g.aoff + g.ab * k, act_blocks(f, j.a[g.qi[k]]), g.ab);
+        for (size_t k = 0; k < g.qi.size(); k++) cp.push_back({pack + g.aoff + g.ab * k, act_blocks(f, j.a[g.qi[k]]), g.ab});
         for (size_t k = 0; k < g.qf.size(); k++)
-            memcpy(pack.data() + g.xoff + sizeof(float) * j.cols * k, j.a[g.qf[k]].x, sizeof(float) * j.cols);
+            cp.push_back({pack + g.xoff + sizeof(float) * j.cols * k, j.a[g.qf[k]].x, sizeof(float) * j.cols});
         const void *dW = g.dW;
         if (!dW) {
             dW = static_cast<uint8_t *>(wt) + g.woff;
@@ -1521,7 +1629,10 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
             reqs.push_back({j.type, dW, static_cast<uint8_t *>(at) + g.aoff, yd, nullptr, nullptr, 0, j.rows, j.cols,
                             (int)g.qi.size(), g.ab, (size_t)j.rows});
     }
-    if (abytes && (e = hipMemcpy(at, pack.data(), abytes, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "activation upload");
+    host_copies(cp);
+    g_table_pending = true;
+    if (abytes && (e = hipMemcpyAsync(at, hin, abytes, hipMemcpyHostToDevice, nullptr)) != hipSuccess)
+        return hip_fail(e, "activation upload");
     for (int i = 0; i < njobs; i++) {   // the float-path activations, stream-ordered before the batch's launches
         const es_hip_host_job &j = jobs[i];
         const Stage &g = st[i];
@@ -1533,18 +1644,20 @@ int es_hip_run_jobs_host(const es_hip_host_job *jobs, int njobs) {
                                   nullptr))
             return rc;
     }
-    if (int rc = run_sync(reqs, nullptr)) return rc;
-    if ((e = hipStreamSynchronize(nullptr)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    std::vector<uint8_t> out(ybytes);
-    if (ybytes && (e = hipMemcpy(out.data(), yt, ybytes, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "output download");
+    if (int rc = run_launch(reqs, nullptr, -1)) return rc;
+    if (ybytes && (e = hipMemcpyAsync(hout, yt, ybytes, hipMemcpyDeviceToHost, nullptr)) != hipSuccess)
+        return hip_fail(e, "output download");
+    if (int rc = finish(nullptr)) return rc;
+    cp.clear();
     for (int i = 0; i < njobs; i++) {
         const es_hip_host_job &j = jobs[i];
         if (j.rows == 0 || j.nb == 0) continue;
-        const float *src = reinterpret_cast<const float *>(out.data() + st[i].yoff);
+        const float *src = reinterpret_cast<const float *>(static_cast<const uint8_t *>(hout) + st[i].yoff);
         int k = 0;
-        for (int q : st[i].qi) memcpy(j.y + j.ys * q, src + (size_t)j.rows * k++, sizeof(float) * j.rows);
-        for (int q : st[i].qf) memcpy(j.y + j.ys * q, src + (size_t)j.rows * k++, sizeof(float) * j.rows);
+        for (int q : st[i].qi) cp.push_back({j.y + j.ys * q, src + (size_t)j.rows * k++, sizeof(float) * j.rows});
+        for (int q : st[i].qf) cp.push_back({j.y + j.ys * q, src + (size_t)j.rows * k++, sizeof(float) * j.rows});
     }
+    host_copies(cp);
     return ES_HIP_OK;
 }
 

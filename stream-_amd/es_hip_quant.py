@@ -541,11 +541,13 @@ class Lib:
             raise EsHipError(-1, err)
         return y
 
-    def run_jobs_host(self, jobs):
-        """jobs: list of (type, W host uint8, rows, cols, acts [nb, nblocks], y [nb, ys] float32 written in place), each
-        optionally extended by (x [nb, cols] fp32, floats): the activations listed in floats carry no blocks (float path)"""
+    @staticmethod
+    def host_jobs(jobs):
+        """(es_hip_host_job array, keep-alive list) for jobs: list of (type, W host uint8, rows, cols, acts [nb, nblocks],
+        y [nb, ys] float32 written in place), each optionally extended by (x [nb, cols] fp32, floats): the activations
+        listed in floats carry no blocks (float path)"""
         arr = (HostJob * max(len(jobs), 1))()
-        keep = []
+        keep = [arr]
         for k, job in enumerate(jobs):
             t, W, rows, cols, acts, y = job[:6]
             x, floats = (job[6], job[7]) if len(job) > 6 else (None, ())
@@ -555,6 +557,11 @@ class Lib:
             keep += [acts, x, recs]
             nb = acts.shape[0] if acts is not None else x.shape[0]
             arr[k] = HostJob(t, W.ctypes.data, rows, cols, C.cast(recs, C.c_void_p), y.ctypes.data, nb, y.strides[0] // 4)
+        return arr, keep
+
+    def run_jobs_host(self, jobs):
+        """es_hip_run_jobs_host over host_jobs(jobs)"""
+        arr, keep = self.host_jobs(jobs)
         self._check(self._L.es_hip_run_jobs_host(arr, len(jobs)))
         del keep
 
