@@ -12,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <array>
 #include <map>
 #include <mutex>
@@ -432,6 +433,7 @@ bool mk_eligible(const Req &q) {
 }
 
 std::atomic<int> g_pk_on{1};   // the persistent direct kernel (0: products take the per-tile launches)
+std::atomic<uint64_t> g_cfg_gen{0};   // bumped by every setting that changes how a batch is planned
 
 // The persistent direct kernel: Q4_K / Q3_K products that the direct kernels take (at least g_mk_min / g_mk3_min
 // activations), with an even number (>= 2) of superblocks per row and no gathered activations, every activation row
@@ -476,32 +478,46 @@ bool pk_schedule(PkGroup &g, int cus) {
             for (int t0 = 0; t0 < p.na; t0 += T)
                 (t64 ? v64 : v128).push_back(Tl{pi, rt, t0, std::min(T, p.na - t0), t64, pk_cost(p.nbk, t64)});
     }
-    // LPT of a tile set over workgroups [base, base + n) (n a multiple of 8), row tiles kept on one XCD
-    auto lpt = [&](const std::vector<Tl> &ts, int base, int n, std::vector<std::vector<int>> &own, std::vector<double> &load) {
-        std::map<std::pair<int, int>, double> rtc;   // (product, row tile) -> cost
-        for (const Tl &t : ts) rtc[{t.p, t.rt}] += t.c;
-        std::vector<std::pair<double, std::pair<int, int>>> order;
-        for (auto &e : rtc) order.push_back({e.second, e.first});
-        std::stable_sort(order.begin(), order.end(), [](const auto &a, const auto &b) { return a.first > b.first; });
+    // LPT of a tile set over workgroups [base, base + n) (n a multiple of 8), row tiles kept on one XCD. Row tiles are
+    // numbered through rtb (product p's row tile rt is rtb[p] + rt); tiles go longest first (ties in list order), each to
+    // the least loaded workgroup of its XCD (ties to the lowest index), through one min-heap per XCD.
+    std::vector<int> rtb(g.prods.size() + 1, 0);
+    for (size_t pi = 0; pi < g.prods.size(); pi++)
+        rtb[pi + 1] = rtb[pi] + (g.prods[pi].r1 - g.prods[pi].r0 + esq::MK_ROWS - 1) / esq::MK_ROWS;
+    // seq receives the tiles' indices in the order they were placed and wg_of[i] tile i's workgroup
+    auto lpt = [&](const std::vector<Tl> &ts, int base, int n, std::vector<int> &seq, std::vector<int> &wg_of,
+                   std::vector<double> &load) {
+        std::vector<double> rtc(rtb.back(), 0.0);
+        for (const Tl &t : ts) rtc[rtb[t.p] + t.rt] += t.c;
+        std::vector<int> order;
+        for (int i = 0; i < rtb.back(); i++)
+            if (rtc[i] > 0) order.push_back(i);
+        std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return rtc[a] > rtc[b]; });
         double xl[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        std::map<std::pair<int, int>, int> xcd;
-        for (auto &o : order) {
+        std::vector<int8_t> xcd(rtb.back(), 0);
+        for (int o : order) {
             int x = 0;
             for (int i = 1; i < 8; i++)
                 if (xl[i] < xl[x]) x = i;
-            xcd[o.second] = x;
-            xl[x] += o.first;
+            xcd[o] = (int8_t)x;
+            xl[x] += rtc[o];
         }
-        std::vector<int> idx(ts.size());
-        for (size_t i = 0; i < ts.size(); i++) idx[i] = (int)i;
-        std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return ts[a].c > ts[b].c; });
-        for (int i : idx) {
-            const int x = xcd[{ts[i].p, ts[i].rt}];
-            int best = -1;
-            for (int w = base + ((x - base) % 8 + 8) % 8; w < base + n; w += 8)
-                if (best < 0 || load[w] < load[best]) best = w;
-            own[best].push_back(i);
-            load[best] += ts[i].c;
+        seq.resize(ts.size());
+        for (size_t i = 0; i < ts.size(); i++) seq[i] = (int)i;
+        std::stable_sort(seq.begin(), seq.end(), [&](int a, int b) { return ts[a].c > ts[b].c; });
+        wg_of.assign(ts.size(), -1);
+        typedef std::pair<double, int> LW;   // (load, workgroup)
+        std::vector<LW> heap[8];
+        for (int w = base; w < base + n; w++) heap[w % 8].push_back({load[w], w});
+        for (auto &h : heap) std::make_heap(h.begin(), h.end(), std::greater<LW>());
+        for (int i : seq) {
+            std::vector<LW> &h = heap[xcd[rtb[ts[i].p] + ts[i].rt]];
+            std::pop_heap(h.begin(), h.end(), std::greater<LW>());
+            LW &top = h.back();
+            wg_of[i] = top.second;
+            load[top.second] += ts[i].c;
+            top.first = load[top.second];
+            std::push_heap(h.begin(), h.end(), std::greater<LW>());
         }
     };
     // choose g64 (and the 128-wide tiles cut in two) for the smallest makespan
@@ -509,11 +525,16 @@ bool pk_schedule(PkGroup &g, int cus) {
     int best_g64 = 0, best_h = 0;
     const double w64 = [&] { double w = 0; for (const Tl &t : v64) w += t.c; return w; }();
     const double w128 = [&] { double w = 0; for (const Tl &t : v128) w += t.c; return w; }();
+    // candidates: the split that gives each set workgroups in proportion to its load, and one step of 8 either side
     std::vector<int> cands;
     if (v64.empty()) cands.push_back(0);
     else if (v128.empty()) cands.push_back(G);
-    else
-        for (int c = 8; c <= G - 8; c += 8) cands.push_back(c);
+    else {
+        const int c0 = (int)std::lround(G * w64 / (w64 + w128) / 8) * 8;
+        for (int c = c0 - 8; c <= c0 + 8; c += 8)
+            if (c >= 8 && c <= G - 8) cands.push_back(c);
+        if (cands.empty()) cands.push_back(c0 < 8 ? 8 : G - 8);
+    }
     auto build = [&](int g64, int h, std::vector<Tl> &a64, std::vector<Tl> &a128) {
         a64 = v64;
         a128.assign(v128.begin(), v128.end() - h);
@@ -524,6 +545,7 @@ bool pk_schedule(PkGroup &g, int cus) {
         }
         (void)g64;
     };
+    std::vector<int> seq64, wg64, seq128, wg128;
     for (int g64 : cands) {
         int h = 0;
         if (g64 > 0 && g64 < G && !v128.empty()) {
@@ -534,48 +556,56 @@ bool pk_schedule(PkGroup &g, int cus) {
         std::vector<Tl> a64, a128;
         build(g64, h, a64, a128);
         if ((!a64.empty() && g64 == 0) || (!a128.empty() && g64 == G)) continue;
-        std::vector<std::vector<int>> own(G);
         std::vector<double> load(G, 0.0);
-        if (!a64.empty()) lpt(a64, 0, g64, own, load);
-        if (!a128.empty()) lpt(a128, g64, G - g64, own, load);
+        if (!a64.empty()) lpt(a64, 0, g64, seq64, wg64, load);
+        if (!a128.empty()) lpt(a128, g64, G - g64, seq128, wg128, load);
         const double ms = *std::max_element(load.begin(), load.end());
         if (ms < best_ms - 1e-9) { best_ms = ms; best_g64 = g64; best_h = h; }
     }
     std::vector<Tl> a64, a128;
     build(best_g64, best_h, a64, a128);
-    std::vector<std::vector<int>> own(G);
     std::vector<double> load(G, 0.0);
-    if (!a64.empty()) lpt(a64, 0, best_g64, own, load);
-    std::vector<std::vector<int>> own128(G);
-    if (!a128.empty()) lpt(a128, best_g64, G - best_g64, own128, load);
+    seq64.clear();
+    seq128.clear();
+    if (!a64.empty()) lpt(a64, 0, best_g64, seq64, wg64, load);
+    if (!a128.empty()) lpt(a128, best_g64, G - best_g64, seq128, wg128, load);
+    // each workgroup's tiles in the order they were placed (longest first)
+    std::vector<int> cnt(G + 1, 0);
+    for (int i : seq64) cnt[wg64[i] + 1]++;
+    for (int i : seq128) cnt[wg128[i] + 1]++;
+    for (int w = 0; w < G; w++) {
+        if (cnt[w + 1] > esq::PK_MAX_TILES) return false;
+        cnt[w + 1] += cnt[w];
+    }
+    std::vector<std::pair<const Tl *, int>> placed(seq64.size() + seq128.size());
+    {
+        std::vector<int> at(cnt.begin(), cnt.end() - 1);
+        for (int i : seq64) placed[at[wg64[i]]++] = {&a64[i], wg64[i]};
+        for (int i : seq128) placed[at[wg128[i]]++] = {&a128[i], wg128[i]};
+    }
     g.grid = G;
     g.g64 = best_g64;
     g.tiles.clear();
-    g.wgptr.assign(1, 0);
-    for (int w = 0; w < G; w++) {
-        const bool is64 = w < best_g64;
-        const std::vector<int> &mine = is64 ? own[w] : own128[w];
-        if ((int)mine.size() > esq::PK_MAX_TILES) return false;
-        for (int i : mine) {
-            const Tl &t = is64 ? a64[i] : a128[i];
-            const PkGroup::Prod &p = g.prods[t.p];
-            const int row0 = p.r0 + esq::MK_ROWS * t.rt;
-            esq::PkTile r{};
-            r.w = p.W + (size_t)row0 * p.row_bytes;
-            r.act = p.act;
-            r.y = p.y + (size_t)t.t0 * p.ystride + row0;
-            r.astride = p.astride;
-            r.ystride4 = 4u * p.ystride;
-            r.row_bytes = p.row_bytes;
-            r.nbk = p.nbk;
-            r.t64 = t.t64 ? 1 : 0;
-            r.tok0 = t.t0;
-            r.na = p.na;
-            r.rows = std::min(esq::MK_ROWS, p.r1 - row0);
-            r.ntok = t.nt;
-            g.tiles.push_back(r);
-        }
-        g.wgptr.push_back((int)g.tiles.size());
+    g.tiles.reserve(placed.size());
+    g.wgptr.assign(cnt.begin(), cnt.end());
+    for (const auto &pt : placed) {
+        const Tl &t = *pt.first;
+        const PkGroup::Prod &p = g.prods[t.p];
+        const int row0 = p.r0 + esq::MK_ROWS * t.rt;
+        esq::PkTile r{};
+        r.w = p.W + (size_t)row0 * p.row_bytes;
+        r.act = p.act;
+        r.y = p.y + (size_t)t.t0 * p.ystride + row0;
+        r.astride = p.astride;
+        r.ystride4 = 4u * p.ystride;
+        r.row_bytes = p.row_bytes;
+        r.nbk = p.nbk;
+        r.t64 = t.t64 ? 1 : 0;
+        r.tok0 = t.t0;
+        r.na = p.na;
+        r.rows = std::min(esq::MK_ROWS, p.r1 - row0);
+        r.ntok = t.nt;
+        g.tiles.push_back(r);
     }
     return true;
 }
@@ -1077,6 +1107,74 @@ void *reg_lookup(const void *h, size_t n) {
     return static_cast<uint8_t *>(it->second.dev) + (a - it->first);
 }
 
+// Batches without a pre-pass workspace are kept after their first call, tables on the device: the engine repeats the same
+// products on the same buffers at every step (dense_n's gate/up and down per layer), and a repeat then launches from the
+// kept tables with no planning and no upload. Such tables are read-only, so every stream may share them. The key is every
+// request field and the planning settings' generation; at most BC_MAX batches are kept, the least recently used one freed
+// first (hipFree waits for kernels that may still read it).
+struct CachedBatch {
+    std::vector<Req> reqs;
+    uint64_t gen, tick;
+    Batch bt;
+    void *dev;
+};
+constexpr size_t BC_MAX = 64;
+std::mutex g_bc_mu;
+std::vector<CachedBatch> g_bc;
+uint64_t g_bc_tick = 0;
+
+bool same_reqs(const std::vector<Req> &a, const std::vector<Req> &b) {
+    if (a.size() != b.size()) return false;
+    for (size_t i = 0; i < a.size(); i++) {
+        const Req &x = a[i], &y = b[i];
+        if (x.type != y.type || x.W != y.W || x.act != y.act || x.y != y.y || x.ints != y.ints || x.aux != y.aux ||
+            x.r0 != y.r0 || x.r1 != y.r1 || x.cols != y.cols || x.na != y.na || x.astride != y.astride ||
+            x.ystride != y.ystride || x.arow != y.arow || x.act_rows != y.act_rows)
+            return false;
+    }
+    return true;
+}
+
+// A kept batch for reqs, launched on s: 1 if launched (rc set), 0 if none is kept.
+int cached_launch(const std::vector<Req> &reqs, hipStream_t s, int order, int &rc) {
+    const uint64_t gen = g_cfg_gen.load();
+    std::lock_guard<std::mutex> lk(g_bc_mu);
+    for (CachedBatch &c : g_bc)
+        if (c.gen == gen && same_reqs(c.reqs, reqs)) {
+            c.tick = ++g_bc_tick;
+            rc = launch_batch(c.bt, static_cast<const uint8_t *>(c.dev), order >= 0 ? order : g_order.load(), s);
+            return 1;
+        }
+    return 0;
+}
+
+// Keeps a planned batch without a pre-pass workspace and launches it on s: 1 if kept (rc set), 0 if it cannot be kept.
+int keep_and_launch(const std::vector<Req> &reqs, Batch &bt, hipStream_t s, int order, int &rc) {
+    if (bt.ws_bytes != 0 || bt.table_bytes == 0) return 0;
+    const uint64_t gen = g_cfg_gen.load();
+    void *dev = nullptr;
+    hipError_t e = hipMalloc(&dev, bt.table_bytes);
+    if (e != hipSuccess) { rc = hip_fail(e, "hipMalloc (kept job tables)"); return 1; }
+    bind(bt, static_cast<uint8_t *>(dev) + align256(bt.table_bytes));
+    const std::vector<uint8_t> img = table_image(bt);
+    // the upload is complete before any stream may launch from the tables
+    if ((e = hipMemcpy(dev, img.data(), img.size(), hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipDeviceSynchronize()) != hipSuccess) {
+        (void)hipFree(dev);
+        rc = hip_fail(e, "job table upload");
+        return 1;
+    }
+    std::lock_guard<std::mutex> lk(g_bc_mu);
+    if (g_bc.size() >= BC_MAX) {
+        auto lru = std::min_element(g_bc.begin(), g_bc.end(), [](const CachedBatch &a, const CachedBatch &b) { return a.tick < b.tick; });
+        (void)hipFree(lru->dev);
+        g_bc.erase(lru);
+    }
+    g_bc.push_back(CachedBatch{reqs, gen, ++g_bc_tick, std::move(bt), dev});
+    rc = launch_batch(g_bc.back().bt, static_cast<const uint8_t *>(dev), order >= 0 ? order : g_order.load(), s);
+    return 1;
+}
+
 // Plan, upload the job tables (and bind the pre-pass workspace) in scratch, launch: the path shared by run_jobs,
 // run_jobs_host and the host drop-ins. The caller holds g_call_mu. The tables go up from page-locked staging, stream-ordered
 // behind the caller's earlier work on s; every call waits for its kernels before it returns (with sync here, or, for the
@@ -1094,11 +1192,20 @@ int settle() {   // before the staging or the scratch is reused: the wait a fail
 }
 
 int run_launch(const std::vector<Req> &reqs, hipStream_t s, int order) {   // order -1: es_hip_set_order's
+    int rc = ES_HIP_OK;
+    if (cached_launch(reqs, s, order, rc)) {
+        if (!rc) g_table_pending = true;   // the caller's wait follows
+        return rc;
+    }
     Batch bt;
-    if (int rc = plan_batch(reqs, bt)) return rc;
+    if (int e = plan_batch(reqs, bt)) return e;
     if (bt.mv.empty() && bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.pkg.empty()) return ES_HIP_OK;
+    if (int e = settle()) return e;
+    if (keep_and_launch(reqs, bt, s, order, rc)) {
+        g_table_pending = true;
+        return rc;
+    }
     hipError_t e;
-    if (int rc = settle()) return rc;
     void *dev = nullptr, *htab = nullptr;
     const size_t ws_at = align256(bt.table_bytes);
     if (int rc = g_table.get(ws_at + bt.ws_bytes, &dev)) return rc;
@@ -1210,18 +1317,20 @@ int es_hip_synchronize(void) {
 // pre-passes) with a stream-ordered allocation for the job tables and the pre-pass workspace, freed in stream order. The
 // tables are copied from pageable memory, which the copy has consumed when it returns.
 static int run_async(const std::vector<Req> &reqs, hipStream_t s) {
+    int rc = ES_HIP_OK;
+    if (cached_launch(reqs, s, -1, rc)) return rc;
     Batch bt;
-    if (int rc = plan_batch(reqs, bt)) return rc;
+    if (int e = plan_batch(reqs, bt)) return e;
     if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.pkg.empty() && bt.mv.size() <= 1 &&
         (bt.mv.empty() || bt.mv[0].jobs.size() == 1))
         return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
+    if (keep_and_launch(reqs, bt, s, -1, rc)) return rc;
     void *dev = nullptr;
     const size_t ws_at = align256(bt.table_bytes);
     hipError_t e = hipMallocAsync(&dev, std::max<size_t>(ws_at + bt.ws_bytes, 256), s);
     if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (tables and workspace)");
     bind(bt, static_cast<uint8_t *>(dev) + ws_at);
     const std::vector<uint8_t> img = table_image(bt);
-    int rc = ES_HIP_OK;
     if (!img.empty() && (e = hipMemcpyAsync(dev, img.data(), img.size(), hipMemcpyHostToDevice, s)) != hipSuccess)
         rc = hip_fail(e, "job table upload");
     if (!rc) rc = launch_batch(bt, static_cast<const uint8_t *>(dev), g_order.load(), s);
@@ -1402,8 +1511,9 @@ void es_hip_plan_destroy(es_hip_plan *p) {
     delete p;
 }
 
-int es_hip_set_mfma_min_batch(int n) { return g_mm_min.exchange(n); }
+int es_hip_set_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_mm_min.exchange(n); }
 int es_hip_set_mfma_tile(int bm, int bn, int waves) {
+    g_cfg_gen.fetch_add(1);
     if (bm == 0 && bn == 0 && waves == 0) {
         g_mm_tile.store(0);
         return ES_HIP_OK;
@@ -1412,20 +1522,20 @@ int es_hip_set_mfma_tile(int bm, int bn, int waves) {
     g_mm_tile.store(bm | bn << 10 | waves << 20);
     return ES_HIP_OK;
 }
-int es_hip_set_small_batch_min(int n) { return g_mq_min.exchange(n); }
-int es_hip_set_batched32_min(int n) { return g_mb_min.exchange(n); }
-int es_hip_set_batched32_mfma_min(int n) { return g_mbm_min.exchange(n); }
-int es_hip_set_q6k_mfma_min_batch(int n) { return g_mm6_min.exchange(n); }
-int es_hip_set_q2k_mfma_min_batch(int n) { return g_mm2_min.exchange(n); }
-int es_hip_set_direct_mfma_min_batch(int n) { return g_mk_min.exchange(n); }
-int es_hip_set_direct_mfma_min_tiles(int n) { return g_mk_min_tiles.exchange(n); }
-int es_hip_set_q5k_mfma_min_batch(int n) { return g_mk5_min.exchange(n); }
-int es_hip_set_q3k_mfma_min_batch(int n) { return g_mk3_min.exchange(n); }
-int es_hip_set_direct_persistent(int on) { return g_pk_on.exchange(on ? 1 : 0); }
-int es_hip_set_q2k_expert_max_batch(int n) { return g_mx_max.exchange(n); }
-int es_hip_set_batched32_direct(int on) { return g_mbx_on.exchange(on ? 1 : 0); }
-int es_hip_set_q6k_persistent(int on) { return esq::mm6_set_persistent(on); }
-int es_hip_set_direct_mfma_tok64(int on) { return g_mk_tok64.exchange(on ? 1 : 0); }
+int es_hip_set_small_batch_min(int n) { g_cfg_gen.fetch_add(1); return g_mq_min.exchange(n); }
+int es_hip_set_batched32_min(int n) { g_cfg_gen.fetch_add(1); return g_mb_min.exchange(n); }
+int es_hip_set_batched32_mfma_min(int n) { g_cfg_gen.fetch_add(1); return g_mbm_min.exchange(n); }
+int es_hip_set_q6k_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_mm6_min.exchange(n); }
+int es_hip_set_q2k_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_mm2_min.exchange(n); }
+int es_hip_set_direct_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_mk_min.exchange(n); }
+int es_hip_set_direct_mfma_min_tiles(int n) { g_cfg_gen.fetch_add(1); return g_mk_min_tiles.exchange(n); }
+int es_hip_set_q5k_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_mk5_min.exchange(n); }
+int es_hip_set_q3k_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_mk3_min.exchange(n); }
+int es_hip_set_direct_persistent(int on) { g_cfg_gen.fetch_add(1); return g_pk_on.exchange(on ? 1 : 0); }
+int es_hip_set_q2k_expert_max_batch(int n) { g_cfg_gen.fetch_add(1); return g_mx_max.exchange(n); }
+int es_hip_set_batched32_direct(int on) { g_cfg_gen.fetch_add(1); return g_mbx_on.exchange(on ? 1 : 0); }
+int es_hip_set_q6k_persistent(int on) { g_cfg_gen.fetch_add(1); return esq::mm6_set_persistent(on); }
+int es_hip_set_direct_mfma_tok64(int on) { g_cfg_gen.fetch_add(1); return g_mk_tok64.exchange(on ? 1 : 0); }
 
 double es_hip_plan_time_ms(es_hip_plan *p, int warmup, int iters, void *stream) {
     if (!p || iters <= 0) { fail(ES_HIP_EINVAL, "bad plan or iteration count"); return -1.0; }
