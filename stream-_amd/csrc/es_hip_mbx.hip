@@ -48,8 +48,8 @@ template <typename T> __device__ __forceinline__ T lds_ld(uint32_t a) {
 
 template <int F> struct BxFmt;
 // Q4_0: d f16 @0, qs[16] @2, codes 0..15 - 8. Q5_0: d f16 @0, qh u32 @2, qs[16] @6, codes 0..31 - 16.
-// Q8_0: d f16 @0, int8 qs[32] @2 (group i's codes are dword i). ADD: the per-byte bias that makes (c + ADD) ^ 0x80 the
-// signed byte c - offset (no carry between bytes: c + ADD <= 255).
+// Q8_0: d f16 @0, int8 qs[32] @2 (group i's codes are dword i). ADD (Q4_0, Q5_0): the per-byte bias that makes
+// (c + ADD) ^ 0x80 the signed byte c - offset (no carry between bytes: c + ADD <= 255).
 template <> struct BxFmt<ES_HIP_Q4_0> {
     static constexpr int QS = 2, QH = -1;
     static constexpr bool BYTES = false;
@@ -63,7 +63,6 @@ template <> struct BxFmt<ES_HIP_Q5_0> {
 template <> struct BxFmt<ES_HIP_Q8_0> {
     static constexpr int QS = 2, QH = -1;
     static constexpr bool BYTES = true;
-    static constexpr uint32_t ADD = 0u;
 };
 
 struct Stage {

@@ -95,7 +95,7 @@ template <int T> struct MkSlot {
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 template <int F> struct MkFmt;
-template <> struct MkFmt<ES_HIP_Q4_K> { static constexpr int BB = 144, QS = 16, QH = -1; };
+template <> struct MkFmt<ES_HIP_Q4_K> { static constexpr int BB = 144, QS = 16; };
 template <> struct MkFmt<ES_HIP_Q5_K> { static constexpr int BB = 176, QS = 48, QH = 16; };
 template <> struct MkFmt<ES_HIP_Q3_K> { static constexpr int BB = 110, QS = 32, QH = 0; };
 
