@@ -3,7 +3,8 @@ tables built on the device from a routing in device memory, then the expert FFN,
 trip per call. Outputs must equal the oracle's moe_n restatement bit for bit: configs 4 and 5 from device logits (the
 routing equal to the oracle's route()), every reference order, every kernel family (decode kernel, pre-pass +
 matrix-core kernel, expert-sized Q2_K kernel), skewed routings where one expert takes every token, fresh routings and token counts call after call
-on one context without a wait between them, and the rejected shapes."""
+on one context without a wait between them, routing shapes up to 300 experts and k = 16, NaN logits, and the rejected
+shapes."""
 import numpy as np
 import pytest
 
@@ -67,6 +68,58 @@ def test_ctx_config5_qwen3_mixed_from_logits(hipo, orc):
     want_sel, want_w = routed(orc, N, n_exp, k, True, 1239)
     assert np.array_equal(sel, want_sel) and np.array_equal(bits(w), bits(want_w))
     assert np.array_equal(bits(out), bits(orc.moe_ffn(types, ex.host, n, ff, x, want_sel, want_w)))
+    ctx.close()
+
+
+def run_logits_given(hip, ctx, ex, logits, k, norm, x):
+    N, n = logits.shape[0], ex.n
+    dl, dx = hip.upload(np.ascontiguousarray(logits, np.float32)), hip.upload(x)
+    dout = hip.upload(np.full((N, n), -777.0, np.float32))
+    dsel, dw = hip.alloc(N * k * 4), hip.alloc(N * k * 4)
+    ctx.run_logits(N, dl, 0, norm, dx, x.strides[0], dout, n, dsel, dw)
+    hip.synchronize()
+    return (hip.download(dout, np.zeros((N, n), np.float32)), hip.download(dsel, np.zeros((N, k), np.int32)),
+            hip.download(dw, np.zeros((N, k), np.float32)))
+
+
+@pytest.mark.parametrize("n_exp,k,N,norm", [(256, 16, 70, True), (256, 1, 65, False), (300, 8, 20, True), (40, 12, 129, False)],
+                         ids=["e256-k16", "e256-k1", "e300-k8", "e40-k12-n129"])
+def test_ctx_routing_shapes(hipo, orc, n_exp, k, N, norm):
+    """device routing of layers with many experts, k from 1 to 16 and token counts that are not multiples of anything:
+    sel and w equal the oracle's route() (ties, underflowing experts), and the layer's outputs equal the oracle's moe_n"""
+    n, ff = 256, 256
+    types = (E.Q4_K, E.Q4_K, E.Q6_K)
+    ex = Experts(hipo, orc, types, n_exp, n, ff, 300 + n_exp)
+    rng = np.random.default_rng(n_exp * N + k)
+    lg = rng.standard_normal((N, n_exp)).astype(np.float32)
+    lg[0] = 0.0                                                  # all equal: ties everywhere
+    lg[1] = np.round(lg[1] * 2) / 2                              # repeated values
+    lg[2] = (rng.standard_normal(n_exp) * 60).astype(np.float32)  # expf underflows for most experts
+    x = orc.quantize_act(types[0], orc.gauss(17 + N, 1.0, N * n).reshape(N, n))
+    ctx = hipo.moe_ctx(ex.args(np.zeros(1, np.int32), np.zeros((1, k), np.int32), np.zeros((1, k), np.float32)), N, k)
+    out, sel, w = run_logits_given(hipo, ctx, ex, lg, k, norm, x)
+    osel, ow, _ = orc.route_softmax(lg, k, norm)
+    assert np.array_equal(sel, osel) and np.array_equal(bits(w), bits(ow))
+    assert np.array_equal(bits(out), bits(orc.moe_ffn(types, ex.host, n, ff, x, osel, ow)))
+    ctx.close()
+
+
+def test_ctx_routing_nan_logits(hipo, orc):
+    """a token whose logits hold a NaN takes route()'s plain scan (every probability NaN: experts 0, 1, 2, ... in order);
+    the other tokens of the same call route normally"""
+    n, ff, n_exp, k, N = 256, 256, 64, 4, 9
+    types = (E.Q4_K, E.Q4_K, E.Q4_K)
+    ex = Experts(hipo, orc, types, n_exp, n, ff, 333)
+    lg = np.random.default_rng(3).standard_normal((N, n_exp)).astype(np.float32)
+    lg[4, 10] = np.nan
+    x = orc.quantize_act(types[0], orc.gauss(19, 1.0, N * n).reshape(N, n))
+    ctx = hipo.moe_ctx(ex.args(np.zeros(1, np.int32), np.zeros((1, k), np.int32), np.zeros((1, k), np.float32)), N, k)
+    _, sel, w = run_logits_given(hipo, ctx, ex, lg, k, True, x)
+    osel, ow, _ = orc.route_softmax(lg, k, True)
+    assert np.array_equal(sel, osel)
+    assert np.array_equal(sel[4], np.arange(k)) and np.all(np.isnan(w[4]))
+    ok = np.arange(N) != 4
+    assert np.array_equal(bits(w[ok]), bits(ow[ok]))
     ctx.close()
 
 
