@@ -36,10 +36,11 @@ struct MvJob {
     uint64_t row_bytes;
     int r0, r1, cols, na;
     int tile0, rows_per_wg, chain_rows;
-    int pad_;
+    int nt;               // activations per pass (1, 2 or 4): the launch's, or this job's in a launch of mixed widths
 };
 
-// One launch of the decode kernel: format, activations per pass, waves per workgroup, workgroups, LDS bytes.
+// One launch of the decode kernel: format, activations per pass (0: each job's own), waves per workgroup, workgroups,
+// LDS bytes.
 struct MvLaunch {
     int type, nt, waves;
     int grid;

@@ -465,6 +465,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
                             J.y = A.bgu + (size_t)s0 * 2 * ff + (size_t)g * ff;
                         }
                         J.na = c;
+                        J.nt = min(J.nt, c >= 3 ? 4 : c);   // the planner's width for c activations, within the LDS sizing
                         J.tile0 = (njob * u + g) * F.mv_tiles;
                     } else {   // empty: the template's valid pointers, no rows, no activations, after the last real tile
                         J.na = 0;

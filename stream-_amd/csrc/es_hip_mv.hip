@@ -507,17 +507,13 @@ template <int F, int NT> constexpr int units() {
 // whole workgroup runs the per-row chains. order: ES_HIP_ORDER_*; NT activations per pass. One workgroup per tile
 // (rows_per_wg rows of one job).
 template <int F, int NT, int W, bool SEGLOOP>
-__global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob *__restrict__ jobs, int njobs, MvJob single,
-                                                                     int order) {
+__device__ __forceinline__ void mv_body(const MvJob &J, int order) {
     using L = Lane<F>;
     constexpr int LPB = Fmt<F>::LPB, BE = Fmt<F>::BE, BB = Fmt<F>::BB, AB = Fmt<F>::AB;
     constexpr int SLOTS = WAVE / LPB;
     constexpr bool W32 = is32<F>();
     constexpr int U = units<F, NT>();   // row passes whose raw loads a wave issues before using any of them
 
-    MvJob J;
-    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
-    else J = single;
     const int nbk = J.cols / BE;
     const int tile = blockIdx.x - J.tile0;
     const int ra0 = J.r0 + tile * J.rows_per_wg;
@@ -685,6 +681,31 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
     }
 }
 
+template <int F, int NT, int W, bool SEGLOOP>
+__global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob *__restrict__ jobs, int njobs, MvJob single,
+                                                                     int order) {
+    MvJob J;
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
+    else J = single;
+    mv_body<F, NT, W, SEGLOOP>(J, order);
+}
+
+// A launch whose jobs take different activations per pass (J.nt: 1, 2 or 4), e.g. an MoE layer's experts at 1 to 8
+// tokens each: every job runs the body compiled for its own pass width (a single expert's token no longer runs in a
+// four-wide pass with its fewer loads in flight).
+template <int F, int W, bool SEGLOOP>
+__global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel_mixed(const MvJob *__restrict__ jobs, int njobs,
+                                                                           MvJob single, int order) {
+    MvJob J;
+    if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
+    else J = single;
+    switch (J.nt) {
+    case 1: mv_body<F, 1, W, SEGLOOP>(J, order); break;
+    case 2: mv_body<F, 2, W, SEGLOOP>(J, order); break;
+    default: mv_body<F, 4, W, SEGLOOP>(J, order); break;
+    }
+}
+
 }  // namespace esq
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -704,6 +725,10 @@ template <int F, int NT> static MvFn pick_w(int w, bool seg_loop) {
 }
 template <int F> static MvFn pick_nt(int nt, int w, bool seg_loop) {
     switch (nt) {
+    case 0:   // per-job pass widths
+        if (w == 4) return seg_loop ? nullptr : mv_kernel_mixed<F, 4, false>;
+        if (w == 8) return seg_loop ? mv_kernel_mixed<F, 8, true> : mv_kernel_mixed<F, 8, false>;
+        return nullptr;
     case 1: return pick_w<F, 1>(w, seg_loop);
     case 2: return pick_w<F, 2>(w, seg_loop);
     case 4: return pick_w<F, 4>(w, seg_loop);

@@ -202,16 +202,21 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
             max_nbk = std::max(max_nbk, q->cols / f.be);
         }
         g.L.seg_loop = segments(max_nbk, slots) > waves;
-        int nt = max_na >= 3 ? 4 : max_na;   // 3 activations in one pass of 4 rather than two passes of 2
-        while (nt > 1 && (size_t)max_nbk * nt * (w32 ? 9 : 2) * sizeof(float) > LDS_MAX) nt /= 2;   // one row's terms fit
+        // activations per pass: 3 in one pass of 4 rather than two passes of 2; at most what keeps one row's terms in LDS.
+        // Jobs of different counts (an MoE layer's experts) each take their own width in one launch of mixed widths.
+        int nt_cap = 4;
+        while (nt_cap > 1 && (size_t)max_nbk * nt_cap * (w32 ? 9 : 2) * sizeof(float) > LDS_MAX) nt_cap /= 2;
+        auto nt_of = [&](int na) { return std::min(nt_cap, na >= 3 ? 4 : std::max(na, 1)); };
+        bool mixed = false;
+        for (const Req *q : kv.second) mixed = mixed || nt_of(q->na) != nt_of(kv.second[0]->na);
         g.L.type = static_cast<int>(kv.first.first);
-        g.L.nt = nt;
+        g.L.nt = mixed ? 0 : nt_of(kv.second[0]->na);
         g.L.waves = waves;
         int tile = 0;
         size_t lds = 0;
         const int cw = w32 ? 9 : 2;
         for (const Req *q : kv.second) {
-            const int nbk = q->cols / f.be, rows = q->r1 - q->r0;
+            const int nbk = q->cols / f.be, rows = q->r1 - q->r0, nt = nt_of(q->na);
             const int rpi = nbk <= slots ? slots / nbk : 1;
             const int seg = segments(nbk, slots);
             const int rstep = std::max(1, waves / seg) * rpi;   // rows one pass of the workgroup covers
@@ -241,6 +246,7 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
             j.tile0 = tile;
             j.rows_per_wg = rpw;
             j.chain_rows = chain;
+            j.nt = nt;
             tile += (rows + rpw - 1) / rpw;
             lds = std::max(lds, (size_t)chain * per_row);
             g.jobs.push_back(j);
@@ -1908,7 +1914,11 @@ int moe_build(es_hip_moe_plan *p, const es_hip_moe *m, int N, const int *k, cons
     // the two grouped products
     const uint64_t xs = xstride ? xstride : (uint64_t)(n / fg.be) * fg.ab;
     std::vector<Req> gu, dn;
-    for (size_t u = 0; u < uex.size(); u++) {
+    // experts with the most tokens first: their workgroups run longest, so they start first and the launch ends evenly
+    std::vector<int> ord(uex.size());
+    for (size_t u = 0; u < ord.size(); u++) ord[u] = (int)u;
+    std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return cnt[a] > cnt[b]; });
+    for (int u : ord) {
         const int ex = uex[u], s0 = start[u], c = cnt[u];
         float *y = p->bgu + (size_t)s0 * 2 * ff;
         gu.push_back({m->gate_type, m->gate[ex], x, y, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0, N});
@@ -2198,6 +2208,7 @@ int moe_family(es_hip_moe_ctx *c, uint32_t type, int rows, int cols, int umax, i
     M.F.mv.tile0 = 0;
     M.F.mv_tiles = (rows + M.F.mv.rows_per_wg - 1) / M.F.mv.rows_per_wg;
     M.grid = M.L.grid = njob * umax * M.F.mv_tiles;
+    M.L.nt = 0;   // each expert's job takes the width of its own count (the grouping sets it, at most the template's)
     return ES_HIP_OK;
 }
 

@@ -236,6 +236,39 @@ def test_run_jobs_and_plan_mixed_formats(hip, orc):
     plan.close()
 
 
+@pytest.mark.parametrize("mode", [(E.ORDER_X86_CONTRACT, O.CONTRACT, O.PATH_X86), (E.ORDER_SCALAR, O.STRICT, O.PATH_SCALAR)],
+                         ids=["clang", "scalar"])
+def test_decode_launch_of_mixed_pass_widths(hip, orc, mode):
+    """one decode-kernel launch whose jobs take different activations per pass (1, 2 and 4: 1, 2, 3, 5 and 8
+    activations, as an MoE layer's experts do), for a K-quant and a 32-element format, repeated calls through a kept
+    plan and fresh run_jobs calls with new values: every output equals the oracle's"""
+    hip.set_order(mode[0])
+    prev = (hip.set_direct_mfma_min_batch(0), hip.set_mfma_min_batch(0), hip.set_small_batch_min(0),
+            hip.set_batched32_min(0), hip.set_q6k_mfma_min_batch(0))
+    try:
+        for F, rows, cols in (("Q4_K", 200, 2048), ("Q6_K", 70, 768), ("Q5_0", 90, 1024)):
+            t = O.TYPES[F]
+            for rep in range(2):
+                specs, keep, refs = [], [], []
+                for k, na in enumerate((1, 5, 2, 3, 8, 1, 2)):
+                    W, acts = mtest_inputs(orc, t, rows, cols, na, 700 + 10 * k + rep)
+                    dW, dA, dY = hip.upload(W), hip.upload(acts), hip.alloc(na * rows * 4)
+                    keep += [dW, dA, dY]
+                    specs.append(dict(type=t, rows=rows, cols=cols, W=dW, act=dA, astride=acts.strides[0], nb=na, y=dY,
+                                      ystride=rows))
+                    refs.append((dY, na, orc.matvec_multi(t, W, cols, rows, acts, mode[1], mode[2])))
+                hip.run_jobs(specs)
+                for dY, na, ref in refs:
+                    assert np.array_equal(bits(hip.download(dY, np.zeros((na, rows), np.float32))), bits(ref)), (F, na)
+    finally:
+        hip.set_direct_mfma_min_batch(prev[0])
+        hip.set_mfma_min_batch(prev[1])
+        hip.set_small_batch_min(prev[2])
+        hip.set_batched32_min(prev[3])
+        hip.set_q6k_mfma_min_batch(prev[4])
+        hip.set_order(E.ORDER_X86_CONTRACT)
+
+
 def test_invalid_arguments_are_rejected(hip):
     buf = hip.alloc(1 << 16)
     with pytest.raises(E.EsHipError):   # cols not a multiple of the block
