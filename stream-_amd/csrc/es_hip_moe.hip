@@ -376,9 +376,8 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
         U = total;
         lds_sync();   // wfl is rewritten by the next chunk; slot and uex are complete
     }
-    // slot u's expert and its matrices
+    // slot u's expert
     const int ue = tid < U ? uex[tid] : 0;
-    const uint8_t *wgate = pg[ue], *wup = pu[ue], *wdown = pd[ue];
     const int c_me = tid < U ? cnt[ue] : 0;   // thread u: slot u's expert's count
     const int st = block_excl_scan3(make_int3(c_me, 0, 0), wsum, &s_tot).x;
     if (tid < NE) ustart[tid] = st;
@@ -415,10 +414,30 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
         if (p < R && e >= 0 && (same & lt) == 0) atomicAdd(&taken[e], __popcll(same));
         lds_sync();
     }
-    // ---- job tables. Thread u writes slot u's jobs; tiles and pre-pass items are prefix sums over the slots.
-    const int u = tid;
+    // ---- job tables. With a decode-kernel family, slots go by token count, most first (ties in slot order), so the
+    // launch starts its longest workgroups first (the expert-sized and matrix-core families keep slot order, which
+    // measured as fast); the pair rows keep their slot order. Thread r writes the jobs of the slot ranked r; tiles and
+    // pre-pass items are prefix sums in that order. (first and taken are free once the rows are placed.)
+    const bool by_count = sa.GU.kind == MOE_FAM_MV || sa.DN.kind == MOE_FAM_MV;
+    if (by_count && tid < U) first[tid] = c_me;
+    lds_sync();
+    if (tid < U) {
+        int rank = tid;
+        if (by_count) {
+            rank = 0;
+            for (int v = 0; v < U; v++) {
+                const int cv = first[v];
+                rank += (cv > c_me || (cv == c_me && v < tid)) ? 1 : 0;
+            }
+        }
+        taken[rank] = tid;
+    }
+    lds_sync();
+    const int u = tid < U ? taken[tid] : tid;   // the slot whose jobs this thread writes, at position tid
     const bool real = u < U;
-    const int c = c_me, s0 = real ? ustart[u] : 0;
+    const int uexp = real ? uex[u] : 0;
+    const int c = real ? cnt[uexp] : 0, s0 = real ? ustart[u] : 0;
+    const uint8_t *wg_u = pg[uexp], *wu_u = pu[uexp], *wd_u = pd[uexp];
     const int ff = A.ff, n = A.n;
     for (int prod = 0; prod < 2; prod++) {   // 0: gate/up, 1: down
         const MoeFamily &F = prod ? sa.DN : sa.GU;
@@ -446,15 +465,15 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
             w0 = sc.z;
         }
         const int t0 = tiles, i0 = items;
-        const uint8_t *wsrc = prod ? wdown : wgate;
+        const uint8_t *wsrc = prod ? wd_u : wg_u;
         if (F.kind == MOE_FAM_MV) {
             MvJob *jobs = static_cast<MvJob *>(prod ? A.dn_jobs : A.gu_jobs);
             const int end = njob * U * F.mv_tiles;
-            if (u < A.umax)
+            if (tid < A.umax)
                 for (int g = 0; g < njob; g++) {
                     MvJob J = F.mv;
                     if (real) {
-                        J.W = g ? wup : wsrc;
+                        J.W = g ? wu_u : wsrc;
                         if (prod) {
                             J.act = A.ha + (size_t)s0 * A.hstride;
                             J.arow = nullptr;
@@ -466,13 +485,13 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
                         }
                         J.na = c;
                         J.nt = min(J.nt, c >= 3 ? 4 : c);   // the planner's width for c activations, within the LDS sizing
-                        J.tile0 = (njob * u + g) * F.mv_tiles;
+                        J.tile0 = (njob * tid + g) * F.mv_tiles;
                     } else {   // empty: the template's valid pointers, no rows, no activations, after the last real tile
                         J.na = 0;
                         J.r0 = J.r1 = 0;
                         J.tile0 = end;
                     }
-                    jobs[njob * u + g] = J;
+                    jobs[njob * tid + g] = J;
                 }
             if (tid == 0) {   // the sentinel
                 MvJob J = F.mv;
@@ -483,11 +502,11 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
             }
         } else if (F.kind == MOE_FAM_MX) {
             MkJob *jobs = static_cast<MkJob *>(prod ? A.dn_jobs : A.gu_jobs);
-            if (u < A.umax)
+            if (tid < A.umax)
                 for (int g = 0; g < njob; g++) {
                     MkJob J = F.mk;
                     if (real) {
-                        J.W = g ? wup : wsrc;
+                        J.W = g ? wu_u : wsrc;
                         J.act = prod ? A.ha + (size_t)s0 * A.hstride : A.x;
                         J.arow = prod ? nullptr : A.tok_of + s0;
                         J.y = prod ? A.bye + (size_t)s0 * n : A.bgu + (size_t)s0 * 2 * ff + (size_t)g * ff;
@@ -500,7 +519,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
                         J.ntok_tiles = 1;
                         J.tile0 = tot_tiles;
                     }
-                    jobs[njob * u + g] = J;
+                    jobs[njob * tid + g] = J;
                 }
             if (tid == 0) {
                 MkJob J = F.mk;
@@ -514,7 +533,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
             MmJob *jobs = static_cast<MmJob *>(prod ? A.dn_jobs : A.gu_jobs);
             PrepJob *pj = prod ? A.dn_prep : A.gu_prep;
             uint8_t *ws = prod ? A.dn_ws : A.gu_ws;
-            if (u < A.umax) {
+            if (tid < A.umax) {
                 const int na_pad = ntok * F.bn;
                 uint8_t *xq = ws + (size_t)w0 * 256;
                 uint8_t *xm = xq + ((size_t)F.pj.nbk * na_pad * 256 + 255) / 256 * 256;
@@ -531,11 +550,11 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
                     P.na = P.na_pad = 0;
                     P.start = tot_items;
                 }
-                pj[u] = P;
+                pj[tid] = P;
                 for (int g = 0; g < njob; g++) {
                     MmJob J = F.mm;
                     if (real) {
-                        J.W = g ? wup : wsrc;
+                        J.W = g ? wu_u : wsrc;
                         J.xq = xq;
                         J.xm = xm;
                         J.y = prod ? A.bye + (size_t)s0 * n : A.bgu + (size_t)s0 * 2 * ff + (size_t)g * ff;
@@ -549,7 +568,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
                         J.ntok_tiles = 1;
                         J.tile0 = tot_tiles;
                     }
-                    jobs[njob * u + g] = J;
+                    jobs[njob * tid + g] = J;
                 }
             }
             if (tid == 0) {
