@@ -39,6 +39,10 @@ struct MvJob {
     int nt;               // activations per pass (1, 2 or 4): the launch's, or this job's in a launch of mixed widths
 };
 
+// Floats per row of the decode kernel's LDS terms (nbk blocks, nt activations): the K-quants' 2 per (block, activation)
+// plus one, so the pitch is odd; the 32-element formats' 9 per (block, activation).
+__host__ __device__ constexpr int mv_row_pitch(bool w32, int nbk, int nt) { return w32 ? nbk * nt * 9 : nbk * nt * 2 + 1; }
+
 // One launch of the decode kernel: format, activations per pass (0: each job's own), waves per workgroup, workgroups,
 // LDS bytes.
 struct MvLaunch {

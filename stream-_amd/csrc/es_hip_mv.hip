@@ -539,6 +539,10 @@ __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
     const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
     const int cmode = W32 ? (x86 ? CH_LANES : CH_MULADD) : (contract ? CH_FMA : CH_MULADD);
     constexpr int CW = W32 ? 9 : 2;   // floats per (row, block, activation) in LDS
+    // LDS row pitch of the terms, [row][block][activation][CW]: odd for the K-quants, whose chains take one row per lane,
+    // so consecutive rows' terms sit in consecutive banks (an even pitch of 16 or 64 floats put every row of a wave in one
+    // or two banks)
+    const int P = mv_row_pitch(W32, nbk, NT);
     extern __shared__ float lds[];
 
     typename L::Raw raw[U];
@@ -606,7 +610,7 @@ __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
                                 if (t < nt) { v[t].dot = group_sum<LPB>(v[t].dot); v[t].aux = group_sum<LPB>(v[t].aux); }
                         }
                         if (ok[u] && k == 0) {
-                            float *e = lds + ((size_t)(row - ra) * nbk + b) * NT * CW;
+                            float *e = lds + (size_t)(row - ra) * P + (size_t)b * NT * CW;
                             if constexpr (W32) {
 #pragma unroll
                                 for (int t = 0; t < NT; t++) {
@@ -648,8 +652,21 @@ __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
             const int nrow = rb - ra;
             const int per = cmode == CH_LANES ? 8 : 1;
             for (int idx = tid; idx < nrow * nt * per; idx += WAVE * W) {
-                const int i = idx % per, t = (idx / per) % nt, rl = idx / (per * nt);
-                const float *e = lds + (size_t)rl * nbk * NT * CW + t * CW;
+                // K-quants: rows fastest (consecutive lanes read consecutive banks through the odd pitch); 32-element
+                // formats: a row's eight AVX2 chains (per = 8) in consecutive lanes, then activations, then rows
+                int i, t, rl;
+                if constexpr (!W32) {
+                    i = 0;
+                    t = 0;
+#pragma unroll
+                    for (int q = 1; q < NT; q++) t += idx >= q * nrow ? 1 : 0;   // idx / nrow for idx < NT * nrow
+                    rl = idx - t * nrow;
+                } else {
+                    i = idx % per;
+                    t = (idx / per) % nt;
+                    rl = idx / (per * nt);
+                }
+                const float *e = lds + (size_t)rl * P + t * CW;
                 const int oa = cmode == CH_LANES ? 1 + i : 0, ob = cmode == CH_LANES ? 0 : 1;
                 float s = 0.0f;
                 int bb = 0;

@@ -149,7 +149,8 @@ int check_req(const Req &q, const FmtInfo &f) {
     const int nbk = q.cols / f.be;
     // the decode kernel keeps one row's float terms in LDS (at one activation per pass: 9 floats per block for the
     // 32-element formats, 2 per superblock for the K-quants)
-    static_assert((size_t)ES_HIP_MAX_COLS_32 / 32 * 9 * 4 <= LDS_MAX && (size_t)ES_HIP_MAX_COLS_256 / 256 * 2 * 4 <= LDS_MAX,
+    static_assert((size_t)esq::mv_row_pitch(true, ES_HIP_MAX_COLS_32 / 32, 1) * 4 <= LDS_MAX &&
+                  (size_t)esq::mv_row_pitch(false, ES_HIP_MAX_COLS_256 / 256, 1) * 4 <= LDS_MAX,
                   "the header's row limits fit one row's terms");
     const int cmax = f.be == 32 ? ES_HIP_MAX_COLS_32 : ES_HIP_MAX_COLS_256;
     if (q.cols > cmax)
@@ -205,7 +206,7 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
         // activations per pass: 3 in one pass of 4 rather than two passes of 2; at most what keeps one row's terms in LDS.
         // Jobs of different counts (an MoE layer's experts) each take their own width in one launch of mixed widths.
         int nt_cap = 4;
-        while (nt_cap > 1 && (size_t)max_nbk * nt_cap * (w32 ? 9 : 2) * sizeof(float) > LDS_MAX) nt_cap /= 2;
+        while (nt_cap > 1 && (size_t)esq::mv_row_pitch(w32, max_nbk, nt_cap) * sizeof(float) > LDS_MAX) nt_cap /= 2;
         auto nt_of = [&](int na) { return std::min(nt_cap, na >= 3 ? 4 : std::max(na, 1)); };
         bool mixed = false;
         for (const Req *q : kv.second) mixed = mixed || nt_of(q->na) != nt_of(kv.second[0]->na);
@@ -214,13 +215,12 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
         g.L.waves = waves;
         int tile = 0;
         size_t lds = 0;
-        const int cw = w32 ? 9 : 2;
         for (const Req *q : kv.second) {
             const int nbk = q->cols / f.be, rows = q->r1 - q->r0, nt = nt_of(q->na);
             const int rpi = nbk <= slots ? slots / nbk : 1;
             const int seg = segments(nbk, slots);
             const int rstep = std::max(1, waves / seg) * rpi;   // rows one pass of the workgroup covers
-            const size_t per_row = (size_t)nbk * nt * cw * sizeof(float);
+            const size_t per_row = (size_t)esq::mv_row_pitch(w32, nbk, nt) * sizeof(float);
             if (per_row > LDS_MAX) return fail(ES_HIP_EINVAL, "type %u cols %d: a row needs %zu bytes of LDS", q->type, q->cols, per_row);
             int chain_cap = (int)std::min<size_t>(CHAIN_MAX, std::max<size_t>(1, LDS_TARGET / per_row));
             if (chain_cap >= rstep) chain_cap -= chain_cap % rstep;
