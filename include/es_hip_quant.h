@@ -317,10 +317,15 @@ int es_hip_set_batched32_direct(int on);
  * are identical either way. Returns the previous setting. */
 int es_hip_set_q6k_persistent(int on);
 /* Q4_K and Q3_K products that take the direct-activation kernel and have an even number (at least 2) of superblocks per
- * row, with no gathered activations, run, with on != 0 (the default), in one persistent launch per format: two
- * workgroups per CU, each computing a host-scheduled list of tiles (64 rows x 128 or 64 activations) with its loads
- * running ahead across tile boundaries. Q4_K products of this kind then take it at any tile count (config 2's 2048 x 8192
- * down product shares the launch with gate and up). Results are identical either way. Returns the previous setting. */
+ * row, with no gathered activations, run, with on != 0, in one persistent launch per format, each workgroup computing a
+ * host-scheduled list of tiles with its loads running ahead across tile boundaries, in one of two forms: two workgroups
+ * per CU (tiles of 64 rows x 128 or 64 activations), or, for Q4_K, one workgroup of 8 waves per CU (tiles of 64 rows x
+ * 128 activations; four waves stage the activations and the unpacked weights in LDS for the four that run the matrix
+ * cores). on = 1 (the default) picks the second form for Q4_K launches of at least 4 tiles of 128 activations per CU
+ * (config 2's three prefill products in one launch), the first otherwise; on = 2 takes the second for every Q4_K
+ * launch, on = 3 the first for every launch. Q4_K products of this kind take the persistent launch at any tile count
+ * (config 2's 2048 x 8192 down product shares the launch with gate and up). Results are identical in every form.
+ * Returns the previous setting. */
 int es_hip_set_direct_persistent(int on);
 /* Q5_K and Q3_K products on the direct-activation kernel that would have fewer than 256 tiles of 64 rows x 128
  * activations run, with on != 0 (the default) and at least 64 activations, in tiles of 64 activations (twice the

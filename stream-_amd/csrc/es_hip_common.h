@@ -153,6 +153,8 @@ static_assert(sizeof(PkTile) == 64, "tile records are copied into LDS as 16-byte
 constexpr int PK_MAX_TILES = 48;   // tiles per workgroup (their records sit in LDS beside the ring: 80 KB a workgroup)
 // workgroups [0, g64) take the tiles of 64 activations, the rest those of 128
 hipError_t pk_launch(int type, const PkTile *tiles, const int *wgptr, int grid, int g64, int order, hipStream_t s);
+// The wave-specialised form (Q4_K): one workgroup of 8 waves per CU, tiles of 128 activations only.
+hipError_t ws_launch(int type, const PkTile *tiles, const int *wgptr, int grid, int order, hipStream_t s);
 
 // One activation pre-pass: kind 0 writes 16 bytes of meta per activation and superblock (pair sums of the Q4_K
 // sub-blocks, low | high bytes), kind 1 32 bytes (the 16 bsums, low | high bytes), kind 2 32 bytes (the 16 bsums as

@@ -795,6 +795,314 @@ __global__ __launch_bounds__(256, 2) void pk_kernel(const PkTile *__restrict__ t
     else pk_body<F, CONTRACT, false>(tiles, k0, nt, smem);
 }
 
+// ---- the wave-specialised persistent form (Q4_K) ------------------------------------------------------------------------
+// One workgroup of 8 waves per CU runs a host-scheduled list of tiles (64 rows x 128 activations) as a stream of items
+// (tile, superblock), as pk_body does, but splits each item's work by kind over the waves of a SIMD:
+//   waves 0-3 (matrix waves): wave m reads the B operands of rows 16m .. 16m+15 from LDS and runs the item's 8 tile steps
+//     (72 MFMAs and the float epilogue of the tiles two steps back) and the tile's stores, as pk_body does;
+//   waves 4-7 (staging waves): wave 4 + u loads a quarter of the item's activations (values, scales, bsums) and the
+//     weights of rows 16u .. 16u+15 into registers three items ahead, and one item ahead writes them into LDS: the values
+//     swizzled as in mk_kernel, the bsums converted to halves, the weights unpacked into the B operands (build_b).
+// The unpacking and the loads then run beside the matrix work on every SIMD instead of between its tile steps. Every
+// load is an ordinary (compiler-counted) buffer load into registers, so no wait drains loads issued after the ones it
+// needs. LDS: two activation slots and two B-operand slots (item i in slots i & 1) and the tile records; one barrier per
+// item: at barrier i, item i's slots are complete and item i - 1's are free.
+struct WsGeom {
+    using SL = MkSlot<128>;
+    static constexpr uint32_t ACT = SL::BYTES;            // an activation slot (the 128-activation layout of mk_kernel)
+    static constexpr uint32_t PLT = 9 * 1024;             // one row tile's B operands: 9 chunks of 16 bytes per lane
+    static constexpr uint32_t PLS = 4 * PLT;              // a B-operand slot: 4 row tiles
+    static constexpr uint32_t PL0 = 2 * ACT, REC0 = PL0 + 2 * PLS;
+    static constexpr uint32_t BYTES = REC0 + PK_MAX_TILES * sizeof(PkTile);
+    static_assert(BYTES <= 160 * 1024, "the workgroup fits a CU's LDS");
+};
+
+struct WsRec {   // a tile record in scalar registers
+    const uint8_t *w, *act;
+    float *y;
+    uint32_t astride, ystride4, row_bytes;
+    int nbk, tok0, na, rows, ntok;
+};
+__device__ __forceinline__ WsRec ws_rec(uint32_t rec0, int k) {
+    const uint32_t a = rec0 + (uint32_t)k * (uint32_t)sizeof(PkTile);
+    const u32x4 v0 = lds_ld<u32x4>(a), v1 = lds_ld<u32x4>(a + 16), v2 = lds_ld<u32x4>(a + 32), v3 = lds_ld<u32x4>(a + 48);
+    auto u = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
+    auto p = [&](uint32_t lo, uint32_t hi) { return (uint64_t)u(lo) | (uint64_t)u(hi) << 32; };
+    WsRec r;
+    r.w = reinterpret_cast<const uint8_t *>(p(v0.x, v0.y));
+    r.act = reinterpret_cast<const uint8_t *>(p(v0.z, v0.w));
+    r.y = reinterpret_cast<float *>(p(v1.x, v1.y));
+    r.astride = u(v1.z);
+    r.ystride4 = u(v1.w);
+    r.row_bytes = u(v2.x);
+    r.nbk = (int)u(v2.y);
+    r.tok0 = (int)u(v2.w);
+    r.na = (int)u(v3.x);
+    r.rows = (int)u(v3.y);
+    r.ntok = (int)u(v3.z);
+    return r;
+}
+
+// the matrix waves (m = 0 .. 3)
+template <int F, bool CONTRACT>
+__device__ __forceinline__ void ws_matrix(uint8_t *smem, int nt, int nitems, int m) {
+    using G = WsGeom;
+    using SL = MkSlot<128>;
+    constexpr bool FUSED = CONTRACT;
+    const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+    const uint32_t smem0 = lds_addr(smem);
+    uint32_t xo[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int nat = 4 * (lg >> 1) + 8 * (s >> 1) + 2 * (s & 1) + (lg & 1);
+        xo[s] = SL::QS + lr * TROW + 16 * (nat ^ lr);
+    }
+    const uint32_t bso = SL::BS + lg * (128 * 8) + lr * 8, ydo = SL::D + 16 * lg;
+    auto aload = [&](const uint32_t (&xa)[4], uint32_t ba, uint32_t ya, int tt, AOps &A) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) A.x[s] = lds_ld<v4i>(xa[s] + 16 * TROW * tt);
+        A.bs = lds_ld<v4h>(ba + 128 * tt);
+        A.yd = lds_ld<v4f>(ya + 64 * tt);
+    };
+    v4f acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) acc[t] = v4f{0, 0, 0, 0};
+    Pend<F> p0, p1;
+    p0.m = MAcc<F>{};
+    p0.yd = v4f{0, 0, 0, 0};
+    p0.d = p0.dm = 0.f;
+    p1 = p0;
+    const Pend<F> pzero = p0;
+    auto flush = [&](const WsRec &r) {   // as pk_body's: the pending epilogues, the stores, the accumulators cleared
+        epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[6]);
+        epilogue<F, FUSED>(p1.m, p1.d, p1.dm, p1.yd, acc[7]);
+        p0 = pzero;
+        p1 = pzero;
+        const int row = 16 * m + lr;
+        const uint32_t yrange = (uint32_t)(r.ntok - 1) * r.ystride4 + 4u * (uint32_t)r.rows;
+        const __amdgpu_buffer_rsrc_t yrsrc = __builtin_amdgcn_make_buffer_rsrc((void *)r.y, (short)0, (int)yrange, 0x00020000);
+        uint32_t yoff = row < r.rows ? (uint32_t)(4 * lg) * r.ystride4 + 4u * (uint32_t)row : 0x80000000u;
+#pragma unroll
+        for (int tt = 0; tt < 8; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float v = acc[tt][i];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrsrc, (int)yoff, 0, 0);
+                yoff += i < 3 ? r.ystride4 : 13 * r.ystride4;
+            }
+#pragma unroll
+        for (int t = 0; t < 8; t++) acc[t] = v4f{0, 0, 0, 0};
+    };
+    int k = 0, j = 0;
+    WsRec rc = ws_rec(smem0 + G::REC0, 0);
+    for (int i = 0; i < nitems; i++) {
+        lds_sync();   // item i's slots are complete
+        const uint32_t so = (uint32_t)(i & 1) * G::ACT;
+        const uint32_t pb = smem0 + G::PL0 + (uint32_t)(i & 1) * G::PLS + (uint32_t)m * G::PLT + 16u * (uint32_t)lane;
+        BOps<F> B;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            B.lo[s] = lds_ld<v4i>(pb + 1024 * s);
+            B.hi[s] = lds_ld<v4i>(pb + 1024 * (4 + s));
+        }
+        {
+            const u32x4 x = lds_ld<u32x4>(pb + 8192);
+            B.mn = __builtin_bit_cast(v4h, u32x2{x.x, x.y});
+            B.d = __uint_as_float(x.z);
+            B.dm = __uint_as_float(x.w);
+        }
+        const uint32_t xa[4] = {smem0 + so + xo[0], smem0 + so + xo[1], smem0 + so + xo[2], smem0 + so + xo[3]};
+        const uint32_t ba = smem0 + so + bso, ya = smem0 + so + ydo;
+        AOps A[2];
+        aload(xa, ba, ya, 0, A[0]);
+        __builtin_amdgcn_sched_barrier(0);   // every operand of the item's first step requested before its first MFMA
+#pragma unroll
+        for (int tt = 0; tt < 8; tt++) {
+            if (tt + 1 < 8) aload(xa, ba, ya, tt + 1, A[(tt + 1) & 1]);
+            MAcc<F> cur;
+            mma<F>(A[tt & 1], B, cur);
+            epilogue<F, FUSED>(p0.m, p0.d, p0.dm, p0.yd, acc[(tt + 6) % 8]);
+            p0 = p1;
+            p1.m = cur;
+            p1.yd = A[tt & 1].yd;
+            p1.d = B.d;
+            p1.dm = B.dm;
+            step_schedule<9>();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (++j == rc.nbk) {
+            flush(rc);
+            j = 0;
+            if (++k < nt) rc = ws_rec(smem0 + G::REC0, k);
+        }
+    }
+}
+
+// the staging waves (u = 0 .. 3)
+template <int F>
+__device__ __forceinline__ void ws_stage(uint8_t *smem, int nt, int nitems, int u) {
+    using G = WsGeom;
+    using SL = MkSlot<128>;
+    using FM = MkFmt<F>;
+    const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+    const uint32_t smem0 = lds_addr(smem);
+    struct Set {   // one item's loads: 8 value chunks (activations 32u + 4c + lane/16), the scale (activation 32u + lane %
+                   // 32), 8 bsums (activation 32u + lane/2, half lane & 1), the weights' header and two qs chunks
+        u32x4 q[8], bs, h, q0, q1;
+        uint32_t d;
+    };
+    struct LTile {   // the load stream's tile: buffer resources and per-lane offsets
+        __amdgpu_buffer_rsrc_t ar, wr;
+        uint32_t q[8], bs, d, wo;
+        int nbk;
+    };
+    auto ltile = [&](int k) {
+        const WsRec r = ws_rec(smem0 + G::REC0, k);
+        LTile t;
+        t.ar = __builtin_amdgcn_make_buffer_rsrc((void *)r.act, (short)0, (int)0xffffffffu, 0x00020000);
+        t.wr = __builtin_amdgcn_make_buffer_rsrc((void *)r.w, (short)0, (int)0xffffffffu, 0x00020000);
+        auto act_off = [&](int a) { return (uint32_t)min(r.tok0 + a, r.na - 1) * r.astride; };
+#pragma unroll
+        for (int c = 0; c < 8; c++) t.q[c] = act_off(32 * u + 4 * c + (lane >> 4)) + 4 + 16 * (lane & 15);
+        t.bs = act_off(32 * u + (lane >> 1)) + 260 + 16 * (lane & 1);
+        t.d = act_off(32 * u + (lane & 31));
+        t.wo = (uint32_t)min(16 * u + lr, r.rows - 1) * r.row_bytes;
+        t.nbk = r.nbk;
+        return t;
+    };
+    auto ld_value = [&](const LTile &t, int j, int c) {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(t.ar, (int)t.q[c], 292 * j, 0));
+    };
+    auto ld_scales = [&](const LTile &t, int j, Set &S) {
+        S.bs = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(t.ar, (int)t.bs, 292 * j, 0));
+        S.d = __builtin_amdgcn_raw_buffer_load_b32(t.ar, (int)t.d, 292 * j, 0);
+    };
+    auto ld_weights = [&](const LTile &t, int j, Set &S) {
+        const int sw = FM::BB * j;
+        S.h = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(t.wr, (int)t.wo, sw, 0));
+        S.q0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(t.wr, (int)(t.wo + FM::QS + 16 * lg), sw, 0));
+        S.q1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(t.wr, (int)(t.wo + FM::QS + 64 + 16 * lg), sw, 0));
+    };
+    // LDS destinations within a slot: value chunk c of activation a = 32u + 4c + lane/16 at row a, position
+    // (lane % 16) ^ (a & 15); the scale at D + 4a (lanes 32-63 repeat lanes 0-31); the bsums' halves as mk_kernel lays
+    // them out ([lg][activation][4]); this row tile's B operands at chunk c, 16 bytes per lane
+    uint32_t qd[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const int a = 32 * u + 4 * c + (lane >> 4);
+        qd[c] = SL::QS + (uint32_t)a * TROW + 16u * (uint32_t)((lane & 15) ^ (a & 15));
+    }
+    const uint32_t dd = SL::D + 4u * (uint32_t)(32 * u + (lane & 31));
+    const uint32_t bd = SL::BS + (uint32_t)(2 * (lane & 1)) * (128 * 8) + (uint32_t)(32 * u + (lane >> 1)) * 8;
+    const uint32_t pd = G::PL0 + (uint32_t)u * G::PLT + 16u * (uint32_t)lane;
+    auto put_value = [&](const Set &S, int slot, int c) {
+        *reinterpret_cast<u32x4 *>(smem + (uint32_t)slot * G::ACT + qd[c]) = S.q[c];
+    };
+    auto put_scales = [&](const Set &S, int slot) {
+        uint8_t *ab = smem + (uint32_t)slot * G::ACT;
+        *reinterpret_cast<uint32_t *>(ab + dd) = S.d;
+        const uint32_t w[4] = {S.bs.x, S.bs.y, S.bs.z, S.bs.w};
+        uint32_t hv[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {   // two int16 bsums -> two halves (exact: |bsums| <= 16 * 127)
+            const _Float16 e0 = (_Float16)(int16_t)(w[c] & 0xffffu), e1 = (_Float16)(int16_t)(w[c] >> 16);
+            hv[c] = (uint32_t)__builtin_bit_cast(uint16_t, e0) | (uint32_t)__builtin_bit_cast(uint16_t, e1) << 16;
+        }
+        *reinterpret_cast<uint2 *>(ab + bd) = make_uint2(hv[0], hv[1]);
+        *reinterpret_cast<uint2 *>(ab + bd + 128 * 8) = make_uint2(hv[2], hv[3]);
+    };
+    auto put_operands = [&](const Set &S, int slot) {
+        WRaw<F> wr;
+        wr.h = make_uint4(S.h.x, S.h.y, S.h.z, S.h.w);
+        wr.q0 = make_uint4(S.q0.x, S.q0.y, S.q0.z, S.q0.w);
+        wr.q1 = make_uint4(S.q1.x, S.q1.y, S.q1.z, S.q1.w);
+        BOps<F> B;
+        build_b<F>(wr, lg, B);
+        uint8_t *pb = smem + pd + (uint32_t)slot * G::PLS;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            *reinterpret_cast<v4i *>(pb + 1024 * s) = B.lo[s];
+            *reinterpret_cast<v4i *>(pb + 1024 * (4 + s)) = B.hi[s];
+        }
+        const u32x2 mn = __builtin_bit_cast(u32x2, B.mn);
+        *reinterpret_cast<u32x4 *>(pb + 8192) = u32x4{mn.x, mn.y, __float_as_uint(B.d), __float_as_uint(B.dm)};
+    };
+    // the load stream: item (lk, lj); past the last item it repeats the last (loads into a set nobody writes out)
+    int lk = 0, lj = 0;
+    LTile lt = ltile(0);
+    auto advance = [&]() {
+        if (lj + 1 < lt.nbk) {
+            lj++;
+        } else if (lk + 1 < nt) {
+            lk++;
+            lj = 0;
+            lt = ltile(lk);
+        }
+    };
+    auto issue = [&](Set &S) {
+#pragma unroll
+        for (int c = 0; c < 8; c++) S.q[c] = ld_value(lt, lj, c);
+        ld_scales(lt, lj, S);
+        ld_weights(lt, lj, S);
+        advance();
+    };
+    Set S0, S1, S2;
+    issue(S0);
+    issue(S1);
+    issue(S2);
+#pragma unroll
+    for (int c = 0; c < 8; c++) put_value(S0, 0, c);
+    put_scales(S0, 0);
+    put_operands(S0, 0);
+    // item i: the loads of item i + 3 into the set item i used, interleaved with the writes of item i + 1 into slots
+    // (i + 1) & 1 (one value load, one value write; the scales; the weights; the unpacking), so the loads enter the memory
+    // pipeline a few at a time instead of in one burst that stalls the wave
+    auto period = [&](Set &Sl, const Set &Sp, int i) {
+        lds_sync();
+        const int sl = (i + 1) & 1;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            Sl.q[c] = ld_value(lt, lj, c);
+            __builtin_amdgcn_sched_barrier(0);
+            put_value(Sp, sl, c);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        ld_scales(lt, lj, Sl);
+        __builtin_amdgcn_sched_barrier(0);
+        put_scales(Sp, sl);
+        __builtin_amdgcn_sched_barrier(0);
+        ld_weights(lt, lj, Sl);
+        __builtin_amdgcn_sched_barrier(0);
+        put_operands(Sp, sl);
+        advance();
+    };
+    int i = 0;
+    for (; i + 3 <= nitems; i += 3) {
+        period(S0, S1, i);
+        period(S1, S2, i + 1);
+        period(S2, S0, i + 2);
+    }
+    if (i < nitems) period(S0, S1, i++);
+    if (i < nitems) period(S1, S2, i++);
+}
+
+template <int F, bool CONTRACT>
+__global__ __launch_bounds__(512, 1) void ws_kernel(const PkTile *__restrict__ tiles, const int *__restrict__ wgptr) {
+    using G = WsGeom;
+    __shared__ __align__(16) uint8_t smem[G::BYTES];
+    const int k0 = wgptr[blockIdx.x], nt = wgptr[blockIdx.x + 1] - k0;
+    if (nt <= 0) return;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < nt * (int)(sizeof(PkTile) / 16); i += 512)
+        *reinterpret_cast<uint4 *>(smem + G::REC0 + 16 * i) = ldg<uint4>(reinterpret_cast<const uint8_t *>(tiles + k0) + 16 * i);
+    __syncthreads();
+    int nitems = 0;   // every wave counts the items (tile records in LDS, read as scalars)
+    for (int k = 0; k < nt; k++) nitems += ws_rec(lds_addr(smem) + G::REC0, k).nbk;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wave < 4) ws_matrix<F, CONTRACT>(smem, nt, nitems, wave);
+    else ws_stage<F>(smem, nt, nitems, wave - 4);
+}
+
 }  // namespace
 
 template <int F, int T>
@@ -832,6 +1140,15 @@ template <int F>
 static void pk_launch_fmt(bool contract, const PkTile *tiles, const int *wgptr, int grid, int g64, hipStream_t s) {
     if (contract) hipLaunchKernelGGL((pk_kernel<F, true>), dim3(grid), dim3(256), 0, s, tiles, wgptr, g64);
     else hipLaunchKernelGGL((pk_kernel<F, false>), dim3(grid), dim3(256), 0, s, tiles, wgptr, g64);
+}
+
+hipError_t ws_launch(int type, const PkTile *tiles, const int *wgptr, int grid, int order, hipStream_t s) {
+    if (type != ES_HIP_Q4_K) return hipErrorInvalidValue;
+    if (order == ES_HIP_ORDER_X86_CONTRACT)
+        hipLaunchKernelGGL((ws_kernel<ES_HIP_Q4_K, true>), dim3(grid), dim3(512), 0, s, tiles, wgptr);
+    else
+        hipLaunchKernelGGL((ws_kernel<ES_HIP_Q4_K, false>), dim3(grid), dim3(512), 0, s, tiles, wgptr);
+    return hipGetLastError();
 }
 
 hipError_t pk_launch(int type, const PkTile *tiles, const int *wgptr, int grid, int g64, int order, hipStream_t s) {

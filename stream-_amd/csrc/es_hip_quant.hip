@@ -330,6 +330,7 @@ struct PkGroup {
     std::vector<esq::PkTile> tiles;   // in workgroup order
     std::vector<int> wgptr;           // grid + 1 entries: workgroup g takes tiles[wgptr[g] .. wgptr[g + 1])
     int grid = 0, g64 = 0;            // workgroups [0, g64) take the 64-wide tiles
+    bool ws = false;                  // the wave-specialised form (Q4_K): one workgroup per CU, 128-wide tiles only
     size_t off = 0;                   // byte offset of the tiles in the device image; wgptr follows them
 };
 
@@ -438,7 +439,10 @@ bool mk_eligible(const Req &q) {
            ((size_t)q.na + esq::MK_TOK) * mk_ystride(q) * sizeof(float) < ((size_t)1 << 31);
 }
 
-std::atomic<int> g_pk_on{1};   // the persistent direct kernel (0: products take the per-tile launches)
+// the persistent direct kernel: 0 off (products take the per-tile launches), 1 automatic (Q4_K launches of at least 4
+// tiles of 64 rows x 128 activations per CU take the wave-specialised form, others the two-workgroup form), 2 the
+// wave-specialised form for every Q4_K launch, 3 the two-workgroup form for every launch
+std::atomic<int> g_pk_on{1};
 std::atomic<uint64_t> g_cfg_gen{0};   // bumped by every setting that changes how a batch is planned
 
 // The persistent direct kernel: Q4_K / Q3_K products that the direct kernels take (at least g_mk_min / g_mk3_min
@@ -467,8 +471,33 @@ double pk_cost(int nbk, bool t64) { return nbk * (t64 ? 0.6 : 1.0) + 1.0; }
 // each set, all tiles of a row tile go to one XCD (workgroup g runs on XCD g % 8: its L2 reads the row tile's weights
 // once), row tiles are spread over the XCDs and tiles over an XCD's workgroups longest first, each to the least loaded.
 // Returns false when some workgroup would get more than PK_MAX_TILES tiles.
+// The form of a persistent launch: the wave-specialised kernel (one workgroup per CU, 128-wide tiles) measured faster
+// on config 2's three products in one launch (1152 tiles: 75-77 us against 85-86 us), even with gate and up alone (1024
+// tiles), and slower when the tiles leave CUs idle (the down product alone, 128 tiles: 47 us against 37 us).
+bool pk_ws(const PkGroup &g, int cus) {
+    const int on = g_pk_on.load();
+    if (g.type != ES_HIP_Q4_K || on == 3) return false;
+    if (on == 2) return true;
+    long tiles = 0;
+    for (const PkGroup::Prod &p : g.prods)
+        tiles += (long)((p.r1 - p.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS) * ((p.na + 127) / 128);
+    return tiles >= 4L * std::max(cus, 8);
+}
+
+bool pk_schedule_form(PkGroup &g, int cus);
+
+// Schedules a persistent launch in the form pk_ws picks; a wave-specialised schedule with too many tiles for some
+// workgroup falls back to the two-workgroup form (twice the workgroups).
 bool pk_schedule(PkGroup &g, int cus) {
-    const int G = 2 * std::max(cus, 8) / 8 * 8;
+    g.ws = pk_ws(g, cus);
+    if (pk_schedule_form(g, cus)) return true;
+    if (!g.ws) return false;
+    g.ws = false;
+    return pk_schedule_form(g, cus);
+}
+
+bool pk_schedule_form(PkGroup &g, int cus) {
+    const int G = (g.ws ? 1 : 2) * std::max(cus, 8) / 8 * 8;
     struct Tl { int p, rt, t0, nt; bool t64; double c; };
     std::vector<Tl> v128, v64;
     double mean = 0;
@@ -478,7 +507,7 @@ bool pk_schedule(PkGroup &g, int cus) {
     for (int pi = 0; pi < (int)g.prods.size(); pi++) {
         const PkGroup::Prod &p = g.prods[pi];
         const int rts = (p.r1 - p.r0 + esq::MK_ROWS - 1) / esq::MK_ROWS;
-        const bool t64 = p.na <= 64 || pk_cost(p.nbk, false) > mean;
+        const bool t64 = !g.ws && (p.na <= 64 || pk_cost(p.nbk, false) > mean);
         const int T = t64 ? 64 : 128;
         for (int rt = 0; rt < rts; rt++)
             for (int t0 = 0; t0 < p.na; t0 += T)
@@ -989,7 +1018,9 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
         if (!tables) return fail(ES_HIP_EINVAL, "the persistent kernel needs its tile tables on the device");
         const esq::PkTile *tl = reinterpret_cast<const esq::PkTile *>(tables + g.off);
         const int *wp = reinterpret_cast<const int *>(tables + g.off + align256(g.tiles.size() * sizeof(esq::PkTile)));
-        if ((e = esq::pk_launch(g.type, tl, wp, g.grid, g.g64, order, s)) != hipSuccess) return hip_fail(e, "matrix-core launch");
+        if ((e = g.ws ? esq::ws_launch(g.type, tl, wp, g.grid, order, s) : esq::pk_launch(g.type, tl, wp, g.grid, g.g64, order, s)) !=
+            hipSuccess)
+            return hip_fail(e, "matrix-core launch");
     }
     for (const MkGroup &g : bt.mkg) {
         const esq::MkJob *dj = tables ? reinterpret_cast<const esq::MkJob *>(tables + g.off) : nullptr;
@@ -1537,7 +1568,10 @@ int es_hip_set_direct_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_m
 int es_hip_set_direct_mfma_min_tiles(int n) { g_cfg_gen.fetch_add(1); return g_mk_min_tiles.exchange(n); }
 int es_hip_set_q5k_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_mk5_min.exchange(n); }
 int es_hip_set_q3k_mfma_min_batch(int n) { g_cfg_gen.fetch_add(1); return g_mk3_min.exchange(n); }
-int es_hip_set_direct_persistent(int on) { g_cfg_gen.fetch_add(1); return g_pk_on.exchange(on ? 1 : 0); }
+int es_hip_set_direct_persistent(int on) {
+    g_cfg_gen.fetch_add(1);
+    return g_pk_on.exchange(on == 2 || on == 3 ? on : on ? 1 : 0);
+}
 int es_hip_set_q2k_expert_max_batch(int n) { g_cfg_gen.fetch_add(1); return g_mx_max.exchange(n); }
 int es_hip_set_batched32_direct(int on) { g_cfg_gen.fetch_add(1); return g_mbx_on.exchange(on ? 1 : 0); }
 int es_hip_set_q6k_persistent(int on) { g_cfg_gen.fetch_add(1); return esq::mm6_set_persistent(on); }

@@ -1,10 +1,12 @@
-"""GPU parity of the persistent direct-activation kernel (es_hip_mk.hip, pk_kernel): Q4_K and Q3_K products of an even
-number of superblocks share one launch whose workgroups each compute a host-scheduled list of tiles (64 rows x 128 or 64
-activations), their loads running ahead across tile boundaries. Checked bit for bit against the oracle (in every
-reference order) and against the same batches with the persistent launch switched off (the per-tile kernels): config 2's
-three prefill products in one launch (64-wide down tiles, 128-wide gate/up tiles, some of them cut in two), mixed row
-lengths and activation counts in one launch, ragged rows and activation counts, row sub-ranges with padded strides,
-batches of at most 64 activations (64-wide tiles only), plans rerun with new inputs, Q3_K."""
+"""GPU parity of the persistent direct-activation kernels (es_hip_mk.hip): Q4_K and Q3_K products of an even number of
+superblocks share one launch whose workgroups each compute a host-scheduled list of tiles, their loads running ahead
+across tile boundaries. Both forms: pk_kernel (two workgroups per CU, tiles of 64 rows x 128 or 64 activations) and, for
+Q4_K, ws_kernel (one workgroup of 8 waves per CU, 128-activation tiles, four waves staging activations and unpacked
+weights in LDS for the four that run the matrix cores). Checked bit for bit against the oracle (in every reference
+order) and against the same batches with the persistent launch switched off (the per-tile kernels): config 2's three
+prefill products in one launch, mixed row lengths and activation counts in one launch, ragged rows and activation counts
+(tiles of fewer than 128 activations), row sub-ranges with padded strides, batches of at most 64 activations, many tiles
+per workgroup, plans rerun with new inputs, Q3_K."""
 import numpy as np
 import pytest
 
@@ -32,10 +34,12 @@ def inputs(orc, t, rows, cols, na, seed, gauss=False):
     return W, orc.quantize_act(t, x)
 
 
-@pytest.fixture
-def hipp(hip):
-    """the persistent launch on (its default), every batch of >= 8 activations eligible"""
-    prev = (hip.set_direct_persistent(1), hip.set_direct_mfma_min_batch(8), hip.set_q3k_mfma_min_batch(8))
+@pytest.fixture(params=[3, 2], ids=["pk", "ws"])
+def hipp(hip, request):
+    """the persistent launch on in one form (3: two workgroups per CU, 2: wave-specialised for Q4_K), every batch of >= 8
+    activations eligible"""
+    hip.pk_form = request.param
+    prev = (hip.set_direct_persistent(request.param), hip.set_direct_mfma_min_batch(8), hip.set_q3k_mfma_min_batch(8))
     yield hip
     hip.set_direct_persistent(prev[0])
     hip.set_direct_mfma_min_batch(prev[1])
@@ -44,8 +48,9 @@ def hipp(hip):
 
 
 def run_batch(hip, prods, persistent):
-    """one run_jobs call over prods = [(type, W, cols, rows, acts, r0, r1, ystride)]; outputs [na][ystride]"""
-    prev = hip.set_direct_persistent(1 if persistent else 0)
+    """one run_jobs call over prods = [(type, W, cols, rows, acts, r0, r1, ystride)] with the fixture's persistent form
+    (or none); outputs [na][ystride]"""
+    prev = hip.set_direct_persistent(hip.pk_form if persistent else 0)
     try:
         specs, outs, keep = [], [], []
         for (t, W, cols, rows, acts, r0, r1, ystride) in prods:
