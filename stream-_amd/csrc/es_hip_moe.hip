@@ -24,33 +24,43 @@ template <typename TAB> __device__ __forceinline__ float swiglu_tab(float g, flo
         if ((i) < 32) tab[(i)] = T_[(i)];             \
     }
 
-// One workgroup of 256 threads per (pair row, 256-wide block): h, amax, the Q8_K block (d, qs, bsums).
-__global__ __launch_bounds__(256) void swiglu_q8k(const float *__restrict__ gu, int ff, uint8_t *__restrict__ ha,
+// One wave per (pair row, 256-wide block), four per workgroup: h, amax, the Q8_K block (d, qs, bsums). Lane l takes
+// elements 4l .. 4l + 3; the maximum (exact in any order) and the bsums (integer sums) by wave reductions, so the only
+// barrier is the one after expf's table.
+__global__ __launch_bounds__(256) void swiglu_q8k(const float *__restrict__ gu, int ff, int rows, uint8_t *__restrict__ ha,
                                                    uint64_t hstride) {
-    const int r = blockIdx.y, b = blockIdx.x, i = threadIdx.x;
-    ESQ_EXPF_LDS_TABLE(tab, i)
-    const float *g = gu + (size_t)r * 2 * ff + (size_t)b * 256;
-    const float gv = g[i], uv = g[ff + i];
+    const int tid = threadIdx.x, l = tid & 63, nb = ff / 256;
+    ESQ_EXPF_LDS_TABLE(tab, tid)
+    const int item = blockIdx.x * 4 + (tid >> 6);
+    const bool live = item < rows * nb;
+    const int r = live ? item / nb : 0, b = live ? item - r * nb : 0;
+    const float *g = gu + (size_t)r * 2 * ff + (size_t)b * 256 + 4 * l;
+    const float4 gv = *reinterpret_cast<const float4 *>(g), uv = *reinterpret_cast<const float4 *>(g + ff);
     __syncthreads();
-    const float h = swiglu_tab(gv, uv, tab);
-    __shared__ float wmax[4];
-    float a = __builtin_fabsf(h);
-    for (int o = 32; o > 0; o >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, o));   // max is exact in any order
-    if ((i & 63) == 0) wmax[i >> 6] = a;
-    __syncthreads();
-    const float amax = __builtin_fmaxf(__builtin_fmaxf(wmax[0], wmax[1]), __builtin_fmaxf(wmax[2], wmax[3]));
+    if (!live) return;
+    const float h[4] = {swiglu_tab(gv.x, uv.x, tab), swiglu_tab(gv.y, uv.y, tab), swiglu_tab(gv.z, uv.z, tab),
+                        swiglu_tab(gv.w, uv.w, tab)};
+    float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(h[0]), __builtin_fabsf(h[1])),
+                              __builtin_fmaxf(__builtin_fabsf(h[2]), __builtin_fabsf(h[3])));
+    for (int o = 32; o > 0; o >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, o));
+    const float amax = a;
     uint8_t *blk = ha + (size_t)r * hstride + (size_t)b * 292;
-    int q = 0;
+    int q[4] = {0, 0, 0, 0};
     if (amax != 0.0f) {
         const float id = 127.0f / amax;
-        q = static_cast<int>(__builtin_rintf(h * id));   // lrintf: round to nearest even
-        q = q > 127 ? 127 : q < -127 ? -127 : q;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int v = static_cast<int>(__builtin_rintf(h[k] * id));   // lrintf: round to nearest even
+            q[k] = v > 127 ? 127 : v < -127 ? -127 : v;
+        }
     }
-    blk[4 + i] = static_cast<uint8_t>(static_cast<int8_t>(q));
-    int s = q;   // bsums: sums of 16 consecutive qs
-    for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
-    if ((i & 15) == 0) reinterpret_cast<int16_t *>(blk + 260)[i >> 4] = static_cast<int16_t>(s);
-    if (i == 0) *reinterpret_cast<float *>(blk) = amax != 0.0f ? amax / 127.0f : 0.0f;
+    *reinterpret_cast<uint32_t *>(blk + 4 + 4 * l) = (uint32_t)(q[0] & 0xff) | (uint32_t)(q[1] & 0xff) << 8 |
+                                                    (uint32_t)(q[2] & 0xff) << 16 | (uint32_t)(q[3] & 0xff) << 24;
+    int s = q[0] + q[1] + q[2] + q[3];   // bsums: sums of 16 consecutive qs, four lanes each
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if ((l & 3) == 0) reinterpret_cast<int16_t *>(blk + 260)[l >> 2] = static_cast<int16_t>(s);
+    if (l == 0) *reinterpret_cast<float *>(blk) = amax != 0.0f ? amax / 127.0f : 0.0f;
 }
 
 // One workgroup of 256 threads per (pair row, 8 Q8_0 blocks).
@@ -82,6 +92,26 @@ __global__ __launch_bounds__(256) void moe_combine(const float *__restrict__ ye,
     const int kt = k[t];
     for (int j = 0; j < kt; j++) s = s + w[t * kmax + j] * ye[(size_t)rowof[t * kmax + j] * n + i];
     out[(size_t)t * ostride + i] = s;
+}
+
+// The same, four consecutive elements per thread (16-byte loads and stores) when n, the output stride and both
+// pointers allow it.
+__global__ __launch_bounds__(256) void moe_combine4(const float *__restrict__ ye, const int *__restrict__ rowof,
+                                                    const float *__restrict__ w, const int *__restrict__ k, int kmax, int n,
+                                                    float *__restrict__ out, uint64_t ostride) {
+    const int t = blockIdx.y, i = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (i >= n) return;
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int kt = k[t];
+    for (int j = 0; j < kt; j++) {
+        const float wj = w[t * kmax + j];
+        const float4 y = *reinterpret_cast<const float4 *>(ye + (size_t)rowof[t * kmax + j] * n + i);
+        s.x = s.x + wj * y.x;
+        s.y = s.y + wj * y.y;
+        s.z = s.z + wj * y.z;
+        s.w = s.w + wj * y.w;
+    }
+    *reinterpret_cast<float4 *>(out + (size_t)t * ostride + i) = s;
 }
 
 // route() for softmax gating (src/es_engine.c:744-835, the GATE_SOFTMAX path: no gate bias, selection bias, expert groups,
@@ -248,7 +278,7 @@ hipError_t route_softmax_launch(const float *logits, uint64_t ls, int ntok, int 
 
 hipError_t moe_swiglu_launch(const float *gu, int rows, int ff, bool q8k, uint8_t *ha, uint64_t hstride, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    if (q8k) hipLaunchKernelGGL(swiglu_q8k, dim3(ff / 256, rows), dim3(256), 0, s, gu, ff, ha, hstride);
+    if (q8k) hipLaunchKernelGGL(swiglu_q8k, dim3((rows * (ff / 256) + 3) / 4), dim3(256), 0, s, gu, ff, rows, ha, hstride);
     else hipLaunchKernelGGL(swiglu_q80, dim3((ff + 255) / 256, rows), dim3(256), 0, s, gu, ff, ha, hstride);
     return hipGetLastError();
 }
@@ -256,7 +286,10 @@ hipError_t moe_swiglu_launch(const float *gu, int rows, int ff, bool q8k, uint8_
 hipError_t moe_combine_launch(const float *ye, const int *rowof, const float *w, const int *k, int kmax, int ntok, int n,
                               float *out, uint64_t ostride, hipStream_t s) {
     if (ntok <= 0) return hipSuccess;
-    hipLaunchKernelGGL(moe_combine, dim3((n + 255) / 256, ntok), dim3(256), 0, s, ye, rowof, w, k, kmax, n, out, ostride);
+    if (n % 4 == 0 && ostride % 4 == 0 && ((uintptr_t)ye & 15) == 0 && ((uintptr_t)out & 15) == 0)
+        hipLaunchKernelGGL(moe_combine4, dim3((n / 4 + 255) / 256, ntok), dim3(256), 0, s, ye, rowof, w, k, kmax, n, out, ostride);
+    else
+        hipLaunchKernelGGL(moe_combine, dim3((n + 255) / 256, ntok), dim3(256), 0, s, ye, rowof, w, k, kmax, n, out, ostride);
     return hipGetLastError();
 }
 
