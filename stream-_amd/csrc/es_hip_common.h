@@ -110,7 +110,11 @@ struct MkJob {
 // per row tile; with one, tile ids are the row tiles themselves), rows of at most MX_NBK superblocks (the whole row's
 // activations sit in LDS). nbk_max: the longest row of the launch; mx_nbk_max gives the LDS size class it runs in (0: too
 // long).
-constexpr int MX_TOK = 32, MX_ROWS = 256, MX_NBK = 16;
+// rows per workgroup tile: 256 (four waves, two workgroups per CU) or, built with ESQ_MX_ROWS=512, 512 (eight waves, one)
+#ifndef ESQ_MX_ROWS
+#define ESQ_MX_ROWS 256
+#endif
+constexpr int MX_TOK = 32, MX_ROWS = ESQ_MX_ROWS, MX_NBK = 16;
 // the Q6_K matrix-core kernel's persistent form for single products (es_hip_mm6.hip): on (default) or off; returns the
 // previous setting
 int mm6_set_persistent(int on);

@@ -34,8 +34,8 @@
 namespace esq {
 namespace {
 
-constexpr int MX_WAVES = 4, MX_RG = MX_ROWS / (16 * MX_WAVES);
-static_assert(MX_RG == 4 && MX_TOK == 32, "four row groups per wave, two activation tiles");
+constexpr int MX_WAVES = MX_ROWS / 64, MX_RG = 4;
+static_assert((MX_WAVES == 4 || MX_WAVES == 8) && MX_TOK == 32, "four row groups per wave, two activation tiles");
 // LDS bytes per superblock: values, bsums, scales
 constexpr int XV = MX_TOK * 256, XB = 4 * MX_TOK * 8, XD = MX_TOK * 4;
 
@@ -105,7 +105,7 @@ template <bool CONTRACT> __device__ __forceinline__ void epilogue(const MRes &m,
 }
 
 template <int NBKM, bool CONTRACT, bool GATHER>
-__global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
+__global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) void mx_q2k_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
     constexpr uint32_t V0 = 0, BS0 = NBKM * XV, D0 = BS0 + NBKM * XB;
     __shared__ __align__(16) uint8_t smem[NBKM * (XV + XB + XD)];
 
@@ -141,10 +141,10 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
         asm volatile("" : "+s"(sb));
         return J.act + sb;
     };
-    // values: wave w copies activations 4w .. 4w + 3 (and 16 + 4w .. + 3 when the second tile is live) of every superblock,
-    // one instruction each (lane l: activation t = 4w + l/16 (+ 16), LDS position l % 16 of its row, source chunk
-    // (l % 16) ^ (t & 15))
-    {
+    // values: with four waves, wave w copies activations 4w .. 4w + 3 (and 16 + 4w .. + 3 when the second tile is live) of
+    // every superblock, one instruction each (lane l: activation t = 4w + l/16 (+ 16), LDS position l % 16 of its row,
+    // source chunk (l % 16) ^ (t & 15)); with eight, waves 4-7 copy the second tile's
+    if constexpr (MX_WAVES == 4) {
         const int t0 = 4 * wave + (lane >> 4), t1 = t0 + 16;
         const uint32_t o0 = act_off(t0) + 4 + 16 * ((lane & 15) ^ (t0 & 15));
         const uint32_t o1 = act_off(t1) + 4 + 16 * ((lane & 15) ^ (t1 & 15));
@@ -154,10 +154,16 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
             load_lds16(ab, o0, l0 + (uint32_t)b * XV);
             if (two) load_lds16(ab, o1, l0 + (uint32_t)b * XV + 16 * 256);
         }
+    } else if (wave < 4 || two) {
+        const int t0 = 4 * (wave & 3) + 16 * (wave >> 2) + (lane >> 4);
+        const uint32_t o0 = act_off(t0) + 4 + 16 * ((lane & 15) ^ (t0 & 15));
+        const uint32_t l0 = smem0 + V0 + (uint32_t)(4 * (wave & 3) + 16 * (wave >> 2)) * 256;
+        for (int b = 0; b < nbk; b++) load_lds16(sb_base(b), o0, l0 + (uint32_t)b * XV);
     }
-    // bsums: thread tid, activation tb = (tid >> 1) & 31, bsums 8 hb .. 8 hb + 7 of superblocks wave + 4k;
-    // scales: activation td = tid & 31 of superblocks (tid >> 5) + 8k (activations 16..31 only when the second tile is live)
-    constexpr int KB = (NBKM + 3) / 4, KD = (NBKM + 7) / 8;
+    // bsums: thread tid, activation tb = (tid >> 1) & 31, bsums 8 hb .. 8 hb + 7 of superblocks wave + MX_WAVES k;
+    // scales: activation td = tid & 31 of superblocks (tid >> 5) + 2 MX_WAVES k (activations 16..31 only when the second
+    // tile is live)
+    constexpr int KB = (NBKM + MX_WAVES - 1) / MX_WAVES, KD = (NBKM + 2 * MX_WAVES - 1) / (2 * MX_WAVES);
     const int tb = (tid >> 1) & 31, hb = tid & 1, td = tid & 31;
     const bool bs_live = two || tb < 16, d_live = two || td < 16;
     uint4 bsv[KB];
@@ -166,10 +172,10 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
         const uint32_t ob = act_off(tb) + 260 + 16 * hb, od = act_off(td);
 #pragma unroll
         for (int k = 0; k < KB; k++)
-            if (wave + 4 * k < nbk && bs_live) bsv[k] = ldg<uint4>(sb_base(wave + 4 * k) + ob);
+            if (wave + MX_WAVES * k < nbk && bs_live) bsv[k] = ldg<uint4>(sb_base(wave + MX_WAVES * k) + ob);
 #pragma unroll
         for (int k = 0; k < KD; k++) {
-            const int b = (tid >> 5) + 8 * k;
+            const int b = (tid >> 5) + 2 * MX_WAVES * k;
             if (b < nbk && d_live) dv[k] = ldg<float>(J.act + (size_t)(292u * (uint32_t)b + od));
         }
     }
@@ -183,7 +189,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
     uint32_t vq[MX_RG], vs[MX_RG], vd[MX_RG];
 #pragma unroll
     for (int j = 0; j < MX_RG; j++) {
-        const uint32_t o = (uint32_t)min(16 * (4 * j + wave) + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
+        const uint32_t o = (uint32_t)min(16 * (MX_WAVES * j + wave) + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
         vq[j] = o + 16 + 16 * lg;
         vs[j] = o + 8 * (lg >> 1);
         vd[j] = o + 80;
@@ -207,7 +213,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * MX_RG) : "memory");
 #pragma unroll
     for (int k = 0; k < KB; k++) {
-        const int b = wave + 4 * k;
+        const int b = wave + MX_WAVES * k;
         if (b >= nbk || !bs_live) continue;
         const uint32_t w[4] = {bsv[k].x, bsv[k].y, bsv[k].z, bsv[k].w};
         uint32_t hv[4];
@@ -222,7 +228,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
     }
 #pragma unroll
     for (int k = 0; k < KD; k++) {
-        const int b = (tid >> 5) + 8 * k;
+        const int b = (tid >> 5) + 2 * MX_WAVES * k;
         if (b < nbk && d_live) *reinterpret_cast<float *>(smem + D0 + b * XD + td * 4) = dv[k];
     }
     lds_sync();
@@ -288,7 +294,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 ? 2 : 1) void mx_q2k_kerne
     const __amdgpu_buffer_rsrc_t yrsrc = __builtin_amdgcn_make_buffer_rsrc((void *)J.y, (short)0, (int)yrange, 0x00020000);
 #pragma unroll
     for (int j = 0; j < MX_RG; j++) {
-        const int r = row0 + 16 * (4 * j + wave) + lr;
+        const int r = row0 + 16 * (MX_WAVES * j + wave) + lr;
         uint32_t yoff = r < J.r1 ? (uint32_t)(tok0 + 4 * lg) * ys4 + 4u * (uint32_t)r : 0x80000000u;
 #pragma unroll
         for (int u = 0; u < 2; u++) {
