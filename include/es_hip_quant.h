@@ -306,6 +306,12 @@ int es_hip_set_q3k_mfma_min_batch(int n);
  * (no pre-pass). Larger batches, or all with n < 2, run on the LDS-staged Q2_K kernel of es_hip_set_q2k_mfma_min_batch.
  * Results are identical on every kernel. Returns the previous value. */
 int es_hip_set_q2k_expert_max_batch(int n);
+/* A MoE layer whose gate and up projections are Q2_K, whose down projection takes Q8_K activations and whose batches run
+ * on the expert-sized kernel computes, with on != 0 (the default), the gate and up rows of each block of 256 in one
+ * workgroup and writes SwiGLU(gate, up) as that block's Q8_K activation directly (no float gate/up buffer, no SwiGLU
+ * launch); with 0, gate and up run as two jobs and a separate SwiGLU + Q8_K pass follows. Results are identical on both.
+ * Applies to plans and contexts created after the call. Returns the previous setting. */
+int es_hip_set_moe_gated(int on);
 /* Q4_0 / Q5_0 / Q8_0 batches that run on the matrix cores (es_hip_set_batched32_mfma_min) and have rows of at most 4096
  * columns use, with on != 0 (the default), the kernel that copies the activations' Q8_0 rows into LDS once per tile of
  * 16 rows x 32 activations (no pre-pass); with 0, the one that reads them from a pre-pass layout. Results are identical

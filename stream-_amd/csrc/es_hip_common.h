@@ -105,6 +105,8 @@ struct MkJob {
     int tile0, ntok_tiles;
     int rows_per_wg;      // the batched 32-wide kernel's rows per workgroup tile (1 .. MBX_ROWS), set per job by the host
     int pad_;
+    const uint8_t *W2;    // the gated expert kernel: the up projection's row 0 (W is the gate's); y then holds the h rows'
+                          // Q8_K blocks (bytes, ystride bytes apart)
 };
 // Expert-sized Q2_K products (es_hip_mx.hip): the same jobs, workgroup tiles of MX_ROWS rows x MX_TOK activations (ntok_tiles
 // per row tile; with one, tile ids are the row tiles themselves), rows of at most MX_NBK superblocks (the whole row's
@@ -119,6 +121,10 @@ constexpr int MX_TOK = 32, MX_ROWS = ESQ_MX_ROWS, MX_NBK = 16;
 // previous setting
 int mm6_set_persistent(int on);
 int mx_nbk_max(int nbk);
+// The gated form (a Q2_K expert's gate and up products with the SwiGLU and the Q8_K requantization of h fused in): per
+// job, W and W2 the gate's and up's rows, y the first h row's Q8_K blocks (bytes), r0 and r1 multiples of 256
+hipError_t mxg_launch(bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
+                      hipStream_t s);
 hipError_t mx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single,
                      int grid, int order, hipStream_t s);
 // Batched 32-wide formats reading the activations' Q8_0 rows directly (es_hip_mbx.hip): the same jobs, workgroup tiles of
@@ -241,6 +247,7 @@ struct MoeFamily {
     int bn, row_tiles8;
     MkJob mk;              // MX: template job
     int mx_tiles;
+    int gated;             // MX gate/up: the gated kernel (one job per expert slot, h written as Q8_K blocks)
 };
 struct MoeDevArgs {
     const int *sel;         // [ntok][k] routing (experts)
@@ -330,14 +337,27 @@ __device__ __forceinline__ uint2 ldw2(const void *p) {
 #endif
 }
 
-// Sum over groups of G consecutive lanes (G = 1, 2, 4, 8); every lane of a group ends with the group's sum.
+// Sum over groups of G consecutive lanes (G = 1, 2, 4, 8, 16); every lane of a group ends with the group's sum.
 // DPP lane moves, no LDS round trip: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror (lane i of each 8 reads
-// lane 7 - i). After the two quad steps every lane holds its quad's sum; the half mirror pairs each quad with the other
-// quad of its 8 lanes. Integer sums, so the pairing order does not matter.
+// lane 7 - i), row_mirror (lane i of each 16 reads lane 15 - i). After the two quad steps every lane holds its quad's
+// sum; the half mirror pairs each quad with the other quad of its 8 lanes, the mirror each 8 with the other 8 of its 16.
+// Integer sums, so the pairing order does not matter.
 template <int G> __device__ __forceinline__ int group_sum(int v) {
     if constexpr (G >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
     if constexpr (G >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
     if constexpr (G >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+    if constexpr (G >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+    return v;
+}
+// The maximum over groups of G consecutive lanes, the same moves (exact in any order)
+template <int CTRL> __device__ __forceinline__ float dpp_movf(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+template <int G> __device__ __forceinline__ float group_max(float v) {
+    if constexpr (G >= 2) v = __builtin_fmaxf(v, dpp_movf<0xB1>(v));
+    if constexpr (G >= 4) v = __builtin_fmaxf(v, dpp_movf<0x4E>(v));
+    if constexpr (G >= 8) v = __builtin_fmaxf(v, dpp_movf<0x141>(v));
+    if constexpr (G >= 16) v = __builtin_fmaxf(v, dpp_movf<0x140>(v));
     return v;
 }
 

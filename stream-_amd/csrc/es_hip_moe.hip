@@ -42,8 +42,9 @@ __global__ __launch_bounds__(256) void swiglu_q8k(const float *__restrict__ gu, 
                         swiglu_tab(gv.w, uv.w, tab)};
     float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(h[0]), __builtin_fabsf(h[1])),
                               __builtin_fmaxf(__builtin_fabsf(h[2]), __builtin_fabsf(h[3])));
-    for (int o = 32; o > 0; o >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, o));
-    const float amax = a;
+    a = group_max<16>(a);   // DPP within each 16 lanes, then across the four rows
+    a = __builtin_fmaxf(a, __shfl_xor(a, 16));
+    const float amax = __builtin_fmaxf(a, __shfl_xor(a, 32));
     uint8_t *blk = ha + (size_t)r * hstride + (size_t)b * 292;
     int q[4] = {0, 0, 0, 0};
     if (amax != 0.0f) {
@@ -56,9 +57,7 @@ __global__ __launch_bounds__(256) void swiglu_q8k(const float *__restrict__ gu, 
     }
     *reinterpret_cast<uint32_t *>(blk + 4 + 4 * l) = (uint32_t)(q[0] & 0xff) | (uint32_t)(q[1] & 0xff) << 8 |
                                                     (uint32_t)(q[2] & 0xff) << 16 | (uint32_t)(q[3] & 0xff) << 24;
-    int s = q[0] + q[1] + q[2] + q[3];   // bsums: sums of 16 consecutive qs, four lanes each
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    const int s = group_sum<4>(q[0] + q[1] + q[2] + q[3]);   // bsums: sums of 16 consecutive qs, four lanes each
     if ((l & 3) == 0) reinterpret_cast<int16_t *>(blk + 260)[l >> 2] = static_cast<int16_t>(s);
     if (l == 0) *reinterpret_cast<float *>(blk) = amax != 0.0f ? amax / 127.0f : 0.0f;
 }
@@ -82,7 +81,11 @@ __global__ __launch_bounds__(256) void swiglu_q80(const float *__restrict__ gu, 
     if ((e & 31) == 0) *reinterpret_cast<float *>(blk) = d;
 }
 
-// One thread per (token, output element): the token's expert outputs summed in routing order, from s = 0.
+// One thread per (token, output element): the token's expert outputs summed in routing order, from s = 0. The rows are
+// read eight at a time (the last one repeated past k) so that eight loads are in flight before the first sum; the sums
+// then run one by one in routing order.
+constexpr int COMBINE_BATCH = 8;
+
 __global__ __launch_bounds__(256) void moe_combine(const float *__restrict__ ye, const int *__restrict__ rowof,
                                                    const float *__restrict__ w, const int *__restrict__ k, int kmax, int n,
                                                    float *__restrict__ out, uint64_t ostride) {
@@ -90,7 +93,18 @@ __global__ __launch_bounds__(256) void moe_combine(const float *__restrict__ ye,
     if (i >= n) return;
     float s = 0.0f;
     const int kt = k[t];
-    for (int j = 0; j < kt; j++) s = s + w[t * kmax + j] * ye[(size_t)rowof[t * kmax + j] * n + i];
+    for (int j0 = 0; j0 < kt; j0 += COMBINE_BATCH) {
+        float wj[COMBINE_BATCH], y[COMBINE_BATCH];
+#pragma unroll
+        for (int q = 0; q < COMBINE_BATCH; q++) {
+            const int j = min(j0 + q, kt - 1);
+            wj[q] = w[t * kmax + j];
+            y[q] = ye[(size_t)rowof[t * kmax + j] * n + i];
+        }
+#pragma unroll
+        for (int q = 0; q < COMBINE_BATCH; q++)
+            if (j0 + q < kt) s = s + wj[q] * y[q];
+    }
     out[(size_t)t * ostride + i] = s;
 }
 
@@ -103,13 +117,23 @@ __global__ __launch_bounds__(256) void moe_combine4(const float *__restrict__ ye
     if (i >= n) return;
     float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const int kt = k[t];
-    for (int j = 0; j < kt; j++) {
-        const float wj = w[t * kmax + j];
-        const float4 y = *reinterpret_cast<const float4 *>(ye + (size_t)rowof[t * kmax + j] * n + i);
-        s.x = s.x + wj * y.x;
-        s.y = s.y + wj * y.y;
-        s.z = s.z + wj * y.z;
-        s.w = s.w + wj * y.w;
+    for (int j0 = 0; j0 < kt; j0 += COMBINE_BATCH) {
+        float wj[COMBINE_BATCH];
+        float4 y[COMBINE_BATCH];
+#pragma unroll
+        for (int q = 0; q < COMBINE_BATCH; q++) {
+            const int j = min(j0 + q, kt - 1);
+            wj[q] = w[t * kmax + j];
+            y[q] = *reinterpret_cast<const float4 *>(ye + (size_t)rowof[t * kmax + j] * n + i);
+        }
+#pragma unroll
+        for (int q = 0; q < COMBINE_BATCH; q++)
+            if (j0 + q < kt) {
+                s.x = s.x + wj[q] * y[q].x;
+                s.y = s.y + wj[q] * y[q].y;
+                s.z = s.z + wj[q] * y[q].z;
+                s.w = s.w + wj[q] * y[q].w;
+            }
     }
     *reinterpret_cast<float4 *>(out + (size_t)t * ostride + i) = s;
 }
@@ -474,7 +498,7 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
     const int ff = A.ff, n = A.n;
     for (int prod = 0; prod < 2; prod++) {   // 0: gate/up, 1: down
         const MoeFamily &F = prod ? sa.DN : sa.GU;
-        const int njob = prod ? 1 : 2;
+        const int njob = prod || (F.kind == MOE_FAM_MX && F.gated) ? 1 : 2;   // gated: gate and up in one job
         int ntok = 0, tiles = 0, items = 0, units = 0;
         if (F.kind == MOE_FAM_MX && real) {
             ntok = ceil_div(c, MX_TOK);
@@ -543,6 +567,10 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
                         J.act = prod ? A.ha + (size_t)s0 * A.hstride : A.x;
                         J.arow = prod ? nullptr : A.tok_of + s0;
                         J.y = prod ? A.bye + (size_t)s0 * n : A.bgu + (size_t)s0 * 2 * ff + (size_t)g * ff;
+                        if (!prod && F.gated) {   // h's Q8_K blocks of the expert's first pair row
+                            J.W2 = wu_u;
+                            J.y = reinterpret_cast<float *>(A.ha + (size_t)s0 * A.hstride);
+                        }
                         J.na = c;
                         J.ntok_tiles = ntok;
                         J.tile0 = t0 + g * (ntok == 1 ? F.mx_tiles : F.row_tiles8 * ntok);

@@ -30,6 +30,7 @@
 // dall = y.d * d, dmin = y.d * dmin, s += dall * isum - dmin * summs, with the product and difference fused as the clang
 // build fuses them (s + fma(dall, isum, -(dmin * summs))) or every operation rounded (the gcc and portable builds).
 #include "es_hip_common.h"
+#include "es_hip_expf.h"
 
 namespace esq {
 namespace {
@@ -104,10 +105,25 @@ template <bool CONTRACT> __device__ __forceinline__ void epilogue(const MRes &m,
     }
 }
 
-template <int NBKM, bool CONTRACT, bool GATHER>
-__global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) void mx_q2k_kernel(const MkJob *__restrict__ jobs, int njobs, MkJob single) {
+// GATED: the gate and up products of one expert in one workgroup of eight waves (waves 0-3 the gate's 256 rows, waves 4-7
+// the up's same rows, each half split over its waves as the four-wave form splits its tile), followed by h = g / (1 +
+// expf(-g)) * u (src/es_engine.c:913) and h's requantization to Q8_K blocks (src/es_q2k.c:102-125) for the down product:
+// the tile's 256 rows are one block of h, so its absolute maximum, scale, values and bsums are all formed in the
+// workgroup. Gate wave w and up wave 4 + w hold the same rows and activations in the same lanes and registers; each
+// forms h for half of its row groups, taking the partner's values of that half through LDS. The per-activation maxima
+// over the eight waves meet in LDS, the blocks are assembled in LDS and written as dwords. Every float operation and the order of the integer sums are those of the
+// separate SwiGLU kernel (es_hip_moe.hip), so the blocks are bit-identical to its.
+template <int NBKM, bool CONTRACT, bool GATHER, bool GATED>
+__global__ __launch_bounds__(GATED ? 512 : 64 * MX_WAVES, !GATED && NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) void mx_q2k_kernel(
+    const MkJob *__restrict__ jobs, int njobs, MkJob single) {
+    constexpr int NW = GATED ? 8 : MX_WAVES;       // waves of the workgroup
+    constexpr int RW = GATED ? 4 : MX_WAVES;       // waves that split one product's rows
+    constexpr int TROWS = 64 * RW;                 // rows of the tile
     constexpr uint32_t V0 = 0, BS0 = NBKM * XV, D0 = BS0 + NBKM * XB;
-    __shared__ __align__(16) uint8_t smem[NBKM * (XV + XB + XD)];
+    constexpr uint32_t LDS_BYTES = NBKM * (XV + XB + XD) > 32 * 1024 + MX_TOK * 292 + 8 * MX_TOK * 4
+                                       ? NBKM * (XV + XB + XD) : 32 * 1024 + MX_TOK * 292 + 8 * MX_TOK * 4;
+    __shared__ __align__(16) uint8_t smem[GATED ? LDS_BYTES : NBKM * (XV + XB + XD)];
+    __shared__ uint64_t xtab[GATED ? 32 : 1];   // expf's table (the gated epilogue)
 
     MkJob J;
     if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
@@ -122,12 +138,17 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
         rt = xcd + 8 * (kq / J.ntok_tiles);
         tt = kq % J.ntok_tiles;
     }
-    if (rt * MX_ROWS >= J.r1 - J.r0) return;
-    const int row0 = J.r0 + rt * MX_ROWS, tok0 = tt * MX_TOK;
+    if (rt * TROWS >= J.r1 - J.r0) return;
+    const int row0 = J.r0 + rt * TROWS, tok0 = tt * MX_TOK;
     const bool two = J.na - tok0 > 16;   // the second 16-activation tile has activations
     const int nbk = J.cols / 256;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lr = lane & 15, lg = lane >> 4;
+    const int wq = wave % RW;                     // this wave's share of its product's rows
+    if constexpr (GATED) {
+        static constexpr uint64_t T_[32] = ESQ_EXPF_TABLE;
+        if (tid < 32) xtab[tid] = T_[tid];
+    }
     const uint32_t smem0 = lds_addr(smem);
 
     // ---- staging sources: 32-bit offsets from J.act (the host keeps every activation row within 4 GiB of it)
@@ -144,7 +165,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
     // values: with four waves, wave w copies activations 4w .. 4w + 3 (and 16 + 4w .. + 3 when the second tile is live) of
     // every superblock, one instruction each (lane l: activation t = 4w + l/16 (+ 16), LDS position l % 16 of its row,
     // source chunk (l % 16) ^ (t & 15)); with eight, waves 4-7 copy the second tile's
-    if constexpr (MX_WAVES == 4) {
+    if constexpr (NW == 4) {
         const int t0 = 4 * wave + (lane >> 4), t1 = t0 + 16;
         const uint32_t o0 = act_off(t0) + 4 + 16 * ((lane & 15) ^ (t0 & 15));
         const uint32_t o1 = act_off(t1) + 4 + 16 * ((lane & 15) ^ (t1 & 15));
@@ -163,7 +184,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
     // bsums: thread tid, activation tb = (tid >> 1) & 31, bsums 8 hb .. 8 hb + 7 of superblocks wave + MX_WAVES k;
     // scales: activation td = tid & 31 of superblocks (tid >> 5) + 2 MX_WAVES k (activations 16..31 only when the second
     // tile is live)
-    constexpr int KB = (NBKM + MX_WAVES - 1) / MX_WAVES, KD = (NBKM + 2 * MX_WAVES - 1) / (2 * MX_WAVES);
+    constexpr int KB = (NBKM + NW - 1) / NW, KD = (NBKM + 2 * NW - 1) / (2 * NW);
     const int tb = (tid >> 1) & 31, hb = tid & 1, td = tid & 31;
     const bool bs_live = two || tb < 16, d_live = two || td < 16;
     uint4 bsv[KB];
@@ -172,10 +193,10 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
         const uint32_t ob = act_off(tb) + 260 + 16 * hb, od = act_off(td);
 #pragma unroll
         for (int k = 0; k < KB; k++)
-            if (wave + MX_WAVES * k < nbk && bs_live) bsv[k] = ldg<uint4>(sb_base(wave + MX_WAVES * k) + ob);
+            if (wave + NW * k < nbk && bs_live) bsv[k] = ldg<uint4>(sb_base(wave + NW * k) + ob);
 #pragma unroll
         for (int k = 0; k < KD; k++) {
-            const int b = (tid >> 5) + 2 * MX_WAVES * k;
+            const int b = (tid >> 5) + 2 * NW * k;
             if (b < nbk && d_live) dv[k] = ldg<float>(J.act + (size_t)(292u * (uint32_t)b + od));
         }
     }
@@ -183,13 +204,13 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
     // ---- this wave's weight rows (rows past r1 repeat the last one; their results are not stored)
     // Buffer loads from the tile's first row: per-lane offsets per row group (q chunk, scale pair, d | dmin) and the
     // superblock's 84 b in the scalar offset, so a load needs no address arithmetic.
-    const uint8_t *wbase = J.W + (size_t)row0 * J.row_bytes;
-    const uint32_t wrange = (uint32_t)min(MX_ROWS, J.r1 - row0) * (uint32_t)J.row_bytes;
+    const uint8_t *wbase = (GATED && wave >= RW ? J.W2 : J.W) + (size_t)row0 * J.row_bytes;
+    const uint32_t wrange = (uint32_t)min(TROWS, J.r1 - row0) * (uint32_t)J.row_bytes;
     const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc((void *)wbase, (short)0, (int)wrange, 0x00020000);
     uint32_t vq[MX_RG], vs[MX_RG], vd[MX_RG];
 #pragma unroll
     for (int j = 0; j < MX_RG; j++) {
-        const uint32_t o = (uint32_t)min(16 * (MX_WAVES * j + wave) + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
+        const uint32_t o = (uint32_t)min(16 * (RW * j + wq) + lr, J.r1 - 1 - row0) * (uint32_t)J.row_bytes;
         vq[j] = o + 16 + 16 * lg;
         vs[j] = o + 8 * (lg >> 1);
         vd[j] = o + 80;
@@ -213,7 +234,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * MX_RG) : "memory");
 #pragma unroll
     for (int k = 0; k < KB; k++) {
-        const int b = wave + MX_WAVES * k;
+        const int b = wave + NW * k;
         if (b >= nbk || !bs_live) continue;
         const uint32_t w[4] = {bsv[k].x, bsv[k].y, bsv[k].z, bsv[k].w};
         uint32_t hv[4];
@@ -228,7 +249,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
     }
 #pragma unroll
     for (int k = 0; k < KD; k++) {
-        const int b = (tid >> 5) + 2 * MX_WAVES * k;
+        const int b = (tid >> 5) + 2 * NW * k;
         if (b < nbk && d_live) *reinterpret_cast<float *>(smem + D0 + b * XD + td * 4) = dv[k];
     }
     lds_sync();
@@ -285,6 +306,87 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
     epilogue<CONTRACT>(mr[1][0], bd[1], bdm[1], ydl[0], acc[MX_RG - 1][0]);
     if (two) epilogue<CONTRACT>(mr[1][1], bd[1], bdm[1], ydl[1], acc[MX_RG - 1][1]);
 
+    if constexpr (GATED) {
+        // ---- h and its Q8_K blocks. Lane l, register i of tile u, row group j: activation 16u + 4lg + i of the tile, h
+        // column (row) 16 (4j + wq) + lr of the block, in gate wave wq (its gate value) and up wave 4 + wq (its up value)
+        // alike. The two waves split the work: the gate wave forms h for row groups 0 and 1, the up wave for 2 and 3, each
+        // taking the other product's values of its row groups through LDS. LDS (the activation area, free after a
+        // barrier): the exchanged values xv[writer wave][2][2][lane] (four registers each), then the tile's 32 blocks (292
+        // bytes each), then the waves' maxima am[32][wave]. Only the activations of the tile are formed (the second 16 when it has them).
+        v4f *xv = reinterpret_cast<v4f *>(smem);
+        uint8_t *blk = smem + 32 * 1024;
+        float *am = reinterpret_cast<float *>(smem + 32 * 1024 + MX_TOK * 292);
+        const int jo = wave < RW ? 0 : 2;   // the row groups this wave forms: jo, jo + 1
+        const int nu = two ? 2 : 1;
+        __syncthreads();   // every wave is past its last read of the activations
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++)   // the partner's row groups: 2 - jo + jj
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                if (u >= nu) continue;
+                const v4f hi = acc[2 + jj][u], lo = acc[jj][u];   // values, not a selected reference (kept in registers)
+                xv[((wave * 2 + jj) * 2 + u) * 64 + lane] = wave < RW ? hi : lo;
+            }
+        __syncthreads();
+        float h[2][2][4];
+        const int pw = wave ^ RW;   // the partner wave
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            if (u >= nu) continue;
+            const v4f o0 = xv[((pw * 2 + 0) * 2 + u) * 64 + lane], o1 = xv[((pw * 2 + 1) * 2 + u) * 64 + lane];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int jj = 0; jj < 2; jj++) {
+                    const float lo = acc[jj][u][i], hi = acc[2 + jj][u][i];
+                    const float mine = wave < RW ? lo : hi;
+                    const float other = jj ? o1[i] : o0[i];
+                    const float g = wave < RW ? mine : other, v = wave < RW ? other : mine;
+                    h[jj][u][i] = g / (1.0f + esq_expf_tab(-g, xtab)) * v;
+                    a = __builtin_fmaxf(a, __builtin_fabsf(h[jj][u][i]));   // the maximum is exact in any order
+                }
+                a = group_max<16>(a);   // over the 16 rows lr (one DPP row)
+                if (lr == 0) am[(16 * u + 4 * lg + i) * NW + wave] = a;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            if (u >= nu) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 16 * u + 4 * lg + i;
+                const v4f m0 = *reinterpret_cast<const v4f *>(am + t * NW), m1 = *reinterpret_cast<const v4f *>(am + t * NW + 4);
+                const float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(m0[0], m0[1]), __builtin_fmaxf(m0[2], m0[3])),
+                                                   __builtin_fmaxf(__builtin_fmaxf(m1[0], m1[1]), __builtin_fmaxf(m1[2], m1[3])));
+                uint8_t *b = blk + t * 292;
+#pragma unroll
+                for (int jj = 0; jj < 2; jj++) {
+                    int q = 0;
+                    if (amax != 0.0f) {
+                        const int v = static_cast<int>(__builtin_rintf(h[jj][u][i] * (127.0f / amax)));   // lrintf
+                        q = v > 127 ? 127 : v < -127 ? -127 : v;
+                    }
+                    const int g16 = RW * (jo + jj) + wq;   // the block's group of 16 elements
+                    b[4 + 16 * g16 + lr] = static_cast<uint8_t>(static_cast<int8_t>(q));
+                    const int sum = group_sum<16>(q);   // bsums: the 16 elements of the group (one DPP row)
+                    if (lr == 0) reinterpret_cast<int16_t *>(b + 260)[g16] = static_cast<int16_t>(sum);
+                }
+                if (wave == 0 && lr == 0) *reinterpret_cast<float *>(b) = amax != 0.0f ? amax / 127.0f : 0.0f;
+            }
+        }
+        __syncthreads();
+        // the blocks of the tile's activations out, a dword per thread: activation t's block (row0 / 256) of its h row
+        const int nt = min(MX_TOK, J.na - tok0);
+        uint8_t *hy = reinterpret_cast<uint8_t *>(J.y) + (size_t)(row0 / 256) * 292;
+        for (int x = tid; x < nt * 73; x += 64 * NW) {
+            const int t = x / 73, d = x - t * 73;
+            *reinterpret_cast<uint32_t *>(hy + (size_t)(tok0 + t) * J.ystride + 4 * d) =
+                *reinterpret_cast<const uint32_t *>(blk + t * 292 + 4 * d);
+        }
+        return;
+    }
     // ---- outputs: lane l, register i of tile u holds activation tok0 + 16u + 4lg + i, row row0 + 16 (4j + wave) + lr.
     // Buffer stores over y[0, (na - 1) * ystride + r1): the hardware's range check drops those of activations past na
     // (ystride >= r1), and rows past r1 get an offset above the range. The host keeps (na + MX_TOK) * ystride * 4 below
@@ -294,7 +396,7 @@ __global__ __launch_bounds__(64 * MX_WAVES, NBKM <= 8 && MX_WAVES == 4 ? 2 : 1) 
     const __amdgpu_buffer_rsrc_t yrsrc = __builtin_amdgcn_make_buffer_rsrc((void *)J.y, (short)0, (int)yrange, 0x00020000);
 #pragma unroll
     for (int j = 0; j < MX_RG; j++) {
-        const int r = row0 + 16 * (MX_WAVES * j + wave) + lr;
+        const int r = row0 + 16 * (RW * j + wq) + lr;
         uint32_t yoff = r < J.r1 ? (uint32_t)(tok0 + 4 * lg) * ys4 + 4u * (uint32_t)r : 0x80000000u;
 #pragma unroll
         for (int u = 0; u < 2; u++) {
@@ -313,17 +415,41 @@ template <int NBKM>
 void mx_launch_nbk(bool gather, bool contract, const MkJob *jobs, int njobs, const MkJob &single, int grid, hipStream_t s) {
     const dim3 g(grid), b(64 * MX_WAVES);
     if (gather) {
-        if (contract) hipLaunchKernelGGL((mx_q2k_kernel<NBKM, true, true>), g, b, 0, s, jobs, njobs, single);
-        else hipLaunchKernelGGL((mx_q2k_kernel<NBKM, false, true>), g, b, 0, s, jobs, njobs, single);
+        if (contract) hipLaunchKernelGGL((mx_q2k_kernel<NBKM, true, true, false>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mx_q2k_kernel<NBKM, false, true, false>), g, b, 0, s, jobs, njobs, single);
     } else {
-        if (contract) hipLaunchKernelGGL((mx_q2k_kernel<NBKM, true, false>), g, b, 0, s, jobs, njobs, single);
-        else hipLaunchKernelGGL((mx_q2k_kernel<NBKM, false, false>), g, b, 0, s, jobs, njobs, single);
+        if (contract) hipLaunchKernelGGL((mx_q2k_kernel<NBKM, true, false, false>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mx_q2k_kernel<NBKM, false, false, false>), g, b, 0, s, jobs, njobs, single);
+    }
+}
+
+template <int NBKM>
+void mxg_launch_nbk(bool gather, bool contract, const MkJob *jobs, int njobs, const MkJob &single, int grid, hipStream_t s) {
+    const dim3 g(grid), b(512);
+    if (gather) {
+        if (contract) hipLaunchKernelGGL((mx_q2k_kernel<NBKM, true, true, true>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mx_q2k_kernel<NBKM, false, true, true>), g, b, 0, s, jobs, njobs, single);
+    } else {
+        if (contract) hipLaunchKernelGGL((mx_q2k_kernel<NBKM, true, false, true>), g, b, 0, s, jobs, njobs, single);
+        else hipLaunchKernelGGL((mx_q2k_kernel<NBKM, false, false, true>), g, b, 0, s, jobs, njobs, single);
     }
 }
 
 }  // namespace
 
 int mx_nbk_max(int nbk) { return nbk <= 4 ? 4 : nbk <= 8 ? 8 : nbk <= MX_NBK ? MX_NBK : 0; }
+
+hipError_t mxg_launch(bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single, int grid, int order,
+                      hipStream_t s) {
+    const bool contract = order == ES_HIP_ORDER_X86_CONTRACT;
+    switch (mx_nbk_max(nbk_max)) {
+    case 4: mxg_launch_nbk<4>(gather, contract, jobs, njobs, single, grid, s); break;
+    case 8: mxg_launch_nbk<8>(gather, contract, jobs, njobs, single, grid, s); break;
+    case MX_NBK: mxg_launch_nbk<MX_NBK>(gather, contract, jobs, njobs, single, grid, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 hipError_t mx_launch(int type, bool gather, int nbk_max, const MkJob *jobs, int njobs, const MkJob &single, int grid,
                      int order, hipStream_t s) {

@@ -131,6 +131,7 @@ struct Req {   // one product as the launch planner sees it
     size_t astride, ystride;
     const int *arow;   // optional device gather table: activation q is row arow[q] of act
     int act_rows = 0;  // rows of act a gather may index (0: na)
+    const void *W2 = nullptr;   // a gated expert product (Q2_K): the up rows; y then holds h's Q8_K blocks (bytes)
 };
 
 int check_req(const Req &q, const FmtInfo &f) {
@@ -140,6 +141,7 @@ int check_req(const Req &q, const FmtInfo &f) {
     if (q.r1 == q.r0 || q.na == 0) return ES_HIP_OK;
     if (!q.W || !q.act || !q.y) return fail(ES_HIP_EINVAL, "null W, activation or output pointer");
     if (reinterpret_cast<uintptr_t>(q.W) & 3) return fail(ES_HIP_EINVAL, "W must be 4-byte aligned");
+    if (reinterpret_cast<uintptr_t>(q.W2) & 3) return fail(ES_HIP_EINVAL, "W2 must be 4-byte aligned");
     if ((reinterpret_cast<uintptr_t>(q.act) & 3) || (q.astride & 3))
         return fail(ES_HIP_EINVAL, "activation blocks must be 4-byte aligned (pointer and stride)");
     if (reinterpret_cast<uintptr_t>(q.y) & 3) return fail(ES_HIP_EINVAL, "y must be 4-byte aligned");
@@ -275,6 +277,7 @@ std::atomic<int> g_mk_min_tiles{128};   // ... and its 64 x 128 tiles per produc
 std::atomic<int> g_mk5_min{8};          // activations per Q5_K product from which the direct-activation kernel is used
 std::atomic<int> g_mk3_min{8};          // ... per Q3_K product
 std::atomic<int> g_mx_max{64};          // activations per Q2_K product up to which the expert-sized kernel is used (2+)
+std::atomic<int> g_moe_gated{1};        // MoE layers with Q2_K gate/up and a K-quant down: the gated expert kernel
 std::atomic<int> g_mbx_on{1};           // batched 32-wide products on the kernel reading Q8_0 rows (0: the pre-pass one)
 
 struct Prep {   // one activation pre-pass (shared by products that read the same activations)
@@ -311,6 +314,7 @@ struct MkGroup {   // one direct-activation matrix-core launch: products of one 
     int nbkm = 0;     // > 0: the expert-sized kernel (es_hip_mx.hip) in LDS size class nbkm
     bool b32 = false; // ... or with nbkm, the 32-wide kernel reading Q8_0 rows (es_hip_mbx.hip)
     int tok = esq::MK_TOK;   // the direct kernel's activations per tile
+    bool gated = false;      // with nbkm: the gated expert kernel (gate and up of a Q2_K expert, h as Q8_K blocks)
     int grid = 0;
     std::vector<esq::MkJob> jobs;
     size_t off = 0;
@@ -399,6 +403,7 @@ size_t mk_ystride(const Req &q) { return q.na > 1 ? q.ystride : std::max(q.ystri
 bool mx_eligible(const Req &q) {
     const int mx = g_mx_max.load();
     if (q.type != ES_HIP_Q2_K || q.na < 2 || q.na > mx || q.ints || q.r1 <= q.r0 || q.cols / 256 > esq::MX_NBK) return false;
+    if (q.W2 && (q.r0 % 256 || q.r1 % 256)) return false;   // the gated kernel's tiles are whole blocks of h
     const size_t rows = q.arow ? (size_t)std::max(q.act_rows, 0) : (size_t)q.na;
     const size_t stride = q.astride ? q.astride : (size_t)(q.cols / 256) * 292;
     return (!q.arow || q.act_rows > 0) && rows * stride < ((size_t)1 << 32) - 65536 &&
@@ -774,16 +779,23 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
         if (mx_eligible(q)) {   // one launch per LDS size class; MX_ROWS x MX_TOK tiles
             const int nbkm = esq::mx_nbk_max(nbk);
             MkGroup *g = nullptr;
+            const bool gated = q.W2 != nullptr;
             for (MkGroup &x : bt.mkg)
-                if (!x.b32 && x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == nbkm) g = &x;
-            if (!g) { bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr, nbkm}); g = &bt.mkg.back(); }
+                if (!x.b32 && x.type == (int)q.type && x.gather == (q.arow != nullptr) && x.nbkm == nbkm && x.gated == gated)
+                    g = &x;
+            if (!g) {
+                bt.mkg.push_back(MkGroup{(int)q.type, q.arow != nullptr, nbkm});
+                g = &bt.mkg.back();
+                g->gated = gated;
+            }
             esq::MkJob j{};
             j.W = static_cast<const uint8_t *>(q.W);
+            j.W2 = static_cast<const uint8_t *>(q.W2);
             j.act = static_cast<const uint8_t *>(q.act);
             j.arow = q.arow;
             j.y = q.y;
             j.astride = q.astride ? q.astride : (uint64_t)nbk * f.ab;
-            j.ystride = mk_ystride(q);
+            j.ystride = gated ? q.ystride : mk_ystride(q);
             j.row_bytes = (uint64_t)nbk * f.bb;
             j.r0 = q.r0;
             j.r1 = q.r1;
@@ -791,7 +803,8 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
             j.na = q.na;
             j.tile0 = g->grid;
             j.ntok_tiles = (q.na + esq::MX_TOK - 1) / esq::MX_TOK;
-            const int row_tiles = (q.r1 - q.r0 + esq::MX_ROWS - 1) / esq::MX_ROWS;
+            const int trows = gated ? 256 : esq::MX_ROWS;   // the gated kernel's tiles are one block of h
+            const int row_tiles = (q.r1 - q.r0 + trows - 1) / trows;
             g->grid += j.ntok_tiles == 1 ? row_tiles : 8 * ((row_tiles + 7) / 8) * j.ntok_tiles;
             g->jobs.push_back(j);
             continue;
@@ -1025,6 +1038,7 @@ int launch_batch(const Batch &bt, const uint8_t *tables, int order, hipStream_t 
     for (const MkGroup &g : bt.mkg) {
         const esq::MkJob *dj = tables ? reinterpret_cast<const esq::MkJob *>(tables + g.off) : nullptr;
         if ((e = g.b32    ? esq::mbx_launch(g.type, g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
+                 : g.nbkm && g.gated ? esq::mxg_launch(g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
                  : g.nbkm ? esq::mx_launch(g.type, g.gather, g.nbkm, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)
                           : esq::mk_launch(g.type, g.gather, g.tok, dj, (int)g.jobs.size(), g.jobs[0], g.grid, order, s)) !=
             hipSuccess)
@@ -1573,6 +1587,7 @@ int es_hip_set_direct_persistent(int on) {
     return g_pk_on.exchange(on == 2 || on == 3 ? on : on ? 1 : 0);
 }
 int es_hip_set_q2k_expert_max_batch(int n) { g_cfg_gen.fetch_add(1); return g_mx_max.exchange(n); }
+int es_hip_set_moe_gated(int on) { g_cfg_gen.fetch_add(1); return g_moe_gated.exchange(on != 0 ? 1 : 0); }
 int es_hip_set_batched32_direct(int on) { g_cfg_gen.fetch_add(1); return g_mbx_on.exchange(on ? 1 : 0); }
 int es_hip_set_q6k_persistent(int on) { g_cfg_gen.fetch_add(1); return esq::mm6_set_persistent(on); }
 int es_hip_set_direct_mfma_tok64(int on) { g_cfg_gen.fetch_add(1); return g_mk_tok64.exchange(on ? 1 : 0); }
@@ -1846,6 +1861,7 @@ struct es_hip_moe_plan {
     int order = 0;
     int rows = 0, ff = 0, n = 0, ntok = 0, kmax = 0;
     bool h_q8k = true;
+    bool gated = false;          // gate/up on the gated expert kernel: h written as Q8_K blocks, no SwiGLU launch
     uint64_t hstride = 0, ostride = 0;
     float *bgu = nullptr, *bye = nullptr, *out = nullptr, *w = nullptr;
     uint8_t *ha = nullptr;
@@ -1952,11 +1968,22 @@ int moe_build(es_hip_moe_plan *p, const es_hip_moe *m, int N, const int *k, cons
     std::vector<int> ord(uex.size());
     for (size_t u = 0; u < ord.size(); u++) ord[u] = (int)u;
     std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return cnt[a] > cnt[b]; });
+    // Q2_K gate and up with a K-quant down: one gated product per expert when every expert's fits the gated kernel
+    auto gated_req = [&](int ex, int s0, int c) {
+        return Req{m->gate_type, m->gate[ex], x, reinterpret_cast<float *>(p->ha + (size_t)s0 * p->hstride), nullptr, nullptr,
+                   0, ff, n, c, xs, (size_t)p->hstride, arow + s0, N, m->up[ex]};
+    };
+    p->gated = g_moe_gated.load() && m->gate_type == ES_HIP_Q2_K && m->up_type == ES_HIP_Q2_K && p->h_q8k;
+    for (size_t u = 0; u < uex.size() && p->gated; u++) p->gated = mx_eligible(gated_req(uex[u], start[u], cnt[u]));
     for (int u : ord) {
         const int ex = uex[u], s0 = start[u], c = cnt[u];
         float *y = p->bgu + (size_t)s0 * 2 * ff;
-        gu.push_back({m->gate_type, m->gate[ex], x, y, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0, N});
-        gu.push_back({m->up_type, m->up[ex], x, y + ff, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0, N});
+        if (p->gated) {
+            gu.push_back(gated_req(ex, s0, c));
+        } else {
+            gu.push_back({m->gate_type, m->gate[ex], x, y, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0, N});
+            gu.push_back({m->up_type, m->up[ex], x, y + ff, nullptr, nullptr, 0, ff, n, c, xs, (size_t)2 * ff, arow + s0, N});
+        }
         dn.push_back({m->down_type, m->down[ex], p->ha + (size_t)s0 * p->hstride, p->bye + (size_t)s0 * n, nullptr, nullptr, 0, n,
                       ff, c, p->hstride, (size_t)n, nullptr});
     }
@@ -1978,7 +2005,7 @@ int moe_build(es_hip_moe_plan *p, const es_hip_moe *m, int N, const int *k, cons
 
 int moe_run(const es_hip_moe_plan *p, hipStream_t s) {
     if (int rc = launch_batch(p->gu, p->tabs + p->gu_tab, p->order, s)) return rc;
-    hipError_t e = esq::moe_swiglu_launch(p->bgu, p->rows, p->ff, p->h_q8k, p->ha, p->hstride, s);
+    hipError_t e = p->gated ? hipSuccess : esq::moe_swiglu_launch(p->bgu, p->rows, p->ff, p->h_q8k, p->ha, p->hstride, s);
     if (e != hipSuccess) return hip_fail(e, "SwiGLU launch");
     if (int rc = launch_batch(p->dn, p->tabs + p->dn_tab, p->order, s)) return rc;
     e = esq::moe_combine_launch(p->bye, p->rowof, p->w, p->kk, p->kmax, p->ntok, p->n, p->out, p->ostride, s);
@@ -2152,7 +2179,7 @@ struct MoeLaunch {
 
 int moe_family(es_hip_moe_ctx *c, uint32_t type, int rows, int cols, int umax, int njob, int R, double expect, int maxc,
                const uint8_t *w0, const uint8_t *act, const int *arow, uint64_t astride, float *y, uint64_t ystride,
-               uint8_t *ws, MoeLaunch &M) {
+               uint8_t *ws, MoeLaunch &M, bool gated = false) {
     FmtInfo f;
     fmt_info(type, f);
     const int nbk = cols / f.be;
@@ -2163,7 +2190,9 @@ int moe_family(es_hip_moe_ctx *c, uint32_t type, int rows, int cols, int umax, i
     // activation rows: the layer's tokens (gate/up, gathered) or its pair rows (down)
     if (moe_mx_family(type, rows, cols, expect, R, arow ? (size_t)std::max(maxc, 1) : (size_t)R, astride, ystride)) {
         M.F.kind = esq::MOE_FAM_MX;
-        const int row_tiles = (rows + esq::MX_ROWS - 1) / esq::MX_ROWS;
+        M.F.gated = gated ? 1 : 0;
+        const int trows = gated ? 256 : esq::MX_ROWS;   // the gated kernel's tiles are one block of h
+        const int row_tiles = (rows + trows - 1) / trows;
         M.F.mx_tiles = row_tiles;
         M.F.row_tiles8 = 8 * ((row_tiles + 7) / 8);
         esq::MkJob &j = M.F.mk;
@@ -2352,9 +2381,17 @@ int moe_ctx_layer(es_hip_moe_ctx *c, int N, const void *x, size_t xstride, float
     const uint64_t xs = xstride ? xstride : (uint64_t)(n / fg.be) * fg.ab;
     const double expect = (double)R / umax;   // choices per expert if every slot were used
     MoeLaunch G, D;
-    if (int rc = moe_family(c, c->gt, ff, n, umax, 2, R, expect, N, c->w_gate0, static_cast<const uint8_t *>(x), c->tok_of, xs,
-                            c->bgu, 2 * (uint64_t)ff, c->gu_ws, G))
+    // Q2_K gate and up with a K-quant down on the gated expert kernel: one job per expert slot, h written as Q8_K blocks
+    const bool gated = g_moe_gated.load() && c->gt == ES_HIP_Q2_K && c->h_q8k && ff % 256 == 0 &&
+                       moe_mx_family(c->gt, ff, n, expect, R, (size_t)std::max(N, 1), xs, c->hstride);
+    if (gated) {
+        if (int rc = moe_family(c, c->gt, ff, n, umax, 1, R, expect, N, c->w_gate0, static_cast<const uint8_t *>(x), c->tok_of,
+                                xs, reinterpret_cast<float *>(c->ha), c->hstride, c->gu_ws, G, true))
+            return rc;
+    } else if (int rc = moe_family(c, c->gt, ff, n, umax, 2, R, expect, N, c->w_gate0, static_cast<const uint8_t *>(x),
+                                   c->tok_of, xs, c->bgu, 2 * (uint64_t)ff, c->gu_ws, G)) {
         return rc;
+    }
     if (int rc = moe_family(c, c->dt, n, ff, umax, 1, R, expect, N, c->w_down0, c->ha, nullptr, c->hstride, c->bye, (uint64_t)n,
                             c->dn_ws, D))
         return rc;
@@ -2394,8 +2431,10 @@ int moe_ctx_layer(es_hip_moe_ctx *c, int N, const void *x, size_t xstride, float
             return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "MoE decode-kernel launch");
         }
         if (M.F.kind == esq::MOE_FAM_MX) {
-            e = esq::mx_launch((int)type, M.F.mk.arow != nullptr, M.F.mk.cols / 256, static_cast<const esq::MkJob *>(jobs),
-                               M.njobs, M.F.mk, M.grid, order, s);
+            e = M.F.gated ? esq::mxg_launch(M.F.mk.arow != nullptr, M.F.mk.cols / 256, static_cast<const esq::MkJob *>(jobs),
+                                            M.njobs, M.F.mk, M.grid, order, s)
+                          : esq::mx_launch((int)type, M.F.mk.arow != nullptr, M.F.mk.cols / 256,
+                                           static_cast<const esq::MkJob *>(jobs), M.njobs, M.F.mk, M.grid, order, s);
             return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "MoE expert-kernel launch");
         }
         if ((e = esq::prep_launch(prep, M.nprep, M.F.pj, M.items, s)) != hipSuccess) return hip_fail(e, "MoE pre-pass launch");
@@ -2403,7 +2442,8 @@ int moe_ctx_layer(es_hip_moe_ctx *c, int N, const void *x, size_t xstride, float
         return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "MoE matrix-core launch");
     };
     if (int rc = run(G, c->gt, c->gu_jobs, c->gu_prep)) return rc;
-    if ((e = esq::moe_swiglu_launch(c->bgu, R, ff, c->h_q8k, c->ha, c->hstride, s)) != hipSuccess) return hip_fail(e, "SwiGLU launch");
+    if (!G.F.gated && (e = esq::moe_swiglu_launch(c->bgu, R, ff, c->h_q8k, c->ha, c->hstride, s)) != hipSuccess)
+        return hip_fail(e, "SwiGLU launch");
     if (int rc = run(D, c->dt, c->dn_jobs, c->dn_prep)) return rc;
     e = esq::moe_combine_launch(c->bye, c->rowof, c->wv, c->kk, c->k, N, n, out, ostride ? ostride : (uint64_t)n, s);
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "combine launch");

@@ -246,7 +246,7 @@ class Lib:
             ("es_hip_run_jobs_host", i, [vp, i]),
             ("es_hip_set_mfma_min_batch", i, [i]), ("es_hip_set_small_batch_min", i, [i]),
             ("es_hip_set_mfma_tile", i, [i, i, i]),
-            ("es_hip_set_batched32_min", i, [i]), ("es_hip_set_batched32_mfma_min", i, [i]), ("es_hip_set_q6k_mfma_min_batch", i, [i]), ("es_hip_set_q2k_mfma_min_batch", i, [i]), ("es_hip_set_direct_mfma_min_batch", i, [i]), ("es_hip_set_direct_mfma_min_tiles", i, [i]), ("es_hip_set_q5k_mfma_min_batch", i, [i]), ("es_hip_set_q3k_mfma_min_batch", i, [i]), ("es_hip_set_q2k_expert_max_batch", i, [i]), ("es_hip_set_batched32_direct", i, [i]), ("es_hip_set_q6k_persistent", i, [i]), ("es_hip_set_direct_mfma_tok64", i, [i]), ("es_hip_set_direct_persistent", i, [i]),
+            ("es_hip_set_batched32_min", i, [i]), ("es_hip_set_batched32_mfma_min", i, [i]), ("es_hip_set_q6k_mfma_min_batch", i, [i]), ("es_hip_set_q2k_mfma_min_batch", i, [i]), ("es_hip_set_direct_mfma_min_batch", i, [i]), ("es_hip_set_direct_mfma_min_tiles", i, [i]), ("es_hip_set_q5k_mfma_min_batch", i, [i]), ("es_hip_set_q3k_mfma_min_batch", i, [i]), ("es_hip_set_q2k_expert_max_batch", i, [i]), ("es_hip_set_moe_gated", i, [i]), ("es_hip_set_batched32_direct", i, [i]), ("es_hip_set_q6k_persistent", i, [i]), ("es_hip_set_direct_mfma_tok64", i, [i]), ("es_hip_set_direct_persistent", i, [i]),
             ("es_hip_moe_ffn", i, [vp, i, vp, vp, vp, i, vp, sz, vp, sz, vp]),
             ("es_hip_moe_plan_create", vp, [vp, i, vp, vp, vp, i, vp, sz, vp, sz]),
             ("es_hip_moe_plan_run", i, [vp, vp]), ("es_hip_moe_plan_destroy", None, [vp]),
@@ -320,6 +320,9 @@ class Lib:
 
     def set_q2k_expert_max_batch(self, n: int) -> int:
         return self._L.es_hip_set_q2k_expert_max_batch(n)
+
+    def set_moe_gated(self, on: int) -> int:
+        return self._L.es_hip_set_moe_gated(on)
 
     def set_batched32_direct(self, on: int) -> int:
         return self._L.es_hip_set_batched32_direct(on)

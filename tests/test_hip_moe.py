@@ -67,18 +67,24 @@ def test_swiglu_bit_exact(hip, orc):
     assert same.all(), np.flatnonzero(~same)[:10]
 
 
+@pytest.mark.parametrize("gated", [1, 0], ids=["gated", "two-job"])
 @pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
-def test_moe_config4_olmoe_q2k(hipo, orc, mode):
-    """config 4: 64 experts of Q2_K (gate/up 1024x2048, down 2048x1024), 128 tokens, top-8 softmax, no renormalisation"""
+def test_moe_config4_olmoe_q2k(hipo, orc, mode, gated):
+    """config 4: 64 experts of Q2_K (gate/up 1024x2048, down 2048x1024), 128 tokens, top-8 softmax, no renormalisation;
+    gate and up in one workgroup writing SwiGLU's Q8_K blocks (gated), or as two jobs and a SwiGLU pass"""
     hipo.set_order(mode[0])
-    n, ff, n_exp, kmax, N = 2048, 1024, 64, 8, 128
-    types = (E.Q2_K, E.Q2_K, E.Q2_K)
-    ex = Experts(hipo, orc, types, n_exp, n, ff, 46)
-    sel, w = routed(orc, N, n_exp, kmax, False, 1238)
-    x = orc.quantize_act(E.Q2_K, orc.gauss(11, 1.0, N * n).reshape(N, n))
-    out = run_gpu(hipo, ex, x, np.full(N, kmax), sel, w)
-    ref = orc.moe_ffn(types, ex.host, n, ff, x, sel, w, order=mode[1], path=mode[2])
-    assert np.array_equal(bits(out), bits(ref))
+    prev = hipo.set_moe_gated(gated)
+    try:
+        n, ff, n_exp, kmax, N = 2048, 1024, 64, 8, 128
+        types = (E.Q2_K, E.Q2_K, E.Q2_K)
+        ex = Experts(hipo, orc, types, n_exp, n, ff, 46)
+        sel, w = routed(orc, N, n_exp, kmax, False, 1238)
+        x = orc.quantize_act(E.Q2_K, orc.gauss(11, 1.0, N * n).reshape(N, n))
+        out = run_gpu(hipo, ex, x, np.full(N, kmax), sel, w)
+        ref = orc.moe_ffn(types, ex.host, n, ff, x, sel, w, order=mode[1], path=mode[2])
+        assert np.array_equal(bits(out), bits(ref))
+    finally:
+        hipo.set_moe_gated(prev)
 
 
 def test_moe_config5_qwen3_mixed(hipo, orc):

@@ -36,13 +36,15 @@ def run_logits(hip, ctx, orc, ex, N, n_exp, k, norm, seed, xseed):
     return x, out, sel, w
 
 
-@pytest.mark.parametrize("family", ["expert", "prepass"])
+@pytest.mark.parametrize("family", ["expert", "expert-two-job", "prepass"])
 @pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
 def test_ctx_config4_olmoe_q2k_from_logits(hipo, orc, mode, family):
     """config 4: 64 Q2_K experts (gate/up 1024x2048, down 2048x1024), 128 tokens top-8: the expert-sized kernel family
-    (default) and the pre-pass + matrix-core family (the expert kernel switched off)"""
+    (default) with gate and up in one workgroup writing SwiGLU's Q8_K blocks, the same family with gate and up as two jobs
+    and a SwiGLU pass, and the pre-pass + matrix-core family (the expert kernel switched off)"""
     hipo.set_order(mode[0])
-    prev = hipo.set_q2k_expert_max_batch(64 if family == "expert" else 1)
+    prev = hipo.set_q2k_expert_max_batch(1 if family == "prepass" else 64)
+    prev_g = hipo.set_moe_gated(0 if family == "expert-two-job" else 1)
     try:
         n, ff, n_exp, k, N = 2048, 1024, 64, 8, 128
         types = (E.Q2_K, E.Q2_K, E.Q2_K)
@@ -56,6 +58,7 @@ def test_ctx_config4_olmoe_q2k_from_logits(hipo, orc, mode, family):
         ctx.close()
     finally:
         hipo.set_q2k_expert_max_batch(prev)
+        hipo.set_moe_gated(prev_g)
 
 
 def test_ctx_config5_qwen3_mixed_from_logits(hipo, orc):
