@@ -217,18 +217,22 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_q6k_kernel(const MmJob *__res
         // ---- A operands: per slice ks the four planes, and the scales as halves for corr
         const uint32_t u[4] = {scw.x ^ 0x80808080u, scw.y ^ 0x80808080u, scw.z ^ 0x80808080u, scw.w ^ 0x80808080u};   // sc + 128
         v4i p1[4], p2[4], p3[4], p4[4];
+        // the qh dwords shifted by this lane's field pair once (2 qo bits): field 2 qn + qo of each byte then sits at bits
+        // 4 qn .. 4 qn + 1, so slice ks takes it with one shift (qn = 0) or none (qn = 1)
+        const uint32_t qs0[4] = {qh0.x >> (2 * qo), qh0.y >> (2 * qo), qh0.z >> (2 * qo), qh0.w >> (2 * qo)};
+        const uint32_t qs1[4] = {qh1.x >> (2 * qo), qh1.y >> (2 * qo), qh1.z >> (2 * qo), qh1.w >> (2 * qo)};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int n = ks >> 1, qn = ks & 1;
             const uint32_t lsc = __builtin_amdgcn_perm(0, u[ks] & 0x0f0f0f0fu, sel);          // l, in both halves
             const uint32_t hsc = __builtin_amdgcn_perm(0, (u[ks] >> 4) & 0x0f0f0f0fu, sel);   // h
-            const uint4 qlv = n ? ql1 : ql0, qhv = n ? qh1 : qh0;
-            const uint32_t qlw[4] = {qlv.x, qlv.y, qlv.z, qlv.w}, qhw[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
-            const uint32_t shq = 4 * qn + 2 * qo;
+            const uint4 qlv = n ? ql1 : ql0;
+            const uint32_t qlw[4] = {qlv.x, qlv.y, qlv.z, qlv.w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t nib = qn ? (qlw[i] >> 4) & 0x0f0f0f0fu : qlw[i] & 0x0f0f0f0fu;
-                const uint32_t qu = nib | (((qhw[i] >> shq) & 0x03030303u) << 4);   // 6-bit codes, one per byte
+                const uint32_t qsw = n ? qs1[i] : qs0[i];
+                const uint32_t qu = nib | ((qn ? qsw : qsw << 4) & 0x30303030u);   // 6-bit codes, one per byte
                 const uint32_t a = (qu >> 3) & 0x07070707u, bb = qu & 0x07070707u;
                 // a h - q_u per byte: (a h + 128 - q_u) stays in 65..233, so no borrow crosses a byte
                 p1[ks][i] = (int)(((pk_mul_u16(a, hsc) | 0x80808080u) - qu) ^ 0x80808080u);
