@@ -124,7 +124,7 @@ class Workload:
             b.close()
 
 
-def route_topk(rng, n_tok, n_exp, k, norm_topk):
+def route_topk(rng, n_tok, n_exp, k, norm_topk, with_logits=False):
     """synthetic routing: softmax over N(0,1) logits, the k largest probabilities (route(), src/es_engine.c:744-835)"""
     logits = rng.standard_normal((n_tok, n_exp)).astype(np.float32)
     p = np.exp(logits - logits.max(axis=1, keepdims=True))
@@ -133,7 +133,7 @@ def route_topk(rng, n_tok, n_exp, k, norm_topk):
     w = np.take_along_axis(p, sel, axis=1).astype(np.float32)
     if norm_topk:
         w /= w.sum(axis=1, keepdims=True)
-    return sel, w
+    return (sel, w, logits) if with_logits else (sel, w)
 
 
 def moe_rng(config):
@@ -150,7 +150,7 @@ class MoeWorkload:
         self.lib, self.keep, self.plans, self.moe, self.ctx_args = lib, [], [], [], []
         self.n_tok, self.n_exp, self.n, self.norm = n_tok, n_exp, n, norm_topk
         gt, ut, dt = types
-        sel, w = route_topk(rng, n_tok, n_exp, k, norm_topk)
+        sel, w, plan_logits = route_topk(rng, n_tok, n_exp, k, norm_topk, with_logits=True)
         used = sorted(set(sel.reshape(-1).tolist()))
         eb = [E.row_bytes(gt, n) * ff, E.row_bytes(ut, n) * ff, E.row_bytes(dt, ff) * n]
         self.weight_bytes = copies * len(used) * sum(eb)
@@ -159,9 +159,11 @@ class MoeWorkload:
         dx = lib.upload(x)
         self.keep.append(dx)
         self.dx, self.xstride = dx, x.strides[0]
-        # router logits for the device-routed leg: a fresh routing every step (8 sets in rotation)
+        # router logits for the device-routed leg: a fresh routing every step (8 sets in rotation), or the logits of the
+        # plan's own routing (the same experts and counts as the plan, routed again on the device every step)
         self.logits = [lib.upload(rng.standard_normal((n_tok, n_exp)).astype(np.float32)) for _ in range(8)]
-        self.keep += self.logits
+        self.plan_logits = lib.upload(plan_logits)
+        self.keep += self.logits + [self.plan_logits]
         xa = quantize_acts(E.Q5_0, rng.standard_normal((n_tok, n)).astype(np.float32)) if attn else None
         dxa = lib.upload(xa) if attn else None
         for c in range(copies):
@@ -205,18 +207,19 @@ class MoeWorkload:
             self.lib.step_time_ms(self.plans, self.moe, 0, 2)
         return self.lib.step_time_ms(self.plans, self.moe, warmup, steps) / self.copies
 
-    def time_device_routed(self, warmup, steps):
-        """ms per copy (one layer) with the routing computed on the device from fresh logits every step and the layer run
-        through its context (es_hip_moe_ctx_run_logits: grouping and job tables on the device, no host round trip), the
-        attention plans as in time(); HIP events on the null stream around `steps` steps"""
+    def time_device_routed(self, warmup, steps, same_routing=False):
+        """ms per copy (one layer) with the routing computed on the device from fresh logits every step (same_routing:
+        from the logits of the plan's routing, so the layer reads the same experts as time()) and the layer run through
+        its context (es_hip_moe_ctx_run_logits: grouping and job tables on the device, no host round trip), the attention
+        plans as in time(); HIP events on the null stream around `steps` steps"""
         it = [0]
 
         def step():
             for i, (ctx, out) in enumerate(self.ctx_args):
                 if self.plans:
                     self.plans[i].run()
-                ctx.run_logits(self.n_tok, self.logits[it[0] % len(self.logits)], 0, self.norm, self.dx, self.xstride, out,
-                               self.n)
+                lg = self.plan_logits if same_routing else self.logits[it[0] % len(self.logits)]
+                ctx.run_logits(self.n_tok, lg, 0, self.norm, self.dx, self.xstride, out, self.n)
             it[0] += 1
 
         t_end = time.perf_counter() + SETTLE_S
@@ -514,6 +517,7 @@ def only(lib, rng, name, K, Wm, moe_leg="both"):
             out["ms_per_layer"] = round(w.time(Wm, K), 4)
         if moe_leg in ("both", "device"):
             out["device_routed_ms_per_layer"] = round(w.time_device_routed(Wm, K), 4)
+            out["device_routed_same_routing_ms_per_layer"] = round(w.time_device_routed(Wm, K, same_routing=True), 4)
         w.close()
         return out
     if name.startswith("decode_"):   # config 2's decode in another weight format (same shapes, same 38 layer copies)
@@ -602,10 +606,13 @@ def main():
     c4 = MoeWorkload(lib, moe_rng(4), (E.Q2_K, E.Q2_K, E.Q2_K), 2048, 1024, 64, 8, 128, False, 8)
     e4 = c4.time(Wm, max(3, K // 2))
     d4 = c4.time_device_routed(Wm, max(3, K // 2))
+    s4 = c4.time_device_routed(Wm, max(3, K // 2), same_routing=True)
     extra["config4_q2_k_moe"] = {"gbs": round(c4.weight_bytes / c4.copies / (e4 * 1e-3) / 1e9, 1), "ms": round(e4, 4),
                                  "weight_bytes": c4.weight_bytes // c4.copies, "experts_used": c4.distinct,
                                  "hbm_frac": round(c4.weight_bytes / c4.copies / (e4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                 "device_routed_ms": round(d4, 4), "device_routed_vs_plan": round(d4 / e4, 3)}
+                                 "device_routed_ms": round(d4, 4), "device_routed_vs_plan": round(d4 / e4, 3),
+                                 "device_routed_same_routing_ms": round(s4, 4),
+                                 "device_routed_same_routing_vs_plan": round(s4 / e4, 3)}
     c4.close()
     # ---- config 5: Qwen3-30B-A3B-like decode batch of 32: Q5_0 attention q/k/v + 128 experts (Q4_K gate/up 768x2048,
     # Q6_K down 2048x768) top-8 renormalised; 3 layer copies
@@ -613,11 +620,14 @@ def main():
                      attn=((4096, 2048), (512, 2048), (512, 2048)))
     e5 = c5.time(Wm, max(3, K // 2))
     d5 = c5.time_device_routed(Wm, max(3, K // 2))
+    s5 = c5.time_device_routed(Wm, max(3, K // 2), same_routing=True)
     extra["config5_mixed_moe_decode"] = {"gbs": round(c5.weight_bytes / c5.copies / (e5 * 1e-3) / 1e9, 1),
                                          "ms": round(e5, 4), "weight_bytes": c5.weight_bytes // c5.copies,
                                          "experts_used": c5.distinct,
                                          "hbm_frac": round(c5.weight_bytes / c5.copies / (e5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                         "device_routed_ms": round(d5, 4), "device_routed_vs_plan": round(d5 / e5, 3)}
+                                         "device_routed_ms": round(d5, 4), "device_routed_vs_plan": round(d5 / e5, 3),
+                                         "device_routed_same_routing_ms": round(s5, 4),
+                                         "device_routed_same_routing_vs_plan": round(s5 / e5, 3)}
     c5.close()
     # ---- device activation preparation at config 2's prefill shapes (rmsnorm / SwiGLU fused with the quantizers)
     extra["act_prep_t512"] = act_prep_times(lib, rng, K, Wm)
