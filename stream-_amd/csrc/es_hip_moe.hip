@@ -362,9 +362,11 @@ struct MoeBuildArgs {
     MoeFamily GU, DN;
 };
 static_assert(sizeof(MoeBuildArgs) % 4 == 0 && sizeof(MoeBuildArgs) / 4 <= MOE_GROUP_THREADS, "one dword per thread");
+static_assert(MOE_MAX_PAIRS <= (1 << 20) && ROUTE_MAX_EXPERTS <= 1024, "slot order keys fit an int");
 
 __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArgs P) {
-    __shared__ int first[ROUTE_MAX_EXPERTS], cnt[ROUTE_MAX_EXPERTS], slot[ROUTE_MAX_EXPERTS], taken[ROUTE_MAX_EXPERTS];
+    __shared__ __align__(16) int first[ROUTE_MAX_EXPERTS];
+    __shared__ int cnt[ROUTE_MAX_EXPERTS], slot[ROUTE_MAX_EXPERTS], taken[ROUTE_MAX_EXPERTS];
     __shared__ int uex[ROUTE_MAX_EXPERTS], ustart[ROUTE_MAX_EXPERTS];
     __shared__ int wcnt[MOE_GROUP_THREADS / 64][ROUTE_MAX_EXPERTS];   // per wave of a chunk: choices of each expert
     __shared__ int3 wsum[MOE_GROUP_THREADS / 64];
@@ -474,20 +476,34 @@ __global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_build(MoeBuildArg
     // ---- job tables. With a decode-kernel family, slots go by token count, most first (ties in slot order), so the
     // launch starts its longest workgroups first (the expert-sized and matrix-core families keep slot order, which
     // measured as fast); the pair rows keep their slot order. Thread r writes the jobs of the slot ranked r; tiles and
-    // pre-pass items are prefix sums in that order. (first and taken are free once the rows are placed.)
+    // pre-pass items are prefix sums in that order. (first, slot and taken are free once the rows are placed.)
     const bool by_count = sa.GU.kind == MOE_FAM_MV || sa.DN.kind == MOE_FAM_MV;
-    if (by_count && tid < U) first[tid] = c_me;
-    lds_sync();
-    if (tid < U) {
-        int rank = tid;
-        if (by_count) {
-            rank = 0;
-            for (int v = 0; v < U; v++) {
-                const int cv = first[v];
-                rank += (cv > c_me || (cv == c_me && v < tid)) ? 1 : 0;
+    // slot u's order key: its count, then the earlier slot first (counts <= MOE_MAX_PAIRS and slots < 1024, so the key
+    // fits 25 bits and no two are equal); keys padded with -1 to a multiple of four
+    const int U4 = (U + 3) & ~3;
+    if (by_count) {
+        if (tid < U4) first[tid] = tid < U ? c_me << 10 | (1023 - tid) : -1;
+        if (tid < U) slot[tid] = 0;   // the ranks' partial counts
+        lds_sync();
+        // rank of slot u = the keys above its own: thread t counts slot t % S's among keys part t / S of PARTS (S the
+        // power of two >= U), the parts' counts added in LDS
+        const int S = U <= 1 ? 1 : 1 << (32 - __builtin_clz(U - 1)), parts = MOE_GROUP_THREADS / S;
+        const int su = tid & (S - 1), part = tid / S;
+        const int q4 = U4 >> 2, per = (q4 + parts - 1) / parts, v0 = part * per, v1 = min(q4, v0 + per);
+        if (su < U && v0 < v1) {
+            const int me = first[su];
+            const int4 *f4 = reinterpret_cast<const int4 *>(first);
+            int r = 0;
+            for (int v = v0; v < v1; v++) {   // four keys per read, the same address for every lane of a part
+                const int4 q = f4[v];
+                r += (q.x > me ? 1 : 0) + (q.y > me ? 1 : 0) + (q.z > me ? 1 : 0) + (q.w > me ? 1 : 0);
             }
+            atomicAdd(&slot[su], r);
         }
-        taken[rank] = tid;
+        lds_sync();
+        if (tid < U) taken[slot[tid]] = tid;
+    } else if (tid < U) {
+        taken[tid] = tid;
     }
     lds_sync();
     const int u = tid < U ? taken[tid] : tid;   // the slot whose jobs this thread writes, at position tid
