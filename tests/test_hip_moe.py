@@ -99,11 +99,22 @@ def test_moe_config5_qwen3_mixed(hipo, orc):
     assert np.array_equal(bits(out), bits(ref))
 
 
-@pytest.mark.parametrize("types", [(E.Q4_K, E.Q4_K, E.Q5_0), (E.Q5_0, E.Q5_0, E.Q4_0), (E.Q6_K, E.Q6_K, E.Q2_K)],
-                         ids=["q4k-q50", "q50-q40", "q6k-q2k"])
-def test_moe_variable_k_and_gathers(hipo, orc, types):
+@pytest.mark.parametrize("types,gated", [((E.Q4_K, E.Q4_K, E.Q5_0), 1), ((E.Q5_0, E.Q5_0, E.Q4_0), 1),
+                                         ((E.Q6_K, E.Q6_K, E.Q2_K), 1), ((E.Q2_K, E.Q2_K, E.Q2_K), 1),
+                                         ((E.Q2_K, E.Q2_K, E.Q2_K), 0)],
+                         ids=["q4k-q50", "q50-q40", "q6k-q2k", "q2k-gated", "q2k-two-job"])
+def test_moe_variable_k_and_gathers(hipo, orc, types, gated):
     """tokens with 0..kmax experts, experts chosen by several tokens, one expert taking 40 tokens (the matrix-core path
-    with its activation gather for Q4_K), a token stride with padding, Q8_0 requantization for a 32-wide down type"""
+    with its activation gather for Q4_K; for Q2_K two activation tiles of the expert-sized kernel, gated or not), a token
+    stride with padding, Q8_0 requantization for a 32-wide down type"""
+    prev = hipo.set_moe_gated(gated)
+    try:
+        run_variable_k(hipo, orc, types)
+    finally:
+        hipo.set_moe_gated(prev)
+
+
+def run_variable_k(hipo, orc, types):
     n, ff, n_exp, kmax, N = 512, 256, 6, 3, 45
     ex = Experts(hipo, orc, types, n_exp, n, ff, 48)
     rng = np.random.default_rng(4)
