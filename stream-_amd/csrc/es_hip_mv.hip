@@ -34,6 +34,16 @@
 #ifndef K_UNITSN
 #define K_UNITSN 2
 #endif
+// the same at two activations per pass in the per-job-width kernel, whose register budget the four-wide body sets
+#ifndef K_UNITS2M
+#define K_UNITS2M 4
+#endif
+#ifndef Q6K_UNITS2M
+#define Q6K_UNITS2M 1
+#endif
+#ifndef Q6K_UNITS1M
+#define Q6K_UNITS1M 2
+#endif
 // resident waves per SIMD the register allocation must allow
 #ifndef ESQ_MIN_WAVES
 #define ESQ_MIN_WAVES 1
@@ -496,6 +506,12 @@ template <int F, int NT> constexpr int units() {
     else if constexpr (!is32<F>()) return NT == 1 ? ESQ_UNITS : K_UNITSN;
     else return ESQ_UNITS;
 }
+// units of the one- and two-wide bodies of mv_kernel_mixed (0: as units())
+template <int F, int NT> constexpr int units_mixed() {
+    if constexpr (F == ES_HIP_Q6_K || F == ES_HIP_Q3_K) return NT == 1 ? Q6K_UNITS1M : Q6K_UNITS2M;
+    else if constexpr (!is32<F>()) return NT == 1 ? 0 : K_UNITS2M;
+    else return 0;
+}
 
 // ---------------------------------------------------------------------------------------------------------------------
 // The kernel
@@ -506,13 +522,13 @@ template <int F, int NT> constexpr int units() {
 // activation slices for each). All waves write their blocks' float terms to the workgroup's LDS, then the
 // whole workgroup runs the per-row chains. order: ES_HIP_ORDER_*; NT activations per pass. One workgroup per tile
 // (rows_per_wg rows of one job).
-template <int F, int NT, int W, bool SEGLOOP>
+template <int F, int NT, int W, bool SEGLOOP, int UO = 0>
 __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
     using L = Lane<F>;
     constexpr int LPB = Fmt<F>::LPB, BE = Fmt<F>::BE, BB = Fmt<F>::BB, AB = Fmt<F>::AB;
     constexpr int SLOTS = WAVE / LPB;
     constexpr bool W32 = is32<F>();
-    constexpr int U = units<F, NT>();   // row passes whose raw loads a wave issues before using any of them
+    constexpr int U = UO ? UO : units<F, NT>();   // row passes whose raw loads a wave issues before using any of them
 
     const int nbk = J.cols / BE;
     const int tile = blockIdx.x - J.tile0;
@@ -717,8 +733,8 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel_mixed(const
     if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
     switch (J.nt) {
-    case 1: mv_body<F, 1, W, SEGLOOP>(J, order); break;
-    case 2: mv_body<F, 2, W, SEGLOOP>(J, order); break;
+    case 1: mv_body<F, 1, W, SEGLOOP, units_mixed<F, 1>()>(J, order); break;
+    case 2: mv_body<F, 2, W, SEGLOOP, units_mixed<F, 2>()>(J, order); break;
     default: mv_body<F, 4, W, SEGLOOP>(J, order); break;
     }
 }
