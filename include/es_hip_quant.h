@@ -151,10 +151,14 @@ int es_hip_unregister(const void *host);
 /* es_matvec / es_matvec_multi (src/es_quant.h:44-47): host W, host activations (a->q80 for Q4_0/Q5_0/Q8_0, a->q8 for the
  * K-quants; an activation without them takes the float path from a->x, as in the reference), host y. Synchronous. The
  * scratch argument is unused (kept for the prototype). They clear es_hip_last_error() on entry; on failure y is left
- * untouched and es_hip_last_error() says why (the reference's void prototype has no other error channel). Row length
- * limit (every product entry point but the float path's): at most ES_HIP_MAX_COLS_32 columns for the 32-element formats
- * (Q4_0, Q5_0, Q8_0) and ES_HIP_MAX_COLS_256 for the K-quants (one row's float terms stay in a workgroup's LDS in the decode
- * kernel); a longer row is refused with ES_HIP_EINVAL, where the reference takes any multiple of the block size. */
+ * untouched and es_hip_last_error() says why (the reference's void prototype has no other error channel). Row length:
+ * any multiple of the block size, as in the reference. Rows past ES_HIP_MAX_COLS_32 columns for the 32-element formats
+ * (Q4_0, Q5_0, Q8_0) or ES_HIP_MAX_COLS_256 for the K-quants (where one row's float terms stop fitting a workgroup's LDS
+ * in the decode kernel) run as column pieces of at most that length, one launch each in stream order, every piece
+ * continuing the sums where the previous one stopped (the same outputs; the AVX2 order's lane sums between pieces take a
+ * stream-ordered allocation). This holds for es_hip_matvec[_multi], es_hip_matvec[_multi]_dev, es_hip_run_jobs[_host];
+ * the entry points that keep or pre-size their job tables (es_hip_plan_*, es_hip_matvec_multi_dev_noalloc, the dense and
+ * MoE layers) refuse longer rows with ES_HIP_EINVAL. */
 #define ES_HIP_MAX_COLS_32 131072
 #define ES_HIP_MAX_COLS_256 1048576
 void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch);

@@ -37,7 +37,14 @@ struct MvJob {
     int r0, r1, cols, na;
     int tile0, rows_per_wg, chain_rows;
     int nt;               // activations per pass (1, 2 or 4): the launch's, or this job's in a launch of mixed widths
+    // A row longer than one workgroup's LDS holds is run as consecutive column pieces, one launch each, every piece
+    // continuing the chains where the previous one stopped (MV_CHAIN_* flags; 0 for a whole row). The AVX2 order of
+    // the 32-element formats carries eight lane chains per output between pieces, in lanes[((q * (r1 - r0) + r - r0) * 8 + i].
+    int chain;
+    float *lanes;
 };
+constexpr int MV_CHAIN_IN = 1;          // the chains start from the previous piece's values (y, or lanes)
+constexpr int MV_CHAIN_LANES_OUT = 2;   // (AVX2 order, not the last piece) the eight lane chains go to lanes, y untouched
 
 // Floats per row of the decode kernel's LDS terms (nbk blocks, nt activations): the K-quants' 2 per (block, activation)
 // plus one, so the pitch is odd; the 32-element formats' 9 per (block, activation).

@@ -685,6 +685,12 @@ __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
                 const float *e = lds + (size_t)rl * P + t * CW;
                 const int oa = cmode == CH_LANES ? 1 + i : 0, ob = cmode == CH_LANES ? 0 : 1;
                 float s = 0.0f;
+                size_t lane_at = 0;
+                if constexpr (SEGLOOP) {   // (column pieces of long rows run on the SEGLOOP launches only)
+                    lane_at = ((size_t)(t0 + t) * (J.r1 - J.r0) + (ra + rl - J.r0)) * 8 + i;
+                    if (J.chain & MV_CHAIN_IN)   // a later piece of a long row: the chains so far
+                        s = cmode == CH_LANES ? ldg<float>(J.lanes + lane_at) : ldg<float>(J.y + (size_t)(t0 + t) * J.ystride + ra + rl);
+                }
                 int bb = 0;
                 for (; bb + 8 <= nbk; bb += 8) {
                     float ta[8], tb[8];
@@ -701,6 +707,12 @@ __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
                 for (; bb < nbk; bb++) {
                     const float ta = e[bb * NT * CW + oa], tb = e[bb * NT * CW + ob];
                     s = cmode == CH_MULADD ? s + ta * tb : __builtin_fmaf(ta, tb, s);
+                }
+                if constexpr (SEGLOOP) {
+                    if (J.chain & MV_CHAIN_LANES_OUT) {   // the eight chains continue in the next piece
+                        stg<float>(J.lanes + lane_at, s);
+                        continue;
+                    }
                 }
                 if (cmode == CH_LANES) {   // hsum_ps of the eight lanes: ((0+4)+(2+6))+((1+5)+(3+7))  (src/es_quant.c:1185-1187)
                     s = s + __shfl_xor(s, 4);

@@ -132,9 +132,14 @@ struct Req {   // one product as the launch planner sees it
     const int *arow;   // optional device gather table: activation q is row arow[q] of act
     int act_rows = 0;  // rows of act a gather may index (0: na)
     const void *W2 = nullptr;   // a gated expert product (Q2_K): the up rows; y then holds h's Q8_K blocks (bytes)
+    // a column piece of a longer row (decode kernel only): the whole row's bytes, MV_CHAIN_* flags, the lane chains
+    size_t row_bytes = 0;
+    int chain = 0;
+    float *lanes = nullptr;
 };
 
-int check_req(const Req &q, const FmtInfo &f) {
+// whole_row: the row length limit applies (a request the entry point does not cut into column pieces)
+int check_req(const Req &q, const FmtInfo &f, bool whole_row = true) {
     if (q.cols <= 0 || q.cols % f.be) return fail(ES_HIP_EINVAL, "type %u: cols %d is not a positive multiple of %d", q.type, q.cols, f.be);
     if (q.r0 < 0 || q.r1 < q.r0) return fail(ES_HIP_EINVAL, "bad row range [%d, %d)", q.r0, q.r1);
     if (q.na < 0) return fail(ES_HIP_EINVAL, "negative activation count %d", q.na);
@@ -155,7 +160,7 @@ int check_req(const Req &q, const FmtInfo &f) {
                   (size_t)esq::mv_row_pitch(false, ES_HIP_MAX_COLS_256 / 256, 1) * 4 <= LDS_MAX,
                   "the header's row limits fit one row's terms");
     const int cmax = f.be == 32 ? ES_HIP_MAX_COLS_32 : ES_HIP_MAX_COLS_256;
-    if (q.cols > cmax)
+    if (whole_row && q.cols > cmax)
         return fail(ES_HIP_EINVAL, "type %u: cols %d above the %d this library handles (ES_HIP_MAX_COLS_*)", q.type, q.cols, cmax);
     (void)nbk;
     return ES_HIP_OK;
@@ -175,6 +180,7 @@ int segments(int nbk, int slots) {
 }
 
 // Plan the launches: one per (format, workgroup size). The job order inside a launch is kept.
+constexpr int PIECES = 16;   // (in a launch key: column pieces of long rows)
 int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
     out.clear();
     std::map<std::pair<uint32_t, int>, std::vector<const Req *>> by_kind;
@@ -185,8 +191,10 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
         int rc = check_req(q, f);
         if (rc) return rc;
         if (q.r1 == q.r0 || q.na == 0) continue;
+        // launches by format and workgroup size; column pieces of long rows (whose chains only the 8-wave launches that
+        // take several block groups per wave carry) in launches of their own
         const int seg = segments(q.cols / f.be, 64 / f.lpb);
-        by_kind[{q.type, seg <= 4 ? 4 : 8}].push_back(&q);
+        by_kind[{q.type, q.row_bytes ? 8 | PIECES : seg <= 4 ? 4 : 8}].push_back(&q);
         total_blocks += (size_t)(q.r1 - q.r0) * (q.cols / f.be);
     }
     // workgroups of about total/TARGET_WG blocks each, each wave making at least MIN_ITERS row passes, so one launch keeps
@@ -197,14 +205,14 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
         fmt_info(kv.first.first, f);
         const bool w32 = f.be == 32;
         const int slots = 64 / f.lpb;
-        const int waves = kv.first.second;
+        const int waves = kv.first.second & ~PIECES;
         Group g;
         int max_na = 1, max_nbk = 1;
         for (const Req *q : kv.second) {
             max_na = std::max(max_na, q->na);
             max_nbk = std::max(max_nbk, q->cols / f.be);
         }
-        g.L.seg_loop = segments(max_nbk, slots) > waves;
+        g.L.seg_loop = segments(max_nbk, slots) > waves || (kv.first.second & PIECES);
         // activations per pass: 3 in one pass of 4 rather than two passes of 2; at most what keeps one row's terms in LDS.
         // Jobs of different counts (an MoE layer's experts) each take their own width in one launch of mixed widths.
         int nt_cap = 4;
@@ -240,7 +248,9 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
             j.arow = q->arow;
             j.astride = q->astride ? q->astride : (size_t)nbk * f.ab;
             j.ystride = q->ystride;
-            j.row_bytes = (size_t)nbk * f.bb;
+            j.row_bytes = q->row_bytes ? q->row_bytes : (size_t)nbk * f.bb;
+            j.chain = q->chain;
+            j.lanes = q->lanes;
             j.r0 = q->r0;
             j.r1 = q->r1;
             j.cols = q->cols;
@@ -260,8 +270,8 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
     return ES_HIP_OK;
 }
 
-int launch_single(const Group &g, hipStream_t s) {
-    hipError_t e = esq::mv_launch(g.L, nullptr, 1, g.jobs[0], g_order.load(), s);
+int launch_single(const Group &g, hipStream_t s, int order = -1) {
+    hipError_t e = esq::mv_launch(g.L, nullptr, 1, g.jobs[0], order >= 0 ? order : g_order.load(), s);
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "kernel launch");
 }
 
@@ -705,6 +715,10 @@ int plan_batch(const std::vector<Req> &reqs, Batch &bt, bool allow_pk = true) {
         FmtInfo f;
         if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
         if (int rc = check_req(q, f)) return rc;
+        if (q.row_bytes) {   // a piece of a long row: the decode kernel carries its chains
+            mv.push_back(q);
+            continue;
+        }
         if (mb_eligible(q)) {   // batched 32-wide: activation groups of at most 64
             const int mm = g_mbm_min.load();   // (the matrix-core kernels address a matrix with 32-bit offsets)
             const bool mfma = mm > 0 && q.na >= mm && (size_t)q.r1 * (q.cols / 32) * f.bb < ((size_t)1 << 31);
@@ -1180,14 +1194,22 @@ bool same_reqs(const std::vector<Req> &a, const std::vector<Req> &b) {
         const Req &x = a[i], &y = b[i];
         if (x.type != y.type || x.W != y.W || x.act != y.act || x.y != y.y || x.ints != y.ints || x.aux != y.aux ||
             x.r0 != y.r0 || x.r1 != y.r1 || x.cols != y.cols || x.na != y.na || x.astride != y.astride ||
-            x.ystride != y.ystride || x.arow != y.arow || x.act_rows != y.act_rows)
+            x.ystride != y.ystride || x.arow != y.arow || x.act_rows != y.act_rows || x.row_bytes != y.row_bytes ||
+            x.chain != y.chain || x.lanes != y.lanes)
             return false;
     }
     return true;
 }
 
 // A kept batch for reqs, launched on s: 1 if launched (rc set), 0 if none is kept.
+bool has_pieces(const std::vector<Req> &reqs) {
+    for (const Req &q : reqs)
+        if (q.row_bytes) return true;
+    return false;
+}
+
 int cached_launch(const std::vector<Req> &reqs, hipStream_t s, int order, int &rc) {
+    if (has_pieces(reqs)) return 0;   // pieces of a call's long rows are planned each time (their lane chains are per call)
     const uint64_t gen = g_cfg_gen.load();
     std::lock_guard<std::mutex> lk(g_bc_mu);
     for (CachedBatch &c : g_bc)
@@ -1201,7 +1223,7 @@ int cached_launch(const std::vector<Req> &reqs, hipStream_t s, int order, int &r
 
 // Keeps a planned batch without a pre-pass workspace and launches it on s: 1 if kept (rc set), 0 if it cannot be kept.
 int keep_and_launch(const std::vector<Req> &reqs, Batch &bt, hipStream_t s, int order, int &rc) {
-    if (bt.ws_bytes != 0 || bt.table_bytes == 0) return 0;
+    if (bt.ws_bytes != 0 || bt.table_bytes == 0 || has_pieces(reqs)) return 0;
     const uint64_t gen = g_cfg_gen.load();
     void *dev = nullptr;
     hipError_t e = hipMalloc(&dev, bt.table_bytes);
@@ -1242,7 +1264,78 @@ int settle() {   // before the staging or the scratch is reused: the wait a fail
     return ES_HIP_OK;
 }
 
+// Rows longer than ES_HIP_MAX_COLS_* (one row's float terms no longer fit a workgroup's LDS) run as column pieces of at
+// most that many columns, one batch per piece in stream order, each piece continuing the chains where the one before
+// stopped: es_matvec's sums over a row's blocks (src/es_quant.c:1852-1945, per format at :1013-1117 and :1252-1469)
+// are sequential in block order, and the pieces cut them at block boundaries, so every output is the whole row's. A
+// K-quant row (and a 32-element row in the scalar order) carries its one chain in y; the AVX2 order of the 32-element
+// formats carries eight lane chains per output in a stream-ordered allocation. Phase 0 holds every other product and the
+// first piece of each long one; phase p the p-th pieces.
+bool has_long(const std::vector<Req> &reqs) {
+    for (const Req &q : reqs) {
+        FmtInfo f;
+        if (!q.row_bytes && !q.ints && fmt_info(q.type, f) && q.cols > (f.be == 32 ? ES_HIP_MAX_COLS_32 : ES_HIP_MAX_COLS_256))
+            return true;
+    }
+    return false;
+}
+
+template <typename RUN> int run_in_pieces(const std::vector<Req> &reqs, hipStream_t s, int order, RUN run) {
+    const bool x86 = order != ES_HIP_ORDER_SCALAR;
+    size_t nlanes = 0;
+    for (const Req &q : reqs) {   // every long request is checked before anything is allocated or launched
+        FmtInfo f;
+        if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
+        if (q.ints || q.cols <= (f.be == 32 ? ES_HIP_MAX_COLS_32 : ES_HIP_MAX_COLS_256)) continue;
+        if (int rc = check_req(q, f, false)) return rc;
+        if (f.be == 32 && x86 && q.r1 > q.r0 && q.na > 0) nlanes += (size_t)q.na * (q.r1 - q.r0) * 8;
+    }
+    float *lanes = nullptr;
+    if (nlanes) {
+        hipError_t e = hipMallocAsync(reinterpret_cast<void **>(&lanes), nlanes * sizeof(float), s);
+        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (lane chains of long rows)");
+    }
+    std::vector<std::vector<Req>> phases(1);
+    size_t lo = 0;
+    for (const Req &q : reqs) {
+        FmtInfo f;
+        fmt_info(q.type, f);
+        const int cmax = f.be == 32 ? ES_HIP_MAX_COLS_32 : ES_HIP_MAX_COLS_256;
+        if (q.ints || q.cols <= cmax || q.r1 == q.r0 || q.na == 0) {
+            phases[0].push_back(q);
+            continue;
+        }
+        const int nbk = q.cols / f.be, pb = cmax / f.be, np = (nbk + pb - 1) / pb;
+        float *ql = f.be == 32 && x86 ? lanes + lo : nullptr;
+        if (ql) lo += (size_t)q.na * (q.r1 - q.r0) * 8;
+        for (int p = 0; p < np; p++) {
+            const int b0 = p * pb, b1 = std::min(nbk, b0 + pb);
+            Req r = q;
+            r.W = static_cast<const uint8_t *>(q.W) + (size_t)b0 * f.bb;
+            r.act = static_cast<const uint8_t *>(q.act) + (size_t)b0 * f.ab;
+            r.cols = (b1 - b0) * f.be;
+            r.astride = q.astride ? q.astride : (size_t)nbk * f.ab;
+            r.row_bytes = (size_t)nbk * f.bb;
+            r.chain = (p > 0 ? esq::MV_CHAIN_IN : 0) | (ql && p + 1 < np ? esq::MV_CHAIN_LANES_OUT : 0);
+            r.lanes = ql;
+            if ((int)phases.size() <= p) phases.resize(p + 1);
+            phases[p].push_back(r);
+        }
+    }
+    int rc = ES_HIP_OK;
+    for (const std::vector<Req> &ph : phases)
+        if (!rc && !ph.empty()) rc = run(ph, order);
+    if (lanes) {
+        hipError_t e = hipFreeAsync(lanes, s);
+        if (!rc && e != hipSuccess) rc = hip_fail(e, "hipFreeAsync");
+    }
+    return rc;
+}
+
 int run_launch(const std::vector<Req> &reqs, hipStream_t s, int order) {   // order -1: es_hip_set_order's
+    if (has_long(reqs))
+        return run_in_pieces(reqs, s, order >= 0 ? order : g_order.load(),
+                             [&](const std::vector<Req> &ph, int o) { return run_launch(ph, s, o); });
     int rc = ES_HIP_OK;
     if (cached_launch(reqs, s, order, rc)) {
         if (!rc) g_table_pending = true;   // the caller's wait follows
@@ -1367,15 +1460,18 @@ int es_hip_synchronize(void) {
 // Plan and launch a batch in stream order: a single decode job by value; anything else (several jobs per launch,
 // pre-passes) with a stream-ordered allocation for the job tables and the pre-pass workspace, freed in stream order. The
 // tables are copied from pageable memory, which the copy has consumed when it returns.
-static int run_async(const std::vector<Req> &reqs, hipStream_t s) {
+static int run_async(const std::vector<Req> &reqs, hipStream_t s, int order = -1) {
+    if (has_long(reqs))
+        return run_in_pieces(reqs, s, order >= 0 ? order : g_order.load(),
+                             [&](const std::vector<Req> &ph, int o) { return run_async(ph, s, o); });
     int rc = ES_HIP_OK;
-    if (cached_launch(reqs, s, -1, rc)) return rc;
+    if (cached_launch(reqs, s, order, rc)) return rc;
     Batch bt;
     if (int e = plan_batch(reqs, bt)) return e;
     if (bt.mm.empty() && bt.mqg.empty() && bt.mbg.empty() && bt.mkg.empty() && bt.pkg.empty() && bt.mv.size() <= 1 &&
         (bt.mv.empty() || bt.mv[0].jobs.size() == 1))
-        return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s);
-    if (keep_and_launch(reqs, bt, s, -1, rc)) return rc;
+        return bt.mv.empty() ? ES_HIP_OK : launch_single(bt.mv[0], s, order);
+    if (keep_and_launch(reqs, bt, s, order, rc)) return rc;
     void *dev = nullptr;
     const size_t ws_at = align256(bt.table_bytes);
     hipError_t e = hipMallocAsync(&dev, std::max<size_t>(ws_at + bt.ws_bytes, 256), s);
@@ -1384,7 +1480,7 @@ static int run_async(const std::vector<Req> &reqs, hipStream_t s) {
     const std::vector<uint8_t> img = table_image(bt);
     if (!img.empty() && (e = hipMemcpyAsync(dev, img.data(), img.size(), hipMemcpyHostToDevice, s)) != hipSuccess)
         rc = hip_fail(e, "job table upload");
-    if (!rc) rc = launch_batch(bt, static_cast<const uint8_t *>(dev), g_order.load(), s);
+    if (!rc) rc = launch_batch(bt, static_cast<const uint8_t *>(dev), order >= 0 ? order : g_order.load(), s);
     e = hipFreeAsync(dev, s);
     if (rc) return rc;
     return e == hipSuccess ? ES_HIP_OK : hip_fail(e, "hipFreeAsync");

@@ -335,10 +335,44 @@ def test_long_rows(hip, orc, F, cols):
     assert np.array_equal(bits(y1[0]), bits(y[0]))
 
 
-@pytest.mark.parametrize("F", ["Q8_0", "Q4_0", "Q4_K", "Q2_K"])
-def test_row_limit(hip, orc, F):
-    """one block past the longest row the library takes is refused with EINVAL, y untouched, on the device path and the
-    host drop-in (whose void prototype reports through es_hip_last_error)"""
+LONG = [("Q8_0", 3), ("Q4_0", 4096 + 5), ("Q5_0", 2), ("Q4_K", 3), ("Q6_K", 4096 + 1), ("Q2_K", 2)]
+
+
+@pytest.mark.parametrize("F,extra", LONG, ids=[f"{f}+{x}" for f, x in LONG])
+@pytest.mark.parametrize("mode", MODES, ids=["clang", "gcc", "scalar"])
+def test_rows_past_the_limit(order, orc, F, extra, mode):
+    """rows longer than ES_HIP_MAX_COLS_* (131072 / 1048576 columns) run as column pieces of at most that length, each
+    continuing the chains where the one before stopped (the one chain in y; the AVX2 order's eight lane chains per output
+    in a stream-ordered buffer): bit-identical to the oracle's whole-row sums in every order, at one and three
+    activations, through the device entry point, run_jobs and the host drop-in; two and three pieces"""
+    hip = order
+    hip.set_order(mode[0])
+    t = O.TYPES[F]
+    be = O.BLOCK_ELEMS[t]
+    cols = (131072 if be == 32 else 1048576) + extra * be
+    rows = 5
+    W, acts = mtest_inputs(orc, t, rows, cols, 3, 4242 + t + extra)
+    ref = orc.matvec_multi(t, W, cols, rows, acts, mode[2], mode[3])
+    y = hip.matvec_multi(t, W, cols, rows, acts)
+    assert np.array_equal(bits(y), bits(ref)), mismatch_report(y, ref)
+    y1 = hip.matvec_multi(t, W, cols, rows, acts[:1], r0=1, r1=4)
+    assert np.array_equal(bits(y1[0, 1:4]), bits(ref[0, 1:4])) and np.all(y1[0, [0, 4]] == 0)
+    dW, dA = hip.upload(W), hip.upload(np.ascontiguousarray(acts))
+    dY = hip.upload(np.full((3, rows), -1.0, np.float32))
+    hip.run_jobs([dict(type=t, rows=rows, cols=cols, W=dW, act=dA, astride=acts.strides[0], nb=3, y=dY, ystride=rows)])
+    yj = hip.download(dY, np.zeros((3, rows), np.float32))
+    assert np.array_equal(bits(yj), bits(ref))
+    for b in (dW, dA, dY):
+        b.close()
+    yh = np.full((3, rows), -1.0, np.float32)
+    hip.host_matvec_multi(t, W, cols, 0, rows, acts, yh)
+    assert np.array_equal(bits(yh), bits(ref))
+
+
+@pytest.mark.parametrize("F", ["Q8_0", "Q4_K"])
+def test_row_limit_kept_plans(hip, orc, F):
+    """the entry points that keep or pre-size their tables (a kept plan, the no-allocation product) still take rows of at
+    most ES_HIP_MAX_COLS_*: one block more is refused with EINVAL and y is untouched"""
     t = O.TYPES[F]
     cmax = 131072 if O.BLOCK_ELEMS[t] == 32 else 1048576
     c = cmax + O.BLOCK_ELEMS[t]
@@ -346,14 +380,10 @@ def test_row_limit(hip, orc, F):
     dW, dA = hip.alloc(4 * E.row_bytes(t, c)), hip.alloc(nbk * E.ACT_BYTES[t])
     dY = hip.upload(np.full(4, -5.0, np.float32))
     with pytest.raises(E.EsHipError) as ei:
-        hip.matvec_multi_dev(t, dW, c, 0, 4, dA, 0, 1, dY, 0)
+        hip.matvec_multi_dev_noalloc(t, dW, c, 0, 4, dA, 0, 1, dY, 0)
     assert "above" in str(ei.value)
+    with pytest.raises(E.EsHipError):
+        hip.plan([dict(type=t, rows=4, cols=c, W=dW, act=dA, y=dY)])
     assert np.all(hip.download(dY, np.zeros(4, np.float32)) == -5.0)
     for b in (dW, dA, dY):
         b.close()
-    Wh = np.zeros(4 * E.row_bytes(t, c), np.uint8)
-    ah = np.zeros((1, nbk * E.ACT_BYTES[t]), np.uint8)
-    yh = np.full((1, 4), -5.0, np.float32)
-    with pytest.raises(E.EsHipError):   # the host drop-in: void, the error in es_hip_last_error
-        hip.host_matvec_multi(t, Wh, c, 0, 4, ah, yh)
-    assert np.all(yh == -5.0)
