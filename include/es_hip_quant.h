@@ -135,7 +135,9 @@ typedef struct {
 int es_hip_run_jobs(const es_hip_job *jobs, int njobs, void *stream);
 
 /* A prepared job batch: the job table is uploaded once, so a launch costs only the kernel dispatches. The jobs' pointers
- * are captured when the plan is made; the memory they point to may change between runs. */
+ * are captured when the plan is made; the memory they point to may change between runs. A plan with rows past
+ * ES_HIP_MAX_COLS_* keeps one batch per phase of column pieces (run in order) and the lane chains between them, so two
+ * runs of one such plan must not overlap (runs on one stream never do). */
 typedef struct es_hip_plan es_hip_plan;
 es_hip_plan *es_hip_plan_create(const es_hip_job *jobs, int njobs);   /* NULL on failure */
 int          es_hip_plan_run(es_hip_plan *plan, void *stream);
@@ -156,9 +158,9 @@ int es_hip_unregister(const void *host);
  * (Q4_0, Q5_0, Q8_0) or ES_HIP_MAX_COLS_256 for the K-quants (where one row's float terms stop fitting a workgroup's LDS
  * in the decode kernel) run as column pieces of at most that length, one launch each in stream order, every piece
  * continuing the sums where the previous one stopped (the same outputs; the AVX2 order's lane sums between pieces take a
- * stream-ordered allocation). This holds for es_hip_matvec[_multi], es_hip_matvec[_multi]_dev, es_hip_run_jobs[_host];
- * the entry points that keep or pre-size their job tables (es_hip_plan_*, es_hip_matvec_multi_dev_noalloc, the dense and
- * MoE layers) refuse longer rows with ES_HIP_EINVAL. */
+ * stream-ordered allocation). This holds for es_hip_matvec[_multi], es_hip_matvec[_multi]_dev, es_hip_run_jobs[_host]
+ * and es_hip_plan_*; es_hip_matvec_multi_dev_noalloc (whose scratch is sized once) and the dense and MoE layers refuse
+ * longer rows with ES_HIP_EINVAL. */
 #define ES_HIP_MAX_COLS_32 131072
 #define ES_HIP_MAX_COLS_256 1048576
 void es_hip_matvec(uint32_t type, const void *W, int cols, int r0, int r1, const es_hip_act *a, float *y, float *scratch);

@@ -1280,22 +1280,24 @@ bool has_long(const std::vector<Req> &reqs) {
     return false;
 }
 
-template <typename RUN> int run_in_pieces(const std::vector<Req> &reqs, hipStream_t s, int order, RUN run) {
+// checks every long request (before anything is allocated or launched) and counts the floats of its lane chains
+int count_lanes(const std::vector<Req> &reqs, int order, size_t &nlanes) {
     const bool x86 = order != ES_HIP_ORDER_SCALAR;
-    size_t nlanes = 0;
-    for (const Req &q : reqs) {   // every long request is checked before anything is allocated or launched
+    nlanes = 0;
+    for (const Req &q : reqs) {
         FmtInfo f;
         if (!fmt_info(q.type, f)) return fail(ES_HIP_EINVAL, "type %u is not computed by this library", q.type);
         if (q.ints || q.cols <= (f.be == 32 ? ES_HIP_MAX_COLS_32 : ES_HIP_MAX_COLS_256)) continue;
         if (int rc = check_req(q, f, false)) return rc;
         if (f.be == 32 && x86 && q.r1 > q.r0 && q.na > 0) nlanes += (size_t)q.na * (q.r1 - q.r0) * 8;
     }
-    float *lanes = nullptr;
-    if (nlanes) {
-        hipError_t e = hipMallocAsync(reinterpret_cast<void **>(&lanes), nlanes * sizeof(float), s);
-        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (lane chains of long rows)");
-    }
-    std::vector<std::vector<Req>> phases(1);
+    return ES_HIP_OK;
+}
+
+// the phases of reqs (after count_lanes), lane chains in lanes
+void cut_pieces(const std::vector<Req> &reqs, int order, float *lanes, std::vector<std::vector<Req>> &phases) {
+    const bool x86 = order != ES_HIP_ORDER_SCALAR;
+    phases.assign(1, {});
     size_t lo = 0;
     for (const Req &q : reqs) {
         FmtInfo f;
@@ -1322,6 +1324,18 @@ template <typename RUN> int run_in_pieces(const std::vector<Req> &reqs, hipStrea
             phases[p].push_back(r);
         }
     }
+}
+
+template <typename RUN> int run_in_pieces(const std::vector<Req> &reqs, hipStream_t s, int order, RUN run) {
+    size_t nlanes = 0;
+    if (int rc = count_lanes(reqs, order, nlanes)) return rc;
+    float *lanes = nullptr;
+    if (nlanes) {
+        hipError_t e = hipMallocAsync(reinterpret_cast<void **>(&lanes), nlanes * sizeof(float), s);
+        if (e != hipSuccess) return hip_fail(e, "hipMallocAsync (lane chains of long rows)");
+    }
+    std::vector<std::vector<Req>> phases;
+    cut_pieces(reqs, order, lanes, phases);
     int rc = ES_HIP_OK;
     for (const std::vector<Req> &ph : phases)
         if (!rc && !ph.empty()) rc = run(ph, order);
@@ -1620,17 +1634,13 @@ struct es_hip_plan {
     Batch bt;
     uint8_t *dev = nullptr;   // job tables, then the pre-pass workspace
     int order;
+    std::vector<es_hip_plan *> more;   // the later phases of long rows' column pieces, run after this one in order
+    float *lanes = nullptr;            // their lane chains
 };
 
-extern "C" {
-
-es_hip_plan *es_hip_plan_create(const es_hip_job *jobs, int njobs) {
-    if (need_device()) return nullptr;
-    if (njobs < 0 || (njobs > 0 && !jobs)) { fail(ES_HIP_EINVAL, "bad job list"); return nullptr; }
-    std::vector<Req> reqs;
-    to_reqs(jobs, njobs, reqs);
+static es_hip_plan *plan_one(const std::vector<Req> &reqs, int order) {
     auto *p = new es_hip_plan();
-    p->order = g_order.load();
+    p->order = order;
     if (plan_batch(reqs, p->bt)) { delete p; return nullptr; }
     const size_t ws_at = align256(p->bt.table_bytes);
     hipError_t e = hipMalloc(&p->dev, std::max<size_t>(ws_at + p->bt.ws_bytes, 256));
@@ -1647,13 +1657,48 @@ es_hip_plan *es_hip_plan_create(const es_hip_job *jobs, int njobs) {
     return p;
 }
 
+extern "C" {
+
+es_hip_plan *es_hip_plan_create(const es_hip_job *jobs, int njobs) {
+    if (need_device()) return nullptr;
+    if (njobs < 0 || (njobs > 0 && !jobs)) { fail(ES_HIP_EINVAL, "bad job list"); return nullptr; }
+    std::vector<Req> reqs;
+    to_reqs(jobs, njobs, reqs);
+    const int order = g_order.load();
+    if (!has_long(reqs)) return plan_one(reqs, order);
+    // rows past ES_HIP_MAX_COLS_*: one kept batch per phase of column pieces, the lane chains in the plan's own memory
+    size_t nlanes = 0;
+    if (count_lanes(reqs, order, nlanes)) return nullptr;
+    float *lanes = nullptr;
+    if (nlanes) {
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(&lanes), nlanes * sizeof(float));
+        if (e != hipSuccess) { hip_fail(e, "hipMalloc (lane chains of long rows)"); return nullptr; }
+    }
+    std::vector<std::vector<Req>> phases;
+    cut_pieces(reqs, order, lanes, phases);
+    es_hip_plan *p = plan_one(phases[0], order);
+    if (!p) { if (lanes) (void)hipFree(lanes); return nullptr; }
+    p->lanes = lanes;
+    for (size_t i = 1; i < phases.size(); i++) {
+        es_hip_plan *m = plan_one(phases[i], order);
+        if (!m) { es_hip_plan_destroy(p); return nullptr; }
+        p->more.push_back(m);
+    }
+    return p;
+}
+
 int es_hip_plan_run(es_hip_plan *p, void *stream) {
     if (!p) return fail(ES_HIP_EINVAL, "null plan");
-    return launch_batch(p->bt, p->dev, p->order, static_cast<hipStream_t>(stream));
+    int rc = launch_batch(p->bt, p->dev, p->order, static_cast<hipStream_t>(stream));
+    for (es_hip_plan *m : p->more)
+        if (!rc) rc = launch_batch(m->bt, m->dev, m->order, static_cast<hipStream_t>(stream));
+    return rc;
 }
 
 void es_hip_plan_destroy(es_hip_plan *p) {
     if (!p) return;
+    for (es_hip_plan *m : p->more) es_hip_plan_destroy(m);
+    if (p->lanes) (void)hipFree(p->lanes);
     if (p->dev) (void)hipFree(p->dev);
     delete p;
 }

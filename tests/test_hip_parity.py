@@ -367,12 +367,24 @@ def test_rows_past_the_limit(order, orc, F, extra, mode):
     yh = np.full((3, rows), -1.0, np.float32)
     hip.host_matvec_multi(t, W, cols, 0, rows, acts, yh)
     assert np.array_equal(bits(yh), bits(ref))
+    dW, dA = hip.upload(W), hip.upload(np.ascontiguousarray(acts))
+    dY = hip.upload(np.full((3, rows), -1.0, np.float32))
+    plan = hip.plan([dict(type=t, rows=rows, cols=cols, W=dW, act=dA, astride=acts.strides[0], nb=3, y=dY, ystride=rows)])
+    try:
+        for _ in range(2):   # the kept phases and lane chains serve every run
+            hip.memset(dY, 0, 3 * rows * 4)
+            plan.run()
+            assert np.array_equal(bits(hip.download(dY, np.zeros((3, rows), np.float32))), bits(ref))
+    finally:
+        plan.close()
+        for b in (dW, dA, dY):
+            b.close()
 
 
 @pytest.mark.parametrize("F", ["Q8_0", "Q4_K"])
-def test_row_limit_kept_plans(hip, orc, F):
-    """the entry points that keep or pre-size their tables (a kept plan, the no-allocation product) still take rows of at
-    most ES_HIP_MAX_COLS_*: one block more is refused with EINVAL and y is untouched"""
+def test_row_limit_noalloc(hip, orc, F):
+    """the no-allocation product, whose scratch is sized once, still takes rows of at most ES_HIP_MAX_COLS_*: one block
+    more is refused with EINVAL and y is untouched"""
     t = O.TYPES[F]
     cmax = 131072 if O.BLOCK_ELEMS[t] == 32 else 1048576
     c = cmax + O.BLOCK_ELEMS[t]
@@ -382,8 +394,6 @@ def test_row_limit_kept_plans(hip, orc, F):
     with pytest.raises(E.EsHipError) as ei:
         hip.matvec_multi_dev_noalloc(t, dW, c, 0, 4, dA, 0, 1, dY, 0)
     assert "above" in str(ei.value)
-    with pytest.raises(E.EsHipError):
-        hip.plan([dict(type=t, rows=4, cols=c, W=dW, act=dA, y=dY)])
     assert np.all(hip.download(dY, np.zeros(4, np.float32)) == -5.0)
     for b in (dW, dA, dY):
         b.close()
