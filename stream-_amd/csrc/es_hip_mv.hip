@@ -509,7 +509,7 @@ template <int F, int NT> constexpr int units() {
 // units of the one- and two-wide bodies of mv_kernel_mixed (0: as units())
 template <int F, int NT> constexpr int units_mixed() {
     if constexpr (F == ES_HIP_Q6_K || F == ES_HIP_Q3_K) return NT == 1 ? Q6K_UNITS1M : Q6K_UNITS2M;
-    else if constexpr (!is32<F>()) return NT == 1 ? 0 : K_UNITS2M;
+    else if constexpr (F == ES_HIP_Q4_K) return NT == 1 ? 0 : K_UNITS2M;   // (measured for Q4_K; Q5_K's grew past 168 VGPRs)
     else return 0;
 }
 
