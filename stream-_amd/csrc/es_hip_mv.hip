@@ -522,12 +522,7 @@ template <int F, int NT> constexpr int units_mixed() {
 // activation slices for each). All waves write their blocks' float terms to the workgroup's LDS, then the
 // whole workgroup runs the per-row chains. order: ES_HIP_ORDER_*; NT activations per pass. One workgroup per tile
 // (rows_per_wg rows of one job).
-// XP: each chain batch's first raw loads are issued before the previous batch's float phase, so the wave's requests
-// continue through the barriers and the chains. Used for Q6_K at one activation per pass (two units per pass, the
-// fewest in flight): config 3's head 5.76 -> 5.87 TB/s, Q6_K decode at config 2's shapes 5.57 -> 5.70. Slower for the
-// others (Q4_0 decode 2.96 -> 2.75 TB/s, Q3_K 4.59 -> 4.10, Q2_K 5.54 -> 4.92, Q5_K 5.97 -> 5.79; the MoE layer of
-// config 5 0.1148 -> 0.1327 ms), Q4_K unchanged.
-template <int F, int NT, int W, bool SEGLOOP, int UO = 0, bool XP = false>
+template <int F, int NT, int W, bool SEGLOOP, int UO = 0>
 __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
     using L = Lane<F>;
     constexpr int LPB = Fmt<F>::LPB, BE = Fmt<F>::BE, BB = Fmt<F>::BB, AB = Fmt<F>::AB;
@@ -668,24 +663,7 @@ __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
                     }
                 }
             }
-            if constexpr (XP && !SEGLOOP) {
-                // the next chain batch's first raw loads go out before this batch's chains, so the wave's memory
-                // requests continue through the barriers and the float phase (only where the next batch has rows
-                // for this wave: pre is then consumed by that batch's first pass)
-                const int ran = ra + J.chain_rows, rbn = min(ran + J.chain_rows, rend);
-                if (ran < rend && ran + rfirst - rowoff < rbn) {
-#pragma unroll
-                    for (int u = 0; u < U; u++) {
-                        const int row = ran + rfirst + u * rstep;
-                        ok[u] = live && row < rbn;
-                        L::load_raw(ok[u] ? J.W + (size_t)row * J.row_bytes + (size_t)b * BB : dummy, k, raw[u]);
-                    }
-                    pre = true;
-                }
-            }
-            // (with those loads in flight the barriers order LDS only: __syncthreads would wait for them)
-            if constexpr (XP && !SEGLOOP) lds_sync();
-            else __syncthreads();
+            __syncthreads();
             // ---- phase 2: the reference's sequential accumulation over the row's blocks, terms read 8 blocks ahead
             const int nrow = rb - ra;
             const int per = cmode == CH_LANES ? 8 : 1;
@@ -743,8 +721,7 @@ __device__ __forceinline__ void mv_body(const MvJob &J, int order) {
                 }
                 if (i == 0 && t < nt) stg<float>(J.y + (size_t)(t0 + t) * J.ystride + ra + rl, s);
             }
-            if constexpr (XP && !SEGLOOP) lds_sync();
-            else __syncthreads();
+            __syncthreads();
         }
     }
 }
@@ -755,7 +732,7 @@ __global__ __launch_bounds__(WAVE * W, ESQ_MIN_WAVES) void mv_kernel(const MvJob
     MvJob J;
     if (jobs) J = load_tile_job(jobs, njobs, blockIdx.x);
     else J = single;
-    mv_body<F, NT, W, SEGLOOP, 0, F == ES_HIP_Q6_K && NT == 1>(J, order);
+    mv_body<F, NT, W, SEGLOOP>(J, order);
 }
 
 // A launch whose jobs take different activations per pass (J.nt: 1, 2 or 4), e.g. an MoE layer's experts at 1 to 8

@@ -180,6 +180,12 @@ int segments(int nbk, int slots) {
 }
 
 // Plan the launches: one per (format, workgroup size). The job order inside a launch is kept.
+// Q6_K decode at one activation per pass runs faster at three waves per SIMD than at the four its registers allow: its
+// launches reserve 41 KB of LDS per 4-wave workgroup, so three share a CU (config 3's head 5.70 -> 5.86 TB/s, Q6_K
+// decode at config 2's shapes 5.54 -> 5.74; same-process pairs)
+#ifndef ESQ_Q6K_LDS
+#define ESQ_Q6K_LDS 41984
+#endif
 constexpr int PIECES = 16;   // (in a launch key: column pieces of long rows)
 int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
     out.clear();
@@ -263,6 +269,8 @@ int plan_groups(const std::vector<Req> &reqs, std::vector<Group> &out) {
             lds = std::max(lds, (size_t)chain * per_row);
             g.jobs.push_back(j);
         }
+        // Q6_K at one activation per pass: LDS reserved so that three 4-wave workgroups share a CU (three waves per SIMD)
+        if (ESQ_Q6K_LDS && g.L.type == ES_HIP_Q6_K && g.L.nt == 1 && !g.L.seg_loop) lds = std::max<size_t>(lds, ESQ_Q6K_LDS);
         g.L.grid = tile;
         g.L.lds = lds;
         out.push_back(std::move(g));
